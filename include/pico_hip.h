@@ -1,0 +1,203 @@
+/*
+ * pico_hip.h -- C ABI of libpico_hip.so, the MI355X (gfx950) kernels behind the
+ * batch-1 GGUF decode path of pico-engine.
+ *
+ * Every entry point:
+ *   - takes plain device pointers and sizes (no torch or HIP types in the signature;
+ *     a stream is passed as `pe_stream_t`, i.e. a hipStream_t cast to void*, NULL = default stream);
+ *   - validates its arguments on the host and returns a pe_status (PE_OK = 0) BEFORE
+ *     launching anything, so a bad call never reaches the GPU;
+ *   - is asynchronous on the given stream and graph-capturable: it performs no
+ *     allocation, copy or synchronisation; every buffer (workspaces included) is owned
+ *     by the caller;
+ *   - is thread-safe: the library keeps no mutable global state.
+ *
+ * Quantized weights: the decode kernels read a "tiled" copy of a GGUF tensor made
+ * on the device by pe_repack. Tiling is a pure byte permutation of the GGUF blocks
+ * (same byte count, same bit packing): the fields of every block (qs, qh, scales, d)
+ * are gathered into separate planes so each lane can use aligned 8/16-byte loads.
+ * Plane layout for an (n_rows x k) tensor with nb = k / QK blocks per row:
+ *   Q8_0: qs[n_rows][nb][32] | d f16[n_rows][nb]
+ *   Q5_0: qs[n_rows][nb][16] | qh u32[n_rows][nb] | d f16[n_rows][nb]
+ *   Q4_K: qs[n_rows][nb][128] | head[n_rows][nb][16]   (head = d, dmin, scales[12] verbatim)
+ *   Q6_K: ql[n_rows][nb][128] | qh[n_rows][nb][64] | scales[n_rows][nb][16] | d f16[n_rows][nb]
+ * Tiled buffers must be 16-byte aligned.
+ *
+ * Reference citations are to Labeeb2339/pico-engine, src/pico_engine/<file>:<line>.
+ */
+#ifndef PICO_HIP_H
+#define PICO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* pe_stream_t;
+
+/* ggml type ids (same values as dequant.py:15-22) */
+#define PE_TYPE_F32 0
+#define PE_TYPE_F16 1
+#define PE_TYPE_Q5_0 6
+#define PE_TYPE_Q8_0 8
+#define PE_TYPE_Q4_K 12
+#define PE_TYPE_Q6_K 14
+#define PE_TYPE_Q8_K 15
+
+enum pe_status {
+    PE_OK = 0,
+    PE_ERR_NULL = 1,   /* a required pointer is NULL */
+    PE_ERR_TYPE = 2,   /* ggml type not supported by this entry point */
+    PE_ERR_SHAPE = 3,  /* a size is non-positive, not a whole number of blocks, or too large */
+    PE_ERR_ALIGN = 4,  /* a pointer is not aligned as the entry point requires */
+    PE_ERR_LAUNCH = 5, /* the HIP runtime rejected a kernel launch */
+    PE_ERR_SPACE = 6   /* a caller-provided workspace is too small */
+};
+
+/* Human-readable text for a pe_status. Never NULL. */
+const char* pe_strerror(int status);
+
+/* ABI version of this header (bumped on any incompatible change). */
+int pe_abi_version(void);
+
+/* Bytes of n elements of ggml_type; negative pe_status on error.
+ * Replaces nbytes_for (dequant.py:27-48). */
+int64_t pe_nbytes_for(int ggml_type, int64_t n);
+
+/* ---- load-time transforms ------------------------------------------------------------ */
+
+/* Bit-exact fp32 dequantization of n elements of raw GGUF blocks (F32, F16, Q5_0, Q8_0,
+ * Q4_K, Q6_K, Q8_K). `blocks` needs only 2-byte alignment (4 for F32/Q8_K).
+ * Replaces dequantize (dequant.py:243-260). */
+int pe_dequant(int ggml_type, const void* blocks, float* out, int64_t n, pe_stream_t stream);
+
+/* Raw GGUF blocks of an (n_rows x k) tensor -> tiled layout (see above).
+ * Types: Q5_0, Q8_0, Q4_K, Q6_K. `tiled` holds pe_nbytes_for(type, n_rows*k) bytes.
+ * Replaces the load-time unpack_q5_0/q8_0/q6_k/q4_k (dequant.py:79-168) and the
+ * _prep_quant_dense upload (engine.py:198-267): the kernels read this form instead. */
+int pe_repack(int ggml_type, const void* blocks, void* tiled, int64_t n_rows, int64_t k,
+              pe_stream_t stream);
+
+/* Bit-exact fp32 dequantization of a tiled tensor to out[n_rows][k], through the same
+ * device decode routines the GEMV kernels use (so it pins their decode). */
+int pe_dequant_tiled(int ggml_type, const void* tiled, float* out, int64_t n_rows, int64_t k,
+                     pe_stream_t stream);
+
+/* out[l][:] = dequantized row ids[l] of a raw GGUF (vocab x hidden) table, l < n_ids.
+ * An id outside [0, vocab) yields a row of NaN (no out-of-bounds read).
+ * Replaces the embedding gather self.embed[token_ids] (model.py:152) over the fp32
+ * table that _load_weights dequantizes (engine.py:80-98). */
+int pe_embed_gather(int ggml_type, const void* table_blocks, int64_t vocab, int64_t hidden,
+                    const int64_t* ids, int64_t n_ids, float* out, pe_stream_t stream);
+
+/* ---- decode (M = 1) kernels ---------------------------------------------------------- */
+
+/* y[n] = sum_k W[n][k] x[k] (+ residual[n]) (+ bias[n]) for a tiled W (n_rows x k).
+ * residual and bias may be NULL. Types: Q5_0, Q8_0, Q4_K, Q6_K.
+ * Replaces q8_0_gemv (kernels.py:178), q5_0_gemv (kernels.py:211),
+ * q6_k_gemv (kernels.py:286), q4_k_gemv (kernels.py:326), and the fp32 o-projection
+ * addmm with residual (model.py:213). */
+int pe_qgemv(int ggml_type, const void* w_tiled, int64_t n_rows, int64_t k, const float* x,
+             const float* residual, const float* bias, float* y, pe_stream_t stream);
+
+/* y = W (rmsnorm(x) * norm_w): RMSNorm of x (length k, eps) fused into the GEMV.
+ * Replaces q5_0_gemv_norm (kernels.py:253) for every format, and the final
+ * rmsnorm + LM-head q8_0_gemv (model.py:159-162). */
+int pe_qgemv_rmsnorm(int ggml_type, const void* w_tiled, int64_t n_rows, int64_t k,
+                     const float* x, const float* norm_w, float eps, float* y, pe_stream_t stream);
+
+/* act[j] = silu(g_j) * u_j with g = W[j] h, u = W[ffn + j] h, h = rmsnorm(x) * norm_w,
+ * for a tiled W of 2*ffn rows ([gate; up]). norm_w may be NULL (no RMSNorm).
+ * Replaces q5_0_gemv_norm + silu_mul (kernels.py:253, :77; model.py:219-224). */
+int pe_qgemv_rmsnorm_silu(int ggml_type, const void* w_tiled, int64_t ffn, int64_t k,
+                          const float* x, const float* norm_w, float eps, float* act,
+                          pe_stream_t stream);
+
+/* Fused attention prologue of one decode token:
+ *   h = rmsnorm(x) * norm_w;  [q; k; v] = [Wq; Wk; Wv] h + [bq; bk; bv]   (mixed formats)
+ *   q, k <- rotate-half RoPE with cos/sin row *pos;  q -> q_out;
+ *   k, v -> k_cache[kv][*pos][:], v_cache[kv][*pos][:]
+ * Replaces rmsnorm + F.linear(qkv) + rope + index_copy_ (model.py:175-193, kernels.py:26,50).
+ * An out-of-range *pos writes nothing to the cache and NaN to q_out. */
+typedef struct pe_qkv_args {
+    int type_q, type_k, type_v;        /* ggml types of the three tiled segments */
+    const void *w_q, *w_k, *w_v;       /* tiled (n_head*hd x hidden), (n_kv*hd x hidden) x2 */
+    const float *b_q, *b_k, *b_v;      /* biases or NULL */
+    const float* x;                    /* (hidden) residual stream */
+    const float* norm_w;               /* (hidden) attn_norm weight, or NULL */
+    float eps;
+    const float* cos_tab;              /* (rope_rows, hd/2) */
+    const float* sin_tab;
+    int64_t rope_rows;
+    const int64_t* pos;                /* device scalar: position of this token */
+    float* q_out;                      /* (n_head, hd) */
+    float* k_cache;                    /* (n_kv, capacity, hd) */
+    float* v_cache;
+    int64_t capacity;
+    int64_t hidden;
+    int n_head, n_kv, head_dim;
+} pe_qkv_args;
+int pe_qkv_rmsnorm_rope(const pe_qkv_args* args, pe_stream_t stream);
+
+/* Single-query GQA attention over a KV cache, split over positions across CUs with a
+ * log-sum-exp merge (the last split to finish merges; no extra launch).
+ *   q (n_head, hd); k_cache, v_cache (n_kv, capacity, hd); out (n_head, hd)
+ *   valid length S = (len_dev ? *len_dev : 0) + len_add, clamped to [0, capacity];
+ *   len_dtype: 0 = len_dev unused, 1 = int32, 2 = int64. Head h reads kv head h / (n_head/n_kv).
+ *   round_fp16 != 0 rounds the output to fp16 (round-to-nearest-even) and stores it as fp32,
+ *   as the reference kernel does (kernels.py:126). S == 0 gives NaN, as the reference does.
+ * workspace: pe_decode_attn_workspace_bytes(...) bytes, zero-filled once before first use;
+ * it is left zeroed again after every call, so one workspace serves any number of calls
+ * made in order on one stream (calls that overlap must not share it).
+ * Replaces decode_attn (kernels.py:129). */
+int64_t pe_decode_attn_workspace_bytes(int n_head, int n_kv, int head_dim, int64_t capacity);
+int pe_decode_attn(const float* q, const float* k_cache, const float* v_cache, int n_head,
+                   int n_kv, int head_dim, int64_t capacity, const void* len_dev, int len_dtype,
+                   int64_t len_add, float scale, int round_fp16, float* out, void* workspace,
+                   int64_t workspace_bytes, pe_stream_t stream);
+
+/* ---- general / prefill (M >= 1) kernels ------------------------------------------------ */
+
+/* y[r][:] = rmsnorm(x[r][:]) * w for r < rows (row strides in elements).
+ * Replaces rmsnorm (kernels.py:26). */
+int pe_rmsnorm(const float* x, int64_t x_stride, const float* w, float* y, int64_t y_stride,
+               int64_t rows, int64_t n, float eps, pe_stream_t stream);
+
+/* Rotate-half RoPE of x (L, n_head, hd) whose token rows are x_stride elements apart
+ * (heads contiguous within a row), with cos/sin (L, hd/2) rows; writes y likewise.
+ * x == y is allowed. Replaces rope (kernels.py:50). */
+int pe_rope(const float* x, int64_t x_stride, const float* cos_rows, const float* sin_rows,
+            float* y, int64_t y_stride, int64_t L, int n_head, int head_dim, pe_stream_t stream);
+
+/* out[l][j] = silu(g) * u, g = gate_up[l][j], u = gate_up[l][ffn + j].
+ * Replaces silu_mul (kernels.py:77). */
+int pe_silu_mul(const float* gate_up, int64_t gu_stride, float* out, int64_t out_stride,
+                int64_t L, int64_t ffn, pe_stream_t stream);
+
+/* y[m][n] = sum_k W[n][k] x[m][k] (+ bias[n]) (+ residual[m][n]) for m < M, a tiled W.
+ * Row strides in elements. residual may alias y. Replaces the prefill F.linear/addmm/matmul
+ * on fp32-dequantized weights (model.py:177, :213, :223, :235). */
+int pe_qgemm(int ggml_type, const void* w_tiled, int64_t n_rows, int64_t k, const float* x,
+             int64_t x_stride, int64_t m, const float* bias, const float* residual,
+             int64_t res_stride, float* y, int64_t y_stride, pe_stream_t stream);
+
+/* cache[h][pos0 + l][:] = src[l * src_stride + h * hd + :] for both K and V.
+ * Replaces the prefill slice assignment k_buf[:, :L] = k_t (model.py:194-197). */
+int pe_kv_write(const float* k_src, const float* v_src, int64_t src_stride, int n_kv,
+                int head_dim, int64_t L, int64_t pos0, float* k_cache, float* v_cache,
+                int64_t capacity, pe_stream_t stream);
+
+/* Causal GQA attention of L queries at positions pos0..pos0+L-1 over the cache, fp32,
+ * no output rounding. q row l at q + l*q_stride (n_head*hd), out row l at out + l*out_stride.
+ * Replaces the prefill SDPA (model.py:201-209) on the fp32 path. */
+int pe_prefill_attn(const float* q, int64_t q_stride, const float* k_cache, const float* v_cache,
+                    int n_head, int n_kv, int head_dim, int64_t capacity, int64_t L, int64_t pos0,
+                    float scale, float* out, int64_t out_stride, pe_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PICO_HIP_H */

@@ -1,0 +1,341 @@
+// GQA attention over the fp32 KV cache.
+//
+// Decode (one query token), restating decode_attn of the reference (kernels.py:90-158):
+// scores q.k * scale over positions < S (S read from device memory, so one captured graph
+// serves every step), softmax, P.V, output rounded to fp16 and stored as fp32
+// (kernels.py:126). The reference runs one program per query head looping over the whole
+// capacity; here the positions are split in chunks of 64 across workgroups (flash-decoding),
+// one workgroup per (chunk, kv head) serving all the query heads of that kv head, so K/V are
+// read once per kv head and chunks past S cost no KV reads. Each workgroup writes its chunk's
+// (max, sum, P.V) partials; the last one to finish (device-scope counter) merges them with the
+// log-sum-exp rule in a fixed order and resets the counter, so no second launch is needed and
+// the result does not depend on which workgroup finished last.
+//
+// Prefill (L query tokens, causal), restating the fp32 SDPA call of model.py:201-209.
+#include "pe_common.h"
+
+namespace pe {
+
+constexpr int kChunk = 64;   // positions per decode workgroup
+constexpr int kMaxGroup = 16;  // query heads per kv head
+
+struct AttnParams {
+    const float* q;
+    const float* k;
+    const float* v;
+    int n_kv, group;
+    int64_t capacity;
+    const void* len_dev;
+    int len_dtype;
+    int64_t len_add;
+    float scale;
+    int round_fp16;
+    float* out;
+    unsigned* counters;
+    float* partials;
+    int nsplit;
+};
+
+PE_DEV int64_t valid_len(const AttnParams& p) {
+    int64_t S = p.len_add;
+    if (p.len_dtype == 1) S += *reinterpret_cast<const int32_t*>(p.len_dev);
+    else if (p.len_dtype == 2) S += *reinterpret_cast<const int64_t*>(p.len_dev);
+    if (S < 0) S = 0;
+    if (S > p.capacity) S = p.capacity;
+    return S;
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_decode_attn(AttnParams p) {
+    constexpr int DQ = HD / 4;          // dims per thread in the score phase (4 threads / position)
+    constexpr int PS = 256 / HD;        // position slices in the P.V phase
+    constexpr int NPOS = kChunk / PS;   // positions per slice
+    constexpr int REC = HD + 2;         // partial record: m, l, acc[HD]
+    __shared__ float q_lds[kMaxGroup * HD];
+    __shared__ float sc_lds[kMaxGroup * kChunk];
+    __shared__ float red_lds[PS * kMaxGroup * HD];
+    __shared__ float ml_lds[2 * kMaxGroup];
+    __shared__ int last_flag;
+
+    const int t = threadIdx.x;
+    const int split = blockIdx.x, kvh = blockIdx.y;
+    const int G = p.group;
+    const int64_t S = valid_len(p);
+    const int64_t c0 = (int64_t)split * kChunk;
+    const float NEG_INF = -__builtin_huge_valf();
+
+    if (c0 < S) {
+        const float* kbase = p.k + (int64_t)kvh * p.capacity * HD;
+        const float* vbase = p.v + (int64_t)kvh * p.capacity * HD;
+        for (int i = t; i < G * HD; i += 256) q_lds[i] = p.q[(int64_t)kvh * G * HD + i];
+
+        // K part for the score phase, V column slice for the P.V phase (issued together).
+        const int sl = t >> 2, dq = t & 3;
+        float kr[DQ];
+        {
+            const int64_t s = c0 + sl;
+            if (s < p.capacity) {
+                const float4* src = reinterpret_cast<const float4*>(kbase + s * HD + dq * DQ);
+#pragma unroll
+                for (int i = 0; i < DQ / 4; ++i) {
+                    const float4 v4 = src[i];
+                    kr[4 * i] = v4.x; kr[4 * i + 1] = v4.y; kr[4 * i + 2] = v4.z; kr[4 * i + 3] = v4.w;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < DQ; ++i) kr[i] = 0.f;
+            }
+        }
+        const int d = t % HD, js = t / HD;
+        float vr[NPOS];
+#pragma unroll
+        for (int pp = 0; pp < NPOS; ++pp) {
+            const int64_t s = c0 + js * NPOS + pp;
+            vr[pp] = s < p.capacity ? vbase[s * HD + d] : 0.f;
+        }
+        __syncthreads();
+
+        // scores
+        const int64_t s = c0 + sl;
+        for (int g = 0; g < G; ++g) {
+            float part = 0.f;
+#pragma unroll
+            for (int i = 0; i < DQ; ++i) part += q_lds[g * HD + dq * DQ + i] * kr[i];
+            part += __shfl_xor(part, 1, kWave);
+            part += __shfl_xor(part, 2, kWave);
+            if (dq == 0) sc_lds[g * kChunk + sl] = (s < S) ? part * p.scale : NEG_INF;
+        }
+        __syncthreads();
+
+        // chunk softmax statistics: wave w handles heads w, w+4, ...; lane = position
+        {
+            const int w = t >> 6, lane = t & 63;
+            for (int g = w; g < G; g += 4) {
+                const float v = sc_lds[g * kChunk + lane];
+                const float m = group_max<64>(v);
+                const float e = expf(v - m);
+                const float l = group_sum<64>(e);
+                sc_lds[g * kChunk + lane] = e;
+                if (lane == 0) {
+                    ml_lds[2 * g] = m;
+                    ml_lds[2 * g + 1] = l;
+                }
+            }
+        }
+        __syncthreads();
+
+        // P.V over this thread's position slice, then the slices are added in order
+        float acc[kMaxGroup];
+#pragma unroll
+        for (int g = 0; g < kMaxGroup; ++g) {
+            acc[g] = 0.f;
+            if (g < G) {
+#pragma unroll
+                for (int pp = 0; pp < NPOS; ++pp) acc[g] += sc_lds[g * kChunk + js * NPOS + pp] * vr[pp];
+                red_lds[(js * kMaxGroup + g) * HD + d] = acc[g];
+            }
+        }
+        __syncthreads();
+
+        float* rec = p.partials + ((int64_t)kvh * p.nsplit + split) * G * REC;
+        for (int i = t; i < G * HD; i += 256) {
+            const int g = i / HD, dd = i % HD;
+            float a = 0.f;
+#pragma unroll
+            for (int j = 0; j < PS; ++j) a += red_lds[(j * kMaxGroup + g) * HD + dd];
+            rec[g * REC + 2 + dd] = a;
+            if (dd == 0) {
+                rec[g * REC] = ml_lds[2 * g];
+                rec[g * REC + 1] = ml_lds[2 * g + 1];
+            }
+        }
+    }
+
+    // Last workgroup of this kv head merges. Release our partials, count, acquire theirs.
+    __threadfence();
+    __syncthreads();
+    if (t == 0) {
+        const unsigned prev = atomicAdd(&p.counters[kvh], 1u);
+        last_flag = (prev == (unsigned)(p.nsplit - 1));
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    __threadfence();
+
+    const int nvalid = (int)((S + kChunk - 1) / kChunk);
+    const float* base = p.partials + (int64_t)kvh * p.nsplit * G * REC;
+    for (int i = t; i < G * HD; i += 256) {
+        const int g = i / HD, dd = i % HD;
+        float M = NEG_INF;
+        for (int sp = 0; sp < nvalid; ++sp) M = fmaxf(M, base[(sp * G + g) * REC]);
+        float L = 0.f, A = 0.f;
+        for (int sp = 0; sp < nvalid; ++sp) {
+            const float* r = base + (sp * G + g) * REC;
+            const float e = expf(r[0] - M);
+            L += r[1] * e;
+            A += r[2 + dd] * e;
+        }
+        float o = A / L;
+        if (p.round_fp16) o = round_to_f16(o);
+        p.out[((int64_t)kvh * G + g) * HD + dd] = o;
+    }
+    if (t == 0) p.counters[kvh] = 0u;
+}
+
+// ---------------------------------------------------------------------------------------
+struct PrefillParams {
+    const float* q;
+    int64_t q_stride;
+    const float* k;
+    const float* v;
+    int group;
+    int64_t capacity;
+    int64_t pos0;
+    float scale;
+    float* out;
+    int64_t out_stride;
+};
+
+PE_DEV float block_max256(float v, float* lds4) {
+    v = group_max<64>(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) lds4[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(lds4[0], lds4[1]), fmaxf(lds4[2], lds4[3]));
+}
+PE_DEV float block_sum256(float v, float* lds4) {
+    v = group_sum<64>(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) lds4[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return ((lds4[0] + lds4[1]) + lds4[2]) + lds4[3];
+}
+
+// One workgroup per (query token, query head); keys in chunks of 256 with an online softmax.
+template <int HD>
+__global__ __launch_bounds__(256) void k_prefill_attn(PrefillParams p) {
+    constexpr int PS = 256 / HD, NPOS = 256 / PS;
+    __shared__ float q_lds[HD];
+    __shared__ float p_lds[256];
+    __shared__ float red_lds[256];
+    __shared__ float lds4[4];
+    const int t = threadIdx.x;
+    const int64_t l = blockIdx.x;
+    const int h = blockIdx.y, kvh = h / p.group;
+    const int64_t nkeys = p.pos0 + l + 1;  // causal: keys 0..pos
+    const float* qrow = p.q + l * p.q_stride + (int64_t)h * HD;
+    const float* kbase = p.k + (int64_t)kvh * p.capacity * HD;
+    const float* vbase = p.v + (int64_t)kvh * p.capacity * HD;
+    if (t < HD) q_lds[t] = qrow[t];
+    __syncthreads();
+    const float NEG_INF = -__builtin_huge_valf();
+    const int d = t % HD, js = t / HD;
+    float M = NEG_INF, L = 0.f, acc = 0.f;
+    for (int64_t c0 = 0; c0 < nkeys; c0 += 256) {
+        const int64_t s = c0 + t;
+        float sc = NEG_INF;
+        if (s < nkeys) {
+            const float4* kr = reinterpret_cast<const float4*>(kbase + s * HD);
+            float dot = 0.f;
+#pragma unroll
+            for (int i = 0; i < HD / 4; ++i) {
+                const float4 k4 = kr[i];
+                dot += q_lds[4 * i] * k4.x + q_lds[4 * i + 1] * k4.y + q_lds[4 * i + 2] * k4.z +
+                       q_lds[4 * i + 3] * k4.w;
+            }
+            sc = dot * p.scale;
+        }
+        const float mc = block_max256(sc, lds4);
+        const float Mn = fmaxf(M, mc);
+        const float e = expf(sc - Mn);
+        const float lc = block_sum256(e, lds4);
+        const float alpha = expf(M - Mn);
+        L = L * alpha + lc;
+        p_lds[t] = e;
+        __syncthreads();
+        float part = 0.f;
+        for (int pp = 0; pp < NPOS; ++pp) {
+            const int64_t sk = c0 + js * NPOS + pp;
+            if (sk < nkeys) part += p_lds[js * NPOS + pp] * vbase[sk * HD + d];
+        }
+        acc = acc * alpha + part;
+        M = Mn;
+        __syncthreads();
+    }
+    red_lds[t] = acc;
+    __syncthreads();
+    if (t < HD) {
+        float a = 0.f;
+#pragma unroll
+        for (int j = 0; j < PS; ++j) a += red_lds[j * HD + t];
+        p.out[l * p.out_stride + (int64_t)h * HD + t] = a / L;
+    }
+}
+
+}  // namespace pe
+
+using namespace pe;
+
+static int64_t attn_nsplit(int64_t capacity) { return (capacity + kChunk - 1) / kChunk; }
+
+extern "C" int64_t pe_decode_attn_workspace_bytes(int n_head, int n_kv, int head_dim,
+                                                  int64_t capacity) {
+    if (n_head <= 0 || n_kv <= 0 || n_kv > 64 || n_head % n_kv || n_head / n_kv > kMaxGroup ||
+        (head_dim != 64 && head_dim != 128) || capacity <= 0)
+        return -PE_ERR_SHAPE;
+    const int G = n_head / n_kv;
+    return 256 + (int64_t)n_kv * attn_nsplit(capacity) * G * (head_dim + 2) * 4;
+}
+
+extern "C" int pe_decode_attn(const float* q, const float* k_cache, const float* v_cache, int n_head,
+                              int n_kv, int head_dim, int64_t capacity, const void* len_dev,
+                              int len_dtype, int64_t len_add, float scale, int round_fp16,
+                              float* out, void* workspace, int64_t workspace_bytes,
+                              pe_stream_t stream) {
+    const int64_t need = pe_decode_attn_workspace_bytes(n_head, n_kv, head_dim, capacity);
+    if (need < 0) return (int)-need;
+    if (len_dtype < 0 || len_dtype > 2) return PE_ERR_TYPE;
+    if (attn_nsplit(capacity) > 65535) return PE_ERR_SHAPE;
+    if (!q || !k_cache || !v_cache || !out || !workspace || (len_dtype && !len_dev))
+        return PE_ERR_NULL;
+    if (workspace_bytes < need) return PE_ERR_SPACE;
+    if (!aligned(q, 4) || !aligned(k_cache, 16) || !aligned(v_cache, 4) || !aligned(out, 4) ||
+        !aligned(workspace, 16) || (len_dtype == 1 && !aligned(len_dev, 4)) ||
+        (len_dtype == 2 && !aligned(len_dev, 8)))
+        return PE_ERR_ALIGN;
+    AttnParams p{q, k_cache, v_cache, n_kv, n_head / n_kv, capacity, len_dev, len_dtype, len_add,
+                 scale, round_fp16, out, (unsigned*)workspace,
+                 (float*)((char*)workspace + 256), (int)attn_nsplit(capacity)};
+    dim3 grid((unsigned)p.nsplit, (unsigned)n_kv);
+    hipStream_t s = (hipStream_t)stream;
+    if (head_dim == 64)
+        hipLaunchKernelGGL(k_decode_attn<64>, grid, dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL(k_decode_attn<128>, grid, dim3(256), 0, s, p);
+    return launch_status();
+}
+
+extern "C" int pe_prefill_attn(const float* q, int64_t q_stride, const float* k_cache,
+                               const float* v_cache, int n_head, int n_kv, int head_dim,
+                               int64_t capacity, int64_t L, int64_t pos0, float scale, float* out,
+                               int64_t out_stride, pe_stream_t stream) {
+    if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || (head_dim != 64 && head_dim != 128) ||
+        capacity <= 0 || L < 0 || pos0 < 0 || pos0 + L > capacity || L > 0x7FFFFFFF ||
+        n_head > 65535)
+        return PE_ERR_SHAPE;
+    if (L == 0) return PE_OK;
+    if (!q || !k_cache || !v_cache || !out) return PE_ERR_NULL;
+    if (q_stride < (int64_t)n_head * head_dim || out_stride < (int64_t)n_head * head_dim)
+        return PE_ERR_SHAPE;
+    if (!aligned(q, 4) || !aligned(k_cache, 16) || !aligned(v_cache, 4) || !aligned(out, 4))
+        return PE_ERR_ALIGN;
+    PrefillParams p{q, q_stride, k_cache, v_cache, n_head / n_kv, capacity, pos0, scale, out,
+                    out_stride};
+    dim3 grid((unsigned)L, (unsigned)n_head);
+    hipStream_t s = (hipStream_t)stream;
+    if (head_dim == 64)
+        hipLaunchKernelGGL(k_prefill_attn<64>, grid, dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL(k_prefill_attn<128>, grid, dim3(256), 0, s, p);
+    return launch_status();
+}

@@ -1,0 +1,230 @@
+// Load-time kernels: bit-exact dequantization of raw GGUF blocks, the byte permutation
+// into the tiled plane layout, tiled dequantization and the embedding-row gather.
+//
+// Block formats follow the reference's dequant.py (Q5_0 :51-68, Q8_0 :71-76,
+// Q4_K :171-201, Q6_K :204-232, Q8_K :235-240). Every weight is d*q (or d*sc*q - dmin*m)
+// with exact products and at most one rounding, so any evaluation order is bit-identical
+// to the reference; fp16 fields are decoded with pe::h2f, which keeps subnormals.
+#include "pe_common.h"
+
+namespace pe {
+
+PE_DEV uint32_t rd8(const uint8_t* p) { return p[0]; }
+PE_DEV uint32_t rd16(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+PE_DEV uint32_t rd32(const uint8_t* p) { return rd16(p) | (rd16(p + 2) << 16); }
+
+// Weight e of a raw GGUF tensor (byte loads only: blocks are 2-byte aligned at best).
+PE_DEV float raw_element(int type, const uint8_t* raw, int64_t e) {
+    switch (type) {
+        case PE_TYPE_F32: return __uint_as_float(rd32(raw + 4 * e));
+        case PE_TYPE_F16: return h2f(rd16(raw + 2 * e));
+        case PE_TYPE_Q8_0: {
+            const uint8_t* b = raw + (e >> 5) * 34;
+            return (float)(int8_t)b[2 + (e & 31)] * h2f(rd16(b));
+        }
+        case PE_TYPE_Q5_0: {
+            const uint8_t* b = raw + (e >> 5) * 22;
+            const int i = (int)(e & 31);
+            const uint32_t qs = b[6 + (i & 15)];
+            const uint32_t nib = i < 16 ? (qs & 0xFu) : (qs >> 4);
+            const uint32_t code = nib | (((rd32(b + 2) >> i) & 1u) << 4);
+            return (float)((int)code - 16) * h2f(rd16(b));
+        }
+        case PE_TYPE_Q4_K: {
+            const uint8_t* b = raw + (e >> 8) * 144;
+            const int r = (int)(e & 255), j = r >> 5;
+            const uint32_t byte = b[16 + 32 * (j >> 1) + (r & 31)];
+            const uint32_t nib = (j & 1) ? (byte >> 4) : (byte & 0xFu);
+            int sc, mn;
+            k4_scale_min(b + 4, j, sc, mn);
+            const float a = (float)sc * h2f(rd16(b));
+            const float m = (float)mn * h2f(rd16(b + 2));
+            return a * (float)nib - m;
+        }
+        case PE_TYPE_Q6_K: {
+            const uint8_t* b = raw + (e >> 8) * 210;
+            const int r = (int)(e & 255), h = r >> 7, quarter = (r & 127) >> 5, l = r & 31;
+            const uint32_t lb = b[64 * h + l + ((quarter & 1) ? 32 : 0)];
+            const uint32_t low4 = quarter < 2 ? (lb & 0xFu) : (lb >> 4);
+            const uint32_t high2 = (b[128 + 32 * h + l] >> (2 * quarter)) & 3u;
+            const int code = (int)(low4 | (high2 << 4)) - 32;
+            const int s = (int)(int8_t)b[192 + 8 * h + (l >> 4) + 2 * quarter];
+            const float ds = h2f(rd16(b + 208)) * (float)s;  // exact
+            return ds * (float)code;                          // one rounding
+        }
+        case PE_TYPE_Q8_K: {
+            const uint8_t* b = raw + (e >> 8) * 292;
+            return (float)(int8_t)b[4 + (e & 255)] * __uint_as_float(rd32(b));
+        }
+        default: return __uint_as_float(0x7FC00000u);
+    }
+}
+
+__global__ void k_dequant_raw(int type, const uint8_t* __restrict__ raw, float* __restrict__ out,
+                              int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += stride)
+        out[e] = raw_element(type, raw, e);
+}
+
+// One thread per block: scatter the block's fields into their planes.
+__global__ void k_repack(int type, const uint8_t* __restrict__ raw, uint8_t* __restrict__ tiled,
+                         int64_t nblk) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk; b += stride) {
+        switch (type) {
+            case PE_TYPE_Q8_0: {
+                const uint8_t* s = raw + b * 34;
+                uint8_t* q = tiled + b * 32;
+                for (int i = 0; i < 32; ++i) q[i] = s[2 + i];
+                uint8_t* d = tiled + nblk * 32 + b * 2;
+                d[0] = s[0]; d[1] = s[1];
+            } break;
+            case PE_TYPE_Q5_0: {
+                const uint8_t* s = raw + b * 22;
+                uint8_t* q = tiled + b * 16;
+                for (int i = 0; i < 16; ++i) q[i] = s[6 + i];
+                uint8_t* h = tiled + nblk * 16 + b * 4;
+                for (int i = 0; i < 4; ++i) h[i] = s[2 + i];
+                uint8_t* d = tiled + nblk * 20 + b * 2;
+                d[0] = s[0]; d[1] = s[1];
+            } break;
+            case PE_TYPE_Q4_K: {
+                const uint8_t* s = raw + b * 144;
+                uint8_t* q = tiled + b * 128;
+                for (int i = 0; i < 128; ++i) q[i] = s[16 + i];
+                uint8_t* hd = tiled + nblk * 128 + b * 16;
+                for (int i = 0; i < 16; ++i) hd[i] = s[i];
+            } break;
+            case PE_TYPE_Q6_K: {
+                const uint8_t* s = raw + b * 210;
+                uint8_t* l = tiled + b * 128;
+                for (int i = 0; i < 128; ++i) l[i] = s[i];
+                uint8_t* h = tiled + nblk * 128 + b * 64;
+                for (int i = 0; i < 64; ++i) h[i] = s[128 + i];
+                uint8_t* sc = tiled + nblk * 192 + b * 16;
+                for (int i = 0; i < 16; ++i) sc[i] = s[192 + i];
+                uint8_t* d = tiled + nblk * 208 + b * 2;
+                d[0] = s[208]; d[1] = s[209];
+            } break;
+            default: break;
+        }
+    }
+}
+
+// One thread per (row, unit): decode through Fmt<T>::load/dequant, the GEMV's own path.
+template <int T>
+__global__ void k_dequant_tiled(Tiled t, int64_t k, float* __restrict__ out) {
+    const int units = (int)(k / 32);
+    const int64_t total = t.nrows * units;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
+        const int64_t row = idx / units;
+        const int u = (int)(idx % units);
+        typename Fmt<T>::Raw r;
+        Fmt<T>::load(t, row, u, r);
+        float w[32];
+        Fmt<T>::dequant(r, w);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) out[row * k + 32 * u + i] = w[i];
+    }
+}
+
+__global__ void k_embed_gather(int type, const uint8_t* __restrict__ table, int64_t vocab,
+                               int64_t hidden, const int64_t* __restrict__ ids, int64_t n_ids,
+                               float* __restrict__ out) {
+    const int64_t total = n_ids * hidden;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const int64_t l = i / hidden, c = i % hidden;
+        const int64_t id = ids[l];
+        out[i] = (id >= 0 && id < vocab) ? raw_element(type, table, id * hidden + c)
+                                         : __uint_as_float(0x7FC00000u);
+    }
+}
+
+static int grid_for(int64_t n, int block) {
+    int64_t g = (n + block - 1) / block;
+    if (g > 65536) g = 65536;
+    return (int)(g < 1 ? 1 : g);
+}
+
+}  // namespace pe
+
+using namespace pe;
+
+extern "C" int64_t pe_nbytes_for(int type, int64_t n) {
+    const int64_t qk = block_elems(type);
+    if (qk == 0) return -PE_ERR_TYPE;
+    if (n < 0 || n % qk) return -PE_ERR_SHAPE;
+    return (n / qk) * block_bytes(type);
+}
+
+extern "C" int pe_dequant(int type, const void* blocks, float* out, int64_t n, pe_stream_t stream) {
+    if (block_elems(type) == 0) return PE_ERR_TYPE;
+    if (n < 0 || n % block_elems(type)) return PE_ERR_SHAPE;
+    if (n == 0) return PE_OK;
+    if (!blocks || !out) return PE_ERR_NULL;
+    if (!aligned(out, 4)) return PE_ERR_ALIGN;
+    hipLaunchKernelGGL(k_dequant_raw, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t)stream,
+                       type, (const uint8_t*)blocks, out, n);
+    return launch_status();
+}
+
+extern "C" int pe_repack(int type, const void* blocks, void* tiled, int64_t n_rows, int64_t k,
+                         pe_stream_t stream) {
+    if (!is_tiled_type(type)) return PE_ERR_TYPE;
+    if (n_rows <= 0 || k <= 0 || k % block_elems(type)) return PE_ERR_SHAPE;
+    if (!blocks || !tiled) return PE_ERR_NULL;
+    if (!aligned(tiled, 16)) return PE_ERR_ALIGN;
+    const int64_t nblk = n_rows * (k / block_elems(type));
+    hipLaunchKernelGGL(k_repack, dim3(grid_for(nblk, 256)), dim3(256), 0, (hipStream_t)stream,
+                       type, (const uint8_t*)blocks, (uint8_t*)tiled, nblk);
+    return launch_status();
+}
+
+extern "C" int pe_dequant_tiled(int type, const void* tiled, float* out, int64_t n_rows, int64_t k,
+                                pe_stream_t stream) {
+    if (!is_tiled_type(type)) return PE_ERR_TYPE;
+    if (n_rows <= 0 || k <= 0 || k % block_elems(type)) return PE_ERR_SHAPE;
+    if (!tiled || !out) return PE_ERR_NULL;
+    if (!aligned(tiled, 16) || !aligned(out, 4)) return PE_ERR_ALIGN;
+    Tiled t{(const uint8_t*)tiled, n_rows, k / block_elems(type)};
+    const int grid = grid_for(n_rows * (k / 32), 256);
+    hipStream_t s = (hipStream_t)stream;
+    switch (type) {
+        case PE_TYPE_Q8_0: hipLaunchKernelGGL(k_dequant_tiled<PE_TYPE_Q8_0>, dim3(grid), dim3(256), 0, s, t, k, out); break;
+        case PE_TYPE_Q5_0: hipLaunchKernelGGL(k_dequant_tiled<PE_TYPE_Q5_0>, dim3(grid), dim3(256), 0, s, t, k, out); break;
+        case PE_TYPE_Q4_K: hipLaunchKernelGGL(k_dequant_tiled<PE_TYPE_Q4_K>, dim3(grid), dim3(256), 0, s, t, k, out); break;
+        case PE_TYPE_Q6_K: hipLaunchKernelGGL(k_dequant_tiled<PE_TYPE_Q6_K>, dim3(grid), dim3(256), 0, s, t, k, out); break;
+    }
+    return launch_status();
+}
+
+extern "C" int pe_embed_gather(int type, const void* table, int64_t vocab, int64_t hidden,
+                               const int64_t* ids, int64_t n_ids, float* out, pe_stream_t stream) {
+    if (block_elems(type) == 0) return PE_ERR_TYPE;
+    if (vocab <= 0 || hidden <= 0 || n_ids < 0 || hidden % block_elems(type)) return PE_ERR_SHAPE;
+    if (n_ids == 0) return PE_OK;
+    if (!table || !ids || !out) return PE_ERR_NULL;
+    if (!aligned(ids, 8) || !aligned(out, 4)) return PE_ERR_ALIGN;
+    hipLaunchKernelGGL(k_embed_gather, dim3(grid_for(n_ids * hidden, 256)), dim3(256), 0,
+                       (hipStream_t)stream, type, (const uint8_t*)table, vocab, hidden, ids, n_ids,
+                       out);
+    return launch_status();
+}
+
+extern "C" const char* pe_strerror(int status) {
+    switch (status) {
+        case PE_OK: return "ok";
+        case PE_ERR_NULL: return "a required pointer is NULL";
+        case PE_ERR_TYPE: return "ggml type not supported by this entry point";
+        case PE_ERR_SHAPE: return "invalid size (non-positive, not whole blocks, or too large)";
+        case PE_ERR_ALIGN: return "pointer not aligned as required";
+        case PE_ERR_LAUNCH: return "HIP kernel launch failed";
+        case PE_ERR_SPACE: return "workspace too small";
+        default: return "unknown pe_status";
+    }
+}
+
+extern "C" int pe_abi_version(void) { return 1; }

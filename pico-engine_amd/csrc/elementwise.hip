@@ -1,0 +1,137 @@
+// Row-wise and element-wise kernels of the general (prefill / API) path:
+//   rmsnorm   kernels.py:14-34   y = x * (1 / sqrt(sum(x^2)/n + eps)) * w
+//   rope      kernels.py:37-59   rotate-half: [x1 c - x2 s, x1 s + x2 c]
+//   silu_mul  kernels.py:62-87   silu(g) * u from [gate | up] rows
+//   kv write  model.py:194-197   cache[:, pos0:pos0+L] = k, v
+// All accept row strides, so strided views (e.g. q/k inside the fused qkv rows) need no copy.
+#include "pe_common.h"
+
+namespace pe {
+
+__global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x, int64_t xs,
+                                                 const float* __restrict__ w, float* __restrict__ y,
+                                                 int64_t ys, int64_t n, float eps) {
+    __shared__ float lds4[4];
+    const int64_t r = blockIdx.x;
+    const float* xr = x + r * xs;
+    float ss = 0.f;
+    for (int64_t i = threadIdx.x; i < n; i += 256) ss += xr[i] * xr[i];
+    ss = group_sum<64>(ss);
+    if ((threadIdx.x & 63) == 0) lds4[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = ((lds4[0] + lds4[1]) + lds4[2]) + lds4[3];
+    const float rstd = 1.0f / sqrtf(ss / (float)n + eps);
+    float* yr = y + r * ys;
+    for (int64_t i = threadIdx.x; i < n; i += 256) yr[i] = (xr[i] * rstd) * w[i];
+}
+
+__global__ void k_rope(const float* __restrict__ x, int64_t xs, const float* __restrict__ cs,
+                       const float* __restrict__ sn, float* y, int64_t ys, int64_t L, int n_head,
+                       int hd) {
+    const int half = hd / 2;
+    const int64_t total = L * n_head * half;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
+        const int j = (int)(idx % half);
+        const int64_t lh = idx / half;
+        const int h = (int)(lh % n_head);
+        const int64_t l = lh / n_head;
+        const float* xp = x + l * xs + (int64_t)h * hd;
+        const float x1 = xp[j], x2 = xp[j + half];
+        const float c = cs[l * half + j], s = sn[l * half + j];
+        float* yp = y + l * ys + (int64_t)h * hd;
+        yp[j] = x1 * c - x2 * s;
+        yp[j + half] = x1 * s + x2 * c;
+    }
+}
+
+__global__ void k_silu_mul(const float* __restrict__ gu, int64_t gs, float* __restrict__ out,
+                           int64_t os, int64_t L, int64_t ffn) {
+    const int64_t total = L * ffn;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
+        const int64_t l = idx / ffn, j = idx % ffn;
+        const float g = gu[l * gs + j], u = gu[l * gs + ffn + j];
+        out[l * os + j] = (g * (1.0f / (1.0f + expf(-g)))) * u;
+    }
+}
+
+__global__ void k_kv_write(const float* __restrict__ ks, const float* __restrict__ vs, int64_t ss,
+                           int n_kv, int hd, int64_t L, int64_t pos0, float* kc, float* vc,
+                           int64_t cap) {
+    const int64_t total = L * n_kv * hd;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
+        const int d = (int)(idx % hd);
+        const int64_t lh = idx / hd;
+        const int h = (int)(lh % n_kv);
+        const int64_t l = lh / n_kv;
+        const int64_t dst = ((int64_t)h * cap + pos0 + l) * hd + d;
+        kc[dst] = ks[l * ss + (int64_t)h * hd + d];
+        vc[dst] = vs[l * ss + (int64_t)h * hd + d];
+    }
+}
+
+static unsigned grid1d(int64_t n) {
+    int64_t g = (n + 255) / 256;
+    if (g > 65536) g = 65536;
+    return (unsigned)(g < 1 ? 1 : g);
+}
+
+}  // namespace pe
+
+using namespace pe;
+
+extern "C" int pe_rmsnorm(const float* x, int64_t x_stride, const float* w, float* y,
+                          int64_t y_stride, int64_t rows, int64_t n, float eps, pe_stream_t stream) {
+    if (rows < 0 || n <= 0 || x_stride < n || y_stride < n || rows > 0x7FFFFFFF) return PE_ERR_SHAPE;
+    if (rows == 0) return PE_OK;
+    if (!x || !w || !y) return PE_ERR_NULL;
+    if (!aligned(x, 4) || !aligned(w, 4) || !aligned(y, 4)) return PE_ERR_ALIGN;
+    hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, x,
+                       x_stride, w, y, y_stride, n, eps);
+    return launch_status();
+}
+
+extern "C" int pe_rope(const float* x, int64_t x_stride, const float* cos_rows,
+                       const float* sin_rows, float* y, int64_t y_stride, int64_t L, int n_head,
+                       int head_dim, pe_stream_t stream) {
+    if (L < 0 || n_head <= 0 || head_dim <= 0 || head_dim % 2) return PE_ERR_SHAPE;
+    if (x_stride < (int64_t)n_head * head_dim || y_stride < (int64_t)n_head * head_dim)
+        return PE_ERR_SHAPE;
+    if (L == 0) return PE_OK;
+    if (!x || !cos_rows || !sin_rows || !y) return PE_ERR_NULL;
+    if (!aligned(x, 4) || !aligned(y, 4) || !aligned(cos_rows, 4) || !aligned(sin_rows, 4))
+        return PE_ERR_ALIGN;
+    hipLaunchKernelGGL(k_rope, dim3(grid1d(L * n_head * (head_dim / 2))), dim3(256), 0,
+                       (hipStream_t)stream, x, x_stride, cos_rows, sin_rows, y, y_stride, L, n_head,
+                       head_dim);
+    return launch_status();
+}
+
+extern "C" int pe_silu_mul(const float* gate_up, int64_t gu_stride, float* out, int64_t out_stride,
+                           int64_t L, int64_t ffn, pe_stream_t stream) {
+    if (L < 0 || ffn <= 0 || gu_stride < 2 * ffn || out_stride < ffn) return PE_ERR_SHAPE;
+    if (L == 0) return PE_OK;
+    if (!gate_up || !out) return PE_ERR_NULL;
+    if (!aligned(gate_up, 4) || !aligned(out, 4)) return PE_ERR_ALIGN;
+    hipLaunchKernelGGL(k_silu_mul, dim3(grid1d(L * ffn)), dim3(256), 0, (hipStream_t)stream,
+                       gate_up, gu_stride, out, out_stride, L, ffn);
+    return launch_status();
+}
+
+extern "C" int pe_kv_write(const float* k_src, const float* v_src, int64_t src_stride, int n_kv,
+                           int head_dim, int64_t L, int64_t pos0, float* k_cache, float* v_cache,
+                           int64_t capacity, pe_stream_t stream) {
+    if (L < 0 || n_kv <= 0 || head_dim <= 0 || pos0 < 0 || capacity <= 0 || pos0 + L > capacity ||
+        src_stride < (int64_t)n_kv * head_dim)
+        return PE_ERR_SHAPE;
+    if (L == 0) return PE_OK;
+    if (!k_src || !v_src || !k_cache || !v_cache) return PE_ERR_NULL;
+    if (!aligned(k_src, 4) || !aligned(v_src, 4) || !aligned(k_cache, 4) || !aligned(v_cache, 4))
+        return PE_ERR_ALIGN;
+    hipLaunchKernelGGL(k_kv_write, dim3(grid1d(L * n_kv * head_dim)), dim3(256), 0,
+                       (hipStream_t)stream, k_src, v_src, src_stride, n_kv, head_dim, L, pos0,
+                       k_cache, v_cache, capacity);
+    return launch_status();
+}

@@ -1,0 +1,88 @@
+// C entry points of the dequant-GEMV / small-M GEMM kernels (host validation + dispatch).
+#include "gemv_impl.h"
+
+namespace pe {
+
+static int dispatch_gemv(int type, const GemvArgs& a, bool norm, int mode, hipStream_t s) {
+    switch (type) {
+        case PE_TYPE_Q8_0: return gemv_q8_0(a, norm, mode, s);
+        case PE_TYPE_Q5_0: return gemv_q5_0(a, norm, mode, s);
+        case PE_TYPE_Q4_K: return gemv_q4_k(a, norm, mode, s);
+        case PE_TYPE_Q6_K: return gemv_q6_k(a, norm, mode, s);
+        default: return PE_ERR_TYPE;
+    }
+}
+
+static int check_weight(int type, const void* w, int64_t n_rows, int64_t k) {
+    if (!is_tiled_type(type)) return PE_ERR_TYPE;
+    if (n_rows <= 0 || k <= 0 || k % block_elems(type)) return PE_ERR_SHAPE;
+    Shape sh;
+    if (!pick_shape(k / 32, sh)) return PE_ERR_SHAPE;
+    if (!w) return PE_ERR_NULL;
+    if (!aligned(w, 16)) return PE_ERR_ALIGN;
+    return PE_OK;
+}
+
+}  // namespace pe
+
+using namespace pe;
+
+extern "C" int pe_qgemv(int type, const void* w, int64_t n_rows, int64_t k, const float* x,
+                        const float* residual, const float* bias, float* y, pe_stream_t stream) {
+    int st = check_weight(type, w, n_rows, k);
+    if (st) return st;
+    if (!x || !y) return PE_ERR_NULL;
+    if (!aligned(x, 16) || !aligned(y, 4) || !aligned(residual, 4) || !aligned(bias, 4))
+        return PE_ERR_ALIGN;
+    GemvArgs a{Tiled{(const uint8_t*)w, n_rows, k / block_elems(type)},
+               n_rows, k, x, nullptr, 0.f, residual, bias, y, 0};
+    return dispatch_gemv(type, a, false, kModePlain, (hipStream_t)stream);
+}
+
+extern "C" int pe_qgemv_rmsnorm(int type, const void* w, int64_t n_rows, int64_t k, const float* x,
+                                const float* norm_w, float eps, float* y, pe_stream_t stream) {
+    int st = check_weight(type, w, n_rows, k);
+    if (st) return st;
+    if (!x || !norm_w || !y) return PE_ERR_NULL;
+    if (!aligned(x, 16) || !aligned(norm_w, 16) || !aligned(y, 4)) return PE_ERR_ALIGN;
+    GemvArgs a{Tiled{(const uint8_t*)w, n_rows, k / block_elems(type)},
+               n_rows, k, x, norm_w, eps, nullptr, nullptr, y, 0};
+    return dispatch_gemv(type, a, true, kModePlain, (hipStream_t)stream);
+}
+
+extern "C" int pe_qgemv_rmsnorm_silu(int type, const void* w, int64_t ffn, int64_t k,
+                                     const float* x, const float* norm_w, float eps, float* act,
+                                     pe_stream_t stream) {
+    int st = check_weight(type, w, 2 * ffn, k);
+    if (st) return st;
+    if (!x || !act) return PE_ERR_NULL;
+    if (!aligned(x, 16) || !aligned(norm_w, 16) || !aligned(act, 4)) return PE_ERR_ALIGN;
+    GemvArgs a{Tiled{(const uint8_t*)w, 2 * ffn, k / block_elems(type)},
+               ffn, k, x, norm_w, eps, nullptr, nullptr, act, ffn};
+    return dispatch_gemv(type, a, norm_w != nullptr, kModeSilu, (hipStream_t)stream);
+}
+
+extern "C" int pe_qgemm(int type, const void* w, int64_t n_rows, int64_t k, const float* x,
+                        int64_t x_stride, int64_t m, const float* bias, const float* residual,
+                        int64_t res_stride, float* y, int64_t y_stride, pe_stream_t stream) {
+    int st = check_weight(type, w, n_rows, k);
+    if (st) return st;
+    if (m < 0) return PE_ERR_SHAPE;
+    if (m == 0) return PE_OK;
+    if (m > 65535LL * kGemmMT) return PE_ERR_SHAPE;
+    if (!x || !y) return PE_ERR_NULL;
+    if (x_stride < k || y_stride < n_rows || (residual && res_stride < n_rows)) return PE_ERR_SHAPE;
+    if (!aligned(x, 16) || x_stride % 4 || !aligned(y, 4) || !aligned(residual, 4) ||
+        !aligned(bias, 4))
+        return PE_ERR_ALIGN;
+    GemmArgs a{Tiled{(const uint8_t*)w, n_rows, k / block_elems(type)},
+               n_rows, k, m, x, x_stride, bias, residual, res_stride, y, y_stride};
+    hipStream_t s = (hipStream_t)stream;
+    switch (type) {
+        case PE_TYPE_Q8_0: return gemm_q8_0(a, s);
+        case PE_TYPE_Q5_0: return gemm_q5_0(a, s);
+        case PE_TYPE_Q4_K: return gemm_q4_k(a, s);
+        case PE_TYPE_Q6_K: return gemm_q6_k(a, s);
+        default: return PE_ERR_TYPE;
+    }
+}

@@ -1,0 +1,302 @@
+// Shared device helpers for libpico_hip (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "pico_hip.h"
+
+#define PE_DEV __device__ __forceinline__
+
+namespace pe {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------------------
+// fp16 bit pattern -> fp32, decoded from the bit fields with integer ops, so the result
+// never depends on the shader's fp16 denormal mode: subnormal scales (|d| < 2^-14, which
+// N(0, 0.02) weights produce in Q4_K/Q6_K blocks) decode exactly.
+PE_DEV float h2f(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16;
+    const uint32_t em = h & 0x7FFFu;
+    if (em >= 0x7C00u) return __uint_as_float(sign | 0x7F800000u | ((em & 0x3FFu) << 13));
+    if (em >= 0x0400u) return __uint_as_float(sign | ((em << 13) + (112u << 23)));
+    // zero / subnormal: em * 2^-24, exact in fp32
+    const float mag = (float)em * 5.9604644775390625e-8f;
+    return __uint_as_float(sign | __float_as_uint(mag));
+}
+
+// fp32 -> fp16 (round to nearest even) -> fp32, for the reference's fp16 output rounding.
+PE_DEV float round_to_f16(float v) { return __half2float(__float2half_rn(v)); }
+
+// Sum over aligned groups of W lanes (W a power of two <= 64) by butterfly; every lane of
+// a group ends with the same bits (IEEE addition is commutative).
+template <int W>
+PE_DEV float group_sum(float v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+template <int W>
+PE_DEV float group_max(float v) {
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+PE_DEV int sext8(uint32_t w, int byte) { return (int)(int8_t)((w >> (8 * byte)) & 0xFFu); }
+PE_DEV uint32_t ubyte(uint32_t w, int byte) { return (w >> (8 * byte)) & 0xFFu; }
+
+PE_DEV uint32_t word_of(const int4& v, int i) {
+    return (uint32_t)(i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w);
+}
+
+// 6-bit scale and min of sub-block j (0..7) from the 12 packed Q4_K scale bytes
+// (same packing as dequant.py:171-179). s[] holds the 12 bytes.
+PE_DEV void k4_scale_min(const uint8_t* s, int j, int& sc, int& mn) {
+    if (j < 4) {
+        sc = s[j] & 63;
+        mn = s[j + 4] & 63;
+    } else {
+        sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+        mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// Tiled weight planes. A "unit" is 32 consecutive weights of one row (k indices 32u..32u+31)
+// that one lane decodes at a time; units per row = k / 32 for every format, so the activation
+// layout in registers is the same whatever the mix of formats.
+struct Tiled {
+    const uint8_t* base;
+    int64_t nrows;  // rows of the whole tiled tensor (planes span all rows)
+    int64_t nb;     // blocks per row
+};
+
+template <int T>
+struct Fmt;
+
+// Q8_0: block = 32 weights = one unit.  qs[N][nb][32] | d[N][nb]
+template <>
+struct Fmt<PE_TYPE_Q8_0> {
+    static constexpr int QK = 32, BYTES = 34;
+    struct Raw {
+        int4 a, b;
+        uint32_t d;
+    };
+    static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
+        const int64_t blk = row * t.nb + u;
+        const int4* q = reinterpret_cast<const int4*>(t.base + blk * 32);
+        r.a = q[0];
+        r.b = q[1];
+        r.d = reinterpret_cast<const uint16_t*>(t.base + t.nrows * t.nb * 32)[blk];
+    }
+    static PE_DEV int code(const Raw& r, int i) {
+        const int4& v = i < 16 ? r.a : r.b;
+        return sext8(word_of(v, (i & 15) >> 2), i & 3);
+    }
+    static PE_DEV float dot(const Raw& r, const float* x) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) acc += (float)code(r, i) * x[i];
+        return acc * h2f(r.d);
+    }
+    static PE_DEV void dequant(const Raw& r, float* w) {
+        const float d = h2f(r.d);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) w[i] = (float)code(r, i) * d;
+    }
+};
+
+// Q5_0: block = 32 weights = one unit.  qs[N][nb][16] | qh u32[N][nb] | d[N][nb]
+template <>
+struct Fmt<PE_TYPE_Q5_0> {
+    static constexpr int QK = 32, BYTES = 22;
+    struct Raw {
+        int4 qs;
+        uint32_t qh;
+        uint32_t d;
+    };
+    static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
+        const int64_t blk = row * t.nb + u;
+        const int64_t nblk = t.nrows * t.nb;
+        r.qs = *reinterpret_cast<const int4*>(t.base + blk * 16);
+        r.qh = reinterpret_cast<const uint32_t*>(t.base + nblk * 16)[blk];
+        r.d = reinterpret_cast<const uint16_t*>(t.base + nblk * 20)[blk];
+    }
+    // 5-bit code of element e (0..31): nibble of qs[e % 16] (low for e < 16), 5th bit = qh bit e
+    static PE_DEV int code(const Raw& r, int e) {
+        const int j = e & 15;
+        const uint32_t byte = ubyte(word_of(r.qs, j >> 2), j & 3);
+        const uint32_t nib = e < 16 ? (byte & 0xFu) : (byte >> 4);
+        return (int)(nib | (((r.qh >> e) & 1u) << 4));
+    }
+    static PE_DEV float dot(const Raw& r, const float* x) {
+        float acc = 0.f;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) acc += (float)(code(r, e) - 16) * x[e];
+        return acc * h2f(r.d);
+    }
+    static PE_DEV void dequant(const Raw& r, float* w) {
+        const float d = h2f(r.d);
+#pragma unroll
+        for (int e = 0; e < 32; ++e) w[e] = (float)(code(r, e) - 16) * d;
+    }
+};
+
+// Q4_K: super-block of 256 = 8 units. qs[N][nb][128] | head[N][nb][16]
+// Unit u = sub-block j = u%8 of super-block s = u/8: weights 256s + 32j + i (i < 32) are the
+// low (j even) or high (j odd) nibbles of qs bytes [32*(j/2), +32); w = (d*sc_j)*nib - dmin*m_j.
+template <>
+struct Fmt<PE_TYPE_Q4_K> {
+    static constexpr int QK = 256, BYTES = 144;
+    struct Raw {
+        int4 lo, hi;  // the 32 qs bytes of the unit's chunk
+        int4 head;    // d, dmin, scales[12]
+        int sub;      // j
+    };
+    static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
+        const int64_t blk = row * t.nb + (u >> 3);
+        const int j = u & 7;
+        const int4* q = reinterpret_cast<const int4*>(t.base + blk * 128 + 32 * (j >> 1));
+        r.lo = q[0];
+        r.hi = q[1];
+        r.head = *reinterpret_cast<const int4*>(t.base + t.nrows * t.nb * 128 + blk * 16);
+        r.sub = j;
+    }
+    static PE_DEV void scales(const Raw& r, float& a, float& m) {
+        uint8_t s[12];
+#pragma unroll
+        for (int i = 0; i < 12; ++i) s[i] = (uint8_t)ubyte(word_of(r.head, 1 + (i >> 2)), i & 3);
+        int sc, mn;
+        k4_scale_min(s, r.sub, sc, mn);
+        a = (float)sc * h2f((uint32_t)r.head.x & 0xFFFFu);  // exact: 6-bit x 11-bit
+        m = (float)mn * h2f((uint32_t)r.head.x >> 16);      // exact
+    }
+    static PE_DEV uint32_t nib(const Raw& r, int i) {
+        const int4& v = i < 16 ? r.lo : r.hi;
+        const uint32_t b = ubyte(word_of(v, (i & 15) >> 2), i & 3);
+        return (r.sub & 1) ? (b >> 4) : (b & 0xFu);
+    }
+    static PE_DEV float dot(const Raw& r, const float* x) {
+        float a, m;
+        scales(r, a, m);
+        float dq = 0.f, sx = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            dq += (float)nib(r, i) * x[i];
+            sx += x[i];
+        }
+        return a * dq - m * sx;
+    }
+    static PE_DEV void dequant(const Raw& r, float* w) {
+        float a, m;
+        scales(r, a, m);
+#pragma unroll
+        for (int i = 0; i < 32; ++i) w[i] = a * (float)nib(r, i) - m;  // exact product, one rounding
+    }
+};
+
+// Q6_K: super-block of 256 = 8 units. ql[N][nb][128] | qh[N][nb][64] | sc[N][nb][16] | d[N][nb]
+// Unit u = quarter q = u%4 of half hf = (u%8)/4 of super-block s = u/8: weights
+// 256s + 128hf + 32q + l (l < 32) with code = (nibble of ql[64hf + 32(q&1) + l], high for q >= 2)
+// | ((qh[32hf + l] >> 2q) & 3) << 4, minus 32, and scale sc[8hf + 2q + l/16] (dequant.py:204-232).
+template <>
+struct Fmt<PE_TYPE_Q6_K> {
+    static constexpr int QK = 256, BYTES = 210;
+    struct Raw {
+        int4 l0, l1;   // 32 ql bytes
+        int4 h0, h1;   // 32 qh bytes
+        uint32_t sc;   // the two int8 scales (l < 16 in byte 0, l >= 16 in byte 1)
+        uint32_t d;
+        int q;
+    };
+    static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
+        const int64_t blk = row * t.nb + (u >> 3);
+        const int64_t nblk = t.nrows * t.nb;
+        const int hf = (u & 7) >> 2, q = u & 3;
+        const int4* L = reinterpret_cast<const int4*>(t.base + blk * 128 + 64 * hf + 32 * (q & 1));
+        const int4* H = reinterpret_cast<const int4*>(t.base + nblk * 128 + blk * 64 + 32 * hf);
+        r.l0 = L[0];
+        r.l1 = L[1];
+        r.h0 = H[0];
+        r.h1 = H[1];
+        r.sc = reinterpret_cast<const uint16_t*>(t.base + nblk * 192 + blk * 16)[4 * hf + q];
+        r.d = reinterpret_cast<const uint16_t*>(t.base + nblk * 208)[blk];
+        r.q = q;
+    }
+    static PE_DEV int code(const Raw& r, int l) {
+        const int4& lv = l < 16 ? r.l0 : r.l1;
+        const int4& hv = l < 16 ? r.h0 : r.h1;
+        const uint32_t lb = ubyte(word_of(lv, (l & 15) >> 2), l & 3);
+        const uint32_t hb = ubyte(word_of(hv, (l & 15) >> 2), l & 3);
+        const uint32_t low4 = r.q >= 2 ? (lb >> 4) : (lb & 0xFu);
+        return (int)(low4 | (((hb >> (2 * r.q)) & 3u) << 4)) - 32;
+    }
+    static PE_DEV float dot(const Raw& r, const float* x) {
+        float p0 = 0.f, p1 = 0.f;
+#pragma unroll
+        for (int l = 0; l < 16; ++l) {
+            p0 += (float)code(r, l) * x[l];
+            p1 += (float)code(r, 16 + l) * x[16 + l];
+        }
+        return h2f(r.d) * ((float)sext8(r.sc, 0) * p0 + (float)sext8(r.sc, 1) * p1);
+    }
+    static PE_DEV void dequant(const Raw& r, float* w) {
+        const float d = h2f(r.d);
+        const float ds0 = d * (float)sext8(r.sc, 0);  // exact: 11-bit x 8-bit
+        const float ds1 = d * (float)sext8(r.sc, 1);
+#pragma unroll
+        for (int l = 0; l < 16; ++l) {
+            w[l] = ds0 * (float)code(r, l);  // one rounding
+            w[16 + l] = ds1 * (float)code(r, 16 + l);
+        }
+    }
+};
+
+// Load the 32 x values of unit u (x[32u .. 32u+31], the same for every format) with
+// 16-byte loads; x must be 16-byte aligned.
+PE_DEV void load_x_unit(const float* __restrict__ x, int u, float* xr) {
+    const float4* p = reinterpret_cast<const float4*>(x + 32 * u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 v = p[i];
+        xr[4 * i + 0] = v.x;
+        xr[4 * i + 1] = v.y;
+        xr[4 * i + 2] = v.z;
+        xr[4 * i + 3] = v.w;
+    }
+}
+
+// Plane sizes of a tiled tensor in bytes (all planes together) -- same as the GGUF bytes.
+__host__ __device__ inline int64_t block_elems(int type) {
+    switch (type) {
+        case PE_TYPE_F32: case PE_TYPE_F16: return 1;
+        case PE_TYPE_Q5_0: case PE_TYPE_Q8_0: return 32;
+        case PE_TYPE_Q4_K: case PE_TYPE_Q6_K: case PE_TYPE_Q8_K: return 256;
+        default: return 0;
+    }
+}
+__host__ __device__ inline int64_t block_bytes(int type) {
+    switch (type) {
+        case PE_TYPE_F32: return 4;
+        case PE_TYPE_F16: return 2;
+        case PE_TYPE_Q5_0: return 22;
+        case PE_TYPE_Q8_0: return 34;
+        case PE_TYPE_Q4_K: return 144;
+        case PE_TYPE_Q6_K: return 210;
+        case PE_TYPE_Q8_K: return 292;
+        default: return 0;
+    }
+}
+inline bool is_tiled_type(int type) {
+    return type == PE_TYPE_Q5_0 || type == PE_TYPE_Q8_0 || type == PE_TYPE_Q4_K ||
+           type == PE_TYPE_Q6_K;
+}
+inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+inline int launch_status() { return hipGetLastError() == hipSuccess ? PE_OK : PE_ERR_LAUNCH; }
+
+}  // namespace pe

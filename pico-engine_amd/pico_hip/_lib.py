@@ -1,0 +1,98 @@
+"""ctypes binding of libpico_hip.so (the C ABI declared in include/pico_hip.h).
+
+torch is imported first on purpose: torch ships the HIP runtime (libamdhip64.so.7), and
+loading it before this library makes the dynamic linker resolve our dependency to that same
+runtime, so the streams and device pointers torch hands us are valid here. There is no
+fallback: if the library is missing, importing this module raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede the CDLL load, see above)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpico_hip.so")
+ABI_VERSION = 1
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+
+
+class PicoHipError(RuntimeError):
+    """A libpico_hip entry point returned a non-zero pe_status."""
+
+    def __init__(self, status: int, what: str):
+        self.status = status
+        super().__init__(f"{what}: {strerror(status)} (pe_status {status})")
+
+
+class QkvArgs(ctypes.Structure):
+    """Mirror of pe_qkv_args (include/pico_hip.h)."""
+
+    _fields_ = [
+        ("type_q", _I), ("type_k", _I), ("type_v", _I),
+        ("w_q", _P), ("w_k", _P), ("w_v", _P),
+        ("b_q", _P), ("b_k", _P), ("b_v", _P),
+        ("x", _P), ("norm_w", _P), ("eps", _F),
+        ("cos_tab", _P), ("sin_tab", _P), ("rope_rows", _L),
+        ("pos", _P), ("q_out", _P), ("k_cache", _P), ("v_cache", _P),
+        ("capacity", _L), ("hidden", _L),
+        ("n_head", _I), ("n_kv", _I), ("head_dim", _I),
+    ]
+
+
+_SIGNATURES = {
+    "pe_strerror": (ctypes.c_char_p, [_I]),
+    "pe_abi_version": (_I, []),
+    "pe_nbytes_for": (_L, [_I, _L]),
+    "pe_dequant": (_I, [_I, _P, _P, _L, _P]),
+    "pe_repack": (_I, [_I, _P, _P, _L, _L, _P]),
+    "pe_dequant_tiled": (_I, [_I, _P, _P, _L, _L, _P]),
+    "pe_embed_gather": (_I, [_I, _P, _L, _L, _P, _L, _P, _P]),
+    "pe_qgemv": (_I, [_I, _P, _L, _L, _P, _P, _P, _P, _P]),
+    "pe_qgemv_rmsnorm": (_I, [_I, _P, _L, _L, _P, _P, _F, _P, _P]),
+    "pe_qgemv_rmsnorm_silu": (_I, [_I, _P, _L, _L, _P, _P, _F, _P, _P]),
+    "pe_qkv_rmsnorm_rope": (_I, [ctypes.POINTER(QkvArgs), _P]),
+    "pe_decode_attn_workspace_bytes": (_L, [_I, _I, _I, _L]),
+    "pe_decode_attn": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _P, _P, _L, _P]),
+    "pe_rmsnorm": (_I, [_P, _L, _P, _P, _L, _L, _L, _F, _P]),
+    "pe_rope": (_I, [_P, _L, _P, _P, _P, _L, _L, _I, _I, _P]),
+    "pe_silu_mul": (_I, [_P, _L, _P, _L, _L, _L, _P]),
+    "pe_qgemm": (_I, [_I, _P, _L, _L, _P, _L, _L, _P, _P, _L, _P, _L, _P]),
+    "pe_kv_write": (_I, [_P, _P, _L, _I, _I, _L, _L, _P, _P, _L, _P]),
+    "pe_prefill_attn": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _L, _F, _P, _L, _P]),
+}
+
+# Every symbol include/pico_hip.h declares (checked by tests/test_abi.py).
+EXPORTED = tuple(_SIGNATURES)
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is not built; build it with `make -C pico-engine_amd -j8` "
+            "or __graft_entry__.build() (there is no CPU fallback)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.pe_abi_version() != ABI_VERSION:
+        raise ImportError(f"{LIB_PATH}: ABI version {lib.pe_abi_version()} != {ABI_VERSION}")
+    return lib
+
+
+lib = _load()
+
+
+def strerror(status: int) -> str:
+    return lib.pe_strerror(int(status)).decode()
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        raise PicoHipError(int(status), what)

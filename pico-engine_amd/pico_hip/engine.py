@@ -1,0 +1,181 @@
+"""GGUF inference engine over the pico_hip kernels (the reference's engine.py surface).
+
+``Engine(gguf_path, device="cuda")`` loads a dense Qwen2-style GGUF, ``generate(prompt, ...)``
+runs prefill + a graph-replayed decode loop. Kept from the reference (engine.py): config from
+metadata (:26-63), ``_empty_cache`` (:100-121, per layer fp32 (n_kv, capacity, hd) K/V),
+``_build_decode_graph`` (:269-294: side-stream warmups, capture, eager fallback on failure),
+``_decode_step`` (:296-306) and ``generate`` (:308-337).
+
+Loading differs on purpose: instead of dequantizing every tensor to fp32 on the host and
+unpacking the quantized ones to int8 + fp32 scales (engine.py:80-98, :198-267), the GGUF bytes
+go to the device as they are; matrices are tiled there by ``pe_repack`` (a byte permutation,
+same size), F32 norms/biases are used as they are, and the token embedding stays raw for the
+row gather. The fused [gate; up] weight is the two tensors' blocks back to back.
+"""
+
+from __future__ import annotations
+
+import warnings
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from . import kernels as K
+from .dequant import GGML_F16, GGML_F32, QUANT_TYPES
+from .gguf import load as load_gguf, read_tensor_bytes
+from .model import ModelConfig, Transformer
+from .sampler import sample as sample_token
+from .tokenizer import from_gguf as tokenizer_from_gguf
+
+
+class Engine:
+    def __init__(self, gguf_path: str | Path, device: str = "cuda", n_gpu_layers: int = 0):
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError("pico_hip runs on the GPU only (device must be cuda/HIP)")
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        self.gguf = load_gguf(gguf_path)
+        self.cfg = self._build_config()
+        self.weights, self.quant = self._load_weights()
+        self.model = Transformer(self.cfg, self.weights, self.device, self.quant)
+        self.tok = tokenizer_from_gguf(self.gguf.metadata)
+        self._graph = None
+
+    def _build_config(self) -> ModelConfig:
+        m = self.gguf.metadata
+        arch = m["general.architecture"]
+        if f"{arch}.expert_count" in m or arch == "mamba":
+            raise NotImplementedError(f"{arch}: only dense decoder models are supported")
+        n_kv = int(m[f"{arch}.attention.head_count_kv"])
+        head_dim = None
+        for t in self.gguf.tensors:
+            if t.name == "blk.0.attn_k.weight":
+                head_dim = t.shape[1] // n_kv
+                break
+        if head_dim is None:
+            raise ValueError("could not derive head_dim (no blk.0.attn_k.weight)")
+        return ModelConfig(
+            vocab_size=len(m["tokenizer.ggml.tokens"]),
+            n_layers=int(m[f"{arch}.block_count"]),
+            hidden=int(m[f"{arch}.embedding_length"]),
+            n_head=int(m[f"{arch}.attention.head_count"]),
+            n_kv_head=n_kv,
+            head_dim=head_dim,
+            ffn_dim=int(m[f"{arch}.feed_forward_length"]),
+            rope_base=float(m[f"{arch}.rope.freq_base"]),
+            eps=float(m[f"{arch}.attention.layer_norm_rms_epsilon"]),
+            context_len=int(m[f"{arch}.context_length"]),
+        )
+
+    def _upload(self, raw: np.ndarray) -> torch.Tensor:
+        return torch.from_numpy(np.ascontiguousarray(raw)).to(self.device, non_blocking=False)
+
+    def _load_weights(self):
+        weights: dict[str, torch.Tensor] = {}
+        quant: dict[str, object] = {}
+        g = self.gguf
+        by_name = {t.name: t for t in g.tensors}
+        for t in g.tensors:
+            raw = read_tensor_bytes(g, t)
+            shape = tuple(reversed(t.shape))     # logical (rows, cols), as engine.py:92-94
+            if t.name == "token_embd.weight":
+                quant["token_embd"] = K.RawTensor(self._upload(raw), t.ggml_type, shape)
+                continue
+            if t.ggml_type in (GGML_F32, GGML_F16):
+                w = K.dequantize(t.ggml_type, self._upload(raw), t.n_elements).reshape(shape)
+                weights[t.name] = w
+                continue
+            if t.ggml_type not in QUANT_TYPES or len(shape) != 2:
+                raise NotImplementedError(f"{t.name}: ggml type {t.ggml_type} shape {shape}")
+            quant[t.name] = K.pack_weight(self._upload(raw), t.ggml_type, shape[0], shape[1])
+        # fused [gate; up] when both halves share a format (engine.py:224-242, all formats)
+        for i in range(self.cfg.n_layers):
+            gt, ut = by_name[f"blk.{i}.ffn_gate.weight"], by_name[f"blk.{i}.ffn_up.weight"]
+            if gt.ggml_type == ut.ggml_type and gt.shape == ut.shape:
+                both = np.concatenate([read_tensor_bytes(g, gt), read_tensor_bytes(g, ut)])
+                n, k = gt.shape[1], gt.shape[0]
+                quant[f"blk.{i}.ffn_gate_up.weight"] = K.pack_weight(self._upload(both),
+                                                                     gt.ggml_type, 2 * n, k)
+        if "output.weight" in quant:
+            quant["output"] = quant["output.weight"]
+        else:  # tied embeddings without an explicit output tensor
+            e = quant["token_embd"]
+            quant["output"] = K.pack_weight(e.data, e.ggml_type, e.shape[0], e.shape[1])
+        torch.cuda.synchronize(self.device)
+        return weights, quant
+
+    def _empty_cache(self, capacity: int) -> list[tuple[torch.Tensor, torch.Tensor]]:
+        c = self.cfg
+        empty = lambda: torch.zeros(c.n_kv_head, capacity, c.head_dim, device=self.device)
+        cache = [(empty(), empty()) for _ in range(c.n_layers)]
+        self.model.attn_workspace(capacity)
+        return cache
+
+    def _build_decode_graph(self, cache):
+        """Capture the single-token decode forward into a HIP graph (engine.py:269-294).
+        Returns the graph, or None (eager fallback) if capture fails."""
+        self._static_ids = torch.zeros(1, dtype=torch.long, device=self.device)
+        self._static_pos = torch.zeros(1, dtype=torch.long, device=self.device)
+        try:
+            s = torch.cuda.Stream(self.device)
+            s.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(s):
+                for _ in range(3):
+                    self.model.forward(self._static_ids, self._static_pos, cache)
+            torch.cuda.current_stream(self.device).wait_stream(s)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._static_logits = self.model.forward(self._static_ids, self._static_pos, cache)
+            self._graph = g
+            return g
+        except Exception as e:  # noqa: BLE001 -- any capture failure falls back to eager
+            self._graph = None
+            warnings.warn(f"HIP graph capture failed; falling back to eager decode: {e}")
+            return None
+
+    def _decode_step(self, token: int, pos: int, cache, graph):
+        if graph is not None:
+            self._static_ids.fill_(int(token))
+            self._static_pos.fill_(int(pos))
+            graph.replay()
+            return self._static_logits
+        return self.model.forward(
+            torch.tensor([token], device=self.device),
+            torch.tensor([pos], device=self.device),
+            cache,
+        )
+
+    @torch.inference_mode()
+    def generate_ids(self, ids: list[int], max_tokens: int = 64, temperature: float = 0.0,
+                     top_k: int = 0, top_p: float = 1.0, use_graph: bool = True,
+                     eos_id: int | None = None) -> list[int]:
+        """Prefill ``ids`` then decode up to ``max_tokens`` tokens; returns the new ids."""
+        if not ids:
+            return []
+        eos = self.tok.eos_id if eos_id is None else eos_id
+        cache = self._empty_cache(len(ids) + max_tokens)
+        graph = self._build_decode_graph(cache) if use_graph else None
+        tokens = torch.tensor(ids, device=self.device)
+        positions = torch.arange(len(ids), device=self.device)
+        logits = self.model.forward(tokens, positions, cache)
+        generated: list[int] = []
+        for _ in range(max_tokens):
+            nxt = sample_token(logits, temperature, top_k, top_p)
+            if nxt == eos:
+                break
+            pos = len(ids) + len(generated)
+            generated.append(nxt)
+            logits = self._decode_step(nxt, pos, cache, graph)
+        return generated
+
+    @torch.inference_mode()
+    def generate(self, prompt: str, max_tokens: int = 64, temperature: float = 0.7,
+                 top_k: int = 0, top_p: float = 0.9,
+                 use_graph: bool = True) -> tuple[str, list[int]]:
+        ids = self.tok.encode(prompt)
+        if not ids:
+            return "", []
+        generated = self.generate_ids(ids, max_tokens, temperature, top_k, top_p, use_graph)
+        return self.tok.decode(generated), generated

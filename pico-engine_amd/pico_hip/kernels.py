@@ -1,0 +1,389 @@
+"""HIP kernels of the decode path, with the reference's kernels.py names.
+
+Every function launches a hand-written gfx950 kernel from libpico_hip.so through its C ABI on
+torch's current stream (so it is captured by ``torch.cuda.graph``); inputs must already be on
+the GPU -- there is no CPU fallback. Outputs are freshly allocated unless ``out=`` is given.
+
+Reference names kept (src/pico_engine/kernels.py): ``rmsnorm`` (:26), ``rope`` (:50),
+``silu_mul`` (:77), ``decode_attn`` (:129), ``q8_0_gemv`` (:178), ``q5_0_gemv`` (:211),
+``q5_0_gemv_norm`` (:253), ``q6_k_gemv`` (:286), ``q4_k_gemv`` (:326). One signature change:
+the quantized GEMVs take a ``QWeight`` (the GGUF blocks of the tensor, tiled on the device)
+instead of the reference's unpacked (int8 values, fp32 scales) tensors. New fused entry points
+used by model.py: ``qkv_rmsnorm_rope``, ``qgemv_norm_silu``, ``qgemv_norm``, plus the prefill
+kernels ``qgemm``, ``kv_write``, ``prefill_attn`` and the load-time ``dequantize``,
+``pack_weight``, ``embed_gather``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from ._lib import QkvArgs, check, lib
+from .dequant import (BLOCK_SIZE, GGML_Q4_K, GGML_Q5_0, GGML_Q6_K, GGML_Q8_0, QUANT_TYPES,
+                      TYPE_NAMES, nbytes_for)
+
+_VP = ctypes.c_void_p
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else _VP(t.data_ptr())
+
+
+def _stream(dev: torch.device):
+    return _VP(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _on_gpu(*ts: torch.Tensor | None) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError(f"pico_hip kernels need GPU tensors, got a tensor on {t.device}")
+        dev = t.device
+    return dev
+
+
+def _f32c(t: torch.Tensor) -> torch.Tensor:
+    """fp32, contiguous (16-byte aligned start as a fresh allocation guarantees)."""
+    t = t.float().contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+@dataclass
+class QWeight:
+    """A quantized (n x k) weight in the tiled plane layout (see include/pico_hip.h)."""
+
+    data: torch.Tensor  # uint8 on the device, nbytes_for(ggml_type, n*k) bytes
+    ggml_type: int
+    n: int
+    k: int
+
+    @property
+    def shape(self) -> tuple[int, int]:
+        return (self.n, self.k)
+
+    @property
+    def nbytes(self) -> int:
+        return self.data.numel()
+
+    def __repr__(self) -> str:
+        return f"QWeight({TYPE_NAMES[self.ggml_type]}, n={self.n}, k={self.k})"
+
+
+@dataclass
+class RawTensor:
+    """Raw GGUF bytes of a tensor kept untiled on the device (the embedding table)."""
+
+    data: torch.Tensor
+    ggml_type: int
+    shape: tuple[int, ...]  # logical (rows, cols)
+
+
+# ---- load-time ---------------------------------------------------------------------------
+
+def dequantize(ggml_type: int, blocks: torch.Tensor, n: int, out: torch.Tensor | None = None):
+    """Bit-exact fp32 dequantization of raw GGUF blocks (reference dequant.py:243-260)."""
+    dev = _on_gpu(blocks)
+    nbytes_for(ggml_type, n)
+    if out is None:
+        out = torch.empty(n, device=dev, dtype=torch.float32)
+    check(lib.pe_dequant(ggml_type, _ptr(blocks), _ptr(out), n, _stream(dev)), "pe_dequant")
+    return out
+
+
+def pack_weight(blocks: torch.Tensor, ggml_type: int, n: int, k: int) -> QWeight:
+    """Raw GGUF blocks of an (n x k) tensor (device uint8) -> tiled QWeight."""
+    dev = _on_gpu(blocks)
+    if ggml_type not in QUANT_TYPES:
+        raise ValueError(f"no GEMV kernel for {TYPE_NAMES.get(ggml_type, ggml_type)}")
+    size = nbytes_for(ggml_type, n * k)
+    if blocks.numel() != size:
+        raise ValueError(f"{blocks.numel()} bytes for a {n}x{k} {TYPE_NAMES[ggml_type]} tensor, expected {size}")
+    data = torch.empty(size, device=dev, dtype=torch.uint8)
+    check(lib.pe_repack(ggml_type, _ptr(blocks), _ptr(data), n, k, _stream(dev)), "pe_repack")
+    return QWeight(data, ggml_type, n, k)
+
+
+def dequantize_weight(w: QWeight) -> torch.Tensor:
+    """fp32 (n, k) from a tiled weight, through the GEMV kernels' own decode routines."""
+    out = torch.empty(w.n, w.k, device=w.data.device, dtype=torch.float32)
+    check(lib.pe_dequant_tiled(w.ggml_type, _ptr(w.data), _ptr(out), w.n, w.k,
+                               _stream(w.data.device)), "pe_dequant_tiled")
+    return out
+
+
+def embed_gather(table: RawTensor, ids: torch.Tensor, out: torch.Tensor | None = None):
+    """Rows ``ids`` of a raw GGUF (vocab, hidden) table, dequantized (model.py:152)."""
+    dev = _on_gpu(table.data, ids)
+    ids = ids.to(torch.int64).contiguous()
+    vocab, hidden = table.shape
+    if out is None:
+        out = torch.empty(ids.numel(), hidden, device=dev, dtype=torch.float32)
+    check(lib.pe_embed_gather(table.ggml_type, _ptr(table.data), vocab, hidden, _ptr(ids),
+                              ids.numel(), _ptr(out), _stream(dev)), "pe_embed_gather")
+    return out
+
+
+# ---- reference kernels -------------------------------------------------------------------
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """out = x / sqrt(mean(x^2) + eps) * weight over the last dim (kernels.py:26)."""
+    dev = _on_gpu(x, weight)
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    x2 = x2.float()
+    w = weight.float().contiguous()
+    rows, n = x2.shape
+    out = torch.empty(rows, n, device=dev, dtype=torch.float32)
+    check(lib.pe_rmsnorm(_ptr(x2), x2.stride(0), _ptr(w), _ptr(out), n, rows, n, float(eps),
+                         _stream(dev)), "pe_rmsnorm")
+    return out.reshape(x.shape).to(x.dtype)
+
+
+def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Rotate-half RoPE; x (L, n_head, hd) (row-strided views allowed), cos/sin (L, hd/2) (kernels.py:50)."""
+    dev = _on_gpu(x, cos, sin)
+    L, n_head, hd = x.shape
+    if x.dtype != torch.float32 or x.stride(2) != 1 or x.stride(1) != hd:
+        x = x.float().contiguous()
+    c, s = cos.float().contiguous(), sin.float().contiguous()
+    out = torch.empty(L, n_head, hd, device=dev, dtype=torch.float32)
+    check(lib.pe_rope(_ptr(x), x.stride(0), _ptr(c), _ptr(s), _ptr(out), n_head * hd, L, n_head,
+                      hd, _stream(dev)), "pe_rope")
+    return out
+
+
+def silu_mul(gate_up: torch.Tensor, ffn: int) -> torch.Tensor:
+    """silu(gate) * up from the (L, 2*ffn) [gate | up] tensor (kernels.py:77)."""
+    dev = _on_gpu(gate_up)
+    gu = gate_up.float()
+    if gu.dim() == 1:
+        gu = gu.unsqueeze(0)
+    if gu.stride(-1) != 1:
+        gu = gu.contiguous()
+    L = gu.shape[0]
+    out = torch.empty(L, ffn, device=dev, dtype=torch.float32)
+    check(lib.pe_silu_mul(_ptr(gu), gu.stride(0), _ptr(out), ffn, L, ffn, _stream(dev)), "pe_silu_mul")
+    return out
+
+
+def decode_attn_workspace(n_head: int, n_kv: int, hd: int, capacity: int, device) -> torch.Tensor:
+    """Zero-filled workspace for decode_attn (reusable by any number of in-order calls)."""
+    nbytes = lib.pe_decode_attn_workspace_bytes(n_head, n_kv, hd, capacity)
+    check(0 if nbytes >= 0 else -nbytes, "pe_decode_attn_workspace_bytes")
+    return torch.zeros(nbytes, device=device, dtype=torch.uint8)
+
+
+def decode_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                S: torch.Tensor | int | None = None, stride: int | None = None,
+                scale: float | None = None, *, S_offset: int = 0, round_fp16: bool = True,
+                workspace: torch.Tensor | None = None, out: torch.Tensor | None = None):
+    """Single-query GQA attention over the cache (kernels.py:129).
+
+    q (n_head, hd); k/v (n_kv, capacity, hd); valid length S (+ ``S_offset``) read on the
+    device if S is a tensor; ``stride`` (the reference's loop bound = cache capacity) defaults
+    to k.shape[1]. Output rounded to fp16 and returned as fp32 like the reference.
+    """
+    dev = _on_gpu(q, k, v)
+    q = _f32c(q)
+    n_head, hd = q.shape
+    n_kv, capacity, _ = k.shape
+    if stride is not None:
+        capacity = int(stride)
+    if k.numel() < n_kv * capacity * hd or v.numel() < n_kv * capacity * hd:
+        raise ValueError("stride exceeds the cache buffer")
+    k, v = _f32c(k), _f32c(v)
+    if scale is None:
+        scale = hd ** -0.5
+    if S is None:
+        len_dev, dtype_code, add = None, 0, capacity + S_offset
+    elif isinstance(S, int):
+        len_dev, dtype_code, add = None, 0, S + S_offset
+    else:
+        S = S.reshape(-1)
+        if S.dtype not in (torch.int32, torch.int64):
+            S = S.to(torch.int64)
+        S = S.contiguous()
+        _on_gpu(S)
+        len_dev, dtype_code, add = S, (1 if S.dtype == torch.int32 else 2), S_offset
+    if workspace is None:
+        workspace = decode_attn_workspace(n_head, n_kv, hd, capacity, dev)
+    if out is None:
+        out = torch.empty(n_head, hd, device=dev, dtype=torch.float32)
+    check(lib.pe_decode_attn(_ptr(q), _ptr(k), _ptr(v), n_head, n_kv, hd, capacity, _ptr(len_dev),
+                             dtype_code, add, float(scale), int(round_fp16), _ptr(out),
+                             _ptr(workspace), workspace.numel(), _stream(dev)), "pe_decode_attn")
+    return out
+
+
+def qgemv(x: torch.Tensor, w: QWeight, residual: torch.Tensor | None = None,
+          bias: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """y = W x (+ bias) (+ residual) for a tiled quantized W (M = 1)."""
+    dev = _on_gpu(x, w.data, residual, bias)
+    x = _f32c(x.reshape(-1))
+    if x.numel() != w.k:
+        raise ValueError(f"x has {x.numel()} elements, weight expects {w.k}")
+    res = None if residual is None else residual.reshape(-1).float().contiguous()
+    b = None if bias is None else bias.reshape(-1).float().contiguous()
+    if out is None:
+        out = torch.empty(w.n, device=dev, dtype=torch.float32)
+    check(lib.pe_qgemv(w.ggml_type, _ptr(w.data), w.n, w.k, _ptr(x), _ptr(res), _ptr(b), _ptr(out),
+                       _stream(dev)), "pe_qgemv")
+    return out
+
+
+def _typed(w: QWeight, t: int, name: str) -> QWeight:
+    if w.ggml_type != t:
+        raise ValueError(f"{name} needs a {TYPE_NAMES[t]} weight, got {TYPE_NAMES[w.ggml_type]}")
+    return w
+
+
+def q8_0_gemv(x: torch.Tensor, w: QWeight) -> torch.Tensor:
+    """Q8_0 GEMV: W x (kernels.py:178)."""
+    return qgemv(x, _typed(w, GGML_Q8_0, "q8_0_gemv"))
+
+
+def q5_0_gemv(x: torch.Tensor, w: QWeight) -> torch.Tensor:
+    """Q5_0 GEMV: W x (kernels.py:211)."""
+    return qgemv(x, _typed(w, GGML_Q5_0, "q5_0_gemv"))
+
+
+def q6_k_gemv(x: torch.Tensor, w: QWeight, residual: torch.Tensor | None = None) -> torch.Tensor:
+    """Q6_K GEMV: residual + W x (kernels.py:286)."""
+    return qgemv(x, _typed(w, GGML_Q6_K, "q6_k_gemv"), residual=residual)
+
+
+def q4_k_gemv(x: torch.Tensor, w: QWeight, residual: torch.Tensor | None = None) -> torch.Tensor:
+    """Q4_K GEMV: residual + W x (kernels.py:326)."""
+    return qgemv(x, _typed(w, GGML_Q4_K, "q4_k_gemv"), residual=residual)
+
+
+def qgemv_norm(x: torch.Tensor, weight: torch.Tensor, w: QWeight, eps: float,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """W (rmsnorm(x) * weight) in one launch, any quantized format."""
+    dev = _on_gpu(x, weight, w.data)
+    x = _f32c(x.reshape(-1))
+    nw = _f32c(weight.reshape(-1))
+    if out is None:
+        out = torch.empty(w.n, device=dev, dtype=torch.float32)
+    check(lib.pe_qgemv_rmsnorm(w.ggml_type, _ptr(w.data), w.n, w.k, _ptr(x), _ptr(nw), float(eps),
+                               _ptr(out), _stream(dev)), "pe_qgemv_rmsnorm")
+    return out
+
+
+def q5_0_gemv_norm(x: torch.Tensor, weight: torch.Tensor, w: QWeight, eps: float) -> torch.Tensor:
+    """Fused RMSNorm(x, weight) + Q5_0 GEMV (kernels.py:253)."""
+    return qgemv_norm(x, weight, _typed(w, GGML_Q5_0, "q5_0_gemv_norm"), eps)
+
+
+def qgemv_norm_silu(x: torch.Tensor, weight: torch.Tensor | None, w: QWeight, eps: float,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(g) * u with [g; u] = W (rmsnorm(x) * weight), W = [gate; up] (2*ffn rows)."""
+    dev = _on_gpu(x, weight, w.data)
+    if w.n % 2:
+        raise ValueError("gate/up weight needs an even number of rows")
+    ffn = w.n // 2
+    x = _f32c(x.reshape(-1))
+    nw = None if weight is None else _f32c(weight.reshape(-1))
+    if out is None:
+        out = torch.empty(ffn, device=dev, dtype=torch.float32)
+    check(lib.pe_qgemv_rmsnorm_silu(w.ggml_type, _ptr(w.data), ffn, w.k, _ptr(x), _ptr(nw),
+                                    float(eps), _ptr(out), _stream(dev)), "pe_qgemv_rmsnorm_silu")
+    return out
+
+
+def qkv_rmsnorm_rope(x: torch.Tensor, norm_w: torch.Tensor | None, eps: float,
+                     wq: QWeight, wk: QWeight, wv: QWeight,
+                     bq: torch.Tensor | None, bk: torch.Tensor | None, bv: torch.Tensor | None,
+                     cos_tab: torch.Tensor, sin_tab: torch.Tensor, pos: torch.Tensor,
+                     k_cache: torch.Tensor, v_cache: torch.Tensor, n_head: int,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """One decode token: q = RoPE(Wq h + bq) returned; RoPE(Wk h + bk), Wv h + bv written to
+    the caches at position ``pos`` (device int64 scalar); h = rmsnorm(x) * norm_w."""
+    dev = _on_gpu(x, norm_w, wq.data, wk.data, wv.data, pos, k_cache, v_cache)
+    n_kv, capacity, hd = k_cache.shape
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("KV caches must be contiguous (n_kv, capacity, hd) buffers")
+    if pos.dtype != torch.int64:
+        raise ValueError("pos must be an int64 device tensor")
+    x = _f32c(x.reshape(-1))
+    if out is None:
+        out = torch.empty(n_head, hd, device=dev, dtype=torch.float32)
+    a = QkvArgs(wq.ggml_type, wk.ggml_type, wv.ggml_type,
+                wq.data.data_ptr(), wk.data.data_ptr(), wv.data.data_ptr(),
+                None if bq is None else bq.data_ptr(), None if bk is None else bk.data_ptr(),
+                None if bv is None else bv.data_ptr(),
+                x.data_ptr(), None if norm_w is None else norm_w.data_ptr(), float(eps),
+                cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
+                pos.data_ptr(), out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                capacity, wq.k, n_head, n_kv, hd)
+    check(lib.pe_qkv_rmsnorm_rope(ctypes.byref(a), _stream(dev)), "pe_qkv_rmsnorm_rope")
+    return out
+
+
+# ---- prefill (M >= 1) --------------------------------------------------------------------
+
+def qgemm(x: torch.Tensor, w: QWeight, bias: torch.Tensor | None = None,
+          residual: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """y[m] = W x[m] (+ bias) (+ residual[m]) for x (M, k); out may be a column slice view."""
+    dev = _on_gpu(x, w.data, bias, residual)
+    if x.dim() == 1:
+        x = x.unsqueeze(0)
+    if x.dtype != torch.float32 or x.stride(-1) != 1 or x.stride(0) % 4 or x.data_ptr() % 16:
+        x = _f32c(x)
+    M = x.shape[0]
+    if out is None:
+        out = torch.empty(M, w.n, device=dev, dtype=torch.float32)
+    if out.stride(-1) != 1:
+        raise ValueError("out rows must be contiguous")
+    res_stride = 0
+    if residual is not None:
+        if residual.dtype != torch.float32 or residual.stride(-1) != 1:
+            residual = residual.float().contiguous()
+        res_stride = residual.stride(0) if residual.dim() == 2 else w.n
+    check(lib.pe_qgemm(w.ggml_type, _ptr(w.data), w.n, w.k, _ptr(x), x.stride(0), M, _ptr(bias),
+                       _ptr(residual), res_stride, _ptr(out), out.stride(0), _stream(dev)), "pe_qgemm")
+    return out
+
+
+def kv_write(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+             pos0: int = 0) -> None:
+    """cache[h][pos0 + l] = k[l, h] (and v); k, v (L, n_kv, hd) with contiguous rows of heads."""
+    dev = _on_gpu(k, v, k_cache, v_cache)
+    L, n_kv, hd = k.shape
+    if k.stride(2) != 1 or k.stride(1) != hd or v.stride() != k.stride():
+        k, v = k.contiguous(), v.contiguous()
+    check(lib.pe_kv_write(_ptr(k), _ptr(v), k.stride(0), n_kv, hd, L, pos0, _ptr(k_cache),
+                          _ptr(v_cache), k_cache.shape[1], _stream(dev)), "pe_kv_write")
+
+
+def prefill_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos0: int = 0,
+                 scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal GQA attention of q (L, n_head, hd) at positions pos0.. over the cache (fp32)."""
+    dev = _on_gpu(q, k_cache, v_cache)
+    L, n_head, hd = q.shape
+    n_kv, capacity, _ = k_cache.shape
+    if q.stride(2) != 1 or q.stride(1) != hd:
+        q = q.contiguous()
+    if scale is None:
+        scale = hd ** -0.5
+    if out is None:
+        out = torch.empty(L, n_head * hd, device=dev, dtype=torch.float32)
+    check(lib.pe_prefill_attn(_ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), n_head, n_kv, hd,
+                              capacity, L, pos0, float(scale), _ptr(out), out.stride(0),
+                              _stream(dev)), "pe_prefill_attn")
+    return out
+
+
+__all__ = ["QWeight", "RawTensor", "dequantize", "pack_weight", "dequantize_weight", "embed_gather",
+           "rmsnorm", "rope", "silu_mul", "decode_attn", "decode_attn_workspace", "qgemv",
+           "q8_0_gemv", "q5_0_gemv", "q5_0_gemv_norm", "q6_k_gemv", "q4_k_gemv", "qgemv_norm",
+           "qgemv_norm_silu", "qkv_rmsnorm_rope", "qgemm", "kv_write", "prefill_attn",
+           "BLOCK_SIZE"]

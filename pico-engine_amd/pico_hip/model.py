@@ -1,0 +1,169 @@
+"""Dense Qwen2 forward over the pico_hip kernels (the reference's model.py call surface).
+
+``ModelConfig`` and ``Transformer(cfg, weights, device, quant).forward(token_ids, positions,
+cache) -> logits`` keep the reference's signatures (model.py:27-57, :60-62, :128-165).
+Decode (one token) runs five fused HIP launches per layer plus two per token:
+
+  embed_gather                              model.py:152 (Q8_0 row, bit-exact)
+  per layer:
+    qkv_rmsnorm_rope   (norm+QKV+bias+RoPE+cache write)   model.py:175-193
+    decode_attn        (split-KV GQA, fp16-rounded out)   model.py:211
+    qgemv + residual   (o-projection)                     model.py:213
+    qgemv_norm_silu    (norm+gate/up+SiLU*up)             model.py:216-224
+    qgemv + residual   (ffn_down)                         model.py:225-234
+  qgemv_norm           (final norm + LM head)             model.py:159-164
+
+Prefill (L > 1) follows the reference's L > 1 branch op for op in fp32 (its off-CUDA numerics):
+rmsnorm, one small-M GEMM per QKV segment with bias, RoPE, cache write at [0, L), causal
+attention, o-projection + residual, rmsnorm, gate/up GEMM, SiLU*up, down + residual; logits
+from the last row. Every op is a HIP kernel; nothing runs on the CPU.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import kernels as K
+from .kernels import QWeight, RawTensor
+
+
+@dataclass
+class ModelConfig:
+    vocab_size: int
+    n_layers: int
+    hidden: int          # n_embd
+    n_head: int          # query heads
+    n_kv_head: int       # kv heads (GQA)
+    head_dim: int
+    ffn_dim: int
+    rope_base: float
+    eps: float           # RMSNorm epsilon
+    context_len: int
+
+
+@dataclass
+class Layer:
+    attn_norm: torch.Tensor
+    wq: QWeight
+    wk: QWeight
+    wv: QWeight
+    bq: torch.Tensor | None
+    bk: torch.Tensor | None
+    bv: torch.Tensor | None
+    wo: QWeight
+    ffn_norm: torch.Tensor
+    w_gate_up: QWeight | None   # [gate; up] when both share a format, else None
+    w_gate: QWeight
+    w_up: QWeight
+    w_down: QWeight
+
+
+class Transformer:
+    def __init__(self, cfg: ModelConfig, weights: dict[str, torch.Tensor], device: torch.device,
+                 quant: dict | None = None):
+        if torch.device(device).type != "cuda":
+            raise ValueError("pico_hip runs on the GPU only")
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.w = weights                 # name -> fp32 device tensor (norms, biases)
+        self.quant = quant or {}         # name -> QWeight / RawTensor
+        self.embed: RawTensor = self.quant["token_embd"]
+        self.output: QWeight = self.quant["output"]
+        # RoPE tables exactly as the reference builds them (model.py:73-79), on the device.
+        inv_freq = 1.0 / (cfg.rope_base ** (torch.arange(0, cfg.head_dim, 2, device=self.device)
+                                            / cfg.head_dim))
+        pos = torch.arange(cfg.context_len, device=self.device, dtype=torch.float32)
+        angles = pos[:, None] * inv_freq[None, :]
+        self.cos = angles.cos().contiguous()
+        self.sin = angles.sin().contiguous()
+        self.layers = [self._layer_weights(i) for i in range(cfg.n_layers)]
+        self._ws: dict[int, torch.Tensor] = {}
+
+    def _layer_weights(self, i: int) -> Layer:
+        p, q, w = f"blk.{i}.", self.quant, self.w
+        return Layer(
+            attn_norm=w[p + "attn_norm.weight"],
+            wq=q[p + "attn_q.weight"], wk=q[p + "attn_k.weight"], wv=q[p + "attn_v.weight"],
+            bq=w.get(p + "attn_q.bias"), bk=w.get(p + "attn_k.bias"), bv=w.get(p + "attn_v.bias"),
+            wo=q[p + "attn_output.weight"],
+            ffn_norm=w[p + "ffn_norm.weight"],
+            w_gate_up=q.get(p + "ffn_gate_up.weight"),
+            w_gate=q[p + "ffn_gate.weight"], w_up=q[p + "ffn_up.weight"],
+            w_down=q[p + "ffn_down.weight"],
+        )
+
+    def attn_workspace(self, capacity: int) -> torch.Tensor:
+        """Decode-attention workspace for a cache of ``capacity`` (shared by all layers)."""
+        ws = self._ws.get(capacity)
+        if ws is None:
+            c = self.cfg
+            ws = K.decode_attn_workspace(c.n_head, c.n_kv_head, c.head_dim, capacity, self.device)
+            self._ws[capacity] = ws
+        return ws
+
+    @torch.inference_mode()
+    def forward(self, token_ids: torch.Tensor, positions: torch.Tensor,
+                cache: list[tuple[torch.Tensor, torch.Tensor]]) -> torch.Tensor:
+        """Run ``token_ids`` (L,) at ``positions`` (L,) updating ``cache``; logits (vocab,) of
+        the last position. Decode (L == 1) reads the position from device memory only, so the
+        step can be captured once and replayed as a graph."""
+        if token_ids.shape[0] == 1:
+            return self._decode(token_ids, positions, cache)
+        return self._prefill(token_ids, positions, cache)
+
+    # ---- decode ---------------------------------------------------------------------------
+    def _decode(self, token_ids, positions, cache):
+        cfg = self.cfg
+        pos = positions.reshape(-1)[:1]
+        if pos.dtype != torch.int64:
+            pos = pos.to(torch.int64)
+        capacity = cache[0][0].shape[1]
+        ws = self.attn_workspace(capacity)
+        x = K.embed_gather(self.embed, token_ids).reshape(-1)
+        for i, L in enumerate(self.layers):
+            k_buf, v_buf = cache[i]
+            q = K.qkv_rmsnorm_rope(x, L.attn_norm, cfg.eps, L.wq, L.wk, L.wv, L.bq, L.bk, L.bv,
+                                   self.cos, self.sin, pos, k_buf, v_buf, cfg.n_head)
+            attn = K.decode_attn(q, k_buf, v_buf, S=pos, S_offset=1, workspace=ws)
+            x = K.qgemv(attn.reshape(-1), L.wo, residual=x)
+            if L.w_gate_up is not None:
+                act = K.qgemv_norm_silu(x, L.ffn_norm, L.w_gate_up, cfg.eps)
+            else:
+                g = K.qgemv_norm(x, L.ffn_norm, L.w_gate, cfg.eps)
+                u = K.qgemv_norm(x, L.ffn_norm, L.w_up, cfg.eps)
+                act = K.silu_mul(torch.cat([g, u]).unsqueeze(0), cfg.ffn_dim).reshape(-1)
+            x = K.qgemv(act, L.w_down, residual=x)
+        return K.qgemv_norm(x, self.w["output_norm.weight"], self.output, cfg.eps)
+
+    # ---- prefill --------------------------------------------------------------------------
+    def _prefill(self, token_ids, positions, cache):
+        cfg = self.cfg
+        Lt = token_ids.shape[0]
+        hd, nh, nkv = cfg.head_dim, cfg.n_head, cfg.n_kv_head
+        qd, kd = nh * hd, nkv * hd
+        cos = self.cos[positions]
+        sin = self.sin[positions]
+        x = K.embed_gather(self.embed, token_ids)                       # (L, hidden)
+        qkv = torch.empty(Lt, qd + 2 * kd, device=self.device, dtype=torch.float32)
+        for i, L in enumerate(self.layers):
+            k_buf, v_buf = cache[i]
+            h = K.rmsnorm(x, L.attn_norm, cfg.eps)
+            K.qgemm(h, L.wq, bias=L.bq, out=qkv[:, :qd])
+            K.qgemm(h, L.wk, bias=L.bk, out=qkv[:, qd:qd + kd])
+            K.qgemm(h, L.wv, bias=L.bv, out=qkv[:, qd + kd:])
+            qk = qkv[:, :qd + kd].view(Lt, nh + nkv, hd)
+            qk = K.rope(qk, cos, sin)                                     # (L, nh+nkv, hd)
+            v = qkv[:, qd + kd:].view(Lt, nkv, hd)
+            K.kv_write(qk[:, nh:], v, k_buf, v_buf, pos0=0)
+            attn = K.prefill_attn(qk[:, :nh], k_buf, v_buf, pos0=0)     # (L, hidden)
+            x = K.qgemm(attn, L.wo, residual=x)
+            h = K.rmsnorm(x, L.ffn_norm, cfg.eps)
+            if L.w_gate_up is not None:
+                gu = K.qgemm(h, L.w_gate_up)
+            else:
+                gu = torch.cat([K.qgemm(h, L.w_gate), K.qgemm(h, L.w_up)], dim=1)
+            act = K.silu_mul(gu, cfg.ffn_dim)
+            x = K.qgemm(act, L.w_down, residual=x)
+        return K.qgemv_norm(x[-1], self.w["output_norm.weight"], self.output, cfg.eps)

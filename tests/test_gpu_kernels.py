@@ -1,0 +1,376 @@
+"""GPU parity of every kernel against the oracle (bit-exact dequant, 1e-3 relative GEMV and
+attention, as the decode path requires). Run on an MI355X: pytest -m gpu."""
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from helpers import dequant_rows, quantized_normal, random_quant, rel_err
+from oracle import closed
+from oracle import dequant as dq
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3  # relative, fp32 accumulate
+
+KA = json.loads((GOLDEN / "dequant_known_answers.json").read_text())
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def K():
+    from pico_hip import kernels
+    return kernels
+
+
+def dev_bytes(raw: bytes) -> torch.Tensor:
+    return torch.from_numpy(np.frombuffer(raw, np.uint8).copy()).to(DEV)
+
+
+def qweight(K, t, raw, n, k):
+    return K.pack_weight(dev_bytes(raw), t, n, k)
+
+
+# ---- dequantization (bit-exact) ----------------------------------------------------------
+
+@pytest.mark.parametrize("c", KA["cases"], ids=[c["name"] for c in KA["cases"]])
+def test_dequant_known_answers(K, c):
+    out = K.dequantize(c["type"], dev_bytes(bytes.fromhex(c["block_hex"])), c["n"]).cpu().numpy()
+    np.testing.assert_array_equal(out, np.array(c["expected"], np.float32))
+
+
+@pytest.mark.parametrize("t", [dq.Q8_0, dq.Q5_0, dq.Q4_K, dq.Q6_K])
+def test_dequant_random_blocks_bitexact(K, t):
+    qk = dq.BLOCK[t][0]
+    raw = random_quant(t, 64, 8 * qk, seed=11 + t)
+    n = 64 * 8 * qk
+    gpu = K.dequantize(t, dev_bytes(raw), n).cpu().numpy()
+    ref = dq.dequantize(t, raw, n)
+    np.testing.assert_array_equal(gpu.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_f16_f32_q8k(K):
+    rng = np.random.default_rng(1)
+    h = rng.standard_normal(1000).astype(np.float16)
+    h[:5] = np.array([0x0001, 0x03FF, 0x8001, 0x7BFF, 0x0400], np.uint16).view(np.float16)
+    np.testing.assert_array_equal(K.dequantize(dq.F16, dev_bytes(h.tobytes()), 1000).cpu().numpy(),
+                                  h.astype(np.float32))
+    f = rng.standard_normal(999).astype(np.float32)
+    np.testing.assert_array_equal(K.dequantize(dq.F32, dev_bytes(f.tobytes()), 999).cpu().numpy(), f)
+    raw = rng.integers(0, 256, size=(8, 292), dtype=np.uint8)
+    raw[:, 0:4] = (rng.standard_normal(8).astype(np.float32) * 0.01).view(np.uint8).reshape(-1, 4)
+    out = K.dequantize(dq.Q8_K, dev_bytes(raw.tobytes()), 2048).cpu().numpy()
+    np.testing.assert_array_equal(out, dq.dequantize(dq.Q8_K, raw.tobytes(), 2048))
+
+
+@pytest.mark.parametrize("t,n,k", [(dq.Q8_0, 96, 896), (dq.Q5_0, 96, 896), (dq.Q4_K, 40, 4864),
+                                   (dq.Q6_K, 40, 4864), (dq.Q5_0, 8, 4864), (dq.Q8_0, 8, 256)])
+def test_tiled_decode_bitexact(K, t, n, k):
+    """pe_repack + the GEMV kernels' own unit decode reproduce the oracle bit for bit."""
+    raw = random_quant(t, n, k, seed=n + k + t)
+    w = qweight(K, t, raw, n, k)
+    gpu = K.dequantize_weight(w).cpu().numpy()
+    ref = dequant_rows(t, raw, n, k)
+    np.testing.assert_array_equal(gpu.view(np.uint32), ref.view(np.uint32))
+
+
+def test_embed_gather(K):
+    raw = random_quant(dq.Q8_0, 50, 896, seed=3)
+    table = K.RawTensor(dev_bytes(raw), dq.Q8_0, (50, 896))
+    ids = torch.tensor([0, 49, 7, 7, -1, 50], device=DEV)
+    out = K.embed_gather(table, ids).cpu().numpy()
+    ref = dequant_rows(dq.Q8_0, raw, 50, 896)
+    np.testing.assert_array_equal(out[:4], ref[[0, 49, 7, 7]])
+    assert np.all(np.isnan(out[4:]))  # out-of-range ids give NaN rows, no OOB read
+
+
+# ---- dequant-GEMV -------------------------------------------------------------------------
+
+GEMV_SHAPES = [  # (type, K_in, N_out): the config-1 microbench shapes + 7B shapes
+    (dq.Q5_0, 896, 1152), (dq.Q5_0, 896, 896), (dq.Q5_0, 896, 9728), (dq.Q5_0, 4864, 896),
+    (dq.Q8_0, 896, 1152), (dq.Q8_0, 896, 896), (dq.Q8_0, 896, 9728), (dq.Q8_0, 4864, 896),
+    (dq.Q4_K, 4864, 896), (dq.Q6_K, 4864, 896),
+    (dq.Q4_K, 3584, 512), (dq.Q6_K, 3584, 512), (dq.Q4_K, 18944, 256), (dq.Q6_K, 18944, 256),
+    (dq.Q8_0, 1024, 100), (dq.Q5_0, 2048, 64),
+]
+
+
+@pytest.mark.parametrize("t,k,n", GEMV_SHAPES, ids=[f"{dq.BLOCK[t][0]}-{t}-{k}x{n}" for t, k, n in GEMV_SHAPES])
+def test_qgemv_matches_closed_form(K, t, k, n):
+    raw = quantized_normal(t, n, k, seed=k + n + t)
+    w = qweight(K, t, raw, n, k)
+    rng = np.random.default_rng(k * 7 + n)
+    x = rng.standard_normal(k).astype(np.float32)
+    y = K.qgemv(torch.from_numpy(x).to(DEV), w).cpu().numpy()
+    ref = closed.gemv(dequant_rows(t, raw, n, k), x)
+    assert rel_err(y, ref) < TOL
+
+
+def test_qgemv_lm_head_rows(K):
+    """896 -> 151936 Q8_0 (the LM head); a seeded subset of rows checked in float64."""
+    n, k = 151936, 896
+    raw = quantized_normal(dq.Q8_0, n, k, seed=42)
+    w = qweight(K, dq.Q8_0, raw, n, k)
+    x = np.random.default_rng(0).standard_normal(k).astype(np.float32)
+    y = K.qgemv(torch.from_numpy(x).to(DEV), w).cpu().numpy()
+    rows = np.sort(np.random.default_rng(1).choice(n, 4096, replace=False))
+    rows = np.concatenate([rows, [0, n - 1]])
+    blk = np.frombuffer(raw, np.uint8).reshape(n, -1)[rows]
+    ref = closed.gemv(dequant_rows(dq.Q8_0, blk.tobytes(), len(rows), k), x)
+    assert rel_err(y[rows], ref) < TOL
+
+
+@pytest.mark.parametrize("t,k", [(dq.Q8_0, 896), (dq.Q5_0, 896), (dq.Q4_K, 4864), (dq.Q6_K, 4864),
+                                 (dq.Q6_K, 18944)])
+def test_qgemv_one_hot_is_exact_column(K, t, k):
+    """x = e_j gives column j of W exactly: pins row/column indexing and the unit layout."""
+    n = 64
+    raw = random_quant(t, n, k, seed=5 + t)
+    w = qweight(K, t, raw, n, k)
+    W = dequant_rows(t, raw, n, k)
+    for j in (0, 1, 31, 32, 255, 256, k // 2 + 17, k - 1):
+        x = torch.zeros(k, device=DEV)
+        x[j] = 1.0
+        y = K.qgemv(x, w).cpu().numpy()
+        np.testing.assert_array_equal(y, W[:, j])
+
+
+def test_qgemv_residual_bias_and_determinism(K):
+    t, k, n = dq.Q5_0, 896, 1152
+    raw = quantized_normal(t, n, k, seed=9)
+    w = qweight(K, t, raw, n, k)
+    rng = np.random.default_rng(2)
+    x, r, b = (rng.standard_normal(s).astype(np.float32) for s in (k, n, n))
+    X, R, B = (torch.from_numpy(v).to(DEV) for v in (x, r, b))
+    y1 = K.qgemv(X, w, residual=R, bias=B)
+    y2 = K.qgemv(X, w, residual=R, bias=B)
+    assert torch.equal(y1, y2)  # fixed reduction order: bitwise repeatable
+    ref = closed.gemv(dequant_rows(t, raw, n, k), x, bias=b, residual=r)
+    assert rel_err(y1.cpu().numpy(), ref) < TOL
+
+
+@pytest.mark.parametrize("t,k,n", [(dq.Q5_0, 896, 9728), (dq.Q8_0, 896, 4096), (dq.Q4_K, 3584, 1024)])
+def test_qgemv_rmsnorm(K, t, k, n):
+    raw = quantized_normal(t, n, k, seed=t + k)
+    w = qweight(K, t, raw, n, k)
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal(k).astype(np.float32)
+    nw = (rng.standard_normal(k) * 0.5).astype(np.float32)
+    y = K.qgemv_norm(torch.from_numpy(x).to(DEV), torch.from_numpy(nw).to(DEV), w, 1e-6).cpu().numpy()
+    ref = closed.gemv(dequant_rows(t, raw, n, k), closed.rmsnorm(x, nw, 1e-6))
+    assert rel_err(y, ref) < TOL
+
+
+@pytest.mark.parametrize("t,k,ffn", [(dq.Q5_0, 896, 4864), (dq.Q4_K, 3584, 512)])
+def test_qgemv_rmsnorm_silu(K, t, k, ffn):
+    raw = quantized_normal(t, 2 * ffn, k, seed=ffn)
+    w = qweight(K, t, raw, 2 * ffn, k)
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal(k).astype(np.float32)
+    nw = rng.standard_normal(k).astype(np.float32)
+    act = K.qgemv_norm_silu(torch.from_numpy(x).to(DEV), torch.from_numpy(nw).to(DEV), w, 1e-6).cpu().numpy()
+    gu = closed.gemv(dequant_rows(t, raw, 2 * ffn, k), closed.rmsnorm(x, nw, 1e-6))
+    assert rel_err(act, closed.silu_mul(gu[:ffn], gu[ffn:])) < TOL
+
+
+@pytest.mark.parametrize("m", [1, 5, 8, 13, 17])
+@pytest.mark.parametrize("t,k,n", [(dq.Q5_0, 896, 1152), (dq.Q6_K, 4864, 896), (dq.Q8_0, 896, 300)])
+def test_qgemm_prefill(K, m, t, k, n):
+    raw = quantized_normal(t, n, k, seed=m + n)
+    w = qweight(K, t, raw, n, k)
+    rng = np.random.default_rng(m)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    r = rng.standard_normal((m, n)).astype(np.float32)
+    out = torch.full((m, n + 7), float("nan"), device=DEV)  # strided destination
+    K.qgemm(torch.from_numpy(x).to(DEV), w, bias=torch.from_numpy(b).to(DEV),
+            residual=torch.from_numpy(r).to(DEV), out=out[:, 3:3 + n])
+    got = out.cpu().numpy()
+    W = dequant_rows(t, raw, n, k).astype(np.float64)
+    ref = x.astype(np.float64) @ W.T + b + r
+    assert rel_err(got[:, 3:3 + n], ref) < TOL
+    assert np.all(np.isnan(got[:, :3])) and np.all(np.isnan(got[:, 3 + n:]))
+
+
+# ---- attention ----------------------------------------------------------------------------
+
+def _kv(rng, n_kv, cap, hd):
+    return (rng.standard_normal((n_kv, cap, hd)).astype(np.float32),
+            rng.standard_normal((n_kv, cap, hd)).astype(np.float32))
+
+
+@pytest.mark.parametrize("hd,n_head,n_kv", [(64, 14, 2), (128, 28, 4), (64, 4, 4)])
+@pytest.mark.parametrize("S,cap", [(1, 8), (17, 77), (64, 64), (65, 130), (130, 130), (512, 600),
+                                   (4096, 4096)])
+def test_decode_attn(K, hd, n_head, n_kv, S, cap):
+    rng = np.random.default_rng(S + hd)
+    q = rng.standard_normal((n_head, hd)).astype(np.float32)
+    k, v = _kv(rng, n_kv, cap, hd)
+    out = K.decode_attn(torch.from_numpy(q).to(DEV), torch.from_numpy(k).to(DEV),
+                        torch.from_numpy(v).to(DEV), S=torch.tensor([S], device=DEV)).cpu().numpy()
+    ref = closed.attention(q, k, v, S, round_fp16=False)
+    assert rel_err(out, ref) < TOL
+    # the stored values are fp16-representable (kernels.py:126 rounding)
+    np.testing.assert_array_equal(out, out.astype(np.float16).astype(np.float32))
+
+
+def test_decode_attn_long_context_and_len_forms(K):
+    """32768-long cache (config 2), S given as int, int32, int64 tensor, and with an offset."""
+    rng = np.random.default_rng(0)
+    n_head, n_kv, hd, cap = 14, 2, 64, 32768
+    q = rng.standard_normal((n_head, hd)).astype(np.float32)
+    k, v = _kv(rng, n_kv, cap, hd)
+    Q, Kc, Vc = (torch.from_numpy(a).to(DEV) for a in (q, k, v))
+    ref = closed.attention(q, k, v, 32768)
+    for S in (32768, torch.tensor([32768], device=DEV, dtype=torch.int32),
+              torch.tensor([32767], device=DEV)):
+        kw = {"S_offset": 1} if isinstance(S, torch.Tensor) and S.dtype == torch.int64 else {}
+        out = K.decode_attn(Q, Kc, Vc, S=S, **kw).cpu().numpy()
+        assert rel_err(out, ref) < TOL
+    out = K.decode_attn(Q, Kc, Vc, S=None).cpu().numpy()  # default S = capacity
+    assert rel_err(out, ref) < TOL
+
+
+def test_decode_attn_unrounded_and_clamp(K):
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((14, 64)).astype(np.float32)
+    k, v = _kv(rng, 2, 100, 64)
+    Q, Kc, Vc = (torch.from_numpy(a).to(DEV) for a in (q, k, v))
+    out = K.decode_attn(Q, Kc, Vc, S=90, round_fp16=False).cpu().numpy()
+    assert rel_err(out, closed.attention(q, k, v, 90)) < 1e-5
+    over = K.decode_attn(Q, Kc, Vc, S=1000).cpu().numpy()  # S > capacity clamps (kernels.py:110)
+    assert rel_err(over, closed.attention(q, k, v, 100)) < TOL
+    empty = K.decode_attn(Q, Kc, Vc, S=0).cpu().numpy()   # S = 0: 0/0 like the reference
+    assert np.all(np.isnan(empty))
+
+
+def test_decode_attn_workspace_reuse_and_graph(K):
+    """One workspace across many in-order calls and across graph replays with a device S."""
+    rng = np.random.default_rng(9)
+    n_head, n_kv, hd, cap = 14, 2, 64, 300
+    q = rng.standard_normal((n_head, hd)).astype(np.float32)
+    k, v = _kv(rng, n_kv, cap, hd)
+    Q, Kc, Vc = (torch.from_numpy(a).to(DEV) for a in (q, k, v))
+    ws = K.decode_attn_workspace(n_head, n_kv, hd, cap, DEV)
+    pos = torch.zeros(1, dtype=torch.int64, device=DEV)
+    out = torch.empty(n_head, hd, device=DEV)
+    for S in (5, 299, 64, 129, 300):
+        pos.fill_(S - 1)
+        K.decode_attn(Q, Kc, Vc, S=pos, S_offset=1, workspace=ws, out=out)
+        assert rel_err(out.cpu().numpy(), closed.attention(q, k, v, S)) < TOL
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        K.decode_attn(Q, Kc, Vc, S=pos, S_offset=1, workspace=ws, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(g):
+        K.decode_attn(Q, Kc, Vc, S=pos, S_offset=1, workspace=ws, out=out)
+    for S in (1, 200, 64, 300, 65):
+        pos.fill_(S - 1)
+        g.replay()
+        torch.cuda.synchronize()
+        graph_out = out.clone()
+        eager = K.decode_attn(Q, Kc, Vc, S=pos, S_offset=1, workspace=ws)
+        assert torch.equal(graph_out, eager)
+        assert rel_err(graph_out.cpu().numpy(), closed.attention(q, k, v, S)) < TOL
+
+
+@pytest.mark.parametrize("L,pos0,hd", [(1, 0, 64), (13, 0, 64), (40, 5, 64), (300, 0, 64), (9, 0, 128)])
+def test_prefill_attn(K, L, pos0, hd):
+    rng = np.random.default_rng(L)
+    n_head, n_kv, cap = (14, 2, pos0 + L + 3) if hd == 64 else (28, 4, pos0 + L)
+    q = rng.standard_normal((L, n_head, hd)).astype(np.float32)
+    k, v = _kv(rng, n_kv, cap, hd)
+    out = K.prefill_attn(torch.from_numpy(q).to(DEV), torch.from_numpy(k).to(DEV),
+                         torch.from_numpy(v).to(DEV), pos0=pos0).cpu().numpy()
+    ref = closed.causal_attention(q, k, v, pos0).reshape(L, n_head * hd)
+    assert rel_err(out, ref) < TOL
+
+
+# ---- element-wise (reference tests/test_kernels.py:16-70) ---------------------------------
+
+@pytest.mark.parametrize("L", [1, 5])
+def test_rmsnorm(K, L):
+    rng = np.random.default_rng(L)
+    x = rng.standard_normal((L, 896)).astype(np.float32)
+    w = rng.standard_normal(896).astype(np.float32)
+    out = K.rmsnorm(torch.from_numpy(x).to(DEV), torch.from_numpy(w).to(DEV), 1e-6).cpu().numpy()
+    assert np.abs(out - closed.rmsnorm(x, w, 1e-6)).max() < 1e-5
+
+
+def test_rope_contiguous_and_strided_view(K):
+    """The reference's non-contiguous prefill regression (test_kernels.py:40-59)."""
+    rng = np.random.default_rng(0)
+    L, nh, nkv, hd = 5, 14, 2, 64
+    qkv = torch.from_numpy(rng.standard_normal((L, nh * hd + 2 * nkv * hd)).astype(np.float32)).to(DEV)
+    q, k, _ = qkv.split([nh * hd, nkv * hd, nkv * hd], dim=-1)
+    q, k = q.view(L, nh, hd), k.view(L, nkv, hd)
+    assert not q.is_contiguous()
+    c = rng.standard_normal((L, hd // 2)).astype(np.float32)
+    s = rng.standard_normal((L, hd // 2)).astype(np.float32)
+    C, S = torch.from_numpy(c).to(DEV), torch.from_numpy(s).to(DEV)
+    for x in (q, k, q.contiguous()):
+        ref = closed.rope(x.cpu().numpy(), c[:, None, :], s[:, None, :])
+        assert np.abs(K.rope(x, C, S).cpu().numpy() - ref).max() < 1e-5
+
+
+@pytest.mark.parametrize("L", [1, 5])
+def test_silu_mul(K, L):
+    gu = np.random.default_rng(L).standard_normal((L, 2 * 4864)).astype(np.float32)
+    out = K.silu_mul(torch.from_numpy(gu).to(DEV), 4864).cpu().numpy()
+    assert np.abs(out - closed.silu_mul(gu[:, :4864], gu[:, 4864:])).max() < 1e-4
+
+
+def test_kv_write(K):
+    rng = np.random.default_rng(3)
+    L, nkv, hd, cap = 7, 2, 64, 20
+    kk = rng.standard_normal((L, nkv, hd)).astype(np.float32)
+    vv = rng.standard_normal((L, nkv, hd)).astype(np.float32)
+    kc = torch.zeros(nkv, cap, hd, device=DEV)
+    vc = torch.zeros(nkv, cap, hd, device=DEV)
+    K.kv_write(torch.from_numpy(kk).to(DEV), torch.from_numpy(vv).to(DEV), kc, vc, pos0=4)
+    kc, vc = kc.cpu().numpy(), vc.cpu().numpy()
+    np.testing.assert_array_equal(kc[:, 4:11], kk.transpose(1, 0, 2))
+    np.testing.assert_array_equal(vc[:, 4:11], vv.transpose(1, 0, 2))
+    assert not kc[:, :4].any() and not kc[:, 11:].any()
+
+
+# ---- fused QKV prologue -------------------------------------------------------------------
+
+@pytest.mark.parametrize("types,hidden,nh,nkv,hd", [
+    ((dq.Q5_0, dq.Q5_0, dq.Q8_0), 896, 14, 2, 64),
+    ((dq.Q5_0, dq.Q5_0, dq.Q5_0), 896, 14, 2, 64),
+    ((dq.Q4_K, dq.Q4_K, dq.Q6_K), 3584, 28, 4, 128),
+])
+def test_qkv_rmsnorm_rope(K, types, hidden, nh, nkv, hd):
+    rng = np.random.default_rng(hidden)
+    cap, pos, theta = 40, 23, 1e6
+    rows = (nh * hd, nkv * hd, nkv * hd)
+    raws = [quantized_normal(t, r, hidden, seed=i + 1) for i, (t, r) in enumerate(zip(types, rows))]
+    ws = [qweight(K, t, raw, r, hidden) for t, raw, r in zip(types, raws, rows)]
+    bs = [rng.standard_normal(r).astype(np.float32) * 0.1 for r in rows]
+    x = rng.standard_normal(hidden).astype(np.float32)
+    nw = rng.standard_normal(hidden).astype(np.float32)
+    inv = 1.0 / (theta ** (np.arange(0, hd, 2) / hd))
+    ang = (np.arange(64)[:, None] * inv[None, :]).astype(np.float32)
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    kc = torch.zeros(nkv, cap, hd, device=DEV)
+    vc = torch.zeros(nkv, cap, hd, device=DEV)
+    T = lambda a: torch.from_numpy(a).to(DEV)
+    q = K.qkv_rmsnorm_rope(T(x), T(nw), 1e-6, *ws, *(T(b) for b in bs), T(cos), T(sin),
+                           torch.tensor([pos], device=DEV), kc, vc, nh).cpu().numpy()
+    h = closed.rmsnorm(x, nw, 1e-6)
+    outs = [closed.gemv(dequant_rows(t, raw, r, hidden), h, bias=b)
+            for t, raw, r, b in zip(types, raws, rows, bs)]
+    rq = closed.rope(outs[0].reshape(nh, hd), cos[pos], sin[pos])
+    rk = closed.rope(outs[1].reshape(nkv, hd), cos[pos], sin[pos])
+    assert rel_err(q, rq) < TOL
+    kc, vc = kc.cpu().numpy(), vc.cpu().numpy()
+    assert rel_err(kc[:, pos], rk) < TOL
+    assert rel_err(vc[:, pos], outs[2].reshape(nkv, hd)) < TOL
+    kc[:, pos] = 0
+    vc[:, pos] = 0
+    assert not kc.any() and not vc.any()  # nothing else written

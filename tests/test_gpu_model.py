@@ -1,0 +1,89 @@
+"""End-to-end GPU parity: Engine (HIP path) vs the torch-CPU oracle of the reference forward.
+
+* tiny 2-layer model of the 0.5B family (all four formats): prefill and decode logits within
+  1e-3 relative, greedy tokens identical, graph replay == eager (the reference's
+  test_integration.py:29-59 idea, here bitwise);
+* config 0 (Qwen2.5-0.5B architecture, Q4_K_M-style mix, seed 0): the 64 greedy tokens of
+  the committed fixture tests/golden/config0_greedy.json, produced by the oracle.
+"""
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from helpers import rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def tiny(tiny_model):
+    from pico_hip.engine import Engine
+    from oracle.ref_cpu import RefModel
+    return Engine(tiny_model), RefModel(tiny_model)
+
+
+def test_prefill_and_decode_logits_match_oracle(tiny):
+    eng, ref = tiny
+    ids = [3, 500, 17, 999, 42, 7, 256, 1023, 0, 64, 65, 300, 12]
+    cap = len(ids) + 8
+    cache = eng._empty_cache(cap)
+    rcache = ref.empty_cache(cap)
+    lg = eng.model.forward(torch.tensor(ids, device=eng.device), torch.arange(len(ids), device=eng.device), cache)
+    rl = ref.forward(torch.tensor(ids), torch.arange(len(ids)), rcache)
+    assert rel_err(lg.cpu().numpy(), rl.numpy()) < TOL
+    for c, rc in zip(cache, rcache):  # the prefill filled the same KV
+        assert rel_err(c[0][:, :len(ids)].cpu().numpy(), rc[0][:, :len(ids)].numpy()) < TOL
+    tok = int(rl.argmax())
+    for step in range(8):
+        pos = len(ids) + step
+        lg = eng.model.forward(torch.tensor([tok], device=eng.device), torch.tensor([pos], device=eng.device), cache)
+        rl = ref.forward(torch.tensor([tok]), torch.tensor([pos]), rcache)
+        assert rel_err(lg.cpu().numpy(), rl.numpy()) < TOL, step
+        tok = int(rl.argmax())
+
+
+def test_greedy_tokens_match_oracle(tiny):
+    eng, ref = tiny
+    ids = [1, 2, 3, 4, 5, 900, 800, 700]
+    want, margins = ref.greedy(ids, 24)
+    got = eng.generate_ids(ids, 24, temperature=0.0, use_graph=True)
+    assert got == want, (got, want, margins)
+
+
+def test_graph_equals_eager(tiny):
+    eng, _ = tiny
+    ids = [9, 8, 7, 6, 5]
+    cache = eng._empty_cache(len(ids) + 8)
+    graph = eng._build_decode_graph(cache)
+    assert graph is not None, "graph capture failed"
+    logits = eng.model.forward(torch.tensor(ids, device=eng.device), torch.arange(len(ids), device=eng.device), cache)
+    nxt = int(logits.argmax())
+    for step in range(8):
+        pos = len(ids) + step
+        # eager first, then the graph replays the same step over the same cache slot
+        eager = eng.model.forward(torch.tensor([nxt], device=eng.device), torch.tensor([pos], device=eng.device), cache).clone()
+        torch.cuda.synchronize()
+        g = eng._decode_step(nxt, pos, cache, graph).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(eager, g), f"graph diverged from eager at step {step}"
+        nxt = int(eager.argmax())
+
+
+def test_config0_greedy_matches_fixture(model_dir):
+    """Qwen2.5-0.5B-architecture synthetic model, 13-token seeded prompt, 64 greedy tokens."""
+    from pico_hip import synth
+    from pico_hip.engine import Engine
+    fx = json.loads((GOLDEN / "config0_greedy.json").read_text())
+    path = model_dir / "config0.gguf"
+    if not path.exists():
+        synth.build(path, synth.ARCHES["qwen2.5-0.5b"], seed=fx["seed"])
+    assert synth.sha256(path) == fx["gguf_sha256"], "synthetic model is not byte-identical"
+    eng = Engine(path)
+    got = eng.generate_ids(fx["prompt_ids"], fx["n_tokens"], temperature=0.0, use_graph=True)
+    first_diff = next((i for i, (a, b) in enumerate(zip(got, fx["tokens"])) if a != b), None)
+    assert got == fx["tokens"], f"first mismatch at step {first_diff} (margin {fx['margins'][first_diff]})"
