@@ -1,0 +1,258 @@
+#!/usr/bin/env python
+"""Batch-1 decode benchmark of BASELINE config 0 on one MI355X.
+
+Workload: Qwen2.5-0.5B-architecture decoder, random-init N(0,0.02)
+weights quantized into a Q4_K_M-style GGUF (seed 0, pico_hip.synth), a 13-token prompt of
+uniform random ids (numpy default_rng(1234)), fp32 prefill, greedy decode. A "step" is one
+decode token: one replay of the HIP graph holding the whole per-token forward (122 kernels),
+plus the reference loop's argmax read-back and token/position feed (evidence.py:114-124).
+W warm-up runs (fresh cache, graph capture, prefill, K decode steps) precede the timed run;
+in the timed run the prefill happens before the bracket, then K decode steps are timed
+between two device synchronizations. value = K / elapsed (tok/s).
+
+Also reported on the same line:
+  roofline      the dominant kernel (--kernel) timed alone with HIP events on the stream it
+                launches on, rotating >= 1 GiB of distinct weight copies so the 256 MB
+                Infinity Cache cannot serve repeats; achieved = algorithmic bytes per launch /
+                average launch time, against 8 TB/s. traffic comes from the rocprofv3 --pmc
+                summary in profiles/ when present.
+  decode_roofline  weight + KV bytes per token over the measured time per token.
+  cpu_baseline  the torch-CPU restatement of the reference forward (oracle/ref_cpu.py) on the
+                same model and prompt, on this host's cores, over a bounded number of decode
+                steps (about 10-30 s).
+Usage: python bench.py [--steps 64] [--warmup 2] [--kernel gate_up|lm_head|down_q6k|...]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path[:0] = [str(ROOT), str(ROOT / "pico-engine_amd")]
+
+PEAK_HBM_GBPS = 8000.0
+PROMPT_SEED, MODEL_SEED, N_PROMPT = 1234, 0, 13
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def run_decode(eng, prompt, steps, timed: bool):
+    """One evidence._run_once-style run: fresh cache + graph, prefill, `steps` greedy tokens."""
+    import torch
+    cache = eng._empty_cache(len(prompt) + steps)
+    graph = eng._build_decode_graph(cache)
+    if graph is None:
+        raise RuntimeError("HIP graph capture failed")
+    tokens = torch.tensor(prompt, device=eng.device)
+    positions = torch.arange(len(prompt), device=eng.device)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits = eng.model.forward(tokens, positions, cache)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    out = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        tok = int(logits.argmax())
+        out.append(tok)
+        logits = eng._decode_step(tok, len(prompt) + i, cache, graph)
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0, prefill_s, out
+
+
+def kernel_launchers(eng, which: str):
+    """-> (list of launch closures over distinct weight copies, algorithmic bytes per launch,
+    kernel name). Copies are made until >= 1 GiB of distinct weights rotate."""
+    import torch
+    from pico_hip import kernels as K
+    m, cfg = eng.model, eng.cfg
+    L0 = m.layers[0]
+    x = torch.randn(cfg.hidden, device=eng.device)
+    nw = m.layers[0].ffn_norm
+    if which == "gate_up":
+        w, name = L0.w_gate_up, "k_qgemv (Q5_0, rmsnorm+SiLU pair) gate/up 896->2x4864"
+        fn = lambda ww: K.qgemv_norm_silu(x, nw, ww, cfg.eps)
+        io = 4 * (cfg.hidden * 2 + cfg.ffn_dim)
+    elif which == "lm_head":
+        w, name = m.output, "k_qgemv (Q8_0, rmsnorm) LM head 896->151936"
+        fn = lambda ww: K.qgemv_norm(x, m.w["output_norm.weight"], ww, cfg.eps)
+        io = 4 * (cfg.hidden * 2 + cfg.vocab_size)
+    elif which in ("down_q6k", "down_q4k"):
+        li = 0 if which == "down_q6k" else 1
+        w = m.layers[li].w_down
+        name = f"k_qgemv ({'Q6_K' if li == 0 else 'Q4_K'}, +residual) ffn_down 4864->896"
+        a = torch.randn(cfg.ffn_dim, device=eng.device)
+        fn = lambda ww: K.qgemv(a, ww, residual=x)
+        io = 4 * (cfg.ffn_dim + 2 * cfg.hidden)
+    else:
+        raise SystemExit(f"unknown --kernel {which}")
+    copies = max(1, -(-(1 << 30) // w.nbytes))
+    ws = [w] + [K.QWeight(w.data.clone(), w.ggml_type, w.n, w.k) for _ in range(copies - 1)]
+    return [(lambda ww=ww: fn(ww)) for ww in ws], w.nbytes + io, name
+
+
+def time_kernel(launchers, iters: int) -> float:
+    """Average launch duration in us: HIP events on torch's current stream (the stream the
+    kernels launch on), launches round-robin over the distinct copies."""
+    import torch
+    for f in launchers:
+        f()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(iters):
+        launchers[i % len(launchers)]()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1000.0 / iters
+
+
+def traffic_from_profiles(kernel: str):
+    p = ROOT / "profiles" / f"traffic_{kernel}.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("bytes_per_launch")
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def cpu_baseline(path, prompt, budget_s: float):
+    import torch
+    from oracle.ref_cpu import RefModel
+    cores = len(os.sched_getaffinity(0))
+    cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+    torch.set_num_threads(cores)
+    ref = RefModel(path)
+    steps_max = 64
+    cache = ref.empty_cache(len(prompt) + steps_max)
+    logits = ref.forward(torch.tensor(prompt), torch.arange(len(prompt)), cache)
+    done, t0 = 0, time.perf_counter()
+    while done < steps_max:
+        tok = int(logits.argmax())
+        logits = ref.forward(torch.tensor([tok]), torch.tensor([len(prompt) + done]), cache)
+        done += 1
+        if time.perf_counter() - t0 > budget_s and done >= 2:
+            break
+    el = time.perf_counter() - t0
+    return {"value": round(done / el, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"config 0 on the host CPU: fp32 prefill of the 13-token prompt, then {done} "
+                      f"greedy decode steps timed ({el:.1f} s) with oracle/ref_cpu.py (the reference's "
+                      "torch-CPU forward formulations), torch threads = cores"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64, help="timed decode tokens")
+    ap.add_argument("--warmup", type=int, default=2, help="untimed full runs before the timed one")
+    ap.add_argument("--reps", type=int, default=5, help="extra timed runs for median/p10/p90")
+    ap.add_argument("--kernel", default="gate_up", help="dominant kernel for the roofline object")
+    ap.add_argument("--kernel-iters", type=int, default=400)
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline decode")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only time --kernel and a 1 GiB copy (for rocprofv3 --pmc traffic runs)")
+    ap.add_argument("--model-dir", default=os.environ.get("PICO_HIP_CACHE", "/tmp/pico_hip_models"))
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build runs the batch-1 decode on "
+              "exactly one GPU (the multi-GPU sharding plan is design-only).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    from pico_hip import synth
+    from pico_hip.engine import Engine
+
+    arch = synth.ARCHES["qwen2.5-0.5b"]
+    t0 = time.time()
+    path = synth.cached(arch, seed=MODEL_SEED, cache_dir=args.model_dir)
+    log(f"model {path} ready in {time.time() - t0:.1f}s")
+    eng = Engine(path, device="cuda:0")
+    prompt = np.random.default_rng(PROMPT_SEED).integers(0, arch.vocab, size=N_PROMPT).tolist()
+    log(f"engine loaded; {torch.cuda.get_device_name(0)}")
+
+    if args.kernel_only:
+        launchers, alg_bytes, kname = kernel_launchers(eng, args.kernel)
+        avg_us = time_kernel(launchers, args.kernel_iters)
+        src = torch.ones(1 << 28, device=eng.device)   # 1 GiB: the counter calibration copy
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel": kname, "avg_launch_us": avg_us, "algorithmic_bytes": alg_bytes,
+                          "calibration_copy_bytes": src.numel() * 4}), flush=True)
+        return
+
+    for _ in range(args.warmup):
+        run_decode(eng, prompt, args.steps, timed=False)
+    elapsed, prefill_s, tokens = run_decode(eng, prompt, args.steps, timed=True)
+    value = args.steps / elapsed
+    samples = [value]
+    for _ in range(args.reps):
+        e, _, _ = run_decode(eng, prompt, args.steps, timed=True)
+        samples.append(args.steps / e)
+    log(f"decode {value:.1f} tok/s (median of {len(samples)}: {statistics.median(samples):.1f})")
+
+    # decode roofline: weight bytes per token + KV bytes (read S positions, write one)
+    c = eng.cfg
+    weight_bytes = eng.model.weight_bytes_per_token()
+    kv_pos = 2 * c.n_kv_head * c.head_dim * 4 * c.n_layers
+    mean_S = N_PROMPT + (args.steps + 1) / 2.0
+    bytes_per_token = weight_bytes + kv_pos * (mean_S + 1)
+    dec_gbps = bytes_per_token * value / 1e9
+
+    launchers, alg_bytes, kname = kernel_launchers(eng, args.kernel)
+    avg_us = time_kernel(launchers, args.kernel_iters)
+    achieved = alg_bytes / (avg_us * 1e-6) / 1e9
+    log(f"{kname}: {avg_us:.2f} us/launch, {achieved:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(path, prompt, args.cpu_budget)
+        log(f"cpu baseline {cpu['value']} tok/s on {cpu['cores']} cores")
+
+    line = {
+        "metric": "batch-1 decode tok/s (0.5B Q4_K_M arch)",
+        "value": round(value, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1000, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 (Q4_K_M-style packed weights, fp32 activations/KV)",
+        "data": "synthetic: random-init N(0,0.02) weights quantized to GGUF (seed 0), 13 uniform random prompt ids",
+        "config": {"workload": "BASELINE config 0: Qwen2.5-0.5B-arch Q4_K_M-style GGUF, batch 1, "
+                               "13-token prompt, greedy decode, HIP-graph step",
+                   "prompt_tokens": N_PROMPT, "decode_tokens": args.steps, "gguf_sha256": synth.sha256(path)},
+        "decode_samples_tok_s": {"median": round(statistics.median(samples), 2),
+                                 "p10": round(float(np.percentile(samples, 10)), 2),
+                                 "p90": round(float(np.percentile(samples, 90)), 2), "n": len(samples)},
+        "prefill_tok_s": round(N_PROMPT / prefill_s, 1),
+        "decode_roofline": {"bytes_per_token": int(bytes_per_token), "achieved": round(dec_gbps, 1),
+                            "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(dec_gbps / PEAK_HBM_GBPS, 4)},
+        "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
+                     "traffic": traffic_from_profiles(args.kernel), "avg_launch_us": round(avg_us, 3),
+                     "algorithmic_bytes": int(alg_bytes)},
+        "cpu_baseline": cpu,
+        "tokens_head": tokens[:8],
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

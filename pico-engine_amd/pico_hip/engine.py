@@ -70,7 +70,7 @@ class Engine:
         )
 
     def _upload(self, raw: np.ndarray) -> torch.Tensor:
-        return torch.from_numpy(np.ascontiguousarray(raw)).to(self.device, non_blocking=False)
+        return torch.from_numpy(np.array(raw, dtype=np.uint8, copy=True)).to(self.device)
 
     def _load_weights(self):
         weights: dict[str, torch.Tensor] = {}
@@ -113,6 +113,7 @@ class Engine:
         self.model.attn_workspace(capacity)
         return cache
 
+    @torch.inference_mode()
     def _build_decode_graph(self, cache):
         """Capture the single-token decode forward into a HIP graph (engine.py:269-294).
         Returns the graph, or None (eager fallback) if capture fails."""
@@ -135,6 +136,7 @@ class Engine:
             warnings.warn(f"HIP graph capture failed; falling back to eager decode: {e}")
             return None
 
+    @torch.inference_mode()
     def _decode_step(self, token: int, pos: int, cache, graph):
         if graph is not None:
             self._static_ids.fill_(int(token))

@@ -94,6 +94,18 @@ class Transformer:
             w_down=q[p + "ffn_down.weight"],
         )
 
+    def weight_bytes_per_token(self) -> int:
+        """Bytes of weights one decode token reads: every layer's packed matrices, biases and
+        norms, the final norm, the LM head and one embedding row (GGUF sizes)."""
+        total = self.output.nbytes + self.w["output_norm.weight"].numel() * 4
+        total += self.embed.data.numel() // self.embed.shape[0]
+        for L in self.layers:
+            mats = [L.wq, L.wk, L.wv, L.wo, L.w_down]
+            mats += [L.w_gate_up] if L.w_gate_up is not None else [L.w_gate, L.w_up]
+            total += sum(m.nbytes for m in mats)
+            total += sum(t.numel() * 4 for t in (L.attn_norm, L.ffn_norm, L.bq, L.bk, L.bv) if t is not None)
+        return total
+
     def attn_workspace(self, capacity: int) -> torch.Tensor:
         """Decode-attention workspace for a cache of ``capacity`` (shared by all layers)."""
         ws = self._ws.get(capacity)

@@ -60,7 +60,10 @@ def oracle_clib():
 @pytest.fixture(scope="session")
 def model_dir(tmp_path_factory):
     d = os.environ.get("PICO_HIP_CACHE")
-    return Path(d) if d else tmp_path_factory.mktemp("models")
+    if not d:
+        return tmp_path_factory.mktemp("models")
+    Path(d).mkdir(parents=True, exist_ok=True)
+    return Path(d)
 
 
 @pytest.fixture(scope="session")

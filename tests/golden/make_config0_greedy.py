@@ -32,10 +32,8 @@ def main() -> None:
     model_dir = Path(sys.argv[1]) if len(sys.argv) > 1 else Path("/tmp/pico_hip_models")
     model_dir.mkdir(parents=True, exist_ok=True)
     arch = synth.ARCHES["qwen2.5-0.5b"]
-    path = model_dir / "config0.gguf"
     t0 = time.time()
-    if not path.exists():
-        synth.build(path, arch, seed=SEED)
+    path = synth.cached(arch, seed=SEED, cache_dir=model_dir)
     sha = synth.sha256(path)
     print(f"model {path} sha256 {sha} ({time.time() - t0:.1f}s)", flush=True)
     prompt = np.random.default_rng(PROMPT_SEED).integers(0, arch.vocab, size=N_PROMPT).tolist()

@@ -1,0 +1,107 @@
+"""The C ABI (include/pico_hip.h) on a host without a GPU: the library loads, exports every
+declared symbol, and rejects bad arguments with the documented status before any launch."""
+
+import ctypes
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = (ROOT / "include" / "pico_hip.h").read_text()
+
+
+def declared_functions() -> set[str]:
+    return set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]*?\b(pe_\w+)\s*\(", HEADER, re.M))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from pico_hip import _lib
+    return _lib.lib
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    from pico_hip import _lib
+    names = declared_functions()
+    assert len(names) >= 18
+    for n in names:
+        assert hasattr(lib, n), n
+    assert names == set(_lib.EXPORTED)
+
+
+def test_status_strings(lib):
+    from pico_hip._lib import strerror
+    assert strerror(0) == "ok"
+    for code in range(1, 7):
+        assert strerror(code) and strerror(code) != "unknown pe_status"
+    assert strerror(99) == "unknown pe_status"
+
+
+def test_nbytes_and_workspace(lib):
+    assert lib.pe_nbytes_for(12, 4864 * 896) == 2451456
+    assert lib.pe_nbytes_for(14, 4864 * 896) == 3575040
+    assert lib.pe_nbytes_for(6, 896 * 896) == 551936
+    assert lib.pe_nbytes_for(8, 151936 * 896) == 144643072
+    assert lib.pe_nbytes_for(12, 896) == -3        # not a whole super-block
+    assert lib.pe_nbytes_for(99, 32) == -2         # unknown type
+    ws = lib.pe_decode_attn_workspace_bytes(14, 2, 64, 77)
+    assert ws == 256 + 2 * 2 * 7 * 66 * 4
+    assert lib.pe_decode_attn_workspace_bytes(14, 3, 64, 77) == -3   # 14 % 3
+    assert lib.pe_decode_attn_workspace_bytes(14, 2, 96, 77) == -3   # head_dim
+
+
+def test_argument_errors_before_launch(lib):
+    """Invalid calls return a status without touching the GPU (none is present here)."""
+    P = ctypes.c_void_p
+    fake = P(0x1000)          # never dereferenced: validation fails first
+    odd = P(0x1001)
+    # unsupported type / bad shapes / NULL / misalignment
+    assert lib.pe_qgemv(99, fake, 8, 896, fake, None, None, fake, None) == 2
+    assert lib.pe_qgemv(12, fake, 8, 896, fake, None, None, fake, None) == 3   # K % 256
+    assert lib.pe_qgemv(8, None, 8, 896, fake, None, None, fake, None) == 1
+    assert lib.pe_qgemv(8, odd, 8, 896, fake, None, None, fake, None) == 4
+    assert lib.pe_qgemv(8, fake, 8, 896, odd, None, None, fake, None) == 4
+    assert lib.pe_qgemv(8, fake, 0, 896, fake, None, None, fake, None) == 3
+    assert lib.pe_qgemv(8, fake, 8, 64 * 1024, fake, None, None, fake, None) == 3  # K too large
+    assert lib.pe_repack(15, fake, fake, 8, 256, None) == 2                    # Q8_K has no tiled form
+    assert lib.pe_dequant(8, fake, fake, 33, None) == 3
+    assert lib.pe_dequant(8, fake, fake, 0, None) == 0                         # empty is a no-op
+    assert lib.pe_qgemv_rmsnorm(8, fake, 8, 896, fake, None, 1e-6, fake, None) == 1
+    assert lib.pe_qgemm(8, fake, 8, 896, fake, 895, 2, None, None, 0, fake, 8, None) == 3  # x_stride < k
+    assert lib.pe_embed_gather(8, fake, 10, 896, fake, 0, fake, None) == 0
+    assert lib.pe_kv_write(fake, fake, 128, 2, 64, 5, 8, fake, fake, 10, None) == 3  # pos0+L > cap
+    assert lib.pe_prefill_attn(fake, 896, fake, fake, 14, 2, 64, 77, 13, 70, 0.125, fake, 896, None) == 3
+    ws = lib.pe_decode_attn_workspace_bytes(14, 2, 64, 77)
+    assert lib.pe_decode_attn(fake, fake, fake, 14, 2, 64, 77, None, 0, 5, 0.125, 1, fake, fake,
+                              ws - 1, None) == 6
+    assert lib.pe_decode_attn(fake, fake, fake, 14, 2, 64, 77, None, 3, 5, 0.125, 1, fake, fake,
+                              ws, None) == 2
+    assert lib.pe_decode_attn(fake, fake, fake, 14, 2, 64, 77, None, 2, 5, 0.125, 1, fake, fake,
+                              ws, None) == 1
+
+
+def test_qkv_args_struct_matches_header():
+    """ctypes mirror of pe_qkv_args has the header's fields in the header's order."""
+    from pico_hip._lib import QkvArgs
+    body = HEADER[HEADER.index("typedef struct pe_qkv_args"):HEADER.index("} pe_qkv_args;")]
+    fields = []
+    for line in body.splitlines()[1:]:
+        decl = line.split("/*")[0].strip().rstrip(";")
+        if not decl:
+            continue
+        names = decl.split(None, 1)[1] if not decl.startswith("const") else decl.split(None, 2)[2]
+        for n in names.split(","):
+            fields.append(n.strip().lstrip("*").strip())
+    assert [f[0] for f in QkvArgs._fields_] == fields
+
+
+def test_product_has_no_cpu_fallback():
+    """The kernels refuse host tensors instead of computing on the CPU."""
+    import torch
+    from pico_hip import kernels as K
+    with pytest.raises(ValueError, match="GPU tensors"):
+        K.rmsnorm(torch.ones(2, 8), torch.ones(8), 1e-6)
+    with pytest.raises(ValueError, match="GPU"):
+        from pico_hip.model import Transformer
+        Transformer(None, {}, torch.device("cpu"), {})

@@ -79,9 +79,7 @@ def test_config0_greedy_matches_fixture(model_dir):
     from pico_hip import synth
     from pico_hip.engine import Engine
     fx = json.loads((GOLDEN / "config0_greedy.json").read_text())
-    path = model_dir / "config0.gguf"
-    if not path.exists():
-        synth.build(path, synth.ARCHES["qwen2.5-0.5b"], seed=fx["seed"])
+    path = synth.cached(synth.ARCHES["qwen2.5-0.5b"], seed=fx["seed"], cache_dir=model_dir)
     assert synth.sha256(path) == fx["gguf_sha256"], "synthetic model is not byte-identical"
     eng = Engine(path)
     got = eng.generate_ids(fx["prompt_ids"], fx["n_tokens"], temperature=0.0, use_graph=True)

@@ -1,0 +1,111 @@
+"""Host-side logic on the CPU: GGUF read/write, synthetic-model determinism and type mix,
+tokenizer, sampler, engine configuration."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dequant as dq
+from oracle import ref_cpu
+
+
+def test_gguf_roundtrip(tmp_path):
+    from pico_hip import gguf
+    from pico_hip.quantize import quantize
+    w = np.random.default_rng(0).standard_normal(64 * 512).astype(np.float32)
+    tensors = [("a.weight", (512, 64), dq.Q4_K, quantize(dq.Q4_K, w)),
+               ("b.bias", (33,), dq.F32, np.arange(33, dtype=np.float32).view(np.uint8)),
+               ("c.weight", (64, 3), dq.Q8_0, quantize(dq.Q8_0, w[:192]))]
+    meta = {"general.architecture": "qwen2", "x.u": 7, "x.f": 1.5, "x.neg": -3, "x.b": True,
+            "x.s": "héllo", "x.arr": [1, 2, 3], "x.strs": ["a", "bb", ""], "x.farr": [0.5, -1.0]}
+    p = tmp_path / "t.gguf"
+    gguf.write(p, meta, tensors)
+    g = gguf.load(p)
+    assert g.version == 3 and g.alignment == 32 and g.data_start % 32 == 0
+    assert g.metadata == {**meta, "x.neg": -3}
+    for (name, shape, t, raw), info in zip(tensors, g.tensors):
+        assert (info.name, info.shape, info.ggml_type) == (name, shape, t)
+        assert info.offset % 32 == 0
+        assert bytes(gguf.read_tensor_bytes(g, info)) == bytes(memoryview(raw).cast("B"))
+    # the oracle's independent reader sees the same file
+    meta2, tens2 = ref_cpu.read_gguf(p)
+    assert meta2["x.strs"] == ["a", "bb", ""] and tens2["a.weight"][1] == dq.Q4_K
+    assert tens2["c.weight"][2] == bytes(tensors[2][3])
+
+
+def test_gguf_rejects_bad_magic(tmp_path):
+    from pico_hip import gguf
+    p = tmp_path / "bad.gguf"
+    p.write_bytes(b"GGUX" + bytes(20))
+    with pytest.raises(ValueError, match="not a GGUF"):
+        gguf.load(p)
+
+
+def test_synth_is_deterministic_and_uses_the_mix(tmp_path):
+    from pico_hip import gguf, synth
+    arch = synth.tiny_arch(n_layers=2)
+    a = synth.build(tmp_path / "a.gguf", arch, seed=5)
+    b = synth.build(tmp_path / "b.gguf", arch, seed=5)
+    c = synth.build(tmp_path / "c.gguf", arch, seed=6)
+    assert a == b != c
+    g = gguf.load(tmp_path / "a.gguf")
+    types = {t.name: t.ggml_type for t in g.tensors}
+    assert types["blk.0.attn_v.weight"] == dq.Q8_0 and types["blk.1.attn_v.weight"] == dq.Q5_0
+    assert types["blk.0.ffn_down.weight"] == dq.Q6_K and types["blk.1.ffn_down.weight"] == dq.Q4_K
+    assert types["blk.0.attn_q.weight"] == dq.Q5_0 and types["output.weight"] == dq.Q8_0
+    assert "tokenizer.ggml.eos_token_id" not in g.metadata
+    emb = g.tensor("token_embd.weight")
+    out = g.tensor("output.weight")
+    assert bytes(gguf.read_tensor_bytes(g, emb)) == bytes(gguf.read_tensor_bytes(g, out))  # tied
+
+
+def test_7b_mix():
+    from pico_hip import synth
+    a = synth.ARCHES["qwen2.5-7b"]
+    assert synth.q4_k_m_mix(a, 0, "attn_q") == dq.Q4_K
+    assert synth.q4_k_m_mix(a, 3, "attn_v") == dq.Q6_K
+    assert synth.q4_k_m_mix(a, 3, "ffn_down") == dq.Q6_K
+    assert synth.q4_k_m_mix(a, -1, "token_embd") == dq.Q8_0
+
+
+def test_tokenizer_bpe_roundtrip_and_specials():
+    from pico_hip.tokenizer import BPETokenizer, byte_symbols
+    base = [byte_symbols()[b] for b in range(256)]
+    vocab = base + ["he", "ll", "hell", "hello", "Ġw", "Ġwo", "<|im_start|>", "<|im_end|>"]
+    merges = ["h e", "l l", "he ll", "hell o", "Ġ w", "Ġw o"]
+    tok = BPETokenizer(vocab, merges, bos_id=-1, eos_id=vocab.index("<|im_end|>"))
+    ids = tok.encode("<|im_start|>hello world<|im_end|>")
+    assert ids[0] == vocab.index("<|im_start|>") and ids[-1] == vocab.index("<|im_end|>")
+    assert ids[1] == vocab.index("hello") and ids[2] == vocab.index("Ġwo")
+    assert tok.decode(ids[1:-1]) == "hello world"
+    assert tok.decode(tok.encode("naïve €5\n")) == "naïve €5\n"
+    assert tok.n_vocab == len(vocab)
+
+
+def test_tokenizer_from_gguf_metadata():
+    from pico_hip.tokenizer import from_gguf
+    from pico_hip.synth import vocab_tokens
+    tok = from_gguf({"tokenizer.ggml.model": "gpt2", "tokenizer.ggml.tokens": vocab_tokens(300)})
+    assert tok.eos_id == -1 and tok.bos_id == -1
+    assert tok.decode(tok.encode("abc xyz")) == "abc xyz"
+    with pytest.raises(ValueError):
+        from_gguf({"tokenizer.ggml.model": "llama"})
+
+
+def test_sampler():
+    from pico_hip.sampler import sample
+    logits = torch.tensor([0.1, 3.0, 3.0, -1.0])
+    assert sample(logits, temperature=0.0) == 1          # first maximum on ties
+    g = torch.Generator().manual_seed(0)
+    draws = {sample(logits, temperature=1.0, top_k=1, generator=g) for _ in range(40)}
+    assert draws == {1, 2}            # ties with the k-th value survive (sampler.py:23-24)
+    draws = {sample(torch.tensor([0.1, 3.0, 2.0]), 1.0, top_k=1, generator=g) for _ in range(20)}
+    assert draws == {1}
+    draws = {sample(torch.tensor([5.0, 4.9, -9.0]), 1.0, top_p=0.6, generator=g) for _ in range(50)}
+    assert draws <= {0, 1}
+
+
+def test_engine_requires_gpu_device(tiny_model):
+    from pico_hip.engine import Engine
+    with pytest.raises(ValueError, match="GPU only"):
+        Engine(tiny_model, device="cpu")

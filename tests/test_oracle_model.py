@@ -1,0 +1,123 @@
+"""Pins oracle/ref_cpu.py (the torch-CPU restatement of the reference forward) and the
+float64 closed forms it is judged by.
+
+* closed forms against textbook special cases (uniform attention = mean of V, one dominant
+  key = that V row, RoPE at angle 0 = identity and at pi/2 = rotate-half, RMSNorm of a
+  constant vector, GEMV of a one-hot vector = a column);
+* the reference's CPU quantized-GEMV form (int8 + scales) against the float64 GEMV on the
+  dequantized weights, for all four formats;
+* the whole RefModel forward (prefill) against the independent float64 forward in
+  oracle/closed.py on a small synthetic model, and its decode steps against a fresh prefill
+  of the extended sequence (decode-with-cache == recompute), which exercises the cache, the
+  positions and the GQA head mapping;
+* GQA mapping: query head h reads kv head h // group (kernels.py:99), not h % n_kv.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import random_quant, rel_err
+from oracle import closed
+from oracle import dequant as dq
+from oracle import ref_cpu
+
+
+def test_attention_special_cases():
+    rng = np.random.default_rng(0)
+    v = rng.standard_normal((2, 10, 8))
+    k = rng.standard_normal((2, 10, 8))
+    q0 = np.zeros((4, 8))
+    out = closed.attention(q0, k, v, 6)              # uniform weights -> mean of valid V rows
+    np.testing.assert_allclose(out[0], v[0, :6].mean(0), rtol=1e-12)
+    np.testing.assert_allclose(out[3], v[1, :6].mean(0), rtol=1e-12)   # head 3 -> kv 3 // 2 = 1
+    kk = np.zeros((2, 10, 8))
+    kk[:, 4, 0] = 1.0
+    q = np.zeros((4, 8))
+    q[:, 0] = 1e4                                       # key 4 dominates
+    np.testing.assert_allclose(closed.attention(q, kk, v, 10), v[[0, 0, 1, 1], 4], rtol=1e-9)
+    assert closed.attention(q, kk, v, 1)[0].tolist() == v[0, 0].tolist()   # S = 1 -> V[0]
+
+
+def test_rope_and_rmsnorm_special_cases():
+    x = np.arange(8.0)
+    np.testing.assert_allclose(closed.rope(x, np.ones(4), np.zeros(4)), x)
+    np.testing.assert_allclose(closed.rope(x, np.zeros(4), np.ones(4)),
+                               np.concatenate([-x[4:], x[:4]]))
+    c = np.full(16, 3.0)
+    np.testing.assert_allclose(closed.rmsnorm(c, np.full(16, 2.0), 0.0), np.full(16, 2.0))
+    t = torch.tensor([[1.0, 2.0, 3.0, 4.0]])
+    np.testing.assert_allclose(ref_cpu.rmsnorm_cpu(t, torch.ones(4), 1e-6).numpy(),
+                               closed.rmsnorm(t.numpy(), np.ones(4), 1e-6), rtol=1e-6)
+    r = torch.randn(3, 2, 8)
+    cs, sn = torch.randn(3, 1, 4), torch.randn(3, 1, 4)
+    np.testing.assert_allclose(ref_cpu.rope_cpu(r, cs, sn).numpy(),
+                               closed.rope(r.numpy(), cs.numpy(), sn.numpy()), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("t,k", [(dq.Q8_0, 896), (dq.Q5_0, 896), (dq.Q4_K, 4864), (dq.Q6_K, 4864)])
+def test_reference_cpu_gemv_form(t, k):
+    n = 48
+    raw = random_quant(t, n, k, seed=t)
+    W = dq.dequantize(t, raw, n * k).reshape(n, k)
+    entry = ref_cpu._unpacked(t, raw, n, k)
+    x = np.random.default_rng(1).standard_normal(k).astype(np.float32)
+    r = np.random.default_rng(2).standard_normal(n).astype(np.float32)
+    got = ref_cpu.gemv_cpu(entry, torch.from_numpy(x), residual=torch.from_numpy(r)).numpy()
+    assert rel_err(got, closed.gemv(W, x, residual=r)) < 1e-5
+    e = np.zeros(k, np.float32)
+    e[k - 3] = 1.0
+    col = ref_cpu.gemv_cpu(entry, torch.from_numpy(e)).numpy()
+    assert rel_err(col, W[:, k - 3]) < 1e-6
+
+
+@pytest.fixture(scope="module")
+def small(tiny_model):
+    return ref_cpu.RefModel(tiny_model)
+
+
+def _weights64(ref):
+    return {k: v.double().numpy() for k, v in ref.w.items()}
+
+
+def test_ref_forward_matches_float64_forward(small):
+    ids = [3, 1000, 17, 42, 512, 9, 77]
+    cache = small.empty_cache(len(ids))
+    got = small.forward(torch.tensor(ids), torch.arange(len(ids)), cache).numpy()
+    want = closed.forward64(_weights64(small), small.cfg, ids, small.cos.double().numpy(),
+                            small.sin.double().numpy())
+    assert rel_err(got, want) < 1e-4
+
+
+def test_ref_decode_matches_recompute(small):
+    """Decoding token by token with the cache gives the prefill logits of the longer prompt
+    (up to the decode path's fp16 attention rounding and quantized-form GEMVs)."""
+    ids = [5, 6, 7, 8, 900, 901]
+    cache = small.empty_cache(len(ids) + 4)
+    small.forward(torch.tensor(ids[:3]), torch.arange(3), cache)
+    for p in range(3, len(ids)):
+        dec = small.forward(torch.tensor([ids[p]]), torch.tensor([p]), cache).numpy()
+    full = small.forward(torch.tensor(ids), torch.arange(len(ids)), small.empty_cache(len(ids))).numpy()
+    assert rel_err(dec, full) < 5e-3
+
+
+def test_gqa_mapping_is_h_div_group(small):
+    """Make kv heads differ; ref attention must follow h // group (the closed form's rule)."""
+    c = small.cfg
+    cap = 5
+    cache = [(torch.randn(c.n_kv, cap, c.head_dim), torch.randn(c.n_kv, cap, c.head_dim))]
+    q = torch.randn(c.n_head, c.head_dim)
+    group = c.n_head // c.n_kv
+    kr = cache[0][0].repeat_interleave(group, dim=0)
+    vr = cache[0][1].repeat_interleave(group, dim=0)
+    s = torch.softmax(torch.einsum("hd,hsd->hs", q, kr) * c.head_dim ** -0.5, -1)
+    out = torch.einsum("hs,hsd->hd", s, vr).numpy()
+    ref = closed.attention(q.numpy(), cache[0][0].numpy(), cache[0][1].numpy(), cap)
+    assert rel_err(out, ref) < 1e-5
+    # the plausible slip h % n_kv picks other kv heads for some query heads and is caught
+    mod_k = cache[0][0].numpy()[[h % c.n_kv for h in range(c.n_head)]]
+    mod_v = cache[0][1].numpy()[[h % c.n_kv for h in range(c.n_head)]]
+    wrong = closed.attention(q.numpy(), mod_k, mod_v, cap)   # group 1 over the permuted heads
+    assert rel_err(out, wrong) > 1e-2
+    for h in range(c.n_head):
+        np.testing.assert_allclose(out[h], ref[h], rtol=1e-4, atol=1e-6)
