@@ -46,6 +46,18 @@ typedef void* pe_stream_t;
 #define PE_TYPE_Q6_K 14
 #define PE_TYPE_Q8_K 15
 
+/* Vector layouts of the decode entry points (`layout` bit mask).
+ * PE_LAYOUT_NATURAL: x[k] at index k.
+ * PE_LAYOUT_X_UT / PE_LAYOUT_Y_UT: the input x (and the RMSNorm weight) / the output y (and the
+ *   residual) are "unit-transposed": with U = len/32, element k lives at
+ *   ((k % 32) / 4 * U + k / 32) * 4 + k % 4 (8 planes of U float4s). A lane that owns the 32
+ *   weights k = 32u..32u+31 of a row then reads its activations with loads that are
+ *   contiguous across lanes. The decode path keeps every hidden/FFN vector in this layout;
+ *   lengths must be multiples of 32. */
+#define PE_LAYOUT_NATURAL 0
+#define PE_LAYOUT_X_UT 1
+#define PE_LAYOUT_Y_UT 2
+
 enum pe_status {
     PE_OK = 0,
     PE_ERR_NULL = 1,   /* a required pointer is NULL */
@@ -86,33 +98,36 @@ int pe_dequant_tiled(int ggml_type, const void* tiled, float* out, int64_t n_row
                      pe_stream_t stream);
 
 /* out[l][:] = dequantized row ids[l] of a raw GGUF (vocab x hidden) table, l < n_ids.
- * An id outside [0, vocab) yields a row of NaN (no out-of-bounds read).
+ * An id outside [0, vocab) yields a row of NaN (no out-of-bounds read). layout: PE_LAYOUT_Y_UT
+ * writes each row in the unit-transposed layout (hidden % 32 == 0).
  * Replaces the embedding gather self.embed[token_ids] (model.py:152) over the fp32
  * table that _load_weights dequantizes (engine.py:80-98). */
 int pe_embed_gather(int ggml_type, const void* table_blocks, int64_t vocab, int64_t hidden,
-                    const int64_t* ids, int64_t n_ids, float* out, pe_stream_t stream);
+                    const int64_t* ids, int64_t n_ids, float* out, int layout, pe_stream_t stream);
 
 /* ---- decode (M = 1) kernels ---------------------------------------------------------- */
 
 /* y[n] = sum_k W[n][k] x[k] (+ residual[n]) (+ bias[n]) for a tiled W (n_rows x k).
- * residual and bias may be NULL. Types: Q5_0, Q8_0, Q4_K, Q6_K.
+ * residual and bias may be NULL. Types: Q5_0, Q8_0, Q4_K, Q6_K. layout: PE_LAYOUT_* bits for
+ * x (with norm_w in the RMSNorm variants) and y (with residual); bias is always natural.
  * Replaces q8_0_gemv (kernels.py:178), q5_0_gemv (kernels.py:211),
  * q6_k_gemv (kernels.py:286), q4_k_gemv (kernels.py:326), and the fp32 o-projection
  * addmm with residual (model.py:213). */
 int pe_qgemv(int ggml_type, const void* w_tiled, int64_t n_rows, int64_t k, const float* x,
-             const float* residual, const float* bias, float* y, pe_stream_t stream);
+             const float* residual, const float* bias, float* y, int layout, pe_stream_t stream);
 
 /* y = W (rmsnorm(x) * norm_w): RMSNorm of x (length k, eps) fused into the GEMV.
  * Replaces q5_0_gemv_norm (kernels.py:253) for every format, and the final
  * rmsnorm + LM-head q8_0_gemv (model.py:159-162). */
 int pe_qgemv_rmsnorm(int ggml_type, const void* w_tiled, int64_t n_rows, int64_t k,
-                     const float* x, const float* norm_w, float eps, float* y, pe_stream_t stream);
+                     const float* x, const float* norm_w, float eps, float* y, int layout,
+                     pe_stream_t stream);
 
 /* act[j] = silu(g_j) * u_j with g = W[j] h, u = W[ffn + j] h, h = rmsnorm(x) * norm_w,
  * for a tiled W of 2*ffn rows ([gate; up]). norm_w may be NULL (no RMSNorm).
  * Replaces q5_0_gemv_norm + silu_mul (kernels.py:253, :77; model.py:219-224). */
 int pe_qgemv_rmsnorm_silu(int ggml_type, const void* w_tiled, int64_t ffn, int64_t k,
-                          const float* x, const float* norm_w, float eps, float* act,
+                          const float* x, const float* norm_w, float eps, float* act, int layout,
                           pe_stream_t stream);
 
 /* Fused attention prologue of one decode token:
@@ -138,6 +153,7 @@ typedef struct pe_qkv_args {
     int64_t capacity;
     int64_t hidden;
     int n_head, n_kv, head_dim;
+    int layout;                        /* PE_LAYOUT_X_UT: x and norm_w unit-transposed */
 } pe_qkv_args;
 int pe_qkv_rmsnorm_rope(const pe_qkv_args* args, pe_stream_t stream);
 
@@ -151,12 +167,13 @@ int pe_qkv_rmsnorm_rope(const pe_qkv_args* args, pe_stream_t stream);
  * workspace: pe_decode_attn_workspace_bytes(...) bytes, zero-filled once before first use;
  * it is left zeroed again after every call, so one workspace serves any number of calls
  * made in order on one stream (calls that overlap must not share it).
+ * layout: PE_LAYOUT_Y_UT writes out as one unit-transposed vector of n_head*hd elements.
  * Replaces decode_attn (kernels.py:129). */
 int64_t pe_decode_attn_workspace_bytes(int n_head, int n_kv, int head_dim, int64_t capacity);
 int pe_decode_attn(const float* q, const float* k_cache, const float* v_cache, int n_head,
                    int n_kv, int head_dim, int64_t capacity, const void* len_dev, int len_dtype,
                    int64_t len_add, float scale, int round_fp16, float* out, void* workspace,
-                   int64_t workspace_bytes, pe_stream_t stream);
+                   int64_t workspace_bytes, int layout, pe_stream_t stream);
 
 /* ---- general / prefill (M >= 1) kernels ------------------------------------------------ */
 

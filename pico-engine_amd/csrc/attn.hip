@@ -11,6 +11,8 @@
 // log-sum-exp rule in a fixed order and resets the counter, so no second launch is needed and
 // the result does not depend on which workgroup finished last.
 //
+// Caches of at most 1024 positions use a single-pass kernel (one workgroup per query head).
+//
 // Prefill (L query tokens, causal), restating the fp32 SDPA call of model.py:201-209.
 #include "pe_common.h"
 
@@ -34,7 +36,12 @@ struct AttnParams {
     unsigned* counters;
     float* partials;
     int nsplit;
+    int out_ut;  // write out in the unit-transposed layout
 };
+
+PE_DEV int64_t attn_out_index(const AttnParams& p, int64_t i, int64_t total) {
+    return p.out_ut ? ut_index(i, total >> 5) : i;
+}
 
 PE_DEV int64_t valid_len(const AttnParams& p) {
     int64_t S = p.len_add;
@@ -112,9 +119,9 @@ __global__ __launch_bounds__(256) void k_decode_attn(AttnParams p) {
             const int w = t >> 6, lane = t & 63;
             for (int g = w; g < G; g += 4) {
                 const float v = sc_lds[g * kChunk + lane];
-                const float m = group_max<64>(v);
+                const float m = wave_max<64>(v);
                 const float e = expf(v - m);
-                const float l = group_sum<64>(e);
+                const float l = wave_sum<64>(e);
                 sc_lds[g * kChunk + lane] = e;
                 if (lane == 0) {
                     ml_lds[2 * g] = m;
@@ -177,9 +184,101 @@ __global__ __launch_bounds__(256) void k_decode_attn(AttnParams p) {
         }
         float o = A / L;
         if (p.round_fp16) o = round_to_f16(o);
-        p.out[((int64_t)kvh * G + g) * HD + dd] = o;
+        p.out[attn_out_index(p, ((int64_t)kvh * G + g) * HD + dd, (int64_t)p.n_kv * G * HD)] = o;
     }
     if (t == 0) p.counters[kvh] = 0u;
+}
+
+// ---------------------------------------------------------------------------------------
+// Short caches (capacity <= kSmallCap): one workgroup per query head does the whole softmax
+// in one pass -- scores of all S positions into LDS (thread per position), block max/sum,
+// P.V with a thread per (dim, position slice) -- so there is no split, no device-scope
+// fence and no merge on the latency-critical path of a short decode.
+constexpr int kSmallCap = 1024;
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_decode_attn_head(AttnParams p) {
+    constexpr int PS = 256 / HD;   // position slices in the P.V phase
+    constexpr int NPRE = 24;       // V values per thread fetched up front (S <= 24 * PS)
+    __shared__ float q_lds[HD];
+    __shared__ float sc[kSmallCap];
+    __shared__ float red[256];
+    __shared__ float lds4[4];
+    const int t = threadIdx.x, h = blockIdx.x, kvh = h / p.group;
+    const int64_t S = valid_len(p);
+    const float* kb = p.k + (int64_t)kvh * p.capacity * HD;
+    const float* vb = p.v + (int64_t)kvh * p.capacity * HD;
+    const int d = t % HD, js = t / HD;
+    // all first-round loads in flight together: q, this thread's first K row, first V values
+    float4 k0[HD / 4];
+    if (t < S) {
+#pragma unroll
+        for (int i = 0; i < HD / 4; ++i) k0[i] = reinterpret_cast<const float4*>(kb + (int64_t)t * HD)[i];
+    }
+    float vpre[NPRE];
+#pragma unroll
+    for (int j = 0; j < NPRE; ++j) {
+        const int sp = js + j * PS;
+        vpre[j] = sp < S ? vb[(int64_t)sp * HD + d] : 0.f;
+    }
+    if (t < HD) q_lds[t] = p.q[(int64_t)h * HD + t];
+    __syncthreads();
+    const float NEG_INF = -__builtin_huge_valf();
+    float m_loc = NEG_INF;
+    for (int s = t; s < S; s += 256) {
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < HD / 4; ++i) {
+            const float4 k4 = s == t ? k0[i] : reinterpret_cast<const float4*>(kb + (int64_t)s * HD)[i];
+            dot += q_lds[4 * i] * k4.x;
+            dot += q_lds[4 * i + 1] * k4.y;
+            dot += q_lds[4 * i + 2] * k4.z;
+            dot += q_lds[4 * i + 3] * k4.w;
+        }
+        const float v = dot * p.scale;
+        sc[s] = v;
+        m_loc = fmaxf(m_loc, v);
+    }
+    m_loc = wave_max<64>(m_loc);
+    if ((t & 63) == 0) lds4[t >> 6] = m_loc;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(lds4[0], lds4[1]), fmaxf(lds4[2], lds4[3]));
+    float l_loc = 0.f;
+    for (int s = t; s < S; s += 256) {
+        const float e = expf(sc[s] - M);
+        sc[s] = e;
+        l_loc += e;
+    }
+    l_loc = wave_sum<64>(l_loc);
+    __syncthreads();  // every read of lds4 (max) is done and sc[] holds the exponentials
+    if ((t & 63) == 0) lds4[t >> 6] = l_loc;
+    __syncthreads();
+    const float L = ((lds4[0] + lds4[1]) + lds4[2]) + lds4[3];
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < NPRE; ++j) {
+        const int sp = js + j * PS;
+        if (sp < S) acc += sc[sp] * vpre[j];
+    }
+    int s = js + NPRE * PS;
+    for (; s + 7 * PS < S; s += 8 * PS) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = vb[(int64_t)(s + j * PS) * HD + d];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc += sc[s + j * PS] * v[j];
+    }
+    for (; s < S; s += PS) acc += sc[s] * vb[(int64_t)s * HD + d];
+    red[js * HD + d] = acc;
+    __syncthreads();
+    if (t < HD) {
+        float a = 0.f;
+#pragma unroll
+        for (int j = 0; j < PS; ++j) a += red[j * HD + t];
+        float o = a / L;
+        if (p.round_fp16) o = round_to_f16(o);
+        p.out[attn_out_index(p, (int64_t)h * HD + t, (int64_t)p.n_kv * p.group * HD)] = o;
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -197,14 +296,14 @@ struct PrefillParams {
 };
 
 PE_DEV float block_max256(float v, float* lds4) {
-    v = group_max<64>(v);
+    v = wave_max<64>(v);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) lds4[threadIdx.x >> 6] = v;
     __syncthreads();
     return fmaxf(fmaxf(lds4[0], lds4[1]), fmaxf(lds4[2], lds4[3]));
 }
 PE_DEV float block_sum256(float v, float* lds4) {
-    v = group_sum<64>(v);
+    v = wave_sum<64>(v);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) lds4[threadIdx.x >> 6] = v;
     __syncthreads();
@@ -290,11 +389,13 @@ extern "C" int64_t pe_decode_attn_workspace_bytes(int n_head, int n_kv, int head
 extern "C" int pe_decode_attn(const float* q, const float* k_cache, const float* v_cache, int n_head,
                               int n_kv, int head_dim, int64_t capacity, const void* len_dev,
                               int len_dtype, int64_t len_add, float scale, int round_fp16,
-                              float* out, void* workspace, int64_t workspace_bytes,
+                              float* out, void* workspace, int64_t workspace_bytes, int layout,
                               pe_stream_t stream) {
     const int64_t need = pe_decode_attn_workspace_bytes(n_head, n_kv, head_dim, capacity);
     if (need < 0) return (int)-need;
     if (len_dtype < 0 || len_dtype > 2) return PE_ERR_TYPE;
+    if (layout & ~PE_LAYOUT_Y_UT) return PE_ERR_TYPE;
+    if ((layout & PE_LAYOUT_Y_UT) && ((int64_t)n_head * head_dim) % 32) return PE_ERR_SHAPE;
     if (attn_nsplit(capacity) > 65535) return PE_ERR_SHAPE;
     if (!q || !k_cache || !v_cache || !out || !workspace || (len_dtype && !len_dev))
         return PE_ERR_NULL;
@@ -305,9 +406,18 @@ extern "C" int pe_decode_attn(const float* q, const float* k_cache, const float*
         return PE_ERR_ALIGN;
     AttnParams p{q, k_cache, v_cache, n_kv, n_head / n_kv, capacity, len_dev, len_dtype, len_add,
                  scale, round_fp16, out, (unsigned*)workspace,
-                 (float*)((char*)workspace + 256), (int)attn_nsplit(capacity)};
-    dim3 grid((unsigned)p.nsplit, (unsigned)n_kv);
+                 (float*)((char*)workspace + 256), (int)attn_nsplit(capacity),
+                 (layout & PE_LAYOUT_Y_UT) ? 1 : 0};
     hipStream_t s = (hipStream_t)stream;
+    if (capacity <= kSmallCap) {
+        const dim3 grid((unsigned)n_head);
+        if (head_dim == 64)
+            hipLaunchKernelGGL(k_decode_attn_head<64>, grid, dim3(256), 0, s, p);
+        else
+            hipLaunchKernelGGL(k_decode_attn_head<128>, grid, dim3(256), 0, s, p);
+        return launch_status();
+    }
+    const dim3 grid((unsigned)p.nsplit, (unsigned)n_kv);
     if (head_dim == 64)
         hipLaunchKernelGGL(k_decode_attn<64>, grid, dim3(256), 0, s, p);
     else

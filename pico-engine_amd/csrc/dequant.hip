@@ -132,14 +132,15 @@ __global__ void k_dequant_tiled(Tiled t, int64_t k, float* __restrict__ out) {
 
 __global__ void k_embed_gather(int type, const uint8_t* __restrict__ table, int64_t vocab,
                                int64_t hidden, const int64_t* __restrict__ ids, int64_t n_ids,
-                               float* __restrict__ out) {
+                               float* __restrict__ out, int out_ut) {
     const int64_t total = n_ids * hidden;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
         const int64_t l = i / hidden, c = i % hidden;
         const int64_t id = ids[l];
-        out[i] = (id >= 0 && id < vocab) ? raw_element(type, table, id * hidden + c)
-                                         : __uint_as_float(0x7FC00000u);
+        const int64_t dst = out_ut ? l * hidden + ut_index(c, hidden >> 5) : i;
+        out[dst] = (id >= 0 && id < vocab) ? raw_element(type, table, id * hidden + c)
+                                           : __uint_as_float(0x7FC00000u);
     }
 }
 
@@ -202,15 +203,18 @@ extern "C" int pe_dequant_tiled(int type, const void* tiled, float* out, int64_t
 }
 
 extern "C" int pe_embed_gather(int type, const void* table, int64_t vocab, int64_t hidden,
-                               const int64_t* ids, int64_t n_ids, float* out, pe_stream_t stream) {
+                               const int64_t* ids, int64_t n_ids, float* out, int layout,
+                               pe_stream_t stream) {
     if (block_elems(type) == 0) return PE_ERR_TYPE;
+    if (layout & ~PE_LAYOUT_Y_UT) return PE_ERR_TYPE;
+    if ((layout & PE_LAYOUT_Y_UT) && hidden % 32) return PE_ERR_SHAPE;
     if (vocab <= 0 || hidden <= 0 || n_ids < 0 || hidden % block_elems(type)) return PE_ERR_SHAPE;
     if (n_ids == 0) return PE_OK;
     if (!table || !ids || !out) return PE_ERR_NULL;
     if (!aligned(ids, 8) || !aligned(out, 4)) return PE_ERR_ALIGN;
     hipLaunchKernelGGL(k_embed_gather, dim3(grid_for(n_ids * hidden, 256)), dim3(256), 0,
                        (hipStream_t)stream, type, (const uint8_t*)table, vocab, hidden, ids, n_ids,
-                       out);
+                       out, (layout & PE_LAYOUT_Y_UT) ? 1 : 0);
     return launch_status();
 }
 
@@ -227,4 +231,4 @@ extern "C" const char* pe_strerror(int status) {
     }
 }
 
-extern "C" int pe_abi_version(void) { return 1; }
+extern "C" int pe_abi_version(void) { return 2; }

@@ -16,7 +16,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x, in
     const float* xr = x + r * xs;
     float ss = 0.f;
     for (int64_t i = threadIdx.x; i < n; i += 256) ss += xr[i] * xr[i];
-    ss = group_sum<64>(ss);
+    ss = wave_sum<64>(ss);
     if ((threadIdx.x & 63) == 0) lds4[threadIdx.x >> 6] = ss;
     __syncthreads();
     ss = ((lds4[0] + lds4[1]) + lds4[2]) + lds4[3];

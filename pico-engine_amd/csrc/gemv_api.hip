@@ -27,38 +27,49 @@ static int check_weight(int type, const void* w, int64_t n_rows, int64_t k) {
 
 using namespace pe;
 
+static int check_layout(int layout, int64_t n_out) {
+    if (layout & ~(PE_LAYOUT_X_UT | PE_LAYOUT_Y_UT)) return PE_ERR_TYPE;
+    if ((layout & PE_LAYOUT_Y_UT) && n_out % 32) return PE_ERR_SHAPE;
+    return PE_OK;
+}
+
 extern "C" int pe_qgemv(int type, const void* w, int64_t n_rows, int64_t k, const float* x,
-                        const float* residual, const float* bias, float* y, pe_stream_t stream) {
+                        const float* residual, const float* bias, float* y, int layout,
+                        pe_stream_t stream) {
     int st = check_weight(type, w, n_rows, k);
     if (st) return st;
+    if ((st = check_layout(layout, n_rows))) return st;
     if (!x || !y) return PE_ERR_NULL;
     if (!aligned(x, 16) || !aligned(y, 4) || !aligned(residual, 4) || !aligned(bias, 4))
         return PE_ERR_ALIGN;
     GemvArgs a{Tiled{(const uint8_t*)w, n_rows, k / block_elems(type)},
-               n_rows, k, x, nullptr, 0.f, residual, bias, y, 0};
+               n_rows, k, x, nullptr, 0.f, residual, bias, y, 0, layout};
     return dispatch_gemv(type, a, false, kModePlain, (hipStream_t)stream);
 }
 
 extern "C" int pe_qgemv_rmsnorm(int type, const void* w, int64_t n_rows, int64_t k, const float* x,
-                                const float* norm_w, float eps, float* y, pe_stream_t stream) {
+                                const float* norm_w, float eps, float* y, int layout,
+                                pe_stream_t stream) {
     int st = check_weight(type, w, n_rows, k);
     if (st) return st;
+    if ((st = check_layout(layout, n_rows))) return st;
     if (!x || !norm_w || !y) return PE_ERR_NULL;
     if (!aligned(x, 16) || !aligned(norm_w, 16) || !aligned(y, 4)) return PE_ERR_ALIGN;
     GemvArgs a{Tiled{(const uint8_t*)w, n_rows, k / block_elems(type)},
-               n_rows, k, x, norm_w, eps, nullptr, nullptr, y, 0};
+               n_rows, k, x, norm_w, eps, nullptr, nullptr, y, 0, layout};
     return dispatch_gemv(type, a, true, kModePlain, (hipStream_t)stream);
 }
 
 extern "C" int pe_qgemv_rmsnorm_silu(int type, const void* w, int64_t ffn, int64_t k,
                                      const float* x, const float* norm_w, float eps, float* act,
-                                     pe_stream_t stream) {
+                                     int layout, pe_stream_t stream) {
     int st = check_weight(type, w, 2 * ffn, k);
     if (st) return st;
+    if ((st = check_layout(layout, ffn))) return st;
     if (!x || !act) return PE_ERR_NULL;
     if (!aligned(x, 16) || !aligned(norm_w, 16) || !aligned(act, 4)) return PE_ERR_ALIGN;
     GemvArgs a{Tiled{(const uint8_t*)w, 2 * ffn, k / block_elems(type)},
-               ffn, k, x, norm_w, eps, nullptr, nullptr, act, ffn};
+               ffn, k, x, norm_w, eps, nullptr, nullptr, act, ffn, layout};
     return dispatch_gemv(type, a, norm_w != nullptr, kModeSilu, (hipStream_t)stream);
 }
 

@@ -26,6 +26,7 @@ struct GemvArgs {
     const float* bias;
     float* y;
     int64_t up_off;       // SiLU mode: row of the "up" half = task + up_off
+    int layout;           // PE_LAYOUT_* bits: x (and norm_w) / y (and residual) in ut layout
 };
 
 // Sum over a group of GS lanes. GS = 256 is the whole block: wave butterflies, then the four
@@ -33,10 +34,10 @@ struct GemvArgs {
 template <int GS>
 PE_DEV float gsum(float v, float* lds4) {
     if constexpr (GS <= 64) {
-        return group_sum<GS>(v);
+        return wave_sum<GS>(v);
     } else {
         static_assert(GS == 256, "group is a wave part or the whole block");
-        v = group_sum<64>(v);
+        v = wave_sum<64>(v);
         const int w = threadIdx.x >> 6;
         __syncthreads();
         if ((threadIdx.x & 63) == 0) lds4[w] = v;
@@ -45,82 +46,234 @@ PE_DEV float gsum(float v, float* lds4) {
     }
 }
 
-// Load this lane's UPL activation units; with NORM, replace them by rmsnorm(x) * norm_w.
-// rstd = 1 / sqrt(sum(x^2) / k + eps) (kernels.py:21-23).
+// Activations are staged through LDS: the workgroup reads x (and the RMSNorm weight) with
+// fully coalesced 16-byte loads into a padded layout (36 floats per 32-float unit, so the
+// per-lane 16-byte LDS reads of a unit are bank-conflict free), reduces sum(x^2) across the
+// block, and each lane then reads its own units from LDS. Loading its 128 contiguous bytes
+// straight from global memory made every lane touch a different cache line per instruction.
+// kStageMaxK bounds the staged length (dynamic LDS of 2 * kStageMaxK * 36/32 floats); longer
+// activations (no RMSNorm at those lengths) are read per lane.
+constexpr int kStageMaxK = 8192;
+constexpr int kUnitStride = 36;  // floats per staged unit
+
+inline size_t stage_lds_bytes(int64_t k, bool norm) {
+    return k <= kStageMaxK ? (size_t)(k / 32) * kUnitStride * 4 * (norm ? 2 : 1) : 0;
+}
+
+// Block-wide sum (every thread of the block must call it): a one-wave block reduces with DPP
+// only; a 256-thread block adds the four wave sums in wave order through LDS.
+template <int BS>
+PE_DEV float block_sum(float v, float* lds4) {
+    v = wave_sum<64>(v);
+    if constexpr (BS == 64) {
+        return v;
+    } else {
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) lds4[threadIdx.x >> 6] = v;
+        __syncthreads();
+        return ((lds4[0] + lds4[1]) + lds4[2]) + lds4[3];
+    }
+}
+
+// Threads per block for a group width: one wave for GS <= 64 (no block barriers on the
+// latency path), four waves for GS = 256.
+template <int GS>
+constexpr int block_threads() { return GS <= 64 ? 64 : 256; }
+
+// Load this lane's UPL activation units; with NORM, replace them by rmsnorm(x) * norm_w
+// (rstd = 1 / sqrt(sum(x^2) / k + eps), kernels.py:21-23); then the per-unit sums.
+// Every thread of the block must call it (it synchronises the block).
 template <int GS, int UPL, bool NORM>
 PE_DEV void load_activation(const GemvArgs& a, int glane, int units, float (&xr)[UPL][32],
-                            float* lds4) {
+                            UnitSums (&xs)[UPL], float* lds4, float* stage) {
+    constexpr int BS = block_threads<GS>();
+    if (a.layout & PE_LAYOUT_X_UT) {
+        // coalesced direct loads, no staging; the RMSNorm sum is reduced across the group.
 #pragma unroll
-    for (int t = 0; t < UPL; ++t) {
-        const int u = glane + GS * t;
-        if (u < units) {
-            load_x_unit(a.x, u, xr[t]);
-        } else {
+        for (int t = 0; t < UPL; ++t) {
+            const int u = glane + GS * t;
+            if (u < units) {
+                load_x_unit_ut(a.x, u, units, xr[t]);
+            } else {
 #pragma unroll
-            for (int i = 0; i < 32; ++i) xr[t][i] = 0.f;
+                for (int i = 0; i < 32; ++i) xr[t][i] = 0.f;
+            }
+        }
+        if constexpr (NORM) {
+            float ss = 0.f;
+#pragma unroll
+            for (int t = 0; t < UPL; ++t)
+#pragma unroll
+                for (int i = 0; i < 32; ++i) ss += xr[t][i] * xr[t][i];
+            const float rstd = 1.0f / sqrtf(gsum<GS>(ss, lds4) / (float)a.k + a.eps);
+#pragma unroll
+            for (int t = 0; t < UPL; ++t) {
+                const int u = glane + GS * t;
+                if (u < units) {
+                    float wr[32];
+                    load_x_unit_ut(a.norm_w, u, units, wr);
+#pragma unroll
+                    for (int i = 0; i < 32; ++i) xr[t][i] = (xr[t][i] * rstd) * wr[i];
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < UPL; ++t) xs[t] = unit_sums(xr[t]);
+        return;
+    }
+    const bool staged = a.k <= kStageMaxK;
+    float ss = 0.f;
+    if (staged) {
+        float* sx = stage;
+        float* sw = stage + units * kUnitStride;
+        const int n4 = (int)(a.k >> 2);
+        for (int i = threadIdx.x; i < n4; i += BS) {
+            const float4 v = reinterpret_cast<const float4*>(a.x)[i];
+            const int off = (i >> 3) * kUnitStride + (i & 7) * 4;
+            *reinterpret_cast<float4*>(sx + off) = v;
+            if constexpr (NORM) {
+                *reinterpret_cast<float4*>(sw + off) = reinterpret_cast<const float4*>(a.norm_w)[i];
+                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < UPL; ++t) {
+            const int u = glane + GS * t;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (u < units) v = *reinterpret_cast<const float4*>(sx + u * kUnitStride + 4 * i);
+                xr[t][4 * i] = v.x; xr[t][4 * i + 1] = v.y; xr[t][4 * i + 2] = v.z; xr[t][4 * i + 3] = v.w;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < UPL; ++t) {
+            const int u = glane + GS * t;
+            if (u < units) {
+                load_x_unit(a.x, u, xr[t]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 32; ++i) xr[t][i] = 0.f;
+            }
         }
     }
     if constexpr (NORM) {
-        float ss = 0.f;
+        float rstd;
+        if (staged) {
+            rstd = 1.0f / sqrtf(block_sum<BS>(ss, lds4) / (float)a.k + a.eps);
+        } else {
 #pragma unroll
-        for (int t = 0; t < UPL; ++t)
+            for (int t = 0; t < UPL; ++t)
 #pragma unroll
-            for (int i = 0; i < 32; ++i) ss += xr[t][i] * xr[t][i];
-        ss = gsum<GS>(ss, lds4);
-        const float rstd = 1.0f / sqrtf(ss / (float)a.k + a.eps);
+                for (int i = 0; i < 32; ++i) ss += xr[t][i] * xr[t][i];
+            rstd = 1.0f / sqrtf(gsum<GS>(ss, lds4) / (float)a.k + a.eps);
+        }
 #pragma unroll
         for (int t = 0; t < UPL; ++t) {
             const int u = glane + GS * t;
             if (u < units) {
                 float wr[32];
-                load_x_unit(a.norm_w, u, wr);
+                if (staged) {
+                    const float* sw = stage + units * kUnitStride + u * kUnitStride;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const float4 v = *reinterpret_cast<const float4*>(sw + 4 * i);
+                        wr[4 * i] = v.x; wr[4 * i + 1] = v.y; wr[4 * i + 2] = v.z; wr[4 * i + 3] = v.w;
+                    }
+                } else {
+                    load_x_unit(a.norm_w, u, wr);
+                }
 #pragma unroll
                 for (int i = 0; i < 32; ++i) xr[t][i] = (xr[t][i] * rstd) * wr[i];
             }
         }
     }
+#pragma unroll
+    for (int t = 0; t < UPL; ++t) xs[t] = unit_sums(xr[t]);
 }
 
+template <int T, int GS, int UPL, int R>
+PE_DEV void load_task(const GemvArgs& a, int64_t task, int glane, int units,
+                      typename Fmt<T>::Raw (&raw)[R][UPL]) {
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr)
+#pragma unroll
+        for (int t = 0; t < UPL; ++t) {
+            const int u = glane + GS * t;
+            if (u < units) Fmt<T>::load(a.w, task + rr * a.up_off, u, raw[rr][t]);
+        }
+}
+
+// Epilogue operands of a task (lane 0 of the group only), fetched with the weights.
+struct Epi {
+    float res, bias;
+};
+PE_DEV int64_t out_index(const GemvArgs& a, int64_t task) {
+    return (a.layout & PE_LAYOUT_Y_UT) ? ut_index(task, a.n_tasks >> 5) : task;
+}
+PE_DEV Epi load_epi(const GemvArgs& a, int64_t task, bool lane0) {
+    Epi e{0.f, 0.f};
+    if (lane0) {
+        if (a.residual) e.res = a.residual[out_index(a, task)];
+        if (a.bias) e.bias = a.bias[task];
+    }
+    return e;
+}
+
+// Timeline per group: issue the first task's weight (and epilogue) loads, then load and
+// normalise the activations while those are in flight; per task: dot products on the
+// weights in registers, issue the next task's loads, reduce, store.
 template <int T, int GS, int UPL, bool NORM, int MODE>
-__global__ __launch_bounds__(256) void k_qgemv(GemvArgs a) {
-    constexpr int GPB = 256 / GS;
+__global__ __launch_bounds__(block_threads<GS>()) void k_qgemv(GemvArgs a) {
+    constexpr int GPB = block_threads<GS>() / GS;
     constexpr int R = (MODE == kModeSilu) ? 2 : 1;
     __shared__ float lds4[4];
+    extern __shared__ float stage[];
     const int glane = threadIdx.x % GS;
     const int gid = threadIdx.x / GS;
     const int units = (int)(a.k >> 5);
+    const int64_t stride = (int64_t)gridDim.x * GPB;
+    int64_t task = (int64_t)blockIdx.x * GPB + gid;
+
+    typename Fmt<T>::Raw raw[R][UPL];
+    Epi epi{0.f, 0.f};
+    if (task < a.n_tasks) {
+        load_task<T, GS, UPL, R>(a, task, glane, units, raw);
+        if constexpr (MODE == kModePlain) epi = load_epi(a, task, glane == 0);
+    }
 
     float xr[UPL][32];
-    load_activation<GS, UPL, NORM>(a, glane, units, xr, lds4);
+    UnitSums xs[UPL];
+    load_activation<GS, UPL, NORM>(a, glane, units, xr, xs, lds4, stage);
 
-    const int64_t stride = (int64_t)gridDim.x * GPB;
-    for (int64_t task = (int64_t)blockIdx.x * GPB + gid; task < a.n_tasks; task += stride) {
-        typename Fmt<T>::Raw raw[R][UPL];
-#pragma unroll
-        for (int rr = 0; rr < R; ++rr)
-#pragma unroll
-            for (int t = 0; t < UPL; ++t) {
-                const int u = glane + GS * t;
-                if (u < units) Fmt<T>::load(a.w, task + rr * a.up_off, u, raw[rr][t]);
-            }
+    for (; task < a.n_tasks; task += stride) {
         float acc[R];
 #pragma unroll
         for (int rr = 0; rr < R; ++rr) {
             acc[rr] = 0.f;
 #pragma unroll
             for (int t = 0; t < UPL; ++t)
-                if (glane + GS * t < units) acc[rr] += Fmt<T>::dot(raw[rr][t], xr[t]);
-            acc[rr] = gsum<GS>(acc[rr], lds4);
+                if (glane + GS * t < units) acc[rr] += Fmt<T>::dot(raw[rr][t], xr[t], xs[t]);
         }
+        const Epi cur = epi;
+        const int64_t next = task + stride;
+        if (next < a.n_tasks) {
+            load_task<T, GS, UPL, R>(a, next, glane, units, raw);
+            if constexpr (MODE == kModePlain) epi = load_epi(a, next, glane == 0);
+        }
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr) acc[rr] = gsum<GS>(acc[rr], lds4);
         if (glane == 0) {
             if constexpr (MODE == kModeSilu) {
                 const float g = acc[0], u = acc[1];
-                a.y[task] = (g * (1.0f / (1.0f + expf(-g)))) * u;
+                a.y[out_index(a, task)] = (g * (1.0f / (1.0f + expf(-g)))) * u;
             } else {
                 float v = acc[0];
-                if (a.bias) v += a.bias[task];
-                if (a.residual) v = a.residual[task] + v;
-                a.y[task] = v;
+                if (a.bias) v += cur.bias;
+                if (a.residual) v = cur.res + v;
+                a.y[out_index(a, task)] = v;
             }
         }
     }
@@ -142,14 +295,18 @@ inline bool pick_shape(int64_t units, Shape& s) {
     return true;
 }
 
-constexpr int kMaxGemvBlocks = 2048;
+constexpr int kMaxGemvBlocks = 2048;    // 256-thread blocks (prefill GEMM, GS = 256)
+constexpr int kMaxWaveBlocks = 8192;    // one-wave blocks: up to 32 resident waves per CU
 
 template <int T, int GS, int UPL, bool NORM, int MODE>
 void launch_qgemv_shape(const GemvArgs& a, hipStream_t s) {
-    constexpr int GPB = 256 / GS;
+    constexpr int BS = block_threads<GS>();
+    constexpr int GPB = BS / GS;
     int64_t blocks = (a.n_tasks + GPB - 1) / GPB;
-    if (blocks > kMaxGemvBlocks) blocks = kMaxGemvBlocks;
-    hipLaunchKernelGGL((k_qgemv<T, GS, UPL, NORM, MODE>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+    const int64_t cap = BS == 64 ? kMaxWaveBlocks : kMaxGemvBlocks;
+    if (blocks > cap) blocks = cap;
+    const size_t lds = (a.layout & PE_LAYOUT_X_UT) ? 0 : stage_lds_bytes(a.k, NORM);
+    hipLaunchKernelGGL((k_qgemv<T, GS, UPL, NORM, MODE>), dim3((unsigned)blocks), dim3(BS), lds, s, a);
 }
 
 template <int T, bool NORM, int MODE>

@@ -39,6 +39,54 @@ PE_DEV float group_sum(float v) {
     return v;
 }
 
+// DPP / permlane butterflies (gfx950): xor-1 and xor-2 by quad_perm, then the half-row and
+// row mirrors pair lanes of the other quad / half, then permlane16/32 swaps pair rows. Every
+// lane of the group ends with the same bits (each step adds the same two operands).
+template <int CTRL>
+PE_DEV float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+PE_DEV float swap16_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+    return __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+}
+PE_DEV float swap32_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+    return __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+}
+PE_DEV float swap16_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+    return fmaxf(__builtin_bit_cast(float, (int)r[0]), __builtin_bit_cast(float, (int)r[1]));
+}
+PE_DEV float swap32_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+    return fmaxf(__builtin_bit_cast(float, (int)r[0]), __builtin_bit_cast(float, (int)r[1]));
+}
+
+// Sum over aligned groups of W lanes (16, 32 or 64) with DPP; all lanes get the same bits.
+template <int W>
+PE_DEV float wave_sum(float v) {
+    static_assert(W == 16 || W == 32 || W == 64, "row, half-wave or wave");
+    v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_mov<0x141>(v);  // row_half_mirror
+    v += dpp_mov<0x140>(v);  // row_mirror
+    if constexpr (W >= 32) v = swap16_sum(v);
+    if constexpr (W == 64) v = swap32_sum(v);
+    return v;
+}
+template <int W>
+PE_DEV float wave_max(float v) {
+    static_assert(W == 16 || W == 32 || W == 64, "row, half-wave or wave");
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    v = fmaxf(v, dpp_mov<0x140>(v));
+    if constexpr (W >= 32) v = swap16_max(v);
+    if constexpr (W == 64) v = swap32_max(v);
+    return v;
+}
+
 template <int W>
 PE_DEV float group_max(float v) {
 #pragma unroll
@@ -51,6 +99,40 @@ PE_DEV uint32_t ubyte(uint32_t w, int byte) { return (w >> (8 * byte)) & 0xFFu; 
 
 PE_DEV uint32_t word_of(const int4& v, int i) {
     return (uint32_t)(i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w);
+}
+
+// Per-unit activation sums, computed once per kernel and shared by every row: the fast
+// dot products below multiply unsigned byte codes and fold the codes' offsets (+128 for
+// Q8_0, -16 for Q5_0, -32 for Q6_K, the Q4_K min) into these sums.
+struct UnitSums {
+    float all;  // sum of the unit's 32 activations
+    float lo;   // sum of the first 16
+};
+
+PE_DEV UnitSums unit_sums(const float* x) {
+    float a = 0.f, b = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) a += x[i];
+#pragma unroll
+    for (int i = 16; i < 32; ++i) b += x[i];
+    return {a + b, a};
+}
+
+// byte b (0..3) of w as a float: one v_cvt_f32_ubyte<b>
+PE_DEV float fbyte(uint32_t w, int b) { return (float)((w >> (8 * b)) & 0xFFu); }
+
+// Sum over the four bytes of `codes` (unsigned) times x[0..3].
+PE_DEV float dot4(uint32_t codes, const float* x, float acc) {
+    acc += fbyte(codes, 0) * x[0];
+    acc += fbyte(codes, 1) * x[1];
+    acc += fbyte(codes, 2) * x[2];
+    acc += fbyte(codes, 3) * x[3];
+    return acc;
+}
+
+// Four bits of `bits` (bit i -> byte i, at bit position 4 of the byte): 0x10 per set bit.
+PE_DEV uint32_t spread4_to_bit4(uint32_t bits4) {
+    return (__umul24(bits4, 0x204081u) & 0x01010101u) << 4;
 }
 
 // 6-bit scale and min of sub-block j (0..7) from the 12 packed Q4_K scale bytes
@@ -97,11 +179,13 @@ struct Fmt<PE_TYPE_Q8_0> {
         const int4& v = i < 16 ? r.a : r.b;
         return sext8(word_of(v, (i & 15) >> 2), i & 3);
     }
-    static PE_DEV float dot(const Raw& r, const float* x) {
+    // sum (q + 128) x - 128 sum x, q + 128 = byte ^ 0x80 (exact codes, 2 ops per weight)
+    static PE_DEV float dot(const Raw& r, const float* x, const UnitSums& xs) {
         float acc = 0.f;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) acc += (float)code(r, i) * x[i];
-        return acc * h2f(r.d);
+        for (int w = 0; w < 8; ++w)
+            acc = dot4(word_of(w < 4 ? r.a : r.b, w & 3) ^ 0x80808080u, x + 4 * w, acc);
+        return (acc - 128.f * xs.all) * h2f(r.d);
     }
     static PE_DEV void dequant(const Raw& r, float* w) {
         const float d = h2f(r.d);
@@ -133,11 +217,19 @@ struct Fmt<PE_TYPE_Q5_0> {
         const uint32_t nib = e < 16 ? (byte & 0xFu) : (byte >> 4);
         return (int)(nib | (((r.qh >> e) & 1u) << 4));
     }
-    static PE_DEV float dot(const Raw& r, const float* x) {
+    // codes of 4 elements at once: nibbles by mask, 5th bits spread from qh by a multiply
+    static PE_DEV float dot(const Raw& r, const float* x, const UnitSums& xs) {
         float acc = 0.f;
 #pragma unroll
-        for (int e = 0; e < 32; ++e) acc += (float)(code(r, e) - 16) * x[e];
-        return acc * h2f(r.d);
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t v = word_of(r.qs, w);
+            const uint32_t lo = (v & 0x0F0F0F0Fu) | spread4_to_bit4(__builtin_amdgcn_ubfe(r.qh, 4 * w, 4));
+            const uint32_t hi = ((v >> 4) & 0x0F0F0F0Fu) |
+                                spread4_to_bit4(__builtin_amdgcn_ubfe(r.qh, 16 + 4 * w, 4));
+            acc = dot4(lo, x + 4 * w, acc);
+            acc = dot4(hi, x + 16 + 4 * w, acc);
+        }
+        return (acc - 16.f * xs.all) * h2f(r.d);
     }
     static PE_DEV void dequant(const Raw& r, float* w) {
         const float d = h2f(r.d);
@@ -180,16 +272,15 @@ struct Fmt<PE_TYPE_Q4_K> {
         const uint32_t b = ubyte(word_of(v, (i & 15) >> 2), i & 3);
         return (r.sub & 1) ? (b >> 4) : (b & 0xFu);
     }
-    static PE_DEV float dot(const Raw& r, const float* x) {
+    static PE_DEV float dot(const Raw& r, const float* x, const UnitSums& xs) {
         float a, m;
         scales(r, a, m);
-        float dq = 0.f, sx = 0.f;
+        const int sh = 4 * (r.sub & 1);
+        float dq = 0.f;
 #pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            dq += (float)nib(r, i) * x[i];
-            sx += x[i];
-        }
-        return a * dq - m * sx;
+        for (int w = 0; w < 8; ++w)
+            dq = dot4((word_of(w < 4 ? r.lo : r.hi, w & 3) >> sh) & 0x0F0F0F0Fu, x + 4 * w, dq);
+        return a * dq - m * xs.all;
     }
     static PE_DEV void dequant(const Raw& r, float* w) {
         float a, m;
@@ -235,14 +326,20 @@ struct Fmt<PE_TYPE_Q6_K> {
         const uint32_t low4 = r.q >= 2 ? (lb >> 4) : (lb & 0xFu);
         return (int)(low4 | (((hb >> (2 * r.q)) & 3u) << 4)) - 32;
     }
-    static PE_DEV float dot(const Raw& r, const float* x) {
+    // unsigned 6-bit codes of 4 elements at once; the -32 offset folds into the half sums
+    static PE_DEV float dot(const Raw& r, const float* x, const UnitSums& xs) {
+        const int lsh = r.q >= 2 ? 4 : 0, hsh = 2 * r.q;
         float p0 = 0.f, p1 = 0.f;
 #pragma unroll
-        for (int l = 0; l < 16; ++l) {
-            p0 += (float)code(r, l) * x[l];
-            p1 += (float)code(r, 16 + l) * x[16 + l];
+        for (int w = 0; w < 8; ++w) {
+            const uint32_t L = word_of(w < 4 ? r.l0 : r.l1, w & 3);
+            const uint32_t H = word_of(w < 4 ? r.h0 : r.h1, w & 3);
+            const uint32_t c = ((L >> lsh) & 0x0F0F0F0Fu) | (((H >> hsh) & 0x03030303u) << 4);
+            if (w < 4) p0 = dot4(c, x + 4 * w, p0);
+            else p1 = dot4(c, x + 4 * w, p1);
         }
-        return h2f(r.d) * ((float)sext8(r.sc, 0) * p0 + (float)sext8(r.sc, 1) * p1);
+        return h2f(r.d) * ((float)sext8(r.sc, 0) * (p0 - 32.f * xs.lo) +
+                           (float)sext8(r.sc, 1) * (p1 - 32.f * (xs.all - xs.lo)));
     }
     static PE_DEV void dequant(const Raw& r, float* w) {
         const float d = h2f(r.d);
@@ -255,6 +352,26 @@ struct Fmt<PE_TYPE_Q6_K> {
         }
     }
 };
+
+// Unit-transposed ("ut") vector layout used between the decode kernels: element k of a vector
+// of U = K/32 units lives at ((k%32)/4 * U + k/32) * 4 + k%4, i.e. 8 planes of U float4s.
+// Lane u reading its unit's 8 float4s then touches consecutive 16-byte slots across lanes
+// (fully coalesced), instead of 128 contiguous bytes per lane.
+PE_DEV int64_t ut_index(int64_t k, int64_t U) {
+    return (((k & 31) >> 2) * U + (k >> 5)) * 4 + (k & 3);
+}
+
+PE_DEV void load_x_unit_ut(const float* __restrict__ x, int u, int U, float* xr) {
+    const float4* p = reinterpret_cast<const float4*>(x) + u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 v = p[(int64_t)i * U];
+        xr[4 * i + 0] = v.x;
+        xr[4 * i + 1] = v.y;
+        xr[4 * i + 2] = v.z;
+        xr[4 * i + 3] = v.w;
+    }
+}
 
 // Load the 32 x values of unit u (x[32u .. 32u+31], the same for every format) with
 // 16-byte loads; x must be 16-byte aligned.

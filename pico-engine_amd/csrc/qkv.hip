@@ -15,108 +15,125 @@ struct QkvParams {
     int64_t k;  // hidden
 };
 
-template <int T, int UPL, int GS>
-PE_DEV void pair_dot(const Tiled& t, int64_t r1, int64_t r2, int glane, int units,
-                     const float (&xr)[UPL][32], float& y1, float& y2) {
-    typename Fmt<T>::Raw p[UPL], q[UPL];
-#pragma unroll
-    for (int i = 0; i < UPL; ++i) {
-        const int u = glane + GS * i;
-        if (u < units) {
-            Fmt<T>::load(t, r1, u, p[i]);
-            Fmt<T>::load(t, r2, u, q[i]);
-        }
-    }
-    y1 = 0.f;
-    y2 = 0.f;
-#pragma unroll
-    for (int i = 0; i < UPL; ++i) {
-        if (glane + GS * i < units) {
-            y1 += Fmt<T>::dot(p[i], xr[i]);
-            y2 += Fmt<T>::dot(q[i], xr[i]);
-        }
-    }
-}
-
-template <int GS, int UPL>
-__global__ __launch_bounds__(256) void k_qkv(QkvParams P) {
-    constexpr int GPB = 256 / GS;
-    __shared__ float lds4[4];
+// One task of one segment: the pair of rows (i, i + hd/2) of head `head`. Weight, bias,
+// position and cos/sin loads are issued before the activation prologue.
+template <int T, int GS, int UPL>
+PE_DEV void qkv_task(const QkvParams& P, int seg, int64_t task, int glane, float* lds4,
+                     float* stage) {
     const pe_qkv_args& a = P.a;
-    const int glane = threadIdx.x % GS;
-    const int gid = threadIdx.x / GS;
     const int units = (int)(P.k >> 5);
     const int hd = a.head_dim, half = hd / 2;
+    const bool valid = task >= 0;
+    const int64_t head = valid ? task / half : 0;
+    const int i = valid ? (int)(task % half) : 0;
+    const int64_t r1 = head * hd + i, r2 = r1 + half;
+    const void* w = seg == 0 ? a.w_q : seg == 1 ? a.w_k : a.w_v;
+    const float* b = seg == 0 ? a.b_q : seg == 1 ? a.b_k : a.b_v;
+    const int64_t seg_rows = (seg == 0 ? a.n_head : a.n_kv) * (int64_t)hd;
+    const Tiled t{(const uint8_t*)w, seg_rows, P.k / (int64_t)Fmt<T>::QK};
+
+    typename Fmt<T>::Raw p[UPL], q[UPL];
+    float b1 = 0.f, b2 = 0.f, c = 1.f, sn = 0.f;
+    const int64_t pos = *a.pos;
+    const bool pos_ok = pos >= 0 && pos < a.capacity && pos < a.rope_rows;
+    if (valid) {
+#pragma unroll
+        for (int j = 0; j < UPL; ++j) {
+            const int u = glane + GS * j;
+            if (u < units) {
+                Fmt<T>::load(t, r1, u, p[j]);
+                Fmt<T>::load(t, r2, u, q[j]);
+            }
+        }
+        if (glane == 0) {
+            if (b) {
+                b1 = b[r1];
+                b2 = b[r2];
+            }
+            if (seg < 2 && pos_ok) {
+                c = a.cos_tab[pos * half + i];
+                sn = a.sin_tab[pos * half + i];
+            }
+        }
+    }
 
     float xr[UPL][32];
+    UnitSums xs[UPL];
     GemvArgs ga{};
     ga.k = P.k;
     ga.x = a.x;
     ga.norm_w = a.norm_w;
     ga.eps = a.eps;
+    ga.layout = a.layout & PE_LAYOUT_X_UT;
     if (a.norm_w)
-        load_activation<GS, UPL, true>(ga, glane, units, xr, lds4);
+        load_activation<GS, UPL, true>(ga, glane, units, xr, xs, lds4, stage);
     else
-        load_activation<GS, UPL, false>(ga, glane, units, xr, lds4);
+        load_activation<GS, UPL, false>(ga, glane, units, xr, xs, lds4, stage);
 
-    const int64_t pos = *a.pos;
-    const bool pos_ok = pos >= 0 && pos < a.capacity && pos < a.rope_rows;
-    const int64_t tq = (int64_t)a.n_head * half, tk = (int64_t)a.n_kv * half;
-    const int64_t n_tasks = tq + 2 * tk;
-    const int64_t stride = (int64_t)gridDim.x * GPB;
-
-    for (int64_t task = (int64_t)blockIdx.x * GPB + gid; task < n_tasks; task += stride) {
-        int seg;
-        int64_t local;
-        if (task < tq) { seg = 0; local = task; }
-        else if (task < tq + tk) { seg = 1; local = task - tq; }
-        else { seg = 2; local = task - tq - tk; }
-        const int64_t head = local / half;
-        const int i = (int)(local % half);
-        const int64_t r1 = head * hd + i, r2 = r1 + half;
-        const int type = seg == 0 ? a.type_q : seg == 1 ? a.type_k : a.type_v;
-        const void* w = seg == 0 ? a.w_q : seg == 1 ? a.w_k : a.w_v;
-        const float* b = seg == 0 ? a.b_q : seg == 1 ? a.b_k : a.b_v;
-        const int64_t seg_rows = (seg == 0 ? a.n_head : a.n_kv) * (int64_t)hd;
-        const int64_t nb = P.k / (int64_t)block_elems(type);
-        const Tiled t{(const uint8_t*)w, seg_rows, nb};
-        float y1 = 0.f, y2 = 0.f;
-        switch (type) {
-            case PE_TYPE_Q8_0: pair_dot<PE_TYPE_Q8_0, UPL, GS>(t, r1, r2, glane, units, xr, y1, y2); break;
-            case PE_TYPE_Q5_0: pair_dot<PE_TYPE_Q5_0, UPL, GS>(t, r1, r2, glane, units, xr, y1, y2); break;
-            case PE_TYPE_Q4_K: pair_dot<PE_TYPE_Q4_K, UPL, GS>(t, r1, r2, glane, units, xr, y1, y2); break;
-            case PE_TYPE_Q6_K: pair_dot<PE_TYPE_Q6_K, UPL, GS>(t, r1, r2, glane, units, xr, y1, y2); break;
-            default: break;
-        }
-        y1 = gsum<GS>(y1, lds4);
-        y2 = gsum<GS>(y2, lds4);
-        if (glane != 0) continue;
-        if (b) {
-            y1 += b[r1];
-            y2 += b[r2];
-        }
-        if (seg == 2) {
-            if (pos_ok) {
-                float* dst = a.v_cache + (head * a.capacity + pos) * hd;
-                dst[i] = y1;
-                dst[i + half] = y2;
+    float y1 = 0.f, y2 = 0.f;
+    if (valid) {
+#pragma unroll
+        for (int j = 0; j < UPL; ++j) {
+            if (glane + GS * j < units) {
+                y1 += Fmt<T>::dot(p[j], xr[j], xs[j]);
+                y2 += Fmt<T>::dot(q[j], xr[j], xs[j]);
             }
-            continue;
         }
-        float o1 = __uint_as_float(0x7FC00000u), o2 = o1;
+    }
+    y1 = gsum<GS>(y1, lds4);
+    y2 = gsum<GS>(y2, lds4);
+    if (!valid || glane != 0) return;
+    y1 += b1;
+    y2 += b2;
+    if (seg == 2) {
         if (pos_ok) {
-            const float c = a.cos_tab[pos * half + i], sn = a.sin_tab[pos * half + i];
-            o1 = y1 * c - y2 * sn;
-            o2 = y1 * sn + y2 * c;
+            float* dst = a.v_cache + (head * a.capacity + pos) * hd;
+            dst[i] = y1;
+            dst[i + half] = y2;
         }
-        if (seg == 0) {
-            a.q_out[r1] = o1;
-            a.q_out[r2] = o2;
-        } else if (pos_ok) {
-            float* dst = a.k_cache + (head * a.capacity + pos) * hd;
-            dst[i] = o1;
-            dst[i + half] = o2;
-        }
+        return;
+    }
+    float o1 = __uint_as_float(0x7FC00000u), o2 = o1;
+    if (pos_ok) {
+        o1 = y1 * c - y2 * sn;
+        o2 = y1 * sn + y2 * c;
+    }
+    if (seg == 0) {
+        a.q_out[r1] = o1;
+        a.q_out[r2] = o2;
+    } else if (pos_ok) {
+        float* dst = a.k_cache + (head * a.capacity + pos) * hd;
+        dst[i] = o1;
+        dst[i + half] = o2;
+    }
+}
+
+// Blocks [0, bq) serve q, [bq, bq + bk) k, the rest v: one segment (one format) per block.
+template <int GS, int UPL>
+__global__ __launch_bounds__(block_threads<GS>()) void k_qkv(QkvParams P) {
+    constexpr int GPB = block_threads<GS>() / GS;
+    __shared__ float lds4[4];
+    extern __shared__ float stage[];
+    const pe_qkv_args& a = P.a;
+    const int half = a.head_dim / 2;
+    const int64_t tq = (int64_t)a.n_head * half, tk = (int64_t)a.n_kv * half;
+    const int64_t bq = (tq + GPB - 1) / GPB, bk = (tk + GPB - 1) / GPB;
+    int64_t blk = blockIdx.x;
+    int seg;
+    int64_t ntask;
+    if (blk < bq) { seg = 0; ntask = tq; }
+    else if (blk < bq + bk) { seg = 1; blk -= bq; ntask = tk; }
+    else { seg = 2; blk -= bq + bk; ntask = tk; }
+    const int64_t task0 = blk * GPB + threadIdx.x / GS;
+    const int64_t task = task0 < ntask ? task0 : -1;
+    const int glane = threadIdx.x % GS;
+    const int type = seg == 0 ? a.type_q : seg == 1 ? a.type_k : a.type_v;
+    switch (type) {
+        case PE_TYPE_Q8_0: qkv_task<PE_TYPE_Q8_0, GS, UPL>(P, seg, task, glane, lds4, stage); break;
+        case PE_TYPE_Q5_0: qkv_task<PE_TYPE_Q5_0, GS, UPL>(P, seg, task, glane, lds4, stage); break;
+        case PE_TYPE_Q4_K: qkv_task<PE_TYPE_Q4_K, GS, UPL>(P, seg, task, glane, lds4, stage); break;
+        case PE_TYPE_Q6_K: qkv_task<PE_TYPE_Q6_K, GS, UPL>(P, seg, task, glane, lds4, stage); break;
+        default: break;
     }
 }
 
@@ -147,20 +164,23 @@ extern "C" int pe_qkv_rmsnorm_rope(const pe_qkv_args* args, pe_stream_t stream) 
         !aligned(a.b_k, 4) || !aligned(a.b_v, 4))
         return PE_ERR_ALIGN;
     QkvParams P{a, a.hidden};
-    const int64_t tasks = (int64_t)(a.n_head + 2 * a.n_kv) * (a.head_dim / 2);
-    const int gpb = 256 / sh.gs;
-    int64_t blocks = (tasks + gpb - 1) / gpb;
-    if (blocks > kMaxGemvBlocks) blocks = kMaxGemvBlocks;
+    const int bs = sh.gs <= 64 ? 64 : 256;
+    const int gpb = bs / sh.gs;
+    const int64_t tq = (int64_t)a.n_head * (a.head_dim / 2), tk = (int64_t)a.n_kv * (a.head_dim / 2);
+    const int64_t blocks = (tq + gpb - 1) / gpb + 2 * ((tk + gpb - 1) / gpb);
+    if (blocks > 65535) return PE_ERR_SHAPE;
     hipStream_t s = (hipStream_t)stream;
-    dim3 g((unsigned)blocks), b(256);
+    dim3 g((unsigned)blocks), b((unsigned)bs);
+    if (a.layout & ~PE_LAYOUT_X_UT) return PE_ERR_TYPE;
+    const size_t lds = (a.layout & PE_LAYOUT_X_UT) ? 0 : stage_lds_bytes(a.hidden, a.norm_w != nullptr);
     switch (sh.gs * 16 + sh.upl) {
-        case 32 * 16 + 1: hipLaunchKernelGGL((k_qkv<32, 1>), g, b, 0, s, P); break;
-        case 64 * 16 + 1: hipLaunchKernelGGL((k_qkv<64, 1>), g, b, 0, s, P); break;
-        case 64 * 16 + 2: hipLaunchKernelGGL((k_qkv<64, 2>), g, b, 0, s, P); break;
-        case 64 * 16 + 3: hipLaunchKernelGGL((k_qkv<64, 3>), g, b, 0, s, P); break;
-        case 64 * 16 + 4: hipLaunchKernelGGL((k_qkv<64, 4>), g, b, 0, s, P); break;
-        case 256 * 16 + 3: hipLaunchKernelGGL((k_qkv<256, 3>), g, b, 0, s, P); break;
-        case 256 * 16 + 4: hipLaunchKernelGGL((k_qkv<256, 4>), g, b, 0, s, P); break;
+        case 32 * 16 + 1: hipLaunchKernelGGL((k_qkv<32, 1>), g, b, lds, s, P); break;
+        case 64 * 16 + 1: hipLaunchKernelGGL((k_qkv<64, 1>), g, b, lds, s, P); break;
+        case 64 * 16 + 2: hipLaunchKernelGGL((k_qkv<64, 2>), g, b, lds, s, P); break;
+        case 64 * 16 + 3: hipLaunchKernelGGL((k_qkv<64, 3>), g, b, lds, s, P); break;
+        case 64 * 16 + 4: hipLaunchKernelGGL((k_qkv<64, 4>), g, b, lds, s, P); break;
+        case 256 * 16 + 3: hipLaunchKernelGGL((k_qkv<256, 3>), g, b, lds, s, P); break;
+        case 256 * 16 + 4: hipLaunchKernelGGL((k_qkv<256, 4>), g, b, lds, s, P); break;
         default: return PE_ERR_SHAPE;
     }
     return launch_status();

@@ -14,7 +14,10 @@ import os
 import torch  # noqa: F401  (must precede the CDLL load, see above)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpico_hip.so")
-ABI_VERSION = 1
+
+# layout bits (include/pico_hip.h)
+LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT = 0, 1, 2
+ABI_VERSION = 2
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -42,6 +45,7 @@ class QkvArgs(ctypes.Structure):
         ("pos", _P), ("q_out", _P), ("k_cache", _P), ("v_cache", _P),
         ("capacity", _L), ("hidden", _L),
         ("n_head", _I), ("n_kv", _I), ("head_dim", _I),
+        ("layout", _I),
     ]
 
 
@@ -52,13 +56,13 @@ _SIGNATURES = {
     "pe_dequant": (_I, [_I, _P, _P, _L, _P]),
     "pe_repack": (_I, [_I, _P, _P, _L, _L, _P]),
     "pe_dequant_tiled": (_I, [_I, _P, _P, _L, _L, _P]),
-    "pe_embed_gather": (_I, [_I, _P, _L, _L, _P, _L, _P, _P]),
-    "pe_qgemv": (_I, [_I, _P, _L, _L, _P, _P, _P, _P, _P]),
-    "pe_qgemv_rmsnorm": (_I, [_I, _P, _L, _L, _P, _P, _F, _P, _P]),
-    "pe_qgemv_rmsnorm_silu": (_I, [_I, _P, _L, _L, _P, _P, _F, _P, _P]),
+    "pe_embed_gather": (_I, [_I, _P, _L, _L, _P, _L, _P, _I, _P]),
+    "pe_qgemv": (_I, [_I, _P, _L, _L, _P, _P, _P, _P, _I, _P]),
+    "pe_qgemv_rmsnorm": (_I, [_I, _P, _L, _L, _P, _P, _F, _P, _I, _P]),
+    "pe_qgemv_rmsnorm_silu": (_I, [_I, _P, _L, _L, _P, _P, _F, _P, _I, _P]),
     "pe_qkv_rmsnorm_rope": (_I, [ctypes.POINTER(QkvArgs), _P]),
     "pe_decode_attn_workspace_bytes": (_L, [_I, _I, _I, _L]),
-    "pe_decode_attn": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _P, _P, _L, _P]),
+    "pe_decode_attn": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _P, _P, _L, _I, _P]),
     "pe_rmsnorm": (_I, [_P, _L, _P, _P, _L, _L, _L, _F, _P]),
     "pe_rope": (_I, [_P, _L, _P, _P, _P, _L, _L, _I, _I, _P]),
     "pe_silu_mul": (_I, [_P, _L, _P, _L, _L, _L, _P]),

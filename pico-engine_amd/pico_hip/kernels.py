@@ -21,7 +21,7 @@ from dataclasses import dataclass
 
 import torch
 
-from ._lib import QkvArgs, check, lib
+from ._lib import LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT, QkvArgs, check, lib
 from .dequant import (BLOCK_SIZE, GGML_Q4_K, GGML_Q5_0, GGML_Q6_K, GGML_Q8_0, QUANT_TYPES,
                       TYPE_NAMES, nbytes_for)
 
@@ -53,6 +53,19 @@ def _f32c(t: torch.Tensor) -> torch.Tensor:
     if t.data_ptr() % 16:
         t = t.clone()
     return t
+
+
+def to_ut(v: torch.Tensor) -> torch.Tensor:
+    """Natural -> unit-transposed layout of a 1-D vector (len % 32 == 0): element k moves to
+    ((k % 32) // 4 * U + k // 32) * 4 + k % 4, U = len / 32 (see include/pico_hip.h)."""
+    n = v.numel()
+    return v.reshape(n // 32, 8, 4).transpose(0, 1).contiguous().reshape(n)
+
+
+def from_ut(v: torch.Tensor) -> torch.Tensor:
+    """Unit-transposed -> natural layout of a 1-D vector."""
+    n = v.numel()
+    return v.reshape(8, n // 32, 4).transpose(0, 1).contiguous().reshape(n)
 
 
 @dataclass
@@ -118,15 +131,17 @@ def dequantize_weight(w: QWeight) -> torch.Tensor:
     return out
 
 
-def embed_gather(table: RawTensor, ids: torch.Tensor, out: torch.Tensor | None = None):
-    """Rows ``ids`` of a raw GGUF (vocab, hidden) table, dequantized (model.py:152)."""
+def embed_gather(table: RawTensor, ids: torch.Tensor, out: torch.Tensor | None = None,
+                 layout: int = LAYOUT_NATURAL):
+    """Rows ``ids`` of a raw GGUF (vocab, hidden) table, dequantized (model.py:152);
+    ``layout=LAYOUT_Y_UT`` writes each row unit-transposed."""
     dev = _on_gpu(table.data, ids)
     ids = ids.to(torch.int64).contiguous()
     vocab, hidden = table.shape
     if out is None:
         out = torch.empty(ids.numel(), hidden, device=dev, dtype=torch.float32)
     check(lib.pe_embed_gather(table.ggml_type, _ptr(table.data), vocab, hidden, _ptr(ids),
-                              ids.numel(), _ptr(out), _stream(dev)), "pe_embed_gather")
+                              ids.numel(), _ptr(out), layout, _stream(dev)), "pe_embed_gather")
     return out
 
 
@@ -184,7 +199,8 @@ def decode_attn_workspace(n_head: int, n_kv: int, hd: int, capacity: int, device
 def decode_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                 S: torch.Tensor | int | None = None, stride: int | None = None,
                 scale: float | None = None, *, S_offset: int = 0, round_fp16: bool = True,
-                workspace: torch.Tensor | None = None, out: torch.Tensor | None = None):
+                workspace: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                layout: int = LAYOUT_NATURAL):
     """Single-query GQA attention over the cache (kernels.py:129).
 
     q (n_head, hd); k/v (n_kv, capacity, hd); valid length S (+ ``S_offset``) read on the
@@ -219,13 +235,15 @@ def decode_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         out = torch.empty(n_head, hd, device=dev, dtype=torch.float32)
     check(lib.pe_decode_attn(_ptr(q), _ptr(k), _ptr(v), n_head, n_kv, hd, capacity, _ptr(len_dev),
                              dtype_code, add, float(scale), int(round_fp16), _ptr(out),
-                             _ptr(workspace), workspace.numel(), _stream(dev)), "pe_decode_attn")
+                             _ptr(workspace), workspace.numel(), layout, _stream(dev)), "pe_decode_attn")
     return out
 
 
 def qgemv(x: torch.Tensor, w: QWeight, residual: torch.Tensor | None = None,
-          bias: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
-    """y = W x (+ bias) (+ residual) for a tiled quantized W (M = 1)."""
+          bias: torch.Tensor | None = None, out: torch.Tensor | None = None,
+          layout: int = LAYOUT_NATURAL) -> torch.Tensor:
+    """y = W x (+ bias) (+ residual) for a tiled quantized W (M = 1); ``layout`` bits say
+    which of x / (y, residual) are unit-transposed."""
     dev = _on_gpu(x, w.data, residual, bias)
     x = _f32c(x.reshape(-1))
     if x.numel() != w.k:
@@ -235,7 +253,7 @@ def qgemv(x: torch.Tensor, w: QWeight, residual: torch.Tensor | None = None,
     if out is None:
         out = torch.empty(w.n, device=dev, dtype=torch.float32)
     check(lib.pe_qgemv(w.ggml_type, _ptr(w.data), w.n, w.k, _ptr(x), _ptr(res), _ptr(b), _ptr(out),
-                       _stream(dev)), "pe_qgemv")
+                       layout, _stream(dev)), "pe_qgemv")
     return out
 
 
@@ -266,7 +284,7 @@ def q4_k_gemv(x: torch.Tensor, w: QWeight, residual: torch.Tensor | None = None)
 
 
 def qgemv_norm(x: torch.Tensor, weight: torch.Tensor, w: QWeight, eps: float,
-               out: torch.Tensor | None = None) -> torch.Tensor:
+               out: torch.Tensor | None = None, layout: int = LAYOUT_NATURAL) -> torch.Tensor:
     """W (rmsnorm(x) * weight) in one launch, any quantized format."""
     dev = _on_gpu(x, weight, w.data)
     x = _f32c(x.reshape(-1))
@@ -274,7 +292,7 @@ def qgemv_norm(x: torch.Tensor, weight: torch.Tensor, w: QWeight, eps: float,
     if out is None:
         out = torch.empty(w.n, device=dev, dtype=torch.float32)
     check(lib.pe_qgemv_rmsnorm(w.ggml_type, _ptr(w.data), w.n, w.k, _ptr(x), _ptr(nw), float(eps),
-                               _ptr(out), _stream(dev)), "pe_qgemv_rmsnorm")
+                               _ptr(out), layout, _stream(dev)), "pe_qgemv_rmsnorm")
     return out
 
 
@@ -284,7 +302,7 @@ def q5_0_gemv_norm(x: torch.Tensor, weight: torch.Tensor, w: QWeight, eps: float
 
 
 def qgemv_norm_silu(x: torch.Tensor, weight: torch.Tensor | None, w: QWeight, eps: float,
-                    out: torch.Tensor | None = None) -> torch.Tensor:
+                    out: torch.Tensor | None = None, layout: int = LAYOUT_NATURAL) -> torch.Tensor:
     """silu(g) * u with [g; u] = W (rmsnorm(x) * weight), W = [gate; up] (2*ffn rows)."""
     dev = _on_gpu(x, weight, w.data)
     if w.n % 2:
@@ -295,7 +313,7 @@ def qgemv_norm_silu(x: torch.Tensor, weight: torch.Tensor | None, w: QWeight, ep
     if out is None:
         out = torch.empty(ffn, device=dev, dtype=torch.float32)
     check(lib.pe_qgemv_rmsnorm_silu(w.ggml_type, _ptr(w.data), ffn, w.k, _ptr(x), _ptr(nw),
-                                    float(eps), _ptr(out), _stream(dev)), "pe_qgemv_rmsnorm_silu")
+                                    float(eps), _ptr(out), layout, _stream(dev)), "pe_qgemv_rmsnorm_silu")
     return out
 
 
@@ -304,7 +322,7 @@ def qkv_rmsnorm_rope(x: torch.Tensor, norm_w: torch.Tensor | None, eps: float,
                      bq: torch.Tensor | None, bk: torch.Tensor | None, bv: torch.Tensor | None,
                      cos_tab: torch.Tensor, sin_tab: torch.Tensor, pos: torch.Tensor,
                      k_cache: torch.Tensor, v_cache: torch.Tensor, n_head: int,
-                     out: torch.Tensor | None = None) -> torch.Tensor:
+                     out: torch.Tensor | None = None, layout: int = LAYOUT_NATURAL) -> torch.Tensor:
     """One decode token: q = RoPE(Wq h + bq) returned; RoPE(Wk h + bk), Wv h + bv written to
     the caches at position ``pos`` (device int64 scalar); h = rmsnorm(x) * norm_w."""
     dev = _on_gpu(x, norm_w, wq.data, wk.data, wv.data, pos, k_cache, v_cache)
@@ -323,7 +341,7 @@ def qkv_rmsnorm_rope(x: torch.Tensor, norm_w: torch.Tensor | None, eps: float,
                 x.data_ptr(), None if norm_w is None else norm_w.data_ptr(), float(eps),
                 cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
                 pos.data_ptr(), out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-                capacity, wq.k, n_head, n_kv, hd)
+                capacity, wq.k, n_head, n_kv, hd, layout)
     check(lib.pe_qkv_rmsnorm_rope(ctypes.byref(a), _stream(dev)), "pe_qkv_rmsnorm_rope")
     return out
 
@@ -382,7 +400,7 @@ def prefill_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     return out
 
 
-__all__ = ["QWeight", "RawTensor", "dequantize", "pack_weight", "dequantize_weight", "embed_gather",
+__all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "QWeight", "RawTensor", "dequantize", "pack_weight", "dequantize_weight", "embed_gather",
            "rmsnorm", "rope", "silu_mul", "decode_attn", "decode_attn_workspace", "qgemv",
            "q8_0_gemv", "q5_0_gemv", "q5_0_gemv_norm", "q6_k_gemv", "q4_k_gemv", "qgemv_norm",
            "qgemv_norm_silu", "qkv_rmsnorm_rope", "qgemm", "kv_write", "prefill_attn",

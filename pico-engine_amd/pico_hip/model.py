@@ -46,6 +46,8 @@ class ModelConfig:
 @dataclass
 class Layer:
     attn_norm: torch.Tensor
+    attn_norm_ut: torch.Tensor   # unit-transposed copies for the decode kernels
+    ffn_norm_ut: torch.Tensor
     wq: QWeight
     wk: QWeight
     wv: QWeight
@@ -79,12 +81,15 @@ class Transformer:
         self.cos = angles.cos().contiguous()
         self.sin = angles.sin().contiguous()
         self.layers = [self._layer_weights(i) for i in range(cfg.n_layers)]
+        self.output_norm_ut = K.to_ut(self.w["output_norm.weight"])
         self._ws: dict[int, torch.Tensor] = {}
 
     def _layer_weights(self, i: int) -> Layer:
         p, q, w = f"blk.{i}.", self.quant, self.w
         return Layer(
             attn_norm=w[p + "attn_norm.weight"],
+            attn_norm_ut=K.to_ut(w[p + "attn_norm.weight"]),
+            ffn_norm_ut=K.to_ut(w[p + "ffn_norm.weight"]),
             wq=q[p + "attn_q.weight"], wk=q[p + "attn_k.weight"], wv=q[p + "attn_v.weight"],
             bq=w.get(p + "attn_q.bias"), bk=w.get(p + "attn_k.bias"), bv=w.get(p + "attn_v.bias"),
             wo=q[p + "attn_output.weight"],
@@ -127,27 +132,31 @@ class Transformer:
 
     # ---- decode ---------------------------------------------------------------------------
     def _decode(self, token_ids, positions, cache):
+        """One token. The hidden and FFN vectors stay in the unit-transposed layout between
+        kernels (each producer writes it, each GEMV reads it with coalesced loads)."""
         cfg = self.cfg
+        XU, YU = K.LAYOUT_X_UT, K.LAYOUT_Y_UT
         pos = positions.reshape(-1)[:1]
         if pos.dtype != torch.int64:
             pos = pos.to(torch.int64)
         capacity = cache[0][0].shape[1]
         ws = self.attn_workspace(capacity)
-        x = K.embed_gather(self.embed, token_ids).reshape(-1)
+        x = K.embed_gather(self.embed, token_ids, layout=YU).reshape(-1)
         for i, L in enumerate(self.layers):
             k_buf, v_buf = cache[i]
-            q = K.qkv_rmsnorm_rope(x, L.attn_norm, cfg.eps, L.wq, L.wk, L.wv, L.bq, L.bk, L.bv,
-                                   self.cos, self.sin, pos, k_buf, v_buf, cfg.n_head)
-            attn = K.decode_attn(q, k_buf, v_buf, S=pos, S_offset=1, workspace=ws)
-            x = K.qgemv(attn.reshape(-1), L.wo, residual=x)
+            q = K.qkv_rmsnorm_rope(x, L.attn_norm_ut, cfg.eps, L.wq, L.wk, L.wv, L.bq, L.bk, L.bv,
+                                   self.cos, self.sin, pos, k_buf, v_buf, cfg.n_head, layout=XU)
+            attn = K.decode_attn(q, k_buf, v_buf, S=pos, S_offset=1, workspace=ws, layout=YU)
+            x = K.qgemv(attn.reshape(-1), L.wo, residual=x, layout=XU | YU)
             if L.w_gate_up is not None:
-                act = K.qgemv_norm_silu(x, L.ffn_norm, L.w_gate_up, cfg.eps)
+                act = K.qgemv_norm_silu(x, L.ffn_norm_ut, L.w_gate_up, cfg.eps, layout=XU | YU)
+                x = K.qgemv(act, L.w_down, residual=x, layout=XU | YU)
             else:
-                g = K.qgemv_norm(x, L.ffn_norm, L.w_gate, cfg.eps)
-                u = K.qgemv_norm(x, L.ffn_norm, L.w_up, cfg.eps)
+                g = K.qgemv_norm(x, L.ffn_norm_ut, L.w_gate, cfg.eps, layout=XU)
+                u = K.qgemv_norm(x, L.ffn_norm_ut, L.w_up, cfg.eps, layout=XU)
                 act = K.silu_mul(torch.cat([g, u]).unsqueeze(0), cfg.ffn_dim).reshape(-1)
-            x = K.qgemv(act, L.w_down, residual=x)
-        return K.qgemv_norm(x, self.w["output_norm.weight"], self.output, cfg.eps)
+                x = K.qgemv(act, L.w_down, residual=x, layout=YU)
+        return K.qgemv_norm(x, self.output_norm_ut, self.output, cfg.eps, layout=XU)
 
     # ---- prefill --------------------------------------------------------------------------
     def _prefill(self, token_ids, positions, cache):

@@ -57,28 +57,32 @@ def test_argument_errors_before_launch(lib):
     fake = P(0x1000)          # never dereferenced: validation fails first
     odd = P(0x1001)
     # unsupported type / bad shapes / NULL / misalignment
-    assert lib.pe_qgemv(99, fake, 8, 896, fake, None, None, fake, None) == 2
-    assert lib.pe_qgemv(12, fake, 8, 896, fake, None, None, fake, None) == 3   # K % 256
-    assert lib.pe_qgemv(8, None, 8, 896, fake, None, None, fake, None) == 1
-    assert lib.pe_qgemv(8, odd, 8, 896, fake, None, None, fake, None) == 4
-    assert lib.pe_qgemv(8, fake, 8, 896, odd, None, None, fake, None) == 4
-    assert lib.pe_qgemv(8, fake, 0, 896, fake, None, None, fake, None) == 3
-    assert lib.pe_qgemv(8, fake, 8, 64 * 1024, fake, None, None, fake, None) == 3  # K too large
+    assert lib.pe_qgemv(99, fake, 8, 896, fake, None, None, fake, 0, None) == 2
+    assert lib.pe_qgemv(12, fake, 8, 896, fake, None, None, fake, 0, None) == 3   # K % 256
+    assert lib.pe_qgemv(8, None, 8, 896, fake, None, None, fake, 0, None) == 1
+    assert lib.pe_qgemv(8, odd, 8, 896, fake, None, None, fake, 0, None) == 4
+    assert lib.pe_qgemv(8, fake, 8, 896, odd, None, None, fake, 0, None) == 4
+    assert lib.pe_qgemv(8, fake, 0, 896, fake, None, None, fake, 0, None) == 3
+    assert lib.pe_qgemv(8, fake, 8, 64 * 1024, fake, None, None, fake, 0, None) == 3  # K too large
+    assert lib.pe_qgemv(8, fake, 40, 896, fake, None, None, fake, 2, None) == 3  # ut output needs N % 32
+    assert lib.pe_qgemv(8, fake, 64, 896, fake, None, None, fake, 4, None) == 2  # unknown layout bit
     assert lib.pe_repack(15, fake, fake, 8, 256, None) == 2                    # Q8_K has no tiled form
     assert lib.pe_dequant(8, fake, fake, 33, None) == 3
     assert lib.pe_dequant(8, fake, fake, 0, None) == 0                         # empty is a no-op
-    assert lib.pe_qgemv_rmsnorm(8, fake, 8, 896, fake, None, 1e-6, fake, None) == 1
+    assert lib.pe_qgemv_rmsnorm(8, fake, 8, 896, fake, None, 1e-6, fake, 0, None) == 1
     assert lib.pe_qgemm(8, fake, 8, 896, fake, 895, 2, None, None, 0, fake, 8, None) == 3  # x_stride < k
-    assert lib.pe_embed_gather(8, fake, 10, 896, fake, 0, fake, None) == 0
+    assert lib.pe_embed_gather(8, fake, 10, 896, fake, 0, fake, 0, None) == 0
     assert lib.pe_kv_write(fake, fake, 128, 2, 64, 5, 8, fake, fake, 10, None) == 3  # pos0+L > cap
     assert lib.pe_prefill_attn(fake, 896, fake, fake, 14, 2, 64, 77, 13, 70, 0.125, fake, 896, None) == 3
     ws = lib.pe_decode_attn_workspace_bytes(14, 2, 64, 77)
     assert lib.pe_decode_attn(fake, fake, fake, 14, 2, 64, 77, None, 0, 5, 0.125, 1, fake, fake,
-                              ws - 1, None) == 6
+                              ws - 1, 0, None) == 6
     assert lib.pe_decode_attn(fake, fake, fake, 14, 2, 64, 77, None, 3, 5, 0.125, 1, fake, fake,
-                              ws, None) == 2
+                              ws, 0, None) == 2
     assert lib.pe_decode_attn(fake, fake, fake, 14, 2, 64, 77, None, 2, 5, 0.125, 1, fake, fake,
-                              ws, None) == 1
+                              ws, 0, None) == 1
+    assert lib.pe_decode_attn(fake, fake, fake, 14, 2, 64, 77, None, 0, 5, 0.125, 1, fake, fake,
+                              ws, 1, None) == 2   # only PE_LAYOUT_Y_UT applies to the output
 
 
 def test_qkv_args_struct_matches_header():
@@ -105,3 +109,15 @@ def test_product_has_no_cpu_fallback():
     with pytest.raises(ValueError, match="GPU"):
         from pico_hip.model import Transformer
         Transformer(None, {}, torch.device("cpu"), {})
+
+
+def test_unit_transposed_layout_is_the_documented_permutation():
+    import torch
+    from pico_hip.kernels import from_ut, to_ut
+    n = 896
+    v = torch.arange(n, dtype=torch.float32)
+    u = to_ut(v)
+    U = n // 32
+    for k in (0, 1, 3, 4, 31, 32, 100, 895):
+        assert u[((k % 32) // 4 * U + k // 32) * 4 + k % 4] == k
+    assert torch.equal(from_ut(u), v)

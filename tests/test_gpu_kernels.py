@@ -246,17 +246,18 @@ def test_decode_attn_unrounded_and_clamp(K):
     assert np.all(np.isnan(empty))
 
 
-def test_decode_attn_workspace_reuse_and_graph(K):
+@pytest.mark.parametrize("cap", [300, 1500])  # single-pass kernel / split kernel with merge
+def test_decode_attn_workspace_reuse_and_graph(K, cap):
     """One workspace across many in-order calls and across graph replays with a device S."""
     rng = np.random.default_rng(9)
-    n_head, n_kv, hd, cap = 14, 2, 64, 300
+    n_head, n_kv, hd = 14, 2, 64
     q = rng.standard_normal((n_head, hd)).astype(np.float32)
     k, v = _kv(rng, n_kv, cap, hd)
     Q, Kc, Vc = (torch.from_numpy(a).to(DEV) for a in (q, k, v))
     ws = K.decode_attn_workspace(n_head, n_kv, hd, cap, DEV)
     pos = torch.zeros(1, dtype=torch.int64, device=DEV)
     out = torch.empty(n_head, hd, device=DEV)
-    for S in (5, 299, 64, 129, 300):
+    for S in (5, cap - 1, 64, 129, cap):
         pos.fill_(S - 1)
         K.decode_attn(Q, Kc, Vc, S=pos, S_offset=1, workspace=ws, out=out)
         assert rel_err(out.cpu().numpy(), closed.attention(q, k, v, S)) < TOL
@@ -268,7 +269,7 @@ def test_decode_attn_workspace_reuse_and_graph(K):
     torch.cuda.current_stream().wait_stream(s)
     with torch.cuda.graph(g):
         K.decode_attn(Q, Kc, Vc, S=pos, S_offset=1, workspace=ws, out=out)
-    for S in (1, 200, 64, 300, 65):
+    for S in (1, 200, 64, cap, 65):
         pos.fill_(S - 1)
         g.replay()
         torch.cuda.synchronize()
@@ -374,3 +375,55 @@ def test_qkv_rmsnorm_rope(K, types, hidden, nh, nkv, hd):
     kc[:, pos] = 0
     vc[:, pos] = 0
     assert not kc.any() and not vc.any()  # nothing else written
+
+
+# ---- unit-transposed activation layout (the decode path's vectors) ------------------------
+
+@pytest.mark.parametrize("t,k,n", [(dq.Q5_0, 896, 896), (dq.Q6_K, 4864, 896), (dq.Q8_0, 896, 1152),
+                                   (dq.Q4_K, 3584, 512)])
+def test_qgemv_ut_layouts_match_natural(K, t, k, n):
+    raw = quantized_normal(t, n, k, seed=k + 3 * n)
+    w = qweight(K, t, raw, n, k)
+    rng = np.random.default_rng(11)
+    x = torch.from_numpy(rng.standard_normal(k).astype(np.float32)).to(DEV)
+    r = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).to(DEV)
+    nat = K.qgemv(x, w, residual=r)
+    ut = K.qgemv(K.to_ut(x), w, residual=K.to_ut(r), layout=K.LAYOUT_X_UT | K.LAYOUT_Y_UT)
+    assert rel_err(K.from_ut(ut).cpu().numpy(), nat.cpu().numpy()) < 1e-6
+    xo = K.qgemv(K.to_ut(x), w, layout=K.LAYOUT_X_UT)          # ut in, natural out
+    assert rel_err(xo.cpu().numpy(), closed.gemv(dequant_rows(t, raw, n, k), x.cpu().numpy())) < TOL
+
+
+def test_norm_silu_and_lm_head_ut(K):
+    rng = np.random.default_rng(12)
+    k, ffn = 896, 4864
+    raw = quantized_normal(dq.Q5_0, 2 * ffn, k, seed=77)
+    w = qweight(K, dq.Q5_0, raw, 2 * ffn, k)
+    x = torch.from_numpy(rng.standard_normal(k).astype(np.float32)).to(DEV)
+    nw = torch.from_numpy(rng.standard_normal(k).astype(np.float32)).to(DEV)
+    nat = K.qgemv_norm_silu(x, nw, w, 1e-6)
+    ut = K.qgemv_norm_silu(K.to_ut(x), K.to_ut(nw), w, 1e-6, layout=K.LAYOUT_X_UT | K.LAYOUT_Y_UT)
+    assert rel_err(K.from_ut(ut).cpu().numpy(), nat.cpu().numpy()) < 1e-5
+    rawo = quantized_normal(dq.Q8_0, 4096, k, seed=78)
+    wo = qweight(K, dq.Q8_0, rawo, 4096, k)
+    a = K.qgemv_norm(x, nw, wo, 1e-6)
+    b = K.qgemv_norm(K.to_ut(x), K.to_ut(nw), wo, 1e-6, layout=K.LAYOUT_X_UT)
+    assert rel_err(b.cpu().numpy(), a.cpu().numpy()) < 1e-5
+
+
+def test_embed_and_attention_ut_outputs(K):
+    raw = random_quant(dq.Q8_0, 20, 896, seed=4)
+    table = K.RawTensor(dev_bytes(raw), dq.Q8_0, (20, 896))
+    ids = torch.tensor([3, 19], device=DEV)
+    nat = K.embed_gather(table, ids)
+    ut = K.embed_gather(table, ids, layout=K.LAYOUT_Y_UT)
+    for r in range(2):
+        assert torch.equal(K.from_ut(ut[r]), nat[r])
+    rng = np.random.default_rng(5)
+    q = torch.from_numpy(rng.standard_normal((14, 64)).astype(np.float32)).to(DEV)
+    kc = torch.from_numpy(rng.standard_normal((2, 2000, 64)).astype(np.float32)).to(DEV)
+    vc = torch.from_numpy(rng.standard_normal((2, 2000, 64)).astype(np.float32)).to(DEV)
+    for cap, S in ((100, 77), (2000, 1500)):   # single-pass and split kernels
+        a = K.decode_attn(q, kc[:, :cap].contiguous(), vc[:, :cap].contiguous(), S=S)
+        b = K.decode_attn(q, kc[:, :cap].contiguous(), vc[:, :cap].contiguous(), S=S, layout=K.LAYOUT_Y_UT)
+        assert torch.equal(K.from_ut(b.reshape(-1)), a.reshape(-1))
