@@ -4,17 +4,19 @@
 Workload: Qwen2.5-0.5B-architecture decoder, random-init N(0,0.02)
 weights quantized into a Q4_K_M-style GGUF (seed 0, pico_hip.synth), a 13-token prompt of
 uniform random ids (numpy default_rng(1234)), fp32 prefill, greedy decode. A "step" is one
-decode token: one replay of the HIP graph holding the whole per-token forward (122 kernels),
-plus the reference loop's argmax read-back and token/position feed (evidence.py:114-124).
+decode token: one replay of the HIP graph holding the whole per-token forward, ending with
+the greedy pick made on the device (the reference loop's argmax, evidence.py:117-123); the
+host reads the picked ids once per chunk of replays.
 W warm-up runs (fresh cache, graph capture, prefill, K decode steps) precede the timed run;
 in the timed run the prefill happens before the bracket, then K decode steps are timed
 between two device synchronizations. value = K / elapsed (tok/s).
 
 Also reported on the same line:
   roofline      the dominant kernel (--kernel) timed alone with HIP events on the stream it
-                launches on, rotating >= 1 GiB of distinct weight copies so the 256 MB
-                Infinity Cache cannot serve repeats; achieved = algorithmic bytes per launch /
-                average launch time, against 8 TB/s. traffic comes from the rocprofv3 --pmc
+                launches on: one HIP graph of back-to-back launches rotating >= 1 GiB of
+                distinct weight copies (so the 256 MB Infinity Cache cannot serve repeats),
+                replayed; achieved = algorithmic bytes per launch / average launch time,
+                against 8 TB/s. traffic comes from the rocprofv3 --pmc
                 summary in profiles/ when present.
   decode_roofline  weight + KV bytes per token over the measured time per token.
   cpu_baseline  the torch-CPU restatement of the reference forward (oracle/ref_cpu.py) on the
@@ -45,26 +47,23 @@ def log(msg: str) -> None:
 
 
 def run_decode(eng, prompt, steps, timed: bool):
-    """One evidence._run_once-style run: fresh cache + graph, prefill, `steps` greedy tokens."""
+    """One evidence._run_once-style run (evidence.py:96-135): fresh cache + graph, prefill
+    (timed on its own), then `steps` greedy tokens (timed), stopping early only at eos. The
+    greedy pick is made on the device at the end of every step, so the replays go back to
+    back; the host reads the picks once per chunk of replays."""
     import torch
     cache = eng._empty_cache(len(prompt) + steps)
     graph = eng._build_decode_graph(cache)
     if graph is None:
         raise RuntimeError("HIP graph capture failed")
-    tokens = torch.tensor(prompt, device=eng.device)
-    positions = torch.arange(len(prompt), device=eng.device)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    logits = eng.model.forward(tokens, positions, cache)
+    eng.prefill_greedy(prompt, cache)
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t0
-    out = []
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(steps):
-        tok = int(logits.argmax())
-        out.append(tok)
-        logits = eng._decode_step(tok, len(prompt) + i, cache, graph)
+    out = eng.decode_greedy(graph, steps, eng.tok.eos_id)
     torch.cuda.synchronize()
     return time.perf_counter() - t0, prefill_s, out
 
@@ -76,22 +75,24 @@ def kernel_launchers(eng, which: str):
     from pico_hip import kernels as K
     m, cfg = eng.model, eng.cfg
     L0 = m.layers[0]
+    XU, YU = K.LAYOUT_X_UT, K.LAYOUT_Y_UT
+    # the decode step's own launch configuration: activations in the unit-transposed layout
     x = torch.randn(cfg.hidden, device=eng.device)
-    nw = m.layers[0].ffn_norm
     if which == "gate_up":
         w, name = L0.w_gate_up, "k_qgemv (Q5_0, rmsnorm+SiLU pair) gate/up 896->2x4864"
-        fn = lambda ww: K.qgemv_norm_silu(x, nw, ww, cfg.eps)
+        fn = lambda ww: K.qgemv_norm_silu(x, L0.ffn_norm_ut, ww, cfg.eps, layout=XU | YU)
         io = 4 * (cfg.hidden * 2 + cfg.ffn_dim)
     elif which == "lm_head":
-        w, name = m.output, "k_qgemv (Q8_0, rmsnorm) LM head 896->151936"
-        fn = lambda ww: K.qgemv_norm(x, m.w["output_norm.weight"], ww, cfg.eps)
+        w, name = m.output, "k_qgemv (Q8_0, rmsnorm, device greedy pick) LM head 896->151936"
+        g = K.GreedyState(m.output.n, 1, eng.device)
+        fn = lambda ww: K.qgemv_norm_argmax(x, m.output_norm_ut, ww, cfg.eps, g, layout=XU)
         io = 4 * (cfg.hidden * 2 + cfg.vocab_size)
     elif which in ("down_q6k", "down_q4k"):
         li = 0 if which == "down_q6k" else 1
         w = m.layers[li].w_down
         name = f"k_qgemv ({'Q6_K' if li == 0 else 'Q4_K'}, +residual) ffn_down 4864->896"
         a = torch.randn(cfg.ffn_dim, device=eng.device)
-        fn = lambda ww: K.qgemv(a, ww, residual=x)
+        fn = lambda ww: K.qgemv(a, ww, residual=x, layout=XU | YU)
         io = 4 * (cfg.ffn_dim + 2 * cfg.hidden)
     else:
         raise SystemExit(f"unknown --kernel {which}")
@@ -100,20 +101,40 @@ def kernel_launchers(eng, which: str):
     return [(lambda ww=ww: fn(ww)) for ww in ws], w.nbytes + io, name
 
 
-def time_kernel(launchers, iters: int) -> float:
-    """Average launch duration in us: HIP events on torch's current stream (the stream the
-    kernels launch on), launches round-robin over the distinct copies."""
+def time_kernel(launchers, iters: int, graph: bool = True) -> float:
+    """Average launch duration in us, from HIP events on torch's current stream (the stream
+    the kernels launch on). With ``graph`` the launches over the distinct copies are captured
+    once into a HIP graph and replayed, so the figure is the kernel's own back-to-back time
+    (as in the decode step's graph) rather than the host's per-launch overhead; without it
+    the launches are made one by one (used for the rocprofv3 counter runs)."""
     import torch
     for f in launchers:
         f()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if not graph:
+        e0.record()
+        for i in range(iters):
+            launchers[i % len(launchers)]()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / iters
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.inference_mode(), torch.cuda.graph(g, stream=s):   # as the engine captures
+        for f in launchers:
+            f()
+    torch.cuda.current_stream().wait_stream(s)
+    g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, -(-iters // len(launchers)))
     e0.record()
-    for i in range(iters):
-        launchers[i % len(launchers)]()
+    for _ in range(reps):
+        g.replay()
     e1.record()
     e1.synchronize()
-    return e0.elapsed_time(e1) * 1000.0 / iters
+    return e0.elapsed_time(e1) * 1000.0 / (reps * len(launchers))
 
 
 def traffic_from_profiles(kernel: str):
@@ -184,7 +205,7 @@ def main() -> None:
 
     if args.kernel_only:
         launchers, alg_bytes, kname = kernel_launchers(eng, args.kernel)
-        avg_us = time_kernel(launchers, args.kernel_iters)
+        avg_us = time_kernel(launchers, args.kernel_iters, graph=False)
         src = torch.ones(1 << 28, device=eng.device)   # 1 GiB: the counter calibration copy
         dst = torch.empty_like(src)
         for _ in range(4):
@@ -197,11 +218,11 @@ def main() -> None:
     for _ in range(args.warmup):
         run_decode(eng, prompt, args.steps, timed=False)
     elapsed, prefill_s, tokens = run_decode(eng, prompt, args.steps, timed=True)
-    value = args.steps / elapsed
+    value = len(tokens) / elapsed
     samples = [value]
     for _ in range(args.reps):
-        e, _, _ = run_decode(eng, prompt, args.steps, timed=True)
-        samples.append(args.steps / e)
+        e, _, t = run_decode(eng, prompt, args.steps, timed=True)
+        samples.append(len(t) / e)
     log(f"decode {value:.1f} tok/s (median of {len(samples)}: {statistics.median(samples):.1f})")
 
     # decode roofline: weight bytes per token + KV bytes (read S positions, write one)
@@ -229,7 +250,7 @@ def main() -> None:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(elapsed / args.steps * 1000, 4),
+        "ms_per_step": round(elapsed / max(len(tokens), 1) * 1000, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

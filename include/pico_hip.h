@@ -130,6 +130,25 @@ int pe_qgemv_rmsnorm_silu(int ggml_type, const void* w_tiled, int64_t ffn, int64
                           const float* x, const float* norm_w, float eps, float* act, int layout,
                           pe_stream_t stream);
 
+/* Greedy LM head: logits = W (rmsnorm(x) * norm_w) as pe_qgemv_rmsnorm (y may be NULL), and
+ * the index of the largest logit with torch.argmax's rule (first index among equal values,
+ * NaN counts as largest), computed on the device. It replaces
+ * rmsnorm + q8_0_gemv (model.py:159-162) followed by int(torch.argmax(logits).item())
+ * (sampler.py:27, evidence.py:118). The pick goes into a device decode state
+ *   state[0] = token (the next step's input id), state[1] += 1 (its position),
+ *   log[state[2]] = token if state[2] < log_cap, state[2] += 1,
+ * so the next graph-replayed step reads its token and position from the device and the
+ * host need not synchronise per token. layout: PE_LAYOUT_X_UT only.
+ * workspace: pe_qgemv_argmax_workspace_bytes(n_rows) bytes, 256-byte aligned, any contents
+ * (per-workgroup partial picks; a second small kernel of the same call reduces them). Calls
+ * sharing one workspace must not run concurrently. The size function returns a negative
+ * pe_status on error. */
+int64_t pe_qgemv_argmax_workspace_bytes(int64_t n_rows);
+int pe_qgemv_rmsnorm_argmax(int ggml_type, const void* w_tiled, int64_t n_rows, int64_t k,
+                            const float* x, const float* norm_w, float eps, float* y,
+                            int64_t* state, int64_t* log, int64_t log_cap, void* workspace,
+                            int64_t workspace_bytes, int layout, pe_stream_t stream);
+
 /* Fused attention prologue of one decode token:
  *   h = rmsnorm(x) * norm_w;  [q; k; v] = [Wq; Wk; Wv] h + [bq; bk; bv]   (mixed formats)
  *   q, k <- rotate-half RoPE with cos/sin row *pos;  q -> q_out;

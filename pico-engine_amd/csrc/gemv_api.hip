@@ -97,3 +97,28 @@ extern "C" int pe_qgemm(int type, const void* w, int64_t n_rows, int64_t k, cons
         default: return PE_ERR_TYPE;
     }
 }
+
+extern "C" int64_t pe_qgemv_argmax_workspace_bytes(int64_t n_rows) {
+    if (n_rows <= 0 || n_rows > 0x7FFFFFFFLL) return -PE_ERR_SHAPE;
+    return argmax_ws_bytes(n_rows);
+}
+
+extern "C" int pe_qgemv_rmsnorm_argmax(int type, const void* w, int64_t n_rows, int64_t k,
+                                       const float* x, const float* norm_w, float eps, float* y,
+                                       int64_t* state, int64_t* log, int64_t log_cap,
+                                       void* workspace, int64_t workspace_bytes, int layout,
+                                       pe_stream_t stream) {
+    int st = check_weight(type, w, n_rows, k);
+    if (st) return st;
+    if (n_rows > 0x7FFFFFFFLL || log_cap < 0) return PE_ERR_SHAPE;
+    if (layout & ~PE_LAYOUT_X_UT) return PE_ERR_TYPE;
+    if (!x || !norm_w || !state || !workspace) return PE_ERR_NULL;
+    if (!aligned(x, 16) || !aligned(norm_w, 16) || !aligned(y, 4) || !aligned(state, 8) ||
+        !aligned(log, 8) || !aligned(workspace, 256))
+        return PE_ERR_ALIGN;
+    if (workspace_bytes < argmax_ws_bytes(n_rows)) return PE_ERR_SPACE;
+    GemvArgs a{Tiled{(const uint8_t*)w, n_rows, k / block_elems(type)},
+               n_rows, k, x, norm_w, eps, nullptr, nullptr, y, 0, layout,
+               (uint8_t*)workspace, state, log, log ? log_cap : 0};
+    return dispatch_gemv(type, a, true, kModeArgmax, (hipStream_t)stream);
+}

@@ -13,7 +13,7 @@
 
 namespace pe {
 
-enum { kModePlain = 0, kModeSilu = 1 };
+enum { kModePlain = 0, kModeSilu = 1, kModeArgmax = 2 };
 
 struct GemvArgs {
     Tiled w;
@@ -27,7 +27,84 @@ struct GemvArgs {
     float* y;
     int64_t up_off;       // SiLU mode: row of the "up" half = task + up_off
     int layout;           // PE_LAYOUT_* bits: x (and norm_w) / y (and residual) in ut layout
+    // argmax mode: workspace (one u64 key per block from byte kArgmaxPartOff), decode
+    // state {token, pos, count} and the token log
+    uint8_t* am_ws;
+    int64_t* am_state;
+    int64_t* am_log;
+    int64_t am_log_cap;
 };
+
+constexpr int kArgmaxPartOff = 256;
+
+// Order-preserving key of (value, row) for a greedy pick equal to torch.argmax: a larger
+// value wins, equal values go to the lower row, NaN beats every number (the lowest NaN row
+// wins) and -0.0 equals +0.0. Key 0 is never produced (it marks "no task").
+PE_DEV uint64_t argmax_key(float v, int64_t row) {
+    uint32_t u = __float_as_uint(v);
+    if (v != v) u = 0x7FFFFFFFu;
+    else if (u == 0x80000000u) u = 0u;
+    const uint32_t hi = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)hi << 32) | (uint32_t)~(uint32_t)row;
+}
+PE_DEV int64_t argmax_row(uint64_t key) { return (int64_t)(uint32_t)~(uint32_t)key; }
+
+PE_DEV uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const uint32_t lo = __shfl_xor((unsigned)v, m, 64), hi = __shfl_xor((unsigned)(v >> 32), m, 64);
+        const uint64_t o = ((uint64_t)hi << 32) | lo;
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// End of an argmax-mode launch: each block stores the best key of its groups in its own
+// slot. A second, one-block kernel (k_argmax_pick) reduces the slots after the grid is done,
+// so no block needs a device-scope fence (one per block costs an L2 write-back each).
+template <int GPB>
+PE_DEV void argmax_publish(const GemvArgs& a, uint64_t best, int glane, int gid) {
+    if constexpr (GPB == 1) {
+        if (threadIdx.x == 0) reinterpret_cast<uint64_t*>(a.am_ws + kArgmaxPartOff)[blockIdx.x] = best;
+    } else {
+        __shared__ uint64_t keys[GPB];
+        if (glane == 0) keys[gid] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint64_t b = keys[0];
+#pragma unroll
+            for (int g = 1; g < GPB; ++g) b = keys[g] > b ? keys[g] : b;
+            reinterpret_cast<uint64_t*>(a.am_ws + kArgmaxPartOff)[blockIdx.x] = b;
+        }
+    }
+}
+
+constexpr int kPickThreads = 1024;
+
+// Reduce the n_part block keys, write the pick into the decode state, advance the position
+// and append to the log.
+template <int kUnused = 0>
+__global__ __launch_bounds__(kPickThreads) void k_argmax_pick(const uint8_t* ws, int64_t n_part,
+                                                              int64_t* state, int64_t* log,
+                                                              int64_t log_cap) {
+    __shared__ uint64_t wmax[kPickThreads / 64];
+    const uint64_t* part = reinterpret_cast<const uint64_t*>(ws + kArgmaxPartOff);
+    uint64_t b = 0;
+    for (int64_t i = threadIdx.x; i < n_part; i += kPickThreads) b = part[i] > b ? part[i] : b;
+    b = wave_max_u64(b);
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = b;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int w = 0; w < kPickThreads / 64; ++w) b = wmax[w] > b ? wmax[w] : b;
+        const int64_t tok = argmax_row(b);
+        const int64_t c = state[2];
+        state[0] = tok;
+        state[1] = state[1] + 1;
+        state[2] = c + 1;
+        if (log && c >= 0 && c < log_cap) log[c] = tok;
+    }
+}
 
 // Sum over a group of GS lanes. GS = 256 is the whole block: wave butterflies, then the four
 // wave sums are added in wave order through LDS (every thread of the block must call it).
@@ -80,23 +157,33 @@ PE_DEV float block_sum(float v, float* lds4) {
 template <int GS>
 constexpr int block_threads() { return GS <= 64 ? 64 : 256; }
 
-// Load this lane's UPL activation units; with NORM, replace them by rmsnorm(x) * norm_w
-// (rstd = 1 / sqrt(sum(x^2) / k + eps), kernels.py:21-23); then the per-unit sums.
+// Load this lane's UPL activation units and their per-unit sums. With NORM the units hold
+// x * norm_w and the returned factor is rstd = 1 / sqrt(sum(x^2) / k + eps) (kernels.py:21-23);
+// the caller scales the reduced dot product by it. Taking rstd out of the dot product lets
+// the x and norm_w loads issue together and the dot products run while the sum of squares
+// is still being reduced. Without NORM the factor is 1.
 // Every thread of the block must call it (it synchronises the block).
 template <int GS, int UPL, bool NORM>
-PE_DEV void load_activation(const GemvArgs& a, int glane, int units, float (&xr)[UPL][32],
-                            UnitSums (&xs)[UPL], float* lds4, float* stage) {
+PE_DEV float load_activation(const GemvArgs& a, int glane, int units, float (&xr)[UPL][32],
+                             UnitSums (&xs)[UPL], float* lds4, float* stage) {
     constexpr int BS = block_threads<GS>();
+    float rstd = 1.0f;
     if (a.layout & PE_LAYOUT_X_UT) {
         // coalesced direct loads, no staging; the RMSNorm sum is reduced across the group.
+        float wr[UPL][32];
 #pragma unroll
         for (int t = 0; t < UPL; ++t) {
             const int u = glane + GS * t;
             if (u < units) {
                 load_x_unit_ut(a.x, u, units, xr[t]);
+                if constexpr (NORM) load_x_unit_ut(a.norm_w, u, units, wr[t]);
             } else {
 #pragma unroll
                 for (int i = 0; i < 32; ++i) xr[t][i] = 0.f;
+                if constexpr (NORM) {
+#pragma unroll
+                    for (int i = 0; i < 32; ++i) wr[t][i] = 0.f;
+                }
             }
         }
         if constexpr (NORM) {
@@ -104,22 +191,15 @@ PE_DEV void load_activation(const GemvArgs& a, int glane, int units, float (&xr)
 #pragma unroll
             for (int t = 0; t < UPL; ++t)
 #pragma unroll
-                for (int i = 0; i < 32; ++i) ss += xr[t][i] * xr[t][i];
-            const float rstd = 1.0f / sqrtf(gsum<GS>(ss, lds4) / (float)a.k + a.eps);
-#pragma unroll
-            for (int t = 0; t < UPL; ++t) {
-                const int u = glane + GS * t;
-                if (u < units) {
-                    float wr[32];
-                    load_x_unit_ut(a.norm_w, u, units, wr);
-#pragma unroll
-                    for (int i = 0; i < 32; ++i) xr[t][i] = (xr[t][i] * rstd) * wr[i];
+                for (int i = 0; i < 32; ++i) {
+                    ss += xr[t][i] * xr[t][i];
+                    xr[t][i] *= wr[t][i];
                 }
-            }
+            rstd = 1.0f / sqrtf(gsum<GS>(ss, lds4) / (float)a.k + a.eps);
         }
 #pragma unroll
         for (int t = 0; t < UPL; ++t) xs[t] = unit_sums(xr[t]);
-        return;
+        return rstd;
     }
     const bool staged = a.k <= kStageMaxK;
     float ss = 0.f;
@@ -160,7 +240,6 @@ PE_DEV void load_activation(const GemvArgs& a, int glane, int units, float (&xr)
         }
     }
     if constexpr (NORM) {
-        float rstd;
         if (staged) {
             rstd = 1.0f / sqrtf(block_sum<BS>(ss, lds4) / (float)a.k + a.eps);
         } else {
@@ -186,12 +265,13 @@ PE_DEV void load_activation(const GemvArgs& a, int glane, int units, float (&xr)
                     load_x_unit(a.norm_w, u, wr);
                 }
 #pragma unroll
-                for (int i = 0; i < 32; ++i) xr[t][i] = (xr[t][i] * rstd) * wr[i];
+                for (int i = 0; i < 32; ++i) xr[t][i] *= wr[i];
             }
         }
     }
 #pragma unroll
     for (int t = 0; t < UPL; ++t) xs[t] = unit_sums(xr[t]);
+    return rstd;
 }
 
 template <int T, int GS, int UPL, int R>
@@ -237,16 +317,18 @@ __global__ __launch_bounds__(block_threads<GS>()) void k_qgemv(GemvArgs a) {
     const int64_t stride = (int64_t)gridDim.x * GPB;
     int64_t task = (int64_t)blockIdx.x * GPB + gid;
 
+    constexpr bool kEpi = MODE != kModeSilu;
     typename Fmt<T>::Raw raw[R][UPL];
     Epi epi{0.f, 0.f};
+    uint64_t best = 0;  // argmax mode: best key of this group's tasks
     if (task < a.n_tasks) {
         load_task<T, GS, UPL, R>(a, task, glane, units, raw);
-        if constexpr (MODE == kModePlain) epi = load_epi(a, task, glane == 0);
+        if constexpr (kEpi) epi = load_epi(a, task, glane == 0);
     }
 
     float xr[UPL][32];
     UnitSums xs[UPL];
-    load_activation<GS, UPL, NORM>(a, glane, units, xr, xs, lds4, stage);
+    const float rstd = load_activation<GS, UPL, NORM>(a, glane, units, xr, xs, lds4, stage);
 
     for (; task < a.n_tasks; task += stride) {
         float acc[R];
@@ -261,10 +343,10 @@ __global__ __launch_bounds__(block_threads<GS>()) void k_qgemv(GemvArgs a) {
         const int64_t next = task + stride;
         if (next < a.n_tasks) {
             load_task<T, GS, UPL, R>(a, next, glane, units, raw);
-            if constexpr (MODE == kModePlain) epi = load_epi(a, next, glane == 0);
+            if constexpr (kEpi) epi = load_epi(a, next, glane == 0);
         }
 #pragma unroll
-        for (int rr = 0; rr < R; ++rr) acc[rr] = gsum<GS>(acc[rr], lds4);
+        for (int rr = 0; rr < R; ++rr) acc[rr] = gsum<GS>(acc[rr], lds4) * rstd;
         if (glane == 0) {
             if constexpr (MODE == kModeSilu) {
                 const float g = acc[0], u = acc[1];
@@ -273,10 +355,17 @@ __global__ __launch_bounds__(block_threads<GS>()) void k_qgemv(GemvArgs a) {
                 float v = acc[0];
                 if (a.bias) v += cur.bias;
                 if (a.residual) v = cur.res + v;
-                a.y[out_index(a, task)] = v;
+                if constexpr (MODE == kModeArgmax) {
+                    const uint64_t key = argmax_key(v, task);
+                    best = key > best ? key : best;
+                    if (a.y) a.y[task] = v;
+                } else {
+                    a.y[out_index(a, task)] = v;
+                }
             }
         }
     }
+    if constexpr (MODE == kModeArgmax) argmax_publish<GPB>(a, best, glane, gid);
 }
 
 // Lane-group shape for a reduction length of `units` 32-weight units.
@@ -298,6 +387,11 @@ inline bool pick_shape(int64_t units, Shape& s) {
 constexpr int kMaxGemvBlocks = 2048;    // 256-thread blocks (prefill GEMM, GS = 256)
 constexpr int kMaxWaveBlocks = 8192;    // one-wave blocks: up to 32 resident waves per CU
 
+// Argmax-mode workspace: a key per block (never more blocks than rows) after a 256-byte head.
+inline int64_t argmax_ws_bytes(int64_t n_rows) {
+    return kArgmaxPartOff + 8 * (n_rows < kMaxWaveBlocks ? n_rows : kMaxWaveBlocks);
+}
+
 template <int T, int GS, int UPL, bool NORM, int MODE>
 void launch_qgemv_shape(const GemvArgs& a, hipStream_t s) {
     constexpr int BS = block_threads<GS>();
@@ -307,6 +401,9 @@ void launch_qgemv_shape(const GemvArgs& a, hipStream_t s) {
     if (blocks > cap) blocks = cap;
     const size_t lds = (a.layout & PE_LAYOUT_X_UT) ? 0 : stage_lds_bytes(a.k, NORM);
     hipLaunchKernelGGL((k_qgemv<T, GS, UPL, NORM, MODE>), dim3((unsigned)blocks), dim3(BS), lds, s, a);
+    if constexpr (MODE == kModeArgmax)
+        hipLaunchKernelGGL(k_argmax_pick<0>, dim3(1), dim3(kPickThreads), 0, s, a.am_ws, blocks,
+                           a.am_state, a.am_log, a.am_log_cap);
 }
 
 template <int T, bool NORM, int MODE>
@@ -434,6 +531,8 @@ int gemv_dispatch(const GemvArgs& a, bool norm, int mode, hipStream_t s) {
     if (mode == kModeSilu)
         return norm ? launch_qgemv_mode<T, true, kModeSilu>(a, s)
                     : launch_qgemv_mode<T, false, kModeSilu>(a, s);
+    if (mode == kModeArgmax)
+        return norm ? launch_qgemv_mode<T, true, kModeArgmax>(a, s) : PE_ERR_NULL;
     return norm ? launch_qgemv_mode<T, true, kModePlain>(a, s)
                 : launch_qgemv_mode<T, false, kModePlain>(a, s);
 }

@@ -65,10 +65,8 @@ PE_DEV void qkv_task(const QkvParams& P, int seg, int64_t task, int glane, float
     ga.norm_w = a.norm_w;
     ga.eps = a.eps;
     ga.layout = a.layout & PE_LAYOUT_X_UT;
-    if (a.norm_w)
-        load_activation<GS, UPL, true>(ga, glane, units, xr, xs, lds4, stage);
-    else
-        load_activation<GS, UPL, false>(ga, glane, units, xr, xs, lds4, stage);
+    const float rstd = a.norm_w ? load_activation<GS, UPL, true>(ga, glane, units, xr, xs, lds4, stage)
+                                : load_activation<GS, UPL, false>(ga, glane, units, xr, xs, lds4, stage);
 
     float y1 = 0.f, y2 = 0.f;
     if (valid) {
@@ -80,8 +78,8 @@ PE_DEV void qkv_task(const QkvParams& P, int seg, int64_t task, int glane, float
             }
         }
     }
-    y1 = gsum<GS>(y1, lds4);
-    y2 = gsum<GS>(y2, lds4);
+    y1 = gsum<GS>(y1, lds4) * rstd;
+    y2 = gsum<GS>(y2, lds4) * rstd;
     if (!valid || glane != 0) return;
     y1 += b1;
     y2 += b2;

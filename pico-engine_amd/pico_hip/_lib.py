@@ -60,6 +60,8 @@ _SIGNATURES = {
     "pe_qgemv": (_I, [_I, _P, _L, _L, _P, _P, _P, _P, _I, _P]),
     "pe_qgemv_rmsnorm": (_I, [_I, _P, _L, _L, _P, _P, _F, _P, _I, _P]),
     "pe_qgemv_rmsnorm_silu": (_I, [_I, _P, _L, _L, _P, _P, _F, _P, _I, _P]),
+    "pe_qgemv_argmax_workspace_bytes": (_L, [_L]),
+    "pe_qgemv_rmsnorm_argmax": (_I, [_I, _P, _L, _L, _P, _P, _F, _P, _P, _P, _L, _P, _L, _I, _P]),
     "pe_qkv_rmsnorm_rope": (_I, [ctypes.POINTER(QkvArgs), _P]),
     "pe_decode_attn_workspace_bytes": (_L, [_I, _I, _I, _L]),
     "pe_decode_attn": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _P, _P, _L, _I, _P]),

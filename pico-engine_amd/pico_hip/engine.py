@@ -113,22 +113,32 @@ class Engine:
         self.model.attn_workspace(capacity)
         return cache
 
+    # Replays issued between two host reads of the greedy log: the host checks for the stop
+    # token once per chunk instead of synchronising on every token.
+    greedy_chunk = 16
+
     @torch.inference_mode()
     def _build_decode_graph(self, cache):
         """Capture the single-token decode forward into a HIP graph (engine.py:269-294).
-        Returns the graph, or None (eager fallback) if capture fails."""
-        self._static_ids = torch.zeros(1, dtype=torch.long, device=self.device)
-        self._static_pos = torch.zeros(1, dtype=torch.long, device=self.device)
+        The step reads its token and position from ``self._greedy.state`` and ends with the
+        device-side greedy pick, which writes the next token and position back there, so
+        greedy decoding replays the graph back to back. Returns the graph, or None (eager
+        fallback) if capture fails."""
+        capacity = cache[0][0].shape[1]
+        self._greedy = K.GreedyState(self.model.output.n, capacity, self.device)
+        self._static_ids = self._greedy.token
+        self._static_pos = self._greedy.pos
         try:
             s = torch.cuda.Stream(self.device)
             s.wait_stream(torch.cuda.current_stream(self.device))
             with torch.cuda.stream(s):
                 for _ in range(3):
-                    self.model.forward(self._static_ids, self._static_pos, cache)
+                    self.model.forward(self._static_ids, self._static_pos, cache, self._greedy)
             torch.cuda.current_stream(self.device).wait_stream(s)
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                self._static_logits = self.model.forward(self._static_ids, self._static_pos, cache)
+                self._static_logits = self.model.forward(self._static_ids, self._static_pos,
+                                                         cache, self._greedy)
             self._graph = g
             return g
         except Exception as e:  # noqa: BLE001 -- any capture failure falls back to eager
@@ -150,15 +160,50 @@ class Engine:
         )
 
     @torch.inference_mode()
+    def prefill_greedy(self, ids: list[int], cache) -> torch.Tensor:
+        """Prefill ``ids`` and make the first greedy pick on the device (it lands in the
+        greedy state as the next input, at position len(ids)). Needs _build_decode_graph
+        first (it owns the greedy state). Returns the prefill logits."""
+        self._greedy.reset(0, len(ids) - 1, 0)
+        tokens = torch.tensor(ids, device=self.device)
+        positions = torch.arange(len(ids), device=self.device)
+        return self.model.forward(tokens, positions, cache, self._greedy)
+
+    @torch.inference_mode()
+    def decode_greedy(self, graph, max_tokens: int, eos: int | None) -> list[int]:
+        """Greedy tokens after prefill_greedy: the same ids as the host loop
+        ``nxt = argmax(logits); stop at eos; decode(nxt)`` (evidence.py:117-123) and one
+        decode step per returned token, with the picks made on the device. The graph is
+        replayed in chunks; the log is read once per chunk and cut at the first eos. A stop
+        inside a chunk leaves some extra replays, whose cache rows lie inside the capacity
+        this generation allocated and are never read."""
+        done = 0
+        while True:
+            n = min(self.greedy_chunk, max_tokens - done)
+            for _ in range(n):
+                graph.replay()
+            done += n
+            picks = self._greedy.log[:done + 1].tolist()
+            if eos is not None and eos in picks:
+                return picks[:picks.index(eos)][:max_tokens]
+            if done >= max_tokens:
+                return picks[:max_tokens]
+
+    @torch.inference_mode()
     def generate_ids(self, ids: list[int], max_tokens: int = 64, temperature: float = 0.0,
                      top_k: int = 0, top_p: float = 1.0, use_graph: bool = True,
                      eos_id: int | None = None) -> list[int]:
-        """Prefill ``ids`` then decode up to ``max_tokens`` tokens; returns the new ids."""
+        """Prefill ``ids`` then decode up to ``max_tokens`` tokens; returns the new ids.
+        Greedy decoding with a graph picks tokens on the device; sampling and the eager path
+        pick on the host (sampler.py)."""
         if not ids:
             return []
         eos = self.tok.eos_id if eos_id is None else eos_id
         cache = self._empty_cache(len(ids) + max_tokens)
         graph = self._build_decode_graph(cache) if use_graph else None
+        if graph is not None and temperature <= 0:
+            self.prefill_greedy(ids, cache)
+            return self.decode_greedy(graph, max_tokens, eos)
         tokens = torch.tensor(ids, device=self.device)
         positions = torch.arange(len(ids), device=self.device)
         logits = self.model.forward(tokens, positions, cache)

@@ -296,6 +296,49 @@ def qgemv_norm(x: torch.Tensor, weight: torch.Tensor, w: QWeight, eps: float,
     return out
 
 
+class GreedyState:
+    """Device-side greedy decode state: ``state`` = [token, pos, count] (int64) -- the next
+    step's input id and position, and how many picks were made -- ``log`` of the picked ids,
+    and the argmax workspace (per-workgroup partial picks)."""
+
+    def __init__(self, n_rows: int, log_cap: int, device):
+        nbytes = lib.pe_qgemv_argmax_workspace_bytes(n_rows)
+        check(0 if nbytes >= 0 else -nbytes, "pe_qgemv_argmax_workspace_bytes")
+        self.state = torch.zeros(3, dtype=torch.int64, device=device)
+        self.log = torch.zeros(max(int(log_cap), 1), dtype=torch.int64, device=device)
+        self.log_cap = int(log_cap)
+        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+
+    def reset(self, token: int, pos: int, count: int = 0) -> None:
+        self.state.copy_(torch.tensor([token, pos, count], dtype=torch.int64), non_blocking=False)
+
+    @property
+    def token(self) -> torch.Tensor:
+        return self.state[0:1]
+
+    @property
+    def pos(self) -> torch.Tensor:
+        return self.state[1:2]
+
+
+def qgemv_norm_argmax(x: torch.Tensor, weight: torch.Tensor, w: QWeight, eps: float,
+                      greedy: GreedyState, out: torch.Tensor | None = None,
+                      layout: int = LAYOUT_NATURAL) -> torch.Tensor:
+    """Logits = W (rmsnorm(x) * weight) and the greedy pick (torch.argmax of the logits) into
+    ``greedy`` on the device (state[0] = pick, state[1] += 1, log[state[2]++] = pick)."""
+    dev = _on_gpu(x, weight, w.data, greedy.state)
+    x = _f32c(x.reshape(-1))
+    nw = _f32c(weight.reshape(-1))
+    if out is None:
+        out = torch.empty(w.n, device=dev, dtype=torch.float32)
+    check(lib.pe_qgemv_rmsnorm_argmax(w.ggml_type, _ptr(w.data), w.n, w.k, _ptr(x), _ptr(nw),
+                                      float(eps), _ptr(out), _ptr(greedy.state), _ptr(greedy.log),
+                                      greedy.log_cap, _ptr(greedy.workspace),
+                                      greedy.workspace.numel(), layout, _stream(dev)),
+          "pe_qgemv_rmsnorm_argmax")
+    return out
+
+
 def q5_0_gemv_norm(x: torch.Tensor, weight: torch.Tensor, w: QWeight, eps: float) -> torch.Tensor:
     """Fused RMSNorm(x, weight) + Q5_0 GEMV (kernels.py:253)."""
     return qgemv_norm(x, weight, _typed(w, GGML_Q5_0, "q5_0_gemv_norm"), eps)

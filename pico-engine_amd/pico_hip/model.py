@@ -122,16 +122,24 @@ class Transformer:
 
     @torch.inference_mode()
     def forward(self, token_ids: torch.Tensor, positions: torch.Tensor,
-                cache: list[tuple[torch.Tensor, torch.Tensor]]) -> torch.Tensor:
+                cache: list[tuple[torch.Tensor, torch.Tensor]],
+                greedy: K.GreedyState | None = None) -> torch.Tensor:
         """Run ``token_ids`` (L,) at ``positions`` (L,) updating ``cache``; logits (vocab,) of
-        the last position. Decode (L == 1) reads the position from device memory only, so the
-        step can be captured once and replayed as a graph."""
+        the last position. Decode (L == 1) reads the token and position from device memory
+        only, so the step can be captured once and replayed as a graph. With ``greedy`` the
+        LM head also makes the greedy pick on the device and advances ``greedy.state``
+        (token_ids/positions may then be its ``token``/``pos`` views)."""
         if token_ids.shape[0] == 1:
-            return self._decode(token_ids, positions, cache)
-        return self._prefill(token_ids, positions, cache)
+            return self._decode(token_ids, positions, cache, greedy)
+        return self._prefill(token_ids, positions, cache, greedy)
+
+    def _lm_head(self, x, norm_w, greedy, layout):
+        if greedy is None:
+            return K.qgemv_norm(x, norm_w, self.output, self.cfg.eps, layout=layout)
+        return K.qgemv_norm_argmax(x, norm_w, self.output, self.cfg.eps, greedy, layout=layout)
 
     # ---- decode ---------------------------------------------------------------------------
-    def _decode(self, token_ids, positions, cache):
+    def _decode(self, token_ids, positions, cache, greedy=None):
         """One token. The hidden and FFN vectors stay in the unit-transposed layout between
         kernels (each producer writes it, each GEMV reads it with coalesced loads)."""
         cfg = self.cfg
@@ -156,10 +164,10 @@ class Transformer:
                 u = K.qgemv_norm(x, L.ffn_norm_ut, L.w_up, cfg.eps, layout=XU)
                 act = K.silu_mul(torch.cat([g, u]).unsqueeze(0), cfg.ffn_dim).reshape(-1)
                 x = K.qgemv(act, L.w_down, residual=x, layout=YU)
-        return K.qgemv_norm(x, self.output_norm_ut, self.output, cfg.eps, layout=XU)
+        return self._lm_head(x, self.output_norm_ut, greedy, XU)
 
     # ---- prefill --------------------------------------------------------------------------
-    def _prefill(self, token_ids, positions, cache):
+    def _prefill(self, token_ids, positions, cache, greedy=None):
         cfg = self.cfg
         Lt = token_ids.shape[0]
         hd, nh, nkv = cfg.head_dim, cfg.n_head, cfg.n_kv_head
@@ -187,4 +195,4 @@ class Transformer:
                 gu = torch.cat([K.qgemm(h, L.w_gate), K.qgemm(h, L.w_up)], dim=1)
             act = K.silu_mul(gu, cfg.ffn_dim)
             x = K.qgemm(act, L.w_down, residual=x)
-        return K.qgemv_norm(x[-1], self.w["output_norm.weight"], self.output, cfg.eps)
+        return self._lm_head(x[-1], self.w["output_norm.weight"], greedy, K.LAYOUT_NATURAL)

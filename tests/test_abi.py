@@ -49,6 +49,9 @@ def test_nbytes_and_workspace(lib):
     assert ws == 256 + 2 * 2 * 7 * 66 * 4
     assert lib.pe_decode_attn_workspace_bytes(14, 3, 64, 77) == -3   # 14 % 3
     assert lib.pe_decode_attn_workspace_bytes(14, 2, 96, 77) == -3   # head_dim
+    assert lib.pe_qgemv_argmax_workspace_bytes(151936) == 256 + 8 * 8192
+    assert lib.pe_qgemv_argmax_workspace_bytes(100) == 256 + 8 * 100
+    assert lib.pe_qgemv_argmax_workspace_bytes(0) == -3
 
 
 def test_argument_errors_before_launch(lib):
@@ -83,6 +86,21 @@ def test_argument_errors_before_launch(lib):
                               ws, 0, None) == 1
     assert lib.pe_decode_attn(fake, fake, fake, 14, 2, 64, 77, None, 0, 5, 0.125, 1, fake, fake,
                               ws, 1, None) == 2   # only PE_LAYOUT_Y_UT applies to the output
+
+
+def test_argmax_argument_errors(lib):
+    P = ctypes.c_void_p
+    fake = P(0x1000)
+    ws = lib.pe_qgemv_argmax_workspace_bytes(4096)
+    call = lambda **kw: lib.pe_qgemv_rmsnorm_argmax(
+        kw.get("t", 8), fake, kw.get("n", 4096), 896, fake, kw.get("nw", fake), 1e-6, None, fake,
+        None, 0, kw.get("ws", fake), kw.get("wsb", ws), kw.get("layout", 0), None)
+    assert call(wsb=ws - 1) == 6                  # workspace too small
+    assert call(layout=2) == 2                    # the pick needs natural row order
+    assert call(nw=None) == 1                     # the LM head always normalises
+    assert call(ws=P(0x1010)) == 4                # workspace alignment
+    assert call(t=12) == 3                        # Q4_K needs k % 256 == 0
+    assert call(n=1 << 31, wsb=1 << 40) == 3      # row ids must fit 31 bits
 
 
 def test_qkv_args_struct_matches_header():

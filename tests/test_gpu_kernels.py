@@ -427,3 +427,86 @@ def test_embed_and_attention_ut_outputs(K):
         a = K.decode_attn(q, kc[:, :cap].contiguous(), vc[:, :cap].contiguous(), S=S)
         b = K.decode_attn(q, kc[:, :cap].contiguous(), vc[:, :cap].contiguous(), S=S, layout=K.LAYOUT_Y_UT)
         assert torch.equal(K.from_ut(b.reshape(-1)), a.reshape(-1))
+
+
+# ---- device-side greedy pick (LM head + argmax) -------------------------------------------
+
+def _const_rows_q8(vals, k):
+    """Q8_0 rows whose weights are all vals[r] (exactly representable: d = vals[r] / 127)."""
+    from pico_hip.quantize import quantize
+    W = np.repeat(np.asarray(vals, np.float32)[:, None], k, axis=1)
+    return quantize(dq.Q8_0, W)
+
+
+@pytest.mark.parametrize("t,k,n", [(dq.Q8_0, 896, 151936), (dq.Q5_0, 896, 1000), (dq.Q6_K, 4864, 300),
+                                   (dq.Q8_0, 896, 1)])
+def test_argmax_matches_torch_argmax(K, t, k, n):
+    raw = quantized_normal(t, n, k, seed=n + t)
+    w = qweight(K, t, raw, n, k)
+    rng = np.random.default_rng(n)
+    x = torch.from_numpy(rng.standard_normal(k).astype(np.float32)).to(DEV)
+    nw = torch.from_numpy(rng.standard_normal(k).astype(np.float32)).to(DEV)
+    g = K.GreedyState(n, 4, DEV)
+    g.reset(7, 41, 0)
+    logits = K.qgemv_norm_argmax(x, nw, w, 1e-6, g)
+    ref = K.qgemv_norm(x, nw, w, 1e-6)
+    assert torch.equal(logits, ref)          # same logits as the plain LM head
+    want = int(torch.argmax(ref))
+    st = g.state.tolist()
+    assert st == [want, 42, 1]
+    assert int(g.log[0]) == want
+
+
+def test_argmax_ties_nan_and_state_chain(K):
+    """Lowest row wins among equal maxima (torch.argmax), NaN beats numbers, the state
+    advances over consecutive calls and the log stops at its capacity."""
+    k, n = 896, 20000
+    vals = np.linspace(-0.5, 0.4, n).astype(np.float32)
+    vals[[1234, 5678, 19999]] = 0.9                      # three tied maxima
+    w = K.pack_weight(dev_bytes(_const_rows_q8(vals, k)), dq.Q8_0, n, k)
+    x = torch.ones(k, device=DEV)
+    nw = torch.ones(k, device=DEV)
+    g = K.GreedyState(n, 2, DEV)
+    g.reset(0, 5, 0)
+    for step in range(3):
+        logits = K.qgemv_norm_argmax(x, nw, w, 1e-6, g)
+        assert int(torch.argmax(logits)) == 1234
+        assert g.state.tolist() == [1234, 6 + step, step + 1]
+    assert g.log.tolist() == [1234, 1234]                # capacity 2: the third pick is not logged
+    xn = x.clone()
+    xn[3] = float("nan")                                 # every logit NaN -> row 0 (first NaN)
+    K.qgemv_norm_argmax(xn, nw, w, 1e-6, g)
+    assert int(g.state[0]) == 0
+    neg = torch.full((k,), -1.0, device=DEV)             # all logits negative: argmax = min |vals|
+    logits = K.qgemv_norm_argmax(neg, nw, w, 1e-6, g)
+    assert int(g.state[0]) == int(torch.argmax(logits))
+
+
+def test_argmax_in_graph_replays(K):
+    n, k = 151936, 896
+    raw = quantized_normal(dq.Q8_0, n, k, seed=5)
+    w = qweight(K, dq.Q8_0, raw, n, k)
+    rng = np.random.default_rng(3)
+    xs = [torch.from_numpy(rng.standard_normal(k).astype(np.float32)).to(DEV) for _ in range(4)]
+    nw = torch.ones(k, device=DEV)
+    x = xs[0].clone()
+    g = K.GreedyState(n, 8, DEV)
+    g.reset(0, 0, 0)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        K.qgemv_norm_argmax(x, nw, w, 1e-6, g)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = K.qgemv_norm_argmax(x, nw, w, 1e-6, g)
+    g.reset(0, 100, 0)
+    want = []
+    for xi in xs:
+        x.copy_(xi)
+        graph.replay()
+        torch.cuda.synchronize()
+        want.append(int(torch.argmax(K.qgemv_norm(xi, nw, w, 1e-6))))
+        assert int(torch.argmax(out)) == want[-1]
+    assert g.log[:4].tolist() == want
+    assert g.state.tolist() == [want[-1], 104, 4]

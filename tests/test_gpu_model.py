@@ -55,6 +55,25 @@ def test_greedy_tokens_match_oracle(tiny):
     assert got == want, (got, want, margins)
 
 
+def test_device_greedy_equals_host_loop_and_stops_at_eos(tiny):
+    """Greedy picks made on the device (graph replays, chunked log reads) give the ids of the
+    host loop argmax -> eos check -> decode step (evidence.py:117-123), eos included."""
+    eng, _ = tiny
+    ids = [11, 22, 33, 44]
+    host = eng.generate_ids(ids, 20, temperature=0.0, use_graph=False)
+    assert len(host) == 20
+    for chunk in (16, 3, 1):
+        eng.greedy_chunk = chunk
+        assert eng.generate_ids(ids, 20, temperature=0.0, use_graph=True) == host, chunk
+    eng.greedy_chunk = 16
+    for eos in (host[0], host[5], host[19]):
+        want = host[:host.index(eos)]
+        assert eng.generate_ids(ids, 20, temperature=0.0, use_graph=True, eos_id=eos) == want
+        assert eng.generate_ids(ids, 20, temperature=0.0, use_graph=False, eos_id=eos) == want
+    assert eng.generate_ids(ids, 0, temperature=0.0, use_graph=True) == []
+    assert eng.generate_ids(ids, 1, temperature=0.0, use_graph=True) == host[:1]
+
+
 def test_graph_equals_eager(tiny):
     eng, _ = tiny
     ids = [9, 8, 7, 6, 5]
