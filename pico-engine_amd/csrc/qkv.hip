@@ -17,9 +17,9 @@ struct QkvParams {
 
 // One task of one segment: the pair of rows (i, i + hd/2) of head `head`. Weight, bias,
 // position and cos/sin loads are issued before the activation prologue.
-template <int T, int GS, int UPL>
-PE_DEV void qkv_task(const QkvParams& P, int seg, int64_t task, int glane, float* lds4,
-                     float* stage) {
+template <int T, int GS, int UPL, int SEG>
+PE_DEV void qkv_task(const QkvParams& P, int64_t task, int glane, float* lds4, float* stage) {
+    constexpr int seg = SEG;
     const pe_qkv_args& a = P.a;
     const int units = (int)(P.k >> 5);
     const int hd = a.head_dim, half = hd / 2;
@@ -27,9 +27,9 @@ PE_DEV void qkv_task(const QkvParams& P, int seg, int64_t task, int glane, float
     const int64_t head = valid ? task / half : 0;
     const int i = valid ? (int)(task % half) : 0;
     const int64_t r1 = head * hd + i, r2 = r1 + half;
-    const void* w = seg == 0 ? a.w_q : seg == 1 ? a.w_k : a.w_v;
-    const float* b = seg == 0 ? a.b_q : seg == 1 ? a.b_k : a.b_v;
-    const int64_t seg_rows = (seg == 0 ? a.n_head : a.n_kv) * (int64_t)hd;
+    const void* w = SEG == 0 ? a.w_q : SEG == 1 ? a.w_k : a.w_v;
+    const float* b = SEG == 0 ? a.b_q : SEG == 1 ? a.b_k : a.b_v;
+    const int64_t seg_rows = (SEG == 0 ? a.n_head : a.n_kv) * (int64_t)hd;
     const Tiled t{(const uint8_t*)w, seg_rows, P.k / (int64_t)Fmt<T>::QK};
 
     typename Fmt<T>::Raw p[UPL], q[UPL];
@@ -106,6 +106,18 @@ PE_DEV void qkv_task(const QkvParams& P, int seg, int64_t task, int glane, float
     }
 }
 
+template <int GS, int UPL, int SEG>
+PE_DEV void qkv_segment(const QkvParams& P, int type, int64_t task, int glane, float* lds4,
+                        float* stage) {
+    switch (type) {
+        case PE_TYPE_Q8_0: qkv_task<PE_TYPE_Q8_0, GS, UPL, SEG>(P, task, glane, lds4, stage); break;
+        case PE_TYPE_Q5_0: qkv_task<PE_TYPE_Q5_0, GS, UPL, SEG>(P, task, glane, lds4, stage); break;
+        case PE_TYPE_Q4_K: qkv_task<PE_TYPE_Q4_K, GS, UPL, SEG>(P, task, glane, lds4, stage); break;
+        case PE_TYPE_Q6_K: qkv_task<PE_TYPE_Q6_K, GS, UPL, SEG>(P, task, glane, lds4, stage); break;
+        default: break;
+    }
+}
+
 // Blocks [0, bq) serve q, [bq, bq + bk) k, the rest v: one segment (one format) per block.
 template <int GS, int UPL>
 __global__ __launch_bounds__(block_threads<GS>()) void k_qkv(QkvParams P) {
@@ -125,14 +137,12 @@ __global__ __launch_bounds__(block_threads<GS>()) void k_qkv(QkvParams P) {
     const int64_t task0 = blk * GPB + threadIdx.x / GS;
     const int64_t task = task0 < ntask ? task0 : -1;
     const int glane = threadIdx.x % GS;
-    const int type = seg == 0 ? a.type_q : seg == 1 ? a.type_k : a.type_v;
-    switch (type) {
-        case PE_TYPE_Q8_0: qkv_task<PE_TYPE_Q8_0, GS, UPL>(P, seg, task, glane, lds4, stage); break;
-        case PE_TYPE_Q5_0: qkv_task<PE_TYPE_Q5_0, GS, UPL>(P, seg, task, glane, lds4, stage); break;
-        case PE_TYPE_Q4_K: qkv_task<PE_TYPE_Q4_K, GS, UPL>(P, seg, task, glane, lds4, stage); break;
-        case PE_TYPE_Q6_K: qkv_task<PE_TYPE_Q6_K, GS, UPL>(P, seg, task, glane, lds4, stage); break;
-        default: break;
-    }
+    // The segment is a template argument below: selecting fields of the argument block with a
+    // run-time segment index made the compiler copy the block to scratch memory and read it
+    // back (a memory round trip before the first weight load).
+    if (seg == 0) qkv_segment<GS, UPL, 0>(P, a.type_q, task, glane, lds4, stage);
+    else if (seg == 1) qkv_segment<GS, UPL, 1>(P, a.type_k, task, glane, lds4, stage);
+    else qkv_segment<GS, UPL, 2>(P, a.type_v, task, glane, lds4, stage);
 }
 
 }  // namespace pe
