@@ -194,6 +194,50 @@ int pe_decode_attn(const float* q, const float* k_cache, const float* v_cache, i
                    int64_t len_add, float scale, int round_fp16, float* out, void* workspace,
                    int64_t workspace_bytes, int layout, pe_stream_t stream);
 
+/* Whole attention block of one decode token in one launch (short caches):
+ *   h = rmsnorm(x) * norm_w;  [q; k; v] = [Wq; Wk; Wv] h + [bq; bk; bv];  RoPE(q, k) at *pos;
+ *   k, v -> cache row *pos;  a = decode attention of q over cache rows 0..*pos (GQA, scale,
+ *   output rounded to fp16 when round_fp16);  x_out = x + Wo a.
+ * Replaces, per layer, model.py:175-193 (rmsnorm, F.linear qkv, rope, index_copy_),
+ * model.py:211 (decode_attn, kernels.py:129) and model.py:213 (torch.addmm o-projection).
+ * Inside the launch, producer workgroups compute q, k, v and signal per-head counters in the
+ * workspace; consumer workgroups wait for them (bounded waits), compute the attention of every
+ * head and one slice of the o-projection rows. Vectors are in the natural layout.
+ * Limits: head_dim 64; n_kv <= 8; n_head / n_kv <= 16; capacity <= 512 / n_kv;
+ * hidden == n_head * head_dim, hidden % 64 == 0 and hidden <= 1024 (larger shapes use
+ * pe_qkv_rmsnorm_rope + pe_decode_attn + pe_qgemv). PE_ERR_SHAPE otherwise.
+ * An out-of-range *pos writes nothing to the cache and NaN to x_out.
+ * workspace: pe_attn_block_workspace_bytes(...) bytes, 256-byte aligned, zero-filled once
+ * before first use; calls that share it must run in order on one stream. The first 32-bit
+ * word is an error flag: non-zero after an internal wait ran out (it cannot in a correct
+ * launch; it bounds the damage of a fault elsewhere). Results of that call and of later ones
+ * are then invalid until the workspace is zero-filled again.
+ */
+typedef struct pe_attn_block_args {
+    int type_q, type_k, type_v, type_o;  /* ggml types of the tiled weights */
+    const void *w_q, *w_k, *w_v, *w_o;   /* (n_head*hd x hidden), (n_kv*hd x hidden) x2, (hidden x n_head*hd) */
+    const float *b_q, *b_k, *b_v;        /* biases or NULL */
+    const float* x;                      /* (hidden) residual stream */
+    const float* norm_w;                 /* (hidden) attn_norm weight */
+    float eps;
+    const float* cos_tab;                /* (rope_rows, hd/2) */
+    const float* sin_tab;
+    int64_t rope_rows;
+    const int64_t* pos;                  /* device scalar: position of this token */
+    float* k_cache;                      /* (n_kv, capacity, hd) */
+    float* v_cache;
+    int64_t capacity;
+    float* x_out;                        /* (hidden), must not alias x */
+    int64_t hidden;
+    int n_head, n_kv, head_dim;
+    float scale;
+    int round_fp16;
+} pe_attn_block_args;
+int64_t pe_attn_block_workspace_bytes(int64_t hidden, int n_head, int n_kv, int head_dim,
+                                      int64_t capacity);
+int pe_attn_block(const pe_attn_block_args* args, void* workspace, int64_t workspace_bytes,
+                  pe_stream_t stream);
+
 /* ---- general / prefill (M >= 1) kernels ------------------------------------------------ */
 
 /* y[r][:] = rmsnorm(x[r][:]) * w for r < rows (row strides in elements).

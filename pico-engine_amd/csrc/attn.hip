@@ -107,7 +107,7 @@ __global__ __launch_bounds__(256) void k_decode_attn(AttnParams p) {
         for (int g = 0; g < G; ++g) {
             float part = 0.f;
 #pragma unroll
-            for (int i = 0; i < DQ; ++i) part += q_lds[g * HD + dq * DQ + i] * kr[i];
+            for (int i = 0; i < DQ; ++i) part = fmaf(q_lds[g * HD + dq * DQ + i], kr[i], part);
             part += __shfl_xor(part, 1, kWave);
             part += __shfl_xor(part, 2, kWave);
             if (dq == 0) sc_lds[g * kChunk + sl] = (s < S) ? part * p.scale : NEG_INF;
@@ -138,7 +138,7 @@ __global__ __launch_bounds__(256) void k_decode_attn(AttnParams p) {
             acc[g] = 0.f;
             if (g < G) {
 #pragma unroll
-                for (int pp = 0; pp < NPOS; ++pp) acc[g] += sc_lds[g * kChunk + js * NPOS + pp] * vr[pp];
+                for (int pp = 0; pp < NPOS; ++pp) acc[g] = fmaf(sc_lds[g * kChunk + js * NPOS + pp], vr[pp], acc[g]);
                 red_lds[(js * kMaxGroup + g) * HD + d] = acc[g];
             }
         }
@@ -179,8 +179,8 @@ __global__ __launch_bounds__(256) void k_decode_attn(AttnParams p) {
         for (int sp = 0; sp < nvalid; ++sp) {
             const float* r = base + (sp * G + g) * REC;
             const float e = expf(r[0] - M);
-            L += r[1] * e;
-            A += r[2 + dd] * e;
+            L = fmaf(r[1], e, L);
+            A = fmaf(r[2 + dd], e, A);
         }
         float o = A / L;
         if (p.round_fp16) o = round_to_f16(o);
@@ -230,10 +230,10 @@ __global__ __launch_bounds__(256) void k_decode_attn_head(AttnParams p) {
 #pragma unroll
         for (int i = 0; i < HD / 4; ++i) {
             const float4 k4 = s == t ? k0[i] : reinterpret_cast<const float4*>(kb + (int64_t)s * HD)[i];
-            dot += q_lds[4 * i] * k4.x;
-            dot += q_lds[4 * i + 1] * k4.y;
-            dot += q_lds[4 * i + 2] * k4.z;
-            dot += q_lds[4 * i + 3] * k4.w;
+            dot = fmaf(q_lds[4 * i], k4.x, dot);
+            dot = fmaf(q_lds[4 * i + 1], k4.y, dot);
+            dot = fmaf(q_lds[4 * i + 2], k4.z, dot);
+            dot = fmaf(q_lds[4 * i + 3], k4.w, dot);
         }
         const float v = dot * p.scale;
         sc[s] = v;
@@ -258,7 +258,7 @@ __global__ __launch_bounds__(256) void k_decode_attn_head(AttnParams p) {
 #pragma unroll
     for (int j = 0; j < NPRE; ++j) {
         const int sp = js + j * PS;
-        if (sp < S) acc += sc[sp] * vpre[j];
+        if (sp < S) acc = fmaf(sc[sp], vpre[j], acc);
     }
     int s = js + NPRE * PS;
     for (; s + 7 * PS < S; s += 8 * PS) {
@@ -266,9 +266,9 @@ __global__ __launch_bounds__(256) void k_decode_attn_head(AttnParams p) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = vb[(int64_t)(s + j * PS) * HD + d];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc += sc[s + j * PS] * v[j];
+        for (int j = 0; j < 8; ++j) acc = fmaf(sc[s + j * PS], v[j], acc);
     }
-    for (; s < S; s += PS) acc += sc[s] * vb[(int64_t)s * HD + d];
+    for (; s < S; s += PS) acc = fmaf(sc[s], vb[(int64_t)s * HD + d], acc);
     red[js * HD + d] = acc;
     __syncthreads();
     if (t < HD) {
@@ -339,8 +339,10 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillParams p) {
 #pragma unroll
             for (int i = 0; i < HD / 4; ++i) {
                 const float4 k4 = kr[i];
-                dot += q_lds[4 * i] * k4.x + q_lds[4 * i + 1] * k4.y + q_lds[4 * i + 2] * k4.z +
-                       q_lds[4 * i + 3] * k4.w;
+                dot = fmaf(q_lds[4 * i], k4.x, dot);
+                dot = fmaf(q_lds[4 * i + 1], k4.y, dot);
+                dot = fmaf(q_lds[4 * i + 2], k4.z, dot);
+                dot = fmaf(q_lds[4 * i + 3], k4.w, dot);
             }
             sc = dot * p.scale;
         }
@@ -349,15 +351,15 @@ __global__ __launch_bounds__(256) void k_prefill_attn(PrefillParams p) {
         const float e = expf(sc - Mn);
         const float lc = block_sum256(e, lds4);
         const float alpha = expf(M - Mn);
-        L = L * alpha + lc;
+        L = fmaf(L, alpha, lc);
         p_lds[t] = e;
         __syncthreads();
         float part = 0.f;
         for (int pp = 0; pp < NPOS; ++pp) {
             const int64_t sk = c0 + js * NPOS + pp;
-            if (sk < nkeys) part += p_lds[js * NPOS + pp] * vbase[sk * HD + d];
+            if (sk < nkeys) part = fmaf(p_lds[js * NPOS + pp], vbase[sk * HD + d], part);
         }
-        acc = acc * alpha + part;
+        acc = fmaf(acc, alpha, part);
         M = Mn;
         __syncthreads();
     }

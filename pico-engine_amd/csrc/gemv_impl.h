@@ -3,8 +3,9 @@
 // Decode (M = 1) mapping: a "group" of GS lanes (32, 64 or the whole 256-thread block) owns
 // one output task at a time; lane g of the group decodes units g, g+GS, ... (UPL of them,
 // 32 weights each) straight from HBM with aligned 16-byte loads, multiplies them with the
-// matching 32 activations it keeps in registers for the whole kernel, and the group reduces
-// with a butterfly (plus LDS across waves when GS = 256). No MFMA: an M = 1 product reads
+// matching 32 activations it keeps in registers for the whole kernel (staged once per
+// 256-thread block through LDS), and the group reduces with a butterfly (plus LDS across
+// waves when GS = 256). No MFMA: an M = 1 product reads
 // every weight once and is bound by HBM bandwidth. All reductions are in a fixed order, so
 // results are deterministic and identical between eager launches and graph replays.
 #pragma once
@@ -106,19 +107,21 @@ __global__ __launch_bounds__(kPickThreads) void k_argmax_pick(const uint8_t* ws,
     }
 }
 
-// Sum over a group of GS lanes. GS = 256 is the whole block: wave butterflies, then the four
-// wave sums are added in wave order through LDS (every thread of the block must call it).
+// Sum over a group of GS lanes. GS = 128 / 256 spans 2 / 4 waves of a 256-thread block: wave
+// butterflies, then the wave sums of the group are added in wave order through LDS (every
+// thread of the block must call it; lds4 holds 4 floats).
 template <int GS>
 PE_DEV float gsum(float v, float* lds4) {
     if constexpr (GS <= 64) {
         return wave_sum<GS>(v);
     } else {
-        static_assert(GS == 256, "group is a wave part or the whole block");
+        static_assert(GS == 128 || GS == 256, "group is a wave part, two waves or four waves");
         v = wave_sum<64>(v);
         const int w = threadIdx.x >> 6;
         __syncthreads();
         if ((threadIdx.x & 63) == 0) lds4[w] = v;
         __syncthreads();
+        if constexpr (GS == 128) return lds4[w & ~1] + lds4[w | 1];
         return ((lds4[0] + lds4[1]) + lds4[2]) + lds4[3];
     }
 }
@@ -152,8 +155,8 @@ PE_DEV float block_sum(float v, float* lds4) {
     }
 }
 
-// Threads per block for a group width: one wave for GS <= 64 (no block barriers on the
-// latency path), four waves for GS = 256.
+// Threads per block of the QKV kernel for a group width: one wave for GS <= 64 (no block
+// barriers on the latency path), four waves for GS = 128 / 256.
 template <int GS>
 constexpr int block_threads() { return GS <= 64 ? 64 : 256; }
 
@@ -192,7 +195,7 @@ PE_DEV float load_activation(const GemvArgs& a, int glane, int units, float (&xr
             for (int t = 0; t < UPL; ++t)
 #pragma unroll
                 for (int i = 0; i < 32; ++i) {
-                    ss += xr[t][i] * xr[t][i];
+                    ss = fmaf(xr[t][i], xr[t][i], ss);
                     xr[t][i] *= wr[t][i];
                 }
             rstd = 1.0f / sqrtf(gsum<GS>(ss, lds4) / (float)a.k + a.eps);
@@ -213,7 +216,7 @@ PE_DEV float load_activation(const GemvArgs& a, int glane, int units, float (&xr
             *reinterpret_cast<float4*>(sx + off) = v;
             if constexpr (NORM) {
                 *reinterpret_cast<float4*>(sw + off) = reinterpret_cast<const float4*>(a.norm_w)[i];
-                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
             }
         }
         __syncthreads();
@@ -246,7 +249,7 @@ PE_DEV float load_activation(const GemvArgs& a, int glane, int units, float (&xr
 #pragma unroll
             for (int t = 0; t < UPL; ++t)
 #pragma unroll
-                for (int i = 0; i < 32; ++i) ss += xr[t][i] * xr[t][i];
+                for (int i = 0; i < 32; ++i) ss = fmaf(xr[t][i], xr[t][i], ss);
             rstd = 1.0f / sqrtf(gsum<GS>(ss, lds4) / (float)a.k + a.eps);
         }
 #pragma unroll
@@ -302,105 +305,232 @@ PE_DEV Epi load_epi(const GemvArgs& a, int64_t task, bool lane0) {
     return e;
 }
 
-// Timeline per group: issue the first task's weight (and epilogue) loads, then load and
-// normalise the activations while those are in flight; per task: dot products on the
-// weights in registers, issue the next task's loads, reduce, store.
-template <int T, int GS, int UPL, bool NORM, int MODE>
-__global__ __launch_bounds__(block_threads<GS>()) void k_qgemv(GemvArgs a) {
-    constexpr int GPB = block_threads<GS>() / GS;
+// Block-wide sum over NT threads (NT / 64 waves, every thread must call it): wave butterflies,
+// then the wave sums are added in wave order through LDS (lds holds NT / 64 floats).
+template <int NT>
+PE_DEV float block_sum_nt(float v, float* lds) {
+    v = wave_sum<64>(v);
+    if constexpr (NT == 64) {
+        return v;
+    } else {
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+        __syncthreads();
+        float s = lds[0];
+#pragma unroll
+        for (int w = 1; w < NT / 64; ++w) s += lds[w];
+        return s;
+    }
+}
+
+// Activation prologue of the blocked decode GEMV. With k <= kStageMaxK the block copies x
+// (times the RMSNorm weight with NORM) into LDS once -- 16-byte words contiguous across the
+// threads, in the natural or the unit-transposed layout -- as units of 32 floats padded to
+// kUnitStride, then every lane reads its own units from LDS. Longer vectors are read per lane
+// straight from global memory. With NORM the returned factor is rstd = 1 / sqrt(sum(x^2) / k +
+// eps) (kernels.py:21-23), applied by the caller after the dot product; otherwise 1.
+// Every thread of the block must call it.
+template <int NT, int GS, int UPL, bool NORM>
+PE_DEV float stage_activation(const GemvArgs& a, int glane, int units, float (&xr)[UPL][32],
+                              UnitSums (&xs)[UPL], float* lds4, float* stage) {
+    const bool ut = a.layout & PE_LAYOUT_X_UT;
+    float ss = 0.f;
+    if (a.k <= kStageMaxK) {
+        const int n4 = units * 8;
+        for (int i = threadIdx.x; i < n4; i += NT) {
+            const int u = ut ? i % units : i >> 3;
+            const int j = ut ? i / units : i & 7;
+            float4 v = reinterpret_cast<const float4*>(a.x)[i];
+            if constexpr (NORM) {
+                const float4 w = reinterpret_cast<const float4*>(a.norm_w)[i];
+                ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
+                v.x *= w.x;
+                v.y *= w.y;
+                v.z *= w.z;
+                v.w *= w.w;
+            }
+            *reinterpret_cast<float4*>(stage + u * kUnitStride + 4 * j) = v;
+        }
+        float rstd = 1.0f;
+        if constexpr (NORM) rstd = 1.0f / sqrtf(block_sum_nt<NT>(ss, lds4) / (float)a.k + a.eps);
+        else __syncthreads();
+#pragma unroll
+        for (int t = 0; t < UPL; ++t) {
+            const int u = glane + GS * t;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (u < units) v = *reinterpret_cast<const float4*>(stage + u * kUnitStride + 4 * i);
+                xr[t][4 * i] = v.x;
+                xr[t][4 * i + 1] = v.y;
+                xr[t][4 * i + 2] = v.z;
+                xr[t][4 * i + 3] = v.w;
+            }
+            xs[t] = unit_sums(xr[t]);
+        }
+        return rstd;
+    }
+#pragma unroll
+    for (int t = 0; t < UPL; ++t) {
+        const int u = glane + GS * t;
+        if (u < units) {
+            if (ut) load_x_unit_ut(a.x, u, units, xr[t]);
+            else load_x_unit(a.x, u, xr[t]);
+            if constexpr (NORM) {
+                float wr[32];
+                if (ut) load_x_unit_ut(a.norm_w, u, units, wr);
+                else load_x_unit(a.norm_w, u, wr);
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    ss = fmaf(xr[t][i], xr[t][i], ss);
+                    xr[t][i] *= wr[i];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) xr[t][i] = 0.f;
+        }
+        xs[t] = unit_sums(xr[t]);
+    }
+    if constexpr (NORM) {
+        // a group's lanes together hold every unit of x: the group sum is the whole sum(x^2)
+        return 1.0f / sqrtf(gsum<GS>(ss, lds4) / (float)a.k + a.eps);
+    }
+    return 1.0f;
+}
+
+constexpr int kGemvThreads = 256;
+
+// Blocked decode GEMV. A block of kGemvThreads threads owns a chunk of TPG * G consecutive
+// tasks (G = kGemvThreads / GS lane groups; group g takes tasks chunk*CH + i*G + g). Timeline:
+// every weight (and epilogue) load of the chunk is issued first; the activation is staged in
+// LDS once per block while those loads are in flight; then each group computes its TPG tasks
+// from registers, issues the loads of its next chunk (grid-stride over chunks when the grid
+// is capped), reduces with DPP butterflies and stores.
+template <int T, int GS, int UPL, int TPG, bool NORM, int MODE>
+__global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
+    constexpr int NT = kGemvThreads;
+    constexpr int G = NT / GS;
+    constexpr int CH = G * TPG;
     constexpr int R = (MODE == kModeSilu) ? 2 : 1;
-    __shared__ float lds4[4];
+    constexpr bool kEpi = MODE != kModeSilu;
+    __shared__ float lds4[NT / 64];
     extern __shared__ float stage[];
     const int glane = threadIdx.x % GS;
     const int gid = threadIdx.x / GS;
     const int units = (int)(a.k >> 5);
-    const int64_t stride = (int64_t)gridDim.x * GPB;
-    int64_t task = (int64_t)blockIdx.x * GPB + gid;
+    const int64_t nchunk = (a.n_tasks + CH - 1) / CH;
+    int64_t chunk = blockIdx.x;
 
-    constexpr bool kEpi = MODE != kModeSilu;
-    typename Fmt<T>::Raw raw[R][UPL];
-    Epi epi{0.f, 0.f};
-    uint64_t best = 0;  // argmax mode: best key of this group's tasks
-    if (task < a.n_tasks) {
-        load_task<T, GS, UPL, R>(a, task, glane, units, raw);
-        if constexpr (kEpi) epi = load_epi(a, task, glane == 0);
-    }
+    typename Fmt<T>::Raw raw[TPG][R][UPL];
+    Epi epi[TPG];
+    auto issue = [&](int64_t c) {
+#pragma unroll
+        for (int i = 0; i < TPG; ++i) {
+            const int64_t task = c * CH + i * G + gid;
+            if (task < a.n_tasks) {
+                load_task<T, GS, UPL, R>(a, task, glane, units, raw[i]);
+                if constexpr (kEpi) epi[i] = load_epi(a, task, glane == 0);
+            }
+        }
+    };
+    if (chunk < nchunk) issue(chunk);
 
     float xr[UPL][32];
     UnitSums xs[UPL];
-    const float rstd = load_activation<GS, UPL, NORM>(a, glane, units, xr, xs, lds4, stage);
+    const float rstd = stage_activation<NT, GS, UPL, NORM>(a, glane, units, xr, xs, lds4, stage);
 
-    for (; task < a.n_tasks; task += stride) {
-        float acc[R];
+    uint64_t best = 0;  // argmax mode: best key of this group's tasks
+    for (; chunk < nchunk; chunk += gridDim.x) {
+        float acc[TPG][R];
 #pragma unroll
-        for (int rr = 0; rr < R; ++rr) {
-            acc[rr] = 0.f;
+        for (int i = 0; i < TPG; ++i)
 #pragma unroll
-            for (int t = 0; t < UPL; ++t)
-                if (glane + GS * t < units) acc[rr] += Fmt<T>::dot(raw[rr][t], xr[t], xs[t]);
-        }
-        const Epi cur = epi;
-        const int64_t next = task + stride;
-        if (next < a.n_tasks) {
-            load_task<T, GS, UPL, R>(a, next, glane, units, raw);
-            if constexpr (kEpi) epi = load_epi(a, next, glane == 0);
-        }
+            for (int rr = 0; rr < R; ++rr) {
+                acc[i][rr] = 0.f;
 #pragma unroll
-        for (int rr = 0; rr < R; ++rr) acc[rr] = gsum<GS>(acc[rr], lds4) * rstd;
-        if (glane == 0) {
-            if constexpr (MODE == kModeSilu) {
-                const float g = acc[0], u = acc[1];
-                a.y[out_index(a, task)] = (g * (1.0f / (1.0f + expf(-g)))) * u;
-            } else {
-                float v = acc[0];
-                if (a.bias) v += cur.bias;
-                if (a.residual) v = cur.res + v;
-                if constexpr (MODE == kModeArgmax) {
-                    const uint64_t key = argmax_key(v, task);
-                    best = key > best ? key : best;
-                    if (a.y) a.y[task] = v;
+                for (int t = 0; t < UPL; ++t)
+                    if (glane + GS * t < units) acc[i][rr] += Fmt<T>::dot(raw[i][rr][t], xr[t], xs[t]);
+            }
+        Epi cur[TPG];
+#pragma unroll
+        for (int i = 0; i < TPG; ++i) cur[i] = epi[i];
+        const int64_t c0 = chunk;
+        if (chunk + gridDim.x < nchunk) issue(chunk + gridDim.x);
+#pragma unroll
+        for (int i = 0; i < TPG; ++i) {
+#pragma unroll
+            for (int rr = 0; rr < R; ++rr) acc[i][rr] = gsum<GS>(acc[i][rr], lds4) * rstd;
+            const int64_t task = c0 * CH + i * G + gid;
+            if (glane == 0 && task < a.n_tasks) {
+                if constexpr (MODE == kModeSilu) {
+                    const float g = acc[i][0], u = acc[i][1];
+                    a.y[out_index(a, task)] = (g * (1.0f / (1.0f + expf(-g)))) * u;
                 } else {
-                    a.y[out_index(a, task)] = v;
+                    float v = acc[i][0];
+                    if (a.bias) v += cur[i].bias;
+                    if (a.residual) v = cur[i].res + v;
+                    if constexpr (MODE == kModeArgmax) {
+                        const uint64_t key = argmax_key(v, task);
+                        best = key > best ? key : best;
+                        if (a.y) a.y[task] = v;
+                    } else {
+                        a.y[out_index(a, task)] = v;
+                    }
                 }
             }
         }
     }
-    if constexpr (MODE == kModeArgmax) argmax_publish<GPB>(a, best, glane, gid);
+    if constexpr (MODE == kModeArgmax) argmax_publish<G>(a, best, glane, gid);
 }
 
-// Lane-group shape for a reduction length of `units` 32-weight units.
+// Lane-group shape for a reduction length of `units` 32-weight units: one unit per lane up to
+// 256 units (a row of the 4864-long ffn_down spreads over a whole block, which keeps several
+// waves per SIMD busy on the per-weight decode), then up to four units per lane.
 struct Shape {
     int gs, upl;
 };
 inline bool pick_shape(int64_t units, Shape& s) {
     if (units <= 32) s = {32, 1};
     else if (units <= 64) s = {64, 1};
-    else if (units <= 128) s = {64, 2};
-    else if (units <= 192) s = {64, 3};
-    else if (units <= 256) s = {64, 4};
+    else if (units <= 128) s = {128, 1};
+    else if (units <= 256) s = {256, 1};
+    else if (units <= 512) s = {256, 2};
     else if (units <= 768) s = {256, 3};
     else if (units <= 1024) s = {256, 4};
     else return false;
     return true;
 }
 
-constexpr int kMaxGemvBlocks = 2048;    // 256-thread blocks (prefill GEMM, GS = 256)
-constexpr int kMaxWaveBlocks = 8192;    // one-wave blocks: up to 32 resident waves per CU
+// The seven instantiated shapes, as one switch key (gs * 16 + upl).
+#define PE_SHAPE_CASES(X)  \
+    X(32, 1) X(64, 1) X(128, 1) X(256, 1) X(256, 2) X(256, 3) X(256, 4)
 
-// Argmax-mode workspace: a key per block (never more blocks than rows) after a 256-byte head.
+constexpr int kMaxGemvBlocks = 8192;   // blocked decode GEMV: beyond this, blocks loop over chunks
+constexpr int kMaxGemmBlocks = 2048;   // prefill GEMM
+
+// Tasks per group of a launch: the LM-head argmax runs four rows per group (fewer, fuller
+// blocks for the 151936-row product); every other decode GEMV one.
+template <int MODE>
+constexpr int tasks_per_group() { return MODE == kModeArgmax ? 4 : 1; }
+
+// Argmax-mode workspace: a key per block after a 256-byte head, sized for the smallest chunk
+// (one group of kGemvThreads lanes per block, tasks_per_group rows), whatever k is.
 inline int64_t argmax_ws_bytes(int64_t n_rows) {
-    return kArgmaxPartOff + 8 * (n_rows < kMaxWaveBlocks ? n_rows : kMaxWaveBlocks);
+    const int64_t per_block = tasks_per_group<kModeArgmax>();
+    const int64_t blocks = (n_rows + per_block - 1) / per_block;
+    return kArgmaxPartOff + 8 * (blocks < kMaxGemvBlocks ? blocks : kMaxGemvBlocks);
 }
 
 template <int T, int GS, int UPL, bool NORM, int MODE>
 void launch_qgemv_shape(const GemvArgs& a, hipStream_t s) {
-    constexpr int BS = block_threads<GS>();
-    constexpr int GPB = BS / GS;
-    int64_t blocks = (a.n_tasks + GPB - 1) / GPB;
-    const int64_t cap = BS == 64 ? kMaxWaveBlocks : kMaxGemvBlocks;
-    if (blocks > cap) blocks = cap;
-    const size_t lds = (a.layout & PE_LAYOUT_X_UT) ? 0 : stage_lds_bytes(a.k, NORM);
-    hipLaunchKernelGGL((k_qgemv<T, GS, UPL, NORM, MODE>), dim3((unsigned)blocks), dim3(BS), lds, s, a);
+    constexpr int TPG = tasks_per_group<MODE>();
+    constexpr int CH = (kGemvThreads / GS) * TPG;
+    int64_t blocks = (a.n_tasks + CH - 1) / CH;
+    if (blocks > kMaxGemvBlocks) blocks = kMaxGemvBlocks;
+    const size_t lds = a.k <= kStageMaxK ? (size_t)(a.k / 32) * kUnitStride * 4 : 0;
+    hipLaunchKernelGGL((k_qgemv<T, GS, UPL, TPG, NORM, MODE>), dim3((unsigned)blocks),
+                       dim3(kGemvThreads), lds, s, a);
     if constexpr (MODE == kModeArgmax)
         hipLaunchKernelGGL(k_argmax_pick<0>, dim3(1), dim3(kPickThreads), 0, s, a.am_ws, blocks,
                            a.am_state, a.am_log, a.am_log_cap);
@@ -411,13 +541,9 @@ int launch_qgemv_mode(const GemvArgs& a, hipStream_t s) {
     Shape sh;
     if (!pick_shape(a.k / 32, sh)) return PE_ERR_SHAPE;
     switch (sh.gs * 16 + sh.upl) {
-        case 32 * 16 + 1: launch_qgemv_shape<T, 32, 1, NORM, MODE>(a, s); break;
-        case 64 * 16 + 1: launch_qgemv_shape<T, 64, 1, NORM, MODE>(a, s); break;
-        case 64 * 16 + 2: launch_qgemv_shape<T, 64, 2, NORM, MODE>(a, s); break;
-        case 64 * 16 + 3: launch_qgemv_shape<T, 64, 3, NORM, MODE>(a, s); break;
-        case 64 * 16 + 4: launch_qgemv_shape<T, 64, 4, NORM, MODE>(a, s); break;
-        case 256 * 16 + 3: launch_qgemv_shape<T, 256, 3, NORM, MODE>(a, s); break;
-        case 256 * 16 + 4: launch_qgemv_shape<T, 256, 4, NORM, MODE>(a, s); break;
+#define PE_CASE(G, U) case G * 16 + U: launch_qgemv_shape<T, G, U, NORM, MODE>(a, s); break;
+        PE_SHAPE_CASES(PE_CASE)
+#undef PE_CASE
         default: return PE_ERR_SHAPE;
     }
     return launch_status();
@@ -450,12 +576,16 @@ __global__ __launch_bounds__(256) void k_qgemm(GemmArgs a) {
     const int units = (int)(a.k >> 5);
     const int64_t m0 = (int64_t)blockIdx.y * kGemmMT;
     const int64_t stride = (int64_t)gridDim.x * GPB;
-    for (int64_t row = (int64_t)blockIdx.x * GPB + gid; row < a.n; row += stride) {
+    // the loop runs the same number of times in every group of the block (gsum may synchronise
+    // the block); rows past n are computed as zero and not stored
+    for (int64_t r0 = (int64_t)blockIdx.x * GPB; r0 < a.n; r0 += stride) {
+        const int64_t row = r0 + gid;
+        const bool live = row < a.n;
         float w[UPL][32];
 #pragma unroll
         for (int t = 0; t < UPL; ++t) {
             const int u = glane + GS * t;
-            if (u < units) {
+            if (live && u < units) {
                 typename Fmt<T>::Raw r;
                 Fmt<T>::load(a.w, row, u, r);
                 Fmt<T>::dequant(r, w[t]);
@@ -477,14 +607,14 @@ __global__ __launch_bounds__(256) void k_qgemm(GemmArgs a) {
                         float xv[32];
                         load_x_unit(a.x + m * a.x_stride, u, xv);
 #pragma unroll
-                        for (int i = 0; i < 32; ++i) acc[mm] += w[t][i] * xv[i];
+                        for (int i = 0; i < 32; ++i) acc[mm] = fmaf(w[t][i], xv[i], acc[mm]);
                     }
                 }
             }
         }
 #pragma unroll
         for (int mm = 0; mm < kGemmMT; ++mm) acc[mm] = gsum<GS>(acc[mm], lds4);
-        if (glane == 0) {
+        if (glane == 0 && live) {
 #pragma unroll
             for (int mm = 0; mm < kGemmMT; ++mm) {
                 const int64_t m = m0 + mm;
@@ -503,7 +633,7 @@ template <int T, int GS, int UPL>
 void launch_qgemm_shape(const GemmArgs& a, hipStream_t s) {
     constexpr int GPB = 256 / GS;
     int64_t bx = (a.n + GPB - 1) / GPB;
-    if (bx > kMaxGemvBlocks) bx = kMaxGemvBlocks;
+    if (bx > kMaxGemmBlocks) bx = kMaxGemmBlocks;
     const int64_t by = (a.m + kGemmMT - 1) / kGemmMT;
     hipLaunchKernelGGL((k_qgemm<T, GS, UPL>), dim3((unsigned)bx, (unsigned)by), dim3(256), 0, s, a);
 }
@@ -513,13 +643,9 @@ int launch_qgemm(const GemmArgs& a, hipStream_t s) {
     Shape sh;
     if (!pick_shape(a.k / 32, sh)) return PE_ERR_SHAPE;
     switch (sh.gs * 16 + sh.upl) {
-        case 32 * 16 + 1: launch_qgemm_shape<T, 32, 1>(a, s); break;
-        case 64 * 16 + 1: launch_qgemm_shape<T, 64, 1>(a, s); break;
-        case 64 * 16 + 2: launch_qgemm_shape<T, 64, 2>(a, s); break;
-        case 64 * 16 + 3: launch_qgemm_shape<T, 64, 3>(a, s); break;
-        case 64 * 16 + 4: launch_qgemm_shape<T, 64, 4>(a, s); break;
-        case 256 * 16 + 3: launch_qgemm_shape<T, 256, 3>(a, s); break;
-        case 256 * 16 + 4: launch_qgemm_shape<T, 256, 4>(a, s); break;
+#define PE_CASE(G, U) case G * 16 + U: launch_qgemm_shape<T, G, U>(a, s); break;
+        PE_SHAPE_CASES(PE_CASE)
+#undef PE_CASE
         default: return PE_ERR_SHAPE;
     }
     return launch_status();

@@ -123,10 +123,10 @@ PE_DEV float fbyte(uint32_t w, int b) { return (float)((w >> (8 * b)) & 0xFFu); 
 
 // Sum over the four bytes of `codes` (unsigned) times x[0..3].
 PE_DEV float dot4(uint32_t codes, const float* x, float acc) {
-    acc += fbyte(codes, 0) * x[0];
-    acc += fbyte(codes, 1) * x[1];
-    acc += fbyte(codes, 2) * x[2];
-    acc += fbyte(codes, 3) * x[3];
+    acc = fmaf(fbyte(codes, 0), x[0], acc);
+    acc = fmaf(fbyte(codes, 1), x[1], acc);
+    acc = fmaf(fbyte(codes, 2), x[2], acc);
+    acc = fmaf(fbyte(codes, 3), x[3], acc);
     return acc;
 }
 
@@ -185,7 +185,7 @@ struct Fmt<PE_TYPE_Q8_0> {
 #pragma unroll
         for (int w = 0; w < 8; ++w)
             acc = dot4(word_of(w < 4 ? r.a : r.b, w & 3) ^ 0x80808080u, x + 4 * w, acc);
-        return (acc - 128.f * xs.all) * h2f(r.d);
+        return fmaf(-128.f, xs.all, acc) * h2f(r.d);
     }
     static PE_DEV void dequant(const Raw& r, float* w) {
         const float d = h2f(r.d);
@@ -229,7 +229,7 @@ struct Fmt<PE_TYPE_Q5_0> {
             acc = dot4(lo, x + 4 * w, acc);
             acc = dot4(hi, x + 16 + 4 * w, acc);
         }
-        return (acc - 16.f * xs.all) * h2f(r.d);
+        return fmaf(-16.f, xs.all, acc) * h2f(r.d);
     }
     static PE_DEV void dequant(const Raw& r, float* w) {
         const float d = h2f(r.d);
@@ -280,13 +280,13 @@ struct Fmt<PE_TYPE_Q4_K> {
 #pragma unroll
         for (int w = 0; w < 8; ++w)
             dq = dot4((word_of(w < 4 ? r.lo : r.hi, w & 3) >> sh) & 0x0F0F0F0Fu, x + 4 * w, dq);
-        return a * dq - m * xs.all;
+        return fmaf(a, dq, -(m * xs.all));
     }
     static PE_DEV void dequant(const Raw& r, float* w) {
         float a, m;
         scales(r, a, m);
 #pragma unroll
-        for (int i = 0; i < 32; ++i) w[i] = a * (float)nib(r, i) - m;  // exact product, one rounding
+        for (int i = 0; i < 32; ++i) w[i] = fmaf(a, (float)nib(r, i), -m);  // exact product, one rounding
     }
 };
 
@@ -338,8 +338,8 @@ struct Fmt<PE_TYPE_Q6_K> {
             if (w < 4) p0 = dot4(c, x + 4 * w, p0);
             else p1 = dot4(c, x + 4 * w, p1);
         }
-        return h2f(r.d) * ((float)sext8(r.sc, 0) * (p0 - 32.f * xs.lo) +
-                           (float)sext8(r.sc, 1) * (p1 - 32.f * (xs.all - xs.lo)));
+        const float h0 = fmaf(-32.f, xs.lo, p0), h1 = fmaf(-32.f, xs.all - xs.lo, p1);
+        return h2f(r.d) * fmaf((float)sext8(r.sc, 0), h0, (float)sext8(r.sc, 1) * h1);
     }
     static PE_DEV void dequant(const Raw& r, float* w) {
         const float d = h2f(r.d);

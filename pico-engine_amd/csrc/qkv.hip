@@ -182,13 +182,9 @@ extern "C" int pe_qkv_rmsnorm_rope(const pe_qkv_args* args, pe_stream_t stream) 
     if (a.layout & ~PE_LAYOUT_X_UT) return PE_ERR_TYPE;
     const size_t lds = (a.layout & PE_LAYOUT_X_UT) ? 0 : stage_lds_bytes(a.hidden, a.norm_w != nullptr);
     switch (sh.gs * 16 + sh.upl) {
-        case 32 * 16 + 1: hipLaunchKernelGGL((k_qkv<32, 1>), g, b, lds, s, P); break;
-        case 64 * 16 + 1: hipLaunchKernelGGL((k_qkv<64, 1>), g, b, lds, s, P); break;
-        case 64 * 16 + 2: hipLaunchKernelGGL((k_qkv<64, 2>), g, b, lds, s, P); break;
-        case 64 * 16 + 3: hipLaunchKernelGGL((k_qkv<64, 3>), g, b, lds, s, P); break;
-        case 64 * 16 + 4: hipLaunchKernelGGL((k_qkv<64, 4>), g, b, lds, s, P); break;
-        case 256 * 16 + 3: hipLaunchKernelGGL((k_qkv<256, 3>), g, b, lds, s, P); break;
-        case 256 * 16 + 4: hipLaunchKernelGGL((k_qkv<256, 4>), g, b, lds, s, P); break;
+#define PE_CASE(G, U) case G * 16 + U: hipLaunchKernelGGL((k_qkv<G, U>), g, b, lds, s, P); break;
+        PE_SHAPE_CASES(PE_CASE)
+#undef PE_CASE
         default: return PE_ERR_SHAPE;
     }
     return launch_status();

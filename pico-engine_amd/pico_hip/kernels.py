@@ -21,7 +21,8 @@ from dataclasses import dataclass
 
 import torch
 
-from ._lib import LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT, QkvArgs, check, lib
+from ._lib import (LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT, AttnBlockArgs, QkvArgs, check,
+                   lib)
 from .dequant import (BLOCK_SIZE, GGML_Q4_K, GGML_Q5_0, GGML_Q6_K, GGML_Q8_0, QUANT_TYPES,
                       TYPE_NAMES, nbytes_for)
 
@@ -389,6 +390,59 @@ def qkv_rmsnorm_rope(x: torch.Tensor, norm_w: torch.Tensor | None, eps: float,
     return out
 
 
+def attn_block_workspace(hidden: int, n_head: int, n_kv: int, hd: int, capacity: int,
+                         device) -> torch.Tensor | None:
+    """Zero-filled workspace of ``attn_block`` for these shapes, or None when the fused block
+    does not support them (then the model runs qkv_rmsnorm_rope + decode_attn + qgemv)."""
+    nbytes = lib.pe_attn_block_workspace_bytes(hidden, n_head, n_kv, hd, capacity)
+    if nbytes < 0:
+        return None
+    return torch.zeros(nbytes, dtype=torch.uint8, device=device)
+
+
+def attn_block_failed(workspace: torch.Tensor) -> bool:
+    """True when an internal wait of an attn_block launch on this workspace ran out (its first
+    word); results since then are invalid until the workspace is zero-filled again."""
+    return bool(workspace[:4].view(torch.int32).item() != 0)
+
+
+def attn_block(x: torch.Tensor, norm_w: torch.Tensor, eps: float,
+               wq: QWeight, wk: QWeight, wv: QWeight, wo: QWeight,
+               bq: torch.Tensor | None, bk: torch.Tensor | None, bv: torch.Tensor | None,
+               cos_tab: torch.Tensor, sin_tab: torch.Tensor, pos: torch.Tensor,
+               k_cache: torch.Tensor, v_cache: torch.Tensor, n_head: int, workspace: torch.Tensor,
+               scale: float | None = None, round_fp16: bool = True,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """The attention block of one decode token in one launch: returns
+    x + Wo attn(RoPE(Wq h + bq), cache) with h = rmsnorm(x) * norm_w, after writing
+    RoPE(Wk h + bk) and Wv h + bv into the caches at ``pos`` (device int64 scalar).
+    Same result as qkv_rmsnorm_rope, decode_attn (fp16-rounded output) and qgemv with the
+    residual (model.py:175-213)."""
+    dev = _on_gpu(x, norm_w, wq.data, wk.data, wv.data, wo.data, pos, k_cache, v_cache, workspace)
+    n_kv, capacity, hd = k_cache.shape
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("KV caches must be contiguous (n_kv, capacity, hd) buffers")
+    if pos.dtype != torch.int64:
+        raise ValueError("pos must be an int64 device tensor")
+    x = _f32c(x.reshape(-1))
+    nw = _f32c(norm_w.reshape(-1))
+    if out is None:
+        out = torch.empty_like(x)
+    if scale is None:
+        scale = 1.0 / float(hd) ** 0.5
+    a = AttnBlockArgs(wq.ggml_type, wk.ggml_type, wv.ggml_type, wo.ggml_type,
+                      wq.data.data_ptr(), wk.data.data_ptr(), wv.data.data_ptr(), wo.data.data_ptr(),
+                      None if bq is None else bq.data_ptr(), None if bk is None else bk.data_ptr(),
+                      None if bv is None else bv.data_ptr(),
+                      x.data_ptr(), nw.data_ptr(), float(eps),
+                      cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
+                      pos.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), capacity,
+                      out.data_ptr(), x.numel(), n_head, n_kv, hd, float(scale), int(round_fp16))
+    check(lib.pe_attn_block(ctypes.byref(a), _ptr(workspace), workspace.numel(), _stream(dev)),
+          "pe_attn_block")
+    return out
+
+
 # ---- prefill (M >= 1) --------------------------------------------------------------------
 
 def qgemm(x: torch.Tensor, w: QWeight, bias: torch.Tensor | None = None,
@@ -446,5 +500,6 @@ def prefill_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
 __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "QWeight", "RawTensor", "dequantize", "pack_weight", "dequantize_weight", "embed_gather",
            "rmsnorm", "rope", "silu_mul", "decode_attn", "decode_attn_workspace", "qgemv",
            "q8_0_gemv", "q5_0_gemv", "q5_0_gemv_norm", "q6_k_gemv", "q4_k_gemv", "qgemv_norm",
-           "qgemv_norm_silu", "qkv_rmsnorm_rope", "qgemm", "kv_write", "prefill_attn",
+           "qgemv_norm_silu", "qkv_rmsnorm_rope", "attn_block", "attn_block_workspace",
+           "attn_block_failed", "qgemm", "kv_write", "prefill_attn",
            "BLOCK_SIZE"]

@@ -2,16 +2,20 @@
 
 ``ModelConfig`` and ``Transformer(cfg, weights, device, quant).forward(token_ids, positions,
 cache) -> logits`` keep the reference's signatures (model.py:27-57, :60-62, :128-165).
-Decode (one token) runs five fused HIP launches per layer plus two per token:
+Decode (one token) runs three fused HIP launches per layer plus two per token when the
+attention block fits one launch (short caches, the 0.5B family):
 
   embed_gather                              model.py:152 (Q8_0 row, bit-exact)
   per layer:
-    qkv_rmsnorm_rope   (norm+QKV+bias+RoPE+cache write)   model.py:175-193
-    decode_attn        (split-KV GQA, fp16-rounded out)   model.py:211
-    qgemv + residual   (o-projection)                     model.py:213
+    attn_block         (norm+QKV+bias+RoPE+cache write    model.py:175-213
+                        + GQA attention, fp16-rounded
+                        + o-projection + residual)
     qgemv_norm_silu    (norm+gate/up+SiLU*up)             model.py:216-224
     qgemv + residual   (ffn_down)                         model.py:225-234
   qgemv_norm           (final norm + LM head)             model.py:159-164
+
+Otherwise the attention block is three launches: qkv_rmsnorm_rope (model.py:175-193),
+decode_attn (split-KV GQA, model.py:211) and qgemv + residual (o-projection, model.py:213).
 
 Prefill (L > 1) follows the reference's L > 1 branch op for op in fp32 (its off-CUDA numerics):
 rmsnorm, one small-M GEMM per QKV segment with bias, RoPE, cache write at [0, L), causal
@@ -83,6 +87,10 @@ class Transformer:
         self.layers = [self._layer_weights(i) for i in range(cfg.n_layers)]
         self.output_norm_ut = K.to_ut(self.w["output_norm.weight"])
         self._ws: dict[int, torch.Tensor] = {}
+        self._block_ws: torch.Tensor | None = None
+        # one-launch attention block for short caches (attn_block); off by default until it is
+        # faster than the three-launch block on the decode step
+        self.use_attn_block = False
 
     def _layer_weights(self, i: int) -> Layer:
         p, q, w = f"blk.{i}.", self.quant, self.w
@@ -120,6 +128,27 @@ class Transformer:
             self._ws[capacity] = ws
         return ws
 
+    def block_workspace(self, capacity: int) -> torch.Tensor | None:
+        """Workspace of the one-launch attention block (shared by every layer and call, since
+        launches run in order), or None when it does not support these shapes/capacity."""
+        if not self.use_attn_block:
+            return None
+        c = self.cfg
+        probe = K.lib.pe_attn_block_workspace_bytes(c.hidden, c.n_head, c.n_kv_head, c.head_dim,
+                                                    capacity)
+        if probe < 0:
+            return None
+        if self._block_ws is None:
+            self._block_ws = K.attn_block_workspace(c.hidden, c.n_head, c.n_kv_head, c.head_dim,
+                                                    capacity, self.device)
+        return self._block_ws
+
+    def check_device_errors(self) -> None:
+        """Raise if a bounded device-side wait ran out since the workspace was made."""
+        if self._block_ws is not None and K.attn_block_failed(self._block_ws):
+            raise RuntimeError("pe_attn_block: an internal wait ran out; results are invalid "
+                               "(workspace must be zero-filled again)")
+
     @torch.inference_mode()
     def forward(self, token_ids: torch.Tensor, positions: torch.Tensor,
                 cache: list[tuple[torch.Tensor, torch.Tensor]],
@@ -148,6 +177,9 @@ class Transformer:
         if pos.dtype != torch.int64:
             pos = pos.to(torch.int64)
         capacity = cache[0][0].shape[1]
+        block_ws = self.block_workspace(capacity)
+        if block_ws is not None:
+            return self._decode_fused(token_ids, pos, cache, greedy, block_ws)
         ws = self.attn_workspace(capacity)
         x = K.embed_gather(self.embed, token_ids, layout=YU).reshape(-1)
         for i, L in enumerate(self.layers):
@@ -165,6 +197,23 @@ class Transformer:
                 act = K.silu_mul(torch.cat([g, u]).unsqueeze(0), cfg.ffn_dim).reshape(-1)
                 x = K.qgemv(act, L.w_down, residual=x, layout=YU)
         return self._lm_head(x, self.output_norm_ut, greedy, XU)
+
+    def _decode_fused(self, token_ids, pos, cache, greedy, block_ws):
+        """One token with the one-launch attention block; vectors in the natural layout."""
+        cfg = self.cfg
+        x = K.embed_gather(self.embed, token_ids).reshape(-1)
+        for i, L in enumerate(self.layers):
+            k_buf, v_buf = cache[i]
+            x = K.attn_block(x, L.attn_norm, cfg.eps, L.wq, L.wk, L.wv, L.wo, L.bq, L.bk, L.bv,
+                             self.cos, self.sin, pos, k_buf, v_buf, cfg.n_head, block_ws)
+            if L.w_gate_up is not None:
+                act = K.qgemv_norm_silu(x, L.ffn_norm, L.w_gate_up, cfg.eps)
+            else:
+                g = K.qgemv_norm(x, L.ffn_norm, L.w_gate, cfg.eps)
+                u = K.qgemv_norm(x, L.ffn_norm, L.w_up, cfg.eps)
+                act = K.silu_mul(torch.cat([g, u]).unsqueeze(0), cfg.ffn_dim).reshape(-1)
+            x = K.qgemv(act, L.w_down, residual=x)
+        return self._lm_head(x, self.w["output_norm.weight"], greedy, K.LAYOUT_NATURAL)
 
     # ---- prefill --------------------------------------------------------------------------
     def _prefill(self, token_ids, positions, cache, greedy=None):
