@@ -238,6 +238,54 @@ int64_t pe_attn_block_workspace_bytes(int64_t hidden, int n_head, int n_kv, int 
 int pe_attn_block(const pe_attn_block_args* args, void* workspace, int64_t workspace_bytes,
                   pe_stream_t stream);
 
+/* Attention block of one decode token with one workgroup per query head and no communication
+ * between workgroups (short caches). For every query head h:
+ *   hn = rmsnorm(x) * norm_w;  q_h = RoPE(Wq[h] hn + bq[h]);  k, v of kv head h / (n_head/n_kv)
+ *   = RoPE(Wk hn + bk), Wv hn + bv (the first query head of each kv head writes them into cache
+ *   row *pos);  a_h = softmax(q_h . K[0..*pos] * scale) V[0..*pos], rounded to fp16 when
+ *   round_fp16;  partials[h][r] = sum_d Wo[r][h*hd + d] a_h[d] for r < hidden.
+ * The o-projection output is x + sum_h partials[h] (pe_qgemv_sum_rmsnorm_silu adds it).
+ * Replaces, per layer, model.py:175-213: rmsnorm + F.linear qkv + rope + index_copy_
+ * (model.py:175-193), decode_attn (model.py:211, kernels.py:129) and the o-projection addmm
+ * (model.py:213). Limits: head_dim 64, hidden % 32 == 0 and hidden <= 1024, capacity <= 1024;
+ * format combinations: q,k,o Q5_0 with v Q5_0 or Q8_0, or all Q8_0
+ * (pe_attn_head_supported tells, PE_ERR_TYPE / PE_ERR_SHAPE otherwise: then use
+ * pe_qkv_rmsnorm_rope + pe_decode_attn + pe_qgemv). An out-of-range *pos writes nothing to
+ * the cache and NaN partials. Vectors in the natural layout. */
+typedef struct pe_attn_head_args {
+    int type_q, type_k, type_v, type_o;  /* ggml types of the tiled weights */
+    const void *w_q, *w_k, *w_v, *w_o;   /* (n_head*hd x hidden), (n_kv*hd x hidden) x2, (hidden x n_head*hd) */
+    const float *b_q, *b_k, *b_v;        /* biases or NULL */
+    const float* x;                      /* (hidden) residual stream */
+    const float* norm_w;                 /* (hidden) attn_norm weight */
+    float eps;
+    const float* cos_tab;                /* (rope_rows, hd/2) */
+    const float* sin_tab;
+    int64_t rope_rows;
+    const int64_t* pos;                  /* device scalar: position of this token */
+    float* k_cache;                      /* (n_kv, capacity, hd) */
+    float* v_cache;
+    int64_t capacity;
+    float* partials;                     /* (n_head, hidden) per-head o-projection shares */
+    int64_t hidden;
+    int n_head, n_kv, head_dim;
+    float scale;
+    int round_fp16;
+} pe_attn_head_args;
+int pe_attn_head_supported(int type_q, int type_k, int type_v, int type_o, int64_t hidden,
+                           int n_head, int n_kv, int head_dim, int64_t capacity);
+int pe_attn_head(const pe_attn_head_args* args, pe_stream_t stream);
+
+/* pe_qgemv_rmsnorm_silu of x_sum = x + parts[0] + ... + parts[n_parts-1] (added in that order),
+ * the parts stored back to back (part i at parts + i*k); block 0 also stores x_sum (if not
+ * NULL) for the next residual. n_parts <= 16, natural layout, k <= 8192.
+ * Replaces the residual add of the o-projection (model.py:213, after pe_attn_head) fused with
+ * rmsnorm + gate/up + silu_mul (model.py:216-224). */
+int pe_qgemv_sum_rmsnorm_silu(int ggml_type, const void* w_tiled, int64_t ffn, int64_t k,
+                              const float* x, const float* parts, int n_parts,
+                              const float* norm_w, float eps, float* act, float* x_sum,
+                              pe_stream_t stream);
+
 /* ---- general / prefill (M >= 1) kernels ------------------------------------------------ */
 
 /* y[r][:] = rmsnorm(x[r][:]) * w for r < rows (row strides in elements).

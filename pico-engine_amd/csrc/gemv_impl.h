@@ -14,7 +14,8 @@
 
 namespace pe {
 
-enum { kModePlain = 0, kModeSilu = 1, kModeArgmax = 2 };
+// kModeSiluSum: kModeSilu whose staged activation is x + sum of parts (GemvArgs::parts)
+enum { kModePlain = 0, kModeSilu = 1, kModeArgmax = 2, kModeSiluSum = 3 };
 
 struct GemvArgs {
     Tiled w;
@@ -34,7 +35,14 @@ struct GemvArgs {
     int64_t* am_state;
     int64_t* am_log;
     int64_t am_log_cap;
+    // staged activation = x + parts[0] + ... + parts[n_parts-1] (natural layout); block 0
+    // stores that sum to x_sum when it is not NULL
+    const float* parts;
+    int n_parts;
+    float* x_sum;
 };
+
+constexpr int kMaxParts = 16;
 
 constexpr int kArgmaxPartOff = 256;
 
@@ -330,7 +338,7 @@ PE_DEV float block_sum_nt(float v, float* lds) {
 // straight from global memory. With NORM the returned factor is rstd = 1 / sqrt(sum(x^2) / k +
 // eps) (kernels.py:21-23), applied by the caller after the dot product; otherwise 1.
 // Every thread of the block must call it.
-template <int NT, int GS, int UPL, bool NORM>
+template <int NT, int GS, int UPL, bool NORM, bool SUM = false>
 PE_DEV float stage_activation(const GemvArgs& a, int glane, int units, float (&xr)[UPL][32],
                               UnitSums (&xs)[UPL], float* lds4, float* stage) {
     const bool ut = a.layout & PE_LAYOUT_X_UT;
@@ -341,6 +349,23 @@ PE_DEV float stage_activation(const GemvArgs& a, int glane, int units, float (&x
             const int u = ut ? i % units : i >> 3;
             const int j = ut ? i / units : i & 7;
             float4 v = reinterpret_cast<const float4*>(a.x)[i];
+            if constexpr (SUM) {
+                // every part's load is issued before the first add (fixed order, no chain of
+                // dependent round trips)
+                float4 pv[kMaxParts];
+#pragma unroll
+                for (int pp = 0; pp < kMaxParts; ++pp)
+                    if (pp < a.n_parts) pv[pp] = reinterpret_cast<const float4*>(a.parts + (int64_t)pp * a.k)[i];
+#pragma unroll
+                for (int pp = 0; pp < kMaxParts; ++pp)
+                    if (pp < a.n_parts) {
+                        v.x += pv[pp].x;
+                        v.y += pv[pp].y;
+                        v.z += pv[pp].z;
+                        v.w += pv[pp].w;
+                    }
+                if (a.x_sum && blockIdx.x == 0) reinterpret_cast<float4*>(a.x_sum)[i] = v;
+            }
             if constexpr (NORM) {
                 const float4 w = reinterpret_cast<const float4*>(a.norm_w)[i];
                 ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
@@ -412,8 +437,9 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
     constexpr int NT = kGemvThreads;
     constexpr int G = NT / GS;
     constexpr int CH = G * TPG;
-    constexpr int R = (MODE == kModeSilu) ? 2 : 1;
-    constexpr bool kEpi = MODE != kModeSilu;
+    constexpr bool kSilu = MODE == kModeSilu || MODE == kModeSiluSum;
+    constexpr int R = kSilu ? 2 : 1;
+    constexpr bool kEpi = !kSilu;
     __shared__ float lds4[NT / 64];
     extern __shared__ float stage[];
     const int glane = threadIdx.x % GS;
@@ -438,7 +464,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
 
     float xr[UPL][32];
     UnitSums xs[UPL];
-    const float rstd = stage_activation<NT, GS, UPL, NORM>(a, glane, units, xr, xs, lds4, stage);
+    const float rstd =
+        stage_activation<NT, GS, UPL, NORM, MODE == kModeSiluSum>(a, glane, units, xr, xs, lds4, stage);
 
     uint64_t best = 0;  // argmax mode: best key of this group's tasks
     for (; chunk < nchunk; chunk += gridDim.x) {
@@ -463,7 +490,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
             for (int rr = 0; rr < R; ++rr) acc[i][rr] = gsum<GS>(acc[i][rr], lds4) * rstd;
             const int64_t task = c0 * CH + i * G + gid;
             if (glane == 0 && task < a.n_tasks) {
-                if constexpr (MODE == kModeSilu) {
+                if constexpr (kSilu) {
                     const float g = acc[i][0], u = acc[i][1];
                     a.y[out_index(a, task)] = (g * (1.0f / (1.0f + expf(-g)))) * u;
                 } else {
@@ -514,12 +541,17 @@ constexpr int kMaxGemmBlocks = 2048;   // prefill GEMM
 template <int MODE>
 constexpr int tasks_per_group() { return MODE == kModeArgmax ? 4 : 1; }
 
+// Grid cap of a launch: the LM-head argmax runs at most 2048 blocks (each loops over several
+// chunks with the next chunk's loads in flight, so the activation is staged fewer times).
+template <int MODE>
+constexpr int max_blocks() { return MODE == kModeArgmax ? 2048 : kMaxGemvBlocks; }
+
 // Argmax-mode workspace: a key per block after a 256-byte head, sized for the smallest chunk
 // (one group of kGemvThreads lanes per block, tasks_per_group rows), whatever k is.
 inline int64_t argmax_ws_bytes(int64_t n_rows) {
     const int64_t per_block = tasks_per_group<kModeArgmax>();
     const int64_t blocks = (n_rows + per_block - 1) / per_block;
-    return kArgmaxPartOff + 8 * (blocks < kMaxGemvBlocks ? blocks : kMaxGemvBlocks);
+    return kArgmaxPartOff + 8 * (blocks < max_blocks<kModeArgmax>() ? blocks : max_blocks<kModeArgmax>());
 }
 
 template <int T, int GS, int UPL, bool NORM, int MODE>
@@ -527,7 +559,7 @@ void launch_qgemv_shape(const GemvArgs& a, hipStream_t s) {
     constexpr int TPG = tasks_per_group<MODE>();
     constexpr int CH = (kGemvThreads / GS) * TPG;
     int64_t blocks = (a.n_tasks + CH - 1) / CH;
-    if (blocks > kMaxGemvBlocks) blocks = kMaxGemvBlocks;
+    if (blocks > max_blocks<MODE>()) blocks = max_blocks<MODE>();
     const size_t lds = a.k <= kStageMaxK ? (size_t)(a.k / 32) * kUnitStride * 4 : 0;
     hipLaunchKernelGGL((k_qgemv<T, GS, UPL, TPG, NORM, MODE>), dim3((unsigned)blocks),
                        dim3(kGemvThreads), lds, s, a);
@@ -657,6 +689,8 @@ int gemv_dispatch(const GemvArgs& a, bool norm, int mode, hipStream_t s) {
     if (mode == kModeSilu)
         return norm ? launch_qgemv_mode<T, true, kModeSilu>(a, s)
                     : launch_qgemv_mode<T, false, kModeSilu>(a, s);
+    if (mode == kModeSiluSum)
+        return norm && a.k <= kStageMaxK ? launch_qgemv_mode<T, true, kModeSiluSum>(a, s) : PE_ERR_SHAPE;
     if (mode == kModeArgmax)
         return norm ? launch_qgemv_mode<T, true, kModeArgmax>(a, s) : PE_ERR_NULL;
     return norm ? launch_qgemv_mode<T, true, kModePlain>(a, s)

@@ -21,8 +21,8 @@ from dataclasses import dataclass
 
 import torch
 
-from ._lib import (LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT, AttnBlockArgs, QkvArgs, check,
-                   lib)
+from ._lib import (LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT, AttnBlockArgs, AttnHeadArgs, QkvArgs,
+                   check, lib)
 from .dequant import (BLOCK_SIZE, GGML_Q4_K, GGML_Q5_0, GGML_Q6_K, GGML_Q8_0, QUANT_TYPES,
                       TYPE_NAMES, nbytes_for)
 
@@ -443,6 +443,70 @@ def attn_block(x: torch.Tensor, norm_w: torch.Tensor, eps: float,
     return out
 
 
+def attn_head_supported(wq: QWeight, wk: QWeight, wv: QWeight, wo: QWeight, hidden: int,
+                        n_head: int, n_kv: int, hd: int, capacity: int) -> bool:
+    """Whether attn_head covers these formats and shapes (else use the three-launch block)."""
+    return lib.pe_attn_head_supported(wq.ggml_type, wk.ggml_type, wv.ggml_type, wo.ggml_type,
+                                      hidden, n_head, n_kv, hd, capacity) == 0
+
+
+def attn_head(x: torch.Tensor, norm_w: torch.Tensor, eps: float,
+              wq: QWeight, wk: QWeight, wv: QWeight, wo: QWeight,
+              bq: torch.Tensor | None, bk: torch.Tensor | None, bv: torch.Tensor | None,
+              cos_tab: torch.Tensor, sin_tab: torch.Tensor, pos: torch.Tensor,
+              k_cache: torch.Tensor, v_cache: torch.Tensor, n_head: int,
+              scale: float | None = None, round_fp16: bool = True,
+              out: torch.Tensor | None = None) -> torch.Tensor:
+    """The attention block of one decode token, one workgroup per query head: returns the
+    per-head o-projection shares P (n_head, hidden) with x + P.sum(0) = x + Wo attn, after
+    writing RoPE(Wk h + bk) and Wv h + bv into the caches at ``pos`` (device int64 scalar);
+    h = rmsnorm(x) * norm_w, attn = decode attention (fp16-rounded) of RoPE(Wq h + bq)."""
+    dev = _on_gpu(x, norm_w, wq.data, wk.data, wv.data, wo.data, pos, k_cache, v_cache)
+    n_kv, capacity, hd = k_cache.shape
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("KV caches must be contiguous (n_kv, capacity, hd) buffers")
+    if pos.dtype != torch.int64:
+        raise ValueError("pos must be an int64 device tensor")
+    x = _f32c(x.reshape(-1))
+    nw = _f32c(norm_w.reshape(-1))
+    if out is None:
+        out = torch.empty(n_head, x.numel(), device=dev, dtype=torch.float32)
+    if scale is None:
+        scale = 1.0 / float(hd) ** 0.5
+    a = AttnHeadArgs(wq.ggml_type, wk.ggml_type, wv.ggml_type, wo.ggml_type,
+                     wq.data.data_ptr(), wk.data.data_ptr(), wv.data.data_ptr(), wo.data.data_ptr(),
+                     None if bq is None else bq.data_ptr(), None if bk is None else bk.data_ptr(),
+                     None if bv is None else bv.data_ptr(),
+                     x.data_ptr(), nw.data_ptr(), float(eps),
+                     cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
+                     pos.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), capacity,
+                     out.data_ptr(), x.numel(), n_head, n_kv, hd, float(scale), int(round_fp16))
+    check(lib.pe_attn_head(ctypes.byref(a), _stream(dev)), "pe_attn_head")
+    return out
+
+
+def qgemv_sum_norm_silu(x: torch.Tensor, parts: torch.Tensor, weight: torch.Tensor, w: QWeight,
+                        eps: float, out: torch.Tensor | None = None,
+                        x_sum: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(silu(g) * u, x_sum) with x_sum = x + parts.sum(0) (added in row order) and
+    [g; u] = W (rmsnorm(x_sum) * weight); parts (n, k) with n <= 16."""
+    dev = _on_gpu(x, parts, weight, w.data)
+    if w.n % 2:
+        raise ValueError("gate/up weight needs an even number of rows")
+    ffn = w.n // 2
+    x = _f32c(x.reshape(-1))
+    parts = _f32c(parts)
+    nw = _f32c(weight.reshape(-1))
+    if out is None:
+        out = torch.empty(ffn, device=dev, dtype=torch.float32)
+    if x_sum is None:
+        x_sum = torch.empty_like(x)
+    check(lib.pe_qgemv_sum_rmsnorm_silu(w.ggml_type, _ptr(w.data), ffn, w.k, _ptr(x), _ptr(parts),
+                                        parts.shape[0], _ptr(nw), float(eps), _ptr(out), _ptr(x_sum),
+                                        _stream(dev)), "pe_qgemv_sum_rmsnorm_silu")
+    return out, x_sum
+
+
 # ---- prefill (M >= 1) --------------------------------------------------------------------
 
 def qgemm(x: torch.Tensor, w: QWeight, bias: torch.Tensor | None = None,
@@ -501,5 +565,5 @@ __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "
            "rmsnorm", "rope", "silu_mul", "decode_attn", "decode_attn_workspace", "qgemv",
            "q8_0_gemv", "q5_0_gemv", "q5_0_gemv_norm", "q6_k_gemv", "q4_k_gemv", "qgemv_norm",
            "qgemv_norm_silu", "qkv_rmsnorm_rope", "attn_block", "attn_block_workspace",
-           "attn_block_failed", "qgemm", "kv_write", "prefill_attn",
+           "attn_block_failed", "attn_head", "attn_head_supported", "qgemv_sum_norm_silu", "qgemm", "kv_write", "prefill_attn",
            "BLOCK_SIZE"]

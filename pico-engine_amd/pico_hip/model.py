@@ -91,6 +91,10 @@ class Transformer:
         # one-launch attention block for short caches (attn_block); off by default until it is
         # faster than the three-launch block on the decode step
         self.use_attn_block = False
+        # one workgroup per query head for the whole attention block (attn_head), when every
+        # layer's formats and the cache capacity are supported; off by default until it is
+        # faster than the three-launch block
+        self.use_attn_head = False
 
     def _layer_weights(self, i: int) -> Layer:
         p, q, w = f"blk.{i}.", self.quant, self.w
@@ -177,6 +181,8 @@ class Transformer:
         if pos.dtype != torch.int64:
             pos = pos.to(torch.int64)
         capacity = cache[0][0].shape[1]
+        if self.use_attn_head and self._head_ok(capacity):
+            return self._decode_heads(token_ids, pos, cache, greedy)
         block_ws = self.block_workspace(capacity)
         if block_ws is not None:
             return self._decode_fused(token_ids, pos, cache, greedy, block_ws)
@@ -197,6 +203,25 @@ class Transformer:
                 act = K.silu_mul(torch.cat([g, u]).unsqueeze(0), cfg.ffn_dim).reshape(-1)
                 x = K.qgemv(act, L.w_down, residual=x, layout=YU)
         return self._lm_head(x, self.output_norm_ut, greedy, XU)
+
+    def _head_ok(self, capacity: int) -> bool:
+        c = self.cfg
+        return all(L.w_gate_up is not None and
+                   K.attn_head_supported(L.wq, L.wk, L.wv, L.wo, c.hidden, c.n_head, c.n_kv_head,
+                                         c.head_dim, capacity) for L in self.layers)
+
+    def _decode_heads(self, token_ids, pos, cache, greedy):
+        """One token, three launches per layer: attn_head (per-head o-projection shares),
+        the gate/up GEMV that adds them to the residual, and ffn_down with that residual."""
+        cfg = self.cfg
+        x = K.embed_gather(self.embed, token_ids).reshape(-1)
+        for i, L in enumerate(self.layers):
+            k_buf, v_buf = cache[i]
+            parts = K.attn_head(x, L.attn_norm, cfg.eps, L.wq, L.wk, L.wv, L.wo, L.bq, L.bk, L.bv,
+                                self.cos, self.sin, pos, k_buf, v_buf, cfg.n_head)
+            act, x_mid = K.qgemv_sum_norm_silu(x, parts, L.ffn_norm, L.w_gate_up, cfg.eps)
+            x = K.qgemv(act, L.w_down, residual=x_mid)
+        return self._lm_head(x, self.w["output_norm.weight"], greedy, K.LAYOUT_NATURAL)
 
     def _decode_fused(self, token_ids, pos, cache, greedy, block_ws):
         """One token with the one-launch attention block; vectors in the natural layout."""

@@ -49,7 +49,7 @@ def test_nbytes_and_workspace(lib):
     assert ws == 256 + 2 * 2 * 7 * 66 * 4
     assert lib.pe_decode_attn_workspace_bytes(14, 3, 64, 77) == -3   # 14 % 3
     assert lib.pe_decode_attn_workspace_bytes(14, 2, 96, 77) == -3   # head_dim
-    assert lib.pe_qgemv_argmax_workspace_bytes(151936) == 256 + 8 * 8192
+    assert lib.pe_qgemv_argmax_workspace_bytes(151936) == 256 + 8 * 2048   # grid cap
     assert lib.pe_qgemv_argmax_workspace_bytes(100) == 256 + 8 * 25   # a key per 4-row block
     assert lib.pe_qgemv_argmax_workspace_bytes(0) == -3
 

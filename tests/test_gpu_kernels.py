@@ -634,3 +634,99 @@ def test_attn_block_shape_limits(K):
     assert K.attn_block_workspace(896, 14, 2, 64, 257, DEV) is None     # 512 / n_kv positions
     assert K.attn_block_workspace(3584, 28, 4, 128, 128, DEV) is None   # head_dim 128
     assert K.attn_block_workspace(2048, 32, 8, 64, 64, DEV) is None     # > 32 units per row
+
+
+# ---- per-head attention block (attn_head) + partial-sum gate/up ---------------------------
+
+HEAD_CASES = [
+    ((dq.Q5_0, dq.Q5_0, dq.Q8_0, dq.Q5_0), 896, 14, 2, 77),     # config 0, even layer
+    ((dq.Q5_0, dq.Q5_0, dq.Q5_0, dq.Q5_0), 896, 14, 2, 1024),   # odd layer, largest cache
+    ((dq.Q8_0, dq.Q8_0, dq.Q8_0, dq.Q8_0), 256, 4, 4, 40),      # no GQA sharing
+    ((dq.Q5_0, dq.Q5_0, dq.Q8_0, dq.Q5_0), 512, 8, 1, 300),     # MQA: all heads share one kv head
+]
+
+
+@pytest.mark.parametrize("types,hidden,nh,nkv,cap", HEAD_CASES,
+                         ids=[f"{h}-{nh}x{nkv}-cap{cap}" for _, h, nh, nkv, cap in HEAD_CASES])
+def test_attn_head_matches_closed_form_over_steps(K, types, hidden, nh, nkv, cap):
+    """x + sum_h partials[h] and the new cache rows match the float64 closed form of
+    model.py:175-213 step after step (first, second, middle and last cache rows)."""
+    c = _block_case(K, types, hidden, nh, nkv, cap, seed=hidden + cap + 1)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    assert K.attn_head_supported(*c["ws"], c["wo"], hidden, nh, nkv, 64, cap)
+    kc_d, vc_d = T(c["kc"]), T(c["vc"])
+    kc_r, vc_r = c["kc"].astype(np.float64), c["vc"].astype(np.float64)
+    bq, bk, bv = (T(b) for b in c["bs"])
+    steps = [0, 1, cap // 2, cap - 2, cap - 1]
+    for step, pos in enumerate(steps):
+        x = c["rng"].standard_normal(hidden).astype(np.float32)
+        parts = K.attn_head(T(x), T(c["nw"]), 1e-6, *c["ws"], c["wo"], bq, bk, bv, T(c["cos"]),
+                            T(c["sin"]), torch.tensor([pos], device=DEV), kc_d, vc_d, nh)
+        assert parts.shape == (nh, hidden)
+        y = x.astype(np.float64) + parts.cpu().numpy().astype(np.float64).sum(0)
+        ref = _block_ref(c, x, pos, kc_r, vc_r)
+        assert rel_err(y, ref) < TOL, f"step {step} pos {pos}"
+        assert rel_err(kc_d[:, pos].cpu().numpy(), kc_r[:, pos]) < TOL
+        assert rel_err(vc_d[:, pos].cpu().numpy(), vc_r[:, pos]) < TOL
+    untouched = [s for s in range(cap) if s not in steps]
+    np.testing.assert_array_equal(kc_d[:, untouched].cpu().numpy(), c["kc"][:, untouched])
+    np.testing.assert_array_equal(vc_d[:, untouched].cpu().numpy(), c["vc"][:, untouched])
+
+
+def test_attn_head_graph_replay_bad_position_and_support(K):
+    types, hidden, nh, nkv, cap = HEAD_CASES[0]
+    c = _block_case(K, types, hidden, nh, nkv, cap, seed=11)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    args = [T(c["nw"]), 1e-6, *c["ws"], c["wo"], *(T(b) for b in c["bs"]), T(c["cos"]), T(c["sin"])]
+    x = T(c["rng"].standard_normal(hidden).astype(np.float32))
+    kc_e, vc_e, kc_g, vc_g = T(c["kc"]), T(c["vc"]), T(c["kc"]), T(c["vc"])
+    pos_g = torch.tensor([5], device=DEV)
+    out_g = torch.empty(nh, hidden, device=DEV)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(g, stream=s):
+        K.attn_head(x, *args, pos_g, kc_g, vc_g, nh, out=out_g)
+    torch.cuda.current_stream().wait_stream(s)
+    for pos in range(5, 12):
+        pos_g.fill_(pos)
+        g.replay()
+        ye = K.attn_head(x, *args, torch.tensor([pos], device=DEV), kc_e, vc_e, nh)
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, ye), f"replay at pos {pos}"
+    assert torch.equal(kc_g, kc_e) and torch.equal(vc_g, vc_e)
+    before_k, before_v = kc_e.clone(), vc_e.clone()
+    bad = K.attn_head(x, *args, torch.tensor([cap], device=DEV), kc_e, vc_e, nh)
+    assert torch.isnan(bad).all()
+    assert torch.equal(kc_e, before_k) and torch.equal(vc_e, before_v)
+    # format / shape support
+    q4 = K.QWeight(c["ws"][0].data, dq.Q4_K, c["ws"][0].n, c["ws"][0].k)
+    assert not K.attn_head_supported(q4, *c["ws"][1:], c["wo"], hidden, nh, nkv, 64, cap)
+    assert not K.attn_head_supported(*c["ws"], c["wo"], hidden, nh, nkv, 64, 1025)
+    assert not K.attn_head_supported(*c["ws"], c["wo"], hidden, nh, nkv, 128, cap)
+
+
+def test_qgemv_sum_rmsnorm_silu(K):
+    """silu(g) * u of rmsnorm(x + sum of parts); the stored sum equals the float32 sum taken
+    in part order, bit for bit."""
+    t, k, ffn, n = dq.Q5_0, 896, 4864, 14
+    raw = quantized_normal(t, 2 * ffn, k, seed=31)
+    w = qweight(K, t, raw, 2 * ffn, k)
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal(k).astype(np.float32)
+    parts = (rng.standard_normal((n, k)) * 0.3).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    T = lambda a: torch.from_numpy(a).to(DEV)
+    act, xs = K.qgemv_sum_norm_silu(T(x), T(parts), T(nw), w, 1e-6)
+    want = x.copy()
+    for p in parts:
+        want = (want + p).astype(np.float32)
+    np.testing.assert_array_equal(xs.cpu().numpy(), want)
+    Wd = dequant_rows(t, raw, 2 * ffn, k)
+    h = closed.rmsnorm(want, nw, 1e-6)
+    ref = closed.silu_mul(closed.gemv(Wd[:ffn], h), closed.gemv(Wd[ffn:], h))
+    assert rel_err(act.cpu().numpy(), ref) < TOL
+    # no parts: the plain fused gate/up
+    plain = K.qgemv_norm_silu(T(want), T(nw), w, 1e-6)
+    act0, _ = K.qgemv_sum_norm_silu(T(want), T(parts[:0].copy()), T(nw), w, 1e-6)
+    assert torch.equal(plain, act0)
