@@ -286,6 +286,24 @@ int pe_qgemv_sum_rmsnorm_silu(int ggml_type, const void* w_tiled, int64_t ffn, i
                               const float* norm_w, float eps, float* act, float* x_sum,
                               pe_stream_t stream);
 
+/* Decode attention of every head fused with the o-projection (short caches), one launch:
+ *   a = decode_attn(q, k_cache, v_cache, S) as pe_decode_attn (GQA, scale, output rounded to
+ *       fp16 when round_fp16; S from len_dev/len_dtype/len_add as there);
+ *   y[r] = residual[r] + sum_k Wo[r][k] a[k]  (residual may be NULL), r < hidden.
+ * Every workgroup recomputes the attention of all heads on the matrix cores (fp32 MFMA) for
+ * its rows of Wo, so no second launch or cross-workgroup exchange is needed.
+ * Replaces decode_attn (model.py:211, kernels.py:129) + the o-projection addmm (model.py:213).
+ * Limits: head_dim 64, n_kv 1 or 2, n_head / n_kv <= 16, n_head * 64 <= 1024, capacity <= 256
+ * (pe_attn_oproj_supported tells; otherwise pe_decode_attn + pe_qgemv). Wo is a tiled
+ * (hidden x n_head*64) weight of wo_type. layout: PE_LAYOUT_Y_UT for residual and y.
+ * S == 0 gives NaN (as the reference). */
+int pe_attn_oproj_supported(int n_head, int n_kv, int head_dim, int64_t capacity, int wo_type,
+                            int64_t hidden);
+int pe_attn_oproj(const float* q, const float* k_cache, const float* v_cache, int n_head, int n_kv,
+                  int head_dim, int64_t capacity, const void* len_dev, int len_dtype,
+                  int64_t len_add, float scale, int round_fp16, int wo_type, const void* wo_tiled,
+                  int64_t hidden, const float* residual, float* y, int layout, pe_stream_t stream);
+
 /* ---- general / prefill (M >= 1) kernels ------------------------------------------------ */
 
 /* y[r][:] = rmsnorm(x[r][:]) * w for r < rows (row strides in elements).

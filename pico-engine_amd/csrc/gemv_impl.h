@@ -338,63 +338,53 @@ PE_DEV float block_sum_nt(float v, float* lds) {
 // straight from global memory. With NORM the returned factor is rstd = 1 / sqrt(sum(x^2) / k +
 // eps) (kernels.py:21-23), applied by the caller after the dot product; otherwise 1.
 // Every thread of the block must call it.
-template <int NT, int GS, int UPL, bool NORM, bool SUM = false>
-PE_DEV float stage_activation(const GemvArgs& a, int glane, int units, float (&xr)[UPL][32],
-                              UnitSums (&xs)[UPL], float* lds4, float* stage) {
+// Activation loads of one thread for the staged path, held in registers between the issue and
+// the LDS staging so that the weight loads can be issued in between: the staging then waits
+// only for these (vector loads retire in issue order), and the weights are still in flight
+// while the block stages x and reduces the RMSNorm sum.
+// A shape (GS, UPL) covers at most GS * UPL units of 8 float4s, i.e. act_loads<NT, GS, UPL>()
+// float4s per thread of an NT-thread block. Shapes for more than kStageMaxK weights per row
+// never stage (they read per lane), so they hold a single unused slot.
+template <int NT, int GS, int UPL>
+constexpr int act_loads() {
+    return GS * UPL * 32 > kStageMaxK ? 1 : (GS * UPL * 8 + NT - 1) / NT;
+}
+
+template <int M4>
+struct ActLoads {
+    float4 x[M4];
+    float4 w[M4];
+};
+
+// Issue the float4 loads of x (and the RMSNorm weight) that this thread stages. Indices past
+// the vector are clamped to its last float4 (no branch around the load, which would make the
+// compiler wait for the data right there); finish_activation ignores them.
+template <int NT, bool NORM, int M4>
+PE_DEV void issue_activation(const GemvArgs& a, int units, ActLoads<M4>& L) {
+    if (a.k > kStageMaxK || units * 8 > NT * M4) return;
+    const int n4 = units * 8;
+#pragma unroll
+    for (int m = 0; m < M4; ++m) {
+        const int i = (int)threadIdx.x + NT * m;
+        if (NT * m < n4) {
+            const int ic = i < n4 ? i : n4 - 1;
+            L.x[m] = reinterpret_cast<const float4*>(a.x)[ic];
+            if constexpr (NORM) L.w[m] = reinterpret_cast<const float4*>(a.norm_w)[ic];
+        }
+    }
+}
+
+// Stage the issued activation in LDS (units of 32 floats padded to kUnitStride), reduce the
+// RMSNorm sum over the block, and read this lane's units back. With NORM the units hold
+// x * norm_w and the returned factor is rstd = 1 / sqrt(sum(x^2) / k + eps) (kernels.py:21-23),
+// applied by the caller after the dot product; otherwise 1. Vectors longer than kStageMaxK
+// are read per lane straight from global memory. Every thread of the block must call it.
+// Unstaged path: each lane reads its own units of x (and norm_w) from global memory.
+template <int GS, int UPL, bool NORM>
+PE_DEV float direct_activation(const GemvArgs& a, int glane, int units, float (&xr)[UPL][32],
+                               UnitSums (&xs)[UPL], float* lds4) {
     const bool ut = a.layout & PE_LAYOUT_X_UT;
     float ss = 0.f;
-    if (a.k <= kStageMaxK) {
-        const int n4 = units * 8;
-        for (int i = threadIdx.x; i < n4; i += NT) {
-            const int u = ut ? i % units : i >> 3;
-            const int j = ut ? i / units : i & 7;
-            float4 v = reinterpret_cast<const float4*>(a.x)[i];
-            if constexpr (SUM) {
-                // every part's load is issued before the first add (fixed order, no chain of
-                // dependent round trips)
-                float4 pv[kMaxParts];
-#pragma unroll
-                for (int pp = 0; pp < kMaxParts; ++pp)
-                    if (pp < a.n_parts) pv[pp] = reinterpret_cast<const float4*>(a.parts + (int64_t)pp * a.k)[i];
-#pragma unroll
-                for (int pp = 0; pp < kMaxParts; ++pp)
-                    if (pp < a.n_parts) {
-                        v.x += pv[pp].x;
-                        v.y += pv[pp].y;
-                        v.z += pv[pp].z;
-                        v.w += pv[pp].w;
-                    }
-                if (a.x_sum && blockIdx.x == 0) reinterpret_cast<float4*>(a.x_sum)[i] = v;
-            }
-            if constexpr (NORM) {
-                const float4 w = reinterpret_cast<const float4*>(a.norm_w)[i];
-                ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
-                v.x *= w.x;
-                v.y *= w.y;
-                v.z *= w.z;
-                v.w *= w.w;
-            }
-            *reinterpret_cast<float4*>(stage + u * kUnitStride + 4 * j) = v;
-        }
-        float rstd = 1.0f;
-        if constexpr (NORM) rstd = 1.0f / sqrtf(block_sum_nt<NT>(ss, lds4) / (float)a.k + a.eps);
-        else __syncthreads();
-#pragma unroll
-        for (int t = 0; t < UPL; ++t) {
-            const int u = glane + GS * t;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (u < units) v = *reinterpret_cast<const float4*>(stage + u * kUnitStride + 4 * i);
-                xr[t][4 * i] = v.x;
-                xr[t][4 * i + 1] = v.y;
-                xr[t][4 * i + 2] = v.z;
-                xr[t][4 * i + 3] = v.w;
-            }
-            xs[t] = unit_sums(xr[t]);
-        }
-        return rstd;
-    }
 #pragma unroll
     for (int t = 0; t < UPL; ++t) {
         const int u = glane + GS * t;
@@ -424,12 +414,147 @@ PE_DEV float stage_activation(const GemvArgs& a, int glane, int units, float (&x
     return 1.0f;
 }
 
+template <int NT, int GS, int UPL, bool NORM, bool SUM = false>
+PE_DEV float finish_activation(const GemvArgs& a, int glane, int units,
+                               const ActLoads<act_loads<NT, GS, UPL>()>& L, float (&xr)[UPL][32],
+                               UnitSums (&xs)[UPL], float* lds4, float* stage) {
+    constexpr int M4 = act_loads<NT, GS, UPL>();
+    const bool ut = a.layout & PE_LAYOUT_X_UT;
+    float ss = 0.f;
+    if (a.k <= kStageMaxK && units * 8 <= NT * M4) {
+        const int n4 = units * 8;
+#pragma unroll
+        for (int m = 0; m < M4; ++m) {
+            const int i = (int)threadIdx.x + NT * m;
+            if (NT * m >= n4 || i >= n4) continue;
+            const int u = ut ? i % units : i >> 3;
+            const int j = ut ? i / units : i & 7;
+            float4 v = L.x[m];
+            if constexpr (SUM) {
+                // every part's load is issued before the first add (fixed order, no chain of
+                // dependent round trips)
+                float4 pv[kMaxParts];
+#pragma unroll
+                for (int pp = 0; pp < kMaxParts; ++pp)
+                    if (pp < a.n_parts) pv[pp] = reinterpret_cast<const float4*>(a.parts + (int64_t)pp * a.k)[i];
+#pragma unroll
+                for (int pp = 0; pp < kMaxParts; ++pp)
+                    if (pp < a.n_parts) {
+                        v.x += pv[pp].x;
+                        v.y += pv[pp].y;
+                        v.z += pv[pp].z;
+                        v.w += pv[pp].w;
+                    }
+                if (a.x_sum && blockIdx.x == 0) reinterpret_cast<float4*>(a.x_sum)[i] = v;
+            }
+            if constexpr (NORM) {
+                const float4 w = L.w[m];
+                ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
+                v.x *= w.x;
+                v.y *= w.y;
+                v.z *= w.z;
+                v.w *= w.w;
+            }
+            *reinterpret_cast<float4*>(stage + u * kUnitStride + 4 * j) = v;
+        }
+        float rstd = 1.0f;
+        if constexpr (NORM) rstd = 1.0f / sqrtf(block_sum_nt<NT>(ss, lds4) / (float)a.k + a.eps);
+        else __syncthreads();
+#pragma unroll
+        for (int t = 0; t < UPL; ++t) {
+            const int u = glane + GS * t;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (u < units) v = *reinterpret_cast<const float4*>(stage + u * kUnitStride + 4 * i);
+                xr[t][4 * i] = v.x;
+                xr[t][4 * i + 1] = v.y;
+                xr[t][4 * i + 2] = v.z;
+                xr[t][4 * i + 3] = v.w;
+            }
+            xs[t] = unit_sums(xr[t]);
+        }
+        return rstd;
+    }
+    return direct_activation<GS, UPL, NORM>(a, glane, units, xr, xs, lds4);
+}
+
+
+// Stage without a register holder: each thread loads, normalises and stores one float4 at a
+// time (for long activations, where a holder would cost occupancy). Same result as
+// issue_activation + finish_activation.
+template <int NT, int GS, int UPL, bool NORM, bool SUM = false>
+PE_DEV float stream_activation(const GemvArgs& a, int glane, int units, float (&xr)[UPL][32],
+                               UnitSums (&xs)[UPL], float* lds4, float* stage) {
+    if (a.k > kStageMaxK) return direct_activation<GS, UPL, NORM>(a, glane, units, xr, xs, lds4);
+    const bool ut = a.layout & PE_LAYOUT_X_UT;
+    const int n4 = units * 8;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n4; i += NT) {
+        const int u = ut ? i % units : i >> 3;
+        const int j = ut ? i / units : i & 7;
+        float4 v = reinterpret_cast<const float4*>(a.x)[i];
+        if constexpr (SUM) {
+            float4 pv[kMaxParts];
+#pragma unroll
+            for (int pp = 0; pp < kMaxParts; ++pp)
+                if (pp < a.n_parts) pv[pp] = reinterpret_cast<const float4*>(a.parts + (int64_t)pp * a.k)[i];
+#pragma unroll
+            for (int pp = 0; pp < kMaxParts; ++pp)
+                if (pp < a.n_parts) {
+                    v.x += pv[pp].x;
+                    v.y += pv[pp].y;
+                    v.z += pv[pp].z;
+                    v.w += pv[pp].w;
+                }
+            if (a.x_sum && blockIdx.x == 0) reinterpret_cast<float4*>(a.x_sum)[i] = v;
+        }
+        if constexpr (NORM) {
+            const float4 w = reinterpret_cast<const float4*>(a.norm_w)[i];
+            ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
+            v.x *= w.x;
+            v.y *= w.y;
+            v.z *= w.z;
+            v.w *= w.w;
+        }
+        *reinterpret_cast<float4*>(stage + u * kUnitStride + 4 * j) = v;
+    }
+    float rstd = 1.0f;
+    if constexpr (NORM) rstd = 1.0f / sqrtf(block_sum_nt<NT>(ss, lds4) / (float)a.k + a.eps);
+    else __syncthreads();
+#pragma unroll
+    for (int t = 0; t < UPL; ++t) {
+        const int u = glane + GS * t;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (u < units) v = *reinterpret_cast<const float4*>(stage + u * kUnitStride + 4 * i);
+            xr[t][4 * i] = v.x;
+            xr[t][4 * i + 1] = v.y;
+            xr[t][4 * i + 2] = v.z;
+            xr[t][4 * i + 3] = v.w;
+        }
+        xs[t] = unit_sums(xr[t]);
+    }
+    return rstd;
+}
+
+// Issue and stage in one call (for kernels with no weight loads to slot in between).
+template <int NT, int GS, int UPL, bool NORM, bool SUM = false>
+PE_DEV float stage_activation(const GemvArgs& a, int glane, int units, float (&xr)[UPL][32],
+                              UnitSums (&xs)[UPL], float* lds4, float* stage) {
+    ActLoads<act_loads<NT, GS, UPL>()> L;
+    issue_activation<NT, NORM>(a, units, L);
+    return finish_activation<NT, GS, UPL, NORM, SUM>(a, glane, units, L, xr, xs, lds4, stage);
+}
+
 constexpr int kGemvThreads = 256;
 
 // Blocked decode GEMV. A block of kGemvThreads threads owns a chunk of TPG * G consecutive
 // tasks (G = kGemvThreads / GS lane groups; group g takes tasks chunk*CH + i*G + g). Timeline:
-// every weight (and epilogue) load of the chunk is issued first; the activation is staged in
-// LDS once per block while those loads are in flight; then each group computes its TPG tasks
+// the activation loads are issued, then every weight (and epilogue) load of the chunk; the
+// activation is staged in LDS once per block while the weights are in flight (waiting for the
+// activation does not wait for the weights, which were issued later); then each group computes its TPG tasks
 // from registers, issues the loads of its next chunk (grid-stride over chunks when the grid
 // is capped), reduces with DPP butterflies and stores.
 template <int T, int GS, int UPL, int TPG, bool NORM, int MODE>
@@ -460,12 +585,23 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
             }
         }
     };
-    if (chunk < nchunk) issue(chunk);
-
+    // activation first when it takes at most two float4s per thread (the 896-long vectors);
+    // long activations (ffn_down's 4864) would hold too many registers across the weight
+    // loads, so there the weights go first
+    constexpr bool kActFirst = act_loads<NT, GS, UPL>() <= 2;
+    constexpr bool kSum = MODE == kModeSiluSum;
     float xr[UPL][32];
     UnitSums xs[UPL];
-    const float rstd =
-        stage_activation<NT, GS, UPL, NORM, MODE == kModeSiluSum>(a, glane, units, xr, xs, lds4, stage);
+    float rstd;
+    if constexpr (kActFirst) {
+        ActLoads<act_loads<NT, GS, UPL>()> act;
+        issue_activation<NT, NORM>(a, units, act);
+        if (chunk < nchunk) issue(chunk);
+        rstd = finish_activation<NT, GS, UPL, NORM, kSum>(a, glane, units, act, xr, xs, lds4, stage);
+    } else {
+        if (chunk < nchunk) issue(chunk);
+        rstd = stream_activation<NT, GS, UPL, NORM, kSum>(a, glane, units, xr, xs, lds4, stage);
+    }
 
     uint64_t best = 0;  // argmax mode: best key of this group's tasks
     for (; chunk < nchunk; chunk += gridDim.x) {

@@ -390,6 +390,43 @@ def qkv_rmsnorm_rope(x: torch.Tensor, norm_w: torch.Tensor | None, eps: float,
     return out
 
 
+def attn_oproj_supported(n_head: int, n_kv: int, hd: int, capacity: int, wo: QWeight) -> bool:
+    """Whether attn_oproj covers these shapes (else decode_attn + qgemv)."""
+    return lib.pe_attn_oproj_supported(n_head, n_kv, hd, capacity, wo.ggml_type, wo.n) == 0
+
+
+def attn_oproj(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, wo: QWeight,
+               residual: torch.Tensor | None = None, S: torch.Tensor | int | None = None,
+               S_offset: int = 0, scale: float | None = None, round_fp16: bool = True,
+               out: torch.Tensor | None = None, layout: int = LAYOUT_NATURAL) -> torch.Tensor:
+    """residual + Wo decode_attn(q, k, v, S) in one launch (same S conventions and fp16
+    output rounding as decode_attn; layout applies to residual and the result)."""
+    dev = _on_gpu(q, k, v, wo.data, residual)
+    n_head, hd = q.shape[-2], q.shape[-1]
+    n_kv, capacity = k.shape[0], k.shape[1]
+    q = _f32c(q.reshape(n_head, hd))
+    if not (k.is_contiguous() and v.is_contiguous()):
+        raise ValueError("KV caches must be contiguous (n_kv, capacity, hd) buffers")
+    if scale is None:
+        scale = 1.0 / float(hd) ** 0.5
+    len_dev, len_dtype, len_add = None, 0, int(S_offset)
+    if isinstance(S, torch.Tensor):
+        len_dev = S
+        len_dtype = {torch.int32: 1, torch.int64: 2}[S.dtype]
+    elif S is not None:
+        len_add += int(S)
+    else:
+        len_add += capacity
+    if out is None:
+        out = torch.empty(wo.n, device=dev, dtype=torch.float32)
+    res = None if residual is None else _f32c(residual.reshape(-1))
+    check(lib.pe_attn_oproj(_ptr(q), _ptr(k), _ptr(v), n_head, n_kv, hd, capacity, _ptr(len_dev),
+                            len_dtype, len_add, float(scale), int(round_fp16), wo.ggml_type,
+                            _ptr(wo.data), wo.n, _ptr(res), _ptr(out), layout, _stream(dev)),
+          "pe_attn_oproj")
+    return out
+
+
 def attn_block_workspace(hidden: int, n_head: int, n_kv: int, hd: int, capacity: int,
                          device) -> torch.Tensor | None:
     """Zero-filled workspace of ``attn_block`` for these shapes, or None when the fused block
@@ -565,5 +602,5 @@ __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "
            "rmsnorm", "rope", "silu_mul", "decode_attn", "decode_attn_workspace", "qgemv",
            "q8_0_gemv", "q5_0_gemv", "q5_0_gemv_norm", "q6_k_gemv", "q4_k_gemv", "qgemv_norm",
            "qgemv_norm_silu", "qkv_rmsnorm_rope", "attn_block", "attn_block_workspace",
-           "attn_block_failed", "attn_head", "attn_head_supported", "qgemv_sum_norm_silu", "qgemm", "kv_write", "prefill_attn",
+           "attn_block_failed", "attn_oproj", "attn_oproj_supported", "attn_head", "attn_head_supported", "qgemv_sum_norm_silu", "qgemm", "kv_write", "prefill_attn",
            "BLOCK_SIZE"]

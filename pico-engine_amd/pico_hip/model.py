@@ -95,6 +95,9 @@ class Transformer:
         # layer's formats and the cache capacity are supported; off by default until it is
         # faster than the three-launch block
         self.use_attn_head = False
+        # attention + o-projection in one launch (attn_oproj) for short caches; off by default
+        # until it is faster than decode_attn + qgemv
+        self.use_attn_oproj = False
 
     def _layer_weights(self, i: int) -> Layer:
         p, q, w = f"blk.{i}.", self.quant, self.w
@@ -192,8 +195,12 @@ class Transformer:
             k_buf, v_buf = cache[i]
             q = K.qkv_rmsnorm_rope(x, L.attn_norm_ut, cfg.eps, L.wq, L.wk, L.wv, L.bq, L.bk, L.bv,
                                    self.cos, self.sin, pos, k_buf, v_buf, cfg.n_head, layout=XU)
-            attn = K.decode_attn(q, k_buf, v_buf, S=pos, S_offset=1, workspace=ws, layout=YU)
-            x = K.qgemv(attn.reshape(-1), L.wo, residual=x, layout=XU | YU)
+            if self.use_attn_oproj and K.attn_oproj_supported(cfg.n_head, cfg.n_kv_head,
+                                                              cfg.head_dim, capacity, L.wo):
+                x = K.attn_oproj(q, k_buf, v_buf, L.wo, residual=x, S=pos, S_offset=1, layout=YU)
+            else:
+                attn = K.decode_attn(q, k_buf, v_buf, S=pos, S_offset=1, workspace=ws, layout=YU)
+                x = K.qgemv(attn.reshape(-1), L.wo, residual=x, layout=XU | YU)
             if L.w_gate_up is not None:
                 act = K.qgemv_norm_silu(x, L.ffn_norm_ut, L.w_gate_up, cfg.eps, layout=XU | YU)
                 x = K.qgemv(act, L.w_down, residual=x, layout=XU | YU)

@@ -730,3 +730,53 @@ def test_qgemv_sum_rmsnorm_silu(K):
     plain = K.qgemv_norm_silu(T(want), T(nw), w, 1e-6)
     act0, _ = K.qgemv_sum_norm_silu(T(want), T(parts[:0].copy()), T(nw), w, 1e-6)
     assert torch.equal(plain, act0)
+
+
+# ---- attention + o-projection in one launch (attn_oproj) ---------------------------------
+
+OPROJ_CASES = [
+    (dq.Q5_0, 14, 2, 77, [1, 17, 61, 77]),     # config 0 shapes
+    (dq.Q5_0, 14, 2, 256, [255, 256]),         # largest cache
+    (dq.Q8_0, 8, 1, 64, [3, 40]),              # MQA: one kv head for all
+    (dq.Q4_K, 8, 2, 100, [33, 100]),           # K-quant o-projection (512 columns)
+]
+
+
+@pytest.mark.parametrize("t,nh,nkv,cap,Ss", OPROJ_CASES,
+                         ids=[f"t{t}-{nh}x{nkv}-cap{cap}" for t, nh, nkv, cap, _ in OPROJ_CASES])
+def test_attn_oproj_matches_closed_form(K, t, nh, nkv, cap, Ss):
+    hd, hidden = 64, 896
+    rng = np.random.default_rng(nh * cap + t)
+    q = rng.standard_normal((nh, hd)).astype(np.float32)
+    k, v = _kv(rng, nkv, cap, hd)
+    x = rng.standard_normal(hidden).astype(np.float32)
+    raw = quantized_normal(t, hidden, nh * hd, seed=cap + t)
+    wo = qweight(K, t, raw, hidden, nh * hd)
+    W = dequant_rows(t, raw, hidden, nh * hd)
+    T = lambda a: torch.from_numpy(a).to(DEV)
+    assert K.attn_oproj_supported(nh, nkv, hd, cap, wo)
+    for S in Ss:
+        y = K.attn_oproj(T(q), T(k), T(v), wo, residual=T(x), S=torch.tensor([S - 1], device=DEV),
+                         S_offset=1).cpu().numpy()
+        attn = closed.attention(q, k, v, S, round_fp16=True).reshape(-1)
+        assert rel_err(y, closed.gemv(W, attn, residual=x)) < TOL, f"S={S}"
+        # same as the two-launch path
+        a2 = K.decode_attn(T(q), T(k), T(v), S=S)
+        y2 = K.qgemv(a2.reshape(-1), wo, residual=T(x)).cpu().numpy()
+        assert rel_err(y, y2) < TOL
+
+
+def test_attn_oproj_layout_empty_and_limits(K):
+    hd, nh, nkv, cap, hidden = 64, 14, 2, 77, 896
+    rng = np.random.default_rng(5)
+    q = torch.from_numpy(rng.standard_normal((nh, hd)).astype(np.float32)).to(DEV)
+    k, v = (torch.from_numpy(a).to(DEV) for a in _kv(rng, nkv, cap, hd))
+    x = torch.from_numpy(rng.standard_normal(hidden).astype(np.float32)).to(DEV)
+    wo = qweight(K, dq.Q5_0, quantized_normal(dq.Q5_0, hidden, nh * hd, seed=5), hidden, nh * hd)
+    nat = K.attn_oproj(q, k, v, wo, residual=x, S=40)
+    ut = K.attn_oproj(q, k, v, wo, residual=K.to_ut(x), S=40, layout=K.LAYOUT_Y_UT)
+    assert torch.equal(K.from_ut(ut), nat)
+    assert torch.isnan(K.attn_oproj(q, k, v, wo, residual=x, S=0)).all()
+    assert not K.attn_oproj_supported(nh, nkv, 128, cap, wo)
+    assert not K.attn_oproj_supported(nh, nkv, hd, 257, wo)
+    assert not K.attn_oproj_supported(28, 4, hd, cap, wo)
