@@ -285,15 +285,25 @@ PE_DEV float load_activation(const GemvArgs& a, int glane, int units, float (&xr
     return rstd;
 }
 
+// Weight loads of a task. A task or unit past the end is clamped to the last one (its data is
+// never used): no lane branches around the loads, so the wait that the activation staging
+// does before them (vector loads retire in issue order) can leave them in flight. Whole-block
+// groups (GS = 256, the ffn_down rows) are the exception: up to 40% of their lanes hold no unit
+// (152 units of 256 lanes), and there skipping those lanes' loads is measured to be faster.
 template <int T, int GS, int UPL, int R>
 PE_DEV void load_task(const GemvArgs& a, int64_t task, int glane, int units,
                       typename Fmt<T>::Raw (&raw)[R][UPL]) {
+    const int64_t tc = task < a.n_tasks ? task : a.n_tasks - 1;
 #pragma unroll
     for (int rr = 0; rr < R; ++rr)
 #pragma unroll
         for (int t = 0; t < UPL; ++t) {
             const int u = glane + GS * t;
-            if (u < units) Fmt<T>::load(a.w, task + rr * a.up_off, u, raw[rr][t]);
+            if constexpr (GS == 256) {
+                if (u < units) Fmt<T>::load(a.w, tc + rr * a.up_off, u, raw[rr][t]);
+            } else {
+                Fmt<T>::load(a.w, tc + rr * a.up_off, u < units ? u : units - 1, raw[rr][t]);
+            }
         }
 }
 
@@ -304,12 +314,13 @@ struct Epi {
 PE_DEV int64_t out_index(const GemvArgs& a, int64_t task) {
     return (a.layout & PE_LAYOUT_Y_UT) ? ut_index(task, a.n_tasks >> 5) : task;
 }
-PE_DEV Epi load_epi(const GemvArgs& a, int64_t task, bool lane0) {
+// Every lane loads (lane 0's copy is used), from a clamped task: the only branches are on the
+// launch-uniform pointers.
+PE_DEV Epi load_epi(const GemvArgs& a, int64_t task) {
+    const int64_t tc = task < a.n_tasks ? task : a.n_tasks - 1;
     Epi e{0.f, 0.f};
-    if (lane0) {
-        if (a.residual) e.res = a.residual[out_index(a, task)];
-        if (a.bias) e.bias = a.bias[task];
-    }
+    if (a.residual) e.res = a.residual[out_index(a, tc)];
+    if (a.bias) e.bias = a.bias[tc];
     return e;
 }
 
@@ -579,16 +590,15 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
 #pragma unroll
         for (int i = 0; i < TPG; ++i) {
             const int64_t task = c * CH + i * G + gid;
-            if (task < a.n_tasks) {
-                load_task<T, GS, UPL, R>(a, task, glane, units, raw[i]);
-                if constexpr (kEpi) epi[i] = load_epi(a, task, glane == 0);
-            }
+            load_task<T, GS, UPL, R>(a, task, glane, units, raw[i]);
+            if constexpr (kEpi) epi[i] = load_epi(a, task);
         }
     };
-    // activation first when it takes at most two float4s per thread (the 896-long vectors);
-    // long activations (ffn_down's 4864) would hold too many registers across the weight
-    // loads, so there the weights go first
-    constexpr bool kActFirst = act_loads<NT, GS, UPL>() <= 2;
+    // activation first when it takes at most six float4s per thread (up to 6144 weights per
+    // row): the staging then waits for the activation alone while the weights stay in flight.
+    // Longer activations would hold too many registers across the weight loads, so there the
+    // weights go first and the activation streams through LDS after them.
+    constexpr bool kActFirst = act_loads<NT, GS, UPL>() <= 6;
     constexpr bool kSum = MODE == kModeSiluSum;
     float xr[UPL][32];
     UnitSums xs[UPL];
@@ -596,10 +606,10 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
     if constexpr (kActFirst) {
         ActLoads<act_loads<NT, GS, UPL>()> act;
         issue_activation<NT, NORM>(a, units, act);
-        if (chunk < nchunk) issue(chunk);
+        issue(chunk);  // the grid is at most nchunk blocks
         rstd = finish_activation<NT, GS, UPL, NORM, kSum>(a, glane, units, act, xr, xs, lds4, stage);
     } else {
-        if (chunk < nchunk) issue(chunk);
+        issue(chunk);
         rstd = stream_activation<NT, GS, UPL, NORM, kSum>(a, glane, units, xr, xs, lds4, stage);
     }
 
