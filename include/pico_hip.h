@@ -278,13 +278,34 @@ int pe_attn_head(const pe_attn_head_args* args, pe_stream_t stream);
 
 /* pe_qgemv_rmsnorm_silu of x_sum = x + parts[0] + ... + parts[n_parts-1] (added in that order),
  * the parts stored back to back (part i at parts + i*k); block 0 also stores x_sum (if not
- * NULL) for the next residual. n_parts <= 16, natural layout, k <= 8192.
- * Replaces the residual add of the o-projection (model.py:213, after pe_attn_head) fused with
- * rmsnorm + gate/up + silu_mul (model.py:216-224). */
+ * NULL) for the next residual. n_parts <= 16, k <= 8192. layout: PE_LAYOUT_X_UT when x, the
+ * parts, norm_w and x_sum are unit-transposed, PE_LAYOUT_Y_UT for act. Up to 4 parts are
+ * loaded with x, before the weights.
+ * Replaces the residual add of the o-projection (model.py:213, after pe_attn_head or
+ * pe_attn_gproj) fused with rmsnorm + gate/up + silu_mul (model.py:216-224). */
 int pe_qgemv_sum_rmsnorm_silu(int ggml_type, const void* w_tiled, int64_t ffn, int64_t k,
                               const float* x, const float* parts, int n_parts,
                               const float* norm_w, float eps, float* act, float* x_sum,
-                              pe_stream_t stream);
+                              int layout, pe_stream_t stream);
+
+/* Decode attention of each kv group fused with the group's share of the o-projection, one
+ * launch, no communication between workgroups. For kv head j with query heads
+ * h = j*G .. j*G+G-1 (G = n_head / n_kv):
+ *   a_h = softmax(q_h . K_j[0..S) * scale) V_j[0..S), rounded to fp16 when round_fp16;
+ *   parts[j][r] = sum_{h in group j} sum_d Wo[r][h*head_dim + d] a_h[d]   for r < hidden,
+ * S as for pe_decode_attn (len_dev/len_dtype/len_add). The o-projection output with its
+ * residual is x + parts[0] + ... + parts[n_kv-1] (pe_qgemv_sum_rmsnorm_silu adds it).
+ * layout: PE_LAYOUT_Y_UT stores each part unit-transposed. S = 0 gives NaN parts (softmax of
+ * nothing), as pe_decode_attn.
+ * Replaces decode_attn (model.py:211, kernels.py:129) and the o-projection addmm
+ * (model.py:213). Limits (pe_attn_gproj_supported): head_dim 64, n_kv <= 4, n_head / n_kv <= 8,
+ * capacity <= 128, hidden % 32 == 0, n_head*head_dim a multiple of the Wo block. */
+int pe_attn_gproj_supported(int n_head, int n_kv, int head_dim, int64_t capacity, int wo_type,
+                            int64_t hidden);
+int pe_attn_gproj(const float* q, const float* k_cache, const float* v_cache, int n_head, int n_kv,
+                  int head_dim, int64_t capacity, const void* len_dev, int len_dtype, int64_t len_add,
+                  float scale, int round_fp16, int wo_type, const void* wo_tiled, int64_t hidden,
+                  float* parts, int layout, pe_stream_t stream);
 
 /* Decode attention of every head fused with the o-projection (short caches), one launch:
  *   a = decode_attn(q, k_cache, v_cache, S) as pe_decode_attn (GQA, scale, output rounded to

@@ -231,4 +231,4 @@ extern "C" const char* pe_strerror(int status) {
     }
 }
 
-extern "C" int pe_abi_version(void) { return 2; }
+extern "C" int pe_abi_version(void) { return 3; }

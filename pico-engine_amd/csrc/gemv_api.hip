@@ -76,17 +76,19 @@ extern "C" int pe_qgemv_rmsnorm_silu(int type, const void* w, int64_t ffn, int64
 extern "C" int pe_qgemv_sum_rmsnorm_silu(int type, const void* w, int64_t ffn, int64_t k,
                                          const float* x, const float* parts, int n_parts,
                                          const float* norm_w, float eps, float* act, float* x_sum,
-                                         pe_stream_t stream) {
+                                         int layout, pe_stream_t stream) {
     int st = check_weight(type, w, 2 * ffn, k);
     if (st) return st;
+    if ((st = check_layout(layout, ffn))) return st;
+    if ((layout & PE_LAYOUT_X_UT) && k % 32) return PE_ERR_SHAPE;
     if (n_parts < 0 || n_parts > kMaxParts || k > kStageMaxK) return PE_ERR_SHAPE;
     if (!x || !act || !norm_w || (n_parts && !parts)) return PE_ERR_NULL;
     if (!aligned(x, 16) || !aligned(parts, 16) || !aligned(norm_w, 16) || !aligned(act, 4) ||
         !aligned(x_sum, 16))
         return PE_ERR_ALIGN;
     GemvArgs a{Tiled{(const uint8_t*)w, 2 * ffn, k / block_elems(type)},
-               ffn, k, x, norm_w, eps, nullptr, nullptr, act, ffn, PE_LAYOUT_NATURAL};
-    a.parts = n_parts ? parts : nullptr;
+               ffn, k, x, norm_w, eps, nullptr, nullptr, act, ffn, layout};
+    a.parts = n_parts ? parts : x;  // read (never added) by the early part loads
     a.n_parts = n_parts;
     a.x_sum = x_sum;
     return dispatch_gemv(type, a, true, kModeSiluSum, (hipStream_t)stream);

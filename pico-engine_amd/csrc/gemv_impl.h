@@ -14,8 +14,13 @@
 
 namespace pe {
 
-// kModeSiluSum: kModeSilu whose staged activation is x + sum of parts (GemvArgs::parts)
-enum { kModePlain = 0, kModeSilu = 1, kModeArgmax = 2, kModeSiluSum = 3 };
+// kModeSiluSum: kModeSilu whose staged activation is x + sum of parts (GemvArgs::parts), at
+// most kEarlyParts of them, loaded with x; kModeSiluSumMany: the same for more parts, loaded
+// after the weights. Two modes, so that neither has a load under a run-time branch between the
+// weight loads and the staging (which would make the staging wait for the weights).
+enum { kModePlain = 0, kModeSilu = 1, kModeArgmax = 2, kModeSiluSum = 3, kModeSiluSumMany = 4 };
+// How a staging routine adds parts: not at all, from the early loads, or loading them itself.
+enum { kSumNone = 0, kSumEarly = 1, kSumLate = 2 };
 
 struct GemvArgs {
     Tiled w;
@@ -361,16 +366,21 @@ constexpr int act_loads() {
     return GS * UPL * 32 > kStageMaxK ? 1 : (GS * UPL * 8 + NT - 1) / NT;
 }
 
+// Parts (GemvArgs::parts) a summed-activation launch issues together with x; parts past these
+// are loaded after the weights.
+constexpr int kEarlyParts = 4;
+
 template <int M4>
 struct ActLoads {
     float4 x[M4];
     float4 w[M4];
+    float4 p[kEarlyParts][M4];  // summed-activation mode only
 };
 
 // Issue the float4 loads of x (and the RMSNorm weight) that this thread stages. Indices past
 // the vector are clamped to its last float4 (no branch around the load, which would make the
 // compiler wait for the data right there); finish_activation ignores them.
-template <int NT, bool NORM, int M4>
+template <int NT, bool NORM, int M4, int SUM = kSumNone>
 PE_DEV void issue_activation(const GemvArgs& a, int units, ActLoads<M4>& L) {
     if (a.k > kStageMaxK || units * 8 > NT * M4) return;
     const int n4 = units * 8;
@@ -381,6 +391,17 @@ PE_DEV void issue_activation(const GemvArgs& a, int units, ActLoads<M4>& L) {
             const int ic = i < n4 ? i : n4 - 1;
             L.x[m] = reinterpret_cast<const float4*>(a.x)[ic];
             if constexpr (NORM) L.w[m] = reinterpret_cast<const float4*>(a.norm_w)[ic];
+            if constexpr (SUM == kSumEarly) {
+                // slots past n_parts re-read the last part (never added; parts points at x when
+                // there is none): no branch around a load, and no slot whose address the
+                // compiler can prove equal to another load's (it would wait for that one)
+                const int last = a.n_parts > 0 ? a.n_parts - 1 : 0;
+#pragma unroll
+                for (int pp = 0; pp < kEarlyParts; ++pp) {
+                    const float* b = a.parts + (int64_t)(pp < last ? pp : last) * a.k;
+                    L.p[pp][m] = reinterpret_cast<const float4*>(b)[ic];
+                }
+            }
         }
     }
 }
@@ -425,7 +446,7 @@ PE_DEV float direct_activation(const GemvArgs& a, int glane, int units, float (&
     return 1.0f;
 }
 
-template <int NT, int GS, int UPL, bool NORM, bool SUM = false>
+template <int NT, int GS, int UPL, bool NORM, int SUM = kSumNone>
 PE_DEV float finish_activation(const GemvArgs& a, int glane, int units,
                                const ActLoads<act_loads<NT, GS, UPL>()>& L, float (&xr)[UPL][32],
                                UnitSums (&xs)[UPL], float* lds4, float* stage) {
@@ -441,13 +462,18 @@ PE_DEV float finish_activation(const GemvArgs& a, int glane, int units,
             const int u = ut ? i % units : i >> 3;
             const int j = ut ? i / units : i & 7;
             float4 v = L.x[m];
-            if constexpr (SUM) {
-                // every part's load is issued before the first add (fixed order, no chain of
-                // dependent round trips)
+            if constexpr (SUM != kSumNone) {
+                // x + parts[0] + parts[1] + ... in that order; late parts are all loaded before
+                // the first add (no chain of dependent round trips)
                 float4 pv[kMaxParts];
+                if constexpr (SUM == kSumEarly) {
 #pragma unroll
-                for (int pp = 0; pp < kMaxParts; ++pp)
-                    if (pp < a.n_parts) pv[pp] = reinterpret_cast<const float4*>(a.parts + (int64_t)pp * a.k)[i];
+                    for (int pp = 0; pp < kEarlyParts; ++pp) pv[pp] = L.p[pp][m];
+                } else {
+#pragma unroll
+                    for (int pp = 0; pp < kMaxParts; ++pp)
+                        if (pp < a.n_parts) pv[pp] = reinterpret_cast<const float4*>(a.parts + (int64_t)pp * a.k)[i];
+                }
 #pragma unroll
                 for (int pp = 0; pp < kMaxParts; ++pp)
                     if (pp < a.n_parts) {
@@ -494,7 +520,7 @@ PE_DEV float finish_activation(const GemvArgs& a, int glane, int units,
 // Stage without a register holder: each thread loads, normalises and stores one float4 at a
 // time (for long activations, where a holder would cost occupancy). Same result as
 // issue_activation + finish_activation.
-template <int NT, int GS, int UPL, bool NORM, bool SUM = false>
+template <int NT, int GS, int UPL, bool NORM, int SUM = kSumNone>
 PE_DEV float stream_activation(const GemvArgs& a, int glane, int units, float (&xr)[UPL][32],
                                UnitSums (&xs)[UPL], float* lds4, float* stage) {
     if (a.k > kStageMaxK) return direct_activation<GS, UPL, NORM>(a, glane, units, xr, xs, lds4);
@@ -551,7 +577,7 @@ PE_DEV float stream_activation(const GemvArgs& a, int glane, int units, float (&
 }
 
 // Issue and stage in one call (for kernels with no weight loads to slot in between).
-template <int NT, int GS, int UPL, bool NORM, bool SUM = false>
+template <int NT, int GS, int UPL, bool NORM, int SUM = kSumNone>
 PE_DEV float stage_activation(const GemvArgs& a, int glane, int units, float (&xr)[UPL][32],
                               UnitSums (&xs)[UPL], float* lds4, float* stage) {
     ActLoads<act_loads<NT, GS, UPL>()> L;
@@ -573,7 +599,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
     constexpr int NT = kGemvThreads;
     constexpr int G = NT / GS;
     constexpr int CH = G * TPG;
-    constexpr bool kSilu = MODE == kModeSilu || MODE == kModeSiluSum;
+    constexpr bool kSilu = MODE == kModeSilu || MODE == kModeSiluSum || MODE == kModeSiluSumMany;
     constexpr int R = kSilu ? 2 : 1;
     constexpr bool kEpi = !kSilu;
     __shared__ float lds4[NT / 64];
@@ -599,13 +625,13 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
     // Longer activations would hold too many registers across the weight loads, so there the
     // weights go first and the activation streams through LDS after them.
     constexpr bool kActFirst = act_loads<NT, GS, UPL>() <= 6;
-    constexpr bool kSum = MODE == kModeSiluSum;
+    constexpr int kSum = MODE == kModeSiluSum ? kSumEarly : MODE == kModeSiluSumMany ? kSumLate : kSumNone;
     float xr[UPL][32];
     UnitSums xs[UPL];
     float rstd;
     if constexpr (kActFirst) {
         ActLoads<act_loads<NT, GS, UPL>()> act;
-        issue_activation<NT, NORM>(a, units, act);
+        issue_activation<NT, NORM, act_loads<NT, GS, UPL>(), kSum>(a, units, act);
         issue(chunk);  // the grid is at most nchunk blocks
         rstd = finish_activation<NT, GS, UPL, NORM, kSum>(a, glane, units, act, xr, xs, lds4, stage);
     } else {
@@ -835,8 +861,11 @@ int gemv_dispatch(const GemvArgs& a, bool norm, int mode, hipStream_t s) {
     if (mode == kModeSilu)
         return norm ? launch_qgemv_mode<T, true, kModeSilu>(a, s)
                     : launch_qgemv_mode<T, false, kModeSilu>(a, s);
-    if (mode == kModeSiluSum)
-        return norm && a.k <= kStageMaxK ? launch_qgemv_mode<T, true, kModeSiluSum>(a, s) : PE_ERR_SHAPE;
+    if (mode == kModeSiluSum) {
+        if (!norm || a.k > kStageMaxK) return PE_ERR_SHAPE;
+        return a.n_parts <= kEarlyParts ? launch_qgemv_mode<T, true, kModeSiluSum>(a, s)
+                                        : launch_qgemv_mode<T, true, kModeSiluSumMany>(a, s);
+    }
     if (mode == kModeArgmax)
         return norm ? launch_qgemv_mode<T, true, kModeArgmax>(a, s) : PE_ERR_NULL;
     return norm ? launch_qgemv_mode<T, true, kModePlain>(a, s)

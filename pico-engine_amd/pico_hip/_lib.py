@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpico_hip
 
 # layout bits (include/pico_hip.h)
 LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT = 0, 1, 2
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -101,7 +101,9 @@ _SIGNATURES = {
     "pe_attn_block": (_I, [ctypes.POINTER(AttnBlockArgs), _P, _L, _P]),
     "pe_attn_head_supported": (_I, [_I, _I, _I, _I, _L, _I, _I, _I, _L]),
     "pe_attn_head": (_I, [ctypes.POINTER(AttnHeadArgs), _P]),
-    "pe_qgemv_sum_rmsnorm_silu": (_I, [_I, _P, _L, _L, _P, _P, _I, _P, _F, _P, _P, _P]),
+    "pe_qgemv_sum_rmsnorm_silu": (_I, [_I, _P, _L, _L, _P, _P, _I, _P, _F, _P, _P, _I, _P]),
+    "pe_attn_gproj_supported": (_I, [_I, _I, _I, _L, _I, _L]),
+    "pe_attn_gproj": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _I, _P, _L, _P, _I, _P]),
     "pe_attn_oproj_supported": (_I, [_I, _I, _I, _L, _I, _L]),
     "pe_attn_oproj": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _I, _P, _L, _P, _P, _I, _P]),
     "pe_rmsnorm": (_I, [_P, _L, _P, _P, _L, _L, _L, _F, _P]),

@@ -427,6 +427,44 @@ def attn_oproj(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, wo: QWeight,
     return out
 
 
+def attn_gproj_supported(n_head: int, n_kv: int, hd: int, capacity: int, wo: QWeight) -> bool:
+    """Whether attn_gproj covers these shapes (else decode_attn + qgemv)."""
+    return lib.pe_attn_gproj_supported(n_head, n_kv, hd, capacity, wo.ggml_type, wo.n) == 0
+
+
+def attn_gproj(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, wo: QWeight,
+               S: torch.Tensor | int | None = None, S_offset: int = 0, scale: float | None = None,
+               round_fp16: bool = True, out: torch.Tensor | None = None,
+               layout: int = LAYOUT_NATURAL) -> torch.Tensor:
+    """Per-kv-group shares of Wo decode_attn(q, k, v, S), shape (n_kv, wo.n): part j is Wo
+    restricted to the columns of kv group j's query heads times their attention output, so
+    ``residual + parts.sum(0)`` (in row order) is the o-projection with its residual. Same S
+    conventions and fp16 output rounding as decode_attn; layout LAYOUT_Y_UT stores each part
+    unit-transposed."""
+    dev = _on_gpu(q, k, v, wo.data)
+    n_head, hd = q.shape[-2], q.shape[-1]
+    n_kv, capacity = k.shape[0], k.shape[1]
+    q = _f32c(q.reshape(n_head, hd))
+    if not (k.is_contiguous() and v.is_contiguous()):
+        raise ValueError("KV caches must be contiguous (n_kv, capacity, hd) buffers")
+    if scale is None:
+        scale = 1.0 / float(hd) ** 0.5
+    len_dev, len_dtype, len_add = None, 0, int(S_offset)
+    if isinstance(S, torch.Tensor):
+        len_dev = S
+        len_dtype = {torch.int32: 1, torch.int64: 2}[S.dtype]
+    elif S is not None:
+        len_add += int(S)
+    else:
+        len_add += capacity
+    if out is None:
+        out = torch.empty(n_kv, wo.n, device=dev, dtype=torch.float32)
+    check(lib.pe_attn_gproj(_ptr(q), _ptr(k), _ptr(v), n_head, n_kv, hd, capacity, _ptr(len_dev),
+                            len_dtype, len_add, float(scale), int(round_fp16), wo.ggml_type,
+                            _ptr(wo.data), wo.n, _ptr(out), layout, _stream(dev)), "pe_attn_gproj")
+    return out
+
+
 def attn_block_workspace(hidden: int, n_head: int, n_kv: int, hd: int, capacity: int,
                          device) -> torch.Tensor | None:
     """Zero-filled workspace of ``attn_block`` for these shapes, or None when the fused block
@@ -524,9 +562,11 @@ def attn_head(x: torch.Tensor, norm_w: torch.Tensor, eps: float,
 
 def qgemv_sum_norm_silu(x: torch.Tensor, parts: torch.Tensor, weight: torch.Tensor, w: QWeight,
                         eps: float, out: torch.Tensor | None = None,
-                        x_sum: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+                        x_sum: torch.Tensor | None = None,
+                        layout: int = LAYOUT_NATURAL) -> tuple[torch.Tensor, torch.Tensor]:
     """(silu(g) * u, x_sum) with x_sum = x + parts.sum(0) (added in row order) and
-    [g; u] = W (rmsnorm(x_sum) * weight); parts (n, k) with n <= 16."""
+    [g; u] = W (rmsnorm(x_sum) * weight); parts (n, k) with n <= 16. layout: LAYOUT_X_UT when
+    x, parts, weight and x_sum are unit-transposed, LAYOUT_Y_UT for the result."""
     dev = _on_gpu(x, parts, weight, w.data)
     if w.n % 2:
         raise ValueError("gate/up weight needs an even number of rows")
@@ -540,7 +580,7 @@ def qgemv_sum_norm_silu(x: torch.Tensor, parts: torch.Tensor, weight: torch.Tens
         x_sum = torch.empty_like(x)
     check(lib.pe_qgemv_sum_rmsnorm_silu(w.ggml_type, _ptr(w.data), ffn, w.k, _ptr(x), _ptr(parts),
                                         parts.shape[0], _ptr(nw), float(eps), _ptr(out), _ptr(x_sum),
-                                        _stream(dev)), "pe_qgemv_sum_rmsnorm_silu")
+                                        layout, _stream(dev)), "pe_qgemv_sum_rmsnorm_silu")
     return out, x_sum
 
 

@@ -98,6 +98,9 @@ class Transformer:
         # attention + o-projection in one launch (attn_oproj) for short caches; off by default
         # until it is faster than decode_attn + qgemv
         self.use_attn_oproj = False
+        # attention of each kv group fused with its share of the o-projection (attn_gproj),
+        # the shares added by the gate/up GEMV: four launches per layer instead of five
+        self.use_attn_gproj = True
 
     def _layer_weights(self, i: int) -> Layer:
         p, q, w = f"blk.{i}.", self.quant, self.w
@@ -195,6 +198,13 @@ class Transformer:
             k_buf, v_buf = cache[i]
             q = K.qkv_rmsnorm_rope(x, L.attn_norm_ut, cfg.eps, L.wq, L.wk, L.wv, L.bq, L.bk, L.bv,
                                    self.cos, self.sin, pos, k_buf, v_buf, cfg.n_head, layout=XU)
+            if (self.use_attn_gproj and L.w_gate_up is not None and
+                    K.attn_gproj_supported(cfg.n_head, cfg.n_kv_head, cfg.head_dim, capacity, L.wo)):
+                parts = K.attn_gproj(q, k_buf, v_buf, L.wo, S=pos, S_offset=1, layout=YU)
+                act, x = K.qgemv_sum_norm_silu(x, parts, L.ffn_norm_ut, L.w_gate_up, cfg.eps,
+                                               layout=XU | YU)
+                x = K.qgemv(act, L.w_down, residual=x, layout=XU | YU)
+                continue
             if self.use_attn_oproj and K.attn_oproj_supported(cfg.n_head, cfg.n_kv_head,
                                                               cfg.head_dim, capacity, L.wo):
                 x = K.attn_oproj(q, k_buf, v_buf, L.wo, residual=x, S=pos, S_offset=1, layout=YU)

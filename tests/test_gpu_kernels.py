@@ -706,10 +706,11 @@ def test_attn_head_graph_replay_bad_position_and_support(K):
     assert not K.attn_head_supported(*c["ws"], c["wo"], hidden, nh, nkv, 128, cap)
 
 
-def test_qgemv_sum_rmsnorm_silu(K):
+@pytest.mark.parametrize("n", [14, 5, 4, 2, 1])
+def test_qgemv_sum_rmsnorm_silu(K, n):
     """silu(g) * u of rmsnorm(x + sum of parts); the stored sum equals the float32 sum taken
-    in part order, bit for bit."""
-    t, k, ffn, n = dq.Q5_0, 896, 4864, 14
+    in part order, bit for bit. Up to 4 parts are loaded with x, more after the weights."""
+    t, k, ffn = dq.Q5_0, 896, 4864
     raw = quantized_normal(t, 2 * ffn, k, seed=31)
     w = qweight(K, t, raw, 2 * ffn, k)
     rng = np.random.default_rng(31)
@@ -730,6 +731,77 @@ def test_qgemv_sum_rmsnorm_silu(K):
     plain = K.qgemv_norm_silu(T(want), T(nw), w, 1e-6)
     act0, _ = K.qgemv_sum_norm_silu(T(want), T(parts[:0].copy()), T(nw), w, 1e-6)
     assert torch.equal(plain, act0)
+    # unit-transposed x, parts, norm weight and sum, unit-transposed act: the same sum, and the
+    # plain fused gate/up of that sum in the same layout bit for bit (the RMSNorm sum of
+    # squares is reduced in a layout-dependent order, so only to rounding across layouts)
+    UT = K.LAYOUT_X_UT | K.LAYOUT_Y_UT
+    pu = torch.stack([K.to_ut(T(pp)) for pp in parts])
+    act_u, xs_u = K.qgemv_sum_norm_silu(K.to_ut(T(x)), pu, K.to_ut(T(nw)), w, 1e-6, layout=UT)
+    assert torch.equal(K.from_ut(xs_u), xs)
+    assert torch.equal(act_u, K.qgemv_norm_silu(K.to_ut(T(want)), K.to_ut(T(nw)), w, 1e-6, layout=UT))
+    assert rel_err(K.from_ut(act_u).cpu().numpy(), act.cpu().numpy()) < 1e-6
+
+
+# ---- attention of a kv group + its o-projection share in one launch (attn_gproj) -----------
+
+GPROJ_CASES = [
+    (dq.Q5_0, 14, 2, 77, [1, 17, 61, 64, 65, 77]),   # config 0 shapes, both 64-position passes
+    (dq.Q5_0, 14, 2, 128, [127, 128]),               # largest cache
+    (dq.Q8_0, 8, 1, 64, [3, 40]),                    # MQA: one group of 8 query heads
+    (dq.Q4_K, 8, 2, 100, [33, 100]),                 # K-quant o-projection (512 columns)
+    (dq.Q6_K, 16, 4, 50, [7, 50]),                   # four groups (four parts)
+]
+
+
+@pytest.mark.parametrize("t,nh,nkv,cap,Ss", GPROJ_CASES,
+                         ids=[f"t{t}-{nh}x{nkv}-cap{cap}" for t, nh, nkv, cap, _ in GPROJ_CASES])
+def test_attn_gproj_matches_closed_form(K, t, nh, nkv, cap, Ss):
+    """Part j = Wo[:, columns of group j] . attention of group j's heads; x + the parts in
+    order is the o-projection with its residual."""
+    hd, hidden = 64, 896
+    rng = np.random.default_rng(nh * cap + t + 7)
+    q = rng.standard_normal((nh, hd)).astype(np.float32)
+    k, v = _kv(rng, nkv, cap, hd)
+    x = rng.standard_normal(hidden).astype(np.float32)
+    raw = quantized_normal(t, hidden, nh * hd, seed=cap + t)
+    wo = qweight(K, t, raw, hidden, nh * hd)
+    W = dequant_rows(t, raw, hidden, nh * hd)
+    T = lambda a: torch.from_numpy(a).to(DEV)
+    G = nh // nkv
+    assert K.attn_gproj_supported(nh, nkv, hd, cap, wo)
+    for S in Ss:
+        parts = K.attn_gproj(T(q), T(k), T(v), wo, S=torch.tensor([S - 1], device=DEV),
+                             S_offset=1).cpu().numpy()
+        assert parts.shape == (nkv, hidden)
+        attn = closed.attention(q, k, v, S, round_fp16=True).reshape(-1)
+        for j in range(nkv):
+            cols = slice(j * G * hd, (j + 1) * G * hd)
+            assert rel_err(parts[j], closed.gemv(W[:, cols], attn[cols])) < TOL, f"S={S} j={j}"
+        y = x.copy()
+        for pp in parts:
+            y = (y + pp).astype(np.float32)
+        assert rel_err(y, closed.gemv(W, attn, residual=x)) < TOL, f"S={S}"
+
+
+def test_attn_gproj_layout_empty_and_limits(K):
+    hd, nh, nkv, cap, hidden = 64, 14, 2, 77, 896
+    rng = np.random.default_rng(6)
+    q = torch.from_numpy(rng.standard_normal((nh, hd)).astype(np.float32)).to(DEV)
+    k, v = (torch.from_numpy(a).to(DEV) for a in _kv(rng, nkv, cap, hd))
+    wo = qweight(K, dq.Q5_0, quantized_normal(dq.Q5_0, hidden, nh * hd, seed=6), hidden, nh * hd)
+    nat = K.attn_gproj(q, k, v, wo, S=40)
+    ut = K.attn_gproj(q, k, v, wo, S=40, layout=K.LAYOUT_Y_UT)
+    for j in range(nkv):
+        assert torch.equal(K.from_ut(ut[j]), nat[j])
+    # the same attention as decode_attn, whatever the o-projection split
+    a2 = K.decode_attn(q, k, v, S=40)
+    y2 = K.qgemv(a2.reshape(-1), wo)
+    assert rel_err(nat.sum(0).cpu().numpy(), y2.cpu().numpy()) < TOL
+    assert torch.isnan(K.attn_gproj(q, k, v, wo, S=0)).all()
+    assert not K.attn_gproj_supported(nh, nkv, 128, cap, wo)      # head_dim 128
+    assert not K.attn_gproj_supported(nh, nkv, hd, 129, wo)       # capacity past 128
+    assert not K.attn_gproj_supported(28, 2, hd, cap, wo)         # 14 query heads per group
+    assert not K.attn_gproj_supported(10, 5, hd, cap, wo)         # 5 kv heads
 
 
 # ---- attention + o-projection in one launch (attn_oproj) ---------------------------------

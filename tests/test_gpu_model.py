@@ -93,21 +93,33 @@ def test_graph_equals_eager(tiny):
         nxt = int(eager.argmax())
 
 
+PATHS = {  # model flags of each attention-block path of the decode step
+    "three_launch": dict(use_attn_block=False, use_attn_head=False, use_attn_gproj=False),
+    "attn_gproj": dict(use_attn_block=False, use_attn_head=False, use_attn_gproj=True),
+    "attn_block": dict(use_attn_block=True, use_attn_head=False, use_attn_gproj=False),
+    "attn_head": dict(use_attn_block=False, use_attn_head=True, use_attn_gproj=False),
+}
+
+
+def _set_path(m, path):
+    old = {k: getattr(m, k) for k in PATHS[path]}
+    for k, v in PATHS[path].items():
+        setattr(m, k, v)
+    return old
+
+
 def test_fused_attention_block_equals_three_launch_path(tiny):
-    """The one-launch attention blocks (attn_block, attn_head + partial-sum gate/up) and the
-    three-launch block (qkv_rmsnorm_rope, decode_attn, qgemv) give the same decode logits to
-    1e-3 and the same greedy ids."""
+    """The fused attention blocks (attn_block; attn_head and attn_gproj with the partial-sum
+    gate/up) and the three-launch block (qkv_rmsnorm_rope, decode_attn, qgemv) give the same
+    decode logits to 1e-3 and the same greedy ids."""
     eng, _ = tiny
     m = eng.model
     ids = [5, 6, 7, 8, 9, 10]
-    default = m.use_attn_block
-    m.use_attn_block = True
-    assert m.block_workspace(len(ids) + 10) is not None
     outs = {}
-    head_default = m.use_attn_head
-    m.use_attn_head = False
-    for fused in (True, False):
-        m.use_attn_block = fused
+    for path in PATHS:
+        old = _set_path(m, path)
+        if path == "attn_block":
+            assert m.block_workspace(len(ids) + 10) is not None
         cache = eng._empty_cache(len(ids) + 10)
         lg = m.forward(torch.tensor(ids, device=eng.device), torch.arange(len(ids), device=eng.device), cache)
         seq = []
@@ -117,40 +129,27 @@ def test_fused_attention_block_equals_three_launch_path(tiny):
                            torch.tensor([len(ids) + step], device=eng.device), cache)
             seq.append(lg.cpu().numpy())
             tok = int(lg.argmax())
-        outs[fused] = seq
-    m.use_attn_block = default
-    m.use_attn_head = True
-    cache = eng._empty_cache(len(ids) + 10)
-    lg = m.forward(torch.tensor(ids, device=eng.device), torch.arange(len(ids), device=eng.device), cache)
-    seq = []
-    tok = int(lg.argmax())
-    for step in range(10):
-        lg = m.forward(torch.tensor([tok], device=eng.device),
-                       torch.tensor([len(ids) + step], device=eng.device), cache)
-        seq.append(lg.cpu().numpy())
-        tok = int(lg.argmax())
-    outs["heads"] = seq
-    m.use_attn_head = head_default
-    for a, b, c in zip(outs[True], outs[False], outs["heads"]):
-        assert rel_err(c, b) < TOL
-        assert int(np.argmax(c)) == int(np.argmax(b))
-        assert rel_err(a, b) < TOL
-        assert int(np.argmax(a)) == int(np.argmax(b))
+        outs[path] = seq
+        for k, v in old.items():
+            setattr(m, k, v)
+    for path in PATHS:
+        for a, b in zip(outs[path], outs["three_launch"]):
+            assert rel_err(a, b) < TOL, path
+            assert int(np.argmax(a)) == int(np.argmax(b)), path
     m.check_device_errors()
 
 
-@pytest.mark.parametrize("path", ["attn_head", "attn_block", "three_launch"])
+@pytest.mark.parametrize("path", list(PATHS))
 def test_config0_greedy_matches_fixture(model_dir, path):
     """Qwen2.5-0.5B-architecture synthetic model, 13-token seeded prompt, 64 greedy tokens,
-    with each attention-block path (three_launch is the default)."""
+    with each attention-block path of the decode step."""
     from pico_hip import synth
     from pico_hip.engine import Engine
     fx = json.loads((GOLDEN / "config0_greedy.json").read_text())
-    path = synth.cached(synth.ARCHES["qwen2.5-0.5b"], seed=fx["seed"], cache_dir=model_dir)
-    assert synth.sha256(path) == fx["gguf_sha256"], "synthetic model is not byte-identical"
-    eng = Engine(path)
-    eng.model.use_attn_head = path == "attn_head"
-    eng.model.use_attn_block = path == "attn_block"
+    gguf = synth.cached(synth.ARCHES["qwen2.5-0.5b"], seed=fx["seed"], cache_dir=model_dir)
+    assert synth.sha256(gguf) == fx["gguf_sha256"], "synthetic model is not byte-identical"
+    eng = Engine(gguf)
+    _set_path(eng.model, path)
     got = eng.generate_ids(fx["prompt_ids"], fx["n_tokens"], temperature=0.0, use_graph=True)
     first_diff = next((i for i, (a, b) in enumerate(zip(got, fx["tokens"])) if a != b), None)
     assert got == fx["tokens"], f"first mismatch at step {first_diff} (margin {fx['margins'][first_diff]})"
