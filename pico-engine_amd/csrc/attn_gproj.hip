@@ -43,13 +43,23 @@ struct GpParams {
     int layout;            // PE_LAYOUT_Y_UT: each part unit-transposed
 };
 
-PE_DEV int64_t gp_len(const GpParams& p) {
+// The valid length S from two vector loads issued before every other load (a scalar load would
+// be waited for by the first LDS wait): the low word of the device value and, for an int64
+// value, its high word (the low word again for an int32 one, so that no load is conditional).
+struct GpLen {
+    int lo, hi;
+};
+PE_DEV GpLen gp_len_load(const GpParams& p) {
+    const int* lp = p.len_dtype ? reinterpret_cast<const int*>(p.len_dev) : reinterpret_cast<const int*>(p.q);
+    return {lp[0], lp[p.len_dtype == 2 ? 1 : 0]};
+}
+PE_DEV int gp_len(const GpParams& p, GpLen v) {
     int64_t S = p.len_add;
-    if (p.len_dtype == 1) S += *reinterpret_cast<const int32_t*>(p.len_dev);
-    else if (p.len_dtype == 2) S += *reinterpret_cast<const int64_t*>(p.len_dev);
+    if (p.len_dtype == 1) S += v.lo;
+    else if (p.len_dtype == 2) S += (int64_t)(((uint64_t)(uint32_t)v.hi << 32) | (uint32_t)v.lo);
     if (S < 0) S = 0;
     if (S > p.capacity) S = p.capacity;
-    return S;
+    return __builtin_amdgcn_readfirstlane((int)S);
 }
 
 // Sum over aligned groups of 8 lanes (DPP quad permutes, then the half-row mirror; all 8
@@ -84,7 +94,9 @@ __global__ __launch_bounds__(kGpThreads) void k_attn_gproj(GpParams p) {
     const float* kb = p.k_cache + (int64_t)j * p.capacity * kGpHd;
     const float* vb = p.v_cache + (int64_t)j * p.capacity * kGpHd;
 
-    // ---- loads, in the order they are used: q, K, V, then the o-projection weights
+    // ---- loads, in the order they are used: the valid length, q, K, V, the o-projection
+    // weights
+    const GpLen lv = gp_len_load(p);
     const int nq4 = G * kGpHd / 4;
     const int qi = t & (NH * kGpHd / 4 - 1);
     const float4 qv = reinterpret_cast<const float4*>(p.q + (int64_t)j * G * kGpHd)[qi < nq4 ? qi : nq4 - 1];
@@ -108,26 +120,31 @@ __global__ __launch_bounds__(kGpThreads) void k_attn_gproj(GpParams p) {
     Fmt<T>::load(p.wo, r0 + orow < p.hidden ? r0 + orow : p.hidden - 1,
                  j * gunits + (ou < gunits ? ou : gunits - 1), w);
 
+    const int S = gp_len(p, lv);
     if (t < NH * kGpHd / 4) q_lds[t] = t < nq4 ? qv : make_float4(0.f, 0.f, 0.f, 0.f);
     __syncthreads();
 
-    // ---- scores: the 8 lanes of a position each dot 8 dimensions, then add across the 8
+    // ---- scores: the 8 lanes of a position each dot 8 dimensions, then add across the 8.
+    // A wave covers 8 positions; one whose positions all lie past S skips the phase (the
+    // softmax never reads their scores).
+    const bool wave_live = kGpSlicePos * __builtin_amdgcn_readfirstlane(t >> 6) < S;
+    if (wave_live) {
 #pragma unroll
-    for (int h = 0; h < NH; ++h) {
-        const float4 q0 = q_lds[h * (kGpHd / 4) + 2 * ko], q1 = q_lds[h * (kGpHd / 4) + 2 * ko + 1];
-        float s = 0.f;
-        s = fmaf(q0.x, kr[0].x, s);
-        s = fmaf(q0.y, kr[0].y, s);
-        s = fmaf(q0.z, kr[0].z, s);
-        s = fmaf(q0.w, kr[0].w, s);
-        s = fmaf(q1.x, kr[1].x, s);
-        s = fmaf(q1.y, kr[1].y, s);
-        s = fmaf(q1.z, kr[1].z, s);
-        s = fmaf(q1.w, kr[1].w, s);
-        s = octet_sum(s);
-        if (ko == 0) sc[h * kGpMaxCap + kp] = s * p.scale;
+        for (int h = 0; h < NH; ++h) {
+            const float4 q0 = q_lds[h * (kGpHd / 4) + 2 * ko], q1 = q_lds[h * (kGpHd / 4) + 2 * ko + 1];
+            float s = 0.f;
+            s = fmaf(q0.x, kr[0].x, s);
+            s = fmaf(q0.y, kr[0].y, s);
+            s = fmaf(q0.z, kr[0].z, s);
+            s = fmaf(q0.w, kr[0].w, s);
+            s = fmaf(q1.x, kr[1].x, s);
+            s = fmaf(q1.y, kr[1].y, s);
+            s = fmaf(q1.z, kr[1].z, s);
+            s = fmaf(q1.w, kr[1].w, s);
+            s = octet_sum(s);
+            if (ko == 0) sc[h * kGpMaxCap + kp] = s * p.scale;
+        }
     }
-    const int S = (int)gp_len(p);  // a device value: read after the loads above are out
     __syncthreads();
 
     // ---- softmax rows: wave h takes head slot h (exponentials kept unnormalised, zero past
@@ -154,20 +171,26 @@ __global__ __launch_bounds__(kGpThreads) void k_attn_gproj(GpParams p) {
     for (int i = 0; i < kGpSlicePos; ++i) vr[i] = kGpSlicePos * vsl + i < S ? vr[i] : 0.f;
     __syncthreads();
 
-    // ---- P.V: lane (vd, vsl) sums its 8 positions for every head slot
+    // ---- P.V: lane (vd, vsl) sums its 8 positions for every head slot (a wave holds one
+    // slice; a slice wholly past S adds zeros)
+    if (!wave_live) {
 #pragma unroll
-    for (int h = 0; h < NH; ++h) {
-        const float4 p0 = sc4[h][2 * vsl], p1 = sc4[h][2 * vsl + 1];
-        float a = 0.f;
-        a = fmaf(p0.x, vr[0], a);
-        a = fmaf(p0.y, vr[1], a);
-        a = fmaf(p0.z, vr[2], a);
-        a = fmaf(p0.w, vr[3], a);
-        a = fmaf(p1.x, vr[4], a);
-        a = fmaf(p1.y, vr[5], a);
-        a = fmaf(p1.z, vr[6], a);
-        a = fmaf(p1.w, vr[7], a);
-        red[vsl][h * kGpHd + vd] = a;
+        for (int h = 0; h < NH; ++h) red[vsl][h * kGpHd + vd] = 0.f;
+    } else {
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            const float4 p0 = sc4[h][2 * vsl], p1 = sc4[h][2 * vsl + 1];
+            float a = 0.f;
+            a = fmaf(p0.x, vr[0], a);
+            a = fmaf(p0.y, vr[1], a);
+            a = fmaf(p0.z, vr[2], a);
+            a = fmaf(p0.w, vr[3], a);
+            a = fmaf(p1.x, vr[4], a);
+            a = fmaf(p1.y, vr[5], a);
+            a = fmaf(p1.z, vr[6], a);
+            a = fmaf(p1.w, vr[7], a);
+            red[vsl][h * kGpHd + vd] = a;
+        }
     }
     __syncthreads();
     if (t < G * kGpHd) {
