@@ -9,22 +9,32 @@
 // the gate/up GEMV's summed-activation mode (pe_qgemv_sum_rmsnorm_silu) adds the parts to x
 // in that order while it stages its activation, so the o-projection needs no launch of its own.
 //
-// Workgroup (rb, j) owns o-projection rows [64 rb, 64 rb + 64) of group j and recomputes the
-// group's attention itself: no exchange between workgroups. Every load that depends on no
-// other load (o-projection weights, q, the K and V rows of every position) is issued at
-// kernel start with clamped indices; positions past the valid length are masked afterwards.
+// Workgroup (rb, j) owns o-projection rows [kGpRows rb, kGpRows (rb + 1)) of group j and
+// recomputes the group's attention itself: no exchange between workgroups. Every load that
+// depends on no other load (the valid length, q, the K and V rows of every position, the
+// o-projection weights) is issued at kernel start with clamped indices; positions past the
+// valid length are masked afterwards.
 #include "gemv_impl.h"
+
+#ifndef KGP_THREADS
+#define KGP_THREADS 512  // measured: 1024 is slower, fewer than 512 is not supported
+#endif
 
 namespace pe {
 
-constexpr int kGpThreads = 1024;  // 16 waves: 4 per SIMD, every phase split 16 ways
+constexpr int kGpThreads = KGP_THREADS;
 constexpr int kGpHd = 64;
-constexpr int kGpRows = 64;       // o-projection rows per workgroup, 16 lanes per row
-constexpr int kGpMaxCap = 128;    // cache positions: one per 8 lanes in the score phase
+constexpr int kGpRows = kGpThreads / 16;  // o-projection rows per workgroup, 16 lanes per row
+constexpr int kGpMaxCap = 128;            // cache positions
 constexpr int kGpMaxGroup = 8;    // query heads per kv head (<= 16 units of a row per lane group)
 constexpr int kGpMaxKv = 4;       // kv heads, i.e. parts
-constexpr int kGpSlices = kGpThreads / kGpHd;        // P.V position slices (16)
-constexpr int kGpSlicePos = kGpMaxCap / kGpSlices;   // positions per slice (8)
+constexpr int kGpPassPos = kGpThreads / 8;            // score phase: 8 lanes per position
+constexpr int kGpPasses = kGpMaxCap / kGpPassPos;      // positions held per lane
+constexpr int kGpSlices = kGpThreads / kGpHd;          // P.V position slices
+constexpr int kGpSlicePos = kGpMaxCap / kGpSlices;     // positions per slice
+static_assert(kGpThreads / 64 >= kGpMaxGroup, "the softmax runs one wave per head slot");
+static_assert(kGpThreads >= kGpMaxGroup * kGpHd, "the P.V combine runs one thread per output");
+static_assert(kGpMaxCap % kGpPassPos == 0 && kGpSlicePos % 4 == 0, "position tiling");
 
 struct GpParams {
     const float* q;        // (n_head, 64), after RoPE
@@ -100,15 +110,17 @@ __global__ __launch_bounds__(kGpThreads) void k_attn_gproj(GpParams p) {
     const int nq4 = G * kGpHd / 4;
     const int qi = t & (NH * kGpHd / 4 - 1);
     const float4 qv = reinterpret_cast<const float4*>(p.q + (int64_t)j * G * kGpHd)[qi < nq4 ? qi : nq4 - 1];
-    const int kp = t >> 3, ko = t & 7;  // scores: position kp, dims 8 ko .. 8 ko + 7
-    float4 kr[2];
-    {
-        const int a = kp < clast ? kp : clast;
+    const int kp = t >> 3, ko = t & 7;  // scores: positions kp + kGpPassPos ps, dims 8 ko ..
+    float4 kr[kGpPasses][2];
+#pragma unroll
+    for (int ps = 0; ps < kGpPasses; ++ps) {
+        const int pp = kp + kGpPassPos * ps;
+        const int a = pp < clast ? pp : clast;
         const float4* pk = reinterpret_cast<const float4*>(kb + (int64_t)a * kGpHd + 8 * ko);
-        kr[0] = pk[0];
-        kr[1] = pk[1];
+        kr[ps][0] = pk[0];
+        kr[ps][1] = pk[1];
     }
-    const int vd = t & 63, vsl = t >> 6;  // P.V: dimension vd, positions 8 vsl .. 8 vsl + 7
+    const int vd = t & 63, vsl = t >> 6;  // P.V: dimension vd, slice vsl of the positions
     float vr[kGpSlicePos];
 #pragma unroll
     for (int i = 0; i < kGpSlicePos; ++i) {
@@ -125,24 +137,27 @@ __global__ __launch_bounds__(kGpThreads) void k_attn_gproj(GpParams p) {
     __syncthreads();
 
     // ---- scores: the 8 lanes of a position each dot 8 dimensions, then add across the 8.
-    // A wave covers 8 positions; one whose positions all lie past S skips the phase (the
-    // softmax never reads their scores).
-    const bool wave_live = kGpSlicePos * __builtin_amdgcn_readfirstlane(t >> 6) < S;
-    if (wave_live) {
+    // A wave covers 8 positions of a pass; one whose positions all lie past S skips the pass
+    // (the softmax never reads their scores).
+    const int wfirst = 8 * __builtin_amdgcn_readfirstlane(t >> 6);
 #pragma unroll
-        for (int h = 0; h < NH; ++h) {
-            const float4 q0 = q_lds[h * (kGpHd / 4) + 2 * ko], q1 = q_lds[h * (kGpHd / 4) + 2 * ko + 1];
-            float s = 0.f;
-            s = fmaf(q0.x, kr[0].x, s);
-            s = fmaf(q0.y, kr[0].y, s);
-            s = fmaf(q0.z, kr[0].z, s);
-            s = fmaf(q0.w, kr[0].w, s);
-            s = fmaf(q1.x, kr[1].x, s);
-            s = fmaf(q1.y, kr[1].y, s);
-            s = fmaf(q1.z, kr[1].z, s);
-            s = fmaf(q1.w, kr[1].w, s);
-            s = octet_sum(s);
-            if (ko == 0) sc[h * kGpMaxCap + kp] = s * p.scale;
+    for (int ps = 0; ps < kGpPasses; ++ps) {
+        if (kGpPassPos * ps + wfirst < S) {
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                const float4 q0 = q_lds[h * (kGpHd / 4) + 2 * ko], q1 = q_lds[h * (kGpHd / 4) + 2 * ko + 1];
+                float s = 0.f;
+                s = fmaf(q0.x, kr[ps][0].x, s);
+                s = fmaf(q0.y, kr[ps][0].y, s);
+                s = fmaf(q0.z, kr[ps][0].z, s);
+                s = fmaf(q0.w, kr[ps][0].w, s);
+                s = fmaf(q1.x, kr[ps][1].x, s);
+                s = fmaf(q1.y, kr[ps][1].y, s);
+                s = fmaf(q1.z, kr[ps][1].z, s);
+                s = fmaf(q1.w, kr[ps][1].w, s);
+                s = octet_sum(s);
+                if (ko == 0) sc[h * kGpMaxCap + kp + kGpPassPos * ps] = s * p.scale;
+            }
         }
     }
     __syncthreads();
@@ -171,24 +186,24 @@ __global__ __launch_bounds__(kGpThreads) void k_attn_gproj(GpParams p) {
     for (int i = 0; i < kGpSlicePos; ++i) vr[i] = kGpSlicePos * vsl + i < S ? vr[i] : 0.f;
     __syncthreads();
 
-    // ---- P.V: lane (vd, vsl) sums its 8 positions for every head slot (a wave holds one
-    // slice; a slice wholly past S adds zeros)
-    if (!wave_live) {
+    // ---- P.V: lane (vd, vsl) sums its kGpSlicePos positions for every head slot (a wave holds
+    // one slice; a slice wholly past S adds zeros)
+    const bool slice_live = kGpSlicePos * __builtin_amdgcn_readfirstlane(t >> 6) < S;
+    if (!slice_live) {
 #pragma unroll
         for (int h = 0; h < NH; ++h) red[vsl][h * kGpHd + vd] = 0.f;
     } else {
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
-            const float4 p0 = sc4[h][2 * vsl], p1 = sc4[h][2 * vsl + 1];
             float a = 0.f;
-            a = fmaf(p0.x, vr[0], a);
-            a = fmaf(p0.y, vr[1], a);
-            a = fmaf(p0.z, vr[2], a);
-            a = fmaf(p0.w, vr[3], a);
-            a = fmaf(p1.x, vr[4], a);
-            a = fmaf(p1.y, vr[5], a);
-            a = fmaf(p1.z, vr[6], a);
-            a = fmaf(p1.w, vr[7], a);
+#pragma unroll
+            for (int i4 = 0; i4 < kGpSlicePos / 4; ++i4) {
+                const float4 pv = sc4[h][(kGpSlicePos / 4) * vsl + i4];
+                a = fmaf(pv.x, vr[4 * i4], a);
+                a = fmaf(pv.y, vr[4 * i4 + 1], a);
+                a = fmaf(pv.z, vr[4 * i4 + 2], a);
+                a = fmaf(pv.w, vr[4 * i4 + 3], a);
+            }
             red[vsl][h * kGpHd + vd] = a;
         }
     }
