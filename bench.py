@@ -79,9 +79,14 @@ def kernel_launchers(eng, which: str):
     # the decode step's own launch configuration: activations in the unit-transposed layout
     x = torch.randn(cfg.hidden, device=eng.device)
     if which == "gate_up":
-        w, name = L0.w_gate_up, "k_qgemv (Q5_0, rmsnorm+SiLU pair) gate/up 896->2x4864"
-        fn = lambda ww: K.qgemv_norm_silu(x, L0.ffn_norm_ut, ww, cfg.eps, layout=XU | YU)
-        io = 4 * (cfg.hidden * 2 + cfg.ffn_dim)
+        # as the decode step runs it: x plus the attention block's n_kv o-projection parts,
+        # RMSNorm, [gate; up] pair, SiLU; the sum is stored for the next residual
+        w = L0.w_gate_up
+        parts = torch.randn(cfg.n_kv_head, cfg.hidden, device=eng.device) * 0.1
+        name = (f"k_qgemv (Q5_0, x + {cfg.n_kv_head} o-proj parts, rmsnorm+SiLU pair) gate/up "
+                f"{cfg.hidden}->2x{cfg.ffn_dim}")
+        fn = lambda ww: K.qgemv_sum_norm_silu(x, parts, L0.ffn_norm_ut, ww, cfg.eps, layout=XU | YU)
+        io = 4 * (cfg.hidden * (3 + cfg.n_kv_head) + cfg.ffn_dim)
     elif which == "lm_head":
         w, name = m.output, "k_qgemv (Q8_0, rmsnorm, device greedy pick) LM head 896->151936"
         g = K.GreedyState(m.output.n, 1, eng.device)
