@@ -176,16 +176,17 @@ typedef struct pe_qkv_args {
 } pe_qkv_args;
 int pe_qkv_rmsnorm_rope(const pe_qkv_args* args, pe_stream_t stream);
 
-/* Single-query GQA attention over a KV cache, split over positions across CUs with a
- * log-sum-exp merge (the last split to finish merges; no extra launch).
+/* Single-query GQA attention over a KV cache. Caches of at most 1024 positions: one launch,
+ * a workgroup per query head. Longer caches: split over 64-position chunks across CUs, then a
+ * log-sum-exp merge launch (one workgroup per query head) in a fixed order.
  *   q (n_head, hd); k_cache, v_cache (n_kv, capacity, hd); out (n_head, hd)
  *   valid length S = (len_dev ? *len_dev : 0) + len_add, clamped to [0, capacity];
  *   len_dtype: 0 = len_dev unused, 1 = int32, 2 = int64. Head h reads kv head h / (n_head/n_kv).
  *   round_fp16 != 0 rounds the output to fp16 (round-to-nearest-even) and stores it as fp32,
  *   as the reference kernel does (kernels.py:126). S == 0 gives NaN, as the reference does.
- * workspace: pe_decode_attn_workspace_bytes(...) bytes, zero-filled once before first use;
- * it is left zeroed again after every call, so one workspace serves any number of calls
- * made in order on one stream (calls that overlap must not share it).
+ * workspace: pe_decode_attn_workspace_bytes(...) bytes (the split records); any contents.
+ * One workspace serves any number of calls made in order on one stream (calls that overlap
+ * must not share it).
  * layout: PE_LAYOUT_Y_UT writes out as one unit-transposed vector of n_head*hd elements.
  * Replaces decode_attn (kernels.py:129). */
 int64_t pe_decode_attn_workspace_bytes(int n_head, int n_kv, int head_dim, int64_t capacity);

@@ -7,9 +7,9 @@
 // capacity; here the positions are split in chunks of 64 across workgroups (flash-decoding),
 // one workgroup per (chunk, kv head) serving all the query heads of that kv head, so K/V are
 // read once per kv head and chunks past S cost no KV reads. Each workgroup writes its chunk's
-// (max, sum, P.V) partials; the last one to finish (device-scope counter) merges them with the
-// log-sum-exp rule in a fixed order and resets the counter, so no second launch is needed and
-// the result does not depend on which workgroup finished last.
+// (max, sum, P.V) record; a second launch (one workgroup per query head) merges the records
+// with the log-sum-exp rule in a fixed order, so the result does not depend on the order in
+// which the workgroups ran.
 //
 // Caches of at most 1024 positions use a single-pass kernel (one workgroup per query head).
 //
@@ -62,7 +62,6 @@ __global__ __launch_bounds__(256) void k_decode_attn(AttnParams p) {
     __shared__ float sc_lds[kMaxGroup * kChunk];
     __shared__ float red_lds[PS * kMaxGroup * HD];
     __shared__ float ml_lds[2 * kMaxGroup];
-    __shared__ int last_flag;
 
     const int t = threadIdx.x;
     const int split = blockIdx.x, kvh = blockIdx.y;
@@ -71,7 +70,8 @@ __global__ __launch_bounds__(256) void k_decode_attn(AttnParams p) {
     const int64_t c0 = (int64_t)split * kChunk;
     const float NEG_INF = -__builtin_huge_valf();
 
-    if (c0 < S) {
+    if (c0 >= S) return;  // chunks past the valid length have no record (the merge skips them)
+    {
         const float* kbase = p.k + (int64_t)kvh * p.capacity * HD;
         const float* vbase = p.v + (int64_t)kvh * p.capacity * HD;
         for (int i = t; i < G * HD; i += 256) q_lds[i] = p.q[(int64_t)kvh * G * HD + i];
@@ -157,36 +157,55 @@ __global__ __launch_bounds__(256) void k_decode_attn(AttnParams p) {
             }
         }
     }
+}
 
-    // Last workgroup of this kv head merges. Release our partials, count, acquire theirs.
-    __threadfence();
-    __syncthreads();
-    if (t == 0) {
-        const unsigned prev = atomicAdd(&p.counters[kvh], 1u);
-        last_flag = (prev == (unsigned)(p.nsplit - 1));
-    }
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
+// Merge of the split records: one workgroup per query head. Lane group j (kMergeThreads / HD
+// of them) takes records j, j + groups, ... of the valid chunks, then the groups are combined in
+// LDS in a fixed order. Every record load is independent of the others, so a group's loads are
+// in flight together instead of forming a chain of dependent round trips.
+constexpr int kMergeThreads = 1024;
 
+template <int HD>
+__global__ __launch_bounds__(kMergeThreads) void k_decode_attn_merge(AttnParams p) {
+    constexpr int REC = HD + 2;
+    constexpr int NG = kMergeThreads / HD;  // lane groups
+    __shared__ float red[NG][HD];
+    __shared__ float ml[2][NG];
+    const int t = threadIdx.x, dd = t % HD, jg = t / HD;
+    const int h = blockIdx.x, G = p.group, kvh = h / G, g = h % G;
+    const int64_t S = valid_len(p);
     const int nvalid = (int)((S + kChunk - 1) / kChunk);
-    const float* base = p.partials + (int64_t)kvh * p.nsplit * G * REC;
-    for (int i = t; i < G * HD; i += 256) {
-        const int g = i / HD, dd = i % HD;
-        float M = NEG_INF;
-        for (int sp = 0; sp < nvalid; ++sp) M = fmaxf(M, base[(sp * G + g) * REC]);
-        float L = 0.f, A = 0.f;
-        for (int sp = 0; sp < nvalid; ++sp) {
-            const float* r = base + (sp * G + g) * REC;
-            const float e = expf(r[0] - M);
-            L = fmaf(r[1], e, L);
-            A = fmaf(r[2 + dd], e, A);
-        }
-        float o = A / L;
-        if (p.round_fp16) o = round_to_f16(o);
-        p.out[attn_out_index(p, ((int64_t)kvh * G + g) * HD + dd, (int64_t)p.n_kv * G * HD)] = o;
+    const float* base = p.partials + (int64_t)kvh * p.nsplit * G * REC + (int64_t)g * REC;
+    const int64_t rstride = (int64_t)G * REC;
+    const float NEG_INF = -__builtin_huge_valf();
+    float m = NEG_INF;
+    for (int sp = jg; sp < nvalid; sp += NG) m = fmaxf(m, base[sp * rstride]);
+    if (dd == 0) ml[0][jg] = m;
+    __syncthreads();
+    float M = ml[0][0];
+#pragma unroll
+    for (int j = 1; j < NG; ++j) M = fmaxf(M, ml[0][j]);
+    float L = 0.f, A = 0.f;
+    for (int sp = jg; sp < nvalid; sp += NG) {
+        const float* r = base + sp * rstride;
+        const float e = expf(r[0] - M);
+        L = fmaf(r[1], e, L);
+        A = fmaf(r[2 + dd], e, A);
     }
-    if (t == 0) p.counters[kvh] = 0u;
+    red[jg][dd] = A;
+    if (dd == 0) ml[1][jg] = L;
+    __syncthreads();
+    if (jg == 0) {
+        float a = red[0][dd], l = ml[1][0];
+#pragma unroll
+        for (int j = 1; j < NG; ++j) {
+            a += red[j][dd];
+            l += ml[1][j];
+        }
+        float o = a / l;
+        if (p.round_fp16) o = round_to_f16(o);
+        p.out[attn_out_index(p, (int64_t)h * HD + dd, (int64_t)p.n_kv * G * HD)] = o;
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -420,10 +439,13 @@ extern "C" int pe_decode_attn(const float* q, const float* k_cache, const float*
         return launch_status();
     }
     const dim3 grid((unsigned)p.nsplit, (unsigned)n_kv);
-    if (head_dim == 64)
+    if (head_dim == 64) {
         hipLaunchKernelGGL(k_decode_attn<64>, grid, dim3(256), 0, s, p);
-    else
+        hipLaunchKernelGGL(k_decode_attn_merge<64>, dim3((unsigned)n_head), dim3(kMergeThreads), 0, s, p);
+    } else {
         hipLaunchKernelGGL(k_decode_attn<128>, grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL(k_decode_attn_merge<128>, dim3((unsigned)n_head), dim3(kMergeThreads), 0, s, p);
+    }
     return launch_status();
 }
 
