@@ -176,7 +176,7 @@ typedef struct pe_qkv_args {
 } pe_qkv_args;
 int pe_qkv_rmsnorm_rope(const pe_qkv_args* args, pe_stream_t stream);
 
-/* Single-query GQA attention over a KV cache. Caches of at most 1024 positions: one launch,
+/* Single-query GQA attention over a KV cache. Caches of at most 256 positions: one launch,
  * a workgroup per query head. Longer caches: split over 64-position chunks across CUs, then a
  * log-sum-exp merge launch (one workgroup per query head) in a fixed order.
  *   q (n_head, hd); k_cache, v_cache (n_kv, capacity, hd); out (n_head, hd)

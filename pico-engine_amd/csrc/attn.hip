@@ -52,109 +52,137 @@ PE_DEV int64_t valid_len(const AttnParams& p) {
     return S;
 }
 
-template <int HD>
+// Sum over aligned groups of 4 lanes (DPP quad permutes; all 4 lanes get the same bits).
+PE_DEV float quad_sum4(float v) {
+    v += dpp_mov<0xB1>(v);  // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);  // quad_perm [2,3,0,1]
+    return v;
+}
+
+// One 64-position chunk of one kv head for all NH head slots (NH >= the group size; slots past
+// the group hold zeros and are not stored). No phase branches on the group size or on the
+// valid length: with branches the compiler waits for each LDS read on its own. Cache rows are
+// clamped to the capacity, positions past S are masked.
+template <int HD, int NH>
 __global__ __launch_bounds__(256) void k_decode_attn(AttnParams p) {
     constexpr int DQ = HD / 4;          // dims per thread in the score phase (4 threads / position)
     constexpr int PS = 256 / HD;        // position slices in the P.V phase
     constexpr int NPOS = kChunk / PS;   // positions per slice
     constexpr int REC = HD + 2;         // partial record: m, l, acc[HD]
-    __shared__ float q_lds[kMaxGroup * HD];
-    __shared__ float sc_lds[kMaxGroup * kChunk];
-    __shared__ float red_lds[PS * kMaxGroup * HD];
-    __shared__ float ml_lds[2 * kMaxGroup];
+    static_assert(NH % 4 == 0 && NPOS % 4 == 0 && DQ % 4 == 0, "tiling");
+    __shared__ float4 q4[NH * HD / 4];
+    __shared__ float4 sc4[NH][kChunk / 4];
+    __shared__ float red[PS][NH * HD];
+    __shared__ float ml[2 * NH];
+    float* sc = reinterpret_cast<float*>(sc4);
 
     const int t = threadIdx.x;
     const int split = blockIdx.x, kvh = blockIdx.y;
     const int G = p.group;
     const int64_t S = valid_len(p);
     const int64_t c0 = (int64_t)split * kChunk;
-    const float NEG_INF = -__builtin_huge_valf();
-
     if (c0 >= S) return;  // chunks past the valid length have no record (the merge skips them)
+    const float NEG_INF = -__builtin_huge_valf();
+    const float* kbase = p.k + (int64_t)kvh * p.capacity * HD;
+    const float* vbase = p.v + (int64_t)kvh * p.capacity * HD;
+    const int64_t clast = p.capacity - 1;
+
+    // loads: q of the group, this thread's K quarter-row, its V column slice
+    const int nq4 = G * HD / 4;
+    float4 qv[(NH * HD / 4 + 255) / 256];
+#pragma unroll
+    for (int i = 0; i < (NH * HD / 4 + 255) / 256; ++i) {
+        const int f = t + 256 * i;
+        qv[i] = reinterpret_cast<const float4*>(p.q + (int64_t)kvh * G * HD)[f < nq4 ? f : nq4 - 1];
+    }
+    const int sl = t >> 2, dq = t & 3;
+    float4 kr[DQ / 4];
     {
-        const float* kbase = p.k + (int64_t)kvh * p.capacity * HD;
-        const float* vbase = p.v + (int64_t)kvh * p.capacity * HD;
-        for (int i = t; i < G * HD; i += 256) q_lds[i] = p.q[(int64_t)kvh * G * HD + i];
+        const int64_t s = c0 + sl < clast ? c0 + sl : clast;
+        const float4* src = reinterpret_cast<const float4*>(kbase + s * HD + dq * DQ);
+#pragma unroll
+        for (int i = 0; i < DQ / 4; ++i) kr[i] = src[i];
+    }
+    const int d = t % HD, js = t / HD;
+    float vr[NPOS];
+#pragma unroll
+    for (int pp = 0; pp < NPOS; ++pp) {
+        const int64_t s = c0 + js * NPOS + pp;
+        vr[pp] = vbase[(s < clast ? s : clast) * HD + d];
+    }
+#pragma unroll
+    for (int i = 0; i < (NH * HD / 4 + 255) / 256; ++i) {
+        const int f = t + 256 * i;
+        if (f < NH * HD / 4) q4[f] = f < nq4 ? qv[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __syncthreads();
 
-        // K part for the score phase, V column slice for the P.V phase (issued together).
-        const int sl = t >> 2, dq = t & 3;
-        float kr[DQ];
-        {
-            const int64_t s = c0 + sl;
-            if (s < p.capacity) {
-                const float4* src = reinterpret_cast<const float4*>(kbase + s * HD + dq * DQ);
+    // scores
+    const bool pos_ok = c0 + sl < S;
 #pragma unroll
-                for (int i = 0; i < DQ / 4; ++i) {
-                    const float4 v4 = src[i];
-                    kr[4 * i] = v4.x; kr[4 * i + 1] = v4.y; kr[4 * i + 2] = v4.z; kr[4 * i + 3] = v4.w;
-                }
-            } else {
+    for (int h = 0; h < NH; ++h) {
+        float part = 0.f;
 #pragma unroll
-                for (int i = 0; i < DQ; ++i) kr[i] = 0.f;
+        for (int i = 0; i < DQ / 4; ++i) {
+            const float4 qq = q4[h * (HD / 4) + dq * (DQ / 4) + i];
+            part = fmaf(qq.x, kr[i].x, part);
+            part = fmaf(qq.y, kr[i].y, part);
+            part = fmaf(qq.z, kr[i].z, part);
+            part = fmaf(qq.w, kr[i].w, part);
+        }
+        part = quad_sum4(part);
+        if (dq == 0) sc[h * kChunk + sl] = pos_ok ? part * p.scale : NEG_INF;
+    }
+    __syncthreads();
+
+    // chunk softmax statistics: wave w handles head slots w, w + 4, ...; lane = position
+    {
+        const int w = t >> 6, lane = t & 63;
+#pragma unroll
+        for (int hh = 0; hh < NH / 4; ++hh) {
+            const int h = w + 4 * hh;
+            const float v = sc[h * kChunk + lane];
+            const float m = wave_max<64>(v);
+            const float e = expf(v - m);
+            const float l = wave_sum<64>(e);
+            sc[h * kChunk + lane] = e;
+            if (lane == 0) {
+                ml[2 * h] = m;
+                ml[2 * h + 1] = l;
             }
         }
-        const int d = t % HD, js = t / HD;
-        float vr[NPOS];
+    }
+    // V past the valid length contributes exact zeros (cache rows there may hold anything)
 #pragma unroll
-        for (int pp = 0; pp < NPOS; ++pp) {
-            const int64_t s = c0 + js * NPOS + pp;
-            vr[pp] = s < p.capacity ? vbase[s * HD + d] : 0.f;
-        }
-        __syncthreads();
+    for (int pp = 0; pp < NPOS; ++pp) vr[pp] = c0 + js * NPOS + pp < S ? vr[pp] : 0.f;
+    __syncthreads();
 
-        // scores
-        const int64_t s = c0 + sl;
-        for (int g = 0; g < G; ++g) {
-            float part = 0.f;
+    // P.V over this thread's position slice, then the slices are added in order
 #pragma unroll
-            for (int i = 0; i < DQ; ++i) part = fmaf(q_lds[g * HD + dq * DQ + i], kr[i], part);
-            part += __shfl_xor(part, 1, kWave);
-            part += __shfl_xor(part, 2, kWave);
-            if (dq == 0) sc_lds[g * kChunk + sl] = (s < S) ? part * p.scale : NEG_INF;
+    for (int h = 0; h < NH; ++h) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i4 = 0; i4 < NPOS / 4; ++i4) {
+            const float4 pv = sc4[h][js * (NPOS / 4) + i4];
+            acc = fmaf(pv.x, vr[4 * i4], acc);
+            acc = fmaf(pv.y, vr[4 * i4 + 1], acc);
+            acc = fmaf(pv.z, vr[4 * i4 + 2], acc);
+            acc = fmaf(pv.w, vr[4 * i4 + 3], acc);
         }
-        __syncthreads();
+        red[js][h * HD + d] = acc;
+    }
+    __syncthreads();
 
-        // chunk softmax statistics: wave w handles heads w, w+4, ...; lane = position
-        {
-            const int w = t >> 6, lane = t & 63;
-            for (int g = w; g < G; g += 4) {
-                const float v = sc_lds[g * kChunk + lane];
-                const float m = wave_max<64>(v);
-                const float e = expf(v - m);
-                const float l = wave_sum<64>(e);
-                sc_lds[g * kChunk + lane] = e;
-                if (lane == 0) {
-                    ml_lds[2 * g] = m;
-                    ml_lds[2 * g + 1] = l;
-                }
-            }
-        }
-        __syncthreads();
-
-        // P.V over this thread's position slice, then the slices are added in order
-        float acc[kMaxGroup];
+    float* rec = p.partials + ((int64_t)kvh * p.nsplit + split) * G * REC;
+    for (int i = t; i < G * HD; i += 256) {
+        const int g = i / HD, dd = i % HD;
+        float a = 0.f;
 #pragma unroll
-        for (int g = 0; g < kMaxGroup; ++g) {
-            acc[g] = 0.f;
-            if (g < G) {
-#pragma unroll
-                for (int pp = 0; pp < NPOS; ++pp) acc[g] = fmaf(sc_lds[g * kChunk + js * NPOS + pp], vr[pp], acc[g]);
-                red_lds[(js * kMaxGroup + g) * HD + d] = acc[g];
-            }
-        }
-        __syncthreads();
-
-        float* rec = p.partials + ((int64_t)kvh * p.nsplit + split) * G * REC;
-        for (int i = t; i < G * HD; i += 256) {
-            const int g = i / HD, dd = i % HD;
-            float a = 0.f;
-#pragma unroll
-            for (int j = 0; j < PS; ++j) a += red_lds[(j * kMaxGroup + g) * HD + dd];
-            rec[g * REC + 2 + dd] = a;
-            if (dd == 0) {
-                rec[g * REC] = ml_lds[2 * g];
-                rec[g * REC + 1] = ml_lds[2 * g + 1];
-            }
+        for (int j = 0; j < PS; ++j) a += red[j][g * HD + dd];
+        rec[g * REC + 2 + dd] = a;
+        if (dd == 0) {
+            rec[g * REC] = ml[2 * g];
+            rec[g * REC + 1] = ml[2 * g + 1];
         }
     }
 }
@@ -164,6 +192,7 @@ __global__ __launch_bounds__(256) void k_decode_attn(AttnParams p) {
 // LDS in a fixed order. Every record load is independent of the others, so a group's loads are
 // in flight together instead of forming a chain of dependent round trips.
 constexpr int kMergeThreads = 1024;
+constexpr int kMergeBatch = 8;
 
 template <int HD>
 __global__ __launch_bounds__(kMergeThreads) void k_decode_attn_merge(AttnParams p) {
@@ -178,19 +207,45 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_attn_merge(AttnParams 
     const float* base = p.partials + (int64_t)kvh * p.nsplit * G * REC + (int64_t)g * REC;
     const int64_t rstride = (int64_t)G * REC;
     const float NEG_INF = -__builtin_huge_valf();
+    // records in batches of kMergeBatch per lane group, every load of a batch issued before
+    // the first use (indices clamped to the last valid record, masked afterwards)
+    const int last = nvalid > 0 ? nvalid - 1 : 0;
     float m = NEG_INF;
-    for (int sp = jg; sp < nvalid; sp += NG) m = fmaxf(m, base[sp * rstride]);
+    for (int s0 = jg; s0 < nvalid; s0 += NG * kMergeBatch) {
+        float mb[kMergeBatch];
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; ++b) {
+            const int sp = s0 + NG * b;
+            mb[b] = base[(int64_t)(sp < last ? sp : last) * rstride];
+        }
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; ++b)
+            if (s0 + NG * b < nvalid) m = fmaxf(m, mb[b]);
+    }
     if (dd == 0) ml[0][jg] = m;
     __syncthreads();
     float M = ml[0][0];
 #pragma unroll
     for (int j = 1; j < NG; ++j) M = fmaxf(M, ml[0][j]);
     float L = 0.f, A = 0.f;
-    for (int sp = jg; sp < nvalid; sp += NG) {
-        const float* r = base + sp * rstride;
-        const float e = expf(r[0] - M);
-        L = fmaf(r[1], e, L);
-        A = fmaf(r[2 + dd], e, A);
+    for (int s0 = jg; s0 < nvalid; s0 += NG * kMergeBatch) {
+        float rm[kMergeBatch], rl[kMergeBatch], ra[kMergeBatch];
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; ++b) {
+            const int sp = s0 + NG * b;
+            const float* r = base + (int64_t)(sp < last ? sp : last) * rstride;
+            rm[b] = r[0];
+            rl[b] = r[1];
+            ra[b] = r[2 + dd];
+        }
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; ++b) {
+            if (s0 + NG * b < nvalid) {
+                const float e = expf(rm[b] - M);
+                L = fmaf(rl[b], e, L);
+                A = fmaf(ra[b], e, A);
+            }
+        }
     }
     red[jg][dd] = A;
     if (dd == 0) ml[1][jg] = L;
@@ -211,9 +266,10 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_attn_merge(AttnParams 
 // ---------------------------------------------------------------------------------------
 // Short caches (capacity <= kSmallCap): one workgroup per query head does the whole softmax
 // in one pass -- scores of all S positions into LDS (thread per position), block max/sum,
-// P.V with a thread per (dim, position slice) -- so there is no split, no device-scope
-// fence and no merge on the latency-critical path of a short decode.
-constexpr int kSmallCap = 1024;
+// P.V with a thread per (dim, position slice) -- so there is no split and no merge launch on
+// the latency-critical path of a short decode. Its time grows with S on one CU; measured, the
+// split path is as fast at 256 positions and faster beyond.
+constexpr int kSmallCap = 256;
 
 template <int HD>
 __global__ __launch_bounds__(256) void k_decode_attn_head(AttnParams p) {
@@ -439,11 +495,14 @@ extern "C" int pe_decode_attn(const float* q, const float* k_cache, const float*
         return launch_status();
     }
     const dim3 grid((unsigned)p.nsplit, (unsigned)n_kv);
+    const bool g8 = p.group <= 8;
     if (head_dim == 64) {
-        hipLaunchKernelGGL(k_decode_attn<64>, grid, dim3(256), 0, s, p);
+        if (g8) hipLaunchKernelGGL((k_decode_attn<64, 8>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((k_decode_attn<64, 16>), grid, dim3(256), 0, s, p);
         hipLaunchKernelGGL(k_decode_attn_merge<64>, dim3((unsigned)n_head), dim3(kMergeThreads), 0, s, p);
     } else {
-        hipLaunchKernelGGL(k_decode_attn<128>, grid, dim3(256), 0, s, p);
+        if (g8) hipLaunchKernelGGL((k_decode_attn<128, 8>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((k_decode_attn<128, 16>), grid, dim3(256), 0, s, p);
         hipLaunchKernelGGL(k_decode_attn_merge<128>, dim3((unsigned)n_head), dim3(kMergeThreads), 0, s, p);
     }
     return launch_status();
