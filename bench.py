@@ -23,6 +23,7 @@ Also reported on the same line:
                 same model and prompt, on this host's cores, over a bounded number of decode
                 steps (about 10-30 s).
 Usage: python bench.py [--steps 64] [--warmup 2] [--kernel gate_up|lm_head|down_q6k|...]
+       python bench.py --micro   (configs 1 and 2: GEMV shapes, decode attention, QKV kernel)
 """
 
 from __future__ import annotations
@@ -142,6 +143,74 @@ def time_kernel(launchers, iters: int, graph: bool = True) -> float:
     return e0.elapsed_time(e1) * 1000.0 / (reps * len(launchers))
 
 
+def micro(device: str) -> None:
+    """BASELINE configs 1 and 2 as kernel microbenchmarks, one JSON line per case: every valid
+    GEMV format x shape (config 1: x ~ N(0,1), W ~ N(0,0.02) quantized), decode attention at
+    L = 512, 4096, 32768 positions (config 2: fp32 K/V ~ N(0,1), 14/2 heads, hd 64) and the
+    fused RMSNorm + QKV + bias + RoPE kernel. Each launch is timed in a graph of back-to-back
+    launches over >= 1 GiB of distinct weight / KV copies; GB/s = algorithmic bytes / time."""
+    import numpy as np
+    import torch
+    from pico_hip import kernels as K
+    from pico_hip.quantize import quantize
+    Q8_0, Q5_0, Q4_K, Q6_K = 8, 6, 12, 14
+    name = {Q8_0: "Q8_0", Q5_0: "Q5_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+
+    def qweight(t, n, k, seed):
+        rng = np.random.default_rng(seed)
+        raw = quantize(t, (rng.standard_normal(n * k) * 0.02).astype(np.float32)).tobytes()
+        return K.pack_weight(torch.from_numpy(np.frombuffer(raw, np.uint8).copy()).to(device), t, n, k)
+
+    def copies(make, nbytes):
+        return [make() for _ in range(max(2, min(4096, -(-(1 << 30) // nbytes))))]
+
+    def emit(case, us, nbytes, **extra):
+        gbps = nbytes / (us * 1e3)
+        print(json.dumps({"micro": case, "us_per_launch": round(us, 3), "algorithmic_bytes": int(nbytes),
+                          "achieved_gbps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4), **extra}),
+              flush=True)
+
+    shapes = [(t, k, n) for t in (Q5_0, Q8_0) for (k, n) in ((896, 1152), (896, 896), (896, 9728),
+                                                             (4864, 896), (896, 151936))]
+    shapes += [(Q4_K, 4864, 896), (Q6_K, 4864, 896)]
+    for i, (t, k, n) in enumerate(shapes):
+        w0 = qweight(t, n, k, 100 + i)
+        ws = [w0] + [K.QWeight(w0.data.clone(), t, n, k) for _ in range(len(copies(lambda: 0, w0.nbytes)) - 1)]
+        x = torch.randn(k, device=device)
+        res = torch.randn(n, device=device)
+        nbytes = w0.nbytes + 4 * (k + 2 * n)
+        us = time_kernel([(lambda ww=ww: K.qgemv(x, ww, residual=res)) for ww in ws], 400)
+        emit("config1_gemv", us, nbytes, format=name[t], shape=f"{k}->{n}", residual=True)
+        del ws
+    nh, nkv, hd = 14, 2, 64
+    q = torch.randn(nh, hd, device=device)
+    for L in (512, 4096, 32768):
+        kvb = 2 * nkv * L * hd * 4
+        kvs = copies(lambda: (torch.randn(nkv, L, hd, device=device), torch.randn(nkv, L, hd, device=device)), kvb)
+        wsp = K.decode_attn_workspace(nh, nkv, hd, L, device)
+        S = torch.tensor([L], device=device)
+        us = time_kernel([(lambda kv=kv: K.decode_attn(q, kv[0], kv[1], S=S, workspace=wsp)) for kv in kvs], 200)
+        emit("config2_decode_attn", us, kvb + 4 * 2 * nh * hd, positions=L, heads=f"{nh}/{nkv}", head_dim=hd)
+        del kvs
+    h = 896
+    wq, wk, wv = qweight(Q5_0, nh * hd, h, 1), qweight(Q5_0, nkv * hd, h, 2), qweight(Q8_0, nkv * hd, h, 3)
+    qkv_bytes = wq.nbytes + wk.nbytes + wv.nbytes
+    trip = [(wq, wk, wv)] + [tuple(K.QWeight(w.data.clone(), w.ggml_type, w.n, w.k) for w in (wq, wk, wv))
+                             for _ in range(len(copies(lambda: 0, qkv_bytes)) - 1)]
+    x = K.to_ut(torch.randn(h, device=device))
+    nw = K.to_ut(torch.ones(h, device=device))
+    bq, bk, bv = (torch.randn(m * hd, device=device) for m in (nh, nkv, nkv))
+    cos = torch.randn(4096, hd // 2, device=device)
+    sin = torch.randn(4096, hd // 2, device=device)
+    pos = torch.tensor([60], device=device)
+    kc = torch.zeros(nkv, 77, hd, device=device)
+    vc = torch.zeros_like(kc)
+    us = time_kernel([(lambda tr=tr: K.qkv_rmsnorm_rope(x, nw, 1e-6, *tr, bq, bk, bv, cos, sin, pos, kc, vc, nh,
+                                                        layout=K.LAYOUT_X_UT)) for tr in trip], 400)
+    emit("config2_qkv_rmsnorm_rope", us, qkv_bytes + 4 * (3 * h + 2 * (nh + 2 * nkv) * hd),
+         shape="896->14x64 + 2x2x64, Q5_0/Q5_0/Q8_0")
+
+
 def traffic_from_profiles(kernel: str):
     p = ROOT / "profiles" / f"traffic_{kernel}.json"
     if p.exists():
@@ -186,6 +255,8 @@ def main() -> None:
     ap.add_argument("--kernel-iters", type=int, default=400)
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--micro", action="store_true",
+                    help="BASELINE configs 1 and 2 kernel microbenchmarks (one JSON line each) instead")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only time --kernel and a 1 GiB copy (for rocprofv3 --pmc traffic runs)")
     ap.add_argument("--model-dir", default=os.environ.get("PICO_HIP_CACHE", "/tmp/pico_hip_models"))
@@ -199,6 +270,10 @@ def main() -> None:
     import torch
     from pico_hip import synth
     from pico_hip.engine import Engine
+
+    if args.micro:
+        micro("cuda:0")
+        return
 
     arch = synth.ARCHES["qwen2.5-0.5b"]
     t0 = time.time()
