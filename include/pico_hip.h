@@ -97,6 +97,29 @@ int pe_repack(int ggml_type, const void* blocks, void* tiled, int64_t n_rows, in
 int pe_dequant_tiled(int ggml_type, const void* tiled, float* out, int64_t n_rows, int64_t k,
                      pe_stream_t stream);
 
+/* pe_dequant_tiled with fp16 output: each exact value rounded to nearest even, out[n_rows][k].
+ * The prefill GEMM's weights (torch autocast rounds the fp32 dequantized weights the same way,
+ * model.py:147-151). */
+int pe_dequant_tiled_f16(int ggml_type, const void* tiled, void* out, int64_t n_rows, int64_t k,
+                         pe_stream_t stream);
+
+/* Prompt-prefill GEMM on the matrix cores: C = A . W^T (+ bias) (+ residual), A fp32 (M, K) with
+ * row stride lda (each element rounded to fp16 as it is read, as autocast rounds F.linear's
+ * operands), W fp16 (N, K) row-major, fp32 accumulation (MFMA 16x16x32 f16), C fp32 (M, N) with
+ * row stride ldc; bias (N) and residual (M, N, row stride ldr) may be NULL; K % 32 == 0.
+ * Replaces the prefill F.linear / addmm / matmul of model.py:177, :213, :218-223 (L > 1). */
+int pe_gemm_f16(const float* a, int64_t lda, const void* w_f16, const float* bias,
+                const float* residual, int64_t ldr, float* c, int64_t ldc, int64_t M, int64_t N,
+                int64_t K, pe_stream_t stream);
+
+/* Causal GQA prompt-prefill attention on the matrix cores (flash attention): as
+ * pe_prefill_attn, with q, k, v rounded to fp16 as they are read, fp32 scores, softmax and
+ * accumulation, the probabilities rounded to fp16 for the P.V product. head_dim 64.
+ * Replaces the fp16 SDPA prefill call of model.py:201-209. */
+int pe_flash_prefill(const float* q, int64_t q_stride, const float* k_cache, const float* v_cache,
+                     int n_head, int n_kv, int head_dim, int64_t capacity, int64_t L, int64_t pos0,
+                     float scale, float* out, int64_t out_stride, pe_stream_t stream);
+
 /* out[l][:] = dequantized row ids[l] of a raw GGUF (vocab x hidden) table, l < n_ids.
  * An id outside [0, vocab) yields a row of NaN (no out-of-bounds read). layout: PE_LAYOUT_Y_UT
  * writes each row in the unit-transposed layout (hidden % 32 == 0).

@@ -112,9 +112,10 @@ __global__ void k_repack(int type, const uint8_t* __restrict__ raw, uint8_t* __r
     }
 }
 
-// One thread per (row, unit): decode through Fmt<T>::load/dequant, the GEMV's own path.
-template <int T>
-__global__ void k_dequant_tiled(Tiled t, int64_t k, float* __restrict__ out) {
+// One thread per (row, unit): decode through Fmt<T>::load/dequant, the GEMV's own path. With a
+// _Float16 output every exact value is rounded to nearest even (the prefill GEMM's weights).
+template <int T, typename O = float>
+__global__ void k_dequant_tiled(Tiled t, int64_t k, O* __restrict__ out) {
     const int units = (int)(k / 32);
     const int64_t total = t.nrows * units;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -126,7 +127,7 @@ __global__ void k_dequant_tiled(Tiled t, int64_t k, float* __restrict__ out) {
         float w[32];
         Fmt<T>::dequant(r, w);
 #pragma unroll
-        for (int i = 0; i < 32; ++i) out[row * k + 32 * u + i] = w[i];
+        for (int i = 0; i < 32; ++i) out[row * k + 32 * u + i] = (O)w[i];
     }
 }
 
@@ -198,6 +199,25 @@ extern "C" int pe_dequant_tiled(int type, const void* tiled, float* out, int64_t
         case PE_TYPE_Q5_0: hipLaunchKernelGGL(k_dequant_tiled<PE_TYPE_Q5_0>, dim3(grid), dim3(256), 0, s, t, k, out); break;
         case PE_TYPE_Q4_K: hipLaunchKernelGGL(k_dequant_tiled<PE_TYPE_Q4_K>, dim3(grid), dim3(256), 0, s, t, k, out); break;
         case PE_TYPE_Q6_K: hipLaunchKernelGGL(k_dequant_tiled<PE_TYPE_Q6_K>, dim3(grid), dim3(256), 0, s, t, k, out); break;
+    }
+    return launch_status();
+}
+
+extern "C" int pe_dequant_tiled_f16(int type, const void* tiled, void* out, int64_t n_rows, int64_t k,
+                                    pe_stream_t stream) {
+    if (!is_tiled_type(type)) return PE_ERR_TYPE;
+    if (n_rows <= 0 || k <= 0 || k % block_elems(type)) return PE_ERR_SHAPE;
+    if (!tiled || !out) return PE_ERR_NULL;
+    if (!aligned(tiled, 16) || !aligned(out, 2)) return PE_ERR_ALIGN;
+    Tiled t{(const uint8_t*)tiled, n_rows, k / block_elems(type)};
+    const int grid = grid_for(n_rows * (k / 32), 256);
+    hipStream_t s = (hipStream_t)stream;
+    _Float16* o = (_Float16*)out;
+    switch (type) {
+        case PE_TYPE_Q8_0: hipLaunchKernelGGL((k_dequant_tiled<PE_TYPE_Q8_0, _Float16>), dim3(grid), dim3(256), 0, s, t, k, o); break;
+        case PE_TYPE_Q5_0: hipLaunchKernelGGL((k_dequant_tiled<PE_TYPE_Q5_0, _Float16>), dim3(grid), dim3(256), 0, s, t, k, o); break;
+        case PE_TYPE_Q4_K: hipLaunchKernelGGL((k_dequant_tiled<PE_TYPE_Q4_K, _Float16>), dim3(grid), dim3(256), 0, s, t, k, o); break;
+        case PE_TYPE_Q6_K: hipLaunchKernelGGL((k_dequant_tiled<PE_TYPE_Q6_K, _Float16>), dim3(grid), dim3(256), 0, s, t, k, o); break;
     }
     return launch_status();
 }

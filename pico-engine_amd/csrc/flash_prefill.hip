@@ -1,0 +1,209 @@
+// Causal GQA prompt-prefill attention on the matrix cores (flash attention).
+//
+// Restates the prefill SDPA call of model.py:201-209 (is_causal, enable_gqa; under the
+// reference's CUDA autocast its operands are fp16): for query token i at absolute position
+// pos0 + i and query head h (kv head h / (n_head / n_kv)),
+//   out[i][h] = softmax_j(q_i . k_j * scale) v_j   over cache positions j <= pos0 + i,
+// with q, k, v rounded to fp16 as they are read, scores, softmax and the output accumulated
+// in fp32 (v_mfma_f32_16x16x32_f16), the probabilities rounded to fp16 for the P.V product.
+//
+// Workgroup = (64-query block, query head), 4 waves of 16 queries. Per 64-key block the
+// workgroup stages K (row-major) and V (transposed, so a lane's MFMA operand -- 8 consecutive
+// keys of one dimension -- is one 16-byte LDS read) in fp16; each wave computes its 16 x 64
+// score tile (8 MFMAs), the online-softmax update with DPP row reductions, writes P to LDS in
+// the operand layout and accumulates O += P V (8 MFMAs). The heaviest query blocks (most keys)
+// are scheduled first.
+#include "pe_common.h"
+
+namespace pe {
+
+typedef _Float16 fh8 __attribute__((ext_vector_type(8)));
+typedef float fv4 __attribute__((ext_vector_type(4)));
+
+constexpr int kFpHd = 64;
+constexpr int kFpQ = 64;       // queries per workgroup
+constexpr int kFpKeys = 64;    // keys per block
+constexpr int kFpRow = 72;     // fp16 elements per LDS row (64 + 8 padding: 144 bytes)
+
+struct FlashParams {
+    const float* q;      // (L, n_head, 64), token rows q_stride floats apart
+    int64_t q_stride;
+    const float* k;      // (n_kv, capacity, 64)
+    const float* v;
+    int group;           // query heads per kv head
+    int64_t capacity;
+    int64_t L;
+    int64_t pos0;
+    float scale;
+    float* out;          // (L, n_head, 64), token rows out_stride floats apart
+    int64_t out_stride;
+};
+
+// Sum / max over aligned groups of 16 lanes (DPP within a row; every lane gets the same bits).
+PE_DEV float row16_max(float v) {
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    v = fmaxf(v, dpp_mov<0x140>(v));
+    return v;
+}
+PE_DEV float row16_sum(float v) {
+    v += dpp_mov<0xB1>(v);
+    v += dpp_mov<0x4E>(v);
+    v += dpp_mov<0x141>(v);
+    v += dpp_mov<0x140>(v);
+    return v;
+}
+
+PE_DEV fh8 f8_to_h8(float4 a, float4 b) {
+    fh8 r;
+    r[0] = (_Float16)a.x; r[1] = (_Float16)a.y; r[2] = (_Float16)a.z; r[3] = (_Float16)a.w;
+    r[4] = (_Float16)b.x; r[5] = (_Float16)b.y; r[6] = (_Float16)b.z; r[7] = (_Float16)b.w;
+    return r;
+}
+
+__global__ __launch_bounds__(256) void k_flash_prefill(FlashParams p) {
+    __shared__ _Float16 ks[kFpKeys * kFpRow];   // K block, [key][dim]
+    __shared__ _Float16 vt[kFpHd * kFpRow];     // V block transposed, [dim][key]
+    __shared__ _Float16 ps[4][16 * kFpRow];     // per wave: P, [query][key]
+    const int t = threadIdx.x, w = t >> 6, l = t & 63;
+    const int li = l & 15, lg = l >> 4;
+    const int64_t nqb = (p.L + kFpQ - 1) / kFpQ;
+    const int64_t qb = nqb - 1 - (int64_t)blockIdx.x;  // heaviest blocks first
+    const int h = blockIdx.y, kvh = h / p.group;
+    const int64_t q0 = qb * kFpQ + 16 * w;            // this wave's first query (token index)
+    const float* kb = p.k + (int64_t)kvh * p.capacity * kFpHd;
+    const float* vb = p.v + (int64_t)kvh * p.capacity * kFpHd;
+    const int64_t n_keys = p.pos0 + p.L;              // cache positions written
+    const float NEG_INF = -__builtin_huge_valf();
+
+    // Q operand of this wave: row li (query q0 + li), dims 32 s + 8 lg .. + 8, s = 0, 1
+    fh8 qa[2];
+    {
+        const int64_t qi = q0 + li < p.L ? q0 + li : p.L - 1;
+        const float* qr = p.q + qi * p.q_stride + (int64_t)h * kFpHd;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const float4 a = *reinterpret_cast<const float4*>(qr + 32 * s + 8 * lg);
+            const float4 b = *reinterpret_cast<const float4*>(qr + 32 * s + 8 * lg + 4);
+            qa[s] = f8_to_h8(a, b);
+        }
+    }
+    // rows of this lane's score / output tiles: query q0 + 4 lg + r
+    float m_run[4], l_run[4];
+    fv4 o[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        m_run[r] = NEG_INF;
+        l_run[r] = 0.f;
+    }
+#pragma unroll
+    for (int d = 0; d < 4; ++d) o[d] = fv4{0.f, 0.f, 0.f, 0.f};
+
+    const int64_t q_last = (qb + 1) * kFpQ - 1 < p.L - 1 ? (qb + 1) * kFpQ - 1 : p.L - 1;
+    const int64_t key_end = p.pos0 + q_last + 1;      // keys this workgroup can see
+    for (int64_t j0 = 0; j0 < key_end; j0 += kFpKeys) {
+        // stage K and V (fp32 -> fp16): 64 keys x 64 dims = 1024 float4 each, 4 per thread
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int f = t + 256 * i, key = f >> 4, d4 = f & 15;
+            const int64_t kr = j0 + key < n_keys ? j0 + key : n_keys - 1;
+            const float4 kv = reinterpret_cast<const float4*>(kb + kr * kFpHd)[d4];
+            const float4 vv = reinterpret_cast<const float4*>(vb + kr * kFpHd)[d4];
+            _Float16* kd = ks + key * kFpRow + 4 * d4;
+            kd[0] = (_Float16)kv.x; kd[1] = (_Float16)kv.y; kd[2] = (_Float16)kv.z; kd[3] = (_Float16)kv.w;
+            vt[(4 * d4 + 0) * kFpRow + key] = (_Float16)vv.x;
+            vt[(4 * d4 + 1) * kFpRow + key] = (_Float16)vv.y;
+            vt[(4 * d4 + 2) * kFpRow + key] = (_Float16)vv.z;
+            vt[(4 * d4 + 3) * kFpRow + key] = (_Float16)vv.w;
+        }
+        __syncthreads();
+
+        // S = Q K^T for 4 key tiles of 16
+        fv4 sacc[4];
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+            sacc[jt] = fv4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const fh8 kbv = *reinterpret_cast<const fh8*>(ks + (16 * jt + li) * kFpRow + 32 * s + 8 * lg);
+                sacc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], kbv, sacc[jt], 0, 0, 0);
+            }
+        }
+        // scale, causal mask, online softmax per row
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t qpos = p.pos0 + q0 + 4 * lg + r;
+            float sv[4], mx = NEG_INF;
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) {
+                const int64_t key = j0 + 16 * jt + li;
+                sv[jt] = (key <= qpos && key < n_keys) ? sacc[jt][r] * p.scale : NEG_INF;
+                mx = fmaxf(mx, sv[jt]);
+            }
+            mx = row16_max(mx);
+            const float m_new = fmaxf(m_run[r], mx);
+            const float corr = m_new == NEG_INF ? 1.f : expf(m_run[r] - m_new);
+            float psum = 0.f;
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) {
+                const float e = m_new == NEG_INF ? 0.f : expf(sv[jt] - m_new);
+                psum += e;
+                ps[w][(4 * lg + r) * kFpRow + 16 * jt + li] = (_Float16)e;
+            }
+            psum = row16_sum(psum);
+            l_run[r] = l_run[r] * corr + psum;
+            m_run[r] = m_new;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) o[d][r] *= corr;
+        }
+        __syncthreads();  // P visible to the whole wave (and K / V reads done before restaging)
+
+        // O += P V: A = P (16 queries x 64 keys), B = V (64 keys x 16 dims) per dim tile
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const fh8 pa = *reinterpret_cast<const fh8*>(&ps[w][li * kFpRow + 32 * s + 8 * lg]);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const fh8 vbv = *reinterpret_cast<const fh8*>(vt + (16 * d + li) * kFpRow + 32 * s + 8 * lg);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vbv, o[d], 0, 0, 0);
+            }
+        }
+        __syncthreads();  // before the next block overwrites K / V / P
+    }
+
+    // out: O[row 4 lg + r][dim 16 d + li] / l
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int64_t qi = q0 + 4 * lg + r;
+        if (qi >= p.L) continue;
+        float* orow = p.out + qi * p.out_stride + (int64_t)h * kFpHd;
+        const float inv = 1.0f / l_run[r];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) orow[16 * d + li] = o[d][r] * inv;
+    }
+}
+
+}  // namespace pe
+
+using namespace pe;
+
+extern "C" int pe_flash_prefill(const float* q, int64_t q_stride, const float* k_cache,
+                                const float* v_cache, int n_head, int n_kv, int head_dim,
+                                int64_t capacity, int64_t L, int64_t pos0, float scale, float* out,
+                                int64_t out_stride, pe_stream_t stream) {
+    if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || head_dim != kFpHd || capacity <= 0 || L < 0 ||
+        pos0 < 0 || pos0 + L > capacity || n_head > 65535)
+        return PE_ERR_SHAPE;
+    if (L == 0) return PE_OK;
+    if ((L + kFpQ - 1) / kFpQ > 0x7FFFFFFF) return PE_ERR_SHAPE;
+    if (!q || !k_cache || !v_cache || !out) return PE_ERR_NULL;
+    if (q_stride < (int64_t)n_head * head_dim || out_stride < (int64_t)n_head * head_dim) return PE_ERR_SHAPE;
+    if (!aligned(q, 16) || q_stride % 4 || !aligned(k_cache, 16) || !aligned(v_cache, 16) ||
+        !aligned(out, 4))
+        return PE_ERR_ALIGN;
+    FlashParams p{q, q_stride, k_cache, v_cache, n_head / n_kv, capacity, L, pos0, scale, out, out_stride};
+    const dim3 grid((unsigned)((L + kFpQ - 1) / kFpQ), (unsigned)n_head);
+    hipLaunchKernelGGL(k_flash_prefill, grid, dim3(256), 0, (hipStream_t)stream, p);
+    return launch_status();
+}

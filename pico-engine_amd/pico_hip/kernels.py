@@ -132,6 +132,49 @@ def dequantize_weight(w: QWeight) -> torch.Tensor:
     return out
 
 
+def dequantize_weight_f16(w: QWeight, out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp16 (n, k) from a tiled weight: the exact values rounded to nearest even (the prefill
+    GEMM operand; autocast rounds the fp32 dequantized weights the same way). ``out`` may be a
+    row slice of a larger contiguous (rows, k) fp16 tensor."""
+    if out is None:
+        out = torch.empty(w.n, w.k, device=w.data.device, dtype=torch.float16)
+    if out.dtype != torch.float16 or tuple(out.shape) != (w.n, w.k) or not out.is_contiguous():
+        raise ValueError("out must be a contiguous (n, k) float16 tensor")
+    check(lib.pe_dequant_tiled_f16(w.ggml_type, _ptr(w.data), _ptr(out), w.n, w.k,
+                                   _stream(w.data.device)), "pe_dequant_tiled_f16")
+    return out
+
+
+def gemm_f16(a: torch.Tensor, w16: torch.Tensor, bias: torch.Tensor | None = None,
+             residual: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """C = A W^T (+ bias) (+ residual) on the matrix cores: A fp32 (M, K) (rows may be strided;
+    rounded to fp16 as read), W fp16 (N, K), fp32 accumulation and result (M, N)."""
+    dev = _on_gpu(a, w16, bias, residual)
+    if a.dim() == 1:
+        a = a.unsqueeze(0)
+    if a.dtype != torch.float32:
+        raise ValueError("a must be float32")
+    if a.stride(1) != 1 or a.stride(0) % 4 or a.data_ptr() % 16:
+        a = a.contiguous()
+    M, K = a.shape
+    N = w16.shape[0]
+    if w16.dtype != torch.float16 or not w16.is_contiguous() or w16.shape[1] != K:
+        raise ValueError("w16 must be a contiguous (N, K) float16 tensor")
+    if out is None:
+        out = torch.empty(M, N, device=dev, dtype=torch.float32)
+    ldr = 0
+    if residual is not None:
+        if residual.dtype != torch.float32 or tuple(residual.shape) != (M, N):
+            raise ValueError("residual must be a float32 (M, N) tensor")
+        if residual.stride(1) != 1:
+            residual = residual.contiguous()
+        ldr = residual.stride(0)
+    check(lib.pe_gemm_f16(_ptr(a), a.stride(0), _ptr(w16), _ptr(None if bias is None else _f32c(bias)),
+                          _ptr(residual), ldr, _ptr(out), out.stride(0), M, N, K, _stream(dev)),
+          "pe_gemm_f16")
+    return out
+
+
 def embed_gather(table: RawTensor, ids: torch.Tensor, out: torch.Tensor | None = None,
                  layout: int = LAYOUT_NATURAL):
     """Rows ``ids`` of a raw GGUF (vocab, hidden) table, dequantized (model.py:152);
@@ -638,9 +681,30 @@ def prefill_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     return out
 
 
+def flash_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos0: int = 0,
+                  scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """prefill_attn on the matrix cores: q, k, v rounded to fp16 as read, fp32 softmax and
+    accumulation (the reference's fp16 SDPA prefill, model.py:201-209); head_dim 64."""
+    dev = _on_gpu(q, k_cache, v_cache)
+    L, n_head, hd = q.shape
+    n_kv, capacity, _ = k_cache.shape
+    if q.stride(2) != 1 or q.stride(1) != hd or q.stride(0) % 4 or q.data_ptr() % 16:
+        q = q.contiguous()
+    if scale is None:
+        scale = hd ** -0.5
+    if out is None:
+        out = torch.empty(L, n_head * hd, device=dev, dtype=torch.float32)
+    check(lib.pe_flash_prefill(_ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), n_head, n_kv, hd,
+                               capacity, L, pos0, float(scale), _ptr(out), out.stride(0),
+                               _stream(dev)), "pe_flash_prefill")
+    return out
+
+
 __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "QWeight", "RawTensor", "dequantize", "pack_weight", "dequantize_weight", "embed_gather",
            "rmsnorm", "rope", "silu_mul", "decode_attn", "decode_attn_workspace", "qgemv",
            "q8_0_gemv", "q5_0_gemv", "q5_0_gemv_norm", "q6_k_gemv", "q4_k_gemv", "qgemv_norm",
            "qgemv_norm_silu", "qkv_rmsnorm_rope", "attn_block", "attn_block_workspace",
            "attn_block_failed", "attn_oproj", "attn_oproj_supported", "attn_head", "attn_head_supported", "qgemv_sum_norm_silu", "qgemm", "kv_write", "prefill_attn",
+           "attn_gproj", "attn_gproj_supported", "qgemv_norm_argmax", "dequantize_weight_f16",
+           "gemm_f16", "flash_prefill",
            "BLOCK_SIZE"]

@@ -101,6 +101,11 @@ class Transformer:
         # attention of each kv group fused with its share of the o-projection (attn_gproj),
         # the shares added by the gate/up GEMV: four launches per layer instead of five
         self.use_attn_gproj = True
+        # prompts of at least this many tokens are prefilled on the matrix cores (fp16
+        # operands, fp32 accumulation: the reference's CUDA autocast prefill, model.py:147-151);
+        # shorter ones by the fp32 path (the reference's off-CUDA numerics). None: never.
+        self.prefill_f16_min_tokens: int | None = 512
+        self._f16: list[dict[str, torch.Tensor]] | None = None
 
     def _layer_weights(self, i: int) -> Layer:
         p, q, w = f"blk.{i}.", self.quant, self.w
@@ -170,7 +175,37 @@ class Transformer:
         (token_ids/positions may then be its ``token``/``pos`` views)."""
         if token_ids.shape[0] == 1:
             return self._decode(token_ids, positions, cache, greedy)
+        m = self.prefill_f16_min_tokens
+        if m is not None and token_ids.shape[0] >= m and self.cfg.head_dim == 64:
+            return self._prefill_f16(token_ids, positions, cache, greedy)
         return self._prefill(token_ids, positions, cache, greedy)
+
+    def f16_weights(self) -> list[dict[str, torch.Tensor]]:
+        """Per layer fp16 (N, K) copies of the linear weights for the matrix-core prefill: qkv
+        ([q; k; v] rows, with the concatenated bias), o, gu ([gate; up]) and down; each value
+        the exact dequantized weight rounded to nearest even. Built once, on first use."""
+        if self._f16 is None:
+            out = []
+            for L in self.layers:
+                qd, kd = L.wq.n, L.wk.n
+                qkv = torch.empty(qd + 2 * kd, L.wq.k, device=self.device, dtype=torch.float16)
+                K.dequantize_weight_f16(L.wq, qkv[:qd])
+                K.dequantize_weight_f16(L.wk, qkv[qd:qd + kd])
+                K.dequantize_weight_f16(L.wv, qkv[qd + kd:])
+                if L.w_gate_up is not None:
+                    gu = K.dequantize_weight_f16(L.w_gate_up)
+                else:
+                    f = L.w_gate.n
+                    gu = torch.empty(2 * f, L.w_gate.k, device=self.device, dtype=torch.float16)
+                    K.dequantize_weight_f16(L.w_gate, gu[:f])
+                    K.dequantize_weight_f16(L.w_up, gu[f:])
+                bias = None
+                if L.bq is not None:
+                    bias = torch.cat([L.bq, L.bk, L.bv]).float().contiguous()
+                out.append(dict(qkv=qkv, qkv_bias=bias, o=K.dequantize_weight_f16(L.wo), gu=gu,
+                                down=K.dequantize_weight_f16(L.w_down)))
+            self._f16 = out
+        return self._f16
 
     def _lm_head(self, x, norm_w, greedy, layout):
         if greedy is None:
@@ -258,6 +293,34 @@ class Transformer:
         return self._lm_head(x, self.w["output_norm.weight"], greedy, K.LAYOUT_NATURAL)
 
     # ---- prefill --------------------------------------------------------------------------
+    def _prefill_f16(self, token_ids, positions, cache, greedy=None):
+        """The prefill on the matrix cores: GEMMs with fp16 operands (pe_gemm_f16) and flash
+        attention (pe_flash_prefill), fp32 residual stream, norms, RoPE and KV cache."""
+        cfg = self.cfg
+        Lt = token_ids.shape[0]
+        hd, nh, nkv = cfg.head_dim, cfg.n_head, cfg.n_kv_head
+        qd, kd = nh * hd, nkv * hd
+        cos = self.cos[positions]
+        sin = self.sin[positions]
+        pos0 = int(positions[0].item()) if positions.numel() else 0
+        w16 = self.f16_weights()
+        x = K.embed_gather(self.embed, token_ids)                       # (L, hidden)
+        qkv = torch.empty(Lt, qd + 2 * kd, device=self.device, dtype=torch.float32)
+        for i, L in enumerate(self.layers):
+            k_buf, v_buf = cache[i]
+            W = w16[i]
+            h = K.rmsnorm(x, L.attn_norm, cfg.eps)
+            K.gemm_f16(h, W["qkv"], bias=W["qkv_bias"], out=qkv)
+            qk = K.rope(qkv[:, :qd + kd].view(Lt, nh + nkv, hd), cos, sin)
+            v = qkv[:, qd + kd:].view(Lt, nkv, hd)
+            K.kv_write(qk[:, nh:], v, k_buf, v_buf, pos0=pos0)
+            attn = K.flash_prefill(qk[:, :nh], k_buf, v_buf, pos0=pos0)  # (L, hidden)
+            x = K.gemm_f16(attn, W["o"], residual=x)
+            h = K.rmsnorm(x, L.ffn_norm, cfg.eps)
+            act = K.silu_mul(K.gemm_f16(h, W["gu"]), cfg.ffn_dim)
+            x = K.gemm_f16(act, W["down"], residual=x)
+        return self._lm_head(x[-1], self.w["output_norm.weight"], greedy, K.LAYOUT_NATURAL)
+
     def _prefill(self, token_ids, positions, cache, greedy=None):
         cfg = self.cfg
         Lt = token_ids.shape[0]

@@ -852,3 +852,62 @@ def test_attn_oproj_layout_empty_and_limits(K):
     assert not K.attn_oproj_supported(nh, nkv, 128, cap, wo)
     assert not K.attn_oproj_supported(nh, nkv, hd, 257, wo)
     assert not K.attn_oproj_supported(28, 4, hd, cap, wo)
+
+
+# ---- prompt-prefill GEMM on the matrix cores (fp16 operands, fp32 accumulate) --------------
+
+@pytest.mark.parametrize("t,n,k", [(dq.Q5_0, 96, 896), (dq.Q8_0, 64, 896), (dq.Q4_K, 40, 4864),
+                                   (dq.Q6_K, 40, 4864)])
+def test_dequant_tiled_f16_is_rounded_exact_value(K, t, n, k):
+    """fp16 weights = the exact dequantized value rounded to nearest even, bit for bit."""
+    raw = random_quant(t, n, k, seed=n + k + t + 1)
+    w = qweight(K, t, raw, n, k)
+    gpu = K.dequantize_weight_f16(w).cpu().numpy()
+    ref = dequant_rows(t, raw, n, k).astype(np.float16)
+    np.testing.assert_array_equal(gpu.view(np.uint16), ref.view(np.uint16))
+
+
+GEMM16_CASES = [  # (M, N, K, bias, residual, a_row_stride_extra)
+    (1, 128, 896, False, False, 0), (13, 1152, 896, True, False, 0), (128, 896, 896, False, True, 0),
+    (300, 9728, 896, False, False, 0), (257, 896, 4864, False, True, 0), (77, 200, 96, True, True, 32),
+    (8192, 1152, 896, True, False, 0),
+]
+
+
+@pytest.mark.parametrize("M,N,Kd,bias,res,extra", GEMM16_CASES)
+def test_gemm_f16_matches_fp16_operand_reference(K, M, N, Kd, bias, res, extra):
+    """C = A W^T (+ bias) (+ residual) against float64 on the same fp16-rounded operands
+    (fp32 accumulation: only the summation order differs)."""
+    rng = np.random.default_rng(M + N + Kd)
+    a = rng.standard_normal((M, Kd + extra)).astype(np.float32)
+    w16 = (rng.standard_normal((N, Kd)) * 0.05).astype(np.float16)
+    b = rng.standard_normal(N).astype(np.float32) if bias else None
+    r = rng.standard_normal((M, N)).astype(np.float32) if res else None
+    T = lambda v: None if v is None else torch.from_numpy(v).to(DEV)
+    A = T(a)[:, :Kd]  # row stride Kd + extra
+    c = K.gemm_f16(A, T(w16), bias=T(b), residual=T(r)).cpu().numpy()
+    ref = a[:, :Kd].astype(np.float16).astype(np.float64) @ w16.astype(np.float64).T
+    if b is not None:
+        ref = ref + b
+    if r is not None:
+        ref = ref + r
+    assert c.shape == (M, N)
+    assert rel_err(c, ref) < 1e-5
+
+
+@pytest.mark.parametrize("L,pos0", [(1, 0), (5, 0), (64, 0), (100, 7), (130, 0), (513, 0)])
+def test_flash_prefill_matches_closed_form(K, L, pos0):
+    """Causal GQA attention on the matrix cores against float64 on the same fp16-rounded q, k,
+    v (the probabilities are rounded to fp16 inside: 2e-3 relative)."""
+    rng = np.random.default_rng(L + pos0)
+    n_head, n_kv, hd, cap = 14, 2, 64, pos0 + L + 3
+    q = rng.standard_normal((L, n_head, hd)).astype(np.float32)
+    k, v = _kv(rng, n_kv, cap, hd)
+    out = K.flash_prefill(torch.from_numpy(q).to(DEV), torch.from_numpy(k).to(DEV),
+                          torch.from_numpy(v).to(DEV), pos0=pos0).cpu().numpy()
+    h16 = lambda a: a.astype(np.float16).astype(np.float32)
+    ref = closed.causal_attention(h16(q), h16(k), h16(v), pos0).reshape(L, n_head * hd)
+    assert rel_err(out, ref) < 2e-3
+    fp32 = K.prefill_attn(torch.from_numpy(q).to(DEV), torch.from_numpy(k).to(DEV),
+                          torch.from_numpy(v).to(DEV), pos0=pos0).cpu().numpy()
+    assert rel_err(out, fp32) < 5e-3  # the fp32 path, to fp16-operand accuracy

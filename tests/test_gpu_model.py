@@ -153,3 +153,29 @@ def test_config0_greedy_matches_fixture(model_dir, path):
     got = eng.generate_ids(fx["prompt_ids"], fx["n_tokens"], temperature=0.0, use_graph=True)
     first_diff = next((i for i, (a, b) in enumerate(zip(got, fx["tokens"])) if a != b), None)
     assert got == fx["tokens"], f"first mismatch at step {first_diff} (margin {fx['margins'][first_diff]})"
+
+
+def test_prefill_f16_close_to_fp32_path(tiny):
+    """The matrix-core prefill (fp16 operands, fp32 accumulation) against the fp32 prefill on
+    the same 300-token prompt: logits, the KV cache it leaves, and the decode step after it."""
+    eng, _ = tiny
+    m = eng.model
+    ids = [(7 * i + 3) % 1024 for i in range(300)]
+    saved = m.prefill_f16_min_tokens
+    out = {}
+    try:
+        for mode, thr in (("fp32", None), ("f16", 2)):
+            m.prefill_f16_min_tokens = thr
+            cache = eng._empty_cache(len(ids) + 4)
+            lg = m.forward(torch.tensor(ids, device=eng.device), torch.arange(len(ids), device=eng.device), cache)
+            nxt = int(lg.argmax())
+            lg2 = m.forward(torch.tensor([nxt], device=eng.device), torch.tensor([len(ids)], device=eng.device), cache)
+            out[mode] = (lg.cpu().numpy(), [c[0][:, :len(ids)].cpu().numpy() for c in cache], lg2.cpu().numpy())
+    finally:
+        m.prefill_f16_min_tokens = saved
+    (l32, c32, d32), (l16, c16, d16) = out["fp32"], out["f16"]
+    assert rel_err(l16, l32) < 2e-2
+    for a, b in zip(c16, c32):
+        assert rel_err(a, b) < 2e-2
+    assert rel_err(d16, d32) < 2e-2
+    assert m._f16 is not None and len(m._f16) == len(m.layers)
