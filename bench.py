@@ -24,6 +24,7 @@ Also reported on the same line:
                 steps (about 10-30 s).
 Usage: python bench.py [--steps 64] [--warmup 2] [--kernel gate_up|lm_head|down_q6k|...]
        python bench.py --micro   (configs 1 and 2: GEMV shapes, decode attention, QKV kernel)
+       python bench.py --config 3   (8192-token prefill on the matrix cores, decode at 8192)
 """
 
 from __future__ import annotations
@@ -211,6 +212,48 @@ def micro(device: str) -> None:
          shape="896->14x64 + 2x2x64, Q5_0/Q5_0/Q8_0")
 
 
+def config3(eng, arch, path) -> None:
+    """the config-0 model with an 8192-token random-id prompt prefilled on the
+    matrix cores (fp16 operands, fp32 accumulation), then 256 greedy decode steps of the
+    graph-captured step at context ~8192. One JSON line: prefill tok/s, its algorithmic
+    TFLOP/s against the 2.5 PFLOP/s dense fp16 MFMA peak, decode tok/s."""
+    import numpy as np
+    import torch
+    L, steps = 8192, 256
+    prompt = np.random.default_rng(PROMPT_SEED + 3).integers(0, arch.vocab, size=L).tolist()
+    cache = eng._empty_cache(L + steps + 8)
+    graph = eng._build_decode_graph(cache)
+    times = []
+    for _ in range(3):  # the first also builds the fp16 weight copies
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eng.prefill_greedy(prompt, cache)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    pf = statistics.median(times[1:])
+    t0 = time.perf_counter()
+    toks = eng.decode_greedy(graph, steps, None)
+    torch.cuda.synchronize()
+    dec = time.perf_counter() - t0
+    c = eng.cfg
+    hd, nh, nkv, h, f = c.head_dim, c.n_head, c.n_kv_head, c.hidden, c.ffn_dim
+    gemm_flop = 2.0 * L * c.n_layers * (h * (nh + 2 * nkv) * hd + nh * hd * h + 2 * f * h + h * f)
+    attn_flop = 4.0 * hd * nh * (L * (L + 1) / 2) * c.n_layers   # causal: QK^T and P.V
+    tflops = (gemm_flop + attn_flop) / pf / 1e12
+    print(json.dumps({"metric": "config 3: 8192-token prefill on MFMA + decode at context 8192",
+                      "prefill_tok_s": round(L / pf, 1), "prefill_ms": round(pf * 1e3, 2),
+                      "prefill_flop": gemm_flop + attn_flop, "prefill_tflops": round(tflops, 1),
+                      "prefill_mfma_frac": round(tflops / 2500.0, 4), "decode_tok_s": round(steps / dec, 1),
+                      "decode_steps": steps, "context": L, "dtype": "fp16 operands, fp32 accumulate (prefill); fp32 (decode)",
+                      "data": "synthetic config-0 model (seed 0), uniform random prompt ids", "tokens_head": toks[:8],
+                      "gguf_sha256": synth_sha(path)}), flush=True)
+
+
+def synth_sha(path):
+    from pico_hip import synth
+    return synth.sha256(path)
+
+
 def traffic_from_profiles(kernel: str):
     p = ROOT / "profiles" / f"traffic_{kernel}.json"
     if p.exists():
@@ -255,6 +298,8 @@ def main() -> None:
     ap.add_argument("--kernel-iters", type=int, default=400)
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--config", type=int, default=0, choices=(0, 3),
+                    help="3: long-context prefill on the matrix cores + decode at 8192 instead")
     ap.add_argument("--micro", action="store_true",
                     help="BASELINE configs 1 and 2 kernel microbenchmarks (one JSON line each) instead")
     ap.add_argument("--kernel-only", action="store_true",
@@ -282,6 +327,9 @@ def main() -> None:
     eng = Engine(path, device="cuda:0")
     prompt = np.random.default_rng(PROMPT_SEED).integers(0, arch.vocab, size=N_PROMPT).tolist()
     log(f"engine loaded; {torch.cuda.get_device_name(0)}")
+    if args.config == 3:
+        config3(eng, arch, path)
+        return
 
     if args.kernel_only:
         launchers, alg_bytes, kname = kernel_launchers(eng, args.kernel)
