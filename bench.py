@@ -25,6 +25,7 @@ Also reported on the same line:
 Usage: python bench.py [--steps 64] [--warmup 2] [--kernel gate_up|lm_head|down_q6k|...]
        python bench.py --micro   (configs 1 and 2: GEMV shapes, decode attention, QKV kernel)
        python bench.py --config 3   (8192-token prefill on the matrix cores, decode at 8192)
+       python bench.py --config 4   (the 7B-architecture model: 128-token prompt, 256 decode steps)
 """
 
 from __future__ import annotations
@@ -89,15 +90,24 @@ def kernel_launchers(eng, which: str):
                 f"{cfg.hidden}->2x{cfg.ffn_dim}")
         fn = lambda ww: K.qgemv_sum_norm_silu(x, parts, L0.ffn_norm_ut, ww, cfg.eps, layout=XU | YU)
         io = 4 * (cfg.hidden * (3 + cfg.n_kv_head) + cfg.ffn_dim)
+    elif which == "gate_up_norm":
+        # the decode step without attn_gproj (head_dim 128: the 7B): RMSNorm, [gate; up], SiLU
+        w = L0.w_gate_up
+        name = (f"k_qgemv ({K.TYPE_NAMES.get(w.ggml_type, w.ggml_type)}, rmsnorm+SiLU pair) gate/up "
+                f"{cfg.hidden}->2x{cfg.ffn_dim}")
+        fn = lambda ww: K.qgemv_norm_silu(x, L0.ffn_norm_ut, ww, cfg.eps, layout=XU | YU)
+        io = 4 * (cfg.hidden * 2 + cfg.ffn_dim)
     elif which == "lm_head":
-        w, name = m.output, "k_qgemv (Q8_0, rmsnorm, device greedy pick) LM head 896->151936"
+        w = m.output
+        name = f"k_qgemv (Q8_0, rmsnorm, device greedy pick) LM head {cfg.hidden}->{cfg.vocab_size}"
         g = K.GreedyState(m.output.n, 1, eng.device)
         fn = lambda ww: K.qgemv_norm_argmax(x, m.output_norm_ut, ww, cfg.eps, g, layout=XU)
         io = 4 * (cfg.hidden * 2 + cfg.vocab_size)
     elif which in ("down_q6k", "down_q4k"):
-        li = 0 if which == "down_q6k" else 1
+        li = 0 if which == "down_q6k" or len(m.layers) < 2 else 1
         w = m.layers[li].w_down
-        name = f"k_qgemv ({'Q6_K' if li == 0 else 'Q4_K'}, +residual) ffn_down 4864->896"
+        name = (f"k_qgemv ({K.TYPE_NAMES.get(w.ggml_type, w.ggml_type)}, +residual) ffn_down "
+                f"{cfg.ffn_dim}->{cfg.hidden}")
         a = torch.randn(cfg.ffn_dim, device=eng.device)
         fn = lambda ww: K.qgemv(a, ww, residual=x, layout=XU | YU)
         io = 4 * (cfg.ffn_dim + 2 * cfg.hidden)
@@ -249,6 +259,66 @@ def config3(eng, arch, path) -> None:
                       "gguf_sha256": synth_sha(path)}), flush=True)
 
 
+def config4(args) -> None:
+    """Qwen2.5-7B-architecture decoder, random-init N(0,0.02) quantized
+    Q4_K_M-style (Q4_K attn q/k/o + gate/up, Q6_K attn_v + ffn_down, Q8_0 token_embd and an
+    untied Q8_0 LM head), built on the GPU (pico_hip.synth, device draws; seed 0). Batch 1,
+    128-token random prompt (fp32 prefill), 256 greedy decode steps of the HIP-graph step.
+    One JSON line: decode tok/s (median of the timed runs), weight + KV bytes per token and
+    their fraction of 8 TB/s, and the gate/up GEMV timed alone over >= 1 GiB of copies."""
+    import numpy as np
+    import torch
+    from pico_hip import synth
+    from pico_hip.engine import Engine
+    arch = synth.ARCHES["qwen2.5-7b"]
+    t0 = time.time()
+    path = synth.cached(arch, seed=MODEL_SEED, cache_dir=args.model_dir, device="cuda:0", progress=log)
+    log(f"7B model {path} ready in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    eng = Engine(path, device="cuda:0")
+    log(f"engine loaded in {time.time() - t0:.1f}s")
+    n_prompt, steps = 128, 256
+    prompt = np.random.default_rng(PROMPT_SEED + 4).integers(0, arch.vocab, size=n_prompt).tolist()
+    run_decode(eng, prompt, steps, timed=False)
+    samples, toks, pf = [], None, []
+    for _ in range(3):
+        el, p_s, out = run_decode(eng, prompt, steps, timed=True)
+        samples.append(len(out) / el)
+        pf.append(p_s)
+        toks = out
+        log(f"7B decode {samples[-1]:.1f} tok/s")
+    value = statistics.median(samples)
+    c = eng.cfg
+    weight_bytes = eng.model.weight_bytes_per_token()
+    kv_pos = 2 * c.n_kv_head * c.head_dim * 4 * c.n_layers
+    mean_S = n_prompt + (steps + 1) / 2.0
+    bytes_per_token = weight_bytes + kv_pos * (mean_S + 1)
+    dec_gbps = bytes_per_token * value / 1e9
+    launchers, alg_bytes, kname = kernel_launchers(eng, "gate_up_norm")
+    avg_us = time_kernel(launchers, 200)
+    achieved = alg_bytes / (avg_us * 1e-6) / 1e9
+    log(f"{kname}: {avg_us:.2f} us/launch, {achieved:.0f} GB/s")
+    print(json.dumps({
+        "metric": "config 4: batch-1 decode tok/s (7B Q4_K_M arch)", "value": round(value, 2),
+        "unit": "tok/s", "n_gpus": 1, "steps": steps, "ms_per_step": round(1000.0 / value, 4),
+        "higher_is_better": True,
+        "dtype": "fp32 (Q4_K_M-style packed weights, fp32 activations/KV)",
+        "data": "synthetic: random-init N(0,0.02) weights drawn and quantized on the GPU (seed 0), "
+                "128 uniform random prompt ids",
+        "config": {"workload": "BASELINE config 4: Qwen2.5-7B-arch Q4_K_M-style GGUF, batch 1, 128-token "
+                               "prompt, 256 greedy decode steps, HIP-graph step",
+                   "gguf_sha256": synth.sha256(path)},
+        "decode_samples_tok_s": [round(v, 2) for v in samples],
+        "prefill_tok_s": round(n_prompt / statistics.median(pf), 1),
+        "decode_roofline": {"bytes_per_token": int(bytes_per_token), "weight_bytes_per_token": int(weight_bytes),
+                            "achieved": round(dec_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                            "frac": round(dec_gbps / PEAK_HBM_GBPS, 4)},
+        "roofline": {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4), "avg_launch_us": round(avg_us, 3),
+                     "algorithmic_bytes": int(alg_bytes)},
+        "tokens_head": toks[:8]}), flush=True)
+
+
 def synth_sha(path):
     from pico_hip import synth
     return synth.sha256(path)
@@ -298,8 +368,9 @@ def main() -> None:
     ap.add_argument("--kernel-iters", type=int, default=400)
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--config", type=int, default=0, choices=(0, 3),
-                    help="3: long-context prefill on the matrix cores + decode at 8192 instead")
+    ap.add_argument("--config", type=int, default=0, choices=(0, 3, 4),
+                    help="3: long-context prefill on the matrix cores + decode at 8192 instead; "
+                         "4: the 7B-architecture model")
     ap.add_argument("--micro", action="store_true",
                     help="BASELINE configs 1 and 2 kernel microbenchmarks (one JSON line each) instead")
     ap.add_argument("--kernel-only", action="store_true",
@@ -318,6 +389,10 @@ def main() -> None:
 
     if args.micro:
         micro("cuda:0")
+        return
+
+    if args.config == 4:
+        config4(args)
         return
 
     arch = synth.ARCHES["qwen2.5-0.5b"]

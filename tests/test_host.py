@@ -109,3 +109,36 @@ def test_engine_requires_gpu_device(tiny_model):
     from pico_hip.engine import Engine
     with pytest.raises(ValueError, match="GPU only"):
         Engine(tiny_model, device="cpu")
+
+
+@pytest.mark.parametrize("t", [dq.F32, dq.F16, dq.Q8_0, dq.Q5_0, dq.Q4_K, dq.Q6_K])
+def test_torch_quantizer_bytes_equal_numpy(t):
+    """quantize_torch (the GPU model builder's quantizer) gives quantize()'s bytes: random
+    N(0, 0.02) blocks plus all-zero, single-spike, opposite-extreme and tiny-value blocks."""
+    from pico_hip.quantize import quantize, quantize_torch
+    rng = np.random.default_rng(100 + t)
+    x = (rng.standard_normal(256 * 48) * 0.02).astype(np.float32)
+    x[:256] = 0.0
+    x[300], x[301] = 0.5, -0.5
+    x[512:768] = 1e-7
+    x[1024] = -3.0
+    got = quantize_torch(t, torch.from_numpy(x)).numpy()
+    np.testing.assert_array_equal(got, quantize(t, x))
+
+
+def test_synthetic_7b_mix_and_device_build(tmp_path):
+    """The 7B mix (Q4_K attention q/k/o and gate/up, Q6_K attn_v and ffn_down, Q8_0 embedding
+    and an untied Q8_0 output) and a reproducible device build (here on the CPU device)."""
+    from pico_hip import gguf, synth
+    arch = synth.tiny_arch(n_layers=1, hidden=512, n_head=4, n_kv=2, head_dim=128, ffn=512, vocab=300,
+                           name="qwen2.5-7b-tiny", tied=False)
+    h1 = synth.build(tmp_path / "a.gguf", arch, seed=1, device="cpu")
+    assert synth.build(tmp_path / "b.gguf", arch, seed=1, device="cpu") == h1
+    g = gguf.load(tmp_path / "a.gguf")
+    types = {t.name: t.ggml_type for t in g.tensors}
+    assert types["blk.0.attn_q.weight"] == dq.Q4_K and types["blk.0.ffn_up.weight"] == dq.Q4_K
+    assert types["blk.0.attn_v.weight"] == dq.Q6_K and types["blk.0.ffn_down.weight"] == dq.Q6_K
+    assert types["token_embd.weight"] == dq.Q8_0 and types["output.weight"] == dq.Q8_0
+    by = {t.name: t for t in g.tensors}
+    assert bytes(gguf.read_tensor_bytes(g, by["output.weight"])) != \
+        bytes(gguf.read_tensor_bytes(g, by["token_embd.weight"]))
