@@ -24,6 +24,7 @@ Also reported on the same line:
                 steps (about 10-30 s).
 Usage: python bench.py [--steps 64] [--warmup 2] [--kernel gate_up|lm_head|down_q6k|...]
        python bench.py --micro   (configs 1 and 2: GEMV shapes, decode attention, QKV kernel)
+       python bench.py --micro --config 4   (the decode kernels at the 7B shapes)
        python bench.py --config 3   (8192-token prefill on the matrix cores, decode at 8192)
        python bench.py --config 4   (the 7B-architecture model: 128-token prompt, 256 decode steps)
 """
@@ -222,6 +223,82 @@ def micro(device: str) -> None:
          shape="896->14x64 + 2x2x64, Q5_0/Q5_0/Q8_0")
 
 
+def micro7b(device: str) -> None:
+    """The decode kernels at the 7B shapes, one JSON line each: o-proj
+    Q4_K 3584->3584 + residual, RMSNorm + [gate; up] Q4_K 3584->2x18944 + SiLU, ffn_down Q6_K
+    18944->3584 + residual, the fused RMSNorm + QKV (Q4_K/Q4_K/Q6_K) + RoPE, and decode attention
+    (28/4 heads, hd 128) at 384 and 4096 positions. Weights N(0,0.02) drawn and quantized on the
+    GPU; timing as in --micro (graphs over >= 1 GiB of distinct copies)."""
+    import torch
+    from pico_hip import kernels as K
+    from pico_hip.quantize import quantize_torch
+    Q8_0, Q4_K, Q6_K = 8, 12, 14
+    gen = torch.Generator(device=device)
+    gen.manual_seed(7)
+
+    def qweight(t, n, k):
+        w = torch.randn(n * k, generator=gen, device=device) * 0.02
+        return K.pack_weight(quantize_torch(t, w), t, n, k)
+
+    def ncopies(nbytes):
+        return max(2, min(4096, -(-(1 << 30) // nbytes)))
+
+    def emit(case, us, nbytes, **extra):
+        gbps = nbytes / (us * 1e3)
+        print(json.dumps({"micro": case, "us_per_launch": round(us, 3), "algorithmic_bytes": int(nbytes),
+                          "achieved_gbps": round(gbps, 1), "frac": round(gbps / PEAK_HBM_GBPS, 4), **extra}),
+              flush=True)
+
+    h, f, nh, nkv, hd = 3584, 18944, 28, 4, 128
+    XU, YU = K.LAYOUT_X_UT, K.LAYOUT_Y_UT
+    x = torch.randn(h, device=device)
+    nw = K.to_ut(torch.ones(h, device=device))
+    res = torch.randn(h, device=device)
+    act = torch.randn(f, device=device)
+    cases = [
+        ("o_proj Q4_K 3584->3584 +res", Q4_K, h, h, lambda ww: K.qgemv(x, ww, residual=res, layout=XU | YU),
+         4 * 3 * h),
+        ("gate_up Q4_K rmsnorm 3584->2x18944 silu", Q4_K, 2 * f, h,
+         lambda ww: K.qgemv_norm_silu(x, nw, ww, 1e-6, layout=XU | YU), 4 * (2 * h + f)),
+        ("ffn_down Q6_K 18944->3584 +res", Q6_K, h, f, lambda ww: K.qgemv(act, ww, residual=res, layout=XU | YU),
+         4 * (f + 2 * h)),
+    ]
+    for name, t, n, k, fn, io in cases:
+        w0 = qweight(t, n, k)
+        ws = [w0] + [K.QWeight(w0.data.clone(), t, n, k) for _ in range(ncopies(w0.nbytes) - 1)]
+        us = time_kernel([(lambda ww=ww: fn(ww)) for ww in ws], 200)
+        emit("config4_gemv", us, w0.nbytes + io, kernel=name)
+        del ws, w0
+        torch.cuda.empty_cache()
+    wq, wk, wv = qweight(Q4_K, nh * hd, h), qweight(Q4_K, nkv * hd, h), qweight(Q6_K, nkv * hd, h)
+    qkv_bytes = wq.nbytes + wk.nbytes + wv.nbytes
+    trip = [(wq, wk, wv)] + [tuple(K.QWeight(w.data.clone(), w.ggml_type, w.n, w.k) for w in (wq, wk, wv))
+                             for _ in range(ncopies(qkv_bytes) - 1)]
+    bq, bk, bv = (torch.randn(m * hd, device=device) for m in (nh, nkv, nkv))
+    cos = torch.randn(4096, hd // 2, device=device)
+    sin = torch.randn(4096, hd // 2, device=device)
+    pos = torch.tensor([200], device=device)
+    kc = torch.zeros(nkv, 384, hd, device=device)
+    vc = torch.zeros_like(kc)
+    xu = K.to_ut(x)
+    us = time_kernel([(lambda tr=tr: K.qkv_rmsnorm_rope(xu, nw, 1e-6, *tr, bq, bk, bv, cos, sin, pos, kc, vc, nh,
+                                                        layout=XU)) for tr in trip], 200)
+    emit("config4_qkv_rmsnorm_rope", us, qkv_bytes + 4 * (3 * h + 2 * (nh + 2 * nkv) * hd),
+         kernel="3584->28x128 + 2x4x128, Q4_K/Q4_K/Q6_K")
+    del trip
+    q = torch.randn(nh, hd, device=device)
+    for L in (384, 4096):
+        kvb = 2 * nkv * L * hd * 4
+        kvs = [(torch.randn(nkv, L, hd, device=device), torch.randn(nkv, L, hd, device=device))
+               for _ in range(ncopies(kvb))]
+        wsp = K.decode_attn_workspace(nh, nkv, hd, L, device)
+        S = torch.tensor([L], device=device)
+        us = time_kernel([(lambda kv=kv: K.decode_attn(q, kv[0], kv[1], S=S, workspace=wsp, layout=YU))
+                          for kv in kvs], 200)
+        emit("config4_decode_attn", us, kvb + 4 * 2 * nh * hd, positions=L, heads=f"{nh}/{nkv}", head_dim=hd)
+        del kvs
+
+
 def config3(eng, arch, path) -> None:
     """the config-0 model with an 8192-token random-id prompt prefilled on the
     matrix cores (fp16 operands, fp32 accumulation), then 256 greedy decode steps of the
@@ -388,7 +465,7 @@ def main() -> None:
     from pico_hip.engine import Engine
 
     if args.micro:
-        micro("cuda:0")
+        micro7b("cuda:0") if args.config == 4 else micro("cuda:0")
         return
 
     if args.config == 4:

@@ -594,7 +594,14 @@ constexpr int kGemvThreads = 256;
 // activation does not wait for the weights, which were issued later); then each group computes its TPG tasks
 // from registers, issues the loads of its next chunk (grid-stride over chunks when the grid
 // is capped), reduces with DPP butterflies and stores.
-template <int T, int GS, int UPL, int TPG, bool NORM, int MODE>
+//
+// DB (the looped form of large launches): two register sets of chunk loads. The loads of the
+// block's next chunk are issued before the current chunk's dot products, so a chunk's weights
+// are in flight during a whole iteration (dot products, reduction, store) instead of only
+// during the reduction; past the block's last chunk the issue re-reads the current chunk
+// (cached) rather than branching around the loads, which would make the compiler wait for
+// every outstanding load at the join.
+template <int T, int GS, int UPL, int TPG, bool NORM, int MODE, bool DB = false>
 __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
     constexpr int NT = kGemvThreads;
     constexpr int G = NT / GS;
@@ -610,16 +617,18 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
     const int64_t nchunk = (a.n_tasks + CH - 1) / CH;
     int64_t chunk = blockIdx.x;
 
-    typename Fmt<T>::Raw raw[TPG][R][UPL];
+    using RawT = typename Fmt<T>::Raw;
+    RawT raw[TPG][R][UPL];
     Epi epi[TPG];
-    auto issue = [&](int64_t c) {
+    auto issue_to = [&](int64_t c, RawT (&rw)[TPG][R][UPL], Epi (&ep)[TPG]) {
 #pragma unroll
         for (int i = 0; i < TPG; ++i) {
             const int64_t task = c * CH + i * G + gid;
-            load_task<T, GS, UPL, R>(a, task, glane, units, raw[i]);
-            if constexpr (kEpi) epi[i] = load_epi(a, task);
+            load_task<T, GS, UPL, R>(a, task, glane, units, rw[i]);
+            if constexpr (kEpi) ep[i] = load_epi(a, task);
         }
     };
+    auto issue = [&](int64_t c) { issue_to(c, raw, epi); };
     // activation first when it takes at most six float4s per thread (up to 6144 weights per
     // row): the staging then waits for the activation alone while the weights stay in flight.
     // Longer activations would hold too many registers across the weight loads, so there the
@@ -640,8 +649,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
     }
 
     uint64_t best = 0;  // argmax mode: best key of this group's tasks
-    for (; chunk < nchunk; chunk += gridDim.x) {
-        float acc[TPG][R];
+    // dot products of a chunk's tasks from a register set
+    auto dots = [&](const RawT (&rw)[TPG][R][UPL], float (&acc)[TPG][R]) {
 #pragma unroll
         for (int i = 0; i < TPG; ++i)
 #pragma unroll
@@ -649,13 +658,11 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
                 acc[i][rr] = 0.f;
 #pragma unroll
                 for (int t = 0; t < UPL; ++t)
-                    if (glane + GS * t < units) acc[i][rr] += Fmt<T>::dot(raw[i][rr][t], xr[t], xs[t]);
+                    if (glane + GS * t < units) acc[i][rr] += Fmt<T>::dot(rw[i][rr][t], xr[t], xs[t]);
             }
-        Epi cur[TPG];
-#pragma unroll
-        for (int i = 0; i < TPG; ++i) cur[i] = epi[i];
-        const int64_t c0 = chunk;
-        if (chunk + gridDim.x < nchunk) issue(chunk + gridDim.x);
+    };
+    // group reductions, epilogue and stores of chunk c0
+    auto finish = [&](int64_t c0, float (&acc)[TPG][R], const Epi (&cur)[TPG]) {
 #pragma unroll
         for (int i = 0; i < TPG; ++i) {
 #pragma unroll
@@ -679,6 +686,37 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
                 }
             }
         }
+    };
+    if constexpr (DB) {
+        RawT raw2[TPG][R][UPL];
+        Epi epi2[TPG];
+        const int64_t step = gridDim.x;
+        while (true) {
+            float acc[TPG][R];
+            const int64_t c1 = chunk + step;
+            issue_to(c1 < nchunk ? c1 : chunk, raw2, epi2);
+            dots(raw, acc);
+            finish(chunk, acc, epi);
+            if (c1 >= nchunk) break;
+            const int64_t c2 = c1 + step;
+            issue_to(c2 < nchunk ? c2 : c1, raw, epi);
+            dots(raw2, acc);
+            finish(c1, acc, epi2);
+            if (c2 >= nchunk) break;
+            chunk = c2;
+        }
+        if constexpr (MODE == kModeArgmax) argmax_publish<G>(a, best, glane, gid);
+        return;
+    }
+    for (; chunk < nchunk; chunk += gridDim.x) {
+        float acc[TPG][R];
+        dots(raw, acc);
+        Epi cur[TPG];
+#pragma unroll
+        for (int i = 0; i < TPG; ++i) cur[i] = epi[i];
+        const int64_t c0 = chunk;
+        if (chunk + gridDim.x < nchunk) issue(chunk + gridDim.x);
+        finish(c0, acc, cur);
     }
     if constexpr (MODE == kModeArgmax) argmax_publish<G>(a, best, glane, gid);
 }
@@ -726,13 +764,46 @@ inline int64_t argmax_ws_bytes(int64_t n_rows) {
     return kArgmaxPartOff + 8 * (blocks < max_blocks<kModeArgmax>() ? blocks : max_blocks<kModeArgmax>());
 }
 
+// Large plain / SiLU-pair launches (more than kLoopMinBlocks blocks at one task per group,
+// e.g. the 7B gate/up and ffn_down) run in the looped, double-buffered form (k_qgemv DB): a
+// capped grid of blocks that each stage the activation once and then walk their chunks with
+// the next chunk's loads in flight, loop_tpg tasks per group per chunk. The per-block
+// activation staging (up to 2 x 14 KB at k = 3584, 74 KB at k = 18944) would otherwise be
+// repeated for every one or two rows, and then dominated the launch.
+constexpr int kLoopMinBlocks = 2048;
+template <int MODE>
+constexpr bool loop_ok() { return MODE == kModePlain || MODE == kModeSilu; }
+// Tasks per group of the looped form: two when one chunk's raw weights take at most 13
+// registers per lane (two register sets of them are live across the dot products), else one.
+template <int T, int UPL, int R>
+constexpr int loop_tpg() {
+    constexpr int per = R * UPL * (int)(sizeof(typename Fmt<T>::Raw) / 4);
+    return per <= 13 ? 2 : 1;
+}
+// Grid of the looped form: whole-block groups (GS = 256, long rows) hold more registers per
+// lane, so fewer of their blocks are resident at once.
+template <int GS>
+constexpr int64_t loop_blocks() { return GS == 256 ? 1024 : 2048; }
+
 template <int T, int GS, int UPL, bool NORM, int MODE>
 void launch_qgemv_shape(const GemvArgs& a, hipStream_t s) {
     constexpr int TPG = tasks_per_group<MODE>();
     constexpr int CH = (kGemvThreads / GS) * TPG;
     int64_t blocks = (a.n_tasks + CH - 1) / CH;
-    if (blocks > max_blocks<MODE>()) blocks = max_blocks<MODE>();
     const size_t lds = a.k <= kStageMaxK ? (size_t)(a.k / 32) * kUnitStride * 4 : 0;
+    if constexpr (loop_ok<MODE>()) {
+        if (blocks > kLoopMinBlocks) {
+            constexpr int R = MODE == kModeSilu ? 2 : 1;
+            constexpr int TL = loop_tpg<T, UPL, R>();
+            constexpr int CHL = (kGemvThreads / GS) * TL;
+            int64_t bl = (a.n_tasks + CHL - 1) / CHL;
+            if (bl > loop_blocks<GS>()) bl = loop_blocks<GS>();
+            hipLaunchKernelGGL((k_qgemv<T, GS, UPL, TL, NORM, MODE, true>), dim3((unsigned)bl),
+                               dim3(kGemvThreads), lds, s, a);
+            return;
+        }
+    }
+    if (blocks > max_blocks<MODE>()) blocks = max_blocks<MODE>();
     hipLaunchKernelGGL((k_qgemv<T, GS, UPL, TPG, NORM, MODE>), dim3((unsigned)blocks),
                        dim3(kGemvThreads), lds, s, a);
     if constexpr (MODE == kModeArgmax)

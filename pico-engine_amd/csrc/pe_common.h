@@ -27,6 +27,15 @@ PE_DEV float h2f(uint32_t h) {
     return __uint_as_float(sign | __float_as_uint(mag));
 }
 
+// fp16 bits -> fp32 with the hardware conversion (v_cvt_f32_f16), for the dot products. The
+// kernels run with fp16 and fp32 denormals preserved (denorm mode 3 in every kernel
+// descriptor: no flush flags are used), so the value is exact for every finite fp16,
+// subnormals included; unlike h2f it may quiet a signalling NaN's payload, which only the
+// bit-exact dequantization (h2f) has to keep.
+PE_DEV float h2f_fast(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
 // fp32 -> fp16 (round to nearest even) -> fp32, for the reference's fp16 output rounding.
 PE_DEV float round_to_f16(float v) { return __half2float(__float2half_rn(v)); }
 
@@ -185,7 +194,7 @@ struct Fmt<PE_TYPE_Q8_0> {
 #pragma unroll
         for (int w = 0; w < 8; ++w)
             acc = dot4(word_of(w < 4 ? r.a : r.b, w & 3) ^ 0x80808080u, x + 4 * w, acc);
-        return fmaf(-128.f, xs.all, acc) * h2f(r.d);
+        return fmaf(-128.f, xs.all, acc) * h2f_fast(r.d);
     }
     static PE_DEV void dequant(const Raw& r, float* w) {
         const float d = h2f(r.d);
@@ -229,7 +238,7 @@ struct Fmt<PE_TYPE_Q5_0> {
             acc = dot4(lo, x + 4 * w, acc);
             acc = dot4(hi, x + 16 + 4 * w, acc);
         }
-        return fmaf(-16.f, xs.all, acc) * h2f(r.d);
+        return fmaf(-16.f, xs.all, acc) * h2f_fast(r.d);
     }
     static PE_DEV void dequant(const Raw& r, float* w) {
         const float d = h2f(r.d);
@@ -258,29 +267,41 @@ struct Fmt<PE_TYPE_Q4_K> {
         r.head = *reinterpret_cast<const int4*>(t.base + t.nrows * t.nb * 128 + blk * 16);
         r.sub = j;
     }
+    // 6-bit scale and min of sub-block j (the packing of k4_scale_min): bytes j%4 of the three
+    // scale words, picked with bit-field extracts at a run-time offset instead of indexing a
+    // byte array (which compiles to a compare/select chain per byte).
     static PE_DEV void scales(const Raw& r, float& a, float& m) {
-        uint8_t s[12];
-#pragma unroll
-        for (int i = 0; i < 12; ++i) s[i] = (uint8_t)ubyte(word_of(r.head, 1 + (i >> 2)), i & 3);
-        int sc, mn;
-        k4_scale_min(s, r.sub, sc, mn);
-        a = (float)sc * h2f((uint32_t)r.head.x & 0xFFFFu);  // exact: 6-bit x 11-bit
-        m = (float)mn * h2f((uint32_t)r.head.x >> 16);      // exact
+        const int j = r.sub, off = 8 * (j & 3);
+        const uint32_t b1 = __builtin_amdgcn_ubfe((uint32_t)r.head.y, off, 8);  // s[j % 4]
+        const uint32_t b2 = __builtin_amdgcn_ubfe((uint32_t)r.head.z, off, 8);  // s[j % 4 + 4]
+        const uint32_t b3 = __builtin_amdgcn_ubfe((uint32_t)r.head.w, off, 8);  // s[j % 4 + 8]
+        const bool lo = j < 4;
+        const uint32_t sc = lo ? (b1 & 63u) : ((b3 & 0xFu) | ((b1 >> 6) << 4));
+        const uint32_t mn = lo ? (b2 & 63u) : ((b3 >> 4) | ((b2 >> 6) << 4));
+        // exact: 6-bit x 11-bit; a NaN d or dmin gives a quiet NaN either way (the product
+        // quiets it), so the hardware conversion matches the bit-field one here
+        a = (float)sc * h2f_fast((uint32_t)r.head.x & 0xFFFFu);
+        m = (float)mn * h2f_fast((uint32_t)r.head.x >> 16);
     }
     static PE_DEV uint32_t nib(const Raw& r, int i) {
         const int4& v = i < 16 ? r.lo : r.hi;
         const uint32_t b = ubyte(word_of(v, (i & 15) >> 2), i & 3);
         return (r.sub & 1) ? (b >> 4) : (b & 0xFu);
     }
+    // The high nibbles are used in place (masked, not shifted down): each code byte is then
+    // 16 x nib, so the sum is exactly 16 x the sum of nib x (a power-of-two scale commutes with
+    // every rounding) and the 1/16 goes into the scale. A run-time shift of the word would be
+    // folded by the compiler into one bit-field extract per byte instead.
     static PE_DEV float dot(const Raw& r, const float* x, const UnitSums& xs) {
         float a, m;
         scales(r, a, m);
-        const int sh = 4 * (r.sub & 1);
+        const bool hi = r.sub & 1;
+        const uint32_t mask = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
         float dq = 0.f;
 #pragma unroll
         for (int w = 0; w < 8; ++w)
-            dq = dot4((word_of(w < 4 ? r.lo : r.hi, w & 3) >> sh) & 0x0F0F0F0Fu, x + 4 * w, dq);
-        return fmaf(a, dq, -(m * xs.all));
+            dq = dot4(word_of(w < 4 ? r.lo : r.hi, w & 3) & mask, x + 4 * w, dq);
+        return fmaf(hi ? a * 0.0625f : a, dq, -(m * xs.all));
     }
     static PE_DEV void dequant(const Raw& r, float* w) {
         float a, m;
@@ -339,7 +360,7 @@ struct Fmt<PE_TYPE_Q6_K> {
             else p1 = dot4(c, x + 4 * w, p1);
         }
         const float h0 = fmaf(-32.f, xs.lo, p0), h1 = fmaf(-32.f, xs.all - xs.lo, p1);
-        return h2f(r.d) * fmaf((float)sext8(r.sc, 0), h0, (float)sext8(r.sc, 1) * h1);
+        return h2f_fast(r.d) * fmaf((float)sext8(r.sc, 0), h0, (float)sext8(r.sc, 1) * h1);
     }
     static PE_DEV void dequant(const Raw& r, float* w) {
         const float d = h2f(r.d);

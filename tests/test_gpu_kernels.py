@@ -194,6 +194,49 @@ def test_qgemm_prefill(K, m, t, k, n):
     assert np.all(np.isnan(got[:, :3])) and np.all(np.isnan(got[:, 3 + n:]))
 
 
+# Launches of more than 2048 blocks at one task per group run the looped form (capped grid,
+# several tasks per group, next chunk's loads in flight): plain with residual in both layouts,
+# RMSNorm, and the SiLU pair, one shape per lane-group width.
+LOOP_SHAPES = [(dq.Q8_0, 896, 20000), (dq.Q4_K, 3584, 6016), (dq.Q5_0, 4864, 2100),
+               (dq.Q6_K, 18944, 2112)]
+
+
+@pytest.mark.parametrize("t,k,n", LOOP_SHAPES, ids=[f"{t}-{k}x{n}" for t, k, n in LOOP_SHAPES])
+def test_qgemv_looped_form(K, t, k, n):
+    raw = quantized_normal(t, n, k, seed=k + 5 * n)
+    w = qweight(K, t, raw, n, k)
+    W = dequant_rows(t, raw, n, k)
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(k).astype(np.float32)
+    r = rng.standard_normal(n).astype(np.float32)
+    xt, rt = torch.from_numpy(x).to(DEV), torch.from_numpy(r).to(DEV)
+    nat = K.qgemv(xt, w, residual=rt)
+    assert rel_err(nat.cpu().numpy(), closed.gemv(W, x, residual=r)) < TOL
+    if n % 32 == 0:
+        ut = K.qgemv(K.to_ut(xt), w, residual=K.to_ut(rt), layout=K.LAYOUT_X_UT | K.LAYOUT_Y_UT)
+        assert rel_err(K.from_ut(ut).cpu().numpy(), nat.cpu().numpy()) < 1e-6
+    if k <= 8192:
+        nw = (rng.standard_normal(k) * 0.5).astype(np.float32)
+        y = K.qgemv_norm(xt, torch.from_numpy(nw).to(DEV), w, 1e-6).cpu().numpy()
+        assert rel_err(y, closed.gemv(W, closed.rmsnorm(x, nw, 1e-6))) < TOL
+    assert torch.equal(K.qgemv(xt, w, residual=rt), nat)  # deterministic
+
+
+def test_qgemv_rmsnorm_silu_looped_form(K):
+    t, k, ffn = dq.Q4_K, 3584, 4200
+    raw = quantized_normal(t, 2 * ffn, k, seed=ffn)
+    w = qweight(K, t, raw, 2 * ffn, k)
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal(k).astype(np.float32)
+    nw = rng.standard_normal(k).astype(np.float32)
+    xt, nt = torch.from_numpy(x).to(DEV), torch.from_numpy(nw).to(DEV)
+    act = K.qgemv_norm_silu(xt, nt, w, 1e-6).cpu().numpy()
+    gu = closed.gemv(dequant_rows(t, raw, 2 * ffn, k), closed.rmsnorm(x, nw, 1e-6))
+    assert rel_err(act, closed.silu_mul(gu[:ffn], gu[ffn:])) < TOL
+    ut = K.qgemv_norm_silu(K.to_ut(xt), K.to_ut(nt), w, 1e-6, layout=K.LAYOUT_X_UT)
+    assert rel_err(ut.cpu().numpy(), act) < 1e-6
+
+
 # ---- attention ----------------------------------------------------------------------------
 
 def _kv(rng, n_kv, cap, hd):
