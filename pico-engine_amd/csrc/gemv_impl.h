@@ -295,7 +295,10 @@ PE_DEV float load_activation(const GemvArgs& a, int glane, int units, float (&xr
 // does before them (vector loads retire in issue order) can leave them in flight. Whole-block
 // groups (GS = 256, the ffn_down rows) are the exception: up to 40% of their lanes hold no unit
 // (152 units of 256 lanes), and there skipping those lanes' loads is measured to be faster.
-template <int T, int GS, int UPL, int R>
+// The double-buffered loop (CLAMP) clamps in every group width: a lane-divergent branch
+// around the loads would make the compiler wait for all outstanding loads after it, the
+// prefetched chunk's included.
+template <int T, int GS, int UPL, int R, bool CLAMP = false>
 PE_DEV void load_task(const GemvArgs& a, int64_t task, int glane, int units,
                       typename Fmt<T>::Raw (&raw)[R][UPL]) {
     const int64_t tc = task < a.n_tasks ? task : a.n_tasks - 1;
@@ -304,7 +307,7 @@ PE_DEV void load_task(const GemvArgs& a, int64_t task, int glane, int units,
 #pragma unroll
         for (int t = 0; t < UPL; ++t) {
             const int u = glane + GS * t;
-            if constexpr (GS == 256) {
+            if constexpr (GS == 256 && !CLAMP) {
                 if (u < units) Fmt<T>::load(a.w, tc + rr * a.up_off, u, raw[rr][t]);
             } else {
                 Fmt<T>::load(a.w, tc + rr * a.up_off, u < units ? u : units - 1, raw[rr][t]);
@@ -624,7 +627,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
 #pragma unroll
         for (int i = 0; i < TPG; ++i) {
             const int64_t task = c * CH + i * G + gid;
-            load_task<T, GS, UPL, R>(a, task, glane, units, rw[i]);
+            load_task<T, GS, UPL, R, DB>(a, task, glane, units, rw[i]);
             if constexpr (kEpi) ep[i] = load_epi(a, task);
         }
     };
@@ -798,7 +801,9 @@ void launch_qgemv_shape(const GemvArgs& a, hipStream_t s) {
             constexpr int CHL = (kGemvThreads / GS) * TL;
             int64_t bl = (a.n_tasks + CHL - 1) / CHL;
             if (bl > loop_blocks<GS>()) bl = loop_blocks<GS>();
-            hipLaunchKernelGGL((k_qgemv<T, GS, UPL, TL, NORM, MODE, true>), dim3((unsigned)bl),
+            // double buffering at one unit per lane; with several (long rows) the second
+            // register set would cut the kernel to one wave per SIMD
+            hipLaunchKernelGGL((k_qgemv<T, GS, UPL, TL, NORM, MODE, UPL == 1>), dim3((unsigned)bl),
                                dim3(kGemvThreads), lds, s, a);
             return;
         }

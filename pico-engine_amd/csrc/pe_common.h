@@ -348,14 +348,18 @@ struct Fmt<PE_TYPE_Q6_K> {
         return (int)(low4 | (((hb >> (2 * r.q)) & 3u) << 4)) - 32;
     }
     // unsigned 6-bit codes of 4 elements at once; the -32 offset folds into the half sums
+    // The two high bits of a code sit at bits 2q, 2q+1 of each qh byte; rotating the whole
+    // word right by (2q - 4) mod 32 moves them to bits 4, 5 of the same byte (one funnel
+    // shift instead of a shift, a mask and a shift back).
     static PE_DEV float dot(const Raw& r, const float* x, const UnitSums& xs) {
-        const int lsh = r.q >= 2 ? 4 : 0, hsh = 2 * r.q;
+        const int lsh = r.q >= 2 ? 4 : 0, rot = (2 * r.q + 28) & 31;
         float p0 = 0.f, p1 = 0.f;
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
             const uint32_t L = word_of(w < 4 ? r.l0 : r.l1, w & 3);
             const uint32_t H = word_of(w < 4 ? r.h0 : r.h1, w & 3);
-            const uint32_t c = ((L >> lsh) & 0x0F0F0F0Fu) | (((H >> hsh) & 0x03030303u) << 4);
+            const uint32_t c = ((L >> lsh) & 0x0F0F0F0Fu) |
+                               (__builtin_amdgcn_alignbit(H, H, rot) & 0x30303030u);
             if (w < 4) p0 = dot4(c, x + 4 * w, p0);
             else p1 = dot4(c, x + 4 * w, p1);
         }
