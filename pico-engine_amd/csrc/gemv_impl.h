@@ -307,10 +307,11 @@ PE_DEV void load_task(const GemvArgs& a, int64_t task, int glane, int units,
 #pragma unroll
         for (int t = 0; t < UPL; ++t) {
             const int u = glane + GS * t;
+            const uint32_t row = (uint32_t)(tc + rr * a.up_off);
             if constexpr (GS == 256 && !CLAMP) {
-                if (u < units) Fmt<T>::load(a.w, tc + rr * a.up_off, u, raw[rr][t]);
+                if (u < units) Fmt<T>::load32(a.w, row, u, raw[rr][t]);
             } else {
-                Fmt<T>::load(a.w, tc + rr * a.up_off, u < units ? u : units - 1, raw[rr][t]);
+                Fmt<T>::load32(a.w, row, u < units ? u : units - 1, raw[rr][t]);
             }
         }
 }
@@ -784,9 +785,11 @@ constexpr int loop_tpg() {
     return per <= 13 ? 2 : 1;
 }
 // Grid of the looped form: whole-block groups (GS = 256, long rows) hold more registers per
-// lane, so fewer of their blocks are resident at once.
+// lane, so fewer of their blocks are resident at once (two per CU: 512 blocks, one round).
+// Swept on MI355X at the 7B shapes: 512 / 1024 / 2048 / 4096 blocks and one or two tasks per
+// group change gate/up by under 10%; ffn_down is fastest at 512.
 template <int GS>
-constexpr int64_t loop_blocks() { return GS == 256 ? 1024 : 2048; }
+constexpr int64_t loop_blocks() { return GS == 256 ? 512 : 2048; }
 
 template <int T, int GS, int UPL, bool NORM, int MODE>
 void launch_qgemv_shape(const GemvArgs& a, hipStream_t s) {
