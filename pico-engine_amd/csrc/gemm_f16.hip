@@ -7,11 +7,13 @@
 // matmul calls of model.py:177, :213, :218-223 (L > 1).
 //
 // Tiling: a 256-thread workgroup computes a 128 x 128 tile of C as 2 x 2 waves of 64 x 64 =
-// 4 x 4 MFMA tiles of 16 x 16. Per 32-wide K step a lane holds, for each of its 4 row tiles
-// and 4 column tiles, 8 consecutive k of one A row and of one W row (the MFMA operand layout:
-// lane i + 16 (k / 8) holds row i, k .. k + 7), read straight from memory as 16-byte loads;
-// the next step's loads are in flight while the current step's 16 MFMAs run. Rows and columns
-// past M / N are clamped on load and masked on store.
+// 4 x 4 MFMA tiles of 16 x 16. Per 32-wide K step the workgroup copies the A tile (fp32 ->
+// fp16) and the W tile into LDS with coalesced 16-byte loads (each A and W row is read from
+// global memory once per workgroup instead of once per wave), double-buffered: the next step's
+// global loads are in flight while the current step's 16 MFMAs per wave run on the other LDS
+// buffer, one barrier per step. LDS rows are padded to 40 halves (80 bytes), which makes the
+// 16-byte operand reads of 8 consecutive rows cover all 32 banks. Rows and columns past M / N
+// are clamped on load and masked on store.
 #include "pe_common.h"
 
 namespace pe {
@@ -33,71 +35,125 @@ struct GemmF16Args {
 
 constexpr int kGfTile = 128;  // workgroup tile (M and N)
 constexpr int kGfK = 32;      // K step
+constexpr int kGfLds = 40;    // LDS row stride in halves (32 + 8 padding)
 
-struct GfRaw {
-    float4 a[4][2];  // 4 row tiles x 8 fp32
-    uint4 b[4];      // 4 column tiles x 8 fp16
-};
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 
-PE_DEV h8 to_h8(float4 lo, float4 hi) {
-    h8 r;
-    r[0] = (_Float16)lo.x; r[1] = (_Float16)lo.y; r[2] = (_Float16)lo.z; r[3] = (_Float16)lo.w;
-    r[4] = (_Float16)hi.x; r[5] = (_Float16)hi.y; r[6] = (_Float16)hi.z; r[7] = (_Float16)hi.w;
-    return r;
+// Tile of this workgroup. Workgroups go to the 8 XCDs round robin (linear id % 8), and each XCD
+// has its own 4 MB L2; the linear id is remapped so that each XCD walks a contiguous range of
+// tiles in an order grouped by kGfGroup row tiles, so the workgroups resident on one XCD at a
+// time share a few A row tiles and W column tiles in that L2 instead of touching all of them.
+// Grids whose tile count is not a multiple of 8 keep the plain row-major order.
+constexpr int kGfGroup = 8;
+PE_DEV void gemm_tile_of_block(int64_t& tm, int64_t& tn) {
+    const int64_t NT = gridDim.x, MT = gridDim.y, total = NT * MT;
+    const int64_t lin = (int64_t)blockIdx.y * NT + blockIdx.x;
+    int64_t t = lin;
+    if (total % 8 == 0) t = (lin % 8) * (total / 8) + lin / 8;
+    const int64_t per_group = (int64_t)kGfGroup * NT;
+    const int64_t g = t / per_group, r = t % per_group;
+    const int64_t m_base = g * kGfGroup;
+    const int64_t gm = (MT - m_base) < kGfGroup ? (MT - m_base) : kGfGroup;  // rows in this group
+    tm = m_base + r % gm;
+    tn = r / gm;
 }
 
 template <bool BIAS, bool RES>
 __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const int64_t m0 = (int64_t)blockIdx.y * kGfTile + (w >> 1) * 64;
-    const int64_t n0 = (int64_t)blockIdx.x * kGfTile + (w & 1) * 64;
-    const int li = l & 15, lk = (l >> 4) * 8;
-    const float* arow[4];
-    const _Float16* wrow[4];
+    __shared__ __align__(16) _Float16 As[2][kGfTile * kGfLds];
+    __shared__ __align__(16) _Float16 Ws[2][kGfTile * kGfLds];
+    const int tid = threadIdx.x;
+    const int w = tid >> 6, l = tid & 63;
+    int64_t tm, tn;
+    gemm_tile_of_block(tm, tn);
+    const int64_t bm = tm * kGfTile, bn = tn * kGfTile;
+    const int wm = (w >> 1) * 64, wn = (w & 1) * 64;  // the wave's 64 x 64 part of the tile
+    const int li = l & 15, lk = (l >> 4) * 8;         // MFMA operand: row li, k lk .. lk + 7
+
+    // global -> registers: A rows ar + 32 i (i < 4), fp32 columns ac .. ac + 3 of the K step;
+    // W rows wr + 64 i (i < 2), fp16 columns wc .. wc + 7
+    const int ar = tid >> 3, ac = (tid & 7) * 4;
+    const int wr = tid >> 2, wc = (tid & 3) * 8;
+    const float* ap[4];
+    const _Float16* wp[2];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const int64_t m = m0 + 16 * t + li, n = n0 + 16 * t + li;
-        arow[t] = p.a + (m < p.M ? m : p.M - 1) * p.lda + lk;
-        wrow[t] = p.w + (n < p.N ? n : p.N - 1) * p.K + lk;
+    for (int i = 0; i < 4; ++i) {
+        const int64_t m = bm + ar + 32 * i;
+        ap[i] = p.a + (m < p.M ? m : p.M - 1) * p.lda + ac;
     }
-    auto load = [&](int64_t k0, GfRaw& r) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            r.a[t][0] = *reinterpret_cast<const float4*>(arow[t] + k0);
-            r.a[t][1] = *reinterpret_cast<const float4*>(arow[t] + k0 + 4);
-            r.b[t] = *reinterpret_cast<const uint4*>(wrow[t] + k0);
-        }
-    };
+    for (int i = 0; i < 2; ++i) {
+        const int64_t n = bn + wr + 64 * i;
+        wp[i] = p.w + (n < p.N ? n : p.N - 1) * p.K + wc;
+    }
+    float4 ra[4];
+    uint4 rw[2];
     f4v acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f4v{0.f, 0.f, 0.f, 0.f};
 
-    GfRaw cur, nxt;
-    load(0, cur);
-    for (int64_t k0 = 0; k0 < p.K; k0 += kGfK) {
-        if (k0 + kGfK < p.K) load(k0 + kGfK, nxt);
-        h8 av[4], bv[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            av[t] = to_h8(cur.a[t][0], cur.a[t][1]);
-            bv[t] = __builtin_bit_cast(h8, cur.b[t]);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
-        cur = nxt;
+// Global loads of K step kk into ra / rw.
+#define PE_GF_GLOAD(kk)                                                                        \
+    do {                                                                                       \
+        const int64_t k0_ = (int64_t)(kk) * kGfK;                                             \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) ra[i] =                                  \
+            *reinterpret_cast<const float4*>(ap[i] + k0_);                                     \
+        _Pragma("unroll") for (int i = 0; i < 2; ++i) rw[i] =                                  \
+            *reinterpret_cast<const uint4*>(wp[i] + k0_);                                      \
+    } while (0)
+// ra (rounded to fp16) / rw into LDS buffer b.
+#define PE_GF_LSTORE(b)                                                                        \
+    do {                                                                                       \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                        \
+            const h4 v_ = {(_Float16)ra[i].x, (_Float16)ra[i].y, (_Float16)ra[i].z,            \
+                           (_Float16)ra[i].w};                                                 \
+            *reinterpret_cast<h4*>(&As[b][(ar + 32 * i) * kGfLds + ac]) = v_;                  \
+        }                                                                                      \
+        _Pragma("unroll") for (int i = 0; i < 2; ++i)                                          \
+            *reinterpret_cast<uint4*>(&Ws[b][(wr + 64 * i) * kGfLds + wc]) = rw[i];            \
+    } while (0)
+// One K step from LDS buffer b (a literal): the next step's global loads go out first, then
+// the 16 MFMAs per wave, then the loaded step is stored into the other buffer. The loads and
+// stores are unconditional (the last step re-reads its own K slice into the unused buffer): a
+// branch around them made the compiler copy the loaded registers at the join.
+#define PE_GF_STEP(kt, b)                                                                      \
+    do {                                                                                       \
+        PE_GF_GLOAD((kt) + 1 < nk ? (kt) + 1 : (kt));                                          \
+        h8 av_[4], bv_[4];                                                                     \
+        _Pragma("unroll") for (int t = 0; t < 4; ++t) {                                        \
+            av_[t] = *reinterpret_cast<const h8*>(&As[b][(wm + 16 * t + li) * kGfLds + lk]);   \
+            bv_[t] = *reinterpret_cast<const h8*>(&Ws[b][(wn + 16 * t + li) * kGfLds + lk]);   \
+        }                                                                                      \
+        _Pragma("unroll") for (int i = 0; i < 4; ++i)                                          \
+            _Pragma("unroll") for (int j = 0; j < 4; ++j) acc[i][j] =                          \
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(av_[i], bv_[j], acc[i][j], 0, 0, 0);    \
+        PE_GF_LSTORE((b) ^ 1);                                                                 \
+        __syncthreads();                                                                       \
+    } while (0)
+
+    const int nk = (int)(p.K / kGfK);
+    PE_GF_GLOAD(0);
+    PE_GF_LSTORE(0);
+    __syncthreads();
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {  // unrolled by two: the LDS buffers alternate at compile time
+        PE_GF_STEP(kt, 0);
+        PE_GF_STEP(kt + 1, 1);
     }
+    if (kt < nk) PE_GF_STEP(kt, 0);
+#undef PE_GF_STEP
+#undef PE_GF_LSTORE
+#undef PE_GF_GLOAD
 
     // D[4 (l / 16) + r][l % 16] of tile (i, j) -> row m0 + 16 i + 4 (l / 16) + r, column n0 + 16 j + l % 16
+    const int64_t m0 = bm + wm, n0 = bn + wn;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int64_t n = n0 + 16 * j + li;
         if (n >= p.N) continue;
-        const float b = BIAS ? p.bias[n] : 0.f;
+        const float bb = BIAS ? p.bias[n] : 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -105,7 +161,7 @@ __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
                 const int64_t m = m0 + 16 * i + 4 * (l >> 4) + r;
                 if (m >= p.M) continue;
                 float v = acc[i][j][r];
-                if (BIAS) v += b;
+                if (BIAS) v += bb;
                 if (RES) v += p.res[m * p.ldr + n];
                 p.c[m * p.ldc + n] = v;
             }
