@@ -823,6 +823,16 @@ template <int T, bool NORM, int MODE>
 int launch_qgemv_mode(const GemvArgs& a, hipStream_t s) {
     Shape sh;
     if (!pick_shape(a.k / 32, sh)) return PE_ERR_SHAPE;
+    // Looped launches with rows of 65..128 units run one wave per row group with two units per
+    // lane instead of two waves with one: the row sum is then a wave-local DPP reduction (no
+    // LDS exchange and no block barriers inside the loop), and each lane reduces once per two
+    // units instead of once per unit.
+    if constexpr (loop_ok<MODE>()) {
+        if (sh.gs == 128 && sh.upl == 1 && (a.n_tasks + 1) / 2 > kLoopMinBlocks) {
+            launch_qgemv_shape<T, 64, 2, NORM, MODE>(a, s);
+            return launch_status();
+        }
+    }
     switch (sh.gs * 16 + sh.upl) {
 #define PE_CASE(G, U) case G * 16 + U: launch_qgemv_shape<T, G, U, NORM, MODE>(a, s); break;
         PE_SHAPE_CASES(PE_CASE)
