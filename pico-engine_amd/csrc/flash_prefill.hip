@@ -7,12 +7,16 @@
 // with q, k, v rounded to fp16 as they are read, scores, softmax and the output accumulated
 // in fp32 (v_mfma_f32_16x16x32_f16), the probabilities rounded to fp16 for the P.V product.
 //
-// Workgroup = (64-query block, query head), 4 waves of 16 queries. Per 64-key block the
-// workgroup stages K (row-major) and V (transposed, so a lane's MFMA operand -- 8 consecutive
-// keys of one dimension -- is one 16-byte LDS read) in fp16; each wave computes its 16 x 64
-// score tile (8 MFMAs), the online-softmax update with DPP row reductions, writes P to LDS in
-// the operand layout and accumulates O += P V (8 MFMAs). The heaviest query blocks (most keys)
-// are scheduled first.
+// Workgroup = (query block, kv head): one wave per (query head of the group, 16-query tile),
+// group x QB/16 waves (QB = 16 * max(1, 16 / group): 14 waves of 32 queries for the
+// 7-heads-per-kv-head models), so each 64-key block of K and V is read from HBM and staged in
+// LDS once for all the query heads that share it. K is staged row-major and V transposed (a
+// lane's MFMA operand -- 8 consecutive keys of one dimension -- is one 16-byte LDS read), both
+// in fp16; the next block's K/V loads are issued before the current block's MFMAs. Each wave
+// computes its 16 x 64 score tile (8 MFMAs), the online-softmax update in the exp2 domain
+// (scale * log2 e folded into the scores) with DPP row reductions, writes P to its own LDS
+// tile (a wave-local handoff, no block barrier) and accumulates O += P V (8 MFMAs). The
+// heaviest query blocks (most keys) are scheduled first.
 #include "pe_common.h"
 
 namespace pe {
@@ -21,9 +25,13 @@ typedef _Float16 fh8 __attribute__((ext_vector_type(8)));
 typedef float fv4 __attribute__((ext_vector_type(4)));
 
 constexpr int kFpHd = 64;
-constexpr int kFpQ = 64;       // queries per workgroup
 constexpr int kFpKeys = 64;    // keys per block
 constexpr int kFpRow = 72;     // fp16 elements per LDS row (64 + 8 padding: 144 bytes)
+constexpr int kFpMaxWaves = 16;
+
+// Queries per workgroup for a group size (query heads per kv head): 16 per wave, at most
+// kFpMaxWaves waves per workgroup.
+inline int flash_qb(int group) { return 16 * (group >= 16 ? 1 : 16 / group); }
 
 struct FlashParams {
     const float* q;      // (L, n_head, 64), token rows q_stride floats apart
@@ -62,20 +70,22 @@ PE_DEV fh8 f8_to_h8(float4 a, float4 b) {
     return r;
 }
 
-__global__ __launch_bounds__(256) void k_flash_prefill(FlashParams p) {
-    __shared__ _Float16 ks[kFpKeys * kFpRow];   // K block, [key][dim]
-    __shared__ _Float16 vt[kFpHd * kFpRow];     // V block transposed, [dim][key]
-    __shared__ _Float16 ps[4][16 * kFpRow];     // per wave: P, [query][key]
-    const int t = threadIdx.x, w = t >> 6, l = t & 63;
+__global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_size) {
+    __shared__ __align__(16) _Float16 ks[kFpKeys * kFpRow];         // K block, [key][dim]
+    __shared__ __align__(16) _Float16 vt[kFpHd * kFpRow];           // V block transposed, [dim][key]
+    __shared__ __align__(16) _Float16 ps[kFpMaxWaves][16 * kFpRow]; // per wave: P, [query][key]
+    const int t = threadIdx.x, nt = blockDim.x, w = t >> 6, l = t & 63;
     const int li = l & 15, lg = l >> 4;
-    const int64_t nqb = (p.L + kFpQ - 1) / kFpQ;
+    const int64_t nqb = (p.L + qb_size - 1) / qb_size;
     const int64_t qb = nqb - 1 - (int64_t)blockIdx.x;  // heaviest blocks first
-    const int h = blockIdx.y, kvh = h / p.group;
-    const int64_t q0 = qb * kFpQ + 16 * w;            // this wave's first query (token index)
+    const int kvh = blockIdx.y;
+    const int h = kvh * p.group + w % p.group;         // this wave's query head
+    const int64_t q0 = qb * qb_size + 16 * (w / p.group);  // this wave's first query (token index)
     const float* kb = p.k + (int64_t)kvh * p.capacity * kFpHd;
     const float* vb = p.v + (int64_t)kvh * p.capacity * kFpHd;
     const int64_t n_keys = p.pos0 + p.L;              // cache positions written
     const float NEG_INF = -__builtin_huge_valf();
+    const float sl2 = p.scale * 1.4426950408889634f;  // scores in log2 units: exp(x) = exp2(x log2 e)
 
     // Q operand of this wave: row li (query q0 + li), dims 32 s + 8 lg .. + 8, s = 0, 1
     fh8 qa[2];
@@ -100,24 +110,42 @@ __global__ __launch_bounds__(256) void k_flash_prefill(FlashParams p) {
 #pragma unroll
     for (int d = 0; d < 4; ++d) o[d] = fv4{0.f, 0.f, 0.f, 0.f};
 
-    const int64_t q_last = (qb + 1) * kFpQ - 1 < p.L - 1 ? (qb + 1) * kFpQ - 1 : p.L - 1;
+    const int64_t q_last = (qb + 1) * qb_size - 1 < p.L - 1 ? (qb + 1) * qb_size - 1 : p.L - 1;
     const int64_t key_end = p.pos0 + q_last + 1;      // keys this workgroup can see
-    for (int64_t j0 = 0; j0 < key_end; j0 += kFpKeys) {
-        // stage K and V (fp32 -> fp16): 64 keys x 64 dims = 1024 float4 each, 4 per thread
+    // K/V block loads: 64 keys x 16 float4 = 1024 float4 each, thread t takes t + nt i (i < 2,
+    // nt >= 576: at least 9 waves); slots past 1024 re-read a valid one and are not stored
+    float4 kr4[2], vr4[2];
+    auto kv_load = [&](int64_t j0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int f = t + 256 * i, key = f >> 4, d4 = f & 15;
+        for (int i = 0; i < 2; ++i) {
+            int f = t + nt * i;
+            f = f < 1024 ? f : f & 1023;
+            const int key = f >> 4, d4 = f & 15;
             const int64_t kr = j0 + key < n_keys ? j0 + key : n_keys - 1;
-            const float4 kv = reinterpret_cast<const float4*>(kb + kr * kFpHd)[d4];
-            const float4 vv = reinterpret_cast<const float4*>(vb + kr * kFpHd)[d4];
-            _Float16* kd = ks + key * kFpRow + 4 * d4;
-            kd[0] = (_Float16)kv.x; kd[1] = (_Float16)kv.y; kd[2] = (_Float16)kv.z; kd[3] = (_Float16)kv.w;
-            vt[(4 * d4 + 0) * kFpRow + key] = (_Float16)vv.x;
-            vt[(4 * d4 + 1) * kFpRow + key] = (_Float16)vv.y;
-            vt[(4 * d4 + 2) * kFpRow + key] = (_Float16)vv.z;
-            vt[(4 * d4 + 3) * kFpRow + key] = (_Float16)vv.w;
+            kr4[i] = reinterpret_cast<const float4*>(kb + kr * kFpHd)[d4];
+            vr4[i] = reinterpret_cast<const float4*>(vb + kr * kFpHd)[d4];
+        }
+    };
+    kv_load(0);
+    for (int64_t j0 = 0; j0 < key_end; j0 += kFpKeys) {
+        // stage this block (fp32 -> fp16), then put the next block's loads in flight
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int f = t + nt * i;
+            if (f < 1024) {
+                const int key = f >> 4, d4 = f & 15;
+                const float4 kv = kr4[i], vv = vr4[i];
+                typedef _Float16 fh4 __attribute__((ext_vector_type(4)));
+                *reinterpret_cast<fh4*>(ks + key * kFpRow + 4 * d4) =
+                    fh4{(_Float16)kv.x, (_Float16)kv.y, (_Float16)kv.z, (_Float16)kv.w};
+                vt[(4 * d4 + 0) * kFpRow + key] = (_Float16)vv.x;
+                vt[(4 * d4 + 1) * kFpRow + key] = (_Float16)vv.y;
+                vt[(4 * d4 + 2) * kFpRow + key] = (_Float16)vv.z;
+                vt[(4 * d4 + 3) * kFpRow + key] = (_Float16)vv.w;
+            }
         }
         __syncthreads();
+        kv_load(j0 + kFpKeys < key_end ? j0 + kFpKeys : j0);
 
         // S = Q K^T for 4 key tiles of 16
         fv4 sacc[4];
@@ -130,7 +158,7 @@ __global__ __launch_bounds__(256) void k_flash_prefill(FlashParams p) {
                 sacc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], kbv, sacc[jt], 0, 0, 0);
             }
         }
-        // scale, causal mask, online softmax per row
+        // scale, causal mask, online softmax per row (base 2)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int64_t qpos = p.pos0 + q0 + 4 * lg + r;
@@ -138,16 +166,16 @@ __global__ __launch_bounds__(256) void k_flash_prefill(FlashParams p) {
 #pragma unroll
             for (int jt = 0; jt < 4; ++jt) {
                 const int64_t key = j0 + 16 * jt + li;
-                sv[jt] = (key <= qpos && key < n_keys) ? sacc[jt][r] * p.scale : NEG_INF;
+                sv[jt] = (key <= qpos && key < n_keys) ? sacc[jt][r] * sl2 : NEG_INF;
                 mx = fmaxf(mx, sv[jt]);
             }
             mx = row16_max(mx);
             const float m_new = fmaxf(m_run[r], mx);
-            const float corr = m_new == NEG_INF ? 1.f : expf(m_run[r] - m_new);
+            const float corr = m_new == NEG_INF ? 1.f : __builtin_amdgcn_exp2f(m_run[r] - m_new);
             float psum = 0.f;
 #pragma unroll
             for (int jt = 0; jt < 4; ++jt) {
-                const float e = m_new == NEG_INF ? 0.f : expf(sv[jt] - m_new);
+                const float e = m_new == NEG_INF ? 0.f : __builtin_amdgcn_exp2f(sv[jt] - m_new);
                 psum += e;
                 ps[w][(4 * lg + r) * kFpRow + 16 * jt + li] = (_Float16)e;
             }
@@ -157,7 +185,10 @@ __global__ __launch_bounds__(256) void k_flash_prefill(FlashParams p) {
 #pragma unroll
             for (int d = 0; d < 4; ++d) o[d][r] *= corr;
         }
-        __syncthreads();  // P visible to the whole wave (and K / V reads done before restaging)
+        // P is read back by the same wave only: a wave-local LDS handoff
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
         // O += P V: A = P (16 queries x 64 keys), B = V (64 keys x 16 dims) per dim tile
 #pragma unroll
@@ -169,7 +200,7 @@ __global__ __launch_bounds__(256) void k_flash_prefill(FlashParams p) {
                 o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vbv, o[d], 0, 0, 0);
             }
         }
-        __syncthreads();  // before the next block overwrites K / V / P
+        __syncthreads();  // every wave is done with K / V before the next block is staged
     }
 
     // out: O[row 4 lg + r][dim 16 d + li] / l
@@ -192,18 +223,21 @@ extern "C" int pe_flash_prefill(const float* q, int64_t q_stride, const float* k
                                 const float* v_cache, int n_head, int n_kv, int head_dim,
                                 int64_t capacity, int64_t L, int64_t pos0, float scale, float* out,
                                 int64_t out_stride, pe_stream_t stream) {
-    if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || head_dim != kFpHd || capacity <= 0 || L < 0 ||
-        pos0 < 0 || pos0 + L > capacity || n_head > 65535)
+    if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > kFpMaxWaves ||
+        head_dim != kFpHd || capacity <= 0 || L < 0 || pos0 < 0 || pos0 + L > capacity || n_kv > 65535)
         return PE_ERR_SHAPE;
     if (L == 0) return PE_OK;
-    if ((L + kFpQ - 1) / kFpQ > 0x7FFFFFFF) return PE_ERR_SHAPE;
+    const int group = n_head / n_kv;
+    const int qb = flash_qb(group);
+    if ((L + qb - 1) / qb > 0x7FFFFFFF) return PE_ERR_SHAPE;
     if (!q || !k_cache || !v_cache || !out) return PE_ERR_NULL;
     if (q_stride < (int64_t)n_head * head_dim || out_stride < (int64_t)n_head * head_dim) return PE_ERR_SHAPE;
     if (!aligned(q, 16) || q_stride % 4 || !aligned(k_cache, 16) || !aligned(v_cache, 16) ||
         !aligned(out, 4))
         return PE_ERR_ALIGN;
     FlashParams p{q, q_stride, k_cache, v_cache, n_head / n_kv, capacity, L, pos0, scale, out, out_stride};
-    const dim3 grid((unsigned)((L + kFpQ - 1) / kFpQ), (unsigned)n_head);
-    hipLaunchKernelGGL(k_flash_prefill, grid, dim3(256), 0, (hipStream_t)stream, p);
+    const int waves = group * (qb / 16);  // 9..16 (at least 576 threads: kv_load assumes it)
+    const dim3 grid((unsigned)((L + qb - 1) / qb), (unsigned)n_kv);
+    hipLaunchKernelGGL(k_flash_prefill, grid, dim3(64 * waves), 0, (hipStream_t)stream, p, qb);
     return launch_status();
 }

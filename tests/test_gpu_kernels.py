@@ -939,11 +939,13 @@ def test_gemm_f16_matches_fp16_operand_reference(K, M, N, Kd, bias, res, extra):
 
 
 @pytest.mark.parametrize("L,pos0", [(1, 0), (5, 0), (64, 0), (100, 7), (130, 0), (513, 0)])
-def test_flash_prefill_matches_closed_form(K, L, pos0):
+@pytest.mark.parametrize("n_head,n_kv", [(14, 2), (8, 8), (16, 4), (16, 1), (9, 3)])
+def test_flash_prefill_matches_closed_form(K, L, pos0, n_head, n_kv):
     """Causal GQA attention on the matrix cores against float64 on the same fp16-rounded q, k,
-    v (the probabilities are rounded to fp16 inside: 2e-3 relative)."""
+    v (the probabilities are rounded to fp16 inside: 2e-3 relative), for group sizes 7, 1, 4,
+    16 and 3 (query blocks of 32, 256, 64, 16 and 80 per workgroup)."""
     rng = np.random.default_rng(L + pos0)
-    n_head, n_kv, hd, cap = 14, 2, 64, pos0 + L + 3
+    hd, cap = 64, pos0 + L + 3
     q = rng.standard_normal((L, n_head, hd)).astype(np.float32)
     k, v = _kv(rng, n_kv, cap, hd)
     out = K.flash_prefill(torch.from_numpy(q).to(DEV), torch.from_numpy(k).to(DEV),
