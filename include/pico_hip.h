@@ -112,6 +112,15 @@ int pe_gemm_f16(const float* a, int64_t lda, const void* w_f16, const float* bia
                 const float* residual, int64_t ldr, float* c, int64_t ldc, int64_t M, int64_t N,
                 int64_t K, pe_stream_t stream);
 
+/* pe_gemm_f16 of the prefill gate/up product with the SiLU product fused into its epilogue:
+ * c[m][f] = silu(g) * u, g = A[m] . Wg[f], u = A[m] . Wu[f] (f < ffn), where w_f16_il holds the
+ * fp16 [gate; up] rows interleaved in groups of 16 (rows 32 b + i = gate row 16 b + i, rows
+ * 32 b + 16 + i = up row 16 b + i; ffn % 16 == 0), c (M, ffn) with row stride ldc. The same
+ * products and SiLU formula as pe_gemm_f16 followed by pe_silu_mul, without the (M, 2 ffn)
+ * intermediate. Replaces model.py:218-224 (L > 1). */
+int pe_gemm_f16_silu(const float* a, int64_t lda, const void* w_f16_il, float* c, int64_t ldc,
+                     int64_t M, int64_t ffn, int64_t K, pe_stream_t stream);
+
 /* Causal GQA prompt-prefill attention on the matrix cores (flash attention): as
  * pe_prefill_attn, with q, k, v rounded to fp16 as they are read, fp32 scores, softmax and
  * accumulation, the probabilities rounded to fp16 for the P.V product. head_dim 64.

@@ -58,7 +58,11 @@ PE_DEV void gemm_tile_of_block(int64_t& tm, int64_t& tn) {
     tn = r / gm;
 }
 
-template <bool BIAS, bool RES>
+// SILU: W holds [gate; up] rows interleaved in groups of 16 (rows 32 b .. 32 b + 15 = gate rows
+// 16 b .., rows 32 b + 16 .. = up rows 16 b ..), so a lane's MFMA tiles j = 2 c and 2 c + 1
+// hold gate and up of the same 16 ffn columns; the epilogue stores silu(g) * u (the formula
+// of k_silu_mul) into C (M, N / 2) and the (M, N) gate/up product is never written.
+template <bool BIAS, bool RES, bool SILU = false>
 __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
     __shared__ __align__(16) _Float16 As[2][kGfTile * kGfLds];
     __shared__ __align__(16) _Float16 Ws[2][kGfTile * kGfLds];
@@ -149,6 +153,24 @@ __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
 
     // D[4 (l / 16) + r][l % 16] of tile (i, j) -> row m0 + 16 i + 4 (l / 16) + r, column n0 + 16 j + l % 16
     const int64_t m0 = bm + wm, n0 = bn + wn;
+    if constexpr (SILU) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int64_t ng = n0 + 32 * c;  // first (gate) row of this 32-row group
+            if (ng >= p.N) continue;
+            const int64_t f = ng / 2 + li;   // ffn column
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t m = m0 + 16 * i + 4 * (l >> 4) + r;
+                    if (m >= p.M) continue;
+                    const float g = acc[i][2 * c][r], u = acc[i][2 * c + 1][r];
+                    p.c[m * p.ldc + f] = (g * (1.0f / (1.0f + expf(-g)))) * u;
+                }
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int64_t n = n0 + 16 * j + li;
@@ -171,6 +193,21 @@ __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
 }  // namespace pe
 
 using namespace pe;
+
+extern "C" int pe_gemm_f16_silu(const float* a, int64_t lda, const void* w_f16_il, float* c,
+                                int64_t ldc, int64_t M, int64_t ffn, int64_t K, pe_stream_t stream) {
+    if (M < 0 || ffn <= 0 || ffn % 16 || K <= 0 || K % kGfK) return PE_ERR_SHAPE;
+    if (M == 0) return PE_OK;
+    const int64_t N = 2 * ffn;
+    if (lda < K || ldc < ffn) return PE_ERR_SHAPE;
+    if ((M + kGfTile - 1) / kGfTile > 65535 || (N + kGfTile - 1) / kGfTile > 65535) return PE_ERR_SHAPE;
+    if (!a || !w_f16_il || !c) return PE_ERR_NULL;
+    if (!aligned(a, 16) || lda % 4 || !aligned(w_f16_il, 16) || !aligned(c, 4)) return PE_ERR_ALIGN;
+    GemmF16Args p{a, lda, (const _Float16*)w_f16_il, nullptr, nullptr, 0, c, ldc, M, N, K};
+    const dim3 grid((unsigned)((N + kGfTile - 1) / kGfTile), (unsigned)((M + kGfTile - 1) / kGfTile));
+    hipLaunchKernelGGL((k_gemm_f16<false, false, true>), grid, dim3(256), 0, (hipStream_t)stream, p);
+    return launch_status();
+}
 
 extern "C" int pe_gemm_f16(const float* a, int64_t lda, const void* w_f16, const float* bias,
                            const float* residual, int64_t ldr, float* c, int64_t ldc, int64_t M,

@@ -175,6 +175,39 @@ def gemm_f16(a: torch.Tensor, w16: torch.Tensor, bias: torch.Tensor | None = Non
     return out
 
 
+def interleave_gate_up_f16(gu16: torch.Tensor) -> torch.Tensor:
+    """(2*ffn, K) fp16 [gate; up] rows -> the layout of gemm_f16_silu: groups of 16 gate rows
+    and the 16 matching up rows alternating (ffn % 16 == 0)."""
+    n, k = gu16.shape
+    ffn = n // 2
+    if n % 2 or ffn % 16:
+        raise ValueError("gate/up rows must be 2 * ffn with ffn % 16 == 0")
+    g = gu16[:ffn].reshape(ffn // 16, 16, k)
+    u = gu16[ffn:].reshape(ffn // 16, 16, k)
+    return torch.stack([g, u], dim=1).reshape(n, k).contiguous()
+
+
+def gemm_f16_silu(a: torch.Tensor, w16_il: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(A Wg^T) * (A Wu^T) on the matrix cores, W = interleave_gate_up_f16([gate; up]):
+    gemm_f16 then silu_mul without the (M, 2 ffn) intermediate (model.py:218-224)."""
+    dev = _on_gpu(a, w16_il)
+    if a.dim() == 1:
+        a = a.unsqueeze(0)
+    if a.dtype != torch.float32:
+        raise ValueError("a must be float32")
+    if a.stride(1) != 1 or a.stride(0) % 4 or a.data_ptr() % 16:
+        a = a.contiguous()
+    M, K = a.shape
+    N = w16_il.shape[0]
+    if w16_il.dtype != torch.float16 or not w16_il.is_contiguous() or w16_il.shape[1] != K or N % 32:
+        raise ValueError("w16_il must be a contiguous (2*ffn, K) float16 tensor, ffn % 16 == 0")
+    if out is None:
+        out = torch.empty(M, N // 2, device=dev, dtype=torch.float32)
+    check(lib.pe_gemm_f16_silu(_ptr(a), a.stride(0), _ptr(w16_il), _ptr(out), out.stride(0), M, N // 2, K,
+                               _stream(dev)), "pe_gemm_f16_silu")
+    return out
+
+
 def embed_gather(table: RawTensor, ids: torch.Tensor, out: torch.Tensor | None = None,
                  layout: int = LAYOUT_NATURAL):
     """Rows ``ids`` of a raw GGUF (vocab, hidden) table, dequantized (model.py:152);
@@ -706,5 +739,5 @@ __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "
            "qgemv_norm_silu", "qkv_rmsnorm_rope", "attn_block", "attn_block_workspace",
            "attn_block_failed", "attn_oproj", "attn_oproj_supported", "attn_head", "attn_head_supported", "qgemv_sum_norm_silu", "qgemm", "kv_write", "prefill_attn",
            "attn_gproj", "attn_gproj_supported", "qgemv_norm_argmax", "dequantize_weight_f16",
-           "gemm_f16", "flash_prefill",
+           "gemm_f16", "gemm_f16_silu", "interleave_gate_up_f16", "flash_prefill",
            "BLOCK_SIZE"]

@@ -182,8 +182,10 @@ class Transformer:
 
     def f16_weights(self) -> list[dict[str, torch.Tensor]]:
         """Per layer fp16 (N, K) copies of the linear weights for the matrix-core prefill: qkv
-        ([q; k; v] rows, with the concatenated bias), o, gu ([gate; up]) and down; each value
-        the exact dequantized weight rounded to nearest even. Built once, on first use."""
+        ([q; k; v] rows, with the concatenated bias), o, gu_il ([gate; up] interleaved in
+        groups of 16 rows for the SiLU-fused GEMM; gu, plain, when ffn % 16 != 0) and down;
+        each value the exact dequantized weight rounded to nearest even. Built once, on first
+        use."""
         if self._f16 is None:
             out = []
             for L in self.layers:
@@ -202,7 +204,10 @@ class Transformer:
                 bias = None
                 if L.bq is not None:
                     bias = torch.cat([L.bq, L.bk, L.bv]).float().contiguous()
-                out.append(dict(qkv=qkv, qkv_bias=bias, o=K.dequantize_weight_f16(L.wo), gu=gu,
+                # [gate; up] interleaved in groups of 16 rows for the SiLU-fused GEMM
+                gu_il = K.interleave_gate_up_f16(gu) if (gu.shape[0] // 2) % 16 == 0 else None
+                out.append(dict(qkv=qkv, qkv_bias=bias, o=K.dequantize_weight_f16(L.wo),
+                                gu=gu if gu_il is None else None, gu_il=gu_il,
                                 down=K.dequantize_weight_f16(L.w_down)))
             self._f16 = out
         return self._f16
@@ -317,7 +322,10 @@ class Transformer:
             attn = K.flash_prefill(qk[:, :nh], k_buf, v_buf, pos0=pos0)  # (L, hidden)
             x = K.gemm_f16(attn, W["o"], residual=x)
             h = K.rmsnorm(x, L.ffn_norm, cfg.eps)
-            act = K.silu_mul(K.gemm_f16(h, W["gu"]), cfg.ffn_dim)
+            if W["gu_il"] is not None:
+                act = K.gemm_f16_silu(h, W["gu_il"])
+            else:
+                act = K.silu_mul(K.gemm_f16(h, W["gu"]), cfg.ffn_dim)
             x = K.gemm_f16(act, W["down"], residual=x)
         return self._lm_head(x[-1], self.w["output_norm.weight"], greedy, K.LAYOUT_NATURAL)
 

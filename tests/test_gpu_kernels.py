@@ -938,6 +938,19 @@ def test_gemm_f16_matches_fp16_operand_reference(K, M, N, Kd, bias, res, extra):
     assert rel_err(c, ref) < 1e-5
 
 
+@pytest.mark.parametrize("M,ffn,Kd", [(300, 4864, 896), (13, 512, 3584), (129, 48, 96), (1, 16, 32)])
+def test_gemm_f16_silu_equals_gemm_then_silu(K, M, ffn, Kd):
+    """The SiLU-fused gate/up GEMM (interleaved rows) gives silu_mul(gemm_f16(A, [gate; up]))
+    bit for bit: the same MFMA accumulation per column and the same SiLU formula."""
+    rng = np.random.default_rng(M + ffn)
+    a = torch.from_numpy(rng.standard_normal((M, Kd)).astype(np.float32)).to(DEV)
+    w16 = torch.from_numpy((rng.standard_normal((2 * ffn, Kd)) * 0.05).astype(np.float16)).to(DEV)
+    ref = K.silu_mul(K.gemm_f16(a, w16), ffn)
+    got = K.gemm_f16_silu(a, K.interleave_gate_up_f16(w16))
+    assert got.shape == (M, ffn)
+    assert torch.equal(got, ref)
+
+
 @pytest.mark.parametrize("L,pos0", [(1, 0), (5, 0), (64, 0), (100, 7), (130, 0), (513, 0)])
 @pytest.mark.parametrize("n_head,n_kv", [(14, 2), (8, 8), (16, 4), (16, 1), (9, 3)])
 def test_flash_prefill_matches_closed_form(K, L, pos0, n_head, n_kv):
