@@ -914,6 +914,8 @@ GEMM16_CASES = [  # (M, N, K, bias, residual, a_row_stride_extra)
     (1, 128, 896, False, False, 0), (13, 1152, 896, True, False, 0), (128, 896, 896, False, True, 0),
     (300, 9728, 896, False, False, 0), (257, 896, 4864, False, True, 0), (77, 200, 96, True, True, 32),
     (8192, 1152, 896, True, False, 0),
+    # 256 x 128 workgroup tiles (>= 512 of them), ragged edges included
+    (4096, 4096, 96, True, True, 0), (4000, 4000, 64, False, False, 32),
 ]
 
 
@@ -938,7 +940,8 @@ def test_gemm_f16_matches_fp16_operand_reference(K, M, N, Kd, bias, res, extra):
     assert rel_err(c, ref) < 1e-5
 
 
-@pytest.mark.parametrize("M,ffn,Kd", [(300, 4864, 896), (13, 512, 3584), (129, 48, 96), (1, 16, 32)])
+@pytest.mark.parametrize("M,ffn,Kd", [(300, 4864, 896), (13, 512, 3584), (129, 48, 96), (1, 16, 32),
+                                      (4096, 2048, 64)])
 def test_gemm_f16_silu_equals_gemm_then_silu(K, M, ffn, Kd):
     """The SiLU-fused gate/up GEMM (interleaved rows) gives silu_mul(gemm_f16(A, [gate; up]))
     bit for bit: the same MFMA accumulation per column and the same SiLU formula."""
