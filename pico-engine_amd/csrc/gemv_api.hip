@@ -16,9 +16,6 @@ static int dispatch_gemv(int type, const GemvArgs& a, bool norm, int mode, hipSt
 static int check_weight(int type, const void* w, int64_t n_rows, int64_t k) {
     if (!is_tiled_type(type)) return PE_ERR_TYPE;
     if (n_rows <= 0 || k <= 0 || k % block_elems(type)) return PE_ERR_SHAPE;
-    // the decode GEMV kernels address the tiled planes with 32-bit offsets (Fmt::load32)
-    if (n_rows >= (1 << 24) || n_rows * (k / block_elems(type)) * block_bytes(type) >= (1LL << 32))
-        return PE_ERR_SHAPE;
     Shape sh;
     if (!pick_shape(k / 32, sh)) return PE_ERR_SHAPE;
     if (!w) return PE_ERR_NULL;

@@ -307,11 +307,10 @@ PE_DEV void load_task(const GemvArgs& a, int64_t task, int glane, int units,
 #pragma unroll
         for (int t = 0; t < UPL; ++t) {
             const int u = glane + GS * t;
-            const uint32_t row = (uint32_t)(tc + rr * a.up_off);
             if constexpr (GS == 256 && !CLAMP) {
-                if (u < units) Fmt<T>::load32(a.w, row, u, raw[rr][t]);
+                if (u < units) Fmt<T>::load(a.w, tc + rr * a.up_off, u, raw[rr][t]);
             } else {
-                Fmt<T>::load32(a.w, row, u < units ? u : units - 1, raw[rr][t]);
+                Fmt<T>::load(a.w, tc + rr * a.up_off, u < units ? u : units - 1, raw[rr][t]);
             }
         }
 }

@@ -184,16 +184,6 @@ struct Fmt<PE_TYPE_Q8_0> {
         r.b = q[1];
         r.d = reinterpret_cast<const uint16_t*>(t.base + t.nrows * t.nb * 32)[blk];
     }
-    // load() with 32-bit offsets from uniform plane bases (tensor < 4 GiB, rows and blocks
-    // per row < 2^24: checked by the GEMV entry points): no 64-bit multiplies per load.
-    static PE_DEV void load32(const Tiled& t, uint32_t row, int u, Raw& r) {
-        const uint32_t blk = __umul24(row, (uint32_t)t.nb) + (uint32_t)u;
-        const int4* q = reinterpret_cast<const int4*>(t.base + (uint64_t)(blk * 32u));
-        r.a = q[0];
-        r.b = q[1];
-        const uint8_t* dp = t.base + t.nrows * t.nb * 32;
-        r.d = *reinterpret_cast<const uint16_t*>(dp + (uint64_t)(blk * 2u));
-    }
     static PE_DEV int code(const Raw& r, int i) {
         const int4& v = i < 16 ? r.a : r.b;
         return sext8(word_of(v, (i & 15) >> 2), i & 3);
@@ -228,13 +218,6 @@ struct Fmt<PE_TYPE_Q5_0> {
         r.qs = *reinterpret_cast<const int4*>(t.base + blk * 16);
         r.qh = reinterpret_cast<const uint32_t*>(t.base + nblk * 16)[blk];
         r.d = reinterpret_cast<const uint16_t*>(t.base + nblk * 20)[blk];
-    }
-    static PE_DEV void load32(const Tiled& t, uint32_t row, int u, Raw& r) {
-        const uint32_t blk = __umul24(row, (uint32_t)t.nb) + (uint32_t)u;
-        const int64_t nblk = t.nrows * t.nb;
-        r.qs = *reinterpret_cast<const int4*>(t.base + (uint64_t)(blk * 16u));
-        r.qh = *reinterpret_cast<const uint32_t*>(t.base + nblk * 16 + (uint64_t)(blk * 4u));
-        r.d = *reinterpret_cast<const uint16_t*>(t.base + nblk * 20 + (uint64_t)(blk * 2u));
     }
     // 5-bit code of element e (0..31): nibble of qs[e % 16] (low for e < 16), 5th bit = qh bit e
     static PE_DEV int code(const Raw& r, int e) {
@@ -282,15 +265,6 @@ struct Fmt<PE_TYPE_Q4_K> {
         r.lo = q[0];
         r.hi = q[1];
         r.head = *reinterpret_cast<const int4*>(t.base + t.nrows * t.nb * 128 + blk * 16);
-        r.sub = j;
-    }
-    static PE_DEV void load32(const Tiled& t, uint32_t row, int u, Raw& r) {
-        const uint32_t blk = __umul24(row, (uint32_t)t.nb) + (uint32_t)(u >> 3);
-        const int j = u & 7;
-        const int4* q = reinterpret_cast<const int4*>(t.base + (uint64_t)(blk * 128u + 32u * (j >> 1)));
-        r.lo = q[0];
-        r.hi = q[1];
-        r.head = *reinterpret_cast<const int4*>(t.base + t.nrows * t.nb * 128 + (uint64_t)(blk * 16u));
         r.sub = j;
     }
     // 6-bit scale and min of sub-block j (the packing of k4_scale_min): bytes j%4 of the three
@@ -363,20 +337,6 @@ struct Fmt<PE_TYPE_Q6_K> {
         r.h1 = H[1];
         r.sc = reinterpret_cast<const uint16_t*>(t.base + nblk * 192 + blk * 16)[4 * hf + q];
         r.d = reinterpret_cast<const uint16_t*>(t.base + nblk * 208)[blk];
-        r.q = q;
-    }
-    static PE_DEV void load32(const Tiled& t, uint32_t row, int u, Raw& r) {
-        const uint32_t blk = __umul24(row, (uint32_t)t.nb) + (uint32_t)(u >> 3);
-        const int64_t nblk = t.nrows * t.nb;
-        const int hf = (u & 7) >> 2, q = u & 3;
-        const int4* L = reinterpret_cast<const int4*>(t.base + (uint64_t)(blk * 128u + 64u * hf + 32u * (q & 1)));
-        const int4* H = reinterpret_cast<const int4*>(t.base + nblk * 128 + (uint64_t)(blk * 64u + 32u * hf));
-        r.l0 = L[0];
-        r.l1 = L[1];
-        r.h0 = H[0];
-        r.h1 = H[1];
-        r.sc = *reinterpret_cast<const uint16_t*>(t.base + nblk * 192 + (uint64_t)(blk * 16u + 2u * (4 * hf + q)));
-        r.d = *reinterpret_cast<const uint16_t*>(t.base + nblk * 208 + (uint64_t)(blk * 2u));
         r.q = q;
     }
     static PE_DEV int code(const Raw& r, int l) {
