@@ -773,7 +773,10 @@ inline int64_t argmax_ws_bytes(int64_t n_rows) {
 // the next chunk's loads in flight, loop_tpg tasks per group per chunk. The per-block
 // activation staging (up to 2 x 14 KB at k = 3584, 74 KB at k = 18944) would otherwise be
 // repeated for every one or two rows, and then dominated the launch.
-constexpr int kLoopMinBlocks = 2048;
+#ifndef PE_LOOP_MIN_BLOCKS
+#define PE_LOOP_MIN_BLOCKS 1024
+#endif
+constexpr int kLoopMinBlocks = PE_LOOP_MIN_BLOCKS;
 template <int MODE>
 constexpr bool loop_ok() { return MODE == kModePlain || MODE == kModeSilu; }
 // Tasks per group of the looped form: two when one chunk's raw weights take at most 13
@@ -790,19 +793,34 @@ constexpr int loop_tpg() {
 template <int GS>
 constexpr int64_t loop_blocks() { return GS == 256 ? 512 : 2048; }
 
+// Grid of a looped launch with nchunk chunks: about PE_LOOP_DIV chunks per block, at least
+// 256 blocks (one per CU) and at most loop_blocks. Swept on MI355X at the 7B shapes (chunks
+// per block 1, 2, 4, 8; looped from 1024 or 2048 natural blocks): two chunks per block from
+// 1024 blocks took the 3584 -> 3584 o-projection from 7.1 to 5.7 us, the others within 3 %.
+#ifndef PE_LOOP_DIV
+#define PE_LOOP_DIV 2
+#endif
+template <int GS>
+int64_t loop_grid(int64_t nchunk) {
+    int64_t bl = (nchunk + PE_LOOP_DIV - 1) / PE_LOOP_DIV;
+    if (bl < 256) bl = 256;
+    if (bl > nchunk) bl = nchunk;
+    return bl < loop_blocks<GS>() ? bl : loop_blocks<GS>();
+}
+
+// loop: run the looped form (decided by the caller from the launch's natural block count).
 template <int T, int GS, int UPL, bool NORM, int MODE>
-void launch_qgemv_shape(const GemvArgs& a, hipStream_t s) {
+void launch_qgemv_shape(const GemvArgs& a, hipStream_t s, bool loop = false) {
     constexpr int TPG = tasks_per_group<MODE>();
     constexpr int CH = (kGemvThreads / GS) * TPG;
     int64_t blocks = (a.n_tasks + CH - 1) / CH;
     const size_t lds = a.k <= kStageMaxK ? (size_t)(a.k / 32) * kUnitStride * 4 : 0;
     if constexpr (loop_ok<MODE>()) {
-        if (blocks > kLoopMinBlocks) {
+        if (loop) {
             constexpr int R = MODE == kModeSilu ? 2 : 1;
             constexpr int TL = loop_tpg<T, UPL, R>();
             constexpr int CHL = (kGemvThreads / GS) * TL;
-            int64_t bl = (a.n_tasks + CHL - 1) / CHL;
-            if (bl > loop_blocks<GS>()) bl = loop_blocks<GS>();
+            const int64_t bl = loop_grid<GS>((a.n_tasks + CHL - 1) / CHL);
             // double buffering at one unit per lane; with several (long rows) the second
             // register set would cut the kernel to one wave per SIMD
             hipLaunchKernelGGL((k_qgemv<T, GS, UPL, TL, NORM, MODE, UPL == 1>), dim3((unsigned)bl),
@@ -826,14 +844,17 @@ int launch_qgemv_mode(const GemvArgs& a, hipStream_t s) {
     // lane instead of two waves with one: the row sum is then a wave-local DPP reduction (no
     // LDS exchange and no block barriers inside the loop), and each lane reduces once per two
     // units instead of once per unit.
+    bool loop = false;
     if constexpr (loop_ok<MODE>()) {
-        if (sh.gs == 128 && sh.upl == 1 && (a.n_tasks + 1) / 2 > kLoopMinBlocks) {
-            launch_qgemv_shape<T, 64, 2, NORM, MODE>(a, s);
+        const int64_t natural = (a.n_tasks + kGemvThreads / sh.gs - 1) / (kGemvThreads / sh.gs);
+        loop = natural > kLoopMinBlocks;
+        if (loop && sh.gs == 128 && sh.upl == 1) {
+            launch_qgemv_shape<T, 64, 2, NORM, MODE>(a, s, true);
             return launch_status();
         }
     }
     switch (sh.gs * 16 + sh.upl) {
-#define PE_CASE(G, U) case G * 16 + U: launch_qgemv_shape<T, G, U, NORM, MODE>(a, s); break;
+#define PE_CASE(G, U) case G * 16 + U: launch_qgemv_shape<T, G, U, NORM, MODE>(a, s, loop); break;
         PE_SHAPE_CASES(PE_CASE)
 #undef PE_CASE
         default: return PE_ERR_SHAPE;
