@@ -846,8 +846,12 @@ int launch_qgemv_mode(const GemvArgs& a, hipStream_t s) {
     // units instead of once per unit.
     bool loop = false;
     if constexpr (loop_ok<MODE>()) {
-        const int64_t natural = (a.n_tasks + kGemvThreads / sh.gs - 1) / (kGemvThreads / sh.gs);
-        loop = natural > kLoopMinBlocks;
+        // looped from 2 * kLoopMinBlocks natural blocks, or from kLoopMinBlocks when each row
+        // would re-stage >= 1024 activation floats (k / groups per block): at k = 896 and 8
+        // groups per block (the 896 -> 9728 product) one pass is faster, measured
+        const int gpb = kGemvThreads / sh.gs;
+        const int64_t natural = (a.n_tasks + gpb - 1) / gpb;
+        loop = natural > 2 * kLoopMinBlocks || (natural > kLoopMinBlocks && a.k / gpb >= 1024);
         if (loop && sh.gs == 128 && sh.upl == 1) {
             launch_qgemv_shape<T, 64, 2, NORM, MODE>(a, s, true);
             return launch_status();
