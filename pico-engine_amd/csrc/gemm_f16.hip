@@ -62,26 +62,30 @@ PE_DEV void gemm_tile_of_block(int64_t& tm, int64_t& tn) {
 // 16 b .., rows 32 b + 16 .. = up rows 16 b ..), so a lane's MFMA tiles j = 2 c and 2 c + 1
 // hold gate and up of the same 16 ffn columns; the epilogue stores silu(g) * u (the formula
 // of k_silu_mul) into C (M, N / 2) and the (M, N) gate/up product is never written.
-template <bool BIAS, bool RES, bool SILU = false>
+// RT: 16-row MFMA tiles per wave along M: 4 (128 x 128 workgroup tile) or 2 (64 x 128, for
+// products whose 128 x 128 grid would leave CUs idle, e.g. N = 896 at M = 8192: 448 -> 896
+// workgroups).
+template <int RT, bool BIAS, bool RES, bool SILU = false>
 __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
-    __shared__ __align__(16) _Float16 As[2][kGfTile * kGfLds];
+    constexpr int BM = 32 * RT;  // workgroup rows
+    __shared__ __align__(16) _Float16 As[2][BM * kGfLds];
     __shared__ __align__(16) _Float16 Ws[2][kGfTile * kGfLds];
     const int tid = threadIdx.x;
     const int w = tid >> 6, l = tid & 63;
     int64_t tm, tn;
     gemm_tile_of_block(tm, tn);
-    const int64_t bm = tm * kGfTile, bn = tn * kGfTile;
-    const int wm = (w >> 1) * 64, wn = (w & 1) * 64;  // the wave's 64 x 64 part of the tile
+    const int64_t bm = tm * BM, bn = tn * kGfTile;
+    const int wm = (w >> 1) * 16 * RT, wn = (w & 1) * 64;  // the wave's (16 RT) x 64 part
     const int li = l & 15, lk = (l >> 4) * 8;         // MFMA operand: row li, k lk .. lk + 7
 
-    // global -> registers: A rows ar + 32 i (i < 4), fp32 columns ac .. ac + 3 of the K step;
+    // global -> registers: A rows ar + 32 i (i < RT), fp32 columns ac .. ac + 3 of the K step;
     // W rows wr + 64 i (i < 2), fp16 columns wc .. wc + 7
     const int ar = tid >> 3, ac = (tid & 7) * 4;
     const int wr = tid >> 2, wc = (tid & 3) * 8;
-    const float* ap[4];
+    const float* ap[RT];
     const _Float16* wp[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < RT; ++i) {
         const int64_t m = bm + ar + 32 * i;
         ap[i] = p.a + (m < p.M ? m : p.M - 1) * p.lda + ac;
     }
@@ -90,11 +94,11 @@ __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
         const int64_t n = bn + wr + 64 * i;
         wp[i] = p.w + (n < p.N ? n : p.N - 1) * p.K + wc;
     }
-    float4 ra[4];
+    float4 ra[RT];
     uint4 rw[2];
-    f4v acc[4][4];
+    f4v acc[RT][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RT; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f4v{0.f, 0.f, 0.f, 0.f};
 
@@ -102,7 +106,7 @@ __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
 #define PE_GF_GLOAD(kk)                                                                        \
     do {                                                                                       \
         const int64_t k0_ = (int64_t)(kk) * kGfK;                                             \
-        _Pragma("unroll") for (int i = 0; i < 4; ++i) ra[i] =                                  \
+        _Pragma("unroll") for (int i = 0; i < RT; ++i) ra[i] =                                 \
             *reinterpret_cast<const float4*>(ap[i] + k0_);                                     \
         _Pragma("unroll") for (int i = 0; i < 2; ++i) rw[i] =                                  \
             *reinterpret_cast<const uint4*>(wp[i] + k0_);                                      \
@@ -110,7 +114,7 @@ __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
 // ra (rounded to fp16) / rw into LDS buffer b.
 #define PE_GF_LSTORE(b)                                                                        \
     do {                                                                                       \
-        _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                        \
+        _Pragma("unroll") for (int i = 0; i < RT; ++i) {                                       \
             const h4 v_ = {(_Float16)ra[i].x, (_Float16)ra[i].y, (_Float16)ra[i].z,            \
                            (_Float16)ra[i].w};                                                 \
             *reinterpret_cast<h4*>(&As[b][(ar + 32 * i) * kGfLds + ac]) = v_;                  \
@@ -125,12 +129,12 @@ __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
 #define PE_GF_STEP(kt, b)                                                                      \
     do {                                                                                       \
         PE_GF_GLOAD((kt) + 1 < nk ? (kt) + 1 : (kt));                                          \
-        h8 av_[4], bv_[4];                                                                     \
-        _Pragma("unroll") for (int t = 0; t < 4; ++t) {                                        \
+        h8 av_[RT], bv_[4];                                                                    \
+        _Pragma("unroll") for (int t = 0; t < RT; ++t)                                         \
             av_[t] = *reinterpret_cast<const h8*>(&As[b][(wm + 16 * t + li) * kGfLds + lk]);   \
+        _Pragma("unroll") for (int t = 0; t < 4; ++t)                                          \
             bv_[t] = *reinterpret_cast<const h8*>(&Ws[b][(wn + 16 * t + li) * kGfLds + lk]);   \
-        }                                                                                      \
-        _Pragma("unroll") for (int i = 0; i < 4; ++i)                                          \
+        _Pragma("unroll") for (int i = 0; i < RT; ++i)                                         \
             _Pragma("unroll") for (int j = 0; j < 4; ++j) acc[i][j] =                          \
                 __builtin_amdgcn_mfma_f32_16x16x32_f16(av_[i], bv_[j], acc[i][j], 0, 0, 0);    \
         PE_GF_LSTORE((b) ^ 1);                                                                 \
@@ -160,7 +164,7 @@ __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
             if (ng >= p.N) continue;
             const int64_t f = ng / 2 + li;   // ffn column
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < RT; ++i)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int64_t m = m0 + 16 * i + 4 * (l >> 4) + r;
@@ -177,7 +181,7 @@ __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
         if (n >= p.N) continue;
         const float bb = BIAS ? p.bias[n] : 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < RT; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t m = m0 + 16 * i + 4 * (l >> 4) + r;
@@ -194,6 +198,17 @@ __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
 
 using namespace pe;
 
+// 64 x 128 workgroup tiles when 128 x 128 ones would make fewer than 512 workgroups (two per
+// CU) and the shorter tile still makes at least 512.
+static bool gf_short(int64_t M, int64_t N) {
+    const int64_t nt = (N + kGfTile - 1) / kGfTile;
+    return ((M + 127) / 128) * nt < 512 && ((M + 63) / 64) * nt >= 512;
+}
+template <int RT>
+static dim3 gf_grid(int64_t M, int64_t N) {
+    return dim3((unsigned)((N + kGfTile - 1) / kGfTile), (unsigned)((M + 32 * RT - 1) / (32 * RT)));
+}
+
 extern "C" int pe_gemm_f16_silu(const float* a, int64_t lda, const void* w_f16_il, float* c,
                                 int64_t ldc, int64_t M, int64_t ffn, int64_t K, pe_stream_t stream) {
     if (M < 0 || ffn <= 0 || ffn % 16 || K <= 0 || K % kGfK) return PE_ERR_SHAPE;
@@ -204,8 +219,9 @@ extern "C" int pe_gemm_f16_silu(const float* a, int64_t lda, const void* w_f16_i
     if (!a || !w_f16_il || !c) return PE_ERR_NULL;
     if (!aligned(a, 16) || lda % 4 || !aligned(w_f16_il, 16) || !aligned(c, 4)) return PE_ERR_ALIGN;
     GemmF16Args p{a, lda, (const _Float16*)w_f16_il, nullptr, nullptr, 0, c, ldc, M, N, K};
-    const dim3 grid((unsigned)((N + kGfTile - 1) / kGfTile), (unsigned)((M + kGfTile - 1) / kGfTile));
-    hipLaunchKernelGGL((k_gemm_f16<false, false, true>), grid, dim3(256), 0, (hipStream_t)stream, p);
+    hipStream_t s = (hipStream_t)stream;
+    if (gf_short(M, N)) hipLaunchKernelGGL((k_gemm_f16<2, false, false, true>), gf_grid<2>(M, N), dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((k_gemm_f16<4, false, false, true>), gf_grid<4>(M, N), dim3(256), 0, s, p);
     return launch_status();
 }
 
@@ -221,11 +237,19 @@ extern "C" int pe_gemm_f16(const float* a, int64_t lda, const void* w_f16, const
         !aligned(residual, 4))
         return PE_ERR_ALIGN;
     GemmF16Args p{a, lda, (const _Float16*)w_f16, bias, residual, ldr, c, ldc, M, N, K};
-    const dim3 grid((unsigned)((N + kGfTile - 1) / kGfTile), (unsigned)((M + kGfTile - 1) / kGfTile));
     hipStream_t s = (hipStream_t)stream;
-    if (bias && residual) hipLaunchKernelGGL((k_gemm_f16<true, true>), grid, dim3(256), 0, s, p);
-    else if (bias) hipLaunchKernelGGL((k_gemm_f16<true, false>), grid, dim3(256), 0, s, p);
-    else if (residual) hipLaunchKernelGGL((k_gemm_f16<false, true>), grid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((k_gemm_f16<false, false>), grid, dim3(256), 0, s, p);
+    if (gf_short(M, N)) {
+        const dim3 grid = gf_grid<2>(M, N);
+        if (bias && residual) hipLaunchKernelGGL((k_gemm_f16<2, true, true>), grid, dim3(256), 0, s, p);
+        else if (bias) hipLaunchKernelGGL((k_gemm_f16<2, true, false>), grid, dim3(256), 0, s, p);
+        else if (residual) hipLaunchKernelGGL((k_gemm_f16<2, false, true>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((k_gemm_f16<2, false, false>), grid, dim3(256), 0, s, p);
+    } else {
+        const dim3 grid = gf_grid<4>(M, N);
+        if (bias && residual) hipLaunchKernelGGL((k_gemm_f16<4, true, true>), grid, dim3(256), 0, s, p);
+        else if (bias) hipLaunchKernelGGL((k_gemm_f16<4, true, false>), grid, dim3(256), 0, s, p);
+        else if (residual) hipLaunchKernelGGL((k_gemm_f16<4, false, true>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((k_gemm_f16<4, false, false>), grid, dim3(256), 0, s, p);
+    }
     return launch_status();
 }

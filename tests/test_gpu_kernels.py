@@ -916,6 +916,8 @@ GEMM16_CASES = [  # (M, N, K, bias, residual, a_row_stride_extra)
     (8192, 1152, 896, True, False, 0),
     # 256 x 128 workgroup tiles (>= 512 of them), ragged edges included
     (4096, 4096, 96, True, True, 0), (4000, 4000, 64, False, False, 32),
+    # 64 x 128 workgroup tiles (the 128 x 128 grid would have < 512 workgroups)
+    (8192, 896, 256, False, True, 0), (4100, 1000, 64, True, False, 0),
 ]
 
 
