@@ -120,10 +120,16 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
         for (int i = 0; i < 2; ++i) {
             int f = t + nt * i;
             f = f < 1024 ? f : f & 1023;
-            const int key = f >> 4, d4 = f & 15;
-            const int64_t kr = j0 + key < n_keys ? j0 + key : n_keys - 1;
-            kr4[i] = reinterpret_cast<const float4*>(kb + kr * kFpHd)[d4];
-            vr4[i] = reinterpret_cast<const float4*>(vb + kr * kFpHd)[d4];
+            // K: 16 consecutive threads read one key row (coalesced, row-major LDS store);
+            // V: consecutive threads read consecutive keys at one dim quad, so the transposed
+            // LDS stores of a wave hit consecutive 16-bit slots (with the K mapping they were
+            // 576 bytes apart, 8-way bank conflicts)
+            const int kkey = f >> 4, kd4 = f & 15;
+            const int vkey = f & 63, vd4 = f >> 6;
+            const int64_t kr = j0 + kkey < n_keys ? j0 + kkey : n_keys - 1;
+            const int64_t vr = j0 + vkey < n_keys ? j0 + vkey : n_keys - 1;
+            kr4[i] = reinterpret_cast<const float4*>(kb + kr * kFpHd)[kd4];
+            vr4[i] = reinterpret_cast<const float4*>(vb + vr * kFpHd)[vd4];
         }
     };
     kv_load(0);
@@ -133,15 +139,16 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
         for (int i = 0; i < 2; ++i) {
             const int f = t + nt * i;
             if (f < 1024) {
-                const int key = f >> 4, d4 = f & 15;
+                const int kkey = f >> 4, kd4 = f & 15;
+                const int vkey = f & 63, vd4 = f >> 6;
                 const float4 kv = kr4[i], vv = vr4[i];
                 typedef _Float16 fh4 __attribute__((ext_vector_type(4)));
-                *reinterpret_cast<fh4*>(ks + key * kFpRow + 4 * d4) =
+                *reinterpret_cast<fh4*>(ks + kkey * kFpRow + 4 * kd4) =
                     fh4{(_Float16)kv.x, (_Float16)kv.y, (_Float16)kv.z, (_Float16)kv.w};
-                vt[(4 * d4 + 0) * kFpRow + key] = (_Float16)vv.x;
-                vt[(4 * d4 + 1) * kFpRow + key] = (_Float16)vv.y;
-                vt[(4 * d4 + 2) * kFpRow + key] = (_Float16)vv.z;
-                vt[(4 * d4 + 3) * kFpRow + key] = (_Float16)vv.w;
+                vt[(4 * vd4 + 0) * kFpRow + vkey] = (_Float16)vv.x;
+                vt[(4 * vd4 + 1) * kFpRow + vkey] = (_Float16)vv.y;
+                vt[(4 * vd4 + 2) * kFpRow + vkey] = (_Float16)vv.z;
+                vt[(4 * vd4 + 3) * kFpRow + vkey] = (_Float16)vv.w;
             }
         }
         __syncthreads();
@@ -158,7 +165,9 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
                 sacc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], kbv, sacc[jt], 0, 0, 0);
             }
         }
-        // scale, causal mask, online softmax per row (base 2)
+        // scale, causal mask, online softmax per row (base 2). Blocks whose 64 keys every
+        // query of the wave sees (all but the diagonal ones) skip the mask (a wave-uniform test).
+        const bool full = j0 + kFpKeys - 1 <= p.pos0 + q0 && j0 + kFpKeys <= n_keys;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int64_t qpos = p.pos0 + q0 + 4 * lg + r;
@@ -166,7 +175,7 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
 #pragma unroll
             for (int jt = 0; jt < 4; ++jt) {
                 const int64_t key = j0 + 16 * jt + li;
-                sv[jt] = (key <= qpos && key < n_keys) ? sacc[jt][r] * sl2 : NEG_INF;
+                sv[jt] = (full || (key <= qpos && key < n_keys)) ? sacc[jt][r] * sl2 : NEG_INF;
                 mx = fmaxf(mx, sv[jt]);
             }
             mx = row16_max(mx);
