@@ -175,7 +175,7 @@ def test_qgemv_rmsnorm_silu(K, t, k, ffn):
     assert rel_err(act, closed.silu_mul(gu[:ffn], gu[ffn:])) < TOL
 
 
-@pytest.mark.parametrize("m", [1, 5, 8, 13, 17])
+@pytest.mark.parametrize("m", [1, 5, 8, 13, 17, 64, 100, 129])
 @pytest.mark.parametrize("t,k,n", [(dq.Q5_0, 896, 1152), (dq.Q6_K, 4864, 896), (dq.Q8_0, 896, 300)])
 def test_qgemm_prefill(K, m, t, k, n):
     raw = quantized_normal(t, n, k, seed=m + n)
