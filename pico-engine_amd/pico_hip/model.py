@@ -176,7 +176,7 @@ class Transformer:
         if token_ids.shape[0] == 1:
             return self._decode(token_ids, positions, cache, greedy)
         m = self.prefill_f16_min_tokens
-        if m is not None and token_ids.shape[0] >= m and self.cfg.head_dim == 64:
+        if m is not None and token_ids.shape[0] >= m:
             return self._prefill_f16(token_ids, positions, cache, greedy)
         return self._prefill(token_ids, positions, cache, greedy)
 
@@ -300,7 +300,8 @@ class Transformer:
     # ---- prefill --------------------------------------------------------------------------
     def _prefill_f16(self, token_ids, positions, cache, greedy=None):
         """The prefill on the matrix cores: GEMMs with fp16 operands (pe_gemm_f16) and flash
-        attention (pe_flash_prefill), fp32 residual stream, norms, RoPE and KV cache."""
+        attention (pe_flash_prefill; head_dim 64, else the fp32 prefill attention), fp32
+        residual stream, norms, RoPE and KV cache."""
         cfg = self.cfg
         Lt = token_ids.shape[0]
         hd, nh, nkv = cfg.head_dim, cfg.n_head, cfg.n_kv_head
@@ -319,7 +320,10 @@ class Transformer:
             qk = K.rope(qkv[:, :qd + kd].view(Lt, nh + nkv, hd), cos, sin)
             v = qkv[:, qd + kd:].view(Lt, nkv, hd)
             K.kv_write(qk[:, nh:], v, k_buf, v_buf, pos0=pos0)
-            attn = K.flash_prefill(qk[:, :nh], k_buf, v_buf, pos0=pos0)  # (L, hidden)
+            if hd == 64:  # matrix-core flash attention
+                attn = K.flash_prefill(qk[:, :nh], k_buf, v_buf, pos0=pos0)  # (L, hidden)
+            else:         # other head sizes: the fp32 causal attention kernel
+                attn = K.prefill_attn(qk[:, :nh], k_buf, v_buf, pos0=pos0)
             x = K.gemm_f16(attn, W["o"], residual=x)
             h = K.rmsnorm(x, L.ffn_norm, cfg.eps)
             if W["gu_il"] is not None:

@@ -250,3 +250,25 @@ def test_device_built_model_matches_oracle(tmp_path):
 
 
 DEV_GPU = "cuda"
+
+
+def test_7b_family_prefill_f16_close_to_fp32_path(tiny7b):
+    """The matrix-core prefill at head_dim 128 (fp16 GEMMs + the fp32 prefill attention)
+    against the fp32 prefill on the same 100-token prompt: logits and the decode step after."""
+    eng, _ = tiny7b
+    m = eng.model
+    ids = [(11 * i + 5) % 2048 for i in range(100)]
+    saved = m.prefill_f16_min_tokens
+    out = {}
+    try:
+        for mode, thr in (("fp32", None), ("f16", 2)):
+            m.prefill_f16_min_tokens = thr
+            cache = eng._empty_cache(len(ids) + 2)
+            lg = m.forward(torch.tensor(ids, device=eng.device), torch.arange(len(ids), device=eng.device), cache)
+            nxt = int(lg.argmax())
+            lg2 = m.forward(torch.tensor([nxt], device=eng.device), torch.tensor([len(ids)], device=eng.device), cache)
+            out[mode] = (lg.cpu().numpy(), lg2.cpu().numpy())
+    finally:
+        m.prefill_f16_min_tokens = saved
+    assert rel_err(out["f16"][0], out["fp32"][0]) < 2e-2
+    assert rel_err(out["f16"][1], out["fp32"][1]) < 2e-2
