@@ -298,10 +298,22 @@ PE_DEV float load_activation(const GemvArgs& a, int glane, int units, float (&xr
 // The double-buffered loop (CLAMP) clamps in every group width: a lane-divergent branch
 // around the loads would make the compiler wait for all outstanding loads after it, the
 // prefetched chunk's included.
-template <int T, int GS, int UPL, int R, bool CLAMP = false>
+template <int T, int GS, int UPL, int R, bool CLAMP = false, int UM = 0>
 PE_DEV void load_task(const GemvArgs& a, int64_t task, int glane, int units,
                       typename Fmt<T>::Raw (&raw)[R][UPL]) {
     const int64_t tc = task < a.n_tasks ? task : a.n_tasks - 1;
+    if constexpr (UM == 1) {
+        // Q4_K unit pair: one load of the chunk and head; the second unit is the same bytes,
+        // the next sub-block (units is a multiple of 8, so 2 glane clamps to an even unit)
+        const int u0 = 2 * glane < units ? 2 * glane : units - 2;
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr) {
+            Fmt<T>::load(a.w, tc + rr * a.up_off, u0, raw[rr][0]);
+            raw[rr][1] = raw[rr][0];
+            raw[rr][1].sub = raw[rr][0].sub + 1;
+        }
+        return;
+    }
 #pragma unroll
     for (int rr = 0; rr < R; ++rr)
 #pragma unroll
@@ -415,14 +427,21 @@ PE_DEV void issue_activation(const GemvArgs& a, int units, ActLoads<M4>& L) {
 // applied by the caller after the dot product; otherwise 1. Vectors longer than kStageMaxK
 // are read per lane straight from global memory. Every thread of the block must call it.
 // Unstaged path: each lane reads its own units of x (and norm_w) from global memory.
-template <int GS, int UPL, bool NORM>
+// Unit of slot t of lane glane. UM 0: units glane, glane + GS, ... (strided). UM 1 (Q4_K at
+// two units per lane): units 2 glane and 2 glane + 1, the low and high nibbles of one 32-byte
+// qs chunk under one 16-byte head, so a lane loads each chunk and head once instead of two
+// lanes loading it twice (half the load bytes per weight).
+template <int GS, int UM>
+PE_DEV int unit_index(int glane, int t) { return UM == 1 ? 2 * glane + t : glane + GS * t; }
+
+template <int GS, int UPL, bool NORM, int UM = 0>
 PE_DEV float direct_activation(const GemvArgs& a, int glane, int units, float (&xr)[UPL][32],
                                UnitSums (&xs)[UPL], float* lds4) {
     const bool ut = a.layout & PE_LAYOUT_X_UT;
     float ss = 0.f;
 #pragma unroll
     for (int t = 0; t < UPL; ++t) {
-        const int u = glane + GS * t;
+        const int u = unit_index<GS, UM>(glane, t);
         if (u < units) {
             if (ut) load_x_unit_ut(a.x, u, units, xr[t]);
             else load_x_unit(a.x, u, xr[t]);
@@ -449,7 +468,7 @@ PE_DEV float direct_activation(const GemvArgs& a, int glane, int units, float (&
     return 1.0f;
 }
 
-template <int NT, int GS, int UPL, bool NORM, int SUM = kSumNone>
+template <int NT, int GS, int UPL, bool NORM, int SUM = kSumNone, int UM = 0>
 PE_DEV float finish_activation(const GemvArgs& a, int glane, int units,
                                const ActLoads<act_loads<NT, GS, UPL>()>& L, float (&xr)[UPL][32],
                                UnitSums (&xs)[UPL], float* lds4, float* stage) {
@@ -502,7 +521,7 @@ PE_DEV float finish_activation(const GemvArgs& a, int glane, int units,
         else __syncthreads();
 #pragma unroll
         for (int t = 0; t < UPL; ++t) {
-            const int u = glane + GS * t;
+            const int u = unit_index<GS, UM>(glane, t);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -516,17 +535,17 @@ PE_DEV float finish_activation(const GemvArgs& a, int glane, int units,
         }
         return rstd;
     }
-    return direct_activation<GS, UPL, NORM>(a, glane, units, xr, xs, lds4);
+    return direct_activation<GS, UPL, NORM, UM>(a, glane, units, xr, xs, lds4);
 }
 
 
 // Stage without a register holder: each thread loads, normalises and stores one float4 at a
 // time (for long activations, where a holder would cost occupancy). Same result as
 // issue_activation + finish_activation.
-template <int NT, int GS, int UPL, bool NORM, int SUM = kSumNone>
+template <int NT, int GS, int UPL, bool NORM, int SUM = kSumNone, int UM = 0>
 PE_DEV float stream_activation(const GemvArgs& a, int glane, int units, float (&xr)[UPL][32],
                                UnitSums (&xs)[UPL], float* lds4, float* stage) {
-    if (a.k > kStageMaxK) return direct_activation<GS, UPL, NORM>(a, glane, units, xr, xs, lds4);
+    if (a.k > kStageMaxK) return direct_activation<GS, UPL, NORM, UM>(a, glane, units, xr, xs, lds4);
     const bool ut = a.layout & PE_LAYOUT_X_UT;
     const int n4 = units * 8;
     float ss = 0.f;
@@ -564,7 +583,7 @@ PE_DEV float stream_activation(const GemvArgs& a, int glane, int units, float (&
     else __syncthreads();
 #pragma unroll
     for (int t = 0; t < UPL; ++t) {
-        const int u = glane + GS * t;
+        const int u = unit_index<GS, UM>(glane, t);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -619,6 +638,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
     const int units = (int)(a.k >> 5);
     const int64_t nchunk = (a.n_tasks + CH - 1) / CH;
     int64_t chunk = blockIdx.x;
+    constexpr int UM = (T == PE_TYPE_Q4_K && GS == 64 && UPL == 2) ? 1 : 0;
 
     using RawT = typename Fmt<T>::Raw;
     RawT raw[TPG][R][UPL];
@@ -627,7 +647,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
 #pragma unroll
         for (int i = 0; i < TPG; ++i) {
             const int64_t task = c * CH + i * G + gid;
-            load_task<T, GS, UPL, R, DB>(a, task, glane, units, rw[i]);
+            load_task<T, GS, UPL, R, DB, UM>(a, task, glane, units, rw[i]);
             if constexpr (kEpi) ep[i] = load_epi(a, task);
         }
     };
@@ -645,10 +665,10 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
         ActLoads<act_loads<NT, GS, UPL>()> act;
         issue_activation<NT, NORM, act_loads<NT, GS, UPL>(), kSum>(a, units, act);
         issue(chunk);  // the grid is at most nchunk blocks
-        rstd = finish_activation<NT, GS, UPL, NORM, kSum>(a, glane, units, act, xr, xs, lds4, stage);
+        rstd = finish_activation<NT, GS, UPL, NORM, kSum, UM>(a, glane, units, act, xr, xs, lds4, stage);
     } else {
         issue(chunk);
-        rstd = stream_activation<NT, GS, UPL, NORM, kSum>(a, glane, units, xr, xs, lds4, stage);
+        rstd = stream_activation<NT, GS, UPL, NORM, kSum, UM>(a, glane, units, xr, xs, lds4, stage);
     }
 
     uint64_t best = 0;  // argmax mode: best key of this group's tasks
@@ -661,7 +681,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
                 acc[i][rr] = 0.f;
 #pragma unroll
                 for (int t = 0; t < UPL; ++t)
-                    if (glane + GS * t < units) acc[i][rr] += Fmt<T>::dot(rw[i][rr][t], xr[t], xs[t]);
+                    if (unit_index<GS, UM>(glane, t) < units) acc[i][rr] += Fmt<T>::dot(rw[i][rr][t], xr[t], xs[t]);
             }
     };
     // group reductions, epilogue and stores of chunk c0
