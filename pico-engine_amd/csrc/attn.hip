@@ -207,27 +207,12 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_attn_merge(AttnParams 
     const float* base = p.partials + (int64_t)kvh * p.nsplit * G * REC + (int64_t)g * REC;
     const int64_t rstride = (int64_t)G * REC;
     const float NEG_INF = -__builtin_huge_valf();
-    // records in batches of kMergeBatch per lane group, every load of a batch issued before
-    // the first use (indices clamped to the last valid record, masked afterwards)
+    // One pass over the records: batches of kMergeBatch per lane group, every load of a batch
+    // issued before the first use (indices clamped to the last valid record, masked
+    // afterwards); the group keeps a running maximum and rescales its sums when it grows
+    // (one read of each record instead of a max pass and a sum pass).
     const int last = nvalid > 0 ? nvalid - 1 : 0;
-    float m = NEG_INF;
-    for (int s0 = jg; s0 < nvalid; s0 += NG * kMergeBatch) {
-        float mb[kMergeBatch];
-#pragma unroll
-        for (int b = 0; b < kMergeBatch; ++b) {
-            const int sp = s0 + NG * b;
-            mb[b] = base[(int64_t)(sp < last ? sp : last) * rstride];
-        }
-#pragma unroll
-        for (int b = 0; b < kMergeBatch; ++b)
-            if (s0 + NG * b < nvalid) m = fmaxf(m, mb[b]);
-    }
-    if (dd == 0) ml[0][jg] = m;
-    __syncthreads();
-    float M = ml[0][0];
-#pragma unroll
-    for (int j = 1; j < NG; ++j) M = fmaxf(M, ml[0][j]);
-    float L = 0.f, A = 0.f;
+    float M = NEG_INF, L = 0.f, A = 0.f;
     for (int s0 = jg; s0 < nvalid; s0 += NG * kMergeBatch) {
         float rm[kMergeBatch], rl[kMergeBatch], ra[kMergeBatch];
 #pragma unroll
@@ -238,15 +223,33 @@ __global__ __launch_bounds__(kMergeThreads) void k_decode_attn_merge(AttnParams 
             rl[b] = r[1];
             ra[b] = r[2 + dd];
         }
+        float bm = NEG_INF;
+#pragma unroll
+        for (int b = 0; b < kMergeBatch; ++b)
+            if (s0 + NG * b < nvalid) bm = fmaxf(bm, rm[b]);
+        const float Mn = fmaxf(M, bm);
+        const float c = M == NEG_INF ? 0.f : expf(M - Mn);
+        L *= c;
+        A *= c;
 #pragma unroll
         for (int b = 0; b < kMergeBatch; ++b) {
             if (s0 + NG * b < nvalid) {
-                const float e = expf(rm[b] - M);
+                const float e = expf(rm[b] - Mn);
                 L = fmaf(rl[b], e, L);
                 A = fmaf(ra[b], e, A);
             }
         }
+        M = Mn;
     }
+    // combine the lane groups in group order at the common maximum
+    if (dd == 0) ml[0][jg] = M;
+    __syncthreads();
+    float Mg = ml[0][0];
+#pragma unroll
+    for (int j = 1; j < NG; ++j) Mg = fmaxf(Mg, ml[0][j]);
+    const float cg = M == NEG_INF ? 0.f : expf(M - Mg);
+    L *= cg;
+    A *= cg;
     red[jg][dd] = A;
     if (dd == 0) ml[1][jg] = L;
     __syncthreads();
