@@ -11,7 +11,8 @@
 // with the log-sum-exp rule in a fixed order, so the result does not depend on the order in
 // which the workgroups ran.
 //
-// Caches of at most 1024 positions use a single-pass kernel (one workgroup per query head).
+// Caches of at most kSmallCap (256) positions use a single-pass kernel (one workgroup per
+// query head).
 //
 // Prefill (L query tokens, causal), restating the fp32 SDPA call of model.py:201-209.
 #include "pe_common.h"

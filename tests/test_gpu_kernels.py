@@ -276,20 +276,22 @@ def test_decode_attn_long_context_and_len_forms(K):
     assert rel_err(out, ref) < TOL
 
 
-def test_decode_attn_unrounded_and_clamp(K):
+# single pass (100), split + merge launch (10 and 24 chunks of 64 positions)
+@pytest.mark.parametrize("cap", [100, 600, 1500])
+def test_decode_attn_unrounded_and_clamp(K, cap):
     rng = np.random.default_rng(8)
     q = rng.standard_normal((14, 64)).astype(np.float32)
-    k, v = _kv(rng, 2, 100, 64)
+    k, v = _kv(rng, 2, cap, 64)
     Q, Kc, Vc = (torch.from_numpy(a).to(DEV) for a in (q, k, v))
     out = K.decode_attn(Q, Kc, Vc, S=90, round_fp16=False).cpu().numpy()
     assert rel_err(out, closed.attention(q, k, v, 90)) < 1e-5
-    over = K.decode_attn(Q, Kc, Vc, S=1000).cpu().numpy()  # S > capacity clamps (kernels.py:110)
-    assert rel_err(over, closed.attention(q, k, v, 100)) < TOL
+    over = K.decode_attn(Q, Kc, Vc, S=cap + 900).cpu().numpy()  # S > capacity clamps (kernels.py:110)
+    assert rel_err(over, closed.attention(q, k, v, cap)) < TOL
     empty = K.decode_attn(Q, Kc, Vc, S=0).cpu().numpy()   # S = 0: 0/0 like the reference
     assert np.all(np.isnan(empty))
 
 
-@pytest.mark.parametrize("cap", [300, 1500])  # single-pass kernel / split kernel with merge
+@pytest.mark.parametrize("cap", [200, 300, 1500])  # single pass / split + merge launch
 def test_decode_attn_workspace_reuse_and_graph(K, cap):
     """One workspace across many in-order calls and across graph replays with a device S."""
     rng = np.random.default_rng(9)
