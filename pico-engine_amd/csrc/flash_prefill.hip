@@ -11,12 +11,14 @@
 // group x QB/16 waves (QB = 16 * max(1, 16 / group): 14 waves of 32 queries for the
 // 7-heads-per-kv-head models), so each 64-key block of K and V is read from HBM and staged in
 // LDS once for all the query heads that share it. K is staged row-major and V transposed (a
-// lane's MFMA operand -- 8 consecutive keys of one dimension -- is one 16-byte LDS read), both
+// lane's MFMA operand -- 8 keys of one dimension -- is one 16-byte LDS read), both
 // in fp16; the next block's K/V loads are issued before the current block's MFMAs. Each wave
-// computes its 16 x 64 score tile (8 MFMAs), the online-softmax update in the exp2 domain
-// (scale * log2 e folded into the scores) with DPP row reductions, writes P to its own LDS
-// tile (a wave-local handoff, no block barrier) and accumulates O += P V (8 MFMAs). The
-// heaviest query blocks (most keys) are scheduled first.
+// computes its 64 x 16 transposed score tile S^T = K Q^T (8 MFMAs), so that every lane holds
+// one query's scores: the online-softmax update (exp2 domain, scale * log2 e applied in the
+// exponent's fma) keeps one running max and sum per lane with two cross-lane steps, and the
+// probabilities go straight from registers into the B operand of O^T += V^T P^T (8 MFMAs),
+// with V^T staged in the matching key order. The heaviest query blocks (most keys) are
+// scheduled first.
 #include "pe_common.h"
 
 namespace pe {
@@ -47,22 +49,6 @@ struct FlashParams {
     int64_t out_stride;
 };
 
-// Sum / max over aligned groups of 16 lanes (DPP within a row; every lane gets the same bits).
-PE_DEV float row16_max(float v) {
-    v = fmaxf(v, dpp_mov<0xB1>(v));
-    v = fmaxf(v, dpp_mov<0x4E>(v));
-    v = fmaxf(v, dpp_mov<0x141>(v));
-    v = fmaxf(v, dpp_mov<0x140>(v));
-    return v;
-}
-PE_DEV float row16_sum(float v) {
-    v += dpp_mov<0xB1>(v);
-    v += dpp_mov<0x4E>(v);
-    v += dpp_mov<0x141>(v);
-    v += dpp_mov<0x140>(v);
-    return v;
-}
-
 PE_DEV fh8 f8_to_h8(float4 a, float4 b) {
     fh8 r;
     r[0] = (_Float16)a.x; r[1] = (_Float16)a.y; r[2] = (_Float16)a.z; r[3] = (_Float16)a.w;
@@ -73,7 +59,6 @@ PE_DEV fh8 f8_to_h8(float4 a, float4 b) {
 __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_size) {
     __shared__ __align__(16) _Float16 ks[kFpKeys * kFpRow];         // K block, [key][dim]
     __shared__ __align__(16) _Float16 vt[kFpHd * kFpRow];           // V block transposed, [dim][key]
-    __shared__ __align__(16) _Float16 ps[kFpMaxWaves][16 * kFpRow]; // per wave: P, [query][key]
     const int t = threadIdx.x, nt = blockDim.x, w = t >> 6, l = t & 63;
     const int li = l & 15, lg = l >> 4;
     const int64_t nqb = (p.L + qb_size - 1) / qb_size;
@@ -99,14 +84,13 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
             qa[s] = f8_to_h8(a, b);
         }
     }
-    // rows of this lane's score / output tiles: query q0 + 4 lg + r
-    float m_run[4], l_run[4];
+    // One query per lane: the score tile is computed transposed, S^T = K Q^T (A = K rows,
+    // B = the Q operand above), so lane (li, lg) holds the scores of query q0 + li against keys
+    // 16 jt + 4 lg + r (r < 4) of the block, and the output transposed, O^T = V^T P^T, holds
+    // dims 16 d + 4 lg + r of the same query. The softmax state is then one (max, sum) per lane.
+    const int64_t qpos = p.pos0 + q0 + li;
+    float m_run = NEG_INF, l_run = 0.f;
     fv4 o[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        m_run[r] = NEG_INF;
-        l_run[r] = 0.f;
-    }
 #pragma unroll
     for (int d = 0; d < 4; ++d) o[d] = fv4{0.f, 0.f, 0.f, 0.f};
 
@@ -134,27 +118,31 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
     };
     kv_load(0);
     for (int64_t j0 = 0; j0 < key_end; j0 += kFpKeys) {
-        // stage this block (fp32 -> fp16), then put the next block's loads in flight
+        // stage this block (fp32 -> fp16), then put the next block's loads in flight. V^T rows
+        // hold the keys of each 32-key slab in the order of the P^T operand: slot 8 g + i is key
+        // 4 g + i for i < 4 and 16 + 4 g + (i - 4) for i >= 4, the keys lane group g holds.
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int f = t + nt * i;
             if (f < 1024) {
                 const int kkey = f >> 4, kd4 = f & 15;
                 const int vkey = f & 63, vd4 = f >> 6;
+                const int c = vkey & 31;
+                const int vpos = (vkey & 32) + 8 * ((c >> 2) & 3) + 4 * (c >> 4) + (c & 3);
                 const float4 kv = kr4[i], vv = vr4[i];
                 typedef _Float16 fh4 __attribute__((ext_vector_type(4)));
                 *reinterpret_cast<fh4*>(ks + kkey * kFpRow + 4 * kd4) =
                     fh4{(_Float16)kv.x, (_Float16)kv.y, (_Float16)kv.z, (_Float16)kv.w};
-                vt[(4 * vd4 + 0) * kFpRow + vkey] = (_Float16)vv.x;
-                vt[(4 * vd4 + 1) * kFpRow + vkey] = (_Float16)vv.y;
-                vt[(4 * vd4 + 2) * kFpRow + vkey] = (_Float16)vv.z;
-                vt[(4 * vd4 + 3) * kFpRow + vkey] = (_Float16)vv.w;
+                vt[(4 * vd4 + 0) * kFpRow + vpos] = (_Float16)vv.x;
+                vt[(4 * vd4 + 1) * kFpRow + vpos] = (_Float16)vv.y;
+                vt[(4 * vd4 + 2) * kFpRow + vpos] = (_Float16)vv.z;
+                vt[(4 * vd4 + 3) * kFpRow + vpos] = (_Float16)vv.w;
             }
         }
         __syncthreads();
         kv_load(j0 + kFpKeys < key_end ? j0 + kFpKeys : j0);
 
-        // S = Q K^T for 4 key tiles of 16
+        // S^T = K Q^T for 4 key tiles of 16
         fv4 sacc[4];
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
@@ -162,65 +150,69 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
                 const fh8 kbv = *reinterpret_cast<const fh8*>(ks + (16 * jt + li) * kFpRow + 32 * s + 8 * lg);
-                sacc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[s], kbv, sacc[jt], 0, 0, 0);
+                sacc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kbv, qa[s], sacc[jt], 0, 0, 0);
             }
         }
-        // scale, causal mask, online softmax per row (base 2). Blocks whose 64 keys every
-        // query of the wave sees (all but the diagonal ones) skip the mask (a wave-uniform test).
+        // causal mask (only blocks not every query of the wave sees in full: a wave-uniform
+        // test), block maximum of the raw scores over the 4 lane groups, online softmax in
+        // base 2 with scale * log2 e applied in the exponent's fma. Every query sees key 0 in
+        // the first block, so the running maximum is finite from then on.
         const bool full = j0 + kFpKeys - 1 <= p.pos0 + q0 && j0 + kFpKeys <= n_keys;
+        float mx = NEG_INF;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t qpos = p.pos0 + q0 + 4 * lg + r;
-            float sv[4], mx = NEG_INF;
+        for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-            for (int jt = 0; jt < 4; ++jt) {
-                const int64_t key = j0 + 16 * jt + li;
-                sv[jt] = (full || (key <= qpos && key < n_keys)) ? sacc[jt][r] * sl2 : NEG_INF;
-                mx = fmaxf(mx, sv[jt]);
+            for (int r = 0; r < 4; ++r) {
+                if (!full) {
+                    const int64_t key = j0 + 16 * jt + 4 * lg + r;
+                    if (!(key <= qpos && key < n_keys)) sacc[jt][r] = NEG_INF;
+                }
+                mx = fmaxf(mx, sacc[jt][r]);
             }
-            mx = row16_max(mx);
-            const float m_new = fmaxf(m_run[r], mx);
-            const float corr = m_new == NEG_INF ? 1.f : __builtin_amdgcn_exp2f(m_run[r] - m_new);
-            float psum = 0.f;
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx * sl2);
+        const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+        float psum = 0.f;
+        fh8 pb[2];  // P^T operand of each 32-key slab: keys 4 lg + i, 16 + 4 lg + i
 #pragma unroll
-            for (int jt = 0; jt < 4; ++jt) {
-                const float e = m_new == NEG_INF ? 0.f : __builtin_amdgcn_exp2f(sv[jt] - m_new);
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float e = __builtin_amdgcn_exp2f(fmaf(sacc[jt][r], sl2, -m_new));
                 psum += e;
-                ps[w][(4 * lg + r) * kFpRow + 16 * jt + li] = (_Float16)e;
+                pb[jt >> 1][4 * (jt & 1) + r] = (_Float16)e;
             }
-            psum = row16_sum(psum);
-            l_run[r] = l_run[r] * corr + psum;
-            m_run[r] = m_new;
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        l_run = l_run * corr + psum;
+        m_run = m_new;
 #pragma unroll
-            for (int d = 0; d < 4; ++d) o[d][r] *= corr;
-        }
-        // P is read back by the same wave only: a wave-local LDS handoff
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[d][r] *= corr;
 
-        // O += P V: A = P (16 queries x 64 keys), B = V (64 keys x 16 dims) per dim tile
+        // O^T += V^T P^T: A = V^T (16 dims x 32 keys) per dim tile, B = P^T (32 keys x 16 queries)
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            const fh8 pa = *reinterpret_cast<const fh8*>(&ps[w][li * kFpRow + 32 * s + 8 * lg]);
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-                const fh8 vbv = *reinterpret_cast<const fh8*>(vt + (16 * d + li) * kFpRow + 32 * s + 8 * lg);
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vbv, o[d], 0, 0, 0);
+                const fh8 va = *reinterpret_cast<const fh8*>(vt + (16 * d + li) * kFpRow + 32 * s + 8 * lg);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[s], o[d], 0, 0, 0);
             }
         }
         __syncthreads();  // every wave is done with K / V before the next block is staged
     }
 
-    // out: O[row 4 lg + r][dim 16 d + li] / l
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int64_t qi = q0 + 4 * lg + r;
-        if (qi >= p.L) continue;
+    // out: O[query q0 + li][dim 16 d + 4 lg + r] / l
+    const int64_t qi = q0 + li;
+    if (qi < p.L) {
         float* orow = p.out + qi * p.out_stride + (int64_t)h * kFpHd;
-        const float inv = 1.0f / l_run[r];
+        const float inv = 1.0f / l_run;
 #pragma unroll
-        for (int d = 0; d < 4; ++d) orow[16 * d + li] = o[d][r] * inv;
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) orow[16 * d + 4 * lg + r] = o[d][r] * inv;
     }
 }
 
