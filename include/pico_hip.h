@@ -121,6 +121,20 @@ int pe_gemm_f16(const float* a, int64_t lda, const void* w_f16, const float* bia
 int pe_gemm_f16_silu(const float* a, int64_t lda, const void* w_f16_il, float* c, int64_t ldc,
                      int64_t M, int64_t ffn, int64_t K, pe_stream_t stream);
 
+/* pe_gemm_f16_silu storing c in fp16 (each value rounded to nearest even): c_f16 (M, ffn) with
+ * row stride ldc (elements). The rounding is the one the next prefill GEMM applies to its fp32
+ * A operand as it reads it, so pe_gemm_h16 on this output gives the same bits as pe_gemm_f16
+ * on the fp32 one, with half the activation bytes. Replaces model.py:218-224 (L > 1). */
+int pe_gemm_f16_silu_h(const float* a, int64_t lda, const void* w_f16_il, void* c_f16,
+                       int64_t ldc, int64_t M, int64_t ffn, int64_t K, pe_stream_t stream);
+
+/* pe_gemm_f16 with A already fp16 in memory: a_f16 (M, K) with row stride lda (elements,
+ * lda % 8 == 0, 16-byte aligned); everything else as pe_gemm_f16.
+ * Replaces the prefill down projection of model.py:235 (L > 1) after pe_gemm_f16_silu_h. */
+int pe_gemm_h16(const void* a_f16, int64_t lda, const void* w_f16, const float* bias,
+                const float* residual, int64_t ldr, float* c, int64_t ldc, int64_t M, int64_t N,
+                int64_t K, pe_stream_t stream);
+
 /* Causal GQA prompt-prefill attention on the matrix cores (flash attention): as
  * pe_prefill_attn, with q, k, v rounded to fp16 as they are read, fp32 scores, softmax and
  * accumulation, the probabilities rounded to fp16 for the P.V product. head_dim 64.

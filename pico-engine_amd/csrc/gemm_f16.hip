@@ -22,13 +22,15 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
 struct GemmF16Args {
-    const float* a;   // (M, K), row stride lda
+    const float* a;   // (M, K), row stride lda (fp32 A)
+    const _Float16* ah;  // (M, K), row stride lda (fp16 A, AH)
     int64_t lda;
     const _Float16* w;  // (N, K) row-major
     const float* bias;  // (N) or NULL
     const float* res;   // (M, N), row stride ldr, or NULL
     int64_t ldr;
     float* c;           // (M, N), row stride ldc
+    _Float16* ch;       // (M, N / 2), row stride ldc (fp16 SiLU output, CH)
     int64_t ldc;
     int64_t M, N, K;
 };
@@ -65,7 +67,10 @@ PE_DEV void gemm_tile_of_block(int64_t& tm, int64_t& tn) {
 // RT: 16-row MFMA tiles per wave along M: 4 (128 x 128 workgroup tile) or 2 (64 x 128, for
 // products whose 128 x 128 grid would leave CUs idle, e.g. N = 896 at M = 8192: 448 -> 896
 // workgroups).
-template <int RT, bool BIAS, bool RES, bool SILU = false>
+// AH: A is fp16 in memory (a producer stored it rounded, the same rounding as the fp32 path's
+// conversion on load): a K step of A is then a plain 16-byte copy per thread and row, laid out
+// like the W tile, and half the bytes. CH (with SILU): C is stored in fp16, rounded to nearest.
+template <int RT, bool BIAS, bool RES, bool SILU = false, bool AH = false, bool CH = false>
 __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
     constexpr int BM = 32 * RT;  // workgroup rows
     __shared__ __align__(16) _Float16 As[2][BM * kGfLds];
@@ -82,12 +87,22 @@ __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
     // W rows wr + 64 i (i < 2), fp16 columns wc .. wc + 7
     const int ar = tid >> 3, ac = (tid & 7) * 4;
     const int wr = tid >> 2, wc = (tid & 3) * 8;
+    constexpr int NAH = RT / 2;  // fp16 A: rows wr + 64 i, 8 halves at column wc
     const float* ap[RT];
+    const _Float16* ahp[NAH];
     const _Float16* wp[2];
+    if constexpr (AH) {
 #pragma unroll
-    for (int i = 0; i < RT; ++i) {
-        const int64_t m = bm + ar + 32 * i;
-        ap[i] = p.a + (m < p.M ? m : p.M - 1) * p.lda + ac;
+        for (int i = 0; i < NAH; ++i) {
+            const int64_t m = bm + wr + 64 * i;
+            ahp[i] = p.ah + (m < p.M ? m : p.M - 1) * p.lda + wc;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+            const int64_t m = bm + ar + 32 * i;
+            ap[i] = p.a + (m < p.M ? m : p.M - 1) * p.lda + ac;
+        }
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -95,6 +110,7 @@ __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
         wp[i] = p.w + (n < p.N ? n : p.N - 1) * p.K + wc;
     }
     float4 ra[RT];
+    uint4 rah[NAH];
     uint4 rw[2];
     f4v acc[RT][4];
 #pragma unroll
@@ -106,18 +122,28 @@ __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
 #define PE_GF_GLOAD(kk)                                                                        \
     do {                                                                                       \
         const int64_t k0_ = (int64_t)(kk) * kGfK;                                             \
-        _Pragma("unroll") for (int i = 0; i < RT; ++i) ra[i] =                                 \
-            *reinterpret_cast<const float4*>(ap[i] + k0_);                                     \
+        if constexpr (AH) {                                                                    \
+            _Pragma("unroll") for (int i = 0; i < NAH; ++i) rah[i] =                           \
+                *reinterpret_cast<const uint4*>(ahp[i] + k0_);                                 \
+        } else {                                                                               \
+            _Pragma("unroll") for (int i = 0; i < RT; ++i) ra[i] =                             \
+                *reinterpret_cast<const float4*>(ap[i] + k0_);                                 \
+        }                                                                                      \
         _Pragma("unroll") for (int i = 0; i < 2; ++i) rw[i] =                                  \
             *reinterpret_cast<const uint4*>(wp[i] + k0_);                                      \
     } while (0)
-// ra (rounded to fp16) / rw into LDS buffer b.
+// ra (rounded to fp16) or rah / rw into LDS buffer b.
 #define PE_GF_LSTORE(b)                                                                        \
     do {                                                                                       \
-        _Pragma("unroll") for (int i = 0; i < RT; ++i) {                                       \
-            const h4 v_ = {(_Float16)ra[i].x, (_Float16)ra[i].y, (_Float16)ra[i].z,            \
-                           (_Float16)ra[i].w};                                                 \
-            *reinterpret_cast<h4*>(&As[b][(ar + 32 * i) * kGfLds + ac]) = v_;                  \
+        if constexpr (AH) {                                                                    \
+            _Pragma("unroll") for (int i = 0; i < NAH; ++i)                                    \
+                *reinterpret_cast<uint4*>(&As[b][(wr + 64 * i) * kGfLds + wc]) = rah[i];       \
+        } else {                                                                               \
+            _Pragma("unroll") for (int i = 0; i < RT; ++i) {                                   \
+                const h4 v_ = {(_Float16)ra[i].x, (_Float16)ra[i].y, (_Float16)ra[i].z,        \
+                               (_Float16)ra[i].w};                                             \
+                *reinterpret_cast<h4*>(&As[b][(ar + 32 * i) * kGfLds + ac]) = v_;              \
+            }                                                                                  \
         }                                                                                      \
         _Pragma("unroll") for (int i = 0; i < 2; ++i)                                          \
             *reinterpret_cast<uint4*>(&Ws[b][(wr + 64 * i) * kGfLds + wc]) = rw[i];            \
@@ -170,7 +196,18 @@ __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
                     const int64_t m = m0 + 16 * i + 4 * (l >> 4) + r;
                     if (m >= p.M) continue;
                     const float g = acc[i][2 * c][r], u = acc[i][2 * c + 1][r];
-                    p.c[m * p.ldc + f] = (g * (1.0f / (1.0f + expf(-g)))) * u;
+                    float y = (g * (1.0f / (1.0f + expf(-g)))) * u;
+                    if constexpr (CH) {
+                        // y is rounded to fp32 first, then to fp16 (the reference's silu_mul
+                        // result, then autocast's operand rounding): without the barrier the
+                        // compiler fuses the product and the conversion into one mixed-precision
+                        // fma that rounds once, which differs on fp32 values halfway between
+                        // two fp16 ones
+                        asm volatile("" : "+v"(y));
+                        p.ch[m * p.ldc + f] = (_Float16)y;
+                    } else {
+                        p.c[m * p.ldc + f] = y;
+                    }
                 }
         }
         return;
@@ -209,47 +246,74 @@ static dim3 gf_grid(int64_t M, int64_t N) {
     return dim3((unsigned)((N + kGfTile - 1) / kGfTile), (unsigned)((M + 32 * RT - 1) / (32 * RT)));
 }
 
-extern "C" int pe_gemm_f16_silu(const float* a, int64_t lda, const void* w_f16_il, float* c,
-                                int64_t ldc, int64_t M, int64_t ffn, int64_t K, pe_stream_t stream) {
+template <bool CH>
+static int gemm_silu_entry(const float* a, int64_t lda, const void* w_f16_il, void* c, int64_t ldc,
+                           int64_t M, int64_t ffn, int64_t K, pe_stream_t stream) {
     if (M < 0 || ffn <= 0 || ffn % 16 || K <= 0 || K % kGfK) return PE_ERR_SHAPE;
     if (M == 0) return PE_OK;
     const int64_t N = 2 * ffn;
     if (lda < K || ldc < ffn) return PE_ERR_SHAPE;
     if ((M + kGfTile - 1) / kGfTile > 65535 || (N + kGfTile - 1) / kGfTile > 65535) return PE_ERR_SHAPE;
     if (!a || !w_f16_il || !c) return PE_ERR_NULL;
-    if (!aligned(a, 16) || lda % 4 || !aligned(w_f16_il, 16) || !aligned(c, 4)) return PE_ERR_ALIGN;
-    GemmF16Args p{a, lda, (const _Float16*)w_f16_il, nullptr, nullptr, 0, c, ldc, M, N, K};
+    if (!aligned(a, 16) || lda % 4 || !aligned(w_f16_il, 16) || !aligned(c, CH ? 2 : 4))
+        return PE_ERR_ALIGN;
+    GemmF16Args p{a, nullptr, lda, (const _Float16*)w_f16_il, nullptr, nullptr, 0,
+                  CH ? nullptr : (float*)c, CH ? (_Float16*)c : nullptr, ldc, M, N, K};
     hipStream_t s = (hipStream_t)stream;
-    if (gf_short(M, N)) hipLaunchKernelGGL((k_gemm_f16<2, false, false, true>), gf_grid<2>(M, N), dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((k_gemm_f16<4, false, false, true>), gf_grid<4>(M, N), dim3(256), 0, s, p);
+    if (gf_short(M, N))
+        hipLaunchKernelGGL((k_gemm_f16<2, false, false, true, false, CH>), gf_grid<2>(M, N), dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL((k_gemm_f16<4, false, false, true, false, CH>), gf_grid<4>(M, N), dim3(256), 0, s, p);
     return launch_status();
 }
 
-extern "C" int pe_gemm_f16(const float* a, int64_t lda, const void* w_f16, const float* bias,
-                           const float* residual, int64_t ldr, float* c, int64_t ldc, int64_t M,
-                           int64_t N, int64_t K, pe_stream_t stream) {
+template <bool AH>
+static int gemm_entry(const void* a, int64_t lda, const void* w_f16, const float* bias,
+                      const float* residual, int64_t ldr, float* c, int64_t ldc, int64_t M,
+                      int64_t N, int64_t K, pe_stream_t stream) {
     if (M < 0 || N <= 0 || K <= 0 || K % kGfK) return PE_ERR_SHAPE;
     if (M == 0) return PE_OK;
     if (lda < K || ldc < N || (residual && ldr < N)) return PE_ERR_SHAPE;
     if ((M + kGfTile - 1) / kGfTile > 65535 || (N + kGfTile - 1) / kGfTile > 65535) return PE_ERR_SHAPE;
     if (!a || !w_f16 || !c) return PE_ERR_NULL;
-    if (!aligned(a, 16) || lda % 4 || !aligned(w_f16, 16) || !aligned(c, 4) || !aligned(bias, 4) ||
-        !aligned(residual, 4))
+    if (!aligned(a, 16) || lda % (AH ? 8 : 4) || !aligned(w_f16, 16) || !aligned(c, 4) ||
+        !aligned(bias, 4) || !aligned(residual, 4))
         return PE_ERR_ALIGN;
-    GemmF16Args p{a, lda, (const _Float16*)w_f16, bias, residual, ldr, c, ldc, M, N, K};
+    GemmF16Args p{AH ? nullptr : (const float*)a, AH ? (const _Float16*)a : nullptr, lda,
+                  (const _Float16*)w_f16, bias, residual, ldr, c, nullptr, ldc, M, N, K};
     hipStream_t s = (hipStream_t)stream;
-    if (gf_short(M, N)) {
-        const dim3 grid = gf_grid<2>(M, N);
-        if (bias && residual) hipLaunchKernelGGL((k_gemm_f16<2, true, true>), grid, dim3(256), 0, s, p);
-        else if (bias) hipLaunchKernelGGL((k_gemm_f16<2, true, false>), grid, dim3(256), 0, s, p);
-        else if (residual) hipLaunchKernelGGL((k_gemm_f16<2, false, true>), grid, dim3(256), 0, s, p);
-        else hipLaunchKernelGGL((k_gemm_f16<2, false, false>), grid, dim3(256), 0, s, p);
-    } else {
-        const dim3 grid = gf_grid<4>(M, N);
-        if (bias && residual) hipLaunchKernelGGL((k_gemm_f16<4, true, true>), grid, dim3(256), 0, s, p);
-        else if (bias) hipLaunchKernelGGL((k_gemm_f16<4, true, false>), grid, dim3(256), 0, s, p);
-        else if (residual) hipLaunchKernelGGL((k_gemm_f16<4, false, true>), grid, dim3(256), 0, s, p);
-        else hipLaunchKernelGGL((k_gemm_f16<4, false, false>), grid, dim3(256), 0, s, p);
-    }
+#define PE_GF_LAUNCH(RT_)                                                                          \
+    do {                                                                                           \
+        const dim3 grid = gf_grid<RT_>(M, N);                                                      \
+        if (bias && residual) hipLaunchKernelGGL((k_gemm_f16<RT_, true, true, false, AH>), grid, dim3(256), 0, s, p); \
+        else if (bias) hipLaunchKernelGGL((k_gemm_f16<RT_, true, false, false, AH>), grid, dim3(256), 0, s, p);       \
+        else if (residual) hipLaunchKernelGGL((k_gemm_f16<RT_, false, true, false, AH>), grid, dim3(256), 0, s, p);   \
+        else hipLaunchKernelGGL((k_gemm_f16<RT_, false, false, false, AH>), grid, dim3(256), 0, s, p);                \
+    } while (0)
+    if (gf_short(M, N)) PE_GF_LAUNCH(2);
+    else PE_GF_LAUNCH(4);
+#undef PE_GF_LAUNCH
     return launch_status();
+}
+
+extern "C" int pe_gemm_f16_silu(const float* a, int64_t lda, const void* w_f16_il, float* c,
+                                int64_t ldc, int64_t M, int64_t ffn, int64_t K, pe_stream_t stream) {
+    return gemm_silu_entry<false>(a, lda, w_f16_il, c, ldc, M, ffn, K, stream);
+}
+
+extern "C" int pe_gemm_f16_silu_h(const float* a, int64_t lda, const void* w_f16_il, void* c_f16,
+                                  int64_t ldc, int64_t M, int64_t ffn, int64_t K, pe_stream_t stream) {
+    return gemm_silu_entry<true>(a, lda, w_f16_il, c_f16, ldc, M, ffn, K, stream);
+}
+
+extern "C" int pe_gemm_f16(const float* a, int64_t lda, const void* w_f16, const float* bias,
+                           const float* residual, int64_t ldr, float* c, int64_t ldc, int64_t M,
+                           int64_t N, int64_t K, pe_stream_t stream) {
+    return gemm_entry<false>(a, lda, w_f16, bias, residual, ldr, c, ldc, M, N, K, stream);
+}
+
+extern "C" int pe_gemm_h16(const void* a_f16, int64_t lda, const void* w_f16, const float* bias,
+                           const float* residual, int64_t ldr, float* c, int64_t ldc, int64_t M,
+                           int64_t N, int64_t K, pe_stream_t stream) {
+    return gemm_entry<true>(a_f16, lda, w_f16, bias, residual, ldr, c, ldc, M, N, K, stream);
 }

@@ -91,6 +91,8 @@ _SIGNATURES = {
     "pe_dequant_tiled_f16": (_I, [_I, _P, _P, _L, _L, _P]),
     "pe_gemm_f16": (_I, [_P, _L, _P, _P, _P, _L, _P, _L, _L, _L, _L, _P]),
     "pe_gemm_f16_silu": (_I, [_P, _L, _P, _P, _L, _L, _L, _L, _P]),
+    "pe_gemm_f16_silu_h": (_I, [_P, _L, _P, _P, _L, _L, _L, _L, _P]),
+    "pe_gemm_h16": (_I, [_P, _L, _P, _P, _P, _L, _P, _L, _L, _L, _L, _P]),
     "pe_flash_prefill": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _L, _F, _P, _L, _P]),
     "pe_embed_gather": (_I, [_I, _P, _L, _L, _P, _L, _P, _I, _P]),
     "pe_qgemv": (_I, [_I, _P, _L, _L, _P, _P, _P, _P, _I, _P]),

@@ -148,13 +148,15 @@ def dequantize_weight_f16(w: QWeight, out: torch.Tensor | None = None) -> torch.
 def gemm_f16(a: torch.Tensor, w16: torch.Tensor, bias: torch.Tensor | None = None,
              residual: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """C = A W^T (+ bias) (+ residual) on the matrix cores: A fp32 (M, K) (rows may be strided;
-    rounded to fp16 as read), W fp16 (N, K), fp32 accumulation and result (M, N)."""
+    rounded to fp16 as read) or fp16 (pe_gemm_h16: the same product of the same fp16 values),
+    W fp16 (N, K), fp32 accumulation and result (M, N)."""
     dev = _on_gpu(a, w16, bias, residual)
     if a.dim() == 1:
         a = a.unsqueeze(0)
-    if a.dtype != torch.float32:
-        raise ValueError("a must be float32")
-    if a.stride(1) != 1 or a.stride(0) % 4 or a.data_ptr() % 16:
+    if a.dtype not in (torch.float32, torch.float16):
+        raise ValueError("a must be float32 or float16")
+    half = a.dtype == torch.float16
+    if a.stride(1) != 1 or a.stride(0) % (8 if half else 4) or a.data_ptr() % 16:
         a = a.contiguous()
     M, K = a.shape
     N = w16.shape[0]
@@ -169,9 +171,10 @@ def gemm_f16(a: torch.Tensor, w16: torch.Tensor, bias: torch.Tensor | None = Non
         if residual.stride(1) != 1:
             residual = residual.contiguous()
         ldr = residual.stride(0)
-    check(lib.pe_gemm_f16(_ptr(a), a.stride(0), _ptr(w16), _ptr(None if bias is None else _f32c(bias)),
-                          _ptr(residual), ldr, _ptr(out), out.stride(0), M, N, K, _stream(dev)),
-          "pe_gemm_f16")
+    fn = lib.pe_gemm_h16 if half else lib.pe_gemm_f16
+    check(fn(_ptr(a), a.stride(0), _ptr(w16), _ptr(None if bias is None else _f32c(bias)),
+             _ptr(residual), ldr, _ptr(out), out.stride(0), M, N, K, _stream(dev)),
+          "pe_gemm_h16" if half else "pe_gemm_f16")
     return out
 
 
@@ -187,9 +190,11 @@ def interleave_gate_up_f16(gu16: torch.Tensor) -> torch.Tensor:
     return torch.stack([g, u], dim=1).reshape(n, k).contiguous()
 
 
-def gemm_f16_silu(a: torch.Tensor, w16_il: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+def gemm_f16_silu(a: torch.Tensor, w16_il: torch.Tensor, out: torch.Tensor | None = None,
+                  half: bool = False) -> torch.Tensor:
     """silu(A Wg^T) * (A Wu^T) on the matrix cores, W = interleave_gate_up_f16([gate; up]):
-    gemm_f16 then silu_mul without the (M, 2 ffn) intermediate (model.py:218-224)."""
+    gemm_f16 then silu_mul without the (M, 2 ffn) intermediate (model.py:218-224). half: the
+    result is stored in fp16 (pe_gemm_f16_silu_h), ready as gemm_f16's A operand."""
     dev = _on_gpu(a, w16_il)
     if a.dim() == 1:
         a = a.unsqueeze(0)
@@ -201,10 +206,14 @@ def gemm_f16_silu(a: torch.Tensor, w16_il: torch.Tensor, out: torch.Tensor | Non
     N = w16_il.shape[0]
     if w16_il.dtype != torch.float16 or not w16_il.is_contiguous() or w16_il.shape[1] != K or N % 32:
         raise ValueError("w16_il must be a contiguous (2*ffn, K) float16 tensor, ffn % 16 == 0")
+    odt = torch.float16 if half else torch.float32
     if out is None:
-        out = torch.empty(M, N // 2, device=dev, dtype=torch.float32)
-    check(lib.pe_gemm_f16_silu(_ptr(a), a.stride(0), _ptr(w16_il), _ptr(out), out.stride(0), M, N // 2, K,
-                               _stream(dev)), "pe_gemm_f16_silu")
+        out = torch.empty(M, N // 2, device=dev, dtype=odt)
+    if out.dtype != odt or out.stride(1) != 1 or tuple(out.shape) != (M, N // 2):
+        raise ValueError(f"out must be a row-major ({M}, {N // 2}) {odt} tensor")
+    fn = lib.pe_gemm_f16_silu_h if half else lib.pe_gemm_f16_silu
+    check(fn(_ptr(a), a.stride(0), _ptr(w16_il), _ptr(out), out.stride(0), M, N // 2, K, _stream(dev)),
+          "pe_gemm_f16_silu_h" if half else "pe_gemm_f16_silu")
     return out
 
 

@@ -327,7 +327,7 @@ class Transformer:
             x = K.gemm_f16(attn, W["o"], residual=x)
             h = K.rmsnorm(x, L.ffn_norm, cfg.eps)
             if W["gu_il"] is not None:
-                act = K.gemm_f16_silu(h, W["gu_il"])
+                act = K.gemm_f16_silu(h, W["gu_il"], half=True)  # fp16: the down GEMM's operand
             else:
                 act = K.silu_mul(K.gemm_f16(h, W["gu"]), cfg.ffn_dim)
             x = K.gemm_f16(act, W["down"], residual=x)

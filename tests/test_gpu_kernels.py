@@ -958,6 +958,42 @@ def test_gemm_f16_silu_equals_gemm_then_silu(K, M, ffn, Kd):
     assert torch.equal(got, ref)
 
 
+@pytest.mark.parametrize("M,N,Kd,bias,res,extra", GEMM16_CASES)
+def test_gemm_h16_equals_gemm_f16_on_fp16_values(K, M, N, Kd, bias, res, extra):
+    """pe_gemm_h16 (A stored in fp16) gives pe_gemm_f16's bits on the same values: A rounded to
+    fp16 before or as it is read is the same operand (row strides with padding included)."""
+    rng = np.random.default_rng(M + N + Kd + 1)
+    a = rng.standard_normal((M, Kd + extra)).astype(np.float16)
+    w16 = (rng.standard_normal((N, Kd)) * 0.05).astype(np.float16)
+    b = rng.standard_normal(N).astype(np.float32) if bias else None
+    r = rng.standard_normal((M, N)).astype(np.float32) if res else None
+    T = lambda v: None if v is None else torch.from_numpy(v).to(DEV)
+    A16 = T(a)[:, :Kd]  # fp16, row stride Kd + extra
+    ref = K.gemm_f16(A16.float(), T(w16), bias=T(b), residual=T(r))
+    got = K.gemm_f16(A16, T(w16), bias=T(b), residual=T(r))
+    assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("M,ffn,Kd", [(300, 4864, 896), (13, 512, 3584), (129, 48, 96), (1, 16, 32),
+                                      (4096, 2048, 64), (8192, 256, 64)])
+def test_gemm_f16_silu_half_output_and_down_product(K, M, ffn, Kd):
+    """The fp16-output SiLU GEMM stores the fp32 result rounded to nearest even, and the down
+    product on it equals the fp32 path's (whose A is rounded the same way as it is read)."""
+    rng = np.random.default_rng(M + ffn + 1)
+    a = torch.from_numpy(rng.standard_normal((M, Kd)).astype(np.float32)).to(DEV)
+    w16 = torch.from_numpy((rng.standard_normal((2 * ffn, Kd)) * 0.05).astype(np.float16)).to(DEV)
+    wil = K.interleave_gate_up_f16(w16)
+    act32 = K.gemm_f16_silu(a, wil)
+    act16 = K.gemm_f16_silu(a, wil, half=True)
+    assert act16.dtype == torch.float16 and act16.shape == (M, ffn)
+    assert torch.equal(act16, act32.half())
+    if ffn % 32:  # the down product's K must be a multiple of 32
+        return
+    wd = torch.from_numpy((rng.standard_normal((96, ffn)) * 0.05).astype(np.float16)).to(DEV)
+    res = torch.from_numpy(rng.standard_normal((M, 96)).astype(np.float32)).to(DEV)
+    assert torch.equal(K.gemm_f16(act16, wd, residual=res), K.gemm_f16(act32, wd, residual=res))
+
+
 @pytest.mark.parametrize("L,pos0", [(1, 0), (5, 0), (64, 0), (100, 7), (130, 0), (513, 0)])
 @pytest.mark.parametrize("n_head,n_kv", [(14, 2), (8, 8), (16, 4), (16, 1), (9, 3)])
 def test_flash_prefill_matches_closed_form(K, L, pos0, n_head, n_kv):
