@@ -241,94 +241,12 @@ int pe_decode_attn(const float* q, const float* k_cache, const float* v_cache, i
                    int64_t len_add, float scale, int round_fp16, float* out, void* workspace,
                    int64_t workspace_bytes, int layout, pe_stream_t stream);
 
-/* Whole attention block of one decode token in one launch (short caches):
- *   h = rmsnorm(x) * norm_w;  [q; k; v] = [Wq; Wk; Wv] h + [bq; bk; bv];  RoPE(q, k) at *pos;
- *   k, v -> cache row *pos;  a = decode attention of q over cache rows 0..*pos (GQA, scale,
- *   output rounded to fp16 when round_fp16);  x_out = x + Wo a.
- * Replaces, per layer, model.py:175-193 (rmsnorm, F.linear qkv, rope, index_copy_),
- * model.py:211 (decode_attn, kernels.py:129) and model.py:213 (torch.addmm o-projection).
- * Inside the launch, producer workgroups compute q, k, v and signal per-head counters in the
- * workspace; consumer workgroups wait for them (bounded waits), compute the attention of every
- * head and one slice of the o-projection rows. Vectors are in the natural layout.
- * Limits: head_dim 64; n_kv <= 8; n_head / n_kv <= 16; capacity <= 512 / n_kv;
- * hidden == n_head * head_dim, hidden % 64 == 0 and hidden <= 1024 (larger shapes use
- * pe_qkv_rmsnorm_rope + pe_decode_attn + pe_qgemv). PE_ERR_SHAPE otherwise.
- * An out-of-range *pos writes nothing to the cache and NaN to x_out.
- * workspace: pe_attn_block_workspace_bytes(...) bytes, 256-byte aligned, zero-filled once
- * before first use; calls that share it must run in order on one stream. The first 32-bit
- * word is an error flag: non-zero after an internal wait ran out (it cannot in a correct
- * launch; it bounds the damage of a fault elsewhere). Results of that call and of later ones
- * are then invalid until the workspace is zero-filled again.
- */
-typedef struct pe_attn_block_args {
-    int type_q, type_k, type_v, type_o;  /* ggml types of the tiled weights */
-    const void *w_q, *w_k, *w_v, *w_o;   /* (n_head*hd x hidden), (n_kv*hd x hidden) x2, (hidden x n_head*hd) */
-    const float *b_q, *b_k, *b_v;        /* biases or NULL */
-    const float* x;                      /* (hidden) residual stream */
-    const float* norm_w;                 /* (hidden) attn_norm weight */
-    float eps;
-    const float* cos_tab;                /* (rope_rows, hd/2) */
-    const float* sin_tab;
-    int64_t rope_rows;
-    const int64_t* pos;                  /* device scalar: position of this token */
-    float* k_cache;                      /* (n_kv, capacity, hd) */
-    float* v_cache;
-    int64_t capacity;
-    float* x_out;                        /* (hidden), must not alias x */
-    int64_t hidden;
-    int n_head, n_kv, head_dim;
-    float scale;
-    int round_fp16;
-} pe_attn_block_args;
-int64_t pe_attn_block_workspace_bytes(int64_t hidden, int n_head, int n_kv, int head_dim,
-                                      int64_t capacity);
-int pe_attn_block(const pe_attn_block_args* args, void* workspace, int64_t workspace_bytes,
-                  pe_stream_t stream);
-
-/* Attention block of one decode token with one workgroup per query head and no communication
- * between workgroups (short caches). For every query head h:
- *   hn = rmsnorm(x) * norm_w;  q_h = RoPE(Wq[h] hn + bq[h]);  k, v of kv head h / (n_head/n_kv)
- *   = RoPE(Wk hn + bk), Wv hn + bv (the first query head of each kv head writes them into cache
- *   row *pos);  a_h = softmax(q_h . K[0..*pos] * scale) V[0..*pos], rounded to fp16 when
- *   round_fp16;  partials[h][r] = sum_d Wo[r][h*hd + d] a_h[d] for r < hidden.
- * The o-projection output is x + sum_h partials[h] (pe_qgemv_sum_rmsnorm_silu adds it).
- * Replaces, per layer, model.py:175-213: rmsnorm + F.linear qkv + rope + index_copy_
- * (model.py:175-193), decode_attn (model.py:211, kernels.py:129) and the o-projection addmm
- * (model.py:213). Limits: head_dim 64, hidden % 32 == 0 and hidden <= 1024, capacity <= 1024;
- * format combinations: q,k,o Q5_0 with v Q5_0 or Q8_0, or all Q8_0
- * (pe_attn_head_supported tells, PE_ERR_TYPE / PE_ERR_SHAPE otherwise: then use
- * pe_qkv_rmsnorm_rope + pe_decode_attn + pe_qgemv). An out-of-range *pos writes nothing to
- * the cache and NaN partials. Vectors in the natural layout. */
-typedef struct pe_attn_head_args {
-    int type_q, type_k, type_v, type_o;  /* ggml types of the tiled weights */
-    const void *w_q, *w_k, *w_v, *w_o;   /* (n_head*hd x hidden), (n_kv*hd x hidden) x2, (hidden x n_head*hd) */
-    const float *b_q, *b_k, *b_v;        /* biases or NULL */
-    const float* x;                      /* (hidden) residual stream */
-    const float* norm_w;                 /* (hidden) attn_norm weight */
-    float eps;
-    const float* cos_tab;                /* (rope_rows, hd/2) */
-    const float* sin_tab;
-    int64_t rope_rows;
-    const int64_t* pos;                  /* device scalar: position of this token */
-    float* k_cache;                      /* (n_kv, capacity, hd) */
-    float* v_cache;
-    int64_t capacity;
-    float* partials;                     /* (n_head, hidden) per-head o-projection shares */
-    int64_t hidden;
-    int n_head, n_kv, head_dim;
-    float scale;
-    int round_fp16;
-} pe_attn_head_args;
-int pe_attn_head_supported(int type_q, int type_k, int type_v, int type_o, int64_t hidden,
-                           int n_head, int n_kv, int head_dim, int64_t capacity);
-int pe_attn_head(const pe_attn_head_args* args, pe_stream_t stream);
-
 /* pe_qgemv_rmsnorm_silu of x_sum = x + parts[0] + ... + parts[n_parts-1] (added in that order),
  * the parts stored back to back (part i at parts + i*k); block 0 also stores x_sum (if not
  * NULL) for the next residual. n_parts <= 16, k <= 8192. layout: PE_LAYOUT_X_UT when x, the
  * parts, norm_w and x_sum are unit-transposed, PE_LAYOUT_Y_UT for act. Up to 4 parts are
  * loaded with x, before the weights.
- * Replaces the residual add of the o-projection (model.py:213, after pe_attn_head or
+ * Replaces the residual add of the o-projection (model.py:213, after
  * pe_attn_gproj) fused with rmsnorm + gate/up + silu_mul (model.py:216-224). */
 int pe_qgemv_sum_rmsnorm_silu(int ggml_type, const void* w_tiled, int64_t ffn, int64_t k,
                               const float* x, const float* parts, int n_parts,
@@ -353,24 +271,6 @@ int pe_attn_gproj(const float* q, const float* k_cache, const float* v_cache, in
                   int head_dim, int64_t capacity, const void* len_dev, int len_dtype, int64_t len_add,
                   float scale, int round_fp16, int wo_type, const void* wo_tiled, int64_t hidden,
                   float* parts, int layout, pe_stream_t stream);
-
-/* Decode attention of every head fused with the o-projection (short caches), one launch:
- *   a = decode_attn(q, k_cache, v_cache, S) as pe_decode_attn (GQA, scale, output rounded to
- *       fp16 when round_fp16; S from len_dev/len_dtype/len_add as there);
- *   y[r] = residual[r] + sum_k Wo[r][k] a[k]  (residual may be NULL), r < hidden.
- * Every workgroup recomputes the attention of all heads on the matrix cores (fp32 MFMA) for
- * its rows of Wo, so no second launch or cross-workgroup exchange is needed.
- * Replaces decode_attn (model.py:211, kernels.py:129) + the o-projection addmm (model.py:213).
- * Limits: head_dim 64, n_kv 1 or 2, n_head / n_kv <= 16, n_head * 64 <= 1024, capacity <= 256
- * (pe_attn_oproj_supported tells; otherwise pe_decode_attn + pe_qgemv). Wo is a tiled
- * (hidden x n_head*64) weight of wo_type. layout: PE_LAYOUT_Y_UT for residual and y.
- * S == 0 gives NaN (as the reference). */
-int pe_attn_oproj_supported(int n_head, int n_kv, int head_dim, int64_t capacity, int wo_type,
-                            int64_t hidden);
-int pe_attn_oproj(const float* q, const float* k_cache, const float* v_cache, int n_head, int n_kv,
-                  int head_dim, int64_t capacity, const void* len_dev, int len_dtype,
-                  int64_t len_add, float scale, int round_fp16, int wo_type, const void* wo_tiled,
-                  int64_t hidden, const float* residual, float* y, int layout, pe_stream_t stream);
 
 /* ---- general / prefill (M >= 1) kernels ------------------------------------------------ */
 

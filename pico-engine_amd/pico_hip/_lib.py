@@ -49,38 +49,6 @@ class QkvArgs(ctypes.Structure):
     ]
 
 
-class AttnBlockArgs(ctypes.Structure):
-    """Mirror of pe_attn_block_args (include/pico_hip.h)."""
-
-    _fields_ = [
-        ("type_q", _I), ("type_k", _I), ("type_v", _I), ("type_o", _I),
-        ("w_q", _P), ("w_k", _P), ("w_v", _P), ("w_o", _P),
-        ("b_q", _P), ("b_k", _P), ("b_v", _P),
-        ("x", _P), ("norm_w", _P), ("eps", _F),
-        ("cos_tab", _P), ("sin_tab", _P), ("rope_rows", _L),
-        ("pos", _P), ("k_cache", _P), ("v_cache", _P), ("capacity", _L),
-        ("x_out", _P), ("hidden", _L),
-        ("n_head", _I), ("n_kv", _I), ("head_dim", _I),
-        ("scale", _F), ("round_fp16", _I),
-    ]
-
-
-class AttnHeadArgs(ctypes.Structure):
-    """Mirror of pe_attn_head_args (include/pico_hip.h)."""
-
-    _fields_ = [
-        ("type_q", _I), ("type_k", _I), ("type_v", _I), ("type_o", _I),
-        ("w_q", _P), ("w_k", _P), ("w_v", _P), ("w_o", _P),
-        ("b_q", _P), ("b_k", _P), ("b_v", _P),
-        ("x", _P), ("norm_w", _P), ("eps", _F),
-        ("cos_tab", _P), ("sin_tab", _P), ("rope_rows", _L),
-        ("pos", _P), ("k_cache", _P), ("v_cache", _P), ("capacity", _L),
-        ("partials", _P), ("hidden", _L),
-        ("n_head", _I), ("n_kv", _I), ("head_dim", _I),
-        ("scale", _F), ("round_fp16", _I),
-    ]
-
-
 _SIGNATURES = {
     "pe_strerror": (ctypes.c_char_p, [_I]),
     "pe_abi_version": (_I, []),
@@ -103,15 +71,9 @@ _SIGNATURES = {
     "pe_qkv_rmsnorm_rope": (_I, [ctypes.POINTER(QkvArgs), _P]),
     "pe_decode_attn_workspace_bytes": (_L, [_I, _I, _I, _L]),
     "pe_decode_attn": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _P, _P, _L, _I, _P]),
-    "pe_attn_block_workspace_bytes": (_L, [_L, _I, _I, _I, _L]),
-    "pe_attn_block": (_I, [ctypes.POINTER(AttnBlockArgs), _P, _L, _P]),
-    "pe_attn_head_supported": (_I, [_I, _I, _I, _I, _L, _I, _I, _I, _L]),
-    "pe_attn_head": (_I, [ctypes.POINTER(AttnHeadArgs), _P]),
     "pe_qgemv_sum_rmsnorm_silu": (_I, [_I, _P, _L, _L, _P, _P, _I, _P, _F, _P, _P, _I, _P]),
     "pe_attn_gproj_supported": (_I, [_I, _I, _I, _L, _I, _L]),
     "pe_attn_gproj": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _I, _P, _L, _P, _I, _P]),
-    "pe_attn_oproj_supported": (_I, [_I, _I, _I, _L, _I, _L]),
-    "pe_attn_oproj": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _I, _P, _L, _P, _P, _I, _P]),
     "pe_rmsnorm": (_I, [_P, _L, _P, _P, _L, _L, _L, _F, _P]),
     "pe_rope": (_I, [_P, _L, _P, _P, _P, _L, _L, _I, _I, _P]),
     "pe_silu_mul": (_I, [_P, _L, _P, _L, _L, _L, _P]),

@@ -184,7 +184,6 @@ class Engine:
                 graph.replay()
             done += n
             picks = self._greedy.log[:done + 1].tolist()
-            self.model.check_device_errors()
             if eos is not None and eos in picks:
                 return picks[:picks.index(eos)][:max_tokens]
             if done >= max_tokens:

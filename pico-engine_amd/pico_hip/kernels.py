@@ -21,8 +21,7 @@ from dataclasses import dataclass
 
 import torch
 
-from ._lib import (LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT, AttnBlockArgs, AttnHeadArgs, QkvArgs,
-                   check, lib)
+from ._lib import LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT, QkvArgs, check, lib
 from .dequant import (BLOCK_SIZE, GGML_Q4_K, GGML_Q5_0, GGML_Q6_K, GGML_Q8_0, QUANT_TYPES,
                       TYPE_NAMES, nbytes_for)
 
@@ -475,43 +474,6 @@ def qkv_rmsnorm_rope(x: torch.Tensor, norm_w: torch.Tensor | None, eps: float,
     return out
 
 
-def attn_oproj_supported(n_head: int, n_kv: int, hd: int, capacity: int, wo: QWeight) -> bool:
-    """Whether attn_oproj covers these shapes (else decode_attn + qgemv)."""
-    return lib.pe_attn_oproj_supported(n_head, n_kv, hd, capacity, wo.ggml_type, wo.n) == 0
-
-
-def attn_oproj(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, wo: QWeight,
-               residual: torch.Tensor | None = None, S: torch.Tensor | int | None = None,
-               S_offset: int = 0, scale: float | None = None, round_fp16: bool = True,
-               out: torch.Tensor | None = None, layout: int = LAYOUT_NATURAL) -> torch.Tensor:
-    """residual + Wo decode_attn(q, k, v, S) in one launch (same S conventions and fp16
-    output rounding as decode_attn; layout applies to residual and the result)."""
-    dev = _on_gpu(q, k, v, wo.data, residual)
-    n_head, hd = q.shape[-2], q.shape[-1]
-    n_kv, capacity = k.shape[0], k.shape[1]
-    q = _f32c(q.reshape(n_head, hd))
-    if not (k.is_contiguous() and v.is_contiguous()):
-        raise ValueError("KV caches must be contiguous (n_kv, capacity, hd) buffers")
-    if scale is None:
-        scale = 1.0 / float(hd) ** 0.5
-    len_dev, len_dtype, len_add = None, 0, int(S_offset)
-    if isinstance(S, torch.Tensor):
-        len_dev = S
-        len_dtype = {torch.int32: 1, torch.int64: 2}[S.dtype]
-    elif S is not None:
-        len_add += int(S)
-    else:
-        len_add += capacity
-    if out is None:
-        out = torch.empty(wo.n, device=dev, dtype=torch.float32)
-    res = None if residual is None else _f32c(residual.reshape(-1))
-    check(lib.pe_attn_oproj(_ptr(q), _ptr(k), _ptr(v), n_head, n_kv, hd, capacity, _ptr(len_dev),
-                            len_dtype, len_add, float(scale), int(round_fp16), wo.ggml_type,
-                            _ptr(wo.data), wo.n, _ptr(res), _ptr(out), layout, _stream(dev)),
-          "pe_attn_oproj")
-    return out
-
-
 def attn_gproj_supported(n_head: int, n_kv: int, hd: int, capacity: int, wo: QWeight) -> bool:
     """Whether attn_gproj covers these shapes (else decode_attn + qgemv)."""
     return lib.pe_attn_gproj_supported(n_head, n_kv, hd, capacity, wo.ggml_type, wo.n) == 0
@@ -547,101 +509,6 @@ def attn_gproj(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, wo: QWeight,
     check(lib.pe_attn_gproj(_ptr(q), _ptr(k), _ptr(v), n_head, n_kv, hd, capacity, _ptr(len_dev),
                             len_dtype, len_add, float(scale), int(round_fp16), wo.ggml_type,
                             _ptr(wo.data), wo.n, _ptr(out), layout, _stream(dev)), "pe_attn_gproj")
-    return out
-
-
-def attn_block_workspace(hidden: int, n_head: int, n_kv: int, hd: int, capacity: int,
-                         device) -> torch.Tensor | None:
-    """Zero-filled workspace of ``attn_block`` for these shapes, or None when the fused block
-    does not support them (then the model runs qkv_rmsnorm_rope + decode_attn + qgemv)."""
-    nbytes = lib.pe_attn_block_workspace_bytes(hidden, n_head, n_kv, hd, capacity)
-    if nbytes < 0:
-        return None
-    return torch.zeros(nbytes, dtype=torch.uint8, device=device)
-
-
-def attn_block_failed(workspace: torch.Tensor) -> bool:
-    """True when an internal wait of an attn_block launch on this workspace ran out (its first
-    word); results since then are invalid until the workspace is zero-filled again."""
-    return bool(workspace[:4].view(torch.int32).item() != 0)
-
-
-def attn_block(x: torch.Tensor, norm_w: torch.Tensor, eps: float,
-               wq: QWeight, wk: QWeight, wv: QWeight, wo: QWeight,
-               bq: torch.Tensor | None, bk: torch.Tensor | None, bv: torch.Tensor | None,
-               cos_tab: torch.Tensor, sin_tab: torch.Tensor, pos: torch.Tensor,
-               k_cache: torch.Tensor, v_cache: torch.Tensor, n_head: int, workspace: torch.Tensor,
-               scale: float | None = None, round_fp16: bool = True,
-               out: torch.Tensor | None = None) -> torch.Tensor:
-    """The attention block of one decode token in one launch: returns
-    x + Wo attn(RoPE(Wq h + bq), cache) with h = rmsnorm(x) * norm_w, after writing
-    RoPE(Wk h + bk) and Wv h + bv into the caches at ``pos`` (device int64 scalar).
-    Same result as qkv_rmsnorm_rope, decode_attn (fp16-rounded output) and qgemv with the
-    residual (model.py:175-213)."""
-    dev = _on_gpu(x, norm_w, wq.data, wk.data, wv.data, wo.data, pos, k_cache, v_cache, workspace)
-    n_kv, capacity, hd = k_cache.shape
-    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
-        raise ValueError("KV caches must be contiguous (n_kv, capacity, hd) buffers")
-    if pos.dtype != torch.int64:
-        raise ValueError("pos must be an int64 device tensor")
-    x = _f32c(x.reshape(-1))
-    nw = _f32c(norm_w.reshape(-1))
-    if out is None:
-        out = torch.empty_like(x)
-    if scale is None:
-        scale = 1.0 / float(hd) ** 0.5
-    a = AttnBlockArgs(wq.ggml_type, wk.ggml_type, wv.ggml_type, wo.ggml_type,
-                      wq.data.data_ptr(), wk.data.data_ptr(), wv.data.data_ptr(), wo.data.data_ptr(),
-                      None if bq is None else bq.data_ptr(), None if bk is None else bk.data_ptr(),
-                      None if bv is None else bv.data_ptr(),
-                      x.data_ptr(), nw.data_ptr(), float(eps),
-                      cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
-                      pos.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), capacity,
-                      out.data_ptr(), x.numel(), n_head, n_kv, hd, float(scale), int(round_fp16))
-    check(lib.pe_attn_block(ctypes.byref(a), _ptr(workspace), workspace.numel(), _stream(dev)),
-          "pe_attn_block")
-    return out
-
-
-def attn_head_supported(wq: QWeight, wk: QWeight, wv: QWeight, wo: QWeight, hidden: int,
-                        n_head: int, n_kv: int, hd: int, capacity: int) -> bool:
-    """Whether attn_head covers these formats and shapes (else use the three-launch block)."""
-    return lib.pe_attn_head_supported(wq.ggml_type, wk.ggml_type, wv.ggml_type, wo.ggml_type,
-                                      hidden, n_head, n_kv, hd, capacity) == 0
-
-
-def attn_head(x: torch.Tensor, norm_w: torch.Tensor, eps: float,
-              wq: QWeight, wk: QWeight, wv: QWeight, wo: QWeight,
-              bq: torch.Tensor | None, bk: torch.Tensor | None, bv: torch.Tensor | None,
-              cos_tab: torch.Tensor, sin_tab: torch.Tensor, pos: torch.Tensor,
-              k_cache: torch.Tensor, v_cache: torch.Tensor, n_head: int,
-              scale: float | None = None, round_fp16: bool = True,
-              out: torch.Tensor | None = None) -> torch.Tensor:
-    """The attention block of one decode token, one workgroup per query head: returns the
-    per-head o-projection shares P (n_head, hidden) with x + P.sum(0) = x + Wo attn, after
-    writing RoPE(Wk h + bk) and Wv h + bv into the caches at ``pos`` (device int64 scalar);
-    h = rmsnorm(x) * norm_w, attn = decode attention (fp16-rounded) of RoPE(Wq h + bq)."""
-    dev = _on_gpu(x, norm_w, wq.data, wk.data, wv.data, wo.data, pos, k_cache, v_cache)
-    n_kv, capacity, hd = k_cache.shape
-    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
-        raise ValueError("KV caches must be contiguous (n_kv, capacity, hd) buffers")
-    if pos.dtype != torch.int64:
-        raise ValueError("pos must be an int64 device tensor")
-    x = _f32c(x.reshape(-1))
-    nw = _f32c(norm_w.reshape(-1))
-    if out is None:
-        out = torch.empty(n_head, x.numel(), device=dev, dtype=torch.float32)
-    if scale is None:
-        scale = 1.0 / float(hd) ** 0.5
-    a = AttnHeadArgs(wq.ggml_type, wk.ggml_type, wv.ggml_type, wo.ggml_type,
-                     wq.data.data_ptr(), wk.data.data_ptr(), wv.data.data_ptr(), wo.data.data_ptr(),
-                     None if bq is None else bq.data_ptr(), None if bk is None else bk.data_ptr(),
-                     None if bv is None else bv.data_ptr(),
-                     x.data_ptr(), nw.data_ptr(), float(eps),
-                     cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
-                     pos.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), capacity,
-                     out.data_ptr(), x.numel(), n_head, n_kv, hd, float(scale), int(round_fp16))
-    check(lib.pe_attn_head(ctypes.byref(a), _stream(dev)), "pe_attn_head")
     return out
 
 
@@ -745,8 +612,7 @@ def flash_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
 __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "QWeight", "RawTensor", "dequantize", "pack_weight", "dequantize_weight", "embed_gather",
            "rmsnorm", "rope", "silu_mul", "decode_attn", "decode_attn_workspace", "qgemv",
            "q8_0_gemv", "q5_0_gemv", "q5_0_gemv_norm", "q6_k_gemv", "q4_k_gemv", "qgemv_norm",
-           "qgemv_norm_silu", "qkv_rmsnorm_rope", "attn_block", "attn_block_workspace",
-           "attn_block_failed", "attn_oproj", "attn_oproj_supported", "attn_head", "attn_head_supported", "qgemv_sum_norm_silu", "qgemm", "kv_write", "prefill_attn",
+           "qgemv_norm_silu", "qkv_rmsnorm_rope", "qgemv_sum_norm_silu", "qgemm", "kv_write", "prefill_attn",
            "attn_gproj", "attn_gproj_supported", "qgemv_norm_argmax", "dequantize_weight_f16",
            "gemm_f16", "gemm_f16_silu", "interleave_gate_up_f16", "flash_prefill",
            "BLOCK_SIZE"]

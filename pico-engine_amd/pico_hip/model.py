@@ -2,25 +2,28 @@
 
 ``ModelConfig`` and ``Transformer(cfg, weights, device, quant).forward(token_ids, positions,
 cache) -> logits`` keep the reference's signatures (model.py:27-57, :60-62, :128-165).
-Decode (one token) runs three fused HIP launches per layer plus two per token when the
-attention block fits one launch (short caches, the 0.5B family):
+Decode (one token) runs four launches per layer plus the embedding row and the LM head:
 
   embed_gather                              model.py:152 (Q8_0 row, bit-exact)
   per layer:
-    attn_block         (norm+QKV+bias+RoPE+cache write    model.py:175-213
-                        + GQA attention, fp16-rounded
-                        + o-projection + residual)
-    qgemv_norm_silu    (norm+gate/up+SiLU*up)             model.py:216-224
+    qkv_rmsnorm_rope   (norm+QKV+bias+RoPE+cache write)   model.py:175-193
+    attn_gproj         (GQA attention per kv group, fp16-  model.py:211-213
+                        rounded, times that group's
+                        columns of Wo: one part per group)
+    qgemv_sum_norm_silu (x + parts, norm, gate/up, SiLU*up) model.py:213-224
     qgemv + residual   (ffn_down)                         model.py:225-234
-  qgemv_norm           (final norm + LM head)             model.py:159-164
+  qgemv_norm(_argmax)  (final norm + LM head [+ greedy])  model.py:159-164
 
-Otherwise the attention block is three launches: qkv_rmsnorm_rope (model.py:175-193),
-decode_attn (split-KV GQA, model.py:211) and qgemv + residual (o-projection, model.py:213).
+Shapes attn_gproj does not cover (head_dim 128, long caches) run decode_attn (split-KV GQA,
+model.py:211) and the o-projection GEMV with the residual (model.py:213) instead, then the
+normed gate/up GEMV.
 
-Prefill (L > 1) follows the reference's L > 1 branch op for op in fp32 (its off-CUDA numerics):
-rmsnorm, one small-M GEMM per QKV segment with bias, RoPE, cache write at [0, L), causal
-attention, o-projection + residual, rmsnorm, gate/up GEMM, SiLU*up, down + residual; logits
-from the last row. Every op is a HIP kernel; nothing runs on the CPU.
+Prefill (L > 1) follows the reference's L > 1 branch op for op: in fp32 for short prompts (its
+off-CUDA numerics): rmsnorm, one small-M GEMM per QKV segment with bias, RoPE, cache write at
+[pos0, pos0 + L), causal attention, o-projection + residual, rmsnorm, gate/up GEMM, SiLU*up,
+down + residual; on the matrix cores (fp16 operands, fp32 accumulation) from
+``prefill_f16_min_tokens`` tokens on. Logits from the last row. Every op is a HIP kernel;
+nothing runs on the CPU.
 """
 
 from __future__ import annotations
@@ -87,17 +90,6 @@ class Transformer:
         self.layers = [self._layer_weights(i) for i in range(cfg.n_layers)]
         self.output_norm_ut = K.to_ut(self.w["output_norm.weight"])
         self._ws: dict[int, torch.Tensor] = {}
-        self._block_ws: torch.Tensor | None = None
-        # one-launch attention block for short caches (attn_block); off by default until it is
-        # faster than the three-launch block on the decode step
-        self.use_attn_block = False
-        # one workgroup per query head for the whole attention block (attn_head), when every
-        # layer's formats and the cache capacity are supported; off by default until it is
-        # faster than the three-launch block
-        self.use_attn_head = False
-        # attention + o-projection in one launch (attn_oproj) for short caches; off by default
-        # until it is faster than decode_attn + qgemv
-        self.use_attn_oproj = False
         # attention of each kv group fused with its share of the o-projection (attn_gproj),
         # the shares added by the gate/up GEMV: four launches per layer instead of five
         self.use_attn_gproj = True
@@ -142,27 +134,6 @@ class Transformer:
             ws = K.decode_attn_workspace(c.n_head, c.n_kv_head, c.head_dim, capacity, self.device)
             self._ws[capacity] = ws
         return ws
-
-    def block_workspace(self, capacity: int) -> torch.Tensor | None:
-        """Workspace of the one-launch attention block (shared by every layer and call, since
-        launches run in order), or None when it does not support these shapes/capacity."""
-        if not self.use_attn_block:
-            return None
-        c = self.cfg
-        probe = K.lib.pe_attn_block_workspace_bytes(c.hidden, c.n_head, c.n_kv_head, c.head_dim,
-                                                    capacity)
-        if probe < 0:
-            return None
-        if self._block_ws is None:
-            self._block_ws = K.attn_block_workspace(c.hidden, c.n_head, c.n_kv_head, c.head_dim,
-                                                    capacity, self.device)
-        return self._block_ws
-
-    def check_device_errors(self) -> None:
-        """Raise if a bounded device-side wait ran out since the workspace was made."""
-        if self._block_ws is not None and K.attn_block_failed(self._block_ws):
-            raise RuntimeError("pe_attn_block: an internal wait ran out; results are invalid "
-                               "(workspace must be zero-filled again)")
 
     @torch.inference_mode()
     def forward(self, token_ids: torch.Tensor, positions: torch.Tensor,
@@ -227,11 +198,6 @@ class Transformer:
         if pos.dtype != torch.int64:
             pos = pos.to(torch.int64)
         capacity = cache[0][0].shape[1]
-        if self.use_attn_head and self._head_ok(capacity):
-            return self._decode_heads(token_ids, pos, cache, greedy)
-        block_ws = self.block_workspace(capacity)
-        if block_ws is not None:
-            return self._decode_fused(token_ids, pos, cache, greedy, block_ws)
         ws = self.attn_workspace(capacity)
         x = K.embed_gather(self.embed, token_ids, layout=YU).reshape(-1)
         for i, L in enumerate(self.layers):
@@ -245,12 +211,8 @@ class Transformer:
                                                layout=XU | YU)
                 x = K.qgemv(act, L.w_down, residual=x, layout=XU | YU)
                 continue
-            if self.use_attn_oproj and K.attn_oproj_supported(cfg.n_head, cfg.n_kv_head,
-                                                              cfg.head_dim, capacity, L.wo):
-                x = K.attn_oproj(q, k_buf, v_buf, L.wo, residual=x, S=pos, S_offset=1, layout=YU)
-            else:
-                attn = K.decode_attn(q, k_buf, v_buf, S=pos, S_offset=1, workspace=ws, layout=YU)
-                x = K.qgemv(attn.reshape(-1), L.wo, residual=x, layout=XU | YU)
+            attn = K.decode_attn(q, k_buf, v_buf, S=pos, S_offset=1, workspace=ws, layout=YU)
+            x = K.qgemv(attn.reshape(-1), L.wo, residual=x, layout=XU | YU)
             if L.w_gate_up is not None:
                 act = K.qgemv_norm_silu(x, L.ffn_norm_ut, L.w_gate_up, cfg.eps, layout=XU | YU)
                 x = K.qgemv(act, L.w_down, residual=x, layout=XU | YU)
@@ -260,42 +222,6 @@ class Transformer:
                 act = K.silu_mul(torch.cat([g, u]).unsqueeze(0), cfg.ffn_dim).reshape(-1)
                 x = K.qgemv(act, L.w_down, residual=x, layout=YU)
         return self._lm_head(x, self.output_norm_ut, greedy, XU)
-
-    def _head_ok(self, capacity: int) -> bool:
-        c = self.cfg
-        return all(L.w_gate_up is not None and
-                   K.attn_head_supported(L.wq, L.wk, L.wv, L.wo, c.hidden, c.n_head, c.n_kv_head,
-                                         c.head_dim, capacity) for L in self.layers)
-
-    def _decode_heads(self, token_ids, pos, cache, greedy):
-        """One token, three launches per layer: attn_head (per-head o-projection shares),
-        the gate/up GEMV that adds them to the residual, and ffn_down with that residual."""
-        cfg = self.cfg
-        x = K.embed_gather(self.embed, token_ids).reshape(-1)
-        for i, L in enumerate(self.layers):
-            k_buf, v_buf = cache[i]
-            parts = K.attn_head(x, L.attn_norm, cfg.eps, L.wq, L.wk, L.wv, L.wo, L.bq, L.bk, L.bv,
-                                self.cos, self.sin, pos, k_buf, v_buf, cfg.n_head)
-            act, x_mid = K.qgemv_sum_norm_silu(x, parts, L.ffn_norm, L.w_gate_up, cfg.eps)
-            x = K.qgemv(act, L.w_down, residual=x_mid)
-        return self._lm_head(x, self.w["output_norm.weight"], greedy, K.LAYOUT_NATURAL)
-
-    def _decode_fused(self, token_ids, pos, cache, greedy, block_ws):
-        """One token with the one-launch attention block; vectors in the natural layout."""
-        cfg = self.cfg
-        x = K.embed_gather(self.embed, token_ids).reshape(-1)
-        for i, L in enumerate(self.layers):
-            k_buf, v_buf = cache[i]
-            x = K.attn_block(x, L.attn_norm, cfg.eps, L.wq, L.wk, L.wv, L.wo, L.bq, L.bk, L.bv,
-                             self.cos, self.sin, pos, k_buf, v_buf, cfg.n_head, block_ws)
-            if L.w_gate_up is not None:
-                act = K.qgemv_norm_silu(x, L.ffn_norm, L.w_gate_up, cfg.eps)
-            else:
-                g = K.qgemv_norm(x, L.ffn_norm, L.w_gate, cfg.eps)
-                u = K.qgemv_norm(x, L.ffn_norm, L.w_up, cfg.eps)
-                act = K.silu_mul(torch.cat([g, u]).unsqueeze(0), cfg.ffn_dim).reshape(-1)
-            x = K.qgemv(act, L.w_down, residual=x)
-        return self._lm_head(x, self.w["output_norm.weight"], greedy, K.LAYOUT_NATURAL)
 
     # ---- prefill --------------------------------------------------------------------------
     def _prefill_f16(self, token_ids, positions, cache, greedy=None):
@@ -340,6 +266,9 @@ class Transformer:
         qd, kd = nh * hd, nkv * hd
         cos = self.cos[positions]
         sin = self.sin[positions]
+        # the cache rows of this chunk start at its first position (the reference always
+        # prefills from 0, model.py:188-197: the same rows for a whole prompt)
+        pos0 = int(positions[0].item()) if positions.numel() else 0
         x = K.embed_gather(self.embed, token_ids)                       # (L, hidden)
         qkv = torch.empty(Lt, qd + 2 * kd, device=self.device, dtype=torch.float32)
         for i, L in enumerate(self.layers):
@@ -351,8 +280,8 @@ class Transformer:
             qk = qkv[:, :qd + kd].view(Lt, nh + nkv, hd)
             qk = K.rope(qk, cos, sin)                                     # (L, nh+nkv, hd)
             v = qkv[:, qd + kd:].view(Lt, nkv, hd)
-            K.kv_write(qk[:, nh:], v, k_buf, v_buf, pos0=0)
-            attn = K.prefill_attn(qk[:, :nh], k_buf, v_buf, pos0=0)     # (L, hidden)
+            K.kv_write(qk[:, nh:], v, k_buf, v_buf, pos0=pos0)
+            attn = K.prefill_attn(qk[:, :nh], k_buf, v_buf, pos0=pos0)  # (L, hidden)
             x = K.qgemm(attn, L.wo, residual=x)
             h = K.rmsnorm(x, L.ffn_norm, cfg.eps)
             if L.w_gate_up is not None:

@@ -557,200 +557,6 @@ def test_argmax_in_graph_replays(K):
     assert g.state.tolist() == [want[-1], 104, 4]
 
 
-# ---- one-launch attention block (qkv + attention + o-projection) -------------------------
-
-def _block_case(K, types, hidden, nh, nkv, cap, seed):
-    hd = 64
-    rng = np.random.default_rng(seed)
-    rows = (nh * hd, nkv * hd, nkv * hd)
-    raws = [quantized_normal(t, r, hidden, seed=seed + i) for i, (t, r) in enumerate(zip(types[:3], rows))]
-    raw_o = quantized_normal(types[3], hidden, nh * hd, seed=seed + 7)
-    ws = [qweight(K, t, raw, r, hidden) for t, raw, r in zip(types, raws, rows)]
-    wo = qweight(K, types[3], raw_o, hidden, nh * hd)
-    bs = [rng.standard_normal(r).astype(np.float32) * 0.1 for r in rows]
-    nw = (1.0 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
-    inv = 1.0 / (1e6 ** (np.arange(0, hd, 2) / hd))
-    ang = (np.arange(cap + 4)[:, None] * inv[None, :]).astype(np.float32)
-    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
-    kc, vc = _kv(rng, nkv, cap, hd)
-    dense = [dequant_rows(t, raw, r, hidden) for t, raw, r in zip(types, raws, rows)]
-    wo_d = dequant_rows(types[3], raw_o, hidden, nh * hd)
-    return dict(ws=ws, wo=wo, bs=bs, nw=nw, cos=cos, sin=sin, kc=kc, vc=vc, dense=dense, wo_d=wo_d,
-                rng=rng, hidden=hidden, nh=nh, nkv=nkv, hd=hd, cap=cap)
-
-
-def _block_ref(c, x, pos, kc, vc):
-    """float64 closed form of model.py:175-213 for one token; updates kc/vc (numpy) in place."""
-    hd, nh, nkv = c["hd"], c["nh"], c["nkv"]
-    h = closed.rmsnorm(x, c["nw"], 1e-6)
-    q, k, v = (closed.gemv(d, h, bias=b) for d, b in zip(c["dense"], c["bs"]))
-    q = closed.rope(q.reshape(nh, hd), c["cos"][pos], c["sin"][pos])
-    k = closed.rope(k.reshape(nkv, hd), c["cos"][pos], c["sin"][pos])
-    kc[:, pos] = k
-    vc[:, pos] = v.reshape(nkv, hd)
-    attn = closed.attention(q, kc, vc, pos + 1, round_fp16=True).reshape(-1)
-    return closed.gemv(c["wo_d"], attn, residual=x)
-
-
-BLOCK_CASES = [
-    ((dq.Q5_0, dq.Q5_0, dq.Q8_0, dq.Q5_0), 896, 14, 2, 77),     # config 0, even layer
-    ((dq.Q5_0, dq.Q5_0, dq.Q5_0, dq.Q5_0), 896, 14, 2, 256),    # config 0, odd layer, max cache
-    ((dq.Q8_0, dq.Q4_K, dq.Q6_K, dq.Q4_K), 512, 8, 4, 128),     # K-quants, 4 kv heads
-    ((dq.Q5_0, dq.Q8_0, dq.Q5_0, dq.Q8_0), 256, 4, 4, 64),      # no GQA sharing (group 1)
-]
-
-
-@pytest.mark.parametrize("types,hidden,nh,nkv,cap", BLOCK_CASES,
-                         ids=[f"{h}-{nh}x{nkv}-cap{cap}" for _, h, nh, nkv, cap in BLOCK_CASES])
-def test_attn_block_matches_closed_form_over_steps(K, types, hidden, nh, nkv, cap):
-    """Consecutive decode steps on one workspace (the per-consumer epochs advance every launch):
-    each step's output and cache row match the float64 closed form, and the three-launch path
-    (qkv_rmsnorm_rope + decode_attn + qgemv) agrees."""
-    c = _block_case(K, types, hidden, nh, nkv, cap, seed=hidden + cap)
-    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
-    ws = K.attn_block_workspace(hidden, nh, nkv, 64, cap, DEV)
-    assert ws is not None
-    kc_d, vc_d = T(c["kc"]), T(c["vc"])
-    kc_r, vc_r = c["kc"].astype(np.float64), c["vc"].astype(np.float64)
-    kc_3, vc_3 = T(c["kc"]), T(c["vc"])
-    bq, bk, bv = (T(b) for b in c["bs"])
-    for step, pos in enumerate([0, 1, cap // 2, cap - 2, cap - 1]):
-        x = c["rng"].standard_normal(hidden).astype(np.float32)
-        p = torch.tensor([pos], device=DEV)
-        y = K.attn_block(T(x), T(c["nw"]), 1e-6, *c["ws"], c["wo"], bq, bk, bv, T(c["cos"]),
-                         T(c["sin"]), p, kc_d, vc_d, nh, ws)
-        ref = _block_ref(c, x, pos, kc_r, vc_r)
-        assert rel_err(y.cpu().numpy(), ref) < TOL, f"step {step} pos {pos}"
-        assert rel_err(kc_d[:, pos].cpu().numpy(), kc_r[:, pos]) < TOL
-        assert rel_err(vc_d[:, pos].cpu().numpy(), vc_r[:, pos]) < TOL
-        q3 = K.qkv_rmsnorm_rope(T(x), T(c["nw"]), 1e-6, *c["ws"], bq, bk, bv, T(c["cos"]),
-                                T(c["sin"]), p, kc_3, vc_3, nh)
-        a3 = K.decode_attn(q3, kc_3, vc_3, S=p, S_offset=1)
-        y3 = K.qgemv(a3.reshape(-1), c["wo"], residual=T(x))
-        assert rel_err(y.cpu().numpy(), y3.cpu().numpy()) < TOL
-    torch.cuda.synchronize()
-    assert not K.attn_block_failed(ws)
-    # rows never written keep their values
-    untouched = [s for s in range(cap) if s not in (0, 1, cap // 2, cap - 2, cap - 1)]
-    np.testing.assert_array_equal(kc_d[:, untouched].cpu().numpy(), c["kc"][:, untouched])
-
-
-def test_attn_block_graph_replays_and_bad_position(K):
-    """Captured once, replayed with the position advanced on the device between replays: every
-    replay equals the eager launch bit for bit. An out-of-range position gives NaN and writes no
-    cache row, and the workspace stays usable."""
-    types, hidden, nh, nkv, cap = BLOCK_CASES[0]
-    c = _block_case(K, types, hidden, nh, nkv, cap, seed=5)
-    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
-    ws = K.attn_block_workspace(hidden, nh, nkv, 64, cap, DEV)
-    args = [T(c["nw"]), 1e-6, *c["ws"], c["wo"], *(T(b) for b in c["bs"]), T(c["cos"]), T(c["sin"])]
-    x = T(c["rng"].standard_normal(hidden).astype(np.float32))
-    kc_e, vc_e = T(c["kc"]), T(c["vc"])
-    kc_g, vc_g = T(c["kc"]), T(c["vc"])
-    pos_g = torch.tensor([3], device=DEV)
-    out_g = torch.empty(hidden, device=DEV)
-    K.attn_block(x, *args, pos_g, kc_g, vc_g, nh, ws, out=out_g)   # warm-up (eager)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.graph(g, stream=s):
-        K.attn_block(x, *args, pos_g, kc_g, vc_g, nh, ws, out=out_g)
-    torch.cuda.current_stream().wait_stream(s)
-    K.attn_block(x, *args, torch.tensor([3], device=DEV), kc_e, vc_e, nh, ws)
-    for pos in range(4, 12):
-        pos_g.fill_(pos)
-        g.replay()
-        ye = K.attn_block(x, *args, torch.tensor([pos], device=DEV), kc_e, vc_e, nh, ws)
-        torch.cuda.synchronize()
-        assert torch.equal(out_g, ye), f"replay at pos {pos}"
-    assert torch.equal(kc_g, kc_e) and torch.equal(vc_g, vc_e)
-    before_k, before_v = kc_e.clone(), vc_e.clone()
-    bad = K.attn_block(x, *args, torch.tensor([cap], device=DEV), kc_e, vc_e, nh, ws)
-    assert torch.isnan(bad).all()
-    assert torch.equal(kc_e, before_k) and torch.equal(vc_e, before_v)
-    good = K.attn_block(x, *args, torch.tensor([5], device=DEV), kc_e, vc_e, nh, ws)
-    torch.cuda.synchronize()
-    assert not K.attn_block_failed(ws) and torch.isfinite(good).all()
-
-
-def test_attn_block_shape_limits(K):
-    assert K.attn_block_workspace(896, 14, 2, 64, 256, DEV) is not None
-    assert K.attn_block_workspace(896, 14, 2, 64, 257, DEV) is None     # 512 / n_kv positions
-    assert K.attn_block_workspace(3584, 28, 4, 128, 128, DEV) is None   # head_dim 128
-    assert K.attn_block_workspace(2048, 32, 8, 64, 64, DEV) is None     # > 32 units per row
-
-
-# ---- per-head attention block (attn_head) + partial-sum gate/up ---------------------------
-
-HEAD_CASES = [
-    ((dq.Q5_0, dq.Q5_0, dq.Q8_0, dq.Q5_0), 896, 14, 2, 77),     # config 0, even layer
-    ((dq.Q5_0, dq.Q5_0, dq.Q5_0, dq.Q5_0), 896, 14, 2, 1024),   # odd layer, largest cache
-    ((dq.Q8_0, dq.Q8_0, dq.Q8_0, dq.Q8_0), 256, 4, 4, 40),      # no GQA sharing
-    ((dq.Q5_0, dq.Q5_0, dq.Q8_0, dq.Q5_0), 512, 8, 1, 300),     # MQA: all heads share one kv head
-]
-
-
-@pytest.mark.parametrize("types,hidden,nh,nkv,cap", HEAD_CASES,
-                         ids=[f"{h}-{nh}x{nkv}-cap{cap}" for _, h, nh, nkv, cap in HEAD_CASES])
-def test_attn_head_matches_closed_form_over_steps(K, types, hidden, nh, nkv, cap):
-    """x + sum_h partials[h] and the new cache rows match the float64 closed form of
-    model.py:175-213 step after step (first, second, middle and last cache rows)."""
-    c = _block_case(K, types, hidden, nh, nkv, cap, seed=hidden + cap + 1)
-    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
-    assert K.attn_head_supported(*c["ws"], c["wo"], hidden, nh, nkv, 64, cap)
-    kc_d, vc_d = T(c["kc"]), T(c["vc"])
-    kc_r, vc_r = c["kc"].astype(np.float64), c["vc"].astype(np.float64)
-    bq, bk, bv = (T(b) for b in c["bs"])
-    steps = [0, 1, cap // 2, cap - 2, cap - 1]
-    for step, pos in enumerate(steps):
-        x = c["rng"].standard_normal(hidden).astype(np.float32)
-        parts = K.attn_head(T(x), T(c["nw"]), 1e-6, *c["ws"], c["wo"], bq, bk, bv, T(c["cos"]),
-                            T(c["sin"]), torch.tensor([pos], device=DEV), kc_d, vc_d, nh)
-        assert parts.shape == (nh, hidden)
-        y = x.astype(np.float64) + parts.cpu().numpy().astype(np.float64).sum(0)
-        ref = _block_ref(c, x, pos, kc_r, vc_r)
-        assert rel_err(y, ref) < TOL, f"step {step} pos {pos}"
-        assert rel_err(kc_d[:, pos].cpu().numpy(), kc_r[:, pos]) < TOL
-        assert rel_err(vc_d[:, pos].cpu().numpy(), vc_r[:, pos]) < TOL
-    untouched = [s for s in range(cap) if s not in steps]
-    np.testing.assert_array_equal(kc_d[:, untouched].cpu().numpy(), c["kc"][:, untouched])
-    np.testing.assert_array_equal(vc_d[:, untouched].cpu().numpy(), c["vc"][:, untouched])
-
-
-def test_attn_head_graph_replay_bad_position_and_support(K):
-    types, hidden, nh, nkv, cap = HEAD_CASES[0]
-    c = _block_case(K, types, hidden, nh, nkv, cap, seed=11)
-    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
-    args = [T(c["nw"]), 1e-6, *c["ws"], c["wo"], *(T(b) for b in c["bs"]), T(c["cos"]), T(c["sin"])]
-    x = T(c["rng"].standard_normal(hidden).astype(np.float32))
-    kc_e, vc_e, kc_g, vc_g = T(c["kc"]), T(c["vc"]), T(c["kc"]), T(c["vc"])
-    pos_g = torch.tensor([5], device=DEV)
-    out_g = torch.empty(nh, hidden, device=DEV)
-    g = torch.cuda.CUDAGraph()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.graph(g, stream=s):
-        K.attn_head(x, *args, pos_g, kc_g, vc_g, nh, out=out_g)
-    torch.cuda.current_stream().wait_stream(s)
-    for pos in range(5, 12):
-        pos_g.fill_(pos)
-        g.replay()
-        ye = K.attn_head(x, *args, torch.tensor([pos], device=DEV), kc_e, vc_e, nh)
-        torch.cuda.synchronize()
-        assert torch.equal(out_g, ye), f"replay at pos {pos}"
-    assert torch.equal(kc_g, kc_e) and torch.equal(vc_g, vc_e)
-    before_k, before_v = kc_e.clone(), vc_e.clone()
-    bad = K.attn_head(x, *args, torch.tensor([cap], device=DEV), kc_e, vc_e, nh)
-    assert torch.isnan(bad).all()
-    assert torch.equal(kc_e, before_k) and torch.equal(vc_e, before_v)
-    # format / shape support
-    q4 = K.QWeight(c["ws"][0].data, dq.Q4_K, c["ws"][0].n, c["ws"][0].k)
-    assert not K.attn_head_supported(q4, *c["ws"][1:], c["wo"], hidden, nh, nkv, 64, cap)
-    assert not K.attn_head_supported(*c["ws"], c["wo"], hidden, nh, nkv, 64, 1025)
-    assert not K.attn_head_supported(*c["ws"], c["wo"], hidden, nh, nkv, 128, cap)
-
-
 @pytest.mark.parametrize("n", [14, 5, 4, 2, 1])
 def test_qgemv_sum_rmsnorm_silu(K, n):
     """silu(g) * u of rmsnorm(x + sum of parts); the stored sum equals the float32 sum taken
@@ -847,56 +653,6 @@ def test_attn_gproj_layout_empty_and_limits(K):
     assert not K.attn_gproj_supported(nh, nkv, hd, 129, wo)       # capacity past 128
     assert not K.attn_gproj_supported(28, 2, hd, cap, wo)         # 14 query heads per group
     assert not K.attn_gproj_supported(10, 5, hd, cap, wo)         # 5 kv heads
-
-
-# ---- attention + o-projection in one launch (attn_oproj) ---------------------------------
-
-OPROJ_CASES = [
-    (dq.Q5_0, 14, 2, 77, [1, 17, 61, 77]),     # config 0 shapes
-    (dq.Q5_0, 14, 2, 256, [255, 256]),         # largest cache
-    (dq.Q8_0, 8, 1, 64, [3, 40]),              # MQA: one kv head for all
-    (dq.Q4_K, 8, 2, 100, [33, 100]),           # K-quant o-projection (512 columns)
-]
-
-
-@pytest.mark.parametrize("t,nh,nkv,cap,Ss", OPROJ_CASES,
-                         ids=[f"t{t}-{nh}x{nkv}-cap{cap}" for t, nh, nkv, cap, _ in OPROJ_CASES])
-def test_attn_oproj_matches_closed_form(K, t, nh, nkv, cap, Ss):
-    hd, hidden = 64, 896
-    rng = np.random.default_rng(nh * cap + t)
-    q = rng.standard_normal((nh, hd)).astype(np.float32)
-    k, v = _kv(rng, nkv, cap, hd)
-    x = rng.standard_normal(hidden).astype(np.float32)
-    raw = quantized_normal(t, hidden, nh * hd, seed=cap + t)
-    wo = qweight(K, t, raw, hidden, nh * hd)
-    W = dequant_rows(t, raw, hidden, nh * hd)
-    T = lambda a: torch.from_numpy(a).to(DEV)
-    assert K.attn_oproj_supported(nh, nkv, hd, cap, wo)
-    for S in Ss:
-        y = K.attn_oproj(T(q), T(k), T(v), wo, residual=T(x), S=torch.tensor([S - 1], device=DEV),
-                         S_offset=1).cpu().numpy()
-        attn = closed.attention(q, k, v, S, round_fp16=True).reshape(-1)
-        assert rel_err(y, closed.gemv(W, attn, residual=x)) < TOL, f"S={S}"
-        # same as the two-launch path
-        a2 = K.decode_attn(T(q), T(k), T(v), S=S)
-        y2 = K.qgemv(a2.reshape(-1), wo, residual=T(x)).cpu().numpy()
-        assert rel_err(y, y2) < TOL
-
-
-def test_attn_oproj_layout_empty_and_limits(K):
-    hd, nh, nkv, cap, hidden = 64, 14, 2, 77, 896
-    rng = np.random.default_rng(5)
-    q = torch.from_numpy(rng.standard_normal((nh, hd)).astype(np.float32)).to(DEV)
-    k, v = (torch.from_numpy(a).to(DEV) for a in _kv(rng, nkv, cap, hd))
-    x = torch.from_numpy(rng.standard_normal(hidden).astype(np.float32)).to(DEV)
-    wo = qweight(K, dq.Q5_0, quantized_normal(dq.Q5_0, hidden, nh * hd, seed=5), hidden, nh * hd)
-    nat = K.attn_oproj(q, k, v, wo, residual=x, S=40)
-    ut = K.attn_oproj(q, k, v, wo, residual=K.to_ut(x), S=40, layout=K.LAYOUT_Y_UT)
-    assert torch.equal(K.from_ut(ut), nat)
-    assert torch.isnan(K.attn_oproj(q, k, v, wo, residual=x, S=0)).all()
-    assert not K.attn_oproj_supported(nh, nkv, 128, cap, wo)
-    assert not K.attn_oproj_supported(nh, nkv, hd, 257, wo)
-    assert not K.attn_oproj_supported(28, 4, hd, cap, wo)
 
 
 # ---- prompt-prefill GEMM on the matrix cores (fp16 operands, fp32 accumulate) --------------

@@ -94,10 +94,8 @@ def test_graph_equals_eager(tiny):
 
 
 PATHS = {  # model flags of each attention-block path of the decode step
-    "three_launch": dict(use_attn_block=False, use_attn_head=False, use_attn_gproj=False),
-    "attn_gproj": dict(use_attn_block=False, use_attn_head=False, use_attn_gproj=True),
-    "attn_block": dict(use_attn_block=True, use_attn_head=False, use_attn_gproj=False),
-    "attn_head": dict(use_attn_block=False, use_attn_head=True, use_attn_gproj=False),
+    "three_launch": dict(use_attn_gproj=False),
+    "attn_gproj": dict(use_attn_gproj=True),
 }
 
 
@@ -109,8 +107,8 @@ def _set_path(m, path):
 
 
 def test_fused_attention_block_equals_three_launch_path(tiny):
-    """The fused attention blocks (attn_block; attn_head and attn_gproj with the partial-sum
-    gate/up) and the three-launch block (qkv_rmsnorm_rope, decode_attn, qgemv) give the same
+    """The fused attention block (attn_gproj with the partial-sum gate/up) and the
+    three-launch block (qkv_rmsnorm_rope, decode_attn, qgemv) give the same
     decode logits to 1e-3 and the same greedy ids."""
     eng, _ = tiny
     m = eng.model
@@ -118,8 +116,6 @@ def test_fused_attention_block_equals_three_launch_path(tiny):
     outs = {}
     for path in PATHS:
         old = _set_path(m, path)
-        if path == "attn_block":
-            assert m.block_workspace(len(ids) + 10) is not None
         cache = eng._empty_cache(len(ids) + 10)
         lg = m.forward(torch.tensor(ids, device=eng.device), torch.arange(len(ids), device=eng.device), cache)
         seq = []
@@ -136,7 +132,6 @@ def test_fused_attention_block_equals_three_launch_path(tiny):
         for a, b in zip(outs[path], outs["three_launch"]):
             assert rel_err(a, b) < TOL, path
             assert int(np.argmax(a)) == int(np.argmax(b)), path
-    m.check_device_errors()
 
 
 @pytest.mark.parametrize("path", list(PATHS))
