@@ -9,8 +9,9 @@
  *     launching anything, so a bad call never reaches the GPU;
  *   - is asynchronous on the given stream and graph-capturable: it performs no
  *     allocation, copy or synchronisation; every buffer (workspaces included) is owned
- *     by the caller;
- *   - is thread-safe: the library keeps no mutable global state.
+ *     by the caller, except the scratch array of pe_decode_attn_noalloc (see there);
+ *   - is thread-safe: the library keeps no mutable global state (pe_decode_attn_noalloc
+ *     caches its scratch array's device address per GPU, set once).
  *
  * Quantized weights: the decode kernels read a "tiled" copy of a GGUF tensor made
  * on the device by pe_repack. Tiling is a pure byte permutation of the GGUF blocks
@@ -240,6 +241,22 @@ int pe_decode_attn(const float* q, const float* k_cache, const float* v_cache, i
                    int n_kv, int head_dim, int64_t capacity, const void* len_dev, int len_dtype,
                    int64_t len_add, float scale, int round_fp16, float* out, void* workspace,
                    int64_t workspace_bytes, int layout, pe_stream_t stream);
+
+/* pe_decode_attn without a workspace argument: the split records go to a scratch array of
+ * 4 MiB (4194304 bytes) compiled into the library, one per GPU, held until the process ends.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It allocates
+ * nothing and calls no allocating routine. Returns PE_ERR_SPACE when
+ * pe_decode_attn_workspace_bytes(n_head, n_kv, head_dim, capacity) exceeds 4 MiB (e.g. more
+ * than about 72,000 positions at 14/2 heads, head_dim 64). All calls on one GPU share its
+ * scratch array, which keeps the last call's records (nothing in it needs clearing: every
+ * record a call reads is written by that call first), so calls that overlap on one GPU race;
+ * calls issued in order on one stream do not. The stream must belong to the current device;
+ * the first call on a device looks the array's address up (not under graph capture). */
+int pe_decode_attn_noalloc(const float* q, const float* k_cache, const float* v_cache, int n_head,
+                           int n_kv, int head_dim, int64_t capacity, const void* len_dev,
+                           int len_dtype, int64_t len_add, float scale, int round_fp16, float* out,
+                           int layout, pe_stream_t stream);
 
 /* pe_qgemv_rmsnorm_silu of x_sum = x + parts[0] + ... + parts[n_parts-1] (added in that order),
  * the parts stored back to back (part i at parts + i*k); block 0 also stores x_sum (if not

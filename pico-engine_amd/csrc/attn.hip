@@ -15,6 +15,8 @@
 // query head).
 //
 // Prefill (L query tokens, causal), restating the fp32 SDPA call of model.py:201-209.
+#include <atomic>
+
 #include "pe_common.h"
 
 namespace pe {
@@ -467,24 +469,93 @@ extern "C" int64_t pe_decode_attn_workspace_bytes(int n_head, int n_kv, int head
     return 256 + (int64_t)n_kv * attn_nsplit(capacity) * G * (head_dim + 2) * 4;
 }
 
-extern "C" int pe_decode_attn(const float* q, const float* k_cache, const float* v_cache, int n_head,
-                              int n_kv, int head_dim, int64_t capacity, const void* len_dev,
-                              int len_dtype, int64_t len_add, float scale, int round_fp16,
-                              float* out, void* workspace, int64_t workspace_bytes, int layout,
-                              pe_stream_t stream) {
+// Host validation shared by pe_decode_attn and pe_decode_attn_noalloc (everything but the
+// workspace pointer and size).
+static int check_decode_attn(const float* q, const float* k_cache, const float* v_cache, int n_head,
+                             int n_kv, int head_dim, int64_t capacity, const void* len_dev,
+                             int len_dtype, float* out, int layout) {
     const int64_t need = pe_decode_attn_workspace_bytes(n_head, n_kv, head_dim, capacity);
     if (need < 0) return (int)-need;
     if (len_dtype < 0 || len_dtype > 2) return PE_ERR_TYPE;
     if (layout & ~PE_LAYOUT_Y_UT) return PE_ERR_TYPE;
     if ((layout & PE_LAYOUT_Y_UT) && ((int64_t)n_head * head_dim) % 32) return PE_ERR_SHAPE;
     if (attn_nsplit(capacity) > 65535) return PE_ERR_SHAPE;
-    if (!q || !k_cache || !v_cache || !out || !workspace || (len_dtype && !len_dev))
-        return PE_ERR_NULL;
-    if (workspace_bytes < need) return PE_ERR_SPACE;
+    if (!q || !k_cache || !v_cache || !out || (len_dtype && !len_dev)) return PE_ERR_NULL;
     if (!aligned(q, 4) || !aligned(k_cache, 16) || !aligned(v_cache, 4) || !aligned(out, 4) ||
-        !aligned(workspace, 16) || (len_dtype == 1 && !aligned(len_dev, 4)) ||
-        (len_dtype == 2 && !aligned(len_dev, 8)))
+        (len_dtype == 1 && !aligned(len_dev, 4)) || (len_dtype == 2 && !aligned(len_dev, 8)))
         return PE_ERR_ALIGN;
+    return PE_OK;
+}
+
+static int launch_decode_attn(const float* q, const float* k_cache, const float* v_cache,
+                              int n_head, int n_kv, int head_dim, int64_t capacity,
+                              const void* len_dev, int len_dtype, int64_t len_add, float scale,
+                              int round_fp16, float* out, void* workspace, int layout,
+                              pe_stream_t stream);
+
+extern "C" int pe_decode_attn(const float* q, const float* k_cache, const float* v_cache, int n_head,
+                              int n_kv, int head_dim, int64_t capacity, const void* len_dev,
+                              int len_dtype, int64_t len_add, float scale, int round_fp16,
+                              float* out, void* workspace, int64_t workspace_bytes, int layout,
+                              pe_stream_t stream) {
+    int st = check_decode_attn(q, k_cache, v_cache, n_head, n_kv, head_dim, capacity, len_dev,
+                               len_dtype, out, layout);
+    if (st) return st;
+    if (!workspace) return PE_ERR_NULL;
+    if (workspace_bytes < pe_decode_attn_workspace_bytes(n_head, n_kv, head_dim, capacity))
+        return PE_ERR_SPACE;
+    if (!aligned(workspace, 16)) return PE_ERR_ALIGN;
+    return launch_decode_attn(q, k_cache, v_cache, n_head, n_kv, head_dim, capacity, len_dev,
+                              len_dtype, len_add, scale, round_fp16, out, workspace, layout, stream);
+}
+
+// Scratch of pe_decode_attn_noalloc: the split records live in this file-scope device array
+// instead of a caller workspace. Each GPU holds its own copy (allocated with the code object,
+// kept until the process ends). Host code never passes `scratch` itself to a kernel (on the
+// host the name is only a stand-in); it uses the device address hipGetSymbolAddress returns,
+// looked up once per device on the first call with that device current.
+constexpr int64_t kAttnScratchBytes = 4LL << 20;
+static __device__ __align__(256) uint8_t scratch[kAttnScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+static std::atomic<void*> g_scratch_ptr[kMaxScratchDevices];
+
+static int scratch_ptr(void** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+        return PE_ERR_LAUNCH;
+    void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (!ptr) {
+        // the same address whichever thread looks it up first
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr)
+            return PE_ERR_LAUNCH;
+        g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+    *out = ptr;
+    return PE_OK;
+}
+
+extern "C" int pe_decode_attn_noalloc(const float* q, const float* k_cache, const float* v_cache,
+                                      int n_head, int n_kv, int head_dim, int64_t capacity,
+                                      const void* len_dev, int len_dtype, int64_t len_add,
+                                      float scale, int round_fp16, float* out, int layout,
+                                      pe_stream_t stream) {
+    int st = check_decode_attn(q, k_cache, v_cache, n_head, n_kv, head_dim, capacity, len_dev,
+                               len_dtype, out, layout);
+    if (st) return st;
+    if (pe_decode_attn_workspace_bytes(n_head, n_kv, head_dim, capacity) > kAttnScratchBytes)
+        return PE_ERR_SPACE;
+    void* ws = nullptr;
+    if ((st = scratch_ptr(&ws))) return st;
+    return launch_decode_attn(q, k_cache, v_cache, n_head, n_kv, head_dim, capacity, len_dev,
+                              len_dtype, len_add, scale, round_fp16, out, ws, layout, stream);
+}
+
+static int launch_decode_attn(const float* q, const float* k_cache, const float* v_cache,
+                              int n_head, int n_kv, int head_dim, int64_t capacity,
+                              const void* len_dev, int len_dtype, int64_t len_add, float scale,
+                              int round_fp16, float* out, void* workspace, int layout,
+                              pe_stream_t stream) {
     AttnParams p{q, k_cache, v_cache, n_kv, n_head / n_kv, capacity, len_dev, len_dtype, len_add,
                  scale, round_fp16, out, (unsigned*)workspace,
                  (float*)((char*)workspace + 256), (int)attn_nsplit(capacity),

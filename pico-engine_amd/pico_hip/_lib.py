@@ -71,6 +71,7 @@ _SIGNATURES = {
     "pe_qkv_rmsnorm_rope": (_I, [ctypes.POINTER(QkvArgs), _P]),
     "pe_decode_attn_workspace_bytes": (_L, [_I, _I, _I, _L]),
     "pe_decode_attn": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _P, _P, _L, _I, _P]),
+    "pe_decode_attn_noalloc": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _P, _I, _P]),
     "pe_qgemv_sum_rmsnorm_silu": (_I, [_I, _P, _L, _L, _P, _P, _I, _P, _F, _P, _P, _I, _P]),
     "pe_attn_gproj_supported": (_I, [_I, _I, _I, _L, _I, _L]),
     "pe_attn_gproj": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _I, _P, _L, _P, _I, _P]),
