@@ -197,17 +197,25 @@ class RefModel:
             self.qkv_b.append(torch.cat([self.w[p + "attn_q.bias"], self.w[p + "attn_k.bias"],
                                          self.w[p + "attn_v.bias"]]))
             self.gu_w.append(torch.cat([self.w[p + "ffn_gate.weight"], self.w[p + "ffn_up.weight"]], 0))
+        # The reference's quantized-kernel slots (engine.py:198-267): the LM head only when
+        # output.weight is Q8_0 (:216-223), gate/up only when every layer's pair is Q5_0
+        # (:225-242), ffn_down per layer when Q6_K or Q4_K (:244-266); every other matrix is
+        # multiplied as fp32 dequantized weights (model.py:163-164, :177, :213, :223, :235).
         self.q = {}
         if unpack_quant:
+            if all(self.types[f"blk.{i}.ffn_{h}.weight"] == dq.Q5_0
+                   for i in range(c.n_layers) for h in ("gate", "up")):
+                for i in range(c.n_layers):
+                    p = f"blk.{i}."
+                    g = self._unpack(p + "ffn_gate.weight")
+                    u = self._unpack(p + "ffn_up.weight")
+                    self.q[p + "gu"] = (g[0], torch.cat([g[1], u[1]]), torch.cat([g[2], u[2]]), None)
             for i in range(c.n_layers):
                 p = f"blk.{i}."
-                g = self._unpack(p + "ffn_gate.weight")
-                u = self._unpack(p + "ffn_up.weight")
-                if g[0] == u[0]:
-                    self.q[p + "gu"] = (g[0], torch.cat([g[1], u[1]]), torch.cat([g[2], u[2]]),
-                                        None if g[3] is None else torch.cat([g[3], u[3]]))
-                self.q[p + "down"] = self._unpack(p + "ffn_down.weight")
-            self.q["output"] = self._unpack("output.weight")
+                if self.types[p + "ffn_down.weight"] in (dq.Q6_K, dq.Q4_K):
+                    self.q[p + "down"] = self._unpack(p + "ffn_down.weight")
+            if self.types.get("output.weight") == dq.Q8_0:
+                self.q["output"] = self._unpack("output.weight")
 
     def _unpack(self, name):
         shape, gt, raw = self.raw[name]
@@ -229,7 +237,9 @@ class RefModel:
         h = rmsnorm_cpu(x, self.w["output_norm.weight"], c.eps)
         if "output" in self.q:
             return gemv_cpu(self.q["output"], h[-1])
-        return h[-1] @ self.w["output.weight"].T
+        # model.py:163-164; a file without output.weight ties the head to token_embd (the
+        # reference requires the tensor; this is the usual GGUF convention for tied models)
+        return h[-1] @ self.w.get("output.weight", self.w["token_embd.weight"]).T
 
     def _layer(self, i, x, positions, cos, sin, cache):
         c = self.cfg

@@ -253,7 +253,7 @@ extern "C" int pe_attn_gproj_supported(int n_head, int n_kv, int head_dim, int64
         n_head / n_kv > kGpMaxGroup || capacity <= 0 || capacity > kGpMaxCap || hidden <= 0 ||
         hidden % 32 || (hidden + kGpRows - 1) / kGpRows > 65535)
         return PE_ERR_SHAPE;
-    if (((int64_t)n_head * head_dim) % block_elems(wo_type)) return PE_ERR_SHAPE;
+    if (((int64_t)n_head * head_dim) % row_multiple(wo_type)) return PE_ERR_SHAPE;
     return PE_OK;
 }
 
@@ -282,6 +282,8 @@ extern "C" int pe_attn_gproj(const float* q, const float* k_cache, const float* 
         case PE_TYPE_Q5_0: hipLaunchKernelGGL(k_attn_gproj<PE_TYPE_Q5_0>, grid, dim3(kGpThreads), 0, s, p); break;
         case PE_TYPE_Q4_K: hipLaunchKernelGGL(k_attn_gproj<PE_TYPE_Q4_K>, grid, dim3(kGpThreads), 0, s, p); break;
         case PE_TYPE_Q6_K: hipLaunchKernelGGL(k_attn_gproj<PE_TYPE_Q6_K>, grid, dim3(kGpThreads), 0, s, p); break;
+        case PE_TYPE_F16: hipLaunchKernelGGL(k_attn_gproj<PE_TYPE_F16>, grid, dim3(kGpThreads), 0, s, p); break;
+        case PE_TYPE_F32: hipLaunchKernelGGL(k_attn_gproj<PE_TYPE_F32>, grid, dim3(kGpThreads), 0, s, p); break;
         default: return PE_ERR_TYPE;
     }
     return launch_status();

@@ -107,6 +107,13 @@ __global__ void k_repack(int type, const uint8_t* __restrict__ raw, uint8_t* __r
                 uint8_t* d = tiled + nblk * 208 + b * 2;
                 d[0] = s[208]; d[1] = s[209];
             } break;
+            case PE_TYPE_F16: {  // unquantized rows are used as stored: a plain copy
+                tiled[2 * b] = raw[2 * b];
+                tiled[2 * b + 1] = raw[2 * b + 1];
+            } break;
+            case PE_TYPE_F32: {
+                for (int i = 0; i < 4; ++i) tiled[4 * b + i] = raw[4 * b + i];
+            } break;
             default: break;
         }
     }
@@ -176,7 +183,7 @@ extern "C" int pe_dequant(int type, const void* blocks, float* out, int64_t n, p
 extern "C" int pe_repack(int type, const void* blocks, void* tiled, int64_t n_rows, int64_t k,
                          pe_stream_t stream) {
     if (!is_tiled_type(type)) return PE_ERR_TYPE;
-    if (n_rows <= 0 || k <= 0 || k % block_elems(type)) return PE_ERR_SHAPE;
+    if (n_rows <= 0 || k <= 0 || k % row_multiple(type)) return PE_ERR_SHAPE;
     if (!blocks || !tiled) return PE_ERR_NULL;
     if (!aligned(tiled, 16)) return PE_ERR_ALIGN;
     const int64_t nblk = n_rows * (k / block_elems(type));
@@ -188,7 +195,7 @@ extern "C" int pe_repack(int type, const void* blocks, void* tiled, int64_t n_ro
 extern "C" int pe_dequant_tiled(int type, const void* tiled, float* out, int64_t n_rows, int64_t k,
                                 pe_stream_t stream) {
     if (!is_tiled_type(type)) return PE_ERR_TYPE;
-    if (n_rows <= 0 || k <= 0 || k % block_elems(type)) return PE_ERR_SHAPE;
+    if (n_rows <= 0 || k <= 0 || k % row_multiple(type)) return PE_ERR_SHAPE;
     if (!tiled || !out) return PE_ERR_NULL;
     if (!aligned(tiled, 16) || !aligned(out, 4)) return PE_ERR_ALIGN;
     Tiled t{(const uint8_t*)tiled, n_rows, k / block_elems(type)};
@@ -199,6 +206,8 @@ extern "C" int pe_dequant_tiled(int type, const void* tiled, float* out, int64_t
         case PE_TYPE_Q5_0: hipLaunchKernelGGL(k_dequant_tiled<PE_TYPE_Q5_0>, dim3(grid), dim3(256), 0, s, t, k, out); break;
         case PE_TYPE_Q4_K: hipLaunchKernelGGL(k_dequant_tiled<PE_TYPE_Q4_K>, dim3(grid), dim3(256), 0, s, t, k, out); break;
         case PE_TYPE_Q6_K: hipLaunchKernelGGL(k_dequant_tiled<PE_TYPE_Q6_K>, dim3(grid), dim3(256), 0, s, t, k, out); break;
+        case PE_TYPE_F16: hipLaunchKernelGGL(k_dequant_tiled<PE_TYPE_F16>, dim3(grid), dim3(256), 0, s, t, k, out); break;
+        case PE_TYPE_F32: hipLaunchKernelGGL(k_dequant_tiled<PE_TYPE_F32>, dim3(grid), dim3(256), 0, s, t, k, out); break;
     }
     return launch_status();
 }
@@ -206,7 +215,7 @@ extern "C" int pe_dequant_tiled(int type, const void* tiled, float* out, int64_t
 extern "C" int pe_dequant_tiled_f16(int type, const void* tiled, void* out, int64_t n_rows, int64_t k,
                                     pe_stream_t stream) {
     if (!is_tiled_type(type)) return PE_ERR_TYPE;
-    if (n_rows <= 0 || k <= 0 || k % block_elems(type)) return PE_ERR_SHAPE;
+    if (n_rows <= 0 || k <= 0 || k % row_multiple(type)) return PE_ERR_SHAPE;
     if (!tiled || !out) return PE_ERR_NULL;
     if (!aligned(tiled, 16) || !aligned(out, 2)) return PE_ERR_ALIGN;
     Tiled t{(const uint8_t*)tiled, n_rows, k / block_elems(type)};
@@ -218,6 +227,8 @@ extern "C" int pe_dequant_tiled_f16(int type, const void* tiled, void* out, int6
         case PE_TYPE_Q5_0: hipLaunchKernelGGL((k_dequant_tiled<PE_TYPE_Q5_0, _Float16>), dim3(grid), dim3(256), 0, s, t, k, o); break;
         case PE_TYPE_Q4_K: hipLaunchKernelGGL((k_dequant_tiled<PE_TYPE_Q4_K, _Float16>), dim3(grid), dim3(256), 0, s, t, k, o); break;
         case PE_TYPE_Q6_K: hipLaunchKernelGGL((k_dequant_tiled<PE_TYPE_Q6_K, _Float16>), dim3(grid), dim3(256), 0, s, t, k, o); break;
+        case PE_TYPE_F16: hipLaunchKernelGGL((k_dequant_tiled<PE_TYPE_F16, _Float16>), dim3(grid), dim3(256), 0, s, t, k, o); break;
+        case PE_TYPE_F32: hipLaunchKernelGGL((k_dequant_tiled<PE_TYPE_F32, _Float16>), dim3(grid), dim3(256), 0, s, t, k, o); break;
     }
     return launch_status();
 }

@@ -9,13 +9,15 @@ static int dispatch_gemv(int type, const GemvArgs& a, bool norm, int mode, hipSt
         case PE_TYPE_Q5_0: return gemv_q5_0(a, norm, mode, s);
         case PE_TYPE_Q4_K: return gemv_q4_k(a, norm, mode, s);
         case PE_TYPE_Q6_K: return gemv_q6_k(a, norm, mode, s);
+        case PE_TYPE_F16: return gemv_f16(a, norm, mode, s);
+        case PE_TYPE_F32: return gemv_f32(a, norm, mode, s);
         default: return PE_ERR_TYPE;
     }
 }
 
 static int check_weight(int type, const void* w, int64_t n_rows, int64_t k) {
     if (!is_tiled_type(type)) return PE_ERR_TYPE;
-    if (n_rows <= 0 || k <= 0 || k % block_elems(type)) return PE_ERR_SHAPE;
+    if (n_rows <= 0 || k <= 0 || k % row_multiple(type)) return PE_ERR_SHAPE;
     Shape sh;
     if (!pick_shape(k / 32, sh)) return PE_ERR_SHAPE;
     if (!w) return PE_ERR_NULL;
@@ -115,6 +117,8 @@ extern "C" int pe_qgemm(int type, const void* w, int64_t n_rows, int64_t k, cons
         case PE_TYPE_Q5_0: return gemm_q5_0(a, s);
         case PE_TYPE_Q4_K: return gemm_q4_k(a, s);
         case PE_TYPE_Q6_K: return gemm_q6_k(a, s);
+        case PE_TYPE_F16: return gemm_f16w(a, s);
+        case PE_TYPE_F32: return gemm_f32w(a, s);
         default: return PE_ERR_TYPE;
     }
 }

@@ -1024,5 +1024,9 @@ int gemm_q8_0(const GemmArgs& a, hipStream_t s);
 int gemm_q5_0(const GemmArgs& a, hipStream_t s);
 int gemm_q4_k(const GemmArgs& a, hipStream_t s);
 int gemm_q6_k(const GemmArgs& a, hipStream_t s);
+int gemv_f16(const GemvArgs& a, bool norm, int mode, hipStream_t s);
+int gemv_f32(const GemvArgs& a, bool norm, int mode, hipStream_t s);
+int gemm_f16w(const GemmArgs& a, hipStream_t s);
+int gemm_f32w(const GemmArgs& a, hipStream_t s);
 
 }  // namespace pe

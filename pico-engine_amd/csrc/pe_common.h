@@ -378,6 +378,65 @@ struct Fmt<PE_TYPE_Q6_K> {
     }
 };
 
+// F16 / F32 matrices (unquantized GGUF tensors): the tiled form is the GGUF row-major form
+// itself (Tiled::nb = k elements per row). Unit u of a row = elements 32u..32u+31, read with
+// 16-byte loads (rows are whole units: k % 32 == 0). The reference multiplies these as fp32
+// (engine.py:80-98 dequantizes them exactly, model.py:163-164, :177, :213).
+template <>
+struct Fmt<PE_TYPE_F16> {
+    static constexpr int QK = 1, BYTES = 2;
+    struct Raw {
+        int4 v[4];
+    };
+    static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
+        const int4* p = reinterpret_cast<const int4*>(t.base + (row * t.nb + 32 * (int64_t)u) * 2);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.v[i] = p[i];
+    }
+    // exact conversions (denormals preserved), fp32 products
+    static PE_DEV float dot(const Raw& r, const float* x, const UnitSums&) {
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) {
+            const uint32_t h2 = word_of(r.v[w >> 2], w & 3);
+            acc = fmaf(h2f_fast(h2 & 0xFFFFu), x[2 * w], acc);
+            acc = fmaf(h2f_fast(h2 >> 16), x[2 * w + 1], acc);
+        }
+        return acc;
+    }
+    static PE_DEV void dequant(const Raw& r, float* w) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t h2 = word_of(r.v[i >> 2], i & 3);
+            w[2 * i] = h2f(h2 & 0xFFFFu);
+            w[2 * i + 1] = h2f(h2 >> 16);
+        }
+    }
+};
+
+template <>
+struct Fmt<PE_TYPE_F32> {
+    static constexpr int QK = 1, BYTES = 4;
+    struct Raw {
+        int4 v[8];
+    };
+    static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
+        const int4* p = reinterpret_cast<const int4*>(t.base + (row * t.nb + 32 * (int64_t)u) * 4);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r.v[i] = p[i];
+    }
+    static PE_DEV float dot(const Raw& r, const float* x, const UnitSums&) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) acc = fmaf(__uint_as_float(word_of(r.v[i >> 2], i & 3)), x[i], acc);
+        return acc;
+    }
+    static PE_DEV void dequant(const Raw& r, float* w) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) w[i] = __uint_as_float(word_of(r.v[i >> 2], i & 3));
+    }
+};
+
 // Unit-transposed ("ut") vector layout used between the decode kernels: element k of a vector
 // of U = K/32 units lives at ((k%32)/4 * U + k/32) * 4 + k%4, i.e. 8 planes of U float4s.
 // Lane u reading its unit's 8 float4s then touches consecutive 16-byte slots across lanes
@@ -433,9 +492,15 @@ __host__ __device__ inline int64_t block_bytes(int type) {
         default: return 0;
     }
 }
+// Weight formats of the tiled GEMV / GEMM / QKV kernels (F16 and F32 rows are used as stored).
 inline bool is_tiled_type(int type) {
     return type == PE_TYPE_Q5_0 || type == PE_TYPE_Q8_0 || type == PE_TYPE_Q4_K ||
-           type == PE_TYPE_Q6_K;
+           type == PE_TYPE_Q6_K || type == PE_TYPE_F16 || type == PE_TYPE_F32;
+}
+// What a tiled row length must be a multiple of: whole blocks, and whole 32-weight units.
+inline int64_t row_multiple(int type) {
+    const int64_t b = block_elems(type);
+    return b < 32 ? 32 : b;
 }
 inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 

@@ -114,6 +114,8 @@ PE_DEV void qkv_segment(const QkvParams& P, int type, int64_t task, int glane, f
         case PE_TYPE_Q5_0: qkv_task<PE_TYPE_Q5_0, GS, UPL, SEG>(P, task, glane, lds4, stage); break;
         case PE_TYPE_Q4_K: qkv_task<PE_TYPE_Q4_K, GS, UPL, SEG>(P, task, glane, lds4, stage); break;
         case PE_TYPE_Q6_K: qkv_task<PE_TYPE_Q6_K, GS, UPL, SEG>(P, task, glane, lds4, stage); break;
+        case PE_TYPE_F16: qkv_task<PE_TYPE_F16, GS, UPL, SEG>(P, task, glane, lds4, stage); break;
+        case PE_TYPE_F32: qkv_task<PE_TYPE_F32, GS, UPL, SEG>(P, task, glane, lds4, stage); break;
         default: break;
     }
 }
@@ -156,7 +158,7 @@ extern "C" int pe_qkv_rmsnorm_rope(const pe_qkv_args* args, pe_stream_t stream) 
     const void* ws[3] = {a.w_q, a.w_k, a.w_v};
     for (int i = 0; i < 3; ++i) {
         if (!is_tiled_type(types[i])) return PE_ERR_TYPE;
-        if (a.hidden <= 0 || a.hidden % block_elems(types[i])) return PE_ERR_SHAPE;
+        if (a.hidden <= 0 || a.hidden % row_multiple(types[i])) return PE_ERR_SHAPE;
         if (!ws[i]) return PE_ERR_NULL;
         if (!aligned(ws[i], 16)) return PE_ERR_ALIGN;
     }

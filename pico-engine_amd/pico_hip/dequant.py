@@ -28,8 +28,10 @@ TYPE_NAMES = {GGML_F32: "F32", GGML_F16: "F16", GGML_Q5_0: "Q5_0", GGML_Q8_0: "Q
 BLOCK_SIZE = {GGML_F32: (1, 4), GGML_F16: (1, 2), GGML_Q5_0: (32, 22), GGML_Q8_0: (32, 34),
               GGML_Q4_K: (256, 144), GGML_Q6_K: (256, 210), GGML_Q8_K: (256, 292)}
 
-# the formats the GEMV kernels read
+# the quantized formats the GEMV kernels read
 QUANT_TYPES = (GGML_Q5_0, GGML_Q8_0, GGML_Q4_K, GGML_Q6_K)
+# every matrix format the GEMV / GEMM / QKV kernels read (F16 and F32 rows as stored)
+MATRIX_TYPES = QUANT_TYPES + (GGML_F16, GGML_F32)
 
 
 def nbytes_for(ggml_type: int, n: int) -> int:

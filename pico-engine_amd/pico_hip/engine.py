@@ -8,9 +8,10 @@ metadata (:26-63), ``_empty_cache`` (:100-121, per layer fp32 (n_kv, capacity, h
 
 Loading differs on purpose: instead of dequantizing every tensor to fp32 on the host and
 unpacking the quantized ones to int8 + fp32 scales (engine.py:80-98, :198-267), the GGUF bytes
-go to the device as they are; matrices are tiled there by ``pe_repack`` (a byte permutation,
-same size), F32 norms/biases are used as they are, and the token embedding stays raw for the
-row gather. The fused [gate; up] weight is the two tensors' blocks back to back.
+go to the device as they are; matrices (quantized, F16 or F32) are tiled there by
+``pe_repack`` (a byte permutation, same size; F16/F32 rows stay as stored), F32 norms/biases
+are used as they are, and the token embedding stays raw for the row gather. The fused
+[gate; up] weight is the two tensors' blocks back to back (uploaded once, not as two tensors).
 """
 
 from __future__ import annotations
@@ -22,7 +23,7 @@ import numpy as np
 import torch
 
 from . import kernels as K
-from .dequant import GGML_F16, GGML_F32, QUANT_TYPES
+from .dequant import GGML_F16, GGML_F32, MATRIX_TYPES
 from .gguf import load as load_gguf, read_tensor_bytes
 from .model import ModelConfig, Transformer
 from .sampler import sample as sample_token
@@ -73,34 +74,43 @@ class Engine:
         return torch.from_numpy(np.array(raw, dtype=np.uint8, copy=True)).to(self.device)
 
     def _load_weights(self):
+        """Device tensors of the GGUF (engine.py:80-98): every 2-D matrix tiled for the kernels
+        (quantized, F16 or F32 alike), the token embedding kept raw for the row gather, and
+        1-D norms and biases as fp32. [gate; up] of a layer whose two halves share a format
+        and shape are uploaded once, as one tensor, instead of as two."""
         weights: dict[str, torch.Tensor] = {}
         quant: dict[str, object] = {}
         g = self.gguf
         by_name = {t.name: t for t in g.tensors}
+        fused = set()
+        for i in range(self.cfg.n_layers):
+            gt = by_name.get(f"blk.{i}.ffn_gate.weight")
+            ut = by_name.get(f"blk.{i}.ffn_up.weight")
+            if gt is not None and ut is not None and gt.ggml_type == ut.ggml_type \
+                    and gt.shape == ut.shape and gt.ggml_type in MATRIX_TYPES:
+                n, k = gt.shape[1], gt.shape[0]
+                both = np.concatenate([read_tensor_bytes(g, gt), read_tensor_bytes(g, ut)])
+                quant[f"blk.{i}.ffn_gate_up.weight"] = K.pack_weight(self._upload(both),
+                                                                     gt.ggml_type, 2 * n, k)
+                fused.update((gt.name, ut.name))
         for t in g.tensors:
+            if t.name in fused:
+                continue
             raw = read_tensor_bytes(g, t)
             shape = tuple(reversed(t.shape))     # logical (rows, cols), as engine.py:92-94
             if t.name == "token_embd.weight":
                 quant["token_embd"] = K.RawTensor(self._upload(raw), t.ggml_type, shape)
                 continue
-            if t.ggml_type in (GGML_F32, GGML_F16):
-                w = K.dequantize(t.ggml_type, self._upload(raw), t.n_elements).reshape(shape)
-                weights[t.name] = w
+            if len(shape) == 2 and t.ggml_type in MATRIX_TYPES:
+                quant[t.name] = K.pack_weight(self._upload(raw), t.ggml_type, shape[0], shape[1])
                 continue
-            if t.ggml_type not in QUANT_TYPES or len(shape) != 2:
-                raise NotImplementedError(f"{t.name}: ggml type {t.ggml_type} shape {shape}")
-            quant[t.name] = K.pack_weight(self._upload(raw), t.ggml_type, shape[0], shape[1])
-        # fused [gate; up] when both halves share a format (engine.py:224-242, all formats)
-        for i in range(self.cfg.n_layers):
-            gt, ut = by_name[f"blk.{i}.ffn_gate.weight"], by_name[f"blk.{i}.ffn_up.weight"]
-            if gt.ggml_type == ut.ggml_type and gt.shape == ut.shape:
-                both = np.concatenate([read_tensor_bytes(g, gt), read_tensor_bytes(g, ut)])
-                n, k = gt.shape[1], gt.shape[0]
-                quant[f"blk.{i}.ffn_gate_up.weight"] = K.pack_weight(self._upload(both),
-                                                                     gt.ggml_type, 2 * n, k)
-        if "output.weight" in quant:
+            if len(shape) == 1 and t.ggml_type in (GGML_F32, GGML_F16):
+                weights[t.name] = K.dequantize(t.ggml_type, self._upload(raw), t.n_elements)
+                continue
+            raise NotImplementedError(f"{t.name}: ggml type {t.ggml_type} shape {shape}")
+        if "output.weight" in by_name:
             quant["output"] = quant["output.weight"]
-        else:  # tied embeddings without an explicit output tensor
+        else:  # no output tensor: tied embeddings (the file's token_embd bytes as the LM head)
             e = quant["token_embd"]
             quant["output"] = K.pack_weight(e.data, e.ggml_type, e.shape[0], e.shape[1])
         torch.cuda.synchronize(self.device)
@@ -143,7 +153,7 @@ class Engine:
             return g
         except Exception as e:  # noqa: BLE001 -- any capture failure falls back to eager
             self._graph = None
-            warnings.warn(f"HIP graph capture failed; falling back to eager decode: {e}")
+            warnings.warn(f"decode step not captured ({e}); each token runs its launches eagerly")
             return None
 
     @torch.inference_mode()
@@ -198,6 +208,9 @@ class Engine:
         pick on the host (sampler.py)."""
         if not ids:
             return []
+        if len(ids) + max_tokens > self.cfg.context_len:
+            raise ValueError(f"{len(ids)} prompt + {max_tokens} new tokens exceed the model's "
+                             f"context length {self.cfg.context_len} (the RoPE table's rows)")
         eos = self.tok.eos_id if eos_id is None else eos_id
         cache = self._empty_cache(len(ids) + max_tokens)
         graph = self._build_decode_graph(cache) if use_graph else None

@@ -81,9 +81,9 @@ def load(path: str | Path) -> GGUF:
     with open(path, "rb") as f:
         magic, version, n_tensors, n_kv = struct.unpack("<IIQQ", f.read(24))
         if magic != GGUF_MAGIC:
-            raise ValueError(f"not a GGUF file (magic {magic:#x})")
+            raise ValueError(f"{path}: first four bytes {magic:#010x} are not the GGUF signature")
         if version not in (2, 3):
-            raise ValueError(f"unsupported GGUF version {version}")
+            raise ValueError(f"{path}: GGUF format version {version} is not 2 or 3")
         metadata: dict[str, object] = {}
         for _ in range(n_kv):
             key = _read_str(f)
@@ -105,9 +105,13 @@ def load(path: str | Path) -> GGUF:
 
 
 def read_tensor_bytes(g: GGUF, t: TensorInfo) -> np.ndarray:
-    """The tensor's raw bytes as a uint8 array (a read-only memory map of the file)."""
+    """The tensor's raw bytes as a uint8 array (a read-only memory map of the file). Raises
+    ValueError when the file ends before the tensor does (a truncated file or a bad offset)."""
     mm = np.memmap(g.path, dtype=np.uint8, mode="r")
     start = g.data_start + t.offset
+    if t.offset < 0 or start + t.n_bytes > mm.size:
+        raise ValueError(f"{g.path}: tensor {t.name} spans bytes [{start}, {start + t.n_bytes}) "
+                         f"but the file has {mm.size}")
     return mm[start:start + t.n_bytes]
 
 

@@ -22,8 +22,8 @@ from dataclasses import dataclass
 import torch
 
 from ._lib import LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT, QkvArgs, check, lib
-from .dequant import (BLOCK_SIZE, GGML_Q4_K, GGML_Q5_0, GGML_Q6_K, GGML_Q8_0, QUANT_TYPES,
-                      TYPE_NAMES, nbytes_for)
+from .dequant import (BLOCK_SIZE, GGML_Q4_K, GGML_Q5_0, GGML_Q6_K, GGML_Q8_0, MATRIX_TYPES,
+                      QUANT_TYPES, TYPE_NAMES, nbytes_for)
 
 _VP = ctypes.c_void_p
 
@@ -70,7 +70,8 @@ def from_ut(v: torch.Tensor) -> torch.Tensor:
 
 @dataclass
 class QWeight:
-    """A quantized (n x k) weight in the tiled plane layout (see include/pico_hip.h)."""
+    """An (n x k) weight matrix in the tiled layout (see include/pico_hip.h): a quantized
+    tensor's planes, or F16/F32 rows as stored."""
 
     data: torch.Tensor  # uint8 on the device, nbytes_for(ggml_type, n*k) bytes
     ggml_type: int
@@ -102,10 +103,15 @@ class RawTensor:
 
 def dequantize(ggml_type: int, blocks: torch.Tensor, n: int, out: torch.Tensor | None = None):
     """Bit-exact fp32 dequantization of raw GGUF blocks (reference dequant.py:243-260)."""
+    need = nbytes_for(ggml_type, n)
+    if blocks.numel() * blocks.element_size() < need:
+        raise ValueError(f"{blocks.numel() * blocks.element_size()} bytes hold fewer than {n} "
+                         f"{TYPE_NAMES.get(ggml_type, ggml_type)} elements ({need} bytes)")
     dev = _on_gpu(blocks)
-    nbytes_for(ggml_type, n)
     if out is None:
         out = torch.empty(n, device=dev, dtype=torch.float32)
+    if out.numel() < n:
+        raise ValueError(f"output holds {out.numel()} of {n} elements")
     check(lib.pe_dequant(ggml_type, _ptr(blocks), _ptr(out), n, _stream(dev)), "pe_dequant")
     return out
 
@@ -113,7 +119,7 @@ def dequantize(ggml_type: int, blocks: torch.Tensor, n: int, out: torch.Tensor |
 def pack_weight(blocks: torch.Tensor, ggml_type: int, n: int, k: int) -> QWeight:
     """Raw GGUF blocks of an (n x k) tensor (device uint8) -> tiled QWeight."""
     dev = _on_gpu(blocks)
-    if ggml_type not in QUANT_TYPES:
+    if ggml_type not in MATRIX_TYPES:
         raise ValueError(f"no GEMV kernel for {TYPE_NAMES.get(ggml_type, ggml_type)}")
     size = nbytes_for(ggml_type, n * k)
     if blocks.numel() != size:
@@ -220,9 +226,13 @@ def embed_gather(table: RawTensor, ids: torch.Tensor, out: torch.Tensor | None =
                  layout: int = LAYOUT_NATURAL):
     """Rows ``ids`` of a raw GGUF (vocab, hidden) table, dequantized (model.py:152);
     ``layout=LAYOUT_Y_UT`` writes each row unit-transposed."""
+    vocab, hidden = table.shape
+    need = nbytes_for(table.ggml_type, vocab * hidden)
+    if table.data.numel() * table.data.element_size() < need:
+        raise ValueError(f"embedding table holds {table.data.numel() * table.data.element_size()} "
+                         f"bytes, a {vocab}x{hidden} {TYPE_NAMES.get(table.ggml_type)} table needs {need}")
     dev = _on_gpu(table.data, ids)
     ids = ids.to(torch.int64).contiguous()
-    vocab, hidden = table.shape
     if out is None:
         out = torch.empty(ids.numel(), hidden, device=dev, dtype=torch.float32)
     check(lib.pe_embed_gather(table.ggml_type, _ptr(table.data), vocab, hidden, _ptr(ids),

@@ -64,8 +64,8 @@ class Layer:
     wo: QWeight
     ffn_norm: torch.Tensor
     w_gate_up: QWeight | None   # [gate; up] when both share a format, else None
-    w_gate: QWeight
-    w_up: QWeight
+    w_gate: QWeight | None      # the halves on their own (only when not fused)
+    w_up: QWeight | None
     w_down: QWeight
 
 
@@ -110,7 +110,7 @@ class Transformer:
             wo=q[p + "attn_output.weight"],
             ffn_norm=w[p + "ffn_norm.weight"],
             w_gate_up=q.get(p + "ffn_gate_up.weight"),
-            w_gate=q[p + "ffn_gate.weight"], w_up=q[p + "ffn_up.weight"],
+            w_gate=q.get(p + "ffn_gate.weight"), w_up=q.get(p + "ffn_up.weight"),
             w_down=q[p + "ffn_down.weight"],
         )
 

@@ -37,7 +37,7 @@ def test_gguf_rejects_bad_magic(tmp_path):
     from pico_hip import gguf
     p = tmp_path / "bad.gguf"
     p.write_bytes(b"GGUX" + bytes(20))
-    with pytest.raises(ValueError, match="not a GGUF"):
+    with pytest.raises(ValueError, match="GGUF signature"):
         gguf.load(p)
 
 
@@ -142,3 +142,45 @@ def test_synthetic_7b_mix_and_device_build(tmp_path):
     by = {t.name: t for t in g.tensors}
     assert bytes(gguf.read_tensor_bytes(g, by["output.weight"])) != \
         bytes(gguf.read_tensor_bytes(g, by["token_embd.weight"]))
+
+
+def test_truncated_gguf_raises_before_upload(tmp_path):
+    """A file that ends inside a tensor's data is rejected when the tensor's bytes are read
+    (the reference's f.read(n_bytes) + reshape raises too), never handed on short."""
+    from pico_hip import gguf
+    from pico_hip.quantize import quantize
+    w = np.random.default_rng(1).standard_normal(32 * 256).astype(np.float32)
+    p = tmp_path / "t.gguf"
+    gguf.write(p, {"general.architecture": "qwen2"},
+               [("a.weight", (256, 32), dq.Q8_0, quantize(dq.Q8_0, w))])
+    data = p.read_bytes()
+    cut = tmp_path / "cut.gguf"
+    cut.write_bytes(data[:-100])
+    g = gguf.load(cut)
+    with pytest.raises(ValueError, match="spans bytes"):
+        gguf.read_tensor_bytes(g, g.tensors[0])
+    assert len(gguf.read_tensor_bytes(gguf.load(p), g.tensors[0])) == g.tensors[0].n_bytes
+
+
+def test_short_buffers_rejected_before_any_launch():
+    """dequantize / embed_gather refuse a byte buffer smaller than the elements they would
+    read (checked on the host, before the device is touched)."""
+    from pico_hip import kernels as K
+    from pico_hip.dequant import GGML_Q8_0
+    with pytest.raises(ValueError, match="fewer than"):
+        K.dequantize(GGML_Q8_0, torch.zeros(33, dtype=torch.uint8), 32)
+    table = K.RawTensor(torch.zeros(34 * 9, dtype=torch.uint8), GGML_Q8_0, (10, 32))
+    with pytest.raises(ValueError, match="embedding table"):
+        K.embed_gather(table, torch.tensor([0]))
+
+
+def test_generate_rejects_more_tokens_than_the_context():
+    """Prompt + new tokens beyond context_len (the RoPE table's rows) raise before anything is
+    allocated or launched."""
+    from pico_hip.engine import Engine
+    from pico_hip.model import ModelConfig
+    eng = Engine.__new__(Engine)   # no device work: the check comes first
+    eng.cfg = ModelConfig(vocab_size=10, n_layers=1, hidden=32, n_head=1, n_kv_head=1,
+                          head_dim=32, ffn_dim=32, rope_base=1e4, eps=1e-6, context_len=16)
+    with pytest.raises(ValueError, match="context length"):
+        eng.generate_ids([1] * 10, max_tokens=7)
