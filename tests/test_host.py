@@ -184,3 +184,36 @@ def test_generate_rejects_more_tokens_than_the_context():
                           head_dim=32, ffn_dim=32, rope_base=1e4, eps=1e-6, context_len=16)
     with pytest.raises(ValueError, match="context length"):
         eng.generate_ids([1] * 10, max_tokens=7)
+
+
+def _golden_tok_sampler():
+    import json
+    from conftest import GOLDEN
+    return json.loads((GOLDEN / "tokenizer_sampler.json").read_text())
+
+
+def test_tokenizer_reference_toy_vocab_known_ids():
+    """The reference's toy vocabulary (its tests/test_tokenizer.py): encodings worked by hand,
+    round trips and vocabulary size."""
+    from pico_hip.tokenizer import BPETokenizer
+    fx = _golden_tok_sampler()["tokenizer"]
+    tok = BPETokenizer(fx["vocab"], fx["merges"], bos_id=fx["bos_id"], eos_id=fx["eos_id"])
+    assert tok.n_vocab == fx["n_vocab"]
+    for case in fx["cases"]:
+        assert tok.encode(case["text"]) == case["ids"], case["text"]
+        assert tok.decode(case["ids"]) == case["text"]
+
+
+def test_sampler_known_answers():
+    """top-k keeps ties with the k-th value, top-p keeps the token that crosses p (the shifted
+    mask), temperature applies first, greedy takes the first maximum: each case may only
+    return its allowed ids, and returns each of them over 400 seeded draws."""
+    from pico_hip.sampler import sample
+    for case in _golden_tok_sampler()["sampler"]:
+        logits = torch.tensor(case["logits"], dtype=torch.float32)
+        g = torch.Generator().manual_seed(0)
+        seen = {sample(logits.clone(), case["temperature"], case["top_k"], case["top_p"], generator=g)
+                for _ in range(400)}
+        assert seen <= set(case["allowed"]), case["what"]
+        if case["all_seen"]:
+            assert seen == set(case["allowed"]), case["what"]
