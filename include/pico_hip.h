@@ -289,6 +289,62 @@ int pe_attn_gproj(const float* q, const float* k_cache, const float* v_cache, in
                   float scale, int round_fp16, int wo_type, const void* wo_tiled, int64_t hidden,
                   float* parts, int layout, pe_stream_t stream);
 
+/* ---- the whole decode step in one launch ---------------------------------------------- */
+
+/* One layer of the model for pe_decode_step: the tiled matrices and their ggml types (Q5_0,
+ * Q8_0, Q4_K, Q6_K), biases (may be NULL), the natural-layout RMSNorm weights and the layer's
+ * KV cache (n_kv, capacity, 64). w_gu is the fused [gate; up] tensor of 2 * ffn rows. */
+typedef struct pe_step_layer {
+    int type_q, type_k, type_v, type_o, type_gu, type_down;
+    const void *w_q, *w_k, *w_v, *w_o, *w_gu, *w_down;
+    const float *b_q, *b_k, *b_v;
+    const float *attn_norm, *ffn_norm;
+    float *k_cache, *v_cache;
+} pe_step_layer;
+
+typedef struct pe_step_args {
+    const pe_step_layer* layers;   /* host array of n_layers entries (validated) */
+    const void* layers_dev;        /* device copy of the same array (read by the kernel) */
+    int n_layers, hidden, ffn, n_head, n_kv, head_dim;
+    int64_t capacity, vocab, rope_rows;
+    float eps, scale;
+    int embed_type;                /* raw GGUF token_embd (vocab x hidden), any dequant type */
+    const void* embed;
+    int out_type;                  /* tiled LM head (vocab x hidden) */
+    const void* w_out;
+    const float* out_norm;         /* natural layout */
+    const float *cos_tab, *sin_tab; /* (rope_rows, 32) */
+    int64_t* state;                /* device decode state {token, pos, count} */
+    int64_t* log;                  /* picked tokens (may be NULL), log_cap entries */
+    int64_t log_cap;
+    float* logits;                 /* (vocab) or NULL */
+    void* workspace;               /* pe_decode_step_workspace_bytes, 256-byte aligned, zeroed once */
+    int64_t workspace_bytes;
+    int n_wg;                      /* workgroups = the device's CU count (64..1024) */
+} pe_step_args;
+
+/* The decode step of one token as ONE launch (one workgroup per CU, every workgroup resident):
+ * the token and position come from state[0], state[1]; the step runs the embedding row, every
+ * layer (RMSNorm, QKV + bias, RoPE, cache write at the position, GQA attention with the output
+ * rounded to fp16, o-projection + residual, RMSNorm, gate/up, SiLU*up, down + residual), the
+ * final RMSNorm and the LM head, and makes the greedy pick on the device exactly as
+ * pe_qgemv_rmsnorm_argmax does (state[0] = token, state[1] += 1, log[state[2]++] = token).
+ * The stages hand their outputs to each other inside the launch through the workspace, as
+ * (value, launch tag) pairs; every wait is bounded. The workspace must be zero-filled before
+ * its first use and then only passed to this entry point, one call at a time (calls sharing a
+ * workspace must not overlap); its word 16 (uint32) reads 0 after a good launch, 1 if a wait
+ * ran out (the grid was not resident at once), 2 if the token or position was out of range
+ * (the caller clears it). pe_decode_step_supported gives PE_OK for the shapes it covers:
+ * head_dim 64, hidden <= 1024, ffn <= 5120, n_head / n_kv <= 8, n_kv * hidden <= 2048,
+ * capacity <= 128.
+ * Replaces Transformer.forward at L = 1 (model.py:128-237) and the greedy sample
+ * (sampler.py:26-27) with one launch per token instead of one per operation. */
+int pe_decode_step_supported(int n_layers, int hidden, int ffn, int n_head, int n_kv,
+                             int head_dim, int64_t capacity, int64_t vocab);
+int64_t pe_decode_step_workspace_bytes(int n_layers, int hidden, int ffn, int n_head, int n_kv,
+                                       int n_wg);
+int pe_decode_step(const pe_step_args* args, pe_stream_t stream);
+
 /* ---- general / prefill (M >= 1) kernels ------------------------------------------------ */
 
 /* y[r][:] = rmsnorm(x[r][:]) * w for r < rows (row strides in elements).

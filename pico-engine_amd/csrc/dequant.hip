@@ -9,57 +9,6 @@
 
 namespace pe {
 
-PE_DEV uint32_t rd8(const uint8_t* p) { return p[0]; }
-PE_DEV uint32_t rd16(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
-PE_DEV uint32_t rd32(const uint8_t* p) { return rd16(p) | (rd16(p + 2) << 16); }
-
-// Weight e of a raw GGUF tensor (byte loads only: blocks are 2-byte aligned at best).
-PE_DEV float raw_element(int type, const uint8_t* raw, int64_t e) {
-    switch (type) {
-        case PE_TYPE_F32: return __uint_as_float(rd32(raw + 4 * e));
-        case PE_TYPE_F16: return h2f(rd16(raw + 2 * e));
-        case PE_TYPE_Q8_0: {
-            const uint8_t* b = raw + (e >> 5) * 34;
-            return (float)(int8_t)b[2 + (e & 31)] * h2f(rd16(b));
-        }
-        case PE_TYPE_Q5_0: {
-            const uint8_t* b = raw + (e >> 5) * 22;
-            const int i = (int)(e & 31);
-            const uint32_t qs = b[6 + (i & 15)];
-            const uint32_t nib = i < 16 ? (qs & 0xFu) : (qs >> 4);
-            const uint32_t code = nib | (((rd32(b + 2) >> i) & 1u) << 4);
-            return (float)((int)code - 16) * h2f(rd16(b));
-        }
-        case PE_TYPE_Q4_K: {
-            const uint8_t* b = raw + (e >> 8) * 144;
-            const int r = (int)(e & 255), j = r >> 5;
-            const uint32_t byte = b[16 + 32 * (j >> 1) + (r & 31)];
-            const uint32_t nib = (j & 1) ? (byte >> 4) : (byte & 0xFu);
-            int sc, mn;
-            k4_scale_min(b + 4, j, sc, mn);
-            const float a = (float)sc * h2f(rd16(b));
-            const float m = (float)mn * h2f(rd16(b + 2));
-            return a * (float)nib - m;
-        }
-        case PE_TYPE_Q6_K: {
-            const uint8_t* b = raw + (e >> 8) * 210;
-            const int r = (int)(e & 255), h = r >> 7, quarter = (r & 127) >> 5, l = r & 31;
-            const uint32_t lb = b[64 * h + l + ((quarter & 1) ? 32 : 0)];
-            const uint32_t low4 = quarter < 2 ? (lb & 0xFu) : (lb >> 4);
-            const uint32_t high2 = (b[128 + 32 * h + l] >> (2 * quarter)) & 3u;
-            const int code = (int)(low4 | (high2 << 4)) - 32;
-            const int s = (int)(int8_t)b[192 + 8 * h + (l >> 4) + 2 * quarter];
-            const float ds = h2f(rd16(b + 208)) * (float)s;  // exact
-            return ds * (float)code;                          // one rounding
-        }
-        case PE_TYPE_Q8_K: {
-            const uint8_t* b = raw + (e >> 8) * 292;
-            return (float)(int8_t)b[4 + (e & 255)] * __uint_as_float(rd32(b));
-        }
-        default: return __uint_as_float(0x7FC00000u);
-    }
-}
-
 __global__ void k_dequant_raw(int type, const uint8_t* __restrict__ raw, float* __restrict__ out,
                               int64_t n) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;

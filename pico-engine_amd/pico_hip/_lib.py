@@ -49,6 +49,38 @@ class QkvArgs(ctypes.Structure):
     ]
 
 
+class StepLayer(ctypes.Structure):
+    """Mirror of pe_step_layer (include/pico_hip.h)."""
+
+    _fields_ = [
+        ("type_q", _I), ("type_k", _I), ("type_v", _I), ("type_o", _I), ("type_gu", _I),
+        ("type_down", _I),
+        ("w_q", _P), ("w_k", _P), ("w_v", _P), ("w_o", _P), ("w_gu", _P), ("w_down", _P),
+        ("b_q", _P), ("b_k", _P), ("b_v", _P),
+        ("attn_norm", _P), ("ffn_norm", _P),
+        ("k_cache", _P), ("v_cache", _P),
+    ]
+
+
+class StepArgs(ctypes.Structure):
+    """Mirror of pe_step_args (include/pico_hip.h)."""
+
+    _fields_ = [
+        ("layers", ctypes.POINTER(StepLayer)), ("layers_dev", _P),
+        ("n_layers", _I), ("hidden", _I), ("ffn", _I), ("n_head", _I), ("n_kv", _I),
+        ("head_dim", _I),
+        ("capacity", _L), ("vocab", _L), ("rope_rows", _L),
+        ("eps", _F), ("scale", _F),
+        ("embed_type", _I), ("embed", _P),
+        ("out_type", _I), ("w_out", _P), ("out_norm", _P),
+        ("cos_tab", _P), ("sin_tab", _P),
+        ("state", _P), ("log", _P), ("log_cap", _L),
+        ("logits", _P),
+        ("workspace", _P), ("workspace_bytes", _L),
+        ("n_wg", _I),
+    ]
+
+
 _SIGNATURES = {
     "pe_strerror": (ctypes.c_char_p, [_I]),
     "pe_abi_version": (_I, []),
@@ -81,6 +113,9 @@ _SIGNATURES = {
     "pe_qgemm": (_I, [_I, _P, _L, _L, _P, _L, _L, _P, _P, _L, _P, _L, _P]),
     "pe_kv_write": (_I, [_P, _P, _L, _I, _I, _L, _L, _P, _P, _L, _P]),
     "pe_prefill_attn": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _L, _F, _P, _L, _P]),
+    "pe_decode_step_supported": (_I, [_I, _I, _I, _I, _I, _I, _L, _L]),
+    "pe_decode_step_workspace_bytes": (_L, [_I, _I, _I, _I, _I, _I]),
+    "pe_decode_step": (_I, [ctypes.POINTER(StepArgs), _P]),
 }
 
 # Every symbol include/pico_hip.h declares (checked by tests/test_abi.py).

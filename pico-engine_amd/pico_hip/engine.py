@@ -194,6 +194,11 @@ class Engine:
                 graph.replay()
             done += n
             picks = self._greedy.log[:done + 1].tolist()
+            err = self.model.step_error()
+            if err:
+                raise RuntimeError(f"pe_decode_step failed (error word {err}): "
+                                   + ("a wait ran out: the launch's workgroups were not all "
+                                      "resident" if err == 1 else "token or position out of range"))
             if eos is not None and eos in picks:
                 return picks[:picks.index(eos)][:max_tokens]
             if done >= max_tokens:

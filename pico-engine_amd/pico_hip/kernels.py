@@ -21,7 +21,8 @@ from dataclasses import dataclass
 
 import torch
 
-from ._lib import LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT, QkvArgs, check, lib
+from ._lib import (LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT, QkvArgs, StepArgs, StepLayer, check,
+                   lib)
 from .dequant import (BLOCK_SIZE, GGML_Q4_K, GGML_Q5_0, GGML_Q6_K, GGML_Q8_0, MATRIX_TYPES,
                       QUANT_TYPES, TYPE_NAMES, nbytes_for)
 
@@ -434,6 +435,100 @@ def qgemv_norm_argmax(x: torch.Tensor, weight: torch.Tensor, w: QWeight, eps: fl
     return out
 
 
+class DecodeStep:
+    """The whole decode step of a model as one launch per token (pe_decode_step): the layer
+    table for one KV cache (host array + device copy) and the exchange workspace. Built once
+    per cache, outside any graph capture; ``run`` launches the step on the current stream
+    (capturable). Greedy only: the pick goes into a GreedyState as pe_qgemv_rmsnorm_argmax's
+    does."""
+
+    def __init__(self, model, cache, workspace: torch.Tensor):
+        c = model.cfg
+        dev = model.device
+        self.n_layers = c.n_layers
+        layers = (StepLayer * c.n_layers)()
+        keep = []
+        for i, L in enumerate(model.layers):
+            k_buf, v_buf = cache[i]
+            an = L.attn_norm.float().contiguous()
+            fn = L.ffn_norm.float().contiguous()
+            keep += [an, fn]
+            layers[i] = StepLayer(L.wq.ggml_type, L.wk.ggml_type, L.wv.ggml_type, L.wo.ggml_type,
+                                  L.w_gate_up.ggml_type, L.w_down.ggml_type,
+                                  _ptr(L.wq.data), _ptr(L.wk.data), _ptr(L.wv.data), _ptr(L.wo.data),
+                                  _ptr(L.w_gate_up.data), _ptr(L.w_down.data),
+                                  _ptr(L.bq), _ptr(L.bk), _ptr(L.bv), _ptr(an), _ptr(fn),
+                                  _ptr(k_buf), _ptr(v_buf))
+        self._layers = layers
+        raw = bytes(memoryview(layers).cast("B"))
+        self._layers_dev = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(dev)
+        self._keep = keep
+        self.workspace = workspace
+        self.out_norm = model.w["output_norm.weight"].float().contiguous()
+        self.capacity = cache[0][0].shape[1]
+        self.logits = torch.empty(model.output.n, device=dev, dtype=torch.float32)
+        self.model = model
+        self.n_wg = workspace_n_wg(dev)
+
+    def run(self, greedy: "GreedyState") -> torch.Tensor:
+        m, c = self.model, self.model.cfg
+        a = StepArgs()
+        a.layers = self._layers
+        a.layers_dev = _ptr(self._layers_dev)
+        a.n_layers, a.hidden, a.ffn = c.n_layers, c.hidden, c.ffn_dim
+        a.n_head, a.n_kv, a.head_dim = c.n_head, c.n_kv_head, c.head_dim
+        a.capacity, a.vocab, a.rope_rows = self.capacity, m.output.n, m.cos.shape[0]
+        a.eps, a.scale = float(c.eps), float(c.head_dim ** -0.5)
+        a.embed_type, a.embed = m.embed.ggml_type, _ptr(m.embed.data)
+        a.out_type, a.w_out, a.out_norm = m.output.ggml_type, _ptr(m.output.data), _ptr(self.out_norm)
+        a.cos_tab, a.sin_tab = _ptr(m.cos), _ptr(m.sin)
+        a.state, a.log, a.log_cap = _ptr(greedy.state), _ptr(greedy.log), greedy.log_cap
+        a.logits = _ptr(self.logits)
+        a.workspace, a.workspace_bytes = _ptr(self.workspace), self.workspace.numel()
+        a.n_wg = self.n_wg
+        check(lib.pe_decode_step(ctypes.byref(a), _stream(self.logits.device)), "pe_decode_step")
+        return self.logits
+
+    def error(self) -> int:
+        """The workspace error word: 0 after good launches, 1 if a wait ran out, 2 if a token or
+        position was out of range (cleared by this call)."""
+        w = int(self.workspace[64:68].view(torch.int32).item())
+        if w:
+            self.workspace[64:68].zero_()
+        return w
+
+
+def workspace_n_wg(device) -> int:
+    """Workgroups of a pe_decode_step launch: one per CU of the device."""
+    return int(torch.cuda.get_device_properties(device).multi_processor_count)
+
+
+def decode_step_workspace(model, device) -> torch.Tensor:
+    c = model.cfg
+    nbytes = lib.pe_decode_step_workspace_bytes(c.n_layers, c.hidden, c.ffn_dim, c.n_head,
+                                                c.n_kv_head, workspace_n_wg(device))
+    check(0 if nbytes >= 0 else -nbytes, "pe_decode_step_workspace_bytes")
+    return torch.zeros(nbytes, dtype=torch.uint8, device=device)
+
+
+def decode_step_supported(model, capacity: int) -> bool:
+    """Whether pe_decode_step covers this model and cache capacity (else the per-operation
+    launches run)."""
+    c = model.cfg
+    if lib.pe_decode_step_supported(c.n_layers, c.hidden, c.ffn_dim, c.n_head, c.n_kv_head,
+                                    c.head_dim, capacity, model.output.n) != 0:
+        return False
+    if model.output.ggml_type not in QUANT_TYPES:
+        return False
+    for L in model.layers:
+        if L.w_gate_up is None:
+            return False
+        for w in (L.wq, L.wk, L.wv, L.wo, L.w_gate_up, L.w_down):
+            if w.ggml_type not in QUANT_TYPES:
+                return False
+    return True
+
+
 def q5_0_gemv_norm(x: torch.Tensor, weight: torch.Tensor, w: QWeight, eps: float) -> torch.Tensor:
     """Fused RMSNorm(x, weight) + Q5_0 GEMV (kernels.py:253)."""
     return qgemv_norm(x, weight, _typed(w, GGML_Q5_0, "q5_0_gemv_norm"), eps)
@@ -624,5 +719,6 @@ __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "
            "q8_0_gemv", "q5_0_gemv", "q5_0_gemv_norm", "q6_k_gemv", "q4_k_gemv", "qgemv_norm",
            "qgemv_norm_silu", "qkv_rmsnorm_rope", "qgemv_sum_norm_silu", "qgemm", "kv_write", "prefill_attn",
            "attn_gproj", "attn_gproj_supported", "qgemv_norm_argmax", "dequantize_weight_f16",
+           "DecodeStep", "decode_step_supported", "decode_step_workspace",
            "gemm_f16", "gemm_f16_silu", "interleave_gate_up_f16", "flash_prefill",
            "BLOCK_SIZE"]

@@ -2,7 +2,9 @@
 
 ``ModelConfig`` and ``Transformer(cfg, weights, device, quant).forward(token_ids, positions,
 cache) -> logits`` keep the reference's signatures (model.py:27-57, :60-62, :128-165).
-Decode (one token) runs four launches per layer plus the embedding row and the LM head:
+A greedy decode step of a model the persistent kernel covers (head_dim 64, hidden <= 1024,
+caches up to 256 positions: the 0.5B family) is one launch, pe_decode_step. Otherwise decode
+(one token) runs four launches per layer plus the embedding row and the LM head:
 
   embed_gather                              model.py:152 (Q8_0 row, bit-exact)
   per layer:
@@ -98,6 +100,12 @@ class Transformer:
         # shorter ones by the fp32 path (the reference's off-CUDA numerics). None: never.
         self.prefill_f16_min_tokens: int | None = 512
         self._f16: list[dict[str, torch.Tensor]] | None = None
+        # greedy decode steps the persistent kernel covers can run as one launch per token
+        # (pe_decode_step) instead of four launches per layer; off by default while it measures
+        # slower than the per-operation launches
+        self.use_step_kernel = False
+        self._step_ws: torch.Tensor | None = None
+        self._steps: dict[tuple[int, int], K.DecodeStep] = {}
 
     def _layer_weights(self, i: int) -> Layer:
         p, q, w = f"blk.{i}.", self.quant, self.w
@@ -189,10 +197,47 @@ class Transformer:
         return K.qgemv_norm_argmax(x, norm_w, self.output, self.cfg.eps, greedy, layout=layout)
 
     # ---- decode ---------------------------------------------------------------------------
+    def decode_step_for(self, cache) -> K.DecodeStep | None:
+        """The one-launch decode step bound to ``cache`` (built on first use, outside any graph
+        capture), or None when pe_decode_step does not cover this model or capacity."""
+        capacity = cache[0][0].shape[1]
+        key = (cache[0][0].data_ptr(), capacity)
+        st = self._steps.get(key)
+        if st is None:
+            if not K.decode_step_supported(self, capacity):
+                return None
+            if self._step_ws is None:
+                self._step_ws = K.decode_step_workspace(self, self.device)
+            if len(self._steps) > 8:   # tables of caches no longer in use
+                self._steps.clear()
+            st = K.DecodeStep(self, cache, self._step_ws)
+            self._steps[key] = st
+        return st
+
+    def step_error(self) -> int:
+        """pe_decode_step's error word (0: none; 1: a wait ran out; 2: a token or position out
+        of range), cleared by the read."""
+        if self._step_ws is None:
+            return 0
+        w = int(self._step_ws[64:68].view(torch.int32).item())
+        if w:
+            self._step_ws[64:68].zero_()
+        return w
+
     def _decode(self, token_ids, positions, cache, greedy=None):
-        """One token. The hidden and FFN vectors stay in the unit-transposed layout between
+        """One token. With a greedy state and a model pe_decode_step covers, the whole step is
+        one launch that reads the token and position from the state. Otherwise four launches
+        per layer; the hidden and FFN vectors stay in the unit-transposed layout between
         kernels (each producer writes it, each GEMV reads it with coalesced loads)."""
         cfg = self.cfg
+        if greedy is not None and self.use_step_kernel:
+            st = self.decode_step_for(cache)
+            if st is not None:
+                if token_ids.data_ptr() != greedy.token.data_ptr():
+                    greedy.token.copy_(token_ids.reshape(-1)[:1].to(torch.int64))
+                if positions.data_ptr() != greedy.pos.data_ptr():
+                    greedy.pos.copy_(positions.reshape(-1)[:1].to(torch.int64))
+                return st.run(greedy)
         XU, YU = K.LAYOUT_X_UT, K.LAYOUT_Y_UT
         pos = positions.reshape(-1)[:1]
         if pos.dtype != torch.int64:

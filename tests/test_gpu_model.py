@@ -74,28 +74,39 @@ def test_device_greedy_equals_host_loop_and_stops_at_eos(tiny):
     assert eng.generate_ids(ids, 1, temperature=0.0, use_graph=True) == host[:1]
 
 
-def test_graph_equals_eager(tiny):
+@pytest.mark.parametrize("step_kernel", [False, True])
+def test_graph_equals_eager(tiny, step_kernel):
+    """The captured greedy step replays the eager greedy step bit for bit (both decode-step
+    paths: four launches per layer, or the one-launch step kernel)."""
     eng, _ = tiny
-    ids = [9, 8, 7, 6, 5]
-    cache = eng._empty_cache(len(ids) + 8)
-    graph = eng._build_decode_graph(cache)
-    assert graph is not None, "graph capture failed"
-    logits = eng.model.forward(torch.tensor(ids, device=eng.device), torch.arange(len(ids), device=eng.device), cache)
-    nxt = int(logits.argmax())
-    for step in range(8):
-        pos = len(ids) + step
-        # eager first, then the graph replays the same step over the same cache slot
-        eager = eng.model.forward(torch.tensor([nxt], device=eng.device), torch.tensor([pos], device=eng.device), cache).clone()
-        torch.cuda.synchronize()
-        g = eng._decode_step(nxt, pos, cache, graph).clone()
-        torch.cuda.synchronize()
-        assert torch.equal(eager, g), f"graph diverged from eager at step {step}"
-        nxt = int(eager.argmax())
+    eng.model.use_step_kernel = step_kernel
+    try:
+        ids = [9, 8, 7, 6, 5]
+        cache = eng._empty_cache(len(ids) + 8)
+        graph = eng._build_decode_graph(cache)
+        assert graph is not None, "graph capture failed"
+        greedy = eng._greedy
+        logits = eng.model.forward(torch.tensor(ids, device=eng.device), torch.arange(len(ids), device=eng.device), cache)
+        nxt = int(logits.argmax())
+        for step in range(8):
+            pos = len(ids) + step
+            # eager first, then the graph replays the same step over the same cache slot
+            eager = eng.model.forward(torch.tensor([nxt], device=eng.device),
+                                      torch.tensor([pos], device=eng.device), cache, greedy).clone()
+            torch.cuda.synchronize()
+            g = eng._decode_step(nxt, pos, cache, graph).clone()
+            torch.cuda.synchronize()
+            assert torch.equal(eager, g), f"graph diverged from eager at step {step}"
+            nxt = int(eager.argmax())
+        assert eng.model.step_error() == 0
+    finally:
+        eng.model.use_step_kernel = False
 
 
-PATHS = {  # model flags of each attention-block path of the decode step
-    "three_launch": dict(use_attn_gproj=False),
-    "attn_gproj": dict(use_attn_gproj=True),
+PATHS = {  # model flags of each path of the decode step
+    "three_launch": dict(use_attn_gproj=False, use_step_kernel=False),
+    "attn_gproj": dict(use_attn_gproj=True, use_step_kernel=False),
+    "step_kernel": dict(use_step_kernel=True),
 }
 
 
@@ -107,9 +118,11 @@ def _set_path(m, path):
 
 
 def test_fused_attention_block_equals_three_launch_path(tiny):
-    """The fused attention block (attn_gproj with the partial-sum gate/up) and the
-    three-launch block (qkv_rmsnorm_rope, decode_attn, qgemv) give the same
-    decode logits to 1e-3 and the same greedy ids."""
+    """Every path of the greedy decode step -- the fused attention block (attn_gproj with the
+    partial-sum gate/up), the three-launch block (qkv_rmsnorm_rope, decode_attn, qgemv) and
+    the one-launch step kernel -- gives the same decode logits to 1e-3 and the same greedy
+    ids."""
+    from pico_hip import kernels as K
     eng, _ = tiny
     m = eng.model
     ids = [5, 6, 7, 8, 9, 10]
@@ -117,17 +130,21 @@ def test_fused_attention_block_equals_three_launch_path(tiny):
     for path in PATHS:
         old = _set_path(m, path)
         cache = eng._empty_cache(len(ids) + 10)
+        greedy = K.GreedyState(m.output.n, len(ids) + 10, eng.device)
         lg = m.forward(torch.tensor(ids, device=eng.device), torch.arange(len(ids), device=eng.device), cache)
         seq = []
         tok = int(lg.argmax())
         for step in range(10):
             lg = m.forward(torch.tensor([tok], device=eng.device),
-                           torch.tensor([len(ids) + step], device=eng.device), cache)
+                           torch.tensor([len(ids) + step], device=eng.device), cache, greedy)
             seq.append(lg.cpu().numpy())
-            tok = int(lg.argmax())
+            nxt = int(lg.argmax())
+            assert int(greedy.state[0]) == nxt, (path, step)   # the device pick
+            tok = nxt
         outs[path] = seq
         for k, v in old.items():
             setattr(m, k, v)
+    assert m.step_error() == 0
     for path in PATHS:
         for a, b in zip(outs[path], outs["three_launch"]):
             assert rel_err(a, b) < TOL, path
