@@ -335,8 +335,8 @@ typedef struct pe_step_args {
  * workspace must not overlap); its word 16 (uint32) reads 0 after a good launch, 1 if a wait
  * ran out (the grid was not resident at once), 2 if the token or position was out of range
  * (the caller clears it). pe_decode_step_supported gives PE_OK for the shapes it covers:
- * head_dim 64, hidden <= 1024, ffn <= 5120, n_head / n_kv <= 8, n_kv * hidden <= 2048,
- * capacity <= 128.
+ * head_dim 64, hidden <= 1024, ffn <= 8192, n_head / n_kv <= 8, n_kv * hidden <= 2048,
+ * capacity <= 128, n_layers <= 64.
  * Replaces Transformer.forward at L = 1 (model.py:128-237) and the greedy sample
  * (sampler.py:26-27) with one launch per token instead of one per operation. */
 int pe_decode_step_supported(int n_layers, int hidden, int ffn, int n_head, int n_kv,

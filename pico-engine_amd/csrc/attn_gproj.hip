@@ -273,7 +273,7 @@ extern "C" int pe_attn_gproj(const float* q, const float* k_cache, const float* 
         return PE_ERR_ALIGN;
     const int64_t qd = (int64_t)n_head * head_dim;
     GpParams p{q, k_cache, v_cache, capacity, len_dev, len_dtype, len_add, scale, round_fp16,
-               n_head / n_kv, Tiled{(const uint8_t*)wo_tiled, hidden, qd / block_elems(wo_type)},
+               n_head / n_kv, make_tiled(wo_tiled, hidden, qd / block_elems(wo_type)),
                hidden, parts, layout};
     const dim3 grid((unsigned)((hidden + kGpRows - 1) / kGpRows), (unsigned)n_kv);
     hipStream_t s = (hipStream_t)stream;

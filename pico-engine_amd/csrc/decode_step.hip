@@ -21,6 +21,8 @@
 // and readiness arrive in one load, and nothing has to be reset between launches (the tag is
 // a launch counter kept in the workspace). Each workgroup issues the weight loads of a stage
 // before it waits for that stage's input, so the weights stream while the dependency resolves.
+// A workgroup has 1024 threads (four waves per SIMD), so every stage's short chains of
+// dependent instructions overlap across waves.
 //
 // Termination: every wait is bounded (kStepSpinMax polls). A workgroup whose wait runs out
 // sets the workspace error word and stops waiting for the rest of the launch (it still
@@ -33,15 +35,17 @@
 
 namespace pe {
 
-constexpr int kNT = 256;                 // threads per workgroup (4 waves)
+constexpr int kNT = 1024;                // threads per workgroup (16 waves, 4 per SIMD)
+constexpr int kWaves = kNT / 64;
 constexpr int kStepHd = 64;              // head_dim
-constexpr int kStepMaxCap = 128;         // cache positions (one per thread in the scores)
+constexpr int kStepMaxCap = 128;         // cache positions (two wave slices of 64)
 constexpr int kStepMaxHidden = 1024;     // hidden <= 32 units: one 32-lane group per row
-constexpr int kStepMaxFfn = 5120;        // ffn <= 160 units: one wave per down row, <= 3 per lane
-constexpr int kStepMaxGroup = 8;         // query heads per kv head (<= 16 units per Wo slice)
+constexpr int kStepMaxFfn = 8192;        // ffn <= 256 units: four waves per down row
+constexpr int kStepMaxGroup = 8;         // query heads per kv head (two waves per head)
 constexpr int kStepMaxKv = 8;
-constexpr int kStepMaxParts = 2048;     // n_kv * hidden: the o-projection parts one workgroup adds
+constexpr int kStepMaxParts = 2048;      // n_kv * hidden: the o-projection parts one workgroup adds
 constexpr uint32_t kStepSpinMax = 1u << 20;
+constexpr int kStepMaxLayers = 64;        // layer table copied into LDS at launch
 
 // LDS layout (floats). Vectors read per lane by unit are stored unit-padded (kUnitStride).
 // The K and V rows of stage A share their space with the polled inputs of stages F and D.
@@ -50,47 +54,18 @@ constexpr int kPadFfn = kStepMaxFfn / 32 * kUnitStride;
 constexpr int kKvFloats = 2 * kStepMaxCap * kStepHd;
 constexpr int kLdsX = 0;                                   // x of the layer (padded)
 constexpr int kLdsXs = kLdsX + kPadHidden;                 // x + parts (padded)
-constexpr int kLdsIn = kLdsXs + kPadHidden;                // polled stage input / K, V rows
+constexpr int kLdsH = kLdsXs + kPadHidden;                 // normed activation (padded)
+constexpr int kLdsIn = kLdsH + kPadHidden;                 // polled stage input / K, V rows
 constexpr int kLdsK = kLdsIn;                              // K rows [pos][64]
 constexpr int kLdsV = kLdsIn + kStepMaxCap * kStepHd;      // V rows [pos][64]
 constexpr int kLdsE = kLdsIn + (kPadFfn > kKvFloats ? kPadFfn : kKvFloats);  // exps [head][pos]
-constexpr int kLdsPv = kLdsE + kStepMaxGroup * kStepMaxCap;                 // P.V wave partials
-constexpr int kLdsAttn = kLdsPv + 4 * kStepMaxGroup * kStepHd;  // attention out (padded units)
+constexpr int kLdsPv = kLdsE + kStepMaxGroup * kStepMaxCap;  // P.V slice partials [2][512]
+constexpr int kLdsAttn = kLdsPv + 2 * kStepMaxGroup * kStepHd;  // attention out (padded units)
 constexpr int kLdsQ = kLdsAttn + kStepMaxGroup * 2 * kUnitStride;  // q of the group, new k, v
 constexpr int kLdsRed = kLdsQ + (kStepMaxGroup + 2) * kStepHd;  // reductions / small values
-constexpr int kLdsFloats = kLdsRed + 64;
+constexpr int kLdsFloats = kLdsRed + 128;
 constexpr size_t kStepLdsBytes = (size_t)kLdsFloats * 4;
 static_assert(kStepLdsBytes > 81920 && kStepLdsBytes <= 160 * 1024, "one workgroup per CU");
-
-// Opaque copies of the thread and workgroup indices: each stage derives its per-thread
-// addresses from them afresh instead of the compiler keeping every stage's addresses live
-// across the whole layer loop.
-PE_DEV int opaque_tid() {
-    int t = threadIdx.x;
-    asm volatile("" : "+v"(t));
-    return t;
-}
-PE_DEV int opaque_wg() {
-    int w = blockIdx.x;
-    asm volatile("" : "+s"(w));
-    return w;
-}
-
-// Copy n_rows contiguous 64-float rows from global memory into LDS with the gfx950 direct
-// global->LDS loads (16 bytes per lane, 1 KB per wave instruction, no registers); rows past
-// `last` re-read row `last` (in bounds). Completes with the issuing wave's vmcnt.
-PE_DEV void rows_to_lds(const float* src, int n_rows, int last, float* dst) {
-    const int tid = opaque_tid(), wv = tid >> 6, lane = tid & 63;
-    const int chunks = (n_rows + 3) >> 2;  // 4 rows (1 KB) per wave instruction
-    for (int ch = wv; ch < chunks; ch += kNT / 64) {
-        int row = 4 * ch + (lane >> 4);
-        row = row < last ? row : last;
-        const float* g = src + (int64_t)row * kStepHd + 4 * (lane & 15);
-        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                         (__attribute__((address_space(3))) void*)(dst + ch * 256),
-                                         16, 0, 0);
-    }
-}
 
 struct StepLayer {  // the device copy of a pe_step_layer
     int type_q, type_k, type_v, type_o, type_gu, type_down;
@@ -155,8 +130,36 @@ struct Ctx {
     bool failed;  // uniform: this workgroup stopped waiting
 };
 
+// Loads and stores through pointers read from the layer table, typed as global memory (else
+// the compiler emits flat accesses, which also count against the LDS wait counter).
+PE_DEV float gld(const float* p, int64_t i) { return ((const PE_GLOBAL float*)p)[i]; }
+PE_DEV void gst(float* p, int64_t i, float v) { ((PE_GLOBAL float*)p)[i] = v; }
+
+// Barrier for LDS only: waits for this wave's LDS accesses (lgkmcnt 0; vmcnt and expcnt left
+// at their maxima) and meets the other waves. __syncthreads also waits for every outstanding
+// global access, which after a publish means waiting for the device-coherent stores to be
+// acknowledged before the next stage may even issue its weight loads.
+PE_DEV void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+}
+
 // Padded LDS index of element k of a unit-read vector.
 PE_DEV int pad_idx(int k) { return (k >> 5) * kUnitStride + (k & 31); }
+
+// Opaque copies of the thread and workgroup indices: each stage derives its per-thread
+// addresses from them afresh instead of the compiler keeping every stage's addresses live
+// across the whole layer loop.
+PE_DEV int opaque_tid() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+PE_DEV int opaque_wg() {
+    int w = blockIdx.x;
+    asm volatile("" : "+s"(w));
+    return w;
+}
 
 // Wait until the n pairs addr(0) .. addr(n - 1) all carry this launch's tag and copy their
 // values into LDS (dst[pad_idx(i)] when PAD, else dst[i]). Thread t polls pairs t, t + kNT, ...;
@@ -164,21 +167,21 @@ PE_DEV int pad_idx(int k) { return (k >> 5) * kUnitStride + (k & 31); }
 template <int MAXJ, bool PAD, typename Addr>
 PE_DEV void poll_map(Addr addr, int n, Ctx& c, float* dst) {
     static_assert(MAXJ <= 32, "one pending bit per slot");
+    const int tid = opaque_tid();
     uint32_t pend = 0;
 #pragma unroll
     for (int j = 0; j < MAXJ; ++j)
-        if ((int)threadIdx.x + j * kNT < n) pend |= 1u << j;
+        if (tid + j * kNT < n) pend |= 1u << j;
     bool give_up = c.failed;
     uint32_t spins = 0;
     while (pend && !give_up) {
         uint64_t v[MAXJ];
 #pragma unroll
-        for (int j = 0; j < MAXJ; ++j)
-            v[j] = ((pend >> j) & 1u) ? ld_pair(addr((int)threadIdx.x + j * kNT)) : 0ull;
+        for (int j = 0; j < MAXJ; ++j) v[j] = ((pend >> j) & 1u) ? ld_pair(addr(tid + j * kNT)) : 0ull;
 #pragma unroll
         for (int j = 0; j < MAXJ; ++j) {
             if (((pend >> j) & 1u) && (uint32_t)(v[j] >> 32) == c.tag) {
-                const int i = (int)threadIdx.x + j * kNT;
+                const int i = tid + j * kNT;
                 dst[PAD ? pad_idx(i) : i] = __uint_as_float((uint32_t)v[j]);
                 pend &= ~(1u << j);
             }
@@ -187,7 +190,7 @@ PE_DEV void poll_map(Addr addr, int n, Ctx& c, float* dst) {
     }
     if (__syncthreads_or(give_up) && !c.failed) {
         c.failed = true;
-        if (threadIdx.x == 0) st_word(c.err, 1u);
+        if (tid == 0) st_word(c.err, 1u);
     }
 }
 
@@ -196,26 +199,33 @@ PE_DEV void poll_vec(const uint64_t* src, int n, Ctx& c, float* dst) {
     poll_map<MAXJ, PAD>([src](int i) { return src + i; }, n, c, dst);
 }
 
-// Block-wide sum in a fixed order (all threads call; result in every thread).
-PE_DEV float block_sum4(float v, float* red) {
+// Block-wide sum in a fixed order (all threads call; result in every thread); red >= 16 floats.
+PE_DEV float block_sum16(float v, float* red) {
     v = wave_sum<64>(v);
+    const int tid = threadIdx.x;
+    if ((tid & 63) == 0) red[tid >> 6] = v;
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    float s = red[0];
+#pragma unroll
+    for (int i = 1; i < kWaves; ++i) s += red[i];
     __syncthreads();
-    return ((red[0] + red[1]) + red[2]) + red[3];
+    return s;
 }
 
-// rstd = 1 / sqrt(mean(v^2) + eps) of the n floats of a padded LDS vector (kernels.py:21-23).
-PE_DEV float padded_rstd(const float* v, int n, float eps, float* red) {
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += kNT) {
-        const float a = v[pad_idx(i)];
-        ss = fmaf(a, a, ss);
+// The RMSNorm of a padded LDS vector v (n <= kNT elements): writes h = v * w (padded; the
+// caller loaded element tid of the natural global weight into w_t) and returns
+// rstd = 1 / sqrt(mean(v^2) + eps) (kernels.py:21-23); the GEMV scales its dot product by rstd.
+PE_DEV float norm_to_lds(const float* v, float w_t, int n, float eps, float* h, float* red) {
+    const int tid = opaque_tid();
+    float a = 0.f;
+    if (tid < n) {
+        a = v[pad_idx(tid)];
+        h[pad_idx(tid)] = a * w_t;
     }
-    return 1.0f / sqrtf(block_sum4(ss, red) / (float)n + eps);
+    return 1.0f / sqrtf(block_sum16(a * a, red) / (float)n + eps);
 }
 
-// Activation unit u of a padded LDS vector, optionally times a (natural, global) weight unit.
+// Activation unit u of a padded LDS vector.
 PE_DEV void lds_unit(const float* v, int u, float* xr) {
     const float4* p = reinterpret_cast<const float4*>(v + u * kUnitStride);
 #pragma unroll
@@ -227,26 +237,28 @@ PE_DEV void lds_unit(const float* v, int u, float* xr) {
         xr[4 * i + 3] = a.w;
     }
 }
-PE_DEV void scale_unit(float* xr, const float4 (&w)[8]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        xr[4 * i] *= w[i].x;
-        xr[4 * i + 1] *= w[i].y;
-        xr[4 * i + 2] *= w[i].z;
-        xr[4 * i + 3] *= w[i].w;
-    }
-}
-PE_DEV void load_unit4(const float* g, int u, float4 (&w)[8]) {
-    const float4* p = reinterpret_cast<const float4*>(g + 32 * u);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) w[i] = p[i];
-}
 
 PE_DEV int64_t tiled_nb(int type, int64_t k) { return k / (int64_t)block_elems(type); }
 
+// Copy n_rows contiguous 64-float rows from global memory into LDS with the gfx950 direct
+// global->LDS loads (16 bytes per lane, 1 KB per wave instruction, no registers); rows past
+// `last` re-read row `last` (in bounds). Completes with the issuing wave's vmcnt.
+PE_DEV void rows_to_lds(const float* src, int n_rows, int last, float* dst) {
+    const int tid = opaque_tid(), wv = tid >> 6, lane = tid & 63;
+    const int chunks = (n_rows + 3) >> 2;  // 4 rows (1 KB) per wave instruction
+    for (int ch = wv; ch < chunks; ch += kWaves) {
+        int row = 4 * ch + (lane >> 4);
+        row = row < last ? row : last;
+        const float* g = src + (int64_t)row * kStepHd + 4 * (lane & 15);
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                         (__attribute__((address_space(3))) void*)(dst + ch * 256),
+                                         16, 0, 0);
+    }
+}
+
 // ---- stage Q: rmsnorm(x) -> rows (d, d + 32) of one head of q, k or v, bias, RoPE ---------
-// Workgroup w < wq: q pairs [w pq, ...); then wk workgroups of k pairs, wk of v pairs. A pass
-// covers 4 pairs (8 lane groups of 32: group g holds row (g & 1) of pair g / 2). x is in LDS.
+// Workgroup w < wq: q pairs [w pq, ...); then wk workgroups of k pairs, wk of v pairs. Lane group
+// g (32 lanes) holds row (g & 1) of pair g / 2 (16 pairs per workgroup at most). x is in LDS.
 template <int T>
 PE_DEV void stage_q(const StepParams& P, const StepLayer& L, Ctx& c, int l, float* lds,
                     int64_t pos, bool pos_ok) {
@@ -260,93 +272,68 @@ PE_DEV void stage_q(const StepParams& P, const StepLayer& L, Ctx& c, int l, floa
     const int npairs = heads * (kStepHd / 2);
     const uint8_t* wt = seg == 0 ? L.w_q : seg == 1 ? L.w_k : L.w_v;
     const float* bias = seg == 0 ? L.b_q : seg == 1 ? L.b_k : L.b_v;
-    const Tiled t{wt, (int64_t)heads * kStepHd, tiled_nb(T, P.hidden)};
+    const Tiled t = make_tiled(wt, (int64_t)heads * kStepHd, tiled_nb(T, P.hidden));
     const int units = P.hidden >> 5;
-    const int tq = opaque_tid();
-    const int g = tq >> 5, glane = tq & 31;
+    const int tid = opaque_tid();
+    const int g = tid >> 5, glane = tid & 31;
     const int u = glane < units ? glane : units - 1;
-    constexpr int kPasses = 2;  // up to 8 pairs per workgroup
-    typename Fmt<T>::Raw raw[kPasses];
-    int pair[kPasses];
-#pragma unroll
-    for (int ps = 0; ps < kPasses; ++ps) {
-        const int pi_local = ps * 4 + (g >> 1);
-        int pi = w0 * P.pq + pi_local;
-        const bool live = pi_local < P.pq && pi < npairs;
-        pair[ps] = live ? pi : -1;
-        pi = live ? pi : 0;
-        const int head = pi >> 5, d = pi & 31;
-        Fmt<T>::load(t, (int64_t)head * kStepHd + d + 32 * (g & 1), u, raw[ps]);
-    }
-    // bias and RoPE factors of each pass's pair, loaded with the weights
-    float pb1[kPasses], pb2[kPasses], pcs[kPasses], psn[kPasses];
-#pragma unroll
-    for (int ps = 0; ps < kPasses; ++ps) {
-        const int pi = pair[ps] >= 0 ? pair[ps] : 0;
-        const int head = pi >> 5, d = pi & 31;
-        const int r1 = head * kStepHd + d;
-        pb1[ps] = bias ? bias[r1] : 0.f;
-        pb2[ps] = bias ? bias[r1 + 32] : 0.f;
-        const int64_t pr = pos_ok ? pos : 0;
-        pcs[ps] = P.cos_tab[pr * 32 + d];
-        psn[ps] = P.sin_tab[pr * 32 + d];
-    }
-    float4 nw[8];
-    load_unit4(L.attn_norm, u, nw);
-    // x of this layer is in lds + kLdsX (polled by the caller)
+    const int pi_local = g >> 1;
+    const int pi0 = w0 * P.pq + pi_local;
+    const bool live = pi_local < P.pq && pi0 < npairs;
+    const int pi = live ? pi0 : 0;
+    const int head = pi >> 5, d = pi & 31;
+    typename Fmt<T>::Raw raw;
+    // the two lane groups of a wave hold the two rows of one pair: `live` is uniform per wave,
+    // and a wave without a pair neither loads nor multiplies
+    if (live) Fmt<T>::load(t, (int64_t)head * kStepHd + d + 32 * (g & 1), u, raw);
+    // bias, RoPE factors and the norm weight, loaded with the weights
+    const int r1 = head * kStepHd + d;
+    const float b1 = bias ? gld(bias, r1) : 0.f, b2 = bias ? gld(bias, r1 + 32) : 0.f;
+    const int64_t pr = pos_ok ? pos : 0;
+    const float cs = P.cos_tab[pr * 32 + d], sn = P.sin_tab[pr * 32 + d];
+    const float nw = gld(L.attn_norm, tid < P.hidden ? tid : 0);
     float* red = lds + kLdsRed;
-    const float rstd = padded_rstd(lds + kLdsX, P.hidden, P.eps, red);
+    const float rstd = norm_to_lds(lds + kLdsX, nw, P.hidden, P.eps, lds + kLdsH, red);
     float xr[32];
-    lds_unit(lds + kLdsX, u, xr);
-    scale_unit(xr, nw);
-    const UnitSums xs = unit_sums(xr);
-    uint64_t* out = P.wl + (int64_t)l * P.layer_stride;
-    const int qd = P.n_head * kStepHd, kd = P.n_kv * kStepHd;
-#pragma unroll
-    for (int ps = 0; ps < kPasses; ++ps) {
-        if (ps * 4 >= P.pq) break;  // uniform
-        float y = glane < units ? Fmt<T>::dot(raw[ps], xr, xs) : 0.f;
+    lds_unit(lds + kLdsH, u, xr);
+    float y = 0.f;
+    if (live) {
+        y = glane < units ? Fmt<T>::dot(raw, xr, unit_sums(xr)) : 0.f;
         y = wave_sum<32>(y) * rstd;
-        // the pair's two rows meet in LDS
-        __syncthreads();
-        if (glane == 0) red[8 + g] = y;
-        __syncthreads();
-        const int pi = pair[ps];
-        if (glane == 0 && (g & 1) == 0 && pi >= 0) {
-            const int head = pi >> 5, d = pi & 31;
-            const int r1 = head * kStepHd + d, r2 = r1 + 32;
-            float y1 = red[8 + g], y2 = red[8 + g + 1];
-            if (bias) {
-                y1 += pb1[ps];
-                y2 += pb2[ps];
+    }
+    // the pair's two rows meet in LDS
+    if (glane == 0) red[32 + g] = y;
+    __syncthreads();
+    if (glane == 0 && (g & 1) == 0 && live) {
+        const int r2 = r1 + 32;
+        const float y1 = red[32 + g] + b1, y2 = red[32 + g + 1] + b2;
+        float o1 = y1, o2 = y2;
+        if (seg < 2) {
+            if (pos_ok) {
+                o1 = y1 * cs - y2 * sn;
+                o2 = y1 * sn + y2 * cs;
+            } else {
+                o1 = o2 = __uint_as_float(0x7FC00000u);
             }
-            float o1 = y1, o2 = y2;
-            if (seg < 2) {
-                if (pos_ok) {
-                    const float cs = pcs[ps], sn = psn[ps];
-                    o1 = y1 * cs - y2 * sn;
-                    o2 = y1 * sn + y2 * cs;
-                } else {
-                    o1 = o2 = __uint_as_float(0x7FC00000u);
-                }
-            }
-            const int base = seg == 0 ? 0 : seg == 1 ? qd : qd + kd;
-            st_pair(out + base + r1, o1, c.tag);
-            st_pair(out + base + r2, o2, c.tag);
-            if (seg > 0 && pos_ok) {  // the cache row of this token (read by later launches)
-                float* cache = (seg == 1 ? L.k_cache : L.v_cache) + ((int64_t)head * P.capacity + pos) * kStepHd;
-                cache[d] = o1;
-                cache[d + 32] = o2;
-            }
+        }
+        uint64_t* out = P.wl + (int64_t)l * P.layer_stride;
+        const int qd = P.n_head * kStepHd, kd = P.n_kv * kStepHd;
+        const int base = seg == 0 ? 0 : seg == 1 ? qd : qd + kd;
+        st_pair(out + base + r1, o1, c.tag);
+        st_pair(out + base + r2, o2, c.tag);
+        if (seg > 0 && pos_ok) {  // the cache row of this token (read by later launches)
+            float* cache = (seg == 1 ? L.k_cache : L.v_cache) + ((int64_t)head * P.capacity + pos) * kStepHd;
+            gst(cache, d, o1);
+            gst(cache, d + 32, o2);
         }
     }
 }
 
 // ---- stage A: attention of kv group j over positions < S, times Wo's columns of group j -----
 // Before the wait: the Wo rows, and the K and V rows of positions < S - 1 (written by earlier
-// launches) copied straight into LDS; the new row comes from the exchange. Scores one position
-// per thread, softmax by block reductions in a fixed order, P.V as wave slices of 64 positions
-// added in order.
+// launches) copied straight into LDS; the new row comes from the exchange. Wave v handles head
+// v / 2 over the 64 positions of slice v % 2: scores (one position per lane), softmax (wave
+// reductions, the two slices combined in order), P.V (one dimension per lane).
 template <int T>
 PE_DEV void stage_a(const StepParams& P, const StepLayer& L, Ctx& c, int l, float* lds, int S) {
     const int nslices = gridDim.x / P.n_kv;
@@ -356,16 +343,15 @@ PE_DEV void stage_a(const StepParams& P, const StepLayer& L, Ctx& c, int l, floa
     const int G = P.group, gunits = 2 * G;  // 32-column units of the group in a Wo row
     const int tid = opaque_tid(), wv = tid >> 6, lane = tid & 63;
     const int r0 = sl * P.ra;
-    // o-projection weights: 16 lanes per row, lane ou holds unit ou of the group's columns
+    // o-projection weights: 16 lanes per row (64 rows at most), lane ou holds unit ou
     const int orow = tid >> 4, ou = tid & 15;
     const int qd = P.n_head * kStepHd;
-    const Tiled wo{L.w_o, P.hidden, tiled_nb(T, qd)};
-    constexpr int kPasses = 2;  // up to 32 rows per workgroup
-    typename Fmt<T>::Raw raw[kPasses];
-#pragma unroll
-    for (int ps = 0; ps < kPasses; ++ps) {
-        const int r = r0 + ps * 16 + orow;
-        Fmt<T>::load(wo, r < P.hidden ? r : P.hidden - 1, j * gunits + (ou < gunits ? ou : gunits - 1), raw[ps]);
+    const Tiled wo = make_tiled(L.w_o, P.hidden, tiled_nb(T, qd));
+    typename Fmt<T>::Raw raw;
+    const bool olive = 4 * wv < P.ra;  // uniform per wave: the wave holds o-projection rows
+    if (olive) {
+        const int r = r0 + orow;
+        Fmt<T>::load(wo, r < P.hidden ? r : P.hidden - 1, j * gunits + (ou < gunits ? ou : gunits - 1), raw);
     }
     const int old = S - 1;  // cache rows written by earlier launches
     float* kl = lds + kLdsK;
@@ -381,7 +367,7 @@ PE_DEV void stage_a(const StepParams& P, const StepLayer& L, Ctx& c, int l, floa
     const uint64_t* qsrc = qkv + (int64_t)j * nq;
     const uint64_t* ksrc = qkv + qd + j * kStepHd;
     const uint64_t* vsrc = qkv + qd + P.n_kv * kStepHd + j * kStepHd;
-    poll_map<3, false>([=](int i) { return i < nq ? qsrc + i : i < nq + kStepHd ? ksrc + (i - nq) : vsrc + (i - nq - kStepHd); },
+    poll_map<1, false>([=](int i) { return i < nq ? qsrc + i : i < nq + kStepHd ? ksrc + (i - nq) : vsrc + (i - nq - kStepHd); },
                        nq + 2 * kStepHd, c, qg);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's K/V copies are in LDS (also when no poll ran)
     __syncthreads();
@@ -390,250 +376,214 @@ PE_DEV void stage_a(const StepParams& P, const StepLayer& L, Ctx& c, int l, floa
         vl[old * kStepHd + tid] = qg[nq + kStepHd + tid];
     }
     __syncthreads();
-    // scores of position tid for every head of the group; the lane's K row is read from LDS
-    // starting at float4 (tid & 15) (rotated, so the 16 lanes of a row of banks read different
-    // banks), and q in the same rotated order
-    float sc[kStepMaxGroup];
-    const bool live = tid < S;
-    {
-        float4 kr[16];
-        const float4* k4 = reinterpret_cast<const float4*>(kl + (live ? tid : 0) * kStepHd);
-        const int rot = tid & 15;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) kr[i] = k4[(i + rot) & 15];
-#pragma unroll
-        for (int h = 0; h < kStepMaxGroup; ++h) {
-            float a0 = 0.f, a1 = 0.f;
-            if (h < G) {
-                const float4* q4 = reinterpret_cast<const float4*>(qg + h * kStepHd);
-#pragma unroll
-                for (int i = 0; i < 16; i += 2) {
-                    const float4 q = q4[(i + rot) & 15], q1 = q4[(i + 1 + rot) & 15];
-                    a0 = fmaf(q.x, kr[i].x, a0);
-                    a0 = fmaf(q.y, kr[i].y, a0);
-                    a0 = fmaf(q.z, kr[i].z, a0);
-                    a0 = fmaf(q.w, kr[i].w, a0);
-                    a1 = fmaf(q1.x, kr[i + 1].x, a1);
-                    a1 = fmaf(q1.y, kr[i + 1].y, a1);
-                    a1 = fmaf(q1.z, kr[i + 1].z, a1);
-                    a1 = fmaf(q1.w, kr[i + 1].w, a1);
-                }
-            }
-            sc[h] = (a0 + a1) * P.scale;
-        }
-    }
-    // softmax over positions per head (block max, exponentials, block sum; fixed orders)
+    const int h = wv >> 1, half = wv & 1;
+    const bool hlive = h < G;                // uniform per wave
+    const int sp = 64 * half + lane;         // this lane's position
+    const bool live = hlive && sp < S;
     float* e = lds + kLdsE;
     float* red = lds + kLdsRed;
-    const float NEG_INF = -__builtin_huge_valf();
-    float m[kStepMaxGroup];
+    // scores: K row and q of head h read from LDS starting at float4 (lane & 15), rotated, so
+    // the 16 lanes of a bank row read different banks
+    float sc = 0.f;
+    if (hlive) {
+        const float4* k4 = reinterpret_cast<const float4*>(kl + (sp < S ? sp : 0) * kStepHd);
+        const float4* q4 = reinterpret_cast<const float4*>(qg + h * kStepHd);
+        const int rot = lane & 15;
+        float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-    for (int h = 0; h < kStepMaxGroup; ++h) m[h] = wave_max<64>(live ? sc[h] : NEG_INF);
-    if (lane == 0) {
-#pragma unroll
-        for (int h = 0; h < kStepMaxGroup; ++h) red[wv * kStepMaxGroup + h] = m[h];
-    }
-    __syncthreads();
-    float ls[kStepMaxGroup];
-#pragma unroll
-    for (int h = 0; h < kStepMaxGroup; ++h) {
-        const float mm = fmaxf(fmaxf(red[h], red[kStepMaxGroup + h]),
-                               fmaxf(red[2 * kStepMaxGroup + h], red[3 * kStepMaxGroup + h]));
-        const float ev = live ? expf(sc[h] - mm) : 0.f;
-        if (tid < kStepMaxCap) e[h * kStepMaxCap + tid] = ev;
-        ls[h] = wave_sum<64>(ev);
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int h = 0; h < kStepMaxGroup; ++h) red[32 + wv * kStepMaxGroup + h] = ls[h];
-    }
-    __syncthreads();
-    // P.V: wave wv < 2 sums its 64 positions for every head (a slice wholly past S adds zeros)
-    float* pv = lds + kLdsPv;  // [slice][head * 64 + d]
-    constexpr int kSlices = kStepMaxCap / 64;
-    if (wv < kSlices) {
-        const int n = S - 64 * wv;  // live positions of the slice (uniform)
-        float acc[kStepMaxGroup];
-#pragma unroll
-        for (int h = 0; h < kStepMaxGroup; ++h) acc[h] = 0.f;
-        if (n > 0) {
-            const float* vs = vl + 64 * wv * kStepHd + lane;
-            for (int i4 = 0; i4 < 16; ++i4) {
-                if (4 * i4 >= n) break;  // uniform
-                const float v0 = vs[(4 * i4) * kStepHd], v1 = vs[(4 * i4 + 1) * kStepHd];
-                const float v2 = vs[(4 * i4 + 2) * kStepHd], v3 = vs[(4 * i4 + 3) * kStepHd];
-#pragma unroll
-                for (int h = 0; h < kStepMaxGroup; ++h) {
-                    if (h < G) {
-                        const float4 ev = reinterpret_cast<const float4*>(e + h * kStepMaxCap + 64 * wv)[i4];
-                        // positions past S have zero exponentials; rows there may hold anything
-                        const float a = fmaf(ev.x, 4 * i4 < n ? v0 : 0.f, acc[h]);
-                        const float b = fmaf(ev.y, 4 * i4 + 1 < n ? v1 : 0.f, a);
-                        const float cc = fmaf(ev.z, 4 * i4 + 2 < n ? v2 : 0.f, b);
-                        acc[h] = fmaf(ev.w, 4 * i4 + 3 < n ? v3 : 0.f, cc);
-                    }
-                }
-            }
+        for (int i = 0; i < 16; i += 2) {
+            const float4 k0 = k4[(i + rot) & 15], k1 = k4[(i + 1 + rot) & 15];
+            const float4 q0 = q4[(i + rot) & 15], q1 = q4[(i + 1 + rot) & 15];
+            a0 = fmaf(q0.x, k0.x, a0);
+            a0 = fmaf(q0.y, k0.y, a0);
+            a0 = fmaf(q0.z, k0.z, a0);
+            a0 = fmaf(q0.w, k0.w, a0);
+            a1 = fmaf(q1.x, k1.x, a1);
+            a1 = fmaf(q1.y, k1.y, a1);
+            a1 = fmaf(q1.z, k1.z, a1);
+            a1 = fmaf(q1.w, k1.w, a1);
         }
-#pragma unroll
-        for (int h = 0; h < kStepMaxGroup; ++h)
-            if (h < G) pv[wv * (kStepMaxGroup * kStepHd) + h * kStepHd + lane] = acc[h];
+        sc = (a0 + a1) * P.scale;
+    }
+    // softmax of head h over its two slices (fixed order: slice 0 then slice 1)
+    const float NEG_INF = -__builtin_huge_valf();
+    const float m = wave_max<64>(live ? sc : NEG_INF);
+    if (lane == 0) red[wv] = m;
+    __syncthreads();
+    const float mm = hlive ? fmaxf(red[2 * h], red[2 * h + 1]) : 0.f;
+    const float ev = live ? expf(sc - mm) : 0.f;
+    if (hlive) e[h * kStepMaxCap + sp] = ev;
+    const float ls = wave_sum<64>(ev);
+    if (lane == 0) red[16 + wv] = ls;
+    __syncthreads();
+    // P.V: lane d of wave (h, half) sums the positions of its slice
+    float* pv = lds + kLdsPv;  // [half][head * 64 + d]
+    if (hlive) {
+        const int n = S - 64 * half;  // live positions of the slice (uniform)
+        float a0 = 0.f, a1 = 0.f;
+        const float* vs = vl + 64 * half * kStepHd + lane;
+        const float4* e4 = reinterpret_cast<const float4*>(e + h * kStepMaxCap + 64 * half);
+        for (int i4 = 0; i4 < 16; i4 += 2) {
+            if (4 * i4 >= n) break;  // uniform
+            const float4 x0 = e4[i4], x1 = e4[i4 + 1];  // zero past S
+            const int b = 4 * i4;
+            // rows past S may hold anything: their (zero) weights must not meet a NaN
+            const float v0 = b < n ? vs[b * kStepHd] : 0.f, v1 = b + 1 < n ? vs[(b + 1) * kStepHd] : 0.f;
+            const float v2 = b + 2 < n ? vs[(b + 2) * kStepHd] : 0.f, v3 = b + 3 < n ? vs[(b + 3) * kStepHd] : 0.f;
+            const float v4 = b + 4 < n ? vs[(b + 4) * kStepHd] : 0.f, v5 = b + 5 < n ? vs[(b + 5) * kStepHd] : 0.f;
+            const float v6 = b + 6 < n ? vs[(b + 6) * kStepHd] : 0.f, v7 = b + 7 < n ? vs[(b + 7) * kStepHd] : 0.f;
+            a0 = fmaf(x0.x, v0, a0);
+            a0 = fmaf(x0.y, v1, a0);
+            a0 = fmaf(x0.z, v2, a0);
+            a0 = fmaf(x0.w, v3, a0);
+            a1 = fmaf(x1.x, v4, a1);
+            a1 = fmaf(x1.y, v5, a1);
+            a1 = fmaf(x1.z, v6, a1);
+            a1 = fmaf(x1.w, v7, a1);
+        }
+        pv[half * (kStepMaxGroup * kStepHd) + h * kStepHd + lane] = a0 + a1;
     }
     __syncthreads();
     float* attn = lds + kLdsAttn;
-    for (int o = tid; o < G * kStepHd; o += kNT) {
-        const int h = o >> 6;
-        constexpr int W = kStepMaxGroup * kStepHd;
-        const float a = pv[o] + pv[W + o];
-        const float lsum = ((red[32 + h] + red[32 + kStepMaxGroup + h]) + red[32 + 2 * kStepMaxGroup + h]) +
-                           red[32 + 3 * kStepMaxGroup + h];
-        attn[pad_idx(o)] = round_to_f16(a / lsum);
+    if (tid < G * kStepHd) {
+        const int hh = tid >> 6;
+        const float a = pv[tid] + pv[kStepMaxGroup * kStepHd + tid];
+        const float lsum = red[16 + 2 * hh] + red[16 + 2 * hh + 1];
+        attn[pad_idx(tid)] = round_to_f16(a / lsum);
     }
     __syncthreads();
     // o-projection share of rows r0 .. r0 + ra
+    if (!olive) return;
     float xr[32];
     lds_unit(attn, ou < gunits ? ou : gunits - 1, xr);
-    const UnitSums xs = unit_sums(xr);
-    uint64_t* parts = P.wl + (int64_t)l * P.layer_stride + P.off_parts + (int64_t)j * P.hidden;
-#pragma unroll
-    for (int ps = 0; ps < kPasses; ++ps) {
-        if (ps * 16 >= P.ra) break;  // uniform
-        float acc = ou < gunits ? Fmt<T>::dot(raw[ps], xr, xs) : 0.f;
-        acc = wave_sum<16>(acc);
-        const int rl = ps * 16 + orow, r = r0 + rl;
-        if (ou == 0 && rl < P.ra && r < P.hidden) st_pair(parts + r, acc, c.tag);
+    float acc = ou < gunits ? Fmt<T>::dot(raw, xr, unit_sums(xr)) : 0.f;
+    acc = wave_sum<16>(acc);
+    const int r = r0 + orow;
+    if (ou == 0 && orow < P.ra && r < P.hidden) {
+        uint64_t* parts = P.wl + (int64_t)l * P.layer_stride + P.off_parts + (int64_t)j * P.hidden;
+        st_pair(parts + r, acc, c.tag);
     }
 }
 
 // ---- stage F: x + parts -> rmsnorm -> [gate; up] -> silu(g) * u ---------------------------
+// Lane group g (32 lanes) computes SiLU pair f0 + g (its gate and up rows, 32 pairs at most).
 template <int T>
 PE_DEV void stage_f(const StepParams& P, const StepLayer& L, Ctx& c, int l, float* lds) {
     const int w = opaque_wg();
-    const int tf = opaque_tid();
-    const int g = tf >> 5, glane = tf & 31;
+    const int tid = opaque_tid();
+    const int g = tid >> 5, glane = tid & 31;
     const int units = P.hidden >> 5;
     const int u = glane < units ? glane : units - 1;
-    const Tiled t{L.w_gu, 2 * (int64_t)P.ffn, tiled_nb(T, P.hidden)};
-    constexpr int kPasses = 4;  // up to 32 pairs per workgroup
-    typename Fmt<T>::Raw rg[kPasses], ru[kPasses];
+    const Tiled t = make_tiled(L.w_gu, 2 * (int64_t)P.ffn, tiled_nb(T, P.hidden));
     const int f0 = w * P.pf;
-#pragma unroll
-    for (int ps = 0; ps < kPasses; ++ps) {
-        const int fl = ps * 8 + g;
-        int f = f0 + fl;
-        f = (fl < P.pf && f < P.ffn) ? f : P.ffn - 1;
-        Fmt<T>::load(t, f, u, rg[ps]);
-        Fmt<T>::load(t, f + P.ffn, u, ru[ps]);
+    const int f = (g < P.pf && f0 + g < P.ffn) ? f0 + g : P.ffn - 1;
+    // a wave whose two lane groups hold no pair neither loads nor multiplies
+    const int g0 = 2 * (tid >> 6);
+    const bool wlive = g0 < P.pf && f0 + g0 < P.ffn;
+    typename Fmt<T>::Raw rg, ru;
+    if (wlive) {
+        Fmt<T>::load(t, f, u, rg);
+        Fmt<T>::load(t, f + P.ffn, u, ru);
     }
-    float4 nw[8];
-    load_unit4(L.ffn_norm, u, nw);
+    const float nw = gld(L.ffn_norm, tid < P.hidden ? tid : 0);
     // parts of this layer -> LDS, xs = x + part_0 + part_1 + ... (in that order)
     float* in = lds + kLdsIn;
     const uint64_t* parts = P.wl + (int64_t)l * P.layer_stride + P.off_parts;
     poll_vec<kStepMaxParts / kNT, false>(parts, P.n_kv * P.hidden, c, in);
     float* xsl = lds + kLdsXs;
-    for (int i = threadIdx.x; i < P.hidden; i += kNT) {
-        float v = lds[kLdsX + pad_idx(i)];
-        for (int jj = 0; jj < P.n_kv; ++jj) v += in[jj * P.hidden + i];
-        xsl[pad_idx(i)] = v;
+    if (tid < P.hidden) {
+        float v = lds[kLdsX + pad_idx(tid)];
+        for (int jj = 0; jj < P.n_kv; ++jj) v += in[jj * P.hidden + tid];
+        xsl[pad_idx(tid)] = v;
     }
     __syncthreads();
     float* red = lds + kLdsRed;
-    const float rstd = padded_rstd(xsl, P.hidden, P.eps, red);
+    const float rstd = norm_to_lds(xsl, nw, P.hidden, P.eps, lds + kLdsH, red);
+    if (!wlive) return;
     float xr[32];
-    lds_unit(xsl, u, xr);
-    scale_unit(xr, nw);
+    lds_unit(lds + kLdsH, u, xr);
     const UnitSums xs = unit_sums(xr);
-    uint64_t* act = P.wl + (int64_t)l * P.layer_stride + P.off_act;
-#pragma unroll
-    for (int ps = 0; ps < kPasses; ++ps) {
-        if (ps * 8 >= P.pf) break;  // uniform
-        float gv = glane < units ? Fmt<T>::dot(rg[ps], xr, xs) : 0.f;
-        float uv = glane < units ? Fmt<T>::dot(ru[ps], xr, xs) : 0.f;
-        gv = wave_sum<32>(gv) * rstd;
-        uv = wave_sum<32>(uv) * rstd;
-        const int fl = ps * 8 + g, f = f0 + fl;
-        if (glane == 0 && fl < P.pf && f < P.ffn)
-            st_pair(act + f, (gv * (1.0f / (1.0f + expf(-gv)))) * uv, c.tag);
+    float gv = glane < units ? Fmt<T>::dot(rg, xr, xs) : 0.f;
+    float uv = glane < units ? Fmt<T>::dot(ru, xr, xs) : 0.f;
+    gv = wave_sum<32>(gv) * rstd;
+    uv = wave_sum<32>(uv) * rstd;
+    if (glane == 0 && g < P.pf && f0 + g < P.ffn) {
+        uint64_t* act = P.wl + (int64_t)l * P.layer_stride + P.off_act;
+        st_pair(act + f0 + g, (gv * (1.0f / (1.0f + expf(-gv)))) * uv, c.tag);
     }
 }
 
 // ---- stage D: xs + Wdown act -> next x ------------------------------------------------------
-// Wave v of the workgroup owns rows r0 + v, r0 + v + 4, ... (pd rows); UPL units per lane.
-template <int T, int UPL>
+// Row r0 + v / 4 (four rows at most) is split over the four waves 4 (v / 4) .. + 3, lane i of
+// quarter q taking unit 64 q + i; the quarters are added in order.
+template <int T>
 PE_DEV void stage_d(const StepParams& P, const StepLayer& L, Ctx& c, int l, float* lds) {
     const int w = opaque_wg();
     const int r0 = w * P.pd;
-    const int td = opaque_tid();
-    const int wv = td >> 6, lane = td & 63;
+    if (r0 >= P.hidden) return;  // uniform: no down rows here
+    const int tid = opaque_tid();
+    const int wv = tid >> 6, lane = tid & 63;
+    const int rl = wv >> 2, q = wv & 3;
     const int units = P.ffn >> 5;
-    const bool has_rows = r0 < P.hidden;
-    const Tiled t{L.w_down, P.hidden, tiled_nb(T, P.ffn)};
-    typename Fmt<T>::Raw raw[UPL];
-    const int rl = wv;  // pd <= 4: one row per wave
+    const Tiled t = make_tiled(L.w_down, P.hidden, tiled_nb(T, P.ffn));
     const int r = r0 + rl < P.hidden ? r0 + rl : P.hidden - 1;
-#pragma unroll
-    for (int k = 0; k < UPL; ++k) {
-        const int uu = lane + 64 * k;
-        Fmt<T>::load(t, r, uu < units ? uu : units - 1, raw[k]);
-    }
-    uint64_t* xo = P.wl + (int64_t)l * P.layer_stride + P.off_x;
-    if (!has_rows) return;  // uniform: this workgroup has no down rows
+    const int uu = 64 * q + lane;
+    typename Fmt<T>::Raw raw;
+    Fmt<T>::load(t, r, uu < units ? uu : units - 1, raw);
     float* in = lds + kLdsIn;
     poll_vec<kStepMaxFfn / kNT, true>(P.wl + (int64_t)l * P.layer_stride + P.off_act, P.ffn, c, in);
     float acc = 0.f;
-#pragma unroll
-    for (int k = 0; k < UPL; ++k) {
-        const int uu = lane + 64 * k;
-        if (uu < units) {
-            float xr[32];
-            lds_unit(in, uu, xr);
-            acc += Fmt<T>::dot(raw[k], xr, unit_sums(xr));
-        }
+    if (uu < units) {
+        float xr[32];
+        lds_unit(in, uu, xr);
+        acc = Fmt<T>::dot(raw, xr, unit_sums(xr));
     }
     acc = wave_sum<64>(acc);
-    if (lane == 0 && rl < P.pd && r0 + rl < P.hidden) {
-        const int rr = r0 + rl;
-        st_pair(xo + rr, lds[kLdsXs + pad_idx(rr)] + acc, c.tag);
+    float* red = lds + kLdsRed;
+    if (lane == 0) red[wv] = acc;
+    __syncthreads();
+    if (tid < 4 && tid < P.pd && r0 + tid < P.hidden) {
+        const int rr = r0 + tid;
+        const float sum = ((red[4 * tid] + red[4 * tid + 1]) + red[4 * tid + 2]) + red[4 * tid + 3];
+        uint64_t* xo = P.wl + (int64_t)l * P.layer_stride + P.off_x;
+        st_pair(xo + rr, lds[kLdsXs + pad_idx(rr)] + sum, c.tag);
     }
 }
 
 // ---- LM head: rows [w pl, ...) of W_out . rmsnorm(x), greedy pick -------------------------
 template <int T>
-PE_DEV uint64_t stage_lm(const StepParams& P, Ctx& c, float* lds) {
+PE_DEV uint64_t stage_lm(const StepParams& P, float* lds) {
     const int w = opaque_wg();
-    const int tl = opaque_tid();
-    const int g = tl >> 5, glane = tl & 31;
+    const int tid = opaque_tid();
+    const int g = tid >> 5, glane = tid & 31;
     const int units = P.hidden >> 5;
     const int u = glane < units ? glane : units - 1;
-    const Tiled t{P.w_out, P.vocab, tiled_nb(T, P.hidden)};
+    const Tiled t = make_tiled(P.w_out, P.vocab, tiled_nb(T, P.hidden));
     const int64_t r0 = (int64_t)w * P.pl;
     const int64_t rend = r0 + P.pl < P.vocab ? r0 + P.pl : P.vocab;
-    float4 nw[8];
-    load_unit4(P.out_norm, u, nw);
-    // x of the last layer was polled into LDS by the caller
-    float* red = lds + kLdsRed;
-    const float rstd = padded_rstd(lds + kLdsX, P.hidden, P.eps, red);
-    float xr[32];
-    lds_unit(lds + kLdsX, u, xr);
-    scale_unit(xr, nw);
-    const UnitSums xs = unit_sums(xr);
-    uint64_t best = 0;
-    // group g takes rows r0 + g, r0 + g + 8, ...; four rows in flight per lane
+    const int64_t last = rend - 1 >= 0 ? rend - 1 : 0;
+    constexpr int kGroups = kNT / 32;
     constexpr int kDepth = 4;
     typename Fmt<T>::Raw raw[kDepth];
-    const int64_t last = rend - 1;
 #pragma unroll
     for (int k = 0; k < kDepth; ++k) {
-        const int64_t r = r0 + g + 8 * k;
+        const int64_t r = r0 + g + kGroups * k;
         Fmt<T>::load(t, r <= last ? r : last, u, raw[k]);
     }
-    for (int64_t base = r0; base < rend; base += 8 * kDepth) {  // same trip count in every group
+    const float nw = P.out_norm[tid < P.hidden ? tid : 0];
+    float* red = lds + kLdsRed;
+    const float rstd = norm_to_lds(lds + kLdsX, nw, P.hidden, P.eps, lds + kLdsH, red);
+    float xr[32];
+    lds_unit(lds + kLdsH, u, xr);
+    const UnitSums xs = unit_sums(xr);
+    uint64_t best = 0;
+    // group g takes rows r0 + g, r0 + g + 32, ...; four rows in flight per lane
+    for (int64_t base = r0; base < rend; base += kGroups * kDepth) {  // same trip count in every group
 #pragma unroll
         for (int k = 0; k < kDepth; ++k) {
-            const int64_t r = base + g + 8 * k;
+            const int64_t r = base + g + kGroups * k;
             float y = glane < units ? Fmt<T>::dot(raw[k], xr, xs) : 0.f;
-            const int64_t rn = r + 8 * kDepth;
+            const int64_t rn = r + kGroups * kDepth;
             Fmt<T>::load(t, rn <= last ? rn : last, u, raw[k]);
             y = wave_sum<32>(y) * rstd;
             if (glane == 0 && r < rend) {
@@ -643,18 +593,18 @@ PE_DEV uint64_t stage_lm(const StepParams& P, Ctx& c, float* lds) {
             }
         }
     }
-    (void)c;
     return best;
 }
 
-// Greedy pick of the launch: block keys -> workgroup 0 -> decode state.
+// The workgroup's best key (group leaders hold theirs) -> its record in the workspace.
 PE_DEV void publish_pick(const StepParams& P, Ctx& c, uint64_t best, float* lds) {
-    uint64_t* keys = reinterpret_cast<uint64_t*>(lds + kLdsRed);  // 8 group keys
+    uint64_t* keys = reinterpret_cast<uint64_t*>(lds + kLdsRed);  // 32 group keys
+    const int tid = threadIdx.x;
     __syncthreads();
-    if ((threadIdx.x & 31) == 0) keys[threadIdx.x >> 5] = best;
+    if ((tid & 31) == 0) keys[tid >> 5] = best;
     __syncthreads();
-    uint64_t b = 0;
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
+        uint64_t b = 0;
 #pragma unroll
         for (int g = 0; g < kNT / 32; ++g) b = keys[g] > b ? keys[g] : b;
         uint64_t* rec = P.ws + P.off_lm + (int64_t)blockIdx.x * 16;
@@ -674,23 +624,19 @@ PE_DEV void dispatch_q(int type, const StepParams& P, const StepLayer& L, Ctx& c
     }
 }
 
-template <int UPL>
-PE_DEV void dispatch_d(int type, const StepParams& P, const StepLayer& L, Ctx& c, int l, float* lds) {
-    switch (type) {
-        case PE_TYPE_Q8_0: stage_d<PE_TYPE_Q8_0, UPL>(P, L, c, l, lds); break;
-        case PE_TYPE_Q5_0: stage_d<PE_TYPE_Q5_0, UPL>(P, L, c, l, lds); break;
-        case PE_TYPE_Q4_K: stage_d<PE_TYPE_Q4_K, UPL>(P, L, c, l, lds); break;
-        case PE_TYPE_Q6_K: stage_d<PE_TYPE_Q6_K, UPL>(P, L, c, l, lds); break;
-        default: break;
-    }
-}
-
-template <int UPLD>
 __global__ __launch_bounds__(kNT, 1) void k_decode_step(StepParams P) {
     extern __shared__ float lds[];
     __shared__ uint32_t s_hdr[4];
+    // the layer table, read once: stages read their layer's types and pointers from LDS
+    __shared__ StepLayer s_layers[kStepMaxLayers];
     const int tid = threadIdx.x, lane = tid & 63;
     uint32_t* wsw = reinterpret_cast<uint32_t*>(P.ws);
+    {
+        constexpr int kWords = sizeof(StepLayer) / 8;
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(P.layers);
+        uint64_t* dst = reinterpret_cast<uint64_t*>(s_layers);
+        for (int i = tid; i < P.n_layers * kWords; i += kNT) dst[i] = src[i];
+    }
     if (tid == 0) {
         s_hdr[0] = wsw[0];                      // launch counter
         s_hdr[1] = (uint32_t)P.state[0];        // token (low word; checked below)
@@ -705,17 +651,18 @@ __global__ __launch_bounds__(kNT, 1) void k_decode_step(StepParams P) {
     const bool pos_ok = s_hdr[3] != 0;
     const int S = pos_ok ? (int)pos + 1 : 1;
     // embedding row of the token (every workgroup decodes it itself; model.py:152)
-    for (int i = tid; i < P.hidden; i += kNT)
-        lds[kLdsX + pad_idx(i)] = pos_ok ? raw_element(P.embed_type, P.embed, token * P.hidden + i)
-                                         : __uint_as_float(0x7FC00000u);
+    if (tid < P.hidden)
+        lds[kLdsX + pad_idx(tid)] = pos_ok ? raw_element(P.embed_type, P.embed, token * P.hidden + tid)
+                                           : __uint_as_float(0x7FC00000u);
     __syncthreads();
     for (int l = 0; l < P.n_layers; ++l) {
-        const StepLayer& L = P.layers[l];
+        const StepLayer& L = s_layers[l];
         if (l > 0) {  // x of this layer = stage D output of the previous one
-            poll_vec<4, true>(P.wl + (int64_t)(l - 1) * P.layer_stride + P.off_x, P.hidden, c, lds + kLdsX);
+            poll_vec<kStepMaxHidden / kNT, true>(P.wl + (int64_t)(l - 1) * P.layer_stride + P.off_x, P.hidden, c, lds + kLdsX);
         }
         dispatch_q(blockIdx.x < P.wq ? L.type_q : blockIdx.x < P.wq + P.wk ? L.type_k : L.type_v,
                    P, L, c, l, lds, pos, pos_ok);
+        lds_barrier();
         switch (L.type_o) {
             case PE_TYPE_Q8_0: stage_a<PE_TYPE_Q8_0>(P, L, c, l, lds, S); break;
             case PE_TYPE_Q5_0: stage_a<PE_TYPE_Q5_0>(P, L, c, l, lds, S); break;
@@ -723,7 +670,7 @@ __global__ __launch_bounds__(kNT, 1) void k_decode_step(StepParams P) {
             case PE_TYPE_Q6_K: stage_a<PE_TYPE_Q6_K>(P, L, c, l, lds, S); break;
             default: break;
         }
-        __syncthreads();
+        lds_barrier();
         switch (L.type_gu) {
             case PE_TYPE_Q8_0: stage_f<PE_TYPE_Q8_0>(P, L, c, l, lds); break;
             case PE_TYPE_Q5_0: stage_f<PE_TYPE_Q5_0>(P, L, c, l, lds); break;
@@ -731,25 +678,30 @@ __global__ __launch_bounds__(kNT, 1) void k_decode_step(StepParams P) {
             case PE_TYPE_Q6_K: stage_f<PE_TYPE_Q6_K>(P, L, c, l, lds); break;
             default: break;
         }
-        __syncthreads();
-        dispatch_d<UPLD>(L.type_down, P, L, c, l, lds);
-        __syncthreads();
+        lds_barrier();
+        switch (L.type_down) {
+            case PE_TYPE_Q8_0: stage_d<PE_TYPE_Q8_0>(P, L, c, l, lds); break;
+            case PE_TYPE_Q5_0: stage_d<PE_TYPE_Q5_0>(P, L, c, l, lds); break;
+            case PE_TYPE_Q4_K: stage_d<PE_TYPE_Q4_K>(P, L, c, l, lds); break;
+            case PE_TYPE_Q6_K: stage_d<PE_TYPE_Q6_K>(P, L, c, l, lds); break;
+            default: break;
+        }
+        lds_barrier();
     }
-    poll_vec<4, true>(P.wl + (int64_t)(P.n_layers - 1) * P.layer_stride + P.off_x, P.hidden, c, lds + kLdsX);
+    poll_vec<kStepMaxHidden / kNT, true>(P.wl + (int64_t)(P.n_layers - 1) * P.layer_stride + P.off_x, P.hidden, c, lds + kLdsX);
     uint64_t best = 0;
     switch (P.out_type) {
-        case PE_TYPE_Q8_0: best = stage_lm<PE_TYPE_Q8_0>(P, c, lds); break;
-        case PE_TYPE_Q5_0: best = stage_lm<PE_TYPE_Q5_0>(P, c, lds); break;
-        case PE_TYPE_Q4_K: best = stage_lm<PE_TYPE_Q4_K>(P, c, lds); break;
-        case PE_TYPE_Q6_K: best = stage_lm<PE_TYPE_Q6_K>(P, c, lds); break;
+        case PE_TYPE_Q8_0: best = stage_lm<PE_TYPE_Q8_0>(P, lds); break;
+        case PE_TYPE_Q5_0: best = stage_lm<PE_TYPE_Q5_0>(P, lds); break;
+        case PE_TYPE_Q4_K: best = stage_lm<PE_TYPE_Q4_K>(P, lds); break;
+        case PE_TYPE_Q6_K: best = stage_lm<PE_TYPE_Q6_K>(P, lds); break;
         default: break;
     }
     publish_pick(P, c, best, lds);
     if (blockIdx.x != 0) return;
-    // workgroup 0: every workgroup's key -> the pick; advance the decode state and the counter
-    float* keyf = lds + kLdsIn;  // hi word of workgroup i at 2i, lo word at 2i + 1
+    // workgroup 0: every workgroup's record -> the pick; advance the decode state and the counter
+    uint64_t b = 0;
     {
-        // the records are 16 pairs apart: poll pair 0 and 1 of each
         bool give_up = c.failed;
         uint32_t spins = 0;
         for (int i = tid; i < (int)gridDim.x; i += kNT) {
@@ -762,28 +714,22 @@ __global__ __launch_bounds__(kNT, 1) void k_decode_step(StepParams P) {
                 if (give_up) break;
                 if ((++spins & 63u) == 0) give_up = spins > kStepSpinMax || ld_word(c.err) != 0;
             }
-            keyf[2 * i] = __uint_as_float((uint32_t)hi);
-            keyf[2 * i + 1] = __uint_as_float((uint32_t)lo);
+            const uint64_t k = ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+            b = k > b ? k : b;
         }
         if (__syncthreads_or(give_up) && !c.failed) {
             c.failed = true;
             if (tid == 0) st_word(c.err, 1u);
         }
     }
-    // the largest key: per thread, per wave (DPP), then the four waves in order
-    uint64_t b = 0;
-    for (int i = tid; i < (int)gridDim.x; i += kNT) {
-        const uint64_t k = ((uint64_t)__float_as_uint(keyf[2 * i]) << 32) | __float_as_uint(keyf[2 * i + 1]);
-        b = k > b ? k : b;
-    }
+    // the largest key: per wave (DPP), then the waves in order
     b = wave_max_u64(b);
     uint64_t* wkeys = reinterpret_cast<uint64_t*>(lds + kLdsRed);
-    __syncthreads();
     if (lane == 0) wkeys[tid >> 6] = b;
     __syncthreads();
     if (tid == 0) {
 #pragma unroll
-        for (int q = 0; q < kNT / 64; ++q) b = wkeys[q] > b ? wkeys[q] : b;
+        for (int q = 0; q < kWaves; ++q) b = wkeys[q] > b ? wkeys[q] : b;
         const int64_t tok = argmax_row(b);
         const int64_t cnt = P.state[2];
         P.state[0] = tok;
@@ -805,6 +751,9 @@ struct StepLayout {
     int64_t layer_stride, off_parts, off_act, off_x, off_lm, total_pairs;
 };
 
+// Workspace layout (64-bit pairs): a 32-pair header (launch counter at word 0, error word at
+// word 16), then per layer q/k/v, parts, act and x (each padded to whole 128-byte lines), then
+// one 16-pair record per workgroup for the LM-head pick.
 static StepLayout step_layout(int n_layers, int hidden, int ffn, int n_head, int n_kv, int n_wg) {
     StepLayout s;
     const int64_t nq = (int64_t)(n_head + 2 * n_kv) * kStepHd;
@@ -812,16 +761,16 @@ static StepLayout step_layout(int n_layers, int hidden, int ffn, int n_head, int
     s.off_act = s.off_parts + a16((int64_t)n_kv * hidden);
     s.off_x = s.off_act + a16(ffn);
     s.layer_stride = s.off_x + a16(hidden);
-    const int64_t head = 32;  // 256 bytes: counter, error words
+    const int64_t head = 32;
     s.off_lm = head + (int64_t)n_layers * s.layer_stride;
     s.total_pairs = s.off_lm + 16LL * n_wg;
-    // offsets of layer data are relative to ws + head
     return s;
 }
 
 extern "C" int pe_decode_step_supported(int n_layers, int hidden, int ffn, int n_head, int n_kv,
                                         int head_dim, int64_t capacity, int64_t vocab) {
-    if (n_layers <= 0 || hidden <= 0 || ffn <= 0 || n_head <= 0 || n_kv <= 0 || vocab <= 0)
+    if (n_layers <= 0 || n_layers > kStepMaxLayers || hidden <= 0 || ffn <= 0 || n_head <= 0 ||
+        n_kv <= 0 || vocab <= 0)
         return PE_ERR_SHAPE;
     if (head_dim != kStepHd || hidden % 32 || hidden > kStepMaxHidden || ffn % 32 ||
         ffn > kStepMaxFfn || n_head % n_kv || n_head / n_kv > kStepMaxGroup || n_kv > kStepMaxKv ||
@@ -843,7 +792,7 @@ extern "C" int pe_decode_step(const pe_step_args* a, pe_stream_t stream) {
     int st = pe_decode_step_supported(a->n_layers, a->hidden, a->ffn, a->n_head, a->n_kv,
                                       a->head_dim, a->capacity, a->vocab);
     if (st) return st;
-    if (a->n_wg < 64 || a->n_wg > 1024) return PE_ERR_SHAPE;
+    if (a->n_wg < 64 || a->n_wg > 1024 || a->n_layers > kStepMaxLayers) return PE_ERR_SHAPE;
     if (!a->layers || !a->layers_dev || !a->embed || !a->w_out || !a->out_norm || !a->cos_tab ||
         !a->sin_tab || !a->state || !a->workspace)
         return PE_ERR_NULL;
@@ -879,13 +828,13 @@ extern "C" int pe_decode_step(const pe_step_args* a, pe_stream_t stream) {
     // QKV split: the fewest pairs per workgroup that fit q, k and v workgroups into the grid
     const int nqp = a->n_head * (kStepHd / 2), nkp = a->n_kv * (kStepHd / 2);
     int pq = 1;
-    while (pq <= 8 && (nqp + pq - 1) / pq + 2 * ((nkp + pq - 1) / pq) > G) ++pq;
-    if (pq > 8) return PE_ERR_SHAPE;
+    while (pq <= kNT / 64 && (nqp + pq - 1) / pq + 2 * ((nkp + pq - 1) / pq) > G) ++pq;
+    if (pq > kNT / 64) return PE_ERR_SHAPE;
     const int nslices = G / a->n_kv;
     const int ra = (a->hidden + nslices - 1) / nslices;
     const int pf = (a->ffn + G - 1) / G;
     const int pd = (a->hidden + G - 1) / G;
-    if (ra > 32 || pf > 32 || pd > 4 || (a->ffn / 32 + 63) / 64 > 3) return PE_ERR_SHAPE;
+    if (ra > kNT / 16 || pf > kNT / 32 || pd > 4) return PE_ERR_SHAPE;
     StepParams P{};
     P.layers = reinterpret_cast<const StepLayer*>(a->layers_dev);
     P.n_layers = a->n_layers;
@@ -925,24 +874,15 @@ extern "C" int pe_decode_step(const pe_step_args* a, pe_stream_t stream) {
     P.pd = pd;
     P.pl = (int)((a->vocab + G - 1) / G);
     hipStream_t s = (hipStream_t)stream;
-    const int upl = (a->ffn / 32 + 63) / 64;
     // more than half of a CU's LDS per workgroup: no two workgroups share a CU
     const size_t lds = kStepLdsBytes;
-    static std::atomic<int> lds_set[5];
-    auto launch = [&](auto kern, int u) -> int {
-        if (!lds_set[u].load(std::memory_order_acquire)) {
-            if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)lds) != hipSuccess)
-                return PE_ERR_LAUNCH;
-            lds_set[u].store(1, std::memory_order_release);
-        }
-        hipLaunchKernelGGL(kern, dim3(G), dim3(kNT), lds, s, P);
-        return launch_status();
-    };
-    switch (upl) {
-        case 1: return launch(k_decode_step<1>, 1);
-        case 2: return launch(k_decode_step<2>, 2);
-        case 3: return launch(k_decode_step<3>, 3);
-        default: return PE_ERR_SHAPE;
+    static std::atomic<int> lds_set{0};
+    if (!lds_set.load(std::memory_order_acquire)) {
+        if (hipFuncSetAttribute((const void*)k_decode_step, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds) != hipSuccess)
+            return PE_ERR_LAUNCH;
+        lds_set.store(1, std::memory_order_release);
     }
+    hipLaunchKernelGGL(k_decode_step, dim3(G), dim3(kNT), lds, s, P);
+    return launch_status();
 }

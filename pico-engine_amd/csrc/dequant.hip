@@ -147,7 +147,7 @@ extern "C" int pe_dequant_tiled(int type, const void* tiled, float* out, int64_t
     if (n_rows <= 0 || k <= 0 || k % row_multiple(type)) return PE_ERR_SHAPE;
     if (!tiled || !out) return PE_ERR_NULL;
     if (!aligned(tiled, 16) || !aligned(out, 4)) return PE_ERR_ALIGN;
-    Tiled t{(const uint8_t*)tiled, n_rows, k / block_elems(type)};
+    const Tiled t = make_tiled(tiled, n_rows, k / block_elems(type));
     const int grid = grid_for(n_rows * (k / 32), 256);
     hipStream_t s = (hipStream_t)stream;
     switch (type) {
@@ -167,7 +167,7 @@ extern "C" int pe_dequant_tiled_f16(int type, const void* tiled, void* out, int6
     if (n_rows <= 0 || k <= 0 || k % row_multiple(type)) return PE_ERR_SHAPE;
     if (!tiled || !out) return PE_ERR_NULL;
     if (!aligned(tiled, 16) || !aligned(out, 2)) return PE_ERR_ALIGN;
-    Tiled t{(const uint8_t*)tiled, n_rows, k / block_elems(type)};
+    const Tiled t = make_tiled(tiled, n_rows, k / block_elems(type));
     const int grid = grid_for(n_rows * (k / 32), 256);
     hipStream_t s = (hipStream_t)stream;
     _Float16* o = (_Float16*)out;

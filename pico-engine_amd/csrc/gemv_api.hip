@@ -44,7 +44,7 @@ extern "C" int pe_qgemv(int type, const void* w, int64_t n_rows, int64_t k, cons
     if (!x || !y) return PE_ERR_NULL;
     if (!aligned(x, 16) || !aligned(y, 4) || !aligned(residual, 4) || !aligned(bias, 4))
         return PE_ERR_ALIGN;
-    GemvArgs a{Tiled{(const uint8_t*)w, n_rows, k / block_elems(type)},
+    GemvArgs a{make_tiled(w, n_rows, k / block_elems(type)),
                n_rows, k, x, nullptr, 0.f, residual, bias, y, 0, layout};
     return dispatch_gemv(type, a, false, kModePlain, (hipStream_t)stream);
 }
@@ -57,7 +57,7 @@ extern "C" int pe_qgemv_rmsnorm(int type, const void* w, int64_t n_rows, int64_t
     if ((st = check_layout(layout, n_rows))) return st;
     if (!x || !norm_w || !y) return PE_ERR_NULL;
     if (!aligned(x, 16) || !aligned(norm_w, 16) || !aligned(y, 4)) return PE_ERR_ALIGN;
-    GemvArgs a{Tiled{(const uint8_t*)w, n_rows, k / block_elems(type)},
+    GemvArgs a{make_tiled(w, n_rows, k / block_elems(type)),
                n_rows, k, x, norm_w, eps, nullptr, nullptr, y, 0, layout};
     return dispatch_gemv(type, a, true, kModePlain, (hipStream_t)stream);
 }
@@ -70,7 +70,7 @@ extern "C" int pe_qgemv_rmsnorm_silu(int type, const void* w, int64_t ffn, int64
     if ((st = check_layout(layout, ffn))) return st;
     if (!x || !act) return PE_ERR_NULL;
     if (!aligned(x, 16) || !aligned(norm_w, 16) || !aligned(act, 4)) return PE_ERR_ALIGN;
-    GemvArgs a{Tiled{(const uint8_t*)w, 2 * ffn, k / block_elems(type)},
+    GemvArgs a{make_tiled(w, 2 * ffn, k / block_elems(type)),
                ffn, k, x, norm_w, eps, nullptr, nullptr, act, ffn, layout};
     return dispatch_gemv(type, a, norm_w != nullptr, kModeSilu, (hipStream_t)stream);
 }
@@ -88,7 +88,7 @@ extern "C" int pe_qgemv_sum_rmsnorm_silu(int type, const void* w, int64_t ffn, i
     if (!aligned(x, 16) || !aligned(parts, 16) || !aligned(norm_w, 16) || !aligned(act, 4) ||
         !aligned(x_sum, 16))
         return PE_ERR_ALIGN;
-    GemvArgs a{Tiled{(const uint8_t*)w, 2 * ffn, k / block_elems(type)},
+    GemvArgs a{make_tiled(w, 2 * ffn, k / block_elems(type)),
                ffn, k, x, norm_w, eps, nullptr, nullptr, act, ffn, layout};
     a.parts = n_parts ? parts : x;  // read (never added) by the early part loads
     a.n_parts = n_parts;
@@ -109,7 +109,7 @@ extern "C" int pe_qgemm(int type, const void* w, int64_t n_rows, int64_t k, cons
     if (!aligned(x, 16) || x_stride % 4 || !aligned(y, 4) || !aligned(residual, 4) ||
         !aligned(bias, 4))
         return PE_ERR_ALIGN;
-    GemmArgs a{Tiled{(const uint8_t*)w, n_rows, k / block_elems(type)},
+    GemmArgs a{make_tiled(w, n_rows, k / block_elems(type)),
                n_rows, k, m, x, x_stride, bias, residual, res_stride, y, y_stride};
     hipStream_t s = (hipStream_t)stream;
     switch (type) {
@@ -142,7 +142,7 @@ extern "C" int pe_qgemv_rmsnorm_argmax(int type, const void* w, int64_t n_rows, 
         !aligned(log, 8) || !aligned(workspace, 256))
         return PE_ERR_ALIGN;
     if (workspace_bytes < argmax_ws_bytes(n_rows)) return PE_ERR_SPACE;
-    GemvArgs a{Tiled{(const uint8_t*)w, n_rows, k / block_elems(type)},
+    GemvArgs a{make_tiled(w, n_rows, k / block_elems(type)),
                n_rows, k, x, norm_w, eps, nullptr, nullptr, y, 0, layout,
                (uint8_t*)workspace, state, log, log ? log_cap : 0};
     return dispatch_gemv(type, a, true, kModeArgmax, (hipStream_t)stream);

@@ -8,6 +8,9 @@
 #include "pico_hip.h"
 
 #define PE_DEV __device__ __forceinline__
+// Global-memory address space: loads through such pointers are global (not flat) loads even
+// when the pointer value was itself read from memory.
+#define PE_GLOBAL __attribute__((address_space(1)))
 
 namespace pe {
 
@@ -161,10 +164,23 @@ PE_DEV void k4_scale_min(const uint8_t* s, int j, int& sc, int& mn) {
 // that one lane decodes at a time; units per row = k / 32 for every format, so the activation
 // layout in registers is the same whatever the mix of formats.
 struct Tiled {
-    const uint8_t* base;
+    const PE_GLOBAL uint8_t* base;
     int64_t nrows;  // rows of the whole tiled tensor (planes span all rows)
     int64_t nb;     // blocks per row
 };
+
+// A tiled tensor view of a (global) device buffer.
+inline __host__ __device__ Tiled make_tiled(const void* base, int64_t nrows, int64_t nb) {
+    return Tiled{(const PE_GLOBAL uint8_t*)base, nrows, nb};
+}
+
+// 16-byte load from global memory (a clang vector type: HIP's int4 class cannot be assigned
+// from an address-space-qualified reference).
+PE_DEV int4 ld16(const PE_GLOBAL uint8_t* p) {
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    const v4i v = *reinterpret_cast<const PE_GLOBAL v4i*>(p);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
 
 template <int T>
 struct Fmt;
@@ -179,10 +195,9 @@ struct Fmt<PE_TYPE_Q8_0> {
     };
     static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
         const int64_t blk = row * t.nb + u;
-        const int4* q = reinterpret_cast<const int4*>(t.base + blk * 32);
-        r.a = q[0];
-        r.b = q[1];
-        r.d = reinterpret_cast<const uint16_t*>(t.base + t.nrows * t.nb * 32)[blk];
+        r.a = ld16(t.base + blk * 32);
+        r.b = ld16(t.base + blk * 32 + 16);
+        r.d = reinterpret_cast<const PE_GLOBAL uint16_t*>(t.base + t.nrows * t.nb * 32)[blk];
     }
     static PE_DEV int code(const Raw& r, int i) {
         const int4& v = i < 16 ? r.a : r.b;
@@ -215,9 +230,9 @@ struct Fmt<PE_TYPE_Q5_0> {
     static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
         const int64_t blk = row * t.nb + u;
         const int64_t nblk = t.nrows * t.nb;
-        r.qs = *reinterpret_cast<const int4*>(t.base + blk * 16);
-        r.qh = reinterpret_cast<const uint32_t*>(t.base + nblk * 16)[blk];
-        r.d = reinterpret_cast<const uint16_t*>(t.base + nblk * 20)[blk];
+        r.qs = ld16(t.base + blk * 16);
+        r.qh = reinterpret_cast<const PE_GLOBAL uint32_t*>(t.base + nblk * 16)[blk];
+        r.d = reinterpret_cast<const PE_GLOBAL uint16_t*>(t.base + nblk * 20)[blk];
     }
     // 5-bit code of element e (0..31): nibble of qs[e % 16] (low for e < 16), 5th bit = qh bit e
     static PE_DEV int code(const Raw& r, int e) {
@@ -261,10 +276,10 @@ struct Fmt<PE_TYPE_Q4_K> {
     static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
         const int64_t blk = row * t.nb + (u >> 3);
         const int j = u & 7;
-        const int4* q = reinterpret_cast<const int4*>(t.base + blk * 128 + 32 * (j >> 1));
-        r.lo = q[0];
-        r.hi = q[1];
-        r.head = *reinterpret_cast<const int4*>(t.base + t.nrows * t.nb * 128 + blk * 16);
+        const PE_GLOBAL uint8_t* q = t.base + blk * 128 + 32 * (j >> 1);
+        r.lo = ld16(q);
+        r.hi = ld16(q + 16);
+        r.head = ld16(t.base + t.nrows * t.nb * 128 + blk * 16);
         r.sub = j;
     }
     // 6-bit scale and min of sub-block j (the packing of k4_scale_min): bytes j%4 of the three
@@ -329,14 +344,14 @@ struct Fmt<PE_TYPE_Q6_K> {
         const int64_t blk = row * t.nb + (u >> 3);
         const int64_t nblk = t.nrows * t.nb;
         const int hf = (u & 7) >> 2, q = u & 3;
-        const int4* L = reinterpret_cast<const int4*>(t.base + blk * 128 + 64 * hf + 32 * (q & 1));
-        const int4* H = reinterpret_cast<const int4*>(t.base + nblk * 128 + blk * 64 + 32 * hf);
-        r.l0 = L[0];
-        r.l1 = L[1];
-        r.h0 = H[0];
-        r.h1 = H[1];
-        r.sc = reinterpret_cast<const uint16_t*>(t.base + nblk * 192 + blk * 16)[4 * hf + q];
-        r.d = reinterpret_cast<const uint16_t*>(t.base + nblk * 208)[blk];
+        const PE_GLOBAL uint8_t* L = t.base + blk * 128 + 64 * hf + 32 * (q & 1);
+        const PE_GLOBAL uint8_t* H = t.base + nblk * 128 + blk * 64 + 32 * hf;
+        r.l0 = ld16(L);
+        r.l1 = ld16(L + 16);
+        r.h0 = ld16(H);
+        r.h1 = ld16(H + 16);
+        r.sc = reinterpret_cast<const PE_GLOBAL uint16_t*>(t.base + nblk * 192 + blk * 16)[4 * hf + q];
+        r.d = reinterpret_cast<const PE_GLOBAL uint16_t*>(t.base + nblk * 208)[blk];
         r.q = q;
     }
     static PE_DEV int code(const Raw& r, int l) {
@@ -389,9 +404,9 @@ struct Fmt<PE_TYPE_F16> {
         int4 v[4];
     };
     static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
-        const int4* p = reinterpret_cast<const int4*>(t.base + (row * t.nb + 32 * (int64_t)u) * 2);
+        const PE_GLOBAL uint8_t* p = t.base + (row * t.nb + 32 * (int64_t)u) * 2;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) r.v[i] = p[i];
+        for (int i = 0; i < 4; ++i) r.v[i] = ld16(p + 16 * i);
     }
     // exact conversions (denormals preserved), fp32 products
     static PE_DEV float dot(const Raw& r, const float* x, const UnitSums&) {
@@ -421,9 +436,9 @@ struct Fmt<PE_TYPE_F32> {
         int4 v[8];
     };
     static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
-        const int4* p = reinterpret_cast<const int4*>(t.base + (row * t.nb + 32 * (int64_t)u) * 4);
+        const PE_GLOBAL uint8_t* p = t.base + (row * t.nb + 32 * (int64_t)u) * 4;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) r.v[i] = p[i];
+        for (int i = 0; i < 8; ++i) r.v[i] = ld16(p + 16 * i);
     }
     static PE_DEV float dot(const Raw& r, const float* x, const UnitSums&) {
         float acc = 0.f;

@@ -30,7 +30,7 @@ PE_DEV void qkv_task(const QkvParams& P, int64_t task, int glane, float* lds4, f
     const void* w = SEG == 0 ? a.w_q : SEG == 1 ? a.w_k : a.w_v;
     const float* b = SEG == 0 ? a.b_q : SEG == 1 ? a.b_k : a.b_v;
     const int64_t seg_rows = (SEG == 0 ? a.n_head : a.n_kv) * (int64_t)hd;
-    const Tiled t{(const uint8_t*)w, seg_rows, P.k / (int64_t)Fmt<T>::QK};
+    const Tiled t = make_tiled(w, seg_rows, P.k / (int64_t)Fmt<T>::QK);
 
     typename Fmt<T>::Raw p[UPL], q[UPL];
     float b1 = 0.f, b2 = 0.f, c = 1.f, sn = 0.f;
