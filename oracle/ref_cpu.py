@@ -162,8 +162,16 @@ def rope_cpu(x, cos, sin):
 class RefModel:
     """The reference's dense forward on the CPU, from a GGUF file."""
 
-    def __init__(self, path: str | Path, unpack_quant: bool = True):
+    def __init__(self, path: str | Path, unpack_quant: bool = True, dequantize=None,
+                 device: str | torch.device = "cpu"):
+        """``dequantize(ggml_type, raw_bytes, n) -> fp32 tensor`` and ``device`` replace the
+        numpy dequantizer and the CPU for models whose fp32 weights are too large for a quick
+        CPU run (7B): the same forward then runs on torch's own ops on ``device``, over
+        weights dequantized by the caller (use unpack_quant=False there: every matrix is then
+        multiplied as fp32 dequantized weights, which the integer GEMV forms equal up to
+        rounding)."""
         meta, tensors = read_gguf(path)
+        self.device = torch.device(device)
         arch = meta["general.architecture"]
         n_kv = int(meta[f"{arch}.attention.head_count_kv"])
         self.cfg = c = RefConfig(
@@ -182,13 +190,15 @@ class RefModel:
         self.w = {}
         for name, (shape, gt, raw) in tensors.items():
             n = int(np.prod(shape))
-            self.w[name] = torch.from_numpy(dq.dequantize(gt, raw, n).reshape(tuple(reversed(shape))))
+            dense = (torch.from_numpy(dq.dequantize(gt, raw, n)) if dequantize is None
+                     else dequantize(gt, raw, n))
+            self.w[name] = dense.reshape(tuple(reversed(shape))).to(self.device)
         self.types = {name: gt for name, (shape, gt, raw) in tensors.items()}
         self.raw = tensors
         inv_freq = 1.0 / (c.rope_base ** (torch.arange(0, c.head_dim, 2) / c.head_dim))
         pos = torch.arange(c.context_len, dtype=torch.float32)
         ang = pos[:, None] * inv_freq[None, :]
-        self.cos, self.sin = ang.cos(), ang.sin()
+        self.cos, self.sin = ang.cos().to(self.device), ang.sin().to(self.device)
         self.qkv_w, self.qkv_b, self.gu_w = [], [], []
         for i in range(c.n_layers):
             p = f"blk.{i}."
@@ -223,8 +233,8 @@ class RefModel:
 
     def empty_cache(self, capacity: int):
         c = self.cfg
-        return [(torch.zeros(c.n_kv, capacity, c.head_dim), torch.zeros(c.n_kv, capacity, c.head_dim))
-                for _ in range(c.n_layers)]
+        z = lambda: torch.zeros(c.n_kv, capacity, c.head_dim, device=self.device)
+        return [(z(), z()) for _ in range(c.n_layers)]
 
     @torch.inference_mode()
     def forward(self, ids: torch.Tensor, positions: torch.Tensor, cache) -> torch.Tensor:

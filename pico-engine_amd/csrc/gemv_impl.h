@@ -872,7 +872,9 @@ int launch_qgemv_mode(const GemvArgs& a, hipStream_t s) {
         const int gpb = kGemvThreads / sh.gs;
         const int64_t natural = (a.n_tasks + gpb - 1) / gpb;
         loop = natural > 2 * kLoopMinBlocks || (natural > kLoopMinBlocks && a.k / gpb >= 1024);
-        if (loop && sh.gs == 128 && sh.upl == 1) {
+        // not the normed plain GEMV (the LM head without a greedy pick): it keeps the argmax
+        // launch's lane groups, so that both give the same logits bit for bit
+        if (loop && sh.gs == 128 && sh.upl == 1 && !(NORM && MODE == kModePlain)) {
             launch_qgemv_shape<T, 64, 2, NORM, MODE>(a, s, true);
             return launch_status();
         }

@@ -483,8 +483,9 @@ def _const_rows_q8(vals, k):
     return quantize(dq.Q8_0, W)
 
 
+# (Q8_0, 3584, 20000): rows of 112 units on a launch large enough for the looped form
 @pytest.mark.parametrize("t,k,n", [(dq.Q8_0, 896, 151936), (dq.Q5_0, 896, 1000), (dq.Q6_K, 4864, 300),
-                                   (dq.Q8_0, 896, 1)])
+                                   (dq.Q8_0, 896, 1), (dq.Q8_0, 3584, 20000)])
 def test_argmax_matches_torch_argmax(K, t, k, n):
     raw = quantized_normal(t, n, k, seed=n + t)
     w = qweight(K, t, raw, n, k)
