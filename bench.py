@@ -80,43 +80,93 @@ def kernel_launchers(eng, which: str):
     m, cfg = eng.model, eng.cfg
     L0 = m.layers[0]
     XU, YU = K.LAYOUT_X_UT, K.LAYOUT_Y_UT
+    tn = lambda w: K.TYPE_NAMES.get(w.ggml_type, w.ggml_type)
+    hd, nh, nkv, h = cfg.head_dim, cfg.n_head, cfg.n_kv_head, cfg.hidden
     # the decode step's own launch configuration: activations in the unit-transposed layout
-    x = torch.randn(cfg.hidden, device=eng.device)
+    x = torch.randn(h, device=eng.device)
     if which == "gate_up":
         # as the decode step runs it: x plus the attention block's n_kv o-projection parts,
         # RMSNorm, [gate; up] pair, SiLU; the sum is stored for the next residual
-        w = L0.w_gate_up
-        parts = torch.randn(cfg.n_kv_head, cfg.hidden, device=eng.device) * 0.1
-        name = (f"k_qgemv (Q5_0, x + {cfg.n_kv_head} o-proj parts, rmsnorm+SiLU pair) gate/up "
-                f"{cfg.hidden}->2x{cfg.ffn_dim}")
-        fn = lambda ww: K.qgemv_sum_norm_silu(x, parts, L0.ffn_norm_ut, ww, cfg.eps, layout=XU | YU)
-        io = 4 * (cfg.hidden * (3 + cfg.n_kv_head) + cfg.ffn_dim)
+        ws = (L0.w_gate_up,)
+        parts = torch.randn(nkv, h, device=eng.device) * 0.1
+        name = (f"k_qgemv (Q5_0, x + {nkv} o-proj parts, rmsnorm+SiLU pair) gate/up "
+                f"{h}->2x{cfg.ffn_dim}")
+        fn = lambda w: K.qgemv_sum_norm_silu(x, parts, L0.ffn_norm_ut, w, cfg.eps, layout=XU | YU)
+        io = 4 * (h * (3 + nkv) + cfg.ffn_dim)
     elif which == "gate_up_norm":
         # the decode step without attn_gproj (head_dim 128: the 7B): RMSNorm, [gate; up], SiLU
-        w = L0.w_gate_up
-        name = (f"k_qgemv ({K.TYPE_NAMES.get(w.ggml_type, w.ggml_type)}, rmsnorm+SiLU pair) gate/up "
-                f"{cfg.hidden}->2x{cfg.ffn_dim}")
-        fn = lambda ww: K.qgemv_norm_silu(x, L0.ffn_norm_ut, ww, cfg.eps, layout=XU | YU)
-        io = 4 * (cfg.hidden * 2 + cfg.ffn_dim)
+        ws = (L0.w_gate_up,)
+        name = f"k_qgemv ({tn(ws[0])}, rmsnorm+SiLU pair) gate/up {h}->2x{cfg.ffn_dim}"
+        fn = lambda w: K.qgemv_norm_silu(x, L0.ffn_norm_ut, w, cfg.eps, layout=XU | YU)
+        io = 4 * (h * 2 + cfg.ffn_dim)
     elif which == "lm_head":
-        w = m.output
-        name = f"k_qgemv (Q8_0, rmsnorm, device greedy pick) LM head {cfg.hidden}->{cfg.vocab_size}"
+        ws = (m.output,)
+        name = f"k_qgemv ({tn(ws[0])}, rmsnorm, device greedy pick) LM head {h}->{cfg.vocab_size}"
         g = K.GreedyState(m.output.n, 1, eng.device)
-        fn = lambda ww: K.qgemv_norm_argmax(x, m.output_norm_ut, ww, cfg.eps, g, layout=XU)
-        io = 4 * (cfg.hidden * 2 + cfg.vocab_size)
+        fn = lambda w: K.qgemv_norm_argmax(x, m.output_norm_ut, w, cfg.eps, g, layout=XU)
+        io = 4 * (h * 2 + cfg.vocab_size)
     elif which in ("down_q6k", "down_q4k"):
-        li = 0 if which == "down_q6k" or len(m.layers) < 2 else 1
-        w = m.layers[li].w_down
-        name = (f"k_qgemv ({K.TYPE_NAMES.get(w.ggml_type, w.ggml_type)}, +residual) ffn_down "
-                f"{cfg.ffn_dim}->{cfg.hidden}")
+        from pico_hip.dequant import GGML_Q4_K, GGML_Q6_K
+        want = GGML_Q6_K if which == "down_q6k" else GGML_Q4_K
+        li = next((i for i, Lr in enumerate(m.layers) if Lr.w_down.ggml_type == want), 0)
+        ws = (m.layers[li].w_down,)
+        name = f"k_qgemv ({tn(ws[0])}, +residual) ffn_down {cfg.ffn_dim}->{h}"
         a = torch.randn(cfg.ffn_dim, device=eng.device)
-        fn = lambda ww: K.qgemv(a, ww, residual=x, layout=XU | YU)
-        io = 4 * (cfg.ffn_dim + 2 * cfg.hidden)
+        fn = lambda w: K.qgemv(a, w, residual=x, layout=XU | YU)
+        io = 4 * (cfg.ffn_dim + 2 * h)
+    elif which == "qkv":
+        # RMSNorm, [Wq; Wk; Wv] + bias, RoPE, K/V row written into the cache at position 40
+        ws = (L0.wq, L0.wk, L0.wv)
+        cap = 64
+        kc = torch.zeros(nkv, cap, hd, device=eng.device)
+        vc = torch.zeros(nkv, cap, hd, device=eng.device)
+        pos = torch.tensor([40], device=eng.device)
+        name = (f"k_qkv ({'/'.join(tn(w) for w in ws)}, rmsnorm, bias, RoPE, cache write) "
+                f"{h}->{nh}x{hd}+2x{nkv}x{hd}")
+        fn = lambda wq, wk, wv: K.qkv_rmsnorm_rope(x, L0.attn_norm_ut, cfg.eps, wq, wk, wv, L0.bq, L0.bk,
+                                                   L0.bv, m.cos, m.sin, pos, kc, vc, nh, layout=XU)
+        io = 4 * (2 * h + (nh + 2 * nkv) * hd + hd + nh * hd + 2 * nkv * hd)
+    elif which == "attn_gproj":
+        # attention over S = 45 cached positions (config 0's mean context: 13-token prompt, 64
+        # decode steps) times each kv group's columns of Wo
+        ws = (L0.wo,)
+        S, cap = 45, 80
+        q = torch.randn(nh, hd, device=eng.device)
+        kc = torch.randn(nkv, cap, hd, device=eng.device)
+        vc = torch.randn(nkv, cap, hd, device=eng.device)
+        name = f"k_attn_gproj ({tn(ws[0])} o-proj, S={S}, {nh}/{nkv} heads) {nh * hd}->{nkv}x{h}"
+        fn = lambda w: K.attn_gproj(q, kc, vc, w, S=S, layout=YU)
+        io = 4 * (nh * hd + 2 * nkv * S * hd + nkv * h)
+    elif which == "oproj":
+        # the o-projection with the residual where attn_gproj does not apply (head_dim 128)
+        ws = (L0.wo,)
+        a = torch.randn(nh * hd, device=eng.device)
+        name = f"k_qgemv ({tn(ws[0])}, +residual) o-proj {nh * hd}->{h}"
+        fn = lambda w: K.qgemv(a, w, residual=x, layout=XU | YU)
+        io = 4 * (nh * hd + 2 * h)
     else:
         raise SystemExit(f"unknown --kernel {which}")
-    copies = max(1, -(-(1 << 30) // w.nbytes))
-    ws = [w] + [K.QWeight(w.data.clone(), w.ggml_type, w.n, w.k) for _ in range(copies - 1)]
-    return [(lambda ww=ww: fn(ww)) for ww in ws], w.nbytes + io, name
+    nbytes = sum(w.nbytes for w in ws)
+    copies = max(1, -(-(1 << 30) // nbytes))
+    sets = [ws] + [tuple(K.QWeight(w.data.clone(), w.ggml_type, w.n, w.k) for w in ws)
+                   for _ in range(copies - 1)]
+    return [(lambda st=st: fn(*st)) for st in sets], nbytes + io, name
+
+
+def kernel_only(eng, args) -> None:
+    """--kernel-only: time --kernel alone (launches one by one, as rocprofv3 --pmc counts
+    them), then four copies of a 1 GiB buffer: the counter calibration (each reads and writes
+    exactly 1 GiB)."""
+    import torch
+    launchers, alg_bytes, kname = kernel_launchers(eng, args.kernel)
+    avg_us = time_kernel(launchers, args.kernel_iters, graph=False)
+    src = torch.ones(1 << 28, device=eng.device)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"kernel": kname, "avg_launch_us": avg_us, "algorithmic_bytes": alg_bytes,
+                      "calibration_copy_bytes": src.numel() * 4}), flush=True)
 
 
 def time_kernel(launchers, iters: int, graph: bool = True) -> float:
@@ -354,6 +404,9 @@ def config4(args) -> None:
     t0 = time.time()
     eng = Engine(path, device="cuda:0")
     log(f"engine loaded in {time.time() - t0:.1f}s")
+    if args.kernel_only:
+        kernel_only(eng, args)
+        return
     n_prompt, steps = 128, 256
     # the 128-token prompt is prefilled on the matrix cores (fp16 operands, fp32 accumulation:
     # the reference's CUDA autocast prefill, model.py:147-151); the fp32 small-M path re-reads
@@ -405,14 +458,14 @@ def synth_sha(path):
     return synth.sha256(path)
 
 
-def traffic_from_profiles(kernel: str):
-    p = ROOT / "profiles" / f"traffic_{kernel}.json"
-    if p.exists():
-        try:
-            return json.loads(p.read_text()).get("bytes_per_launch")
-        except (ValueError, OSError):
-            return None
-    return None
+def traffic_from_profiles(kernel: str, config: int = 0):
+    """HBM bytes per launch of ``kernel`` from the committed counter summary
+    (profiles/traffic_decode_kernels.json: reads by request size + WRITE_SIZE), or None."""
+    p = ROOT / "profiles" / "traffic_decode_kernels.json"
+    try:
+        return json.loads(p.read_text())[f"config{config}_{kernel}"]["bytes_per_launch"]
+    except (ValueError, OSError, KeyError):
+        return None
 
 
 def cpu_baseline(path, prompt, budget_s: float):
@@ -445,7 +498,9 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=64, help="timed decode tokens")
     ap.add_argument("--warmup", type=int, default=2, help="untimed full runs before the timed one")
     ap.add_argument("--reps", type=int, default=5, help="extra timed runs for median/p10/p90")
-    ap.add_argument("--kernel", default="gate_up", help="dominant kernel for the roofline object")
+    ap.add_argument("--kernel", default="gate_up",
+                    help="dominant kernel for the roofline object, or the kernel --kernel-only times: "
+                         "gate_up, gate_up_norm, lm_head, down_q6k, down_q4k, qkv, attn_gproj, oproj")
     ap.add_argument("--kernel-iters", type=int, default=400)
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline decode")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -488,15 +543,7 @@ def main() -> None:
         return
 
     if args.kernel_only:
-        launchers, alg_bytes, kname = kernel_launchers(eng, args.kernel)
-        avg_us = time_kernel(launchers, args.kernel_iters, graph=False)
-        src = torch.ones(1 << 28, device=eng.device)   # 1 GiB: the counter calibration copy
-        dst = torch.empty_like(src)
-        for _ in range(4):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"kernel": kname, "avg_launch_us": avg_us, "algorithmic_bytes": alg_bytes,
-                          "calibration_copy_bytes": src.numel() * 4}), flush=True)
+        kernel_only(eng, args)
         return
 
     for _ in range(args.warmup):

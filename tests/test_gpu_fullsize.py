@@ -2,7 +2,8 @@
 
 Config 3 (the config-0 model, 8192-token prompt, decode at context 8192): causal flash
 attention over 8192 positions against float64 on sampled query rows; the model's 8192-token
-matrix-core prefill and eight decode steps after it against the CPU oracle.
+matrix-core prefill and eight decode steps after it against the CPU oracle. The same model
+(config 0) through 24 decode steps fed random ids, against the CPU oracle.
 
 Config 4 (Qwen2.5-7B architecture): the decode GEMVs at their full shapes against float64 on
 sampled rows (gate/up 3584 -> 2 x 18944 Q4_K with SiLU, ffn_down 18944 -> 3584 Q6_K with the
@@ -89,17 +90,47 @@ def test_flash_prefill_full_length_sampled_rows(K, L, pos0):
 
 # ---- config 3: the config-0 model at context 8192 -----------------------------------------
 
-def test_config3_prefill_8192_and_decode_match_oracle(model_dir):
-    """The config-0 model (seed 0) with an 8192-token random prompt: the matrix-core prefill's
-    logits and the K/V rows it leaves in every layer (sampled positions) against the CPU
-    oracle's fp32 prefill, then eight graph-replayed decode steps at context 8192, fed the
-    oracle's greedy tokens, against the oracle's decode steps on its own cache."""
+@pytest.fixture(scope="module")
+def cfg0(model_dir):
+    """The config-0 model (Qwen2.5-0.5B architecture, seed 0): its arch, Engine and CPU oracle."""
     from pico_hip import synth
     from pico_hip.engine import Engine
     from oracle.ref_cpu import RefModel
     arch = synth.ARCHES["qwen2.5-0.5b"]
     path = synth.cached(arch, seed=0, cache_dir=model_dir)
-    eng = Engine(path)
+    return arch, Engine(path), RefModel(path)
+
+
+def test_config0_decode_teacher_forced_matches_oracle(cfg0):
+    """The config-0 model at full size: a 13-token prompt, then 24 graph-replayed decode steps
+    fed seeded random ids (its own greedy picks settle into a two-token cycle, which would
+    exercise two embedding and LM-head rows), including the first and last vocabulary rows:
+    every step's logits against the CPU oracle, and the device pick equal to the argmax."""
+    arch, eng, ref = cfg0
+    rng = np.random.default_rng(24)
+    prompt = rng.integers(0, arch.vocab, size=13)
+    feed = [0, arch.vocab - 1] + rng.integers(0, arch.vocab, size=22).tolist()
+    cap = len(prompt) + len(feed)
+    cache, rcache = eng._empty_cache(cap), ref.empty_cache(cap)
+    graph = eng._build_decode_graph(cache)
+    assert graph is not None
+    lg = eng.model.forward(torch.from_numpy(prompt).to(DEV), torch.arange(13, device=DEV), cache)
+    rl = ref.forward(torch.from_numpy(prompt), torch.arange(13), rcache)
+    assert rel_err(lg.cpu().numpy(), rl.numpy()) < TOL
+    for s, tok in enumerate(feed):
+        pos = 13 + s
+        got = eng._decode_step(tok, pos, cache, graph).cpu().numpy()
+        assert int(eng._greedy.token) == int(np.argmax(got)), s
+        rl = ref.forward(torch.tensor([tok]), torch.tensor([pos]), rcache)
+        assert rel_err(got, rl.numpy()) < TOL, s
+
+
+def test_config3_prefill_8192_and_decode_match_oracle(cfg0):
+    """The config-0 model (seed 0) with an 8192-token random prompt: the matrix-core prefill's
+    logits and the K/V rows it leaves in every layer (sampled positions) against the CPU
+    oracle's fp32 prefill, then eight graph-replayed decode steps at context 8192, fed the
+    oracle's greedy tokens, against the oracle's decode steps on its own cache."""
+    arch, eng, ref = cfg0
     L, steps = 8192, 8
     assert eng.model.prefill_f16_min_tokens is not None and eng.model.prefill_f16_min_tokens <= L
     ids = np.random.default_rng(8192).integers(0, arch.vocab, size=L)
@@ -109,8 +140,6 @@ def test_config3_prefill_8192_and_decode_match_oracle(model_dir):
     assert graph is not None
     lg = eng.model.forward(torch.from_numpy(ids).to(DEV), torch.arange(L, device=DEV), cache)
     lg = lg.cpu().numpy()
-
-    ref = RefModel(path)
     rcache = ref.empty_cache(cap)
     rl = ref.forward(torch.from_numpy(ids), torch.arange(L), rcache)
     errs = {"prefill_logits": rel_err(lg, rl.numpy())}

@@ -291,6 +291,31 @@ def test_decode_attn_unrounded_and_clamp(K, cap):
     assert np.all(np.isnan(empty))
 
 
+@pytest.mark.parametrize("cap", [100, 1500, 32768])  # single pass / split + merge launch
+def test_decode_attn_fp16_rounding_is_nearest_even(K, cap):
+    """The stored output is the kernel's own unrounded fp32 result converted to fp16 with
+    round-to-nearest-even (Triton's default for acc.to(tl.float16), kernels.py:126; numpy's
+    astype(float16)): fp16 subnormals kept, values past 65504 to infinity. A truncating,
+    flushing or saturating conversion fails this bit for bit."""
+    rng = np.random.default_rng(cap)
+    q = rng.standard_normal((14, 64)).astype(np.float32)
+    k, v = _kv(rng, 2, cap, 64)
+    Q, Kc = torch.from_numpy(q).to(DEV), torch.from_numpy(k).to(DEV)
+    # normal, fp16-subnormal and overflowing outputs (a mean of 3e4 * (3 + N(0,1)) values)
+    for vscale, shift in ((1.0, 0.0), (3e-6, 0.0), (3e4, 3.0)):
+        Vc = torch.from_numpy((v + np.float32(shift)) * np.float32(vscale)).to(DEV)
+        u = K.decode_attn(Q, Kc, Vc, S=cap - 3, round_fp16=False).cpu().numpy()
+        r = K.decode_attn(Q, Kc, Vc, S=cap - 3).cpu().numpy()
+        with np.errstate(over="ignore"):
+            want = u.astype(np.float16).astype(np.float32)
+        np.testing.assert_array_equal(r, want)
+        assert not np.array_equal(r, u)
+        if vscale > 1:
+            assert np.isinf(r).any()
+        if vscale < 1:
+            assert (np.abs(r[r != 0]) < 6.1e-5).any()
+
+
 @pytest.mark.parametrize("cap", [200, 300, 1500])  # single pass / split + merge launch
 def test_decode_attn_workspace_reuse_and_graph(K, cap):
     """One workspace across many in-order calls and across graph replays with a device S."""
