@@ -225,7 +225,8 @@ int pe_qkv_rmsnorm_rope(const pe_qkv_args* args, pe_stream_t stream);
 
 /* Single-query GQA attention over a KV cache. Caches of at most 256 positions: one launch,
  * a workgroup per query head. Longer caches: split over 64-position chunks across CUs, then a
- * log-sum-exp merge launch (one workgroup per query head) in a fixed order.
+ * log-sum-exp merge launch (one workgroup per query head) in a fixed order; a chunk's record
+ * is P.V[hd], max, sum and two pad words.
  *   q (n_head, hd); k_cache, v_cache (n_kv, capacity, hd); out (n_head, hd)
  *   valid length S = (len_dev ? *len_dev : 0) + len_add, clamped to [0, capacity];
  *   len_dtype: 0 = len_dev unused, 1 = int32, 2 = int64. Head h reads kv head h / (n_head/n_kv).
@@ -248,7 +249,7 @@ int pe_decode_attn(const float* q, const float* k_cache, const float* v_cache, i
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It allocates
  * nothing and calls no allocating routine. Returns PE_ERR_SPACE when
  * pe_decode_attn_workspace_bytes(n_head, n_kv, head_dim, capacity) exceeds 4 MiB (e.g. more
- * than about 72,000 positions at 14/2 heads, head_dim 64). All calls on one GPU share its
+ * than about 70,000 positions at 14/2 heads, head_dim 64). All calls on one GPU share its
  * scratch array, which keeps the last call's records (nothing in it needs clearing: every
  * record a call reads is written by that call first), so calls that overlap on one GPU race;
  * calls issued in order on one stream do not. The stream must belong to the current device;

@@ -62,6 +62,11 @@ PE_DEV float quad_sum4(float v) {
     return v;
 }
 
+// The chunk record of one head slot: P.V[HD], max, sum and two pad words, so that records are
+// 16-byte aligned for the merge's float4 loads.
+template <int HD>
+constexpr int attn_rec() { return HD + 4; }
+
 // One 64-position chunk of one kv head for all NH head slots (NH >= the group size; slots past
 // the group hold zeros and are not stored). No phase branches on the group size or on the
 // valid length: with branches the compiler waits for each LDS read on its own. Cache rows are
@@ -71,7 +76,7 @@ __global__ __launch_bounds__(256) void k_decode_attn(AttnParams p) {
     constexpr int DQ = HD / 4;          // dims per thread in the score phase (4 threads / position)
     constexpr int PS = 256 / HD;        // position slices in the P.V phase
     constexpr int NPOS = kChunk / PS;   // positions per slice
-    constexpr int REC = HD + 2;         // partial record: m, l, acc[HD]
+    constexpr int REC = attn_rec<HD>();  // partial record: acc[HD], m, l, 2 pad words
     static_assert(NH % 4 == 0 && NPOS % 4 == 0 && DQ % 4 == 0, "tiling");
     __shared__ float4 q4[NH * HD / 4];
     __shared__ float4 sc4[NH][kChunk / 4];
@@ -182,90 +187,112 @@ __global__ __launch_bounds__(256) void k_decode_attn(AttnParams p) {
         float a = 0.f;
 #pragma unroll
         for (int j = 0; j < PS; ++j) a += red[j][g * HD + dd];
-        rec[g * REC + 2 + dd] = a;
+        rec[g * REC + dd] = a;
         if (dd == 0) {
-            rec[g * REC] = ml[2 * g];
-            rec[g * REC + 1] = ml[2 * g + 1];
+            rec[g * REC + HD] = ml[2 * g];
+            rec[g * REC + HD + 1] = ml[2 * g + 1];
         }
     }
 }
 
-// Merge of the split records: one workgroup per query head. Lane group j (kMergeThreads / HD
-// of them) takes records j, j + groups, ... of the valid chunks, then the groups are combined in
-// LDS in a fixed order. Every record load is independent of the others, so a group's loads are
-// in flight together instead of forming a chain of dependent round trips.
-constexpr int kMergeThreads = 1024;
+// Merge of the chunk records: one workgroup of NT threads per query head. Lane group j (a
+// float4 of dims per lane, HD / 4 lanes) takes records j, j + groups, ... of the valid chunks,
+// every load of a batch of kMergeBatch records in flight together (one batch covers
+// groups * kMergeBatch chunks: with 1024 threads 32768 positions at head_dim 64). The groups
+// then combine at their common maximum: the groups of a wave by lane swaps, the waves in wave
+// order. Up to kMergeSmall chunks run 256 threads (fewer waves to start and to combine).
 constexpr int kMergeBatch = 8;
+constexpr int kMergeSmall = 128;
 
-template <int HD>
-__global__ __launch_bounds__(kMergeThreads) void k_decode_attn_merge(AttnParams p) {
-    constexpr int REC = HD + 2;
-    constexpr int NG = kMergeThreads / HD;  // lane groups
-    __shared__ float red[NG][HD];
-    __shared__ float ml[2][NG];
-    const int t = threadIdx.x, dd = t % HD, jg = t / HD;
+template <int HD, int NT>
+__global__ __launch_bounds__(NT) void k_decode_attn_merge(AttnParams p) {
+    constexpr int REC = attn_rec<HD>();
+    constexpr int VQ = HD / 4;
+    constexpr int NG = NT / VQ;     // lane groups
+    constexpr int NW = NT / 64;     // waves
+    __shared__ float4 wa[NW][VQ];
+    __shared__ float wm[NW], wl[NW];
+    const int t = threadIdx.x, c = t % VQ, jg = t / VQ, w = t >> 6;
     const int h = blockIdx.x, G = p.group, kvh = h / G, g = h % G;
-    const int64_t S = valid_len(p);
-    const int nvalid = (int)((S + kChunk - 1) / kChunk);
     const float* base = p.partials + (int64_t)kvh * p.nsplit * G * REC + (int64_t)g * REC;
     const int64_t rstride = (int64_t)G * REC;
     const float NEG_INF = -__builtin_huge_valf();
-    // One pass over the records: batches of kMergeBatch per lane group, every load of a batch
-    // issued before the first use (indices clamped to the last valid record, masked
-    // afterwards); the group keeps a running maximum and rescales its sums when it grows
-    // (one read of each record instead of a max pass and a sum pass).
+    const int64_t S = valid_len(p);
+    const int nvalid = (int)((S + kChunk - 1) / kChunk);
     const int last = nvalid > 0 ? nvalid - 1 : 0;
-    float M = NEG_INF, L = 0.f, A = 0.f;
+    float M = NEG_INF, L = 0.f;
+    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s0 = jg; s0 < nvalid; s0 += NG * kMergeBatch) {
-        float rm[kMergeBatch], rl[kMergeBatch], ra[kMergeBatch];
+        float rm[kMergeBatch], rl[kMergeBatch];
+        float4 ra[kMergeBatch];
 #pragma unroll
         for (int b = 0; b < kMergeBatch; ++b) {
             const int sp = s0 + NG * b;
             const float* r = base + (int64_t)(sp < last ? sp : last) * rstride;
-            rm[b] = r[0];
-            rl[b] = r[1];
-            ra[b] = r[2 + dd];
+            ra[b] = reinterpret_cast<const float4*>(r)[c];
+            const float2 ml = reinterpret_cast<const float2*>(r + HD)[0];
+            rm[b] = ml.x;
+            rl[b] = ml.y;
         }
         float bm = NEG_INF;
 #pragma unroll
         for (int b = 0; b < kMergeBatch; ++b)
             if (s0 + NG * b < nvalid) bm = fmaxf(bm, rm[b]);
         const float Mn = fmaxf(M, bm);
-        const float c = M == NEG_INF ? 0.f : expf(M - Mn);
-        L *= c;
-        A *= c;
+        const float cs = M == NEG_INF ? 0.f : expf(M - Mn);
+        L *= cs;
+        A.x *= cs;
+        A.y *= cs;
+        A.z *= cs;
+        A.w *= cs;
 #pragma unroll
         for (int b = 0; b < kMergeBatch; ++b) {
             if (s0 + NG * b < nvalid) {
                 const float e = expf(rm[b] - Mn);
                 L = fmaf(rl[b], e, L);
-                A = fmaf(ra[b], e, A);
+                A.x = fmaf(ra[b].x, e, A.x);
+                A.y = fmaf(ra[b].y, e, A.y);
+                A.z = fmaf(ra[b].z, e, A.z);
+                A.w = fmaf(ra[b].w, e, A.w);
             }
         }
         M = Mn;
     }
-    // combine the lane groups in group order at the common maximum
-    if (dd == 0) ml[0][jg] = M;
-    __syncthreads();
-    float Mg = ml[0][0];
+    // the groups of this wave (64 / VQ of them, lanes VQ apart) at their common maximum
+    float Mw = M;
+    if constexpr (VQ == 16) Mw = swap16_max(Mw);
+    Mw = swap32_max(Mw);
+    const float cw = M == NEG_INF ? 0.f : expf(M - Mw);
+    float v[5] = {A.x * cw, A.y * cw, A.z * cw, A.w * cw, L * cw};
 #pragma unroll
-    for (int j = 1; j < NG; ++j) Mg = fmaxf(Mg, ml[0][j]);
-    const float cg = M == NEG_INF ? 0.f : expf(M - Mg);
-    L *= cg;
-    A *= cg;
-    red[jg][dd] = A;
-    if (dd == 0) ml[1][jg] = L;
+    for (int i = 0; i < 5; ++i) {
+        if constexpr (VQ == 16) v[i] = swap16_sum(v[i]);
+        v[i] = swap32_sum(v[i]);
+    }
+    if ((t & 63) < VQ) {
+        wa[w][c] = make_float4(v[0], v[1], v[2], v[3]);
+        if (c == 0) {
+            wm[w] = Mw;
+            wl[w] = v[4];
+        }
+    }
     __syncthreads();
-    if (jg == 0) {
-        float a = red[0][dd], l = ml[1][0];
+    // the waves in wave order, one thread per output dim
+    if (t < HD) {
+        float Mg = wm[0];
 #pragma unroll
-        for (int j = 1; j < NG; ++j) {
-            a += red[j][dd];
-            l += ml[1][j];
+        for (int j = 1; j < NW; ++j) Mg = fmaxf(Mg, wm[j]);
+        const float* wf = reinterpret_cast<const float*>(wa);
+        float a = 0.f, l = 0.f;
+#pragma unroll
+        for (int j = 0; j < NW; ++j) {
+            const float cj = wm[j] == NEG_INF ? 0.f : expf(wm[j] - Mg);
+            a = fmaf(wf[j * HD + t], cj, a);
+            l = fmaf(wl[j], cj, l);
         }
         float o = a / l;
         if (p.round_fp16) o = round_to_f16(o);
-        p.out[attn_out_index(p, (int64_t)h * HD + dd, (int64_t)p.n_kv * G * HD)] = o;
+        p.out[attn_out_index(p, (int64_t)h * HD + t, (int64_t)p.n_kv * G * HD)] = o;
     }
 }
 
@@ -466,7 +493,7 @@ extern "C" int64_t pe_decode_attn_workspace_bytes(int n_head, int n_kv, int head
         (head_dim != 64 && head_dim != 128) || capacity <= 0)
         return -PE_ERR_SHAPE;
     const int G = n_head / n_kv;
-    return 256 + (int64_t)n_kv * attn_nsplit(capacity) * G * (head_dim + 2) * 4;
+    return 256 + (int64_t)n_kv * attn_nsplit(capacity) * G * (head_dim + 4) * 4;
 }
 
 // Host validation shared by pe_decode_attn and pe_decode_attn_noalloc (everything but the
@@ -574,11 +601,17 @@ static int launch_decode_attn(const float* q, const float* k_cache, const float*
     if (head_dim == 64) {
         if (g8) hipLaunchKernelGGL((k_decode_attn<64, 8>), grid, dim3(256), 0, s, p);
         else hipLaunchKernelGGL((k_decode_attn<64, 16>), grid, dim3(256), 0, s, p);
-        hipLaunchKernelGGL(k_decode_attn_merge<64>, dim3((unsigned)n_head), dim3(kMergeThreads), 0, s, p);
+        if (p.nsplit <= kMergeSmall)
+            hipLaunchKernelGGL((k_decode_attn_merge<64, 256>), dim3((unsigned)n_head), dim3(256), 0, s, p);
+        else
+            hipLaunchKernelGGL((k_decode_attn_merge<64, 1024>), dim3((unsigned)n_head), dim3(1024), 0, s, p);
     } else {
         if (g8) hipLaunchKernelGGL((k_decode_attn<128, 8>), grid, dim3(256), 0, s, p);
         else hipLaunchKernelGGL((k_decode_attn<128, 16>), grid, dim3(256), 0, s, p);
-        hipLaunchKernelGGL(k_decode_attn_merge<128>, dim3((unsigned)n_head), dim3(kMergeThreads), 0, s, p);
+        if (p.nsplit <= kMergeSmall)
+            hipLaunchKernelGGL((k_decode_attn_merge<128, 256>), dim3((unsigned)n_head), dim3(256), 0, s, p);
+        else
+            hipLaunchKernelGGL((k_decode_attn_merge<128, 1024>), dim3((unsigned)n_head), dim3(1024), 0, s, p);
     }
     return launch_status();
 }
