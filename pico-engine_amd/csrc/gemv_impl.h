@@ -120,9 +120,9 @@ __global__ __launch_bounds__(kPickThreads) void k_argmax_pick(const uint8_t* ws,
     }
 }
 
-// Sum over a group of GS lanes. GS = 128 / 256 spans 2 / 4 waves of a 256-thread block: wave
+// Sum over a group of GS lanes. GS = 128 / 256 spans 2 / 4 waves of the block: wave
 // butterflies, then the wave sums of the group are added in wave order through LDS (every
-// thread of the block must call it; lds4 holds 4 floats).
+// thread of the block must call it; lds4 holds a float per wave of the block).
 template <int GS>
 PE_DEV float gsum(float v, float* lds4) {
     if constexpr (GS <= 64) {
@@ -135,7 +135,8 @@ PE_DEV float gsum(float v, float* lds4) {
         if ((threadIdx.x & 63) == 0) lds4[w] = v;
         __syncthreads();
         if constexpr (GS == 128) return lds4[w & ~1] + lds4[w | 1];
-        return ((lds4[0] + lds4[1]) + lds4[2]) + lds4[3];
+        const int b = w & ~3;  // the group's first wave
+        return ((lds4[b] + lds4[b + 1]) + lds4[b + 2]) + lds4[b + 3];
     }
 }
 
@@ -607,7 +608,10 @@ PE_DEV float stage_activation(const GemvArgs& a, int glane, int units, float (&x
     return finish_activation<NT, GS, UPL, NORM, SUM>(a, glane, units, L, xr, xs, lds4, stage);
 }
 
-constexpr int kGemvThreads = 256;
+#ifndef PE_GEMV_THREADS
+#define PE_GEMV_THREADS 256
+#endif
+constexpr int kGemvThreads = PE_GEMV_THREADS;
 
 // Blocked decode GEMV. A block of kGemvThreads threads owns a chunk of TPG * G consecutive
 // tasks (G = kGemvThreads / GS lane groups; group g takes tasks chunk*CH + i*G + g). Timeline:

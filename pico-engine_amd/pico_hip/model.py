@@ -2,9 +2,11 @@
 
 ``ModelConfig`` and ``Transformer(cfg, weights, device, quant).forward(token_ids, positions,
 cache) -> logits`` keep the reference's signatures (model.py:27-57, :60-62, :128-165).
-A greedy decode step of a model the persistent kernel covers (head_dim 64, hidden <= 1024,
-caches up to 256 positions: the 0.5B family) is one launch, pe_decode_step. Otherwise decode
-(one token) runs four launches per layer plus the embedding row and the LM head:
+With ``use_step_kernel`` set (off by default: measured at parity with the four-launch step,
+526 vs 519 us per token at config 0), a greedy decode step of a model the persistent kernel
+covers (head_dim 64, hidden <= 1024, ffn <= 8192, caches up to 128 positions: the 0.5B
+family) is one launch, pe_decode_step. Otherwise decode (one token) runs four launches per
+layer plus the embedding row and the LM head:
 
   embed_gather                              model.py:152 (Q8_0 row, bit-exact)
   per layer:
