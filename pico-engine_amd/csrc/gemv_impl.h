@@ -299,7 +299,7 @@ PE_DEV float load_activation(const GemvArgs& a, int glane, int units, float (&xr
 // The double-buffered loop (CLAMP) clamps in every group width: a lane-divergent branch
 // around the loads would make the compiler wait for all outstanding loads after it, the
 // prefetched chunk's included.
-template <int T, int GS, int UPL, int R, bool CLAMP = false, int UM = 0>
+template <int T, int GS, int UPL, int R, bool CLAMP = false, int UM = 0, bool NT = false>
 PE_DEV void load_task(const GemvArgs& a, int64_t task, int glane, int units,
                       typename Fmt<T>::Raw (&raw)[R][UPL]) {
     const int64_t tc = task < a.n_tasks ? task : a.n_tasks - 1;
@@ -309,7 +309,7 @@ PE_DEV void load_task(const GemvArgs& a, int64_t task, int glane, int units,
         const int u0 = 2 * glane < units ? 2 * glane : units - 2;
 #pragma unroll
         for (int rr = 0; rr < R; ++rr) {
-            Fmt<T>::load(a.w, tc + rr * a.up_off, u0, raw[rr][0]);
+            Fmt<T>::template load<NT>(a.w, tc + rr * a.up_off, u0, raw[rr][0]);
             raw[rr][1] = raw[rr][0];
             raw[rr][1].sub = raw[rr][0].sub + 1;
         }
@@ -321,9 +321,9 @@ PE_DEV void load_task(const GemvArgs& a, int64_t task, int glane, int units,
         for (int t = 0; t < UPL; ++t) {
             const int u = glane + GS * t;
             if constexpr (GS == 256 && !CLAMP) {
-                if (u < units) Fmt<T>::load(a.w, tc + rr * a.up_off, u, raw[rr][t]);
+                if (u < units) Fmt<T>::template load<NT>(a.w, tc + rr * a.up_off, u, raw[rr][t]);
             } else {
-                Fmt<T>::load(a.w, tc + rr * a.up_off, u < units ? u : units - 1, raw[rr][t]);
+                Fmt<T>::template load<NT>(a.w, tc + rr * a.up_off, u < units ? u : units - 1, raw[rr][t]);
             }
         }
 }
@@ -635,6 +635,9 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
     constexpr bool kSilu = MODE == kModeSilu || MODE == kModeSiluSum || MODE == kModeSiluSumMany;
     constexpr int R = kSilu ? 2 : 1;
     constexpr bool kEpi = !kSilu;
+    // the LM head (the argmax launch, and the normed plain GEMV that serves as the LM head
+    // without a greedy pick) streams its weights past the caches
+    constexpr bool kStream = MODE == kModeArgmax || (NORM && MODE == kModePlain);
     __shared__ float lds4[NT / 64];
     extern __shared__ float stage[];
     const int glane = threadIdx.x % GS;
@@ -651,7 +654,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
 #pragma unroll
         for (int i = 0; i < TPG; ++i) {
             const int64_t task = c * CH + i * G + gid;
-            load_task<T, GS, UPL, R, DB, UM>(a, task, glane, units, rw[i]);
+            load_task<T, GS, UPL, R, DB, UM, kStream>(a, task, glane, units, rw[i]);
             if constexpr (kEpi) ep[i] = load_epi(a, task);
         }
     };

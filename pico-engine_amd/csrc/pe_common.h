@@ -182,6 +182,23 @@ PE_DEV int4 ld16(const PE_GLOBAL uint8_t* p) {
     return make_int4(v.x, v.y, v.z, v.w);
 }
 
+// Weight loads, optionally non-temporal (NT): a tensor read once per decode step and larger
+// than the rest of the step's weights together (the LM head, 145 MB at config 0) is streamed
+// without being kept in the caches, so that the layer weights (248 MB) stay in the 256 MB
+// Infinity Cache from one step to the next.
+template <bool NT>
+PE_DEV int4 wld16(const PE_GLOBAL uint8_t* p) {
+    if constexpr (!NT) return ld16(p);
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    const v4i v = __builtin_nontemporal_load(reinterpret_cast<const PE_GLOBAL v4i*>(p));
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+template <bool NT, typename U>
+PE_DEV U wld(const PE_GLOBAL U* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    return *p;
+}
+
 template <int T>
 struct Fmt;
 
@@ -193,11 +210,12 @@ struct Fmt<PE_TYPE_Q8_0> {
         int4 a, b;
         uint32_t d;
     };
+    template <bool NT = false>
     static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
         const int64_t blk = row * t.nb + u;
-        r.a = ld16(t.base + blk * 32);
-        r.b = ld16(t.base + blk * 32 + 16);
-        r.d = reinterpret_cast<const PE_GLOBAL uint16_t*>(t.base + t.nrows * t.nb * 32)[blk];
+        r.a = wld16<NT>(t.base + blk * 32);
+        r.b = wld16<NT>(t.base + blk * 32 + 16);
+        r.d = wld<NT>(reinterpret_cast<const PE_GLOBAL uint16_t*>(t.base + t.nrows * t.nb * 32) + blk);
     }
     static PE_DEV int code(const Raw& r, int i) {
         const int4& v = i < 16 ? r.a : r.b;
@@ -227,12 +245,13 @@ struct Fmt<PE_TYPE_Q5_0> {
         uint32_t qh;
         uint32_t d;
     };
+    template <bool NT = false>
     static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
         const int64_t blk = row * t.nb + u;
         const int64_t nblk = t.nrows * t.nb;
-        r.qs = ld16(t.base + blk * 16);
-        r.qh = reinterpret_cast<const PE_GLOBAL uint32_t*>(t.base + nblk * 16)[blk];
-        r.d = reinterpret_cast<const PE_GLOBAL uint16_t*>(t.base + nblk * 20)[blk];
+        r.qs = wld16<NT>(t.base + blk * 16);
+        r.qh = wld<NT>(reinterpret_cast<const PE_GLOBAL uint32_t*>(t.base + nblk * 16) + blk);
+        r.d = wld<NT>(reinterpret_cast<const PE_GLOBAL uint16_t*>(t.base + nblk * 20) + blk);
     }
     // 5-bit code of element e (0..31): nibble of qs[e % 16] (low for e < 16), 5th bit = qh bit e
     static PE_DEV int code(const Raw& r, int e) {
@@ -273,13 +292,14 @@ struct Fmt<PE_TYPE_Q4_K> {
         int4 head;    // d, dmin, scales[12]
         int sub;      // j
     };
+    template <bool NT = false>
     static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
         const int64_t blk = row * t.nb + (u >> 3);
         const int j = u & 7;
         const PE_GLOBAL uint8_t* q = t.base + blk * 128 + 32 * (j >> 1);
-        r.lo = ld16(q);
-        r.hi = ld16(q + 16);
-        r.head = ld16(t.base + t.nrows * t.nb * 128 + blk * 16);
+        r.lo = wld16<NT>(q);
+        r.hi = wld16<NT>(q + 16);
+        r.head = wld16<NT>(t.base + t.nrows * t.nb * 128 + blk * 16);
         r.sub = j;
     }
     // 6-bit scale and min of sub-block j (the packing of k4_scale_min): bytes j%4 of the three
@@ -340,18 +360,19 @@ struct Fmt<PE_TYPE_Q6_K> {
         uint32_t d;
         int q;
     };
+    template <bool NT = false>
     static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
         const int64_t blk = row * t.nb + (u >> 3);
         const int64_t nblk = t.nrows * t.nb;
         const int hf = (u & 7) >> 2, q = u & 3;
         const PE_GLOBAL uint8_t* L = t.base + blk * 128 + 64 * hf + 32 * (q & 1);
         const PE_GLOBAL uint8_t* H = t.base + nblk * 128 + blk * 64 + 32 * hf;
-        r.l0 = ld16(L);
-        r.l1 = ld16(L + 16);
-        r.h0 = ld16(H);
-        r.h1 = ld16(H + 16);
-        r.sc = reinterpret_cast<const PE_GLOBAL uint16_t*>(t.base + nblk * 192 + blk * 16)[4 * hf + q];
-        r.d = reinterpret_cast<const PE_GLOBAL uint16_t*>(t.base + nblk * 208)[blk];
+        r.l0 = wld16<NT>(L);
+        r.l1 = wld16<NT>(L + 16);
+        r.h0 = wld16<NT>(H);
+        r.h1 = wld16<NT>(H + 16);
+        r.sc = wld<NT>(reinterpret_cast<const PE_GLOBAL uint16_t*>(t.base + nblk * 192 + blk * 16) + 4 * hf + q);
+        r.d = wld<NT>(reinterpret_cast<const PE_GLOBAL uint16_t*>(t.base + nblk * 208) + blk);
         r.q = q;
     }
     static PE_DEV int code(const Raw& r, int l) {
@@ -403,10 +424,11 @@ struct Fmt<PE_TYPE_F16> {
     struct Raw {
         int4 v[4];
     };
+    template <bool NT = false>
     static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
         const PE_GLOBAL uint8_t* p = t.base + (row * t.nb + 32 * (int64_t)u) * 2;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) r.v[i] = ld16(p + 16 * i);
+        for (int i = 0; i < 4; ++i) r.v[i] = wld16<NT>(p + 16 * i);
     }
     // exact conversions (denormals preserved), fp32 products
     static PE_DEV float dot(const Raw& r, const float* x, const UnitSums&) {
@@ -435,10 +457,11 @@ struct Fmt<PE_TYPE_F32> {
     struct Raw {
         int4 v[8];
     };
+    template <bool NT = false>
     static PE_DEV void load(const Tiled& t, int64_t row, int u, Raw& r) {
         const PE_GLOBAL uint8_t* p = t.base + (row * t.nb + 32 * (int64_t)u) * 4;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) r.v[i] = ld16(p + 16 * i);
+        for (int i = 0; i < 8; ++i) r.v[i] = wld16<NT>(p + 16 * i);
     }
     static PE_DEV float dot(const Raw& r, const float* x, const UnitSums&) {
         float acc = 0.f;
