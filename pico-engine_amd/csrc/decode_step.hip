@@ -568,7 +568,7 @@ PE_DEV uint64_t stage_lm(const StepParams& P, float* lds) {
 #pragma unroll
     for (int k = 0; k < kDepth; ++k) {
         const int64_t r = r0 + g + kGroups * k;
-        Fmt<T>::load(t, r <= last ? r : last, u, raw[k]);
+        Fmt<T>::template load<true>(t, r <= last ? r : last, u, raw[k]);   // streamed (LM head)
     }
     const float nw = P.out_norm[tid < P.hidden ? tid : 0];
     float* red = lds + kLdsRed;
@@ -584,7 +584,7 @@ PE_DEV uint64_t stage_lm(const StepParams& P, float* lds) {
             const int64_t r = base + g + kGroups * k;
             float y = glane < units ? Fmt<T>::dot(raw[k], xr, xs) : 0.f;
             const int64_t rn = r + kGroups * kDepth;
-            Fmt<T>::load(t, rn <= last ? rn : last, u, raw[k]);
+            Fmt<T>::template load<true>(t, rn <= last ? rn : last, u, raw[k]);
             y = wave_sum<32>(y) * rstd;
             if (glane == 0 && r < rend) {
                 if (P.logits) P.logits[r] = y;
