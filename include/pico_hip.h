@@ -224,9 +224,10 @@ typedef struct pe_qkv_args {
 int pe_qkv_rmsnorm_rope(const pe_qkv_args* args, pe_stream_t stream);
 
 /* Single-query GQA attention over a KV cache. Caches of at most 256 positions: one launch,
- * a workgroup per query head. Longer caches: split over 64-position chunks across CUs, then a
- * log-sum-exp merge launch (one workgroup per query head) in a fixed order; a chunk's record
- * is P.V[hd], max, sum and two pad words.
+ * a workgroup per query head. Up to 1024 positions (head_dim 64) / 512 (head_dim 128): one
+ * launch, a 1024-thread workgroup per query head. Longer caches: split over 64-position chunks
+ * across CUs, then a log-sum-exp merge launch (one workgroup per query head) in a fixed order;
+ * a chunk's record is P.V[hd], max, sum and two pad words.
  *   q (n_head, hd); k_cache, v_cache (n_kv, capacity, hd); out (n_head, hd)
  *   valid length S = (len_dev ? *len_dev : 0) + len_add, clamped to [0, capacity];
  *   len_dtype: 0 = len_dev unused, 1 = int32, 2 = int64. Head h reads kv head h / (n_head/n_kv).

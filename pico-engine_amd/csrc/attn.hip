@@ -390,6 +390,137 @@ __global__ __launch_bounds__(256) void k_decode_attn_head(AttnParams p) {
 }
 
 // ---------------------------------------------------------------------------------------
+// Mid-size caches (kSmallCap < capacity <= kMidCap<HD>): one workgroup of 1024 threads per
+// query head, one launch and no merge. Every V load of the valid positions is issued at kernel
+// start; K streams in batches of kMidBatch passes (the next batch's loads in flight while one
+// is scored), a row per VQ = HD / 4 lanes (fully coalesced 16-byte loads). Scores go to LDS,
+// the block takes the softmax statistics, and P.V runs over NS = 1024 / VQ position slices
+// (slice js holds positions js, js + NS, ...), combined by lane swaps within a wave and in
+// wave order across waves.
+constexpr int kMidThreads = 1024;
+constexpr int kMidBatch = 4;
+template <int HD>
+constexpr int kMidCap() { return HD == 64 ? 1024 : 512; }
+
+template <int HD>
+__global__ __launch_bounds__(kMidThreads) void k_decode_attn_mid(AttnParams p) {
+    constexpr int VQ = HD / 4;                  // lanes per row
+    constexpr int RP = kMidThreads / VQ;        // rows per pass (64 or 32)
+    constexpr int NS = kMidThreads / VQ;        // P.V slices
+    constexpr int MPV = kMidCap<HD>() / NS;     // V rows per thread (16)
+    constexpr int NW = kMidThreads / 64;
+    constexpr int SPW = 64 / VQ;                // slices per wave (4 or 2)
+    __shared__ float sc[kMidCap<HD>()];
+    __shared__ float4 red4[NW][VQ];
+    __shared__ float wred[NW];
+    const int t = threadIdx.x, w = t >> 6, c = t % VQ, js = t / VQ;
+    const int h = blockIdx.x, kvh = h / p.group;
+    const int64_t S = valid_len(p);
+    const float* kb = p.k + (int64_t)kvh * p.capacity * HD;
+    const float* vb = p.v + (int64_t)kvh * p.capacity * HD;
+    const float4 q4 = reinterpret_cast<const float4*>(p.q + (int64_t)h * HD)[c];
+    const float NEG_INF = -__builtin_huge_valf();
+    // V rows of this thread's slice (positions past S are zero: they contribute nothing)
+    float4 vr[MPV];
+#pragma unroll
+    for (int i = 0; i < MPV; ++i) {
+        const int64_t s = js + (int64_t)NS * i;
+        vr[i] = s < S ? reinterpret_cast<const float4*>(vb + s * HD)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    // scores: pass j covers rows RP j .. RP j + RP - 1; row js of a pass is this thread's
+    const int npass = (int)((S + RP - 1) / RP);
+    float4 kr[2][kMidBatch];
+    auto issue = [&](int b, float4 (&dst)[kMidBatch]) {
+#pragma unroll
+        for (int i = 0; i < kMidBatch; ++i) {
+            const int64_t s = (int64_t)RP * (kMidBatch * b + i) + js;
+            dst[i] = s < S ? reinterpret_cast<const float4*>(kb + s * HD)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    const int nbatch = (npass + kMidBatch - 1) / kMidBatch;
+    float m_loc = NEG_INF;
+    auto score = [&](int b, const float4 (&src)[kMidBatch]) {
+#pragma unroll
+        for (int i = 0; i < kMidBatch; ++i) {
+            const float4 k4 = src[i];
+            float part = q4.x * k4.x;
+            part = fmaf(q4.y, k4.y, part);
+            part = fmaf(q4.z, k4.z, part);
+            part = fmaf(q4.w, k4.w, part);
+            part = wave_sum<VQ>(part);
+            const int64_t s = (int64_t)RP * (kMidBatch * b + i) + js;
+            if (s < S) {
+                const float v = part * p.scale;
+                if (c == 0) sc[s] = v;
+                m_loc = fmaxf(m_loc, v);
+            }
+        }
+    };
+    // two register sets at fixed names (a run-time index into them would go to scratch)
+    issue(0, kr[0]);
+    for (int b = 0; b < nbatch; b += 2) {
+        if (b + 1 < nbatch) issue(b + 1, kr[1]);
+        score(b, kr[0]);
+        if (b + 1 >= nbatch) break;
+        if (b + 2 < nbatch) issue(b + 2, kr[0]);
+        score(b + 1, kr[1]);
+    }
+    // softmax statistics over the S scores
+    m_loc = wave_max<64>(m_loc);
+    if ((t & 63) == 0) wred[w] = m_loc;
+    __syncthreads();
+    float M = wred[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) M = fmaxf(M, wred[i]);
+    float l_loc = 0.f;
+    for (int s = t; s < S; s += kMidThreads) {
+        const float e = expf(sc[s] - M);
+        sc[s] = e;
+        l_loc += e;
+    }
+    l_loc = wave_sum<64>(l_loc);
+    __syncthreads();  // every read of wred (max) is done and sc[] holds the exponentials
+    if ((t & 63) == 0) wred[w] = l_loc;
+    __syncthreads();
+    float L = wred[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) L += wred[i];
+    // P.V over this thread's slice, slices of a wave by lane swaps, waves in wave order
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < MPV; ++i) {
+        const int64_t s = js + (int64_t)NS * i;
+        const float e = s < S ? sc[s] : 0.f;
+        acc.x = fmaf(e, vr[i].x, acc.x);
+        acc.y = fmaf(e, vr[i].y, acc.y);
+        acc.z = fmaf(e, vr[i].z, acc.z);
+        acc.w = fmaf(e, vr[i].w, acc.w);
+    }
+    if constexpr (SPW == 4) {
+        acc.x = swap32_sum(swap16_sum(acc.x));
+        acc.y = swap32_sum(swap16_sum(acc.y));
+        acc.z = swap32_sum(swap16_sum(acc.z));
+        acc.w = swap32_sum(swap16_sum(acc.w));
+    } else {
+        acc.x = swap32_sum(acc.x);
+        acc.y = swap32_sum(acc.y);
+        acc.z = swap32_sum(acc.z);
+        acc.w = swap32_sum(acc.w);
+    }
+    if ((t & 63) < VQ) red4[w][c] = acc;
+    __syncthreads();
+    if (t < HD) {
+        const float* rf = reinterpret_cast<const float*>(red4);
+        float a = rf[t];
+#pragma unroll
+        for (int i = 1; i < NW; ++i) a += rf[i * HD + t];
+        float o = a / L;
+        if (p.round_fp16) o = round_to_f16(o);
+        p.out[attn_out_index(p, (int64_t)h * HD + t, (int64_t)p.n_kv * p.group * HD)] = o;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
 struct PrefillParams {
     const float* q;
     int64_t q_stride;
@@ -594,6 +725,14 @@ static int launch_decode_attn(const float* q, const float* k_cache, const float*
             hipLaunchKernelGGL(k_decode_attn_head<64>, grid, dim3(256), 0, s, p);
         else
             hipLaunchKernelGGL(k_decode_attn_head<128>, grid, dim3(256), 0, s, p);
+        return launch_status();
+    }
+    if (capacity <= (head_dim == 64 ? kMidCap<64>() : kMidCap<128>())) {
+        const dim3 grid((unsigned)n_head);
+        if (head_dim == 64)
+            hipLaunchKernelGGL(k_decode_attn_mid<64>, grid, dim3(kMidThreads), 0, s, p);
+        else
+            hipLaunchKernelGGL(k_decode_attn_mid<128>, grid, dim3(kMidThreads), 0, s, p);
         return launch_status();
     }
     const dim3 grid((unsigned)p.nsplit, (unsigned)n_kv);

@@ -245,8 +245,11 @@ def _kv(rng, n_kv, cap, hd):
 
 
 @pytest.mark.parametrize("hd,n_head,n_kv", [(64, 14, 2), (128, 28, 4), (64, 4, 4)])
+# capacities <= 256: one pass per head; up to 512 (hd 128) / 1024 (hd 64): one 1024-thread
+# workgroup per head; beyond: split chunks + merge launch
 @pytest.mark.parametrize("S,cap", [(1, 8), (17, 77), (64, 64), (65, 130), (130, 130), (512, 600),
-                                   (4096, 4096)])
+                                   (4096, 4096), (257, 300), (1, 400), (300, 512), (512, 512),
+                                   (1000, 1024), (700, 1100)])
 def test_decode_attn(K, hd, n_head, n_kv, S, cap):
     rng = np.random.default_rng(S + hd)
     q = rng.standard_normal((n_head, hd)).astype(np.float32)
