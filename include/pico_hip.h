@@ -144,6 +144,26 @@ int pe_flash_prefill(const float* q, int64_t q_stride, const float* k_cache, con
                      int n_head, int n_kv, int head_dim, int64_t capacity, int64_t L, int64_t pos0,
                      float scale, float* out, int64_t out_stride, pe_stream_t stream);
 
+/* pe_flash_prefill storing out in fp16 (each value rounded to nearest even; out_stride in
+ * elements): the rounding the o-projection GEMM applies to an fp32 operand as it reads it, so
+ * pe_gemm_lt on this output multiplies the same operand bits. Replaces model.py:201-209. */
+int pe_flash_prefill_h16(const float* q, int64_t q_stride, const float* k_cache,
+                         const float* v_cache, int n_head, int n_kv, int head_dim,
+                         int64_t capacity, int64_t L, int64_t pos0, float scale, void* out_f16,
+                         int64_t out_stride, pe_stream_t stream);
+
+/* Plain prefill GEMM on ROCm's hipBLASLt: c (M, N) = a (M, K) . w (N, K)^T (+ bias[N])
+ * (+ residual (M, N)); a and w fp16 row-major (row strides lda and K elements; lda % 8 == 0,
+ * K % 8 == 0, 16-byte aligned), fp32 accumulation, c and residual fp32 with row stride ldc
+ * (residual == c adds in place; ldr must equal ldc). workspace: device memory for hipBLASLt
+ * (32 MiB suffices), any contents; calls that overlap must not share it. The library keeps one
+ * hipBLASLt handle per device and a cache of matmul plans per shape, guarded by a mutex.
+ * Replaces the plain prefill F.linear / addmm calls under autocast (model.py:147-151, :177,
+ * :213, :235): QKV with its bias, the o-projection and ffn_down with the residual. */
+int pe_gemm_lt(const void* a_f16, int64_t lda, const void* w_f16, int64_t M, int64_t N, int64_t K,
+               const float* bias, const float* residual, int64_t ldr, float* c, int64_t ldc,
+               void* workspace, int64_t workspace_bytes, pe_stream_t stream);
+
 /* out[l][:] = dequantized row ids[l] of a raw GGUF (vocab x hidden) table, l < n_ids.
  * An id outside [0, vocab) yields a row of NaN (no out-of-bounds read). layout: PE_LAYOUT_Y_UT
  * writes each row in the unit-transposed layout (hidden % 32 == 0).
@@ -353,6 +373,12 @@ int pe_decode_step(const pe_step_args* args, pe_stream_t stream);
  * Replaces rmsnorm (kernels.py:26). */
 int pe_rmsnorm(const float* x, int64_t x_stride, const float* w, float* y, int64_t y_stride,
                int64_t rows, int64_t n, float eps, pe_stream_t stream);
+
+/* pe_rmsnorm storing y in fp16 (each value rounded to nearest even; y_stride in elements): the
+ * operand of the prefill GEMMs, as they would round an fp32 one. Replaces rmsnorm
+ * (kernels.py:26) before the autocast F.linear of model.py:177. */
+int pe_rmsnorm_h16(const float* x, int64_t x_stride, const float* w, void* y_f16,
+                   int64_t y_stride, int64_t rows, int64_t n, float eps, pe_stream_t stream);
 
 /* Rotate-half RoPE of x (L, n_head, hd) whose token rows are x_stride elements apart
  * (heads contiguous within a row), with cos/sin (L, hd/2) rows; writes y likewise.

@@ -8,8 +8,11 @@
 
 namespace pe {
 
+// OutT _Float16: the normalised row rounded to fp16 (nearest even), the operand the prefill
+// GEMMs multiply.
+template <typename OutT>
 __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x, int64_t xs,
-                                                 const float* __restrict__ w, float* __restrict__ y,
+                                                 const float* __restrict__ w, OutT* __restrict__ y,
                                                  int64_t ys, int64_t n, float eps) {
     __shared__ float lds4[4];
     const int64_t r = blockIdx.x;
@@ -21,8 +24,15 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float* __restrict__ x, in
     __syncthreads();
     ss = ((lds4[0] + lds4[1]) + lds4[2]) + lds4[3];
     const float rstd = 1.0f / sqrtf(ss / (float)n + eps);
-    float* yr = y + r * ys;
-    for (int64_t i = threadIdx.x; i < n; i += 256) yr[i] = (xr[i] * rstd) * w[i];
+    OutT* yr = y + r * ys;
+    for (int64_t i = threadIdx.x; i < n; i += 256) {
+        float v = (xr[i] * rstd) * w[i];
+        // the fp32 value is rounded to fp16 as a value of its own: without the barrier the
+        // compiler fuses the last multiply and the conversion into one mixed-precision
+        // instruction that rounds once (different on fp32 values halfway between fp16 ones)
+        if constexpr (sizeof(OutT) == 2) asm volatile("" : "+v"(v));
+        yr[i] = (OutT)v;
+    }
 }
 
 __global__ void k_rope(const float* __restrict__ x, int64_t xs, const float* __restrict__ cs,
@@ -88,8 +98,19 @@ extern "C" int pe_rmsnorm(const float* x, int64_t x_stride, const float* w, floa
     if (rows == 0) return PE_OK;
     if (!x || !w || !y) return PE_ERR_NULL;
     if (!aligned(x, 4) || !aligned(w, 4) || !aligned(y, 4)) return PE_ERR_ALIGN;
-    hipLaunchKernelGGL(k_rmsnorm, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, x,
+    hipLaunchKernelGGL(k_rmsnorm<float>, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, x,
                        x_stride, w, y, y_stride, n, eps);
+    return launch_status();
+}
+
+extern "C" int pe_rmsnorm_h16(const float* x, int64_t x_stride, const float* w, void* y,
+                              int64_t y_stride, int64_t rows, int64_t n, float eps, pe_stream_t stream) {
+    if (rows < 0 || n <= 0 || x_stride < n || y_stride < n || rows > 0x7FFFFFFF) return PE_ERR_SHAPE;
+    if (rows == 0) return PE_OK;
+    if (!x || !w || !y) return PE_ERR_NULL;
+    if (!aligned(x, 4) || !aligned(w, 4) || !aligned(y, 2)) return PE_ERR_ALIGN;
+    hipLaunchKernelGGL(k_rmsnorm<_Float16>, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, x,
+                       x_stride, w, (_Float16*)y, y_stride, n, eps);
     return launch_status();
 }
 

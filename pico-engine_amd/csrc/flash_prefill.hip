@@ -18,7 +18,7 @@
 // exponent's fma) keeps one running max and sum per lane with two cross-lane steps, and the
 // probabilities go straight from registers into the B operand of O^T += V^T P^T (8 MFMAs),
 // with V^T staged in the matching key order. The heaviest query blocks (most keys) are
-// scheduled first.
+// scheduled so that light blocks share CUs with heavy ones.
 #include "pe_common.h"
 
 namespace pe {
@@ -41,11 +41,12 @@ struct FlashParams {
     const float* k;      // (n_kv, capacity, 64)
     const float* v;
     int group;           // query heads per kv head
+    int n_kv;
     int64_t capacity;
     int64_t L;
     int64_t pos0;
     float scale;
-    float* out;          // (L, n_head, 64), token rows out_stride floats apart
+    float* out;          // (L, n_head, 64), token rows out_stride elements apart
     int64_t out_stride;
 };
 
@@ -56,14 +57,23 @@ PE_DEV fh8 f8_to_h8(float4 a, float4 b) {
     return r;
 }
 
+// OutT _Float16: the output rounded to fp16 (nearest even), the operand of the o-projection
+// GEMM (p.out then points to fp16 rows).
+template <typename OutT>
 __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_size) {
     __shared__ __align__(16) _Float16 ks[kFpKeys * kFpRow];         // K block, [key][dim]
     __shared__ __align__(16) _Float16 vt[kFpHd * kFpRow];           // V block transposed, [dim][key]
     const int t = threadIdx.x, nt = blockDim.x, w = t >> 6, l = t & 63;
     const int li = l & 15, lg = l >> 4;
     const int64_t nqb = (p.L + qb_size - 1) / qb_size;
-    const int64_t qb = nqb - 1 - (int64_t)blockIdx.x;  // heaviest blocks first
-    const int kvh = blockIdx.y;
+    // Workload order: rank r = (query block nqb - 1 - r / n_kv, kv head r % n_kv), heaviest
+    // (most keys) first. The first half of the grid takes ranks in that order and the second
+    // half from the lightest up, so the workgroup that lands on a CU second (grid position
+    // half + i, after position i) pairs a light block with a heavy one instead of two heavy ones.
+    const int64_t total = nqb * p.n_kv, half = (total + 1) / 2, lin = blockIdx.x;
+    const int64_t rank = lin < half ? lin : total - 1 - (lin - half);
+    const int64_t qb = nqb - 1 - rank / p.n_kv;
+    const int kvh = (int)(rank % p.n_kv);
     const int h = kvh * p.group + w % p.group;         // this wave's query head
     const int64_t q0 = qb * qb_size + 16 * (w / p.group);  // this wave's first query (token index)
     const float* kb = p.k + (int64_t)kvh * p.capacity * kFpHd;
@@ -207,12 +217,17 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
     // out: O[query q0 + li][dim 16 d + 4 lg + r] / l
     const int64_t qi = q0 + li;
     if (qi < p.L) {
-        float* orow = p.out + qi * p.out_stride + (int64_t)h * kFpHd;
+        OutT* orow = reinterpret_cast<OutT*>(p.out) + qi * p.out_stride + (int64_t)h * kFpHd;
         const float inv = 1.0f / l_run;
 #pragma unroll
         for (int d = 0; d < 4; ++d)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) orow[16 * d + 4 * lg + r] = o[d][r] * inv;
+            for (int r = 0; r < 4; ++r) {
+                float v = o[d][r] * inv;
+                // rounded to fp16 as a value of its own (no fused mixed-precision multiply)
+                if constexpr (sizeof(OutT) == 2) asm volatile("" : "+v"(v));
+                orow[16 * d + 4 * lg + r] = (OutT)v;
+            }
     }
 }
 
@@ -220,10 +235,10 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
 
 using namespace pe;
 
-extern "C" int pe_flash_prefill(const float* q, int64_t q_stride, const float* k_cache,
-                                const float* v_cache, int n_head, int n_kv, int head_dim,
-                                int64_t capacity, int64_t L, int64_t pos0, float scale, float* out,
-                                int64_t out_stride, pe_stream_t stream) {
+static int flash_prefill(const float* q, int64_t q_stride, const float* k_cache,
+                         const float* v_cache, int n_head, int n_kv, int head_dim,
+                         int64_t capacity, int64_t L, int64_t pos0, float scale, void* out,
+                         int64_t out_stride, bool half_out, pe_stream_t stream) {
     if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > kFpMaxWaves ||
         head_dim != kFpHd || capacity <= 0 || L < 0 || pos0 < 0 || pos0 + L > capacity || n_kv > 65535)
         return PE_ERR_SHAPE;
@@ -234,11 +249,33 @@ extern "C" int pe_flash_prefill(const float* q, int64_t q_stride, const float* k
     if (!q || !k_cache || !v_cache || !out) return PE_ERR_NULL;
     if (q_stride < (int64_t)n_head * head_dim || out_stride < (int64_t)n_head * head_dim) return PE_ERR_SHAPE;
     if (!aligned(q, 16) || q_stride % 4 || !aligned(k_cache, 16) || !aligned(v_cache, 16) ||
-        !aligned(out, 4))
+        !aligned(out, half_out ? 2 : 4))
         return PE_ERR_ALIGN;
-    FlashParams p{q, q_stride, k_cache, v_cache, n_head / n_kv, capacity, L, pos0, scale, out, out_stride};
+    FlashParams p{q, q_stride, k_cache, v_cache, n_head / n_kv, n_kv, capacity, L, pos0, scale, (float*)out,
+                  out_stride};
     const int waves = group * (qb / 16);  // 9..16 (at least 576 threads: kv_load assumes it)
-    const dim3 grid((unsigned)((L + qb - 1) / qb), (unsigned)n_kv);
-    hipLaunchKernelGGL(k_flash_prefill, grid, dim3(64 * waves), 0, (hipStream_t)stream, p, qb);
+    const int64_t nblocks = (L + qb - 1) / qb * (int64_t)n_kv;
+    if (nblocks > 0x7FFFFFFF) return PE_ERR_SHAPE;
+    const dim3 grid((unsigned)nblocks);
+    if (half_out)
+        hipLaunchKernelGGL(k_flash_prefill<_Float16>, grid, dim3(64 * waves), 0, (hipStream_t)stream, p, qb);
+    else
+        hipLaunchKernelGGL(k_flash_prefill<float>, grid, dim3(64 * waves), 0, (hipStream_t)stream, p, qb);
     return launch_status();
+}
+
+extern "C" int pe_flash_prefill(const float* q, int64_t q_stride, const float* k_cache,
+                                const float* v_cache, int n_head, int n_kv, int head_dim,
+                                int64_t capacity, int64_t L, int64_t pos0, float scale, float* out,
+                                int64_t out_stride, pe_stream_t stream) {
+    return flash_prefill(q, q_stride, k_cache, v_cache, n_head, n_kv, head_dim, capacity, L, pos0,
+                         scale, out, out_stride, false, stream);
+}
+
+extern "C" int pe_flash_prefill_h16(const float* q, int64_t q_stride, const float* k_cache,
+                                    const float* v_cache, int n_head, int n_kv, int head_dim,
+                                    int64_t capacity, int64_t L, int64_t pos0, float scale, void* out,
+                                    int64_t out_stride, pe_stream_t stream) {
+    return flash_prefill(q, q_stride, k_cache, v_cache, n_head, n_kv, head_dim, capacity, L, pos0,
+                         scale, out, out_stride, true, stream);
 }

@@ -94,6 +94,8 @@ _SIGNATURES = {
     "pe_gemm_f16_silu_h": (_I, [_P, _L, _P, _P, _L, _L, _L, _L, _P]),
     "pe_gemm_h16": (_I, [_P, _L, _P, _P, _P, _L, _P, _L, _L, _L, _L, _P]),
     "pe_flash_prefill": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _L, _F, _P, _L, _P]),
+    "pe_flash_prefill_h16": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _L, _F, _P, _L, _P]),
+    "pe_gemm_lt": (_I, [_P, _L, _P, _L, _L, _L, _P, _P, _L, _P, _L, _P, _L, _P]),
     "pe_embed_gather": (_I, [_I, _P, _L, _L, _P, _L, _P, _I, _P]),
     "pe_qgemv": (_I, [_I, _P, _L, _L, _P, _P, _P, _P, _I, _P]),
     "pe_qgemv_rmsnorm": (_I, [_I, _P, _L, _L, _P, _P, _F, _P, _I, _P]),
@@ -108,6 +110,7 @@ _SIGNATURES = {
     "pe_attn_gproj_supported": (_I, [_I, _I, _I, _L, _I, _L]),
     "pe_attn_gproj": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _I, _P, _L, _P, _I, _P]),
     "pe_rmsnorm": (_I, [_P, _L, _P, _P, _L, _L, _L, _F, _P]),
+    "pe_rmsnorm_h16": (_I, [_P, _L, _P, _P, _L, _L, _L, _F, _P]),
     "pe_rope": (_I, [_P, _L, _P, _P, _P, _L, _L, _I, _I, _P]),
     "pe_silu_mul": (_I, [_P, _L, _P, _L, _L, _L, _P]),
     "pe_qgemm": (_I, [_I, _P, _L, _L, _P, _L, _L, _P, _P, _L, _P, _L, _P]),

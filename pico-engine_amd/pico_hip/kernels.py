@@ -243,8 +243,10 @@ def embed_gather(table: RawTensor, ids: torch.Tensor, out: torch.Tensor | None =
 
 # ---- reference kernels -------------------------------------------------------------------
 
-def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """out = x / sqrt(mean(x^2) + eps) * weight over the last dim (kernels.py:26)."""
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, half: bool = False) -> torch.Tensor:
+    """out = x / sqrt(mean(x^2) + eps) * weight over the last dim (kernels.py:26). With
+    ``half`` the result is stored in fp16 (rounded to nearest even; pe_rmsnorm_h16), the
+    operand of the prefill GEMMs."""
     dev = _on_gpu(x, weight)
     x2 = x.reshape(-1, x.shape[-1])
     if x2.stride(-1) != 1:
@@ -252,6 +254,11 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     x2 = x2.float()
     w = weight.float().contiguous()
     rows, n = x2.shape
+    if half:
+        out = torch.empty(rows, n, device=dev, dtype=torch.float16)
+        check(lib.pe_rmsnorm_h16(_ptr(x2), x2.stride(0), _ptr(w), _ptr(out), n, rows, n, float(eps),
+                                 _stream(dev)), "pe_rmsnorm_h16")
+        return out.reshape(x.shape)
     out = torch.empty(rows, n, device=dev, dtype=torch.float32)
     check(lib.pe_rmsnorm(_ptr(x2), x2.stride(0), _ptr(w), _ptr(out), n, rows, n, float(eps),
                          _stream(dev)), "pe_rmsnorm")
@@ -696,9 +703,11 @@ def prefill_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
 
 
 def flash_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos0: int = 0,
-                  scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+                  scale: float | None = None, out: torch.Tensor | None = None,
+                  half: bool = False) -> torch.Tensor:
     """prefill_attn on the matrix cores: q, k, v rounded to fp16 as read, fp32 softmax and
-    accumulation (the reference's fp16 SDPA prefill, model.py:201-209); head_dim 64."""
+    accumulation (the reference's fp16 SDPA prefill, model.py:201-209); head_dim 64. With
+    ``half`` the output is stored in fp16 (pe_flash_prefill_h16), the o-projection's operand."""
     dev = _on_gpu(q, k_cache, v_cache)
     L, n_head, hd = q.shape
     n_kv, capacity, _ = k_cache.shape
@@ -707,10 +716,59 @@ def flash_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     if scale is None:
         scale = hd ** -0.5
     if out is None:
-        out = torch.empty(L, n_head * hd, device=dev, dtype=torch.float32)
-    check(lib.pe_flash_prefill(_ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), n_head, n_kv, hd,
-                               capacity, L, pos0, float(scale), _ptr(out), out.stride(0),
-                               _stream(dev)), "pe_flash_prefill")
+        out = torch.empty(L, n_head * hd, device=dev, dtype=torch.float16 if half else torch.float32)
+    if (out.dtype == torch.float16) != half:
+        raise ValueError("out dtype must be float16 with half=True, float32 otherwise")
+    fn = lib.pe_flash_prefill_h16 if half else lib.pe_flash_prefill
+    check(fn(_ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), n_head, n_kv, hd,
+             capacity, L, pos0, float(scale), _ptr(out), out.stride(0), _stream(dev)),
+          "pe_flash_prefill_h16" if half else "pe_flash_prefill")
+    return out
+
+
+GEMM_LT_WORKSPACE = 32 << 20
+
+
+def gemm_lt_workspace(device) -> torch.Tensor:
+    """Device workspace for gemm_lt (hipBLASLt), reusable by calls made in order on a stream."""
+    return torch.empty(GEMM_LT_WORKSPACE, device=device, dtype=torch.uint8)
+
+
+def gemm_lt(a16: torch.Tensor, w16: torch.Tensor, bias: torch.Tensor | None = None,
+            residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
+            workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """C = A W^T (+ bias) (+ residual) on hipBLASLt (pe_gemm_lt): A fp16 (M, K) (rows may be
+    strided), W fp16 (N, K), fp32 accumulation and result (M, N). ``residual`` may be ``out``
+    (added in place); its row stride must equal out's."""
+    dev = _on_gpu(a16, w16, bias, residual)
+    if a16.dim() == 1:
+        a16 = a16.unsqueeze(0)
+    if a16.dtype != torch.float16:
+        raise ValueError("a16 must be float16")
+    if a16.stride(1) != 1 or a16.stride(0) % 8 or a16.data_ptr() % 16:
+        a16 = a16.contiguous()
+    M, K = a16.shape
+    N = w16.shape[0]
+    if w16.dtype != torch.float16 or not w16.is_contiguous() or w16.shape[1] != K:
+        raise ValueError("w16 must be a contiguous (N, K) float16 tensor")
+    if out is None:
+        out = torch.empty(M, N, device=dev, dtype=torch.float32)
+    if out.dtype != torch.float32 or tuple(out.shape) != (M, N) or out.stride(1) != 1:
+        raise ValueError("out must be a float32 (M, N) tensor with unit column stride")
+    ldr = 0
+    if residual is not None:
+        if residual.dtype != torch.float32 or tuple(residual.shape) != (M, N):
+            raise ValueError("residual must be a float32 (M, N) tensor")
+        if residual.stride(1) != 1 or residual.stride(0) != out.stride(0):
+            residual = residual.contiguous()
+            if residual.stride(0) != out.stride(0):
+                raise ValueError("residual must have out's row stride")
+        ldr = residual.stride(0)
+    if workspace is None:
+        workspace = gemm_lt_workspace(dev)
+    check(lib.pe_gemm_lt(_ptr(a16), a16.stride(0), _ptr(w16), M, N, K,
+                         _ptr(None if bias is None else _f32c(bias)), _ptr(residual), ldr, _ptr(out),
+                         out.stride(0), _ptr(workspace), workspace.numel(), _stream(dev)), "pe_gemm_lt")
     return out
 
 
@@ -718,6 +776,7 @@ __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "
            "rmsnorm", "rope", "silu_mul", "decode_attn", "decode_attn_workspace", "qgemv",
            "q8_0_gemv", "q5_0_gemv", "q5_0_gemv_norm", "q6_k_gemv", "q4_k_gemv", "qgemv_norm",
            "qgemv_norm_silu", "qkv_rmsnorm_rope", "qgemv_sum_norm_silu", "qgemm", "kv_write", "prefill_attn",
+           "gemm_lt", "gemm_lt_workspace",
            "attn_gproj", "attn_gproj_supported", "qgemv_norm_argmax", "dequantize_weight_f16",
            "DecodeStep", "decode_step_supported", "decode_step_workspace",
            "gemm_f16", "gemm_f16_silu", "interleave_gate_up_f16", "flash_prefill",

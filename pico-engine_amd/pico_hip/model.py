@@ -101,6 +101,10 @@ class Transformer:
         # operands, fp32 accumulation: the reference's CUDA autocast prefill, model.py:147-151);
         # shorter ones by the fp32 path (the reference's off-CUDA numerics). None: never.
         self.prefill_f16_min_tokens: int | None = 512
+        # the matrix-core prefill's plain products (QKV + bias, o-proj and ffn_down + residual)
+        # on hipBLASLt; off: every product on this library's MFMA GEMM (pe_gemm_f16)
+        self.prefill_blaslt = True
+        self._lt_ws: torch.Tensor | None = None
         self._f16: list[dict[str, torch.Tensor]] | None = None
         # greedy decode steps the persistent kernel covers can run as one launch per token
         # (pe_decode_step) instead of four launches per layer; off by default while it measures
@@ -272,9 +276,13 @@ class Transformer:
 
     # ---- prefill --------------------------------------------------------------------------
     def _prefill_f16(self, token_ids, positions, cache, greedy=None):
-        """The prefill on the matrix cores: GEMMs with fp16 operands (pe_gemm_f16) and flash
-        attention (pe_flash_prefill; head_dim 64, else the fp32 prefill attention), fp32
-        residual stream, norms, RoPE and KV cache."""
+        """The prefill on the matrix cores: GEMMs with fp16 operands and flash attention
+        (pe_flash_prefill; head_dim 64, else the fp32 prefill attention), fp32 residual
+        stream, norms, RoPE and KV cache. The plain products (QKV + bias, o-proj and ffn_down
+        + residual) run on hipBLASLt (pe_gemm_lt) over operands stored in fp16 by their
+        producers (pe_rmsnorm_h16, pe_flash_prefill_h16, the SiLU GEMM), the same values
+        pe_gemm_f16 would round as it reads them; gate/up with its SiLU epilogue stays on
+        pe_gemm_f16_silu_h. prefill_blaslt = False runs every product on pe_gemm_f16."""
         cfg = self.cfg
         Lt = token_ids.shape[0]
         hd, nh, nkv = cfg.head_dim, cfg.n_head, cfg.n_kv_head
@@ -283,27 +291,45 @@ class Transformer:
         sin = self.sin[positions]
         pos0 = int(positions[0].item()) if positions.numel() else 0
         w16 = self.f16_weights()
+        lt = self.prefill_blaslt
+        if lt and self._lt_ws is None:
+            self._lt_ws = K.gemm_lt_workspace(self.device)
+        ws = self._lt_ws
         x = K.embed_gather(self.embed, token_ids)                       # (L, hidden)
+        x_alt = torch.empty_like(x) if lt else None                    # the residual ping-pong
         qkv = torch.empty(Lt, qd + 2 * kd, device=self.device, dtype=torch.float32)
         for i, L in enumerate(self.layers):
             k_buf, v_buf = cache[i]
             W = w16[i]
-            h = K.rmsnorm(x, L.attn_norm, cfg.eps)
-            K.gemm_f16(h, W["qkv"], bias=W["qkv_bias"], out=qkv)
+            if lt:  # the plain products on hipBLASLt, their operands stored in fp16
+                h16 = K.rmsnorm(x, L.attn_norm, cfg.eps, half=True)
+                K.gemm_lt(h16, W["qkv"], bias=W["qkv_bias"], out=qkv, workspace=ws)
+            else:
+                h = K.rmsnorm(x, L.attn_norm, cfg.eps)
+                K.gemm_f16(h, W["qkv"], bias=W["qkv_bias"], out=qkv)
             qk = K.rope(qkv[:, :qd + kd].view(Lt, nh + nkv, hd), cos, sin)
             v = qkv[:, qd + kd:].view(Lt, nkv, hd)
             K.kv_write(qk[:, nh:], v, k_buf, v_buf, pos0=pos0)
-            if hd == 64:  # matrix-core flash attention
-                attn = K.flash_prefill(qk[:, :nh], k_buf, v_buf, pos0=pos0)  # (L, hidden)
-            else:         # other head sizes: the fp32 causal attention kernel
-                attn = K.prefill_attn(qk[:, :nh], k_buf, v_buf, pos0=pos0)
-            x = K.gemm_f16(attn, W["o"], residual=x)
+            if hd == 64 and lt:
+                attn16 = K.flash_prefill(qk[:, :nh], k_buf, v_buf, pos0=pos0, half=True)
+                x, x_alt = K.gemm_lt(attn16, W["o"], residual=x, out=x_alt, workspace=ws), x
+            else:
+                if hd == 64:  # matrix-core flash attention
+                    attn = K.flash_prefill(qk[:, :nh], k_buf, v_buf, pos0=pos0)  # (L, hidden)
+                else:         # other head sizes: the fp32 causal attention kernel
+                    attn = K.prefill_attn(qk[:, :nh], k_buf, v_buf, pos0=pos0)
+                x = K.gemm_f16(attn, W["o"], residual=x)
+                if lt and x_alt.shape != x.shape:
+                    x_alt = torch.empty_like(x)
             h = K.rmsnorm(x, L.ffn_norm, cfg.eps)
             if W["gu_il"] is not None:
                 act = K.gemm_f16_silu(h, W["gu_il"], half=True)  # fp16: the down GEMM's operand
             else:
                 act = K.silu_mul(K.gemm_f16(h, W["gu"]), cfg.ffn_dim)
-            x = K.gemm_f16(act, W["down"], residual=x)
+            if lt and act.dtype == torch.float16:
+                x, x_alt = K.gemm_lt(act, W["down"], residual=x, out=x_alt, workspace=ws), x
+            else:
+                x = K.gemm_f16(act, W["down"], residual=x)
         return self._lm_head(x[-1], self.w["output_norm.weight"], greedy, K.LAYOUT_NATURAL)
 
     def _prefill(self, token_ids, positions, cache, greedy=None):

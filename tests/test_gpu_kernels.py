@@ -729,6 +729,58 @@ def test_gemm_f16_matches_fp16_operand_reference(K, M, N, Kd, bias, res, extra):
     assert rel_err(c, ref) < 1e-5
 
 
+LT_CASES = [  # (M, N, K, bias, residual, a_row_stride_extra): the config-3 prefill products + edges
+    (1, 128, 896, False, False, 0), (13, 1152, 896, True, False, 0), (128, 896, 896, False, True, 0),
+    (257, 896, 4864, False, True, 0), (77, 200, 96, True, True, 32), (8192, 1152, 896, True, False, 0),
+    (8192, 896, 896, False, True, 0), (8192, 896, 4864, False, True, 0),
+]
+
+
+@pytest.mark.parametrize("M,N,Kd,bias,res,extra", LT_CASES)
+def test_gemm_lt_matches_fp16_operand_reference(K, M, N, Kd, bias, res, extra):
+    """pe_gemm_lt (hipBLASLt) against float64 on the same fp16 operands (fp32 accumulation:
+    only the summation order differs), with the bias, the residual, and the residual added in
+    place (residual == out); a strided A included."""
+    rng = np.random.default_rng(M + N + Kd + 7)
+    a = rng.standard_normal((M, Kd + extra)).astype(np.float16)
+    w16 = (rng.standard_normal((N, Kd)) * 0.05).astype(np.float16)
+    b = rng.standard_normal(N).astype(np.float32) if bias else None
+    r = rng.standard_normal((M, N)).astype(np.float32) if res else None
+    T = lambda v: None if v is None else torch.from_numpy(v).to(DEV)
+    A = T(a)[:, :Kd]
+    ws = K.gemm_lt_workspace(DEV)
+    c = K.gemm_lt(A, T(w16), bias=T(b), residual=T(r), workspace=ws).cpu().numpy()
+    ref = a[:, :Kd].astype(np.float64) @ w16.astype(np.float64).T
+    if b is not None:
+        ref = ref + b
+    if r is not None:
+        ref = ref + r
+    assert c.shape == (M, N)
+    assert rel_err(c, ref) < 1e-5
+    if res:
+        x = T(r)
+        K.gemm_lt(A, T(w16), bias=T(b), residual=x, out=x, workspace=ws)
+        assert rel_err(x.cpu().numpy(), ref) < 1e-5
+
+
+def test_rmsnorm_and_flash_half_outputs_are_rounded_fp32_outputs(K):
+    """pe_rmsnorm_h16 and pe_flash_prefill_h16 store the fp32 kernels' values rounded to fp16
+    (nearest even), bit for bit: the operands the prefill GEMMs would round as they read them."""
+    rng = np.random.default_rng(3)
+    x = torch.from_numpy(rng.standard_normal((300, 896)).astype(np.float32)).to(DEV)
+    w = torch.from_numpy(rng.standard_normal(896).astype(np.float32)).to(DEV)
+    h16 = K.rmsnorm(x, w, 1e-6, half=True)
+    assert h16.dtype == torch.float16
+    assert torch.equal(h16, K.rmsnorm(x, w, 1e-6).half())
+    L, nh, nkv, hd = 300, 14, 2, 64
+    q = torch.from_numpy(rng.standard_normal((L, nh, hd)).astype(np.float32)).to(DEV)
+    kc = torch.from_numpy(rng.standard_normal((nkv, L + 5, hd)).astype(np.float32)).to(DEV)
+    vc = torch.from_numpy(rng.standard_normal((nkv, L + 5, hd)).astype(np.float32)).to(DEV)
+    o16 = K.flash_prefill(q, kc, vc, half=True)
+    assert o16.dtype == torch.float16
+    assert torch.equal(o16, K.flash_prefill(q, kc, vc).half())
+
+
 @pytest.mark.parametrize("M,ffn,Kd", [(300, 4864, 896), (13, 512, 3584), (129, 48, 96), (1, 16, 32),
                                       (4096, 2048, 64)])
 def test_gemm_f16_silu_equals_gemm_then_silu(K, M, ffn, Kd):

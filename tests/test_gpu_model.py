@@ -193,6 +193,28 @@ def test_prefill_f16_close_to_fp32_path(tiny):
     assert m._f16 is not None and len(m._f16) == len(m.layers)
 
 
+def test_prefill_hipblaslt_products_match_mfma_products(tiny):
+    """The matrix-core prefill with its plain products (QKV + bias, o-proj and ffn_down +
+    residual) on hipBLASLt against the same prefill with every product on pe_gemm_f16: the
+    operands are the same fp16 values, only the fp32 summation order differs (1e-4)."""
+    eng, _ = tiny
+    m = eng.model
+    ids = [(5 * i + 1) % 1024 for i in range(300)]
+    saved = m.prefill_f16_min_tokens, m.prefill_blaslt
+    out = {}
+    try:
+        m.prefill_f16_min_tokens = 2
+        for lt in (True, False):
+            m.prefill_blaslt = lt
+            cache = eng._empty_cache(len(ids) + 1)
+            lg = m.forward(torch.tensor(ids, device=eng.device), torch.arange(len(ids), device=eng.device), cache)
+            out[lt] = (lg.cpu().numpy(), cache[-1][0][:, :len(ids)].cpu().numpy())
+    finally:
+        m.prefill_f16_min_tokens, m.prefill_blaslt = saved
+    assert rel_err(out[True][0], out[False][0]) < 1e-4
+    assert rel_err(out[True][1], out[False][1]) < 1e-4
+
+
 # ---- the 7B family (BASELINE config 4): head_dim 128, 7 query heads per kv head, Q4_K/Q6_K
 # attention and FFN, untied Q8_0 LM head -----------------------------------------------------
 
