@@ -11,8 +11,10 @@
 // group x QB/16 waves (QB = 16 * max(1, 16 / group): 14 waves of 32 queries for the
 // 7-heads-per-kv-head models), so each 64-key block of K and V is read from HBM and staged in
 // LDS once for all the query heads that share it. K is staged row-major and V transposed (a
-// lane's MFMA operand -- 8 keys of one dimension -- is one 16-byte LDS read), both
-// in fp16; the next block's K/V loads are issued before the current block's MFMAs. Each wave
+// lane's MFMA operand -- 8 keys of one dimension -- is one 16-byte LDS read), both in fp16, in
+// a ring of three blocks: the loop is software-pipelined so that a wave issues the next
+// block's score MFMAs before the current block's softmax (matrix and vector ALUs busy at the
+// same time), with one barrier per block and the loads two blocks ahead in flight. Each wave
 // computes its 64 x 16 transposed score tile S^T = K Q^T (8 MFMAs), so that every lane holds
 // one query's scores: the online-softmax update (exp2 domain, scale * log2 e applied in the
 // exponent's fma) keeps one running max and sum per lane with two cross-lane steps, and the
@@ -30,6 +32,8 @@ constexpr int kFpHd = 64;
 constexpr int kFpKeys = 64;    // keys per block
 constexpr int kFpRow = 72;     // fp16 elements per LDS row (64 + 8 padding: 144 bytes)
 constexpr int kFpMaxWaves = 16;
+constexpr int kFpStages = 3;   // LDS ring depth (K / V^T blocks)
+constexpr int64_t kFpMaxCapacity = 1 << 24;  // cache positions (32-bit key offsets)
 
 // Queries per workgroup for a group size (query heads per kv head): 16 per wave, at most
 // kFpMaxWaves waves per workgroup.
@@ -61,9 +65,11 @@ PE_DEV fh8 f8_to_h8(float4 a, float4 b) {
 // GEMM (p.out then points to fp16 rows).
 template <typename OutT>
 __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_size) {
-    __shared__ __align__(16) _Float16 ks[kFpKeys * kFpRow];         // K block, [key][dim]
-    __shared__ __align__(16) _Float16 vt[kFpHd * kFpRow];           // V block transposed, [dim][key]
-    const int t = threadIdx.x, nt = blockDim.x, w = t >> 6, l = t & 63;
+    // LDS ring of kFpStages K / V^T blocks: block b is staged in slot b % kFpStages
+    __shared__ __align__(16) _Float16 ks[kFpStages * kFpKeys * kFpRow];  // K blocks, [key][dim]
+    __shared__ __align__(16) _Float16 vt[kFpStages * kFpHd * kFpRow];    // V blocks transposed, [dim][key]
+    const int t = threadIdx.x, nt = blockDim.x, l = t & 63;
+    const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave index (wave-uniform)
     const int li = l & 15, lg = l >> 4;
     const int64_t nqb = (p.L + qb_size - 1) / qb_size;
     // Workload order: rank r = (query block nqb - 1 - r / n_kv, kv head r % n_kv), heaviest
@@ -78,7 +84,7 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
     const int64_t q0 = qb * qb_size + 16 * (w / p.group);  // this wave's first query (token index)
     const float* kb = p.k + (int64_t)kvh * p.capacity * kFpHd;
     const float* vb = p.v + (int64_t)kvh * p.capacity * kFpHd;
-    const int64_t n_keys = p.pos0 + p.L;              // cache positions written
+    const int n_keys = (int)(p.pos0 + p.L);           // cache positions written (< 2^24)
     const float NEG_INF = -__builtin_huge_valf();
     const float sl2 = p.scale * 1.4426950408889634f;  // scores in log2 units: exp(x) = exp2(x log2 e)
 
@@ -98,120 +104,179 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
     // B = the Q operand above), so lane (li, lg) holds the scores of query q0 + li against keys
     // 16 jt + 4 lg + r (r < 4) of the block, and the output transposed, O^T = V^T P^T, holds
     // dims 16 d + 4 lg + r of the same query. The softmax state is then one (max, sum) per lane.
-    const int64_t qpos = p.pos0 + q0 + li;
+    const int qpos = (int)(p.pos0 + q0) + li;
     float m_run = NEG_INF, l_run = 0.f;
     fv4 o[4];
 #pragma unroll
     for (int d = 0; d < 4; ++d) o[d] = fv4{0.f, 0.f, 0.f, 0.f};
 
     const int64_t q_last = (qb + 1) * qb_size - 1 < p.L - 1 ? (qb + 1) * qb_size - 1 : p.L - 1;
-    const int64_t key_end = p.pos0 + q_last + 1;      // keys this workgroup can see
-    // K/V block loads: 64 keys x 16 float4 = 1024 float4 each, thread t takes t + nt i (i < 2,
-    // nt >= 576: at least 9 waves); slots past 1024 re-read a valid one and are not stored
-    float4 kr4[2], vr4[2];
-    auto kv_load = [&](int64_t j0) {
+    const int key_end = (int)(p.pos0 + q_last + 1);   // keys this workgroup can see
+    const int nblk = (key_end + kFpKeys - 1) / kFpKeys;
+    // K/V block loads (64 keys x 64 dims each) by the first 8 waves (every launch has at least
+    // 9): waves 0-3 load V, thread t keys 4 (t & 15) .. + 4 at dim quad t >> 4; waves 4-7 load
+    // K, thread t float4 f = t - 256 + 256 i (i < 4) = key f >> 4, dim quad f & 15 (16
+    // consecutive threads read one key row). Keys past the last written position read that
+    // position (masked out of the scores).
+    float4 r4[4];
+    auto kv_load = [&](int j0) {
+        if (w < 4) {
+            const int kg = t & 15, d4 = t >> 4;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            int f = t + nt * i;
-            f = f < 1024 ? f : f & 1023;
-            // K: 16 consecutive threads read one key row (coalesced, row-major LDS store);
-            // V: consecutive threads read consecutive keys at one dim quad, so the transposed
-            // LDS stores of a wave hit consecutive 16-bit slots (with the K mapping they were
-            // 576 bytes apart, 8-way bank conflicts)
-            const int kkey = f >> 4, kd4 = f & 15;
-            const int vkey = f & 63, vd4 = f >> 6;
-            const int64_t kr = j0 + kkey < n_keys ? j0 + kkey : n_keys - 1;
-            const int64_t vr = j0 + vkey < n_keys ? j0 + vkey : n_keys - 1;
-            kr4[i] = reinterpret_cast<const float4*>(kb + kr * kFpHd)[kd4];
-            vr4[i] = reinterpret_cast<const float4*>(vb + vr * kFpHd)[vd4];
+            for (int e = 0; e < 4; ++e) {
+                const int row = min(j0 + 4 * kg + e, n_keys - 1);
+                r4[e] = *reinterpret_cast<const float4*>(vb + (uint32_t)(row * kFpHd + 4 * d4));
+            }
+        } else if (w < 8) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int f = t - 256 + 256 * i;
+                const int row = min(j0 + (f >> 4), n_keys - 1);
+                r4[i] = *reinterpret_cast<const float4*>(kb + (uint32_t)(row * kFpHd + 4 * (f & 15)));
+            }
         }
     };
-    kv_load(0);
-    for (int64_t j0 = 0; j0 < key_end; j0 += kFpKeys) {
-        // stage this block (fp32 -> fp16), then put the next block's loads in flight. V^T rows
-        // hold the keys of each 32-key slab in the order of the P^T operand: slot 8 g + i is key
-        // 4 g + i for i < 4 and 16 + 4 g + (i - 4) for i >= 4, the keys lane group g holds.
+    // stage the loaded block in ring slot `slot` (fp32 -> fp16). V^T rows hold the keys of each
+    // 32-key slab in the order of the P^T operand: slot 8 g + i is key 4 g + i for i < 4 and
+    // 16 + 4 g + (i - 4) for i >= 4, the keys lane group g holds; a V thread's 4 keys are 4
+    // consecutive slots, one 8-byte store per dim (16 threads fill 128 contiguous bytes).
+    auto stage = [&](int slot) {
+        typedef _Float16 fh4 __attribute__((ext_vector_type(4)));
+        if (w < 4) {
+            _Float16* vd = vt + slot * (kFpHd * kFpRow);
+            const int kg = t & 15, d4 = t >> 4;
+            const int vpos = 32 * (kg >> 3) + 8 * (kg & 3) + 4 * ((kg >> 2) & 1);
+            *reinterpret_cast<fh4*>(vd + (4 * d4 + 0) * kFpRow + vpos) =
+                fh4{(_Float16)r4[0].x, (_Float16)r4[1].x, (_Float16)r4[2].x, (_Float16)r4[3].x};
+            *reinterpret_cast<fh4*>(vd + (4 * d4 + 1) * kFpRow + vpos) =
+                fh4{(_Float16)r4[0].y, (_Float16)r4[1].y, (_Float16)r4[2].y, (_Float16)r4[3].y};
+            *reinterpret_cast<fh4*>(vd + (4 * d4 + 2) * kFpRow + vpos) =
+                fh4{(_Float16)r4[0].z, (_Float16)r4[1].z, (_Float16)r4[2].z, (_Float16)r4[3].z};
+            *reinterpret_cast<fh4*>(vd + (4 * d4 + 3) * kFpRow + vpos) =
+                fh4{(_Float16)r4[0].w, (_Float16)r4[1].w, (_Float16)r4[2].w, (_Float16)r4[3].w};
+        } else if (w < 8) {
+            _Float16* kd = ks + slot * (kFpKeys * kFpRow);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int f = t + nt * i;
-            if (f < 1024) {
-                const int kkey = f >> 4, kd4 = f & 15;
-                const int vkey = f & 63, vd4 = f >> 6;
-                const int c = vkey & 31;
-                const int vpos = (vkey & 32) + 8 * ((c >> 2) & 3) + 4 * (c >> 4) + (c & 3);
-                const float4 kv = kr4[i], vv = vr4[i];
-                typedef _Float16 fh4 __attribute__((ext_vector_type(4)));
-                *reinterpret_cast<fh4*>(ks + kkey * kFpRow + 4 * kd4) =
-                    fh4{(_Float16)kv.x, (_Float16)kv.y, (_Float16)kv.z, (_Float16)kv.w};
-                vt[(4 * vd4 + 0) * kFpRow + vpos] = (_Float16)vv.x;
-                vt[(4 * vd4 + 1) * kFpRow + vpos] = (_Float16)vv.y;
-                vt[(4 * vd4 + 2) * kFpRow + vpos] = (_Float16)vv.z;
-                vt[(4 * vd4 + 3) * kFpRow + vpos] = (_Float16)vv.w;
+            for (int i = 0; i < 4; ++i) {
+                const int f = t - 256 + 256 * i;
+                *reinterpret_cast<fh4*>(kd + (f >> 4) * kFpRow + 4 * (f & 15)) =
+                    fh4{(_Float16)r4[i].x, (_Float16)r4[i].y, (_Float16)r4[i].z, (_Float16)r4[i].w};
             }
         }
-        __syncthreads();
-        kv_load(j0 + kFpKeys < key_end ? j0 + kFpKeys : j0);
-
-        // S^T = K Q^T for 4 key tiles of 16
-        fv4 sacc[4];
+    };
+    // S^T = K Q^T for the 4 key tiles of 16 of the block in ring slot `slot`
+    auto scores = [&](int slot, fv4 (&s)[4]) {
+        const _Float16* kd = ks + slot * (kFpKeys * kFpRow);
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
-            sacc[jt] = fv4{0.f, 0.f, 0.f, 0.f};
+            s[jt] = fv4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const fh8 kbv = *reinterpret_cast<const fh8*>(ks + (16 * jt + li) * kFpRow + 32 * s + 8 * lg);
-                sacc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kbv, qa[s], sacc[jt], 0, 0, 0);
+            for (int u = 0; u < 2; ++u) {
+                const fh8 kbv = *reinterpret_cast<const fh8*>(kd + (16 * jt + li) * kFpRow + 32 * u + 8 * lg);
+                s[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kbv, qa[u], s[jt], 0, 0, 0);
             }
         }
-        // causal mask (only blocks not every query of the wave sees in full: a wave-uniform
-        // test), block maximum of the raw scores over the 4 lane groups, online softmax in
-        // base 2 with scale * log2 e applied in the exponent's fma. Every query sees key 0 in
-        // the first block, so the running maximum is finite from then on.
-        const bool full = j0 + kFpKeys - 1 <= p.pos0 + q0 && j0 + kFpKeys <= n_keys;
-        float mx = NEG_INF;
+    };
+    // causal mask of block j0 (only blocks not every query of the wave sees in full: a
+    // wave-uniform test)
+    auto mask = [&](int j0, fv4 (&s)[4]) {
+        if (j0 + kFpKeys - 1 <= (int)(p.pos0 + q0) && j0 + kFpKeys <= n_keys) return;
+        asm volatile("");  // keeps this a branch: the selects cost 4 VALU per score in every block
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                if (!full) {
-                    const int64_t key = j0 + 16 * jt + 4 * lg + r;
-                    if (!(key <= qpos && key < n_keys)) sacc[jt][r] = NEG_INF;
-                }
-                mx = fmaxf(mx, sacc[jt][r]);
+                const int key = j0 + 16 * jt + 4 * lg + r;
+                if (!(key <= qpos && key < n_keys)) s[jt][r] = NEG_INF;
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+    };
+    // online softmax of one block's scores and O^T += V^T P^T from ring slot `slot`: block
+    // maximum of the raw scores over the 4 lane groups, base-2 exponent with scale * log2 e
+    // applied in its fma. Every query sees key 0 in the first block, so the running maximum is
+    // finite from then on.
+    auto softmax_pv = [&](const fv4 (&s)[4], int slot) {
+        float mx = NEG_INF;
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[jt][r]);
+        mx = swap32_max(swap16_max(mx));
         const float m_new = fmaxf(m_run, mx * sl2);
-        const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
         float psum = 0.f;
         fh8 pb[2];  // P^T operand of each 32-key slab: keys 4 lg + i, 16 + 4 lg + i
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float e = __builtin_amdgcn_exp2f(fmaf(sacc[jt][r], sl2, -m_new));
+                const float e = __builtin_amdgcn_exp2f(fmaf(s[jt][r], sl2, -m_new));
                 psum += e;
                 pb[jt >> 1][4 * (jt & 1) + r] = (_Float16)e;
             }
-        psum += __shfl_xor(psum, 16);
-        psum += __shfl_xor(psum, 32);
-        l_run = l_run * corr + psum;
+        psum = swap32_sum(swap16_sum(psum));
+        // rescale by 2^(m_run - m_new) only when some lane's maximum grew: otherwise the factor
+        // is exactly 1 and the products would change nothing (a wave-uniform branch)
+        if (__builtin_amdgcn_ballot_w64(m_new != m_run)) {
+            const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run = l_run * corr + psum;
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o[d][r] *= corr;
+        } else {
+            l_run = l_run + psum;
+        }
         m_run = m_new;
+        // A = V^T (16 dims x 32 keys) per dim tile, B = P^T (32 keys x 16 queries)
+        const _Float16* vd = vt + slot * (kFpHd * kFpRow);
 #pragma unroll
-        for (int d = 0; d < 4; ++d)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) o[d][r] *= corr;
-
-        // O^T += V^T P^T: A = V^T (16 dims x 32 keys) per dim tile, B = P^T (32 keys x 16 queries)
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
+        for (int u = 0; u < 2; ++u) {
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-                const fh8 va = *reinterpret_cast<const fh8*>(vt + (16 * d + li) * kFpRow + 32 * s + 8 * lg);
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[s], o[d], 0, 0, 0);
+                const fh8 va = *reinterpret_cast<const fh8*>(vd + (16 * d + li) * kFpRow + 32 * u + 8 * lg);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[u], o[d], 0, 0, 0);
             }
         }
-        __syncthreads();  // every wave is done with K / V before the next block is staged
+    };
+
+    // Software pipeline: while block b's softmax runs on the vector ALUs, block b + 1's score
+    // MFMAs run on the matrix cores, and block b + 2's loads are in flight. One barrier per
+    // block: when a wave stages block b + 1 (slot (b + 1) % 3), every wave has passed the
+    // barrier after block b's staging, so none still reads block b - 1's K (its scores were
+    // computed before that barrier) and the slowest still reads only block b's K / V (slot
+    // b % 3) and block b - 1's V (slot (b - 1) % 3).
+    kv_load(0);
+    stage(0);
+    __syncthreads();
+    kv_load(kFpKeys < key_end ? kFpKeys : 0);
+    fv4 sa[4], sb[4];
+    scores(0, sa);
+    int slot = 0;
+    // one pipelined block: softmax and P.V of block b (scores in cur, K / V in ring slot
+    // `slot`), scores of block b + 1 into nxt
+    auto step = [&](int b, fv4 (&cur)[4], fv4 (&nxt)[4]) {
+        const int j0 = b * kFpKeys;
+        const int nslot = slot == kFpStages - 1 ? 0 : slot + 1;
+        stage(nslot);
+        __syncthreads();
+        kv_load(j0 + 2 * kFpKeys < key_end ? j0 + 2 * kFpKeys : j0 + kFpKeys);
+        mask(j0, cur);
+        scores(nslot, nxt);
+        softmax_pv(cur, slot);
+        slot = nslot;
+    };
+    // unrolled by two so that the score tiles alternate between sa and sb without copies
+    int b = 0;
+    for (; b + 2 < nblk; b += 2) {
+        step(b, sa, sb);
+        step(b + 1, sb, sa);
+    }
+    if (b + 1 < nblk) {
+        step(b, sa, sb);
+        mask((b + 1) * kFpKeys, sb);
+        softmax_pv(sb, slot);
+    } else {
+        mask(b * kFpKeys, sa);
+        softmax_pv(sa, slot);
     }
 
     // out: O[query q0 + li][dim 16 d + 4 lg + r] / l
@@ -230,7 +295,6 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
             }
     }
 }
-
 }  // namespace pe
 
 using namespace pe;
@@ -240,7 +304,7 @@ static int flash_prefill(const float* q, int64_t q_stride, const float* k_cache,
                          int64_t capacity, int64_t L, int64_t pos0, float scale, void* out,
                          int64_t out_stride, bool half_out, pe_stream_t stream) {
     if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > kFpMaxWaves ||
-        head_dim != kFpHd || capacity <= 0 || L < 0 || pos0 < 0 || pos0 + L > capacity || n_kv > 65535)
+        head_dim != kFpHd || capacity <= 0 || capacity > kFpMaxCapacity || L < 0 || pos0 < 0 || pos0 + L > capacity || n_kv > 65535)
         return PE_ERR_SHAPE;
     if (L == 0) return PE_OK;
     const int group = n_head / n_kv;
@@ -253,7 +317,7 @@ static int flash_prefill(const float* q, int64_t q_stride, const float* k_cache,
         return PE_ERR_ALIGN;
     FlashParams p{q, q_stride, k_cache, v_cache, n_head / n_kv, n_kv, capacity, L, pos0, scale, (float*)out,
                   out_stride};
-    const int waves = group * (qb / 16);  // 9..16 (at least 576 threads: kv_load assumes it)
+    const int waves = group * (qb / 16);  // 9..16 (kv_load and stage use the first 8 waves)
     const int64_t nblocks = (L + qb - 1) / qb * (int64_t)n_kv;
     if (nblocks > 0x7FFFFFFF) return PE_ERR_SHAPE;
     const dim3 grid((unsigned)nblocks);
