@@ -81,6 +81,7 @@ def kernel_launchers(eng, which: str):
     L0 = m.layers[0]
     XU, YU = K.LAYOUT_X_UT, K.LAYOUT_Y_UT
     tn = lambda w: K.TYPE_NAMES.get(w.ggml_type, w.ggml_type)
+    kn = lambda w: "k_mgemv" if K.use_mfma_gemv and w.mfma is not None else "k_qgemv"
     hd, nh, nkv, h = cfg.head_dim, cfg.n_head, cfg.n_kv_head, cfg.hidden
     # the decode step's own launch configuration: activations in the unit-transposed layout
     x = torch.randn(h, device=eng.device)
@@ -96,7 +97,7 @@ def kernel_launchers(eng, which: str):
     elif which == "gate_up_norm":
         # the decode step without attn_gproj (head_dim 128: the 7B): RMSNorm, [gate; up], SiLU
         ws = (L0.w_gate_up,)
-        name = f"k_qgemv ({tn(ws[0])}, rmsnorm+SiLU pair) gate/up {h}->2x{cfg.ffn_dim}"
+        name = f"{kn(ws[0])} ({tn(ws[0])}, rmsnorm+SiLU pair) gate/up {h}->2x{cfg.ffn_dim}"
         fn = lambda w: K.qgemv_norm_silu(x, L0.ffn_norm_ut, w, cfg.eps, layout=XU | YU)
         io = 4 * (h * 2 + cfg.ffn_dim)
     elif which == "lm_head":
@@ -110,7 +111,7 @@ def kernel_launchers(eng, which: str):
         want = GGML_Q6_K if which == "down_q6k" else GGML_Q4_K
         li = next((i for i, Lr in enumerate(m.layers) if Lr.w_down.ggml_type == want), 0)
         ws = (m.layers[li].w_down,)
-        name = f"k_qgemv ({tn(ws[0])}, +residual) ffn_down {cfg.ffn_dim}->{h}"
+        name = f"{kn(ws[0])} ({tn(ws[0])}, +residual) ffn_down {cfg.ffn_dim}->{h}"
         a = torch.randn(cfg.ffn_dim, device=eng.device)
         fn = lambda w: K.qgemv(a, w, residual=x, layout=XU | YU)
         io = 4 * (cfg.ffn_dim + 2 * h)
@@ -141,15 +142,14 @@ def kernel_launchers(eng, which: str):
         # the o-projection with the residual where attn_gproj does not apply (head_dim 128)
         ws = (L0.wo,)
         a = torch.randn(nh * hd, device=eng.device)
-        name = f"k_qgemv ({tn(ws[0])}, +residual) o-proj {nh * hd}->{h}"
+        name = f"{kn(ws[0])} ({tn(ws[0])}, +residual) o-proj {nh * hd}->{h}"
         fn = lambda w: K.qgemv(a, w, residual=x, layout=XU | YU)
         io = 4 * (nh * hd + 2 * h)
     else:
         raise SystemExit(f"unknown --kernel {which}")
     nbytes = sum(w.nbytes for w in ws)
     copies = max(1, -(-(1 << 30) // nbytes))
-    sets = [ws] + [tuple(K.QWeight(w.data.clone(), w.ggml_type, w.n, w.k) for w in ws)
-                   for _ in range(copies - 1)]
+    sets = [ws] + [tuple(w.copy() for w in ws) for _ in range(copies - 1)]
     return [(lambda st=st: fn(*st)) for st in sets], nbytes + io, name
 
 
@@ -237,7 +237,7 @@ def micro(device: str) -> None:
     shapes += [(Q4_K, 4864, 896), (Q6_K, 4864, 896)]
     for i, (t, k, n) in enumerate(shapes):
         w0 = qweight(t, n, k, 100 + i)
-        ws = [w0] + [K.QWeight(w0.data.clone(), t, n, k) for _ in range(len(copies(lambda: 0, w0.nbytes)) - 1)]
+        ws = [w0] + [w0.copy() for _ in range(len(copies(lambda: 0, w0.nbytes)) - 1)]
         x = torch.randn(k, device=device)
         res = torch.randn(n, device=device)
         nbytes = w0.nbytes + 4 * (k + 2 * n)
@@ -257,7 +257,7 @@ def micro(device: str) -> None:
     h = 896
     wq, wk, wv = qweight(Q5_0, nh * hd, h, 1), qweight(Q5_0, nkv * hd, h, 2), qweight(Q8_0, nkv * hd, h, 3)
     qkv_bytes = wq.nbytes + wk.nbytes + wv.nbytes
-    trip = [(wq, wk, wv)] + [tuple(K.QWeight(w.data.clone(), w.ggml_type, w.n, w.k) for w in (wq, wk, wv))
+    trip = [(wq, wk, wv)] + [tuple(w.copy() for w in (wq, wk, wv))
                              for _ in range(len(copies(lambda: 0, qkv_bytes)) - 1)]
     x = K.to_ut(torch.randn(h, device=device))
     nw = K.to_ut(torch.ones(h, device=device))
@@ -315,15 +315,14 @@ def micro7b(device: str) -> None:
     ]
     for name, t, n, k, fn, io in cases:
         w0 = qweight(t, n, k)
-        ws = [w0] + [K.QWeight(w0.data.clone(), t, n, k) for _ in range(ncopies(w0.nbytes) - 1)]
+        ws = [w0] + [w0.copy() for _ in range(ncopies(w0.nbytes) - 1)]
         us = time_kernel([(lambda ww=ww: fn(ww)) for ww in ws], 200)
         emit("config4_gemv", us, w0.nbytes + io, kernel=name)
         del ws, w0
         torch.cuda.empty_cache()
     wq, wk, wv = qweight(Q4_K, nh * hd, h), qweight(Q4_K, nkv * hd, h), qweight(Q6_K, nkv * hd, h)
     qkv_bytes = wq.nbytes + wk.nbytes + wv.nbytes
-    trip = [(wq, wk, wv)] + [tuple(K.QWeight(w.data.clone(), w.ggml_type, w.n, w.k) for w in (wq, wk, wv))
-                             for _ in range(ncopies(qkv_bytes) - 1)]
+    trip = [(wq, wk, wv)] + [tuple(w.copy() for w in (wq, wk, wv)) for _ in range(ncopies(qkv_bytes) - 1)]
     bq, bk, bv = (torch.randn(m * hd, device=device) for m in (nh, nkv, nkv))
     cos = torch.randn(4096, hd // 2, device=device)
     sin = torch.randn(4096, hd // 2, device=device)

@@ -197,6 +197,34 @@ int pe_qgemv_rmsnorm_silu(int ggml_type, const void* w_tiled, int64_t ffn, int64
                           const float* x, const float* norm_w, float eps, float* act, int layout,
                           pe_stream_t stream);
 
+/* Bytes of the "MFMA layout" of an (n x k) Q4_K or Q6_K matrix (k % 256 == 0): rows in groups
+ * of 16 (zero-padded), each (row group, super-block) holding the 16 rows' codes arranged as
+ * the B operands of v_mfma_i32_16x16x32_i8 and their headers / scales (2304 bytes for Q4_K,
+ * 3360 for Q6_K: the GGUF bytes of 16 blocks). -1 for another type or shape. */
+int64_t pe_mfma_bytes(int ggml_type, int64_t n, int64_t k);
+
+/* Raw GGUF blocks of an (n x k) Q4_K / Q6_K matrix -> MFMA layout (pe_mfma_bytes bytes,
+ * 16-byte aligned). The weights of the pe_mgemv products; the same bytes rearranged as the
+ * reference's unpack_* planes (dequant.py:79-168) rearrange them for its GEMVs. */
+int pe_repack_mfma(int ggml_type, const void* blocks, void* w_mfma, int64_t n, int64_t k,
+                   pe_stream_t stream);
+
+/* Decode GEMV of a large Q4_K / Q6_K matrix on the integer matrix cores, from its MFMA layout:
+ *   silu == 0: y[n] = W h + residual[n] (residual may be NULL),
+ *   silu != 0: y[j] = silu(g_j) * u_j, [g; u] = W h over the 2 n rows of W (n % 16 == 0,
+ *              residual must be NULL),
+ * with h = rmsnorm(x) * norm_w (eps) when norm_w is not NULL, else h = x. The activation is
+ * split exactly into four int8 planes per 32 elements (every element to 2^-28 of its
+ * sub-block's largest), the integer products are exact, scales and sums fp32. k % 256 == 0,
+ * k <= 2^20 (the planes of x stay in LDS: about 144 bytes per 32 elements). layout:
+ * PE_LAYOUT_X_UT (x, norm_w) / PE_LAYOUT_Y_UT (y, residual; n % 32 == 0). Deterministic.
+ * Replaces q4_k_gemv / q6_k_gemv (kernels.py:286, :326) with the fused RMSNorm + gate/up +
+ * SiLU and the residual adds of model.py:213-235, for matrices large enough that HBM bounds
+ * them (the 7B-architecture model's gate/up, ffn_down and o-projection). */
+int pe_mgemv(int ggml_type, const void* w_mfma, int64_t n, int64_t k, const float* x,
+             const float* norm_w, float eps, const float* residual, float* y, int silu,
+             int layout, pe_stream_t stream);
+
 /* Greedy LM head: logits = W (rmsnorm(x) * norm_w) as pe_qgemv_rmsnorm (y may be NULL), and
  * the index of the largest logit with torch.argmax's rule (first index among equal values,
  * NaN counts as largest), computed on the device. It replaces

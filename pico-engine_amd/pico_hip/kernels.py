@@ -19,6 +19,8 @@ from __future__ import annotations
 import ctypes
 from dataclasses import dataclass
 
+import os
+
 import torch
 
 from ._lib import (LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT, QkvArgs, StepArgs, StepLayer, check,
@@ -78,6 +80,9 @@ class QWeight:
     ggml_type: int
     n: int
     k: int
+    # the same matrix in the MFMA layout (pe_repack_mfma) when the decode GEMVs run it on the
+    # integer matrix cores (large Q4_K / Q6_K matrices, see mfma_eligible)
+    mfma: torch.Tensor | None = None
 
     @property
     def shape(self) -> tuple[int, int]:
@@ -86,6 +91,11 @@ class QWeight:
     @property
     def nbytes(self) -> int:
         return self.data.numel()
+
+    def copy(self) -> "QWeight":
+        """A distinct device copy (both layouts)."""
+        return QWeight(self.data.clone(), self.ggml_type, self.n, self.k,
+                       None if self.mfma is None else self.mfma.clone())
 
     def __repr__(self) -> str:
         return f"QWeight({TYPE_NAMES[self.ggml_type]}, n={self.n}, k={self.k})"
@@ -117,8 +127,36 @@ def dequantize(ggml_type: int, blocks: torch.Tensor, n: int, out: torch.Tensor |
     return out
 
 
-def pack_weight(blocks: torch.Tensor, ggml_type: int, n: int, k: int) -> QWeight:
-    """Raw GGUF blocks of an (n x k) tensor (device uint8) -> tiled QWeight."""
+# Decode GEMVs of Q4_K / Q6_K matrices of at least this many weights (k % 256 == 0) run on the
+# integer matrix cores (pe_mgemv) from a second copy in the MFMA layout: the 7B model's
+# gate/up and ffn_down, whose per-lane dot products bound the tiled GEMV on the vector ALU.
+# Smaller matrices (the 7B o-projection, 12.8M weights: one item per wave, latency-bound)
+# keep the tiled GEMVs only (measured: 6.3 vs 5.7 us).
+MFMA_MIN_WEIGHTS = 1 << 25
+# off (or PICO_MFMA_GEMV=0 in the environment): every decode GEMV on the tiled kernels
+use_mfma_gemv = os.environ.get("PICO_MFMA_GEMV", "1") != "0"
+
+
+def mfma_eligible(ggml_type: int, n: int, k: int) -> bool:
+    return ggml_type in (GGML_Q4_K, GGML_Q6_K) and k % 256 == 0 and n * k >= MFMA_MIN_WEIGHTS
+
+
+def repack_mfma(blocks: torch.Tensor, ggml_type: int, n: int, k: int) -> torch.Tensor:
+    """Raw GGUF blocks of an (n x k) Q4_K / Q6_K matrix -> its MFMA layout (device uint8)."""
+    dev = _on_gpu(blocks)
+    size = lib.pe_mfma_bytes(ggml_type, n, k)
+    if size < 0:
+        raise ValueError(f"no MFMA layout for a {n}x{k} {TYPE_NAMES.get(ggml_type, ggml_type)} matrix")
+    if blocks.numel() != nbytes_for(ggml_type, n * k):
+        raise ValueError(f"{blocks.numel()} bytes for a {n}x{k} {TYPE_NAMES[ggml_type]} tensor")
+    out = torch.empty(size, device=dev, dtype=torch.uint8)
+    check(lib.pe_repack_mfma(ggml_type, _ptr(blocks), _ptr(out), n, k, _stream(dev)), "pe_repack_mfma")
+    return out
+
+
+def pack_weight(blocks: torch.Tensor, ggml_type: int, n: int, k: int, mfma: bool | None = None) -> QWeight:
+    """Raw GGUF blocks of an (n x k) tensor (device uint8) -> tiled QWeight, with the MFMA
+    layout copy as well when ``mfma`` (default: when mfma_eligible)."""
     dev = _on_gpu(blocks)
     if ggml_type not in MATRIX_TYPES:
         raise ValueError(f"no GEMV kernel for {TYPE_NAMES.get(ggml_type, ggml_type)}")
@@ -127,7 +165,40 @@ def pack_weight(blocks: torch.Tensor, ggml_type: int, n: int, k: int) -> QWeight
         raise ValueError(f"{blocks.numel()} bytes for a {n}x{k} {TYPE_NAMES[ggml_type]} tensor, expected {size}")
     data = torch.empty(size, device=dev, dtype=torch.uint8)
     check(lib.pe_repack(ggml_type, _ptr(blocks), _ptr(data), n, k, _stream(dev)), "pe_repack")
-    return QWeight(data, ggml_type, n, k)
+    if mfma is None:
+        mfma = mfma_eligible(ggml_type, n, k)
+    return QWeight(data, ggml_type, n, k, repack_mfma(blocks, ggml_type, n, k) if mfma else None)
+
+
+def _use_mfma(w: QWeight) -> bool:
+    return use_mfma_gemv and w.mfma is not None
+
+
+def _aligned16(t: torch.Tensor | None) -> torch.Tensor | None:
+    return t if t is None or t.data_ptr() % 16 == 0 else t.clone()
+
+
+def mgemv(x: torch.Tensor, w: QWeight, norm_w: torch.Tensor | None = None, eps: float = 0.0,
+          residual: torch.Tensor | None = None, silu: bool = False, out: torch.Tensor | None = None,
+          layout: int = LAYOUT_NATURAL) -> torch.Tensor:
+    """pe_mgemv: W h (+ residual) or silu(g) * u over [g; u] = W h (``silu``), h = rmsnorm(x) *
+    norm_w when ``norm_w`` is given, on the integer matrix cores from w.mfma."""
+    if w.mfma is None:
+        raise ValueError(f"{w} has no MFMA layout copy")
+    dev = _on_gpu(x, w.mfma, norm_w, residual)
+    x = _aligned16(_f32c(x.reshape(-1)))
+    if x.numel() != w.k:
+        raise ValueError(f"x has {x.numel()} elements, weight expects {w.k}")
+    nw = None if norm_w is None else _aligned16(_f32c(norm_w.reshape(-1)))
+    res = None if residual is None else residual.reshape(-1).float().contiguous()
+    if silu and (w.n % 32 or res is not None):
+        raise ValueError("the SiLU product needs [gate; up] rows in groups of 16 and no residual")
+    n = w.n // 2 if silu else w.n
+    if out is None:
+        out = torch.empty(n, device=dev, dtype=torch.float32)
+    check(lib.pe_mgemv(w.ggml_type, _ptr(w.mfma), n, w.k, _ptr(x), _ptr(nw), float(eps), _ptr(res),
+                       _ptr(out), 1 if silu else 0, layout, _stream(dev)), "pe_mgemv")
+    return out
 
 
 def dequantize_weight(w: QWeight) -> torch.Tensor:
@@ -346,7 +417,10 @@ def qgemv(x: torch.Tensor, w: QWeight, residual: torch.Tensor | None = None,
           bias: torch.Tensor | None = None, out: torch.Tensor | None = None,
           layout: int = LAYOUT_NATURAL) -> torch.Tensor:
     """y = W x (+ bias) (+ residual) for a tiled quantized W (M = 1); ``layout`` bits say
-    which of x / (y, residual) are unit-transposed."""
+    which of x / (y, residual) are unit-transposed. A W with an MFMA layout copy runs on
+    pe_mgemv (without a bias)."""
+    if bias is None and _use_mfma(w):
+        return mgemv(x, w, residual=residual, out=out, layout=layout)
     dev = _on_gpu(x, w.data, residual, bias)
     x = _f32c(x.reshape(-1))
     if x.numel() != w.k:
@@ -388,7 +462,10 @@ def q4_k_gemv(x: torch.Tensor, w: QWeight, residual: torch.Tensor | None = None)
 
 def qgemv_norm(x: torch.Tensor, weight: torch.Tensor, w: QWeight, eps: float,
                out: torch.Tensor | None = None, layout: int = LAYOUT_NATURAL) -> torch.Tensor:
-    """W (rmsnorm(x) * weight) in one launch, any quantized format."""
+    """W (rmsnorm(x) * weight) in one launch, any quantized format (pe_mgemv for a W with an
+    MFMA layout copy)."""
+    if _use_mfma(w):
+        return mgemv(x, w, norm_w=weight, eps=eps, out=out, layout=layout)
     dev = _on_gpu(x, weight, w.data)
     x = _f32c(x.reshape(-1))
     nw = _f32c(weight.reshape(-1))
@@ -543,7 +620,10 @@ def q5_0_gemv_norm(x: torch.Tensor, weight: torch.Tensor, w: QWeight, eps: float
 
 def qgemv_norm_silu(x: torch.Tensor, weight: torch.Tensor | None, w: QWeight, eps: float,
                     out: torch.Tensor | None = None, layout: int = LAYOUT_NATURAL) -> torch.Tensor:
-    """silu(g) * u with [g; u] = W (rmsnorm(x) * weight), W = [gate; up] (2*ffn rows)."""
+    """silu(g) * u with [g; u] = W (rmsnorm(x) * weight), W = [gate; up] (2*ffn rows)
+    (pe_mgemv for a W with an MFMA layout copy whose ffn is a multiple of 16)."""
+    if _use_mfma(w) and w.n % 32 == 0:
+        return mgemv(x, w, norm_w=weight, eps=eps, silu=True, out=out, layout=layout)
     dev = _on_gpu(x, weight, w.data)
     if w.n % 2:
         raise ValueError("gate/up weight needs an even number of rows")
@@ -776,7 +856,7 @@ __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "
            "rmsnorm", "rope", "silu_mul", "decode_attn", "decode_attn_workspace", "qgemv",
            "q8_0_gemv", "q5_0_gemv", "q5_0_gemv_norm", "q6_k_gemv", "q4_k_gemv", "qgemv_norm",
            "qgemv_norm_silu", "qkv_rmsnorm_rope", "qgemv_sum_norm_silu", "qgemm", "kv_write", "prefill_attn",
-           "gemm_lt", "gemm_lt_workspace",
+           "gemm_lt", "gemm_lt_workspace", "mgemv", "repack_mfma", "mfma_eligible", "MFMA_MIN_WEIGHTS",
            "attn_gproj", "attn_gproj_supported", "qgemv_norm_argmax", "dequantize_weight_f16",
            "DecodeStep", "decode_step_supported", "decode_step_workspace",
            "gemm_f16", "gemm_f16_silu", "interleave_gate_up_f16", "flash_prefill",
