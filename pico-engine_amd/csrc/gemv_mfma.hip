@@ -34,7 +34,8 @@
 //     b and + b + 4 in the high one), then the 16 rows' 16-byte headers (d, dmin, the 12
 //     packed 6-bit scale/min bytes) as stored in the GGUF block.
 //   Q6_K (3360 bytes): the low four code bits in the Q4_K arrangement, then the high two bits
-//     [2][64 lanes][4 sub-blocks][16 bits] (nibble b = high bits of codes b and b + 4), the 16
+//     [2][64 lanes][2 sub-block pairs][32 bits] (byte b: the high bits of codes b and b + 4 of
+//     the pair's first sub-block in its high nibble, of the second in its low nibble), the 16
 //     rows' 16 int8 scales, the 16 rows' fp16 d.
 //
 // Work: a workgroup owns up to 16 tiles (one row group, or a gate group and its up group);
@@ -112,11 +113,13 @@ __global__ void k_repack_mfma(const uint8_t* __restrict__ raw, uint8_t* __restri
                     const uint32_t lo = valid ? raw_code<T>(blk, base + b) : 0u;
                     const uint32_t hi = valid ? raw_code<T>(blk, base + b + 4) : 0u;
                     wd |= ((lo & 15u) | ((hi & 15u) << 4)) << (8 * b);
-                    hq |= ((lo >> 4) | ((hi >> 4) << 2)) << (4 * b);
+                    // high bits of codes b and b + 4 as one nibble of byte b: the high nibble
+                    // for even jj, the low nibble for odd jj
+                    hq |= ((lo >> 4) | ((hi >> 4) << 2)) << (8 * b + ((jj & 1) ? 0 : 4));
                 }
                 words[jj] = wd;
-                if (jj < 2) high |= hq << (16 * jj);
-                else high2 |= hq << (16 * (jj - 2));
+                if (jj < 2) high |= hq;
+                else high2 |= hq;
             }
             uint32_t* cw = reinterpret_cast<uint32_t*>(ob + 1024 * c + 16 * l);
             for (int jj = 0; jj < 4; ++jj) cw[jj] = words[jj];
@@ -161,27 +164,40 @@ struct MgArgs {
 // and the stores and residual loads come after the last weight load).
 constexpr int kMgMaxTilesPerWg = 16;
 
-// LDS: planes [k/32][4][32] int8, per sub-block {2^(e - 27), X, X of the first 16, X of the
-// last 16}, the partials [tile][wave][gate 16 | up 16], the sum-of-squares partials.
-inline size_t mg_lds_bytes(int k) {
-    return (size_t)(k / 32) * (128 + 16) + (size_t)kMgMaxTilesPerWg * kMgMaxWaves * 32 * sizeof(float) +
-           16 * sizeof(float);
+// Q4_K matrices with k up to this keep their activation planes in LDS "expanded": each
+// sub-block as the whole 16-row A operand (its four planes in rows 4 (j % 4) .. + 3, zeros
+// elsewhere, 512 bytes), so that a lane reads its A value without selecting it against zero.
+constexpr int kMgExpandMaxK = 4096;
+
+// LDS: planes [k/32][4][32] int8 (expanded: [k/32][16][32]), per sub-block {2^(e - 27), X,
+// -32 X of the first 16, -32 X of the last 16}, the partials [tile][wave][gate 16 | up 16],
+// the sum-of-squares partials.
+inline size_t mg_lds_bytes(int k, bool expanded) {
+    return (size_t)(k / 32) * ((expanded ? 512 : 128) + 16) +
+           (size_t)kMgMaxTilesPerWg * kMgMaxWaves * 32 * sizeof(float) + 16 * sizeof(float);
 }
 
 PE_DEV int64_t mg_index(int64_t i, int64_t len, bool ut) {
     return ut ? ((i & 31) >> 2) * (len >> 5) * 4 + (i >> 5) * 4 + (i & 3) : i;
 }
 
-template <int T, bool SILU, bool NORM>
+template <int T, bool SILU, bool NORM, bool EXP>
 __global__ __launch_bounds__(1024) void k_mgemv(MgArgs a) {
     extern __shared__ __align__(16) uint8_t mg_lds[];
     constexpr int kB = MgFmt<T>::kBlock;
     const int t = threadIdx.x, nt = blockDim.x, l = t & 63;
     const int w = __builtin_amdgcn_readfirstlane(t >> 6);
     const int nsub = a.k >> 5;
+    static_assert(!EXP || T == PE_TYPE_Q4_K, "expanded planes: Q4_K");
+    constexpr int kPlaneStride = EXP ? 512 : 128;  // LDS bytes per sub-block of planes
     uint8_t* planes = mg_lds;
-    float4* sx = reinterpret_cast<float4*>(mg_lds + (size_t)nsub * 128);
-    float* red = reinterpret_cast<float*>(mg_lds + (size_t)nsub * 144);
+    float4* sx = reinterpret_cast<float4*>(mg_lds + (size_t)nsub * kPlaneStride);
+    float* red = reinterpret_cast<float*>(mg_lds + (size_t)nsub * (kPlaneStride + 16));
+    if constexpr (EXP) {  // the zero rows of the expanded A operands
+        for (int i = t; i < nsub * (kPlaneStride / 16); i += nt)
+            reinterpret_cast<uint4*>(planes)[i] = make_uint4(0u, 0u, 0u, 0u);
+        __syncthreads();
+    }
     float* ssp = red + kMgMaxTilesPerWg * kMgMaxWaves * 32;
 
     // Item range of this wave (the same in every tile). A wave walks its (tile, item) pairs
@@ -298,8 +314,9 @@ __global__ __launch_bounds__(1024) void k_mgemv(MgArgs a) {
             }
 #pragma unroll
             for (int p = 0; p < 4; ++p)
-                *reinterpret_cast<uint32_t*>(planes + (size_t)js * 128 + 32 * p + 4 * qq) = pw[p];
-            if (qq == 0) sx[js] = make_float4(sc, sfull, shalf, sother);
+                *reinterpret_cast<uint32_t*>(planes + (size_t)js * kPlaneStride +
+                                             32 * (EXP ? 4 * (js & 3) + p : p) + 4 * qq) = pw[p];
+            if (qq == 0) sx[js] = make_float4(sc, sfull, -32.0f * shalf, -32.0f * sother);
         }
     };
     // The activation loads of up to kPlaneBatch quads per thread are issued together (one
@@ -391,9 +408,15 @@ __global__ __launch_bounds__(1024) void k_mgemv(MgArgs a) {
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj) {
                     const int js = 8 * s + 4 * c + jj;
-                    const uint2 pl = *reinterpret_cast<const uint2*>(planes + (size_t)js * 128 + 32 * (ar & 3) + 8 * g);
-                    const bool mine = (ar >> 2) == jj;
-                    const long A = (long)(((uint64_t)(mine ? pl.y : 0u) << 32) | (mine ? pl.x : 0u));
+                    long A;
+                    if constexpr (EXP) {  // row ar of the expanded operand (zeros but in rows 4 jj ..)
+                        const uint2 pl = *reinterpret_cast<const uint2*>(planes + (size_t)js * 512 + 32 * ar + 8 * g);
+                        A = (long)(((uint64_t)pl.y << 32) | pl.x);
+                    } else {
+                        const uint2 pl = *reinterpret_cast<const uint2*>(planes + (size_t)js * 128 + 32 * (ar & 3) + 8 * g);
+                        const bool mine = (ar >> 2) == jj;
+                        A = (long)(((uint64_t)(mine ? pl.y : 0u) << 32) | (mine ? pl.x : 0u));
+                    }
                     const uint32_t u = word_of(cw, jj);
                     const long B = (long)(((uint64_t)((u >> 4) & 0x0F0F0F0Fu) << 32) | (u & 0x0F0F0F0Fu));
                     C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, C, 0, 0, 0);
@@ -411,9 +434,9 @@ __global__ __launch_bounds__(1024) void k_mgemv(MgArgs a) {
                                (__builtin_amdgcn_ubfe((uint32_t)hd.z, 8 * g + 6, 2) << 4));
                 }
                 const float4 sj = sx[js];
-                float v = fmaf((float)C[2], 128.0f, (float)C[3]);
-                v = fmaf((float)C[1], 16384.0f, v);
-                v = fmaf((float)C[0], 2097152.0f, v);
+                // planes 1-3 combined exactly in int32 (C1 < 2^16: the sum < 2^30)
+                const int low = C[1] * 16384 + C[2] * 128 + C[3];
+                const float v = fmaf((float)C[0], 2097152.0f, (float)low);
                 part = fmaf(d * (float)sc * sj.x, v, part);
                 part = fmaf(-(dmin * (float)mn), sj.y, part);
             }
@@ -434,12 +457,13 @@ __global__ __launch_bounds__(1024) void k_mgemv(MgArgs a) {
                         const bool mine = (ar >> 3) == j2 && ((ar >> 2) & 1) == (g >> 1);
                         const long A = (long)(((uint64_t)(mine ? pl.y : 0u) << 32) | (mine ? pl.x : 0u));
                         const uint32_t u = word_of(cw, jj);
-                        const uint32_t hq = ((jj < 2 ? hw.x : hw.y) >> (16 * (jj & 1))) & 0xFFFFu;
-                        // nibble b of hq -> bits 4..7 of byte b
-                        uint32_t e = (hq | (hq << 8)) & 0x00FF00FFu;
-                        e = ((e | (e << 4)) & 0x0F0F0F0Fu) << 4;
-                        const uint32_t lo = (u & 0x0F0F0F0Fu) | (e & 0x30303030u);
-                        const uint32_t hi = ((u >> 4) & 0x0F0F0F0Fu) | ((e >> 2) & 0x30303030u);
+                        // the high bits sit in one nibble per byte (high for even jj, low for
+                        // odd): shifted to bits 4-5 and masked
+                        const uint32_t hw2 = jj < 2 ? hw.x : hw.y;
+                        const uint32_t el = ((jj & 1) ? hw2 << 4 : hw2) & 0x30303030u;
+                        const uint32_t eh = ((jj & 1) ? hw2 << 2 : hw2 >> 2) & 0x30303030u;
+                        const uint32_t lo = (u & 0x0F0F0F0Fu) | el;
+                        const uint32_t hi = ((u >> 4) & 0x0F0F0F0Fu) | eh;
                         const long B = (long)(((uint64_t)hi << 32) | lo);
                         C = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, C, 0, 0, 0);
                     }
@@ -448,12 +472,12 @@ __global__ __launch_bounds__(1024) void k_mgemv(MgArgs a) {
                     const int grp = 2 * j + (g & 1);  // scale group (16 weights)
                     const int sc = sext8(word_of(hd, grp >> 2), grp & 3);
                     const float4 sj = sx[js];
-                    float v = fmaf((float)C[2], 128.0f, (float)C[3]);
-                    v = fmaf((float)C[1], 16384.0f, v);
+                    // planes 2 and 3 combined exactly in int32 (C2 < 2^18)
+                    float v = fmaf((float)C[1], 16384.0f, (float)(C[2] * 128 + C[3]));
                     v = fmaf((float)C[0], 2097152.0f, v);
-                    const float ds = d * (float)sc;
-                    part = fmaf(ds * sj.x, v, part);
-                    part = fmaf(ds * -32.0f, (g & 1) ? sj.w : sj.z, part);
+                    // d sc (S V - 32 X): -32 X of the scale group is stored with the planes
+                    const float tv = fmaf(sj.x, v, (g & 1) ? sj.w : sj.z);
+                    part = fmaf(d * (float)sc, tv, part);
                 }
             }
         }
@@ -566,7 +590,7 @@ namespace {
 
 // Raises the kernel's dynamic LDS limit once per device, then launches min(tiles, resident
 // workgroups) workgroups (they loop over the tiles).
-template <int T, bool SILU, bool NORM>
+template <int T, bool SILU, bool NORM, bool EXP>
 int launch_mgemv(const MgArgs& a, size_t lds, hipStream_t s) {
     static int configured[64] = {0};
     int dev = 0;
@@ -576,7 +600,7 @@ int launch_mgemv(const MgArgs& a, size_t lds, hipStream_t s) {
         if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeSharedMemPerBlockOptin, dev) != hipSuccess ||
             max_lds <= 0)
             (void)hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
-        if (hipFuncSetAttribute((const void*)k_mgemv<T, SILU, NORM>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        if (hipFuncSetAttribute((const void*)k_mgemv<T, SILU, NORM, EXP>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 max_lds) != hipSuccess)
             return PE_ERR_LAUNCH;
         configured[dev] = max_lds;
@@ -585,13 +609,13 @@ int launch_mgemv(const MgArgs& a, size_t lds, hipStream_t s) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         return PE_ERR_LAUNCH;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_mgemv<T, SILU, NORM>, 64 * a.waves, lds) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_mgemv<T, SILU, NORM, EXP>, 64 * a.waves, lds) !=
             hipSuccess || per_cu <= 0)
         per_cu = 1;
     int64_t grid = std::min<int64_t>(a.tiles, (int64_t)cus * per_cu);
     grid = std::max<int64_t>(grid, (a.tiles + kMgMaxTilesPerWg - 1) / kMgMaxTilesPerWg);
     if (grid > 0x7FFFFFFF) return PE_ERR_SHAPE;
-    hipLaunchKernelGGL((k_mgemv<T, SILU, NORM>), dim3((unsigned)grid), dim3(64 * a.waves), lds, s, a);
+    hipLaunchKernelGGL((k_mgemv<T, SILU, NORM, EXP>), dim3((unsigned)grid), dim3(64 * a.waves), lds, s, a);
     return launch_status();
 }
 
@@ -633,17 +657,24 @@ extern "C" int pe_mgemv(int type, const void* w_mfma, int64_t n, int64_t k, cons
     a.res = residual;
     a.y = y;
     a.layout = layout;
-    const size_t lds = mg_lds_bytes(a.k);
+    const bool exp = type == PE_TYPE_Q4_K && k <= kMgExpandMaxK;
+    const size_t lds = mg_lds_bytes(a.k, exp);
     hipStream_t s = (hipStream_t)stream;
     const bool nrm = norm_w != nullptr;
     if (type == PE_TYPE_Q4_K) {
-        if (silu) return nrm ? launch_mgemv<PE_TYPE_Q4_K, true, true>(a, lds, s)
-                             : launch_mgemv<PE_TYPE_Q4_K, true, false>(a, lds, s);
-        return nrm ? launch_mgemv<PE_TYPE_Q4_K, false, true>(a, lds, s)
-                   : launch_mgemv<PE_TYPE_Q4_K, false, false>(a, lds, s);
+        if (exp) {
+            if (silu) return nrm ? launch_mgemv<PE_TYPE_Q4_K, true, true, true>(a, lds, s)
+                                 : launch_mgemv<PE_TYPE_Q4_K, true, false, true>(a, lds, s);
+            return nrm ? launch_mgemv<PE_TYPE_Q4_K, false, true, true>(a, lds, s)
+                       : launch_mgemv<PE_TYPE_Q4_K, false, false, true>(a, lds, s);
+        }
+        if (silu) return nrm ? launch_mgemv<PE_TYPE_Q4_K, true, true, false>(a, lds, s)
+                             : launch_mgemv<PE_TYPE_Q4_K, true, false, false>(a, lds, s);
+        return nrm ? launch_mgemv<PE_TYPE_Q4_K, false, true, false>(a, lds, s)
+                   : launch_mgemv<PE_TYPE_Q4_K, false, false, false>(a, lds, s);
     }
-    if (silu) return nrm ? launch_mgemv<PE_TYPE_Q6_K, true, true>(a, lds, s)
-                         : launch_mgemv<PE_TYPE_Q6_K, true, false>(a, lds, s);
-    return nrm ? launch_mgemv<PE_TYPE_Q6_K, false, true>(a, lds, s)
-               : launch_mgemv<PE_TYPE_Q6_K, false, false>(a, lds, s);
+    if (silu) return nrm ? launch_mgemv<PE_TYPE_Q6_K, true, true, false>(a, lds, s)
+                         : launch_mgemv<PE_TYPE_Q6_K, true, false, false>(a, lds, s);
+    return nrm ? launch_mgemv<PE_TYPE_Q6_K, false, true, false>(a, lds, s)
+               : launch_mgemv<PE_TYPE_Q6_K, false, false, false>(a, lds, s);
 }
