@@ -78,7 +78,8 @@ __global__ __launch_bounds__(256) void k_decode_attn(AttnParams p) {
     constexpr int NPOS = kChunk / PS;   // positions per slice
     constexpr int REC = attn_rec<HD>();  // partial record: acc[HD], m, l, 2 pad words
     static_assert(NH % 4 == 0 && NPOS % 4 == 0 && DQ % 4 == 0, "tiling");
-    __shared__ float4 q4[NH * HD / 4];
+    constexpr int QI = (NH * HD / 4 + 255) / 256;  // q float4 per thread
+    __shared__ float4 q4[QI * 256];                 // the slots, then padding every thread fills
     __shared__ float4 sc4[NH][kChunk / 4];
     __shared__ float red[PS][NH * HD];
     __shared__ float ml[2 * NH];
@@ -95,11 +96,12 @@ __global__ __launch_bounds__(256) void k_decode_attn(AttnParams p) {
     const float* vbase = p.v + (int64_t)kvh * p.capacity * HD;
     const int64_t clast = p.capacity - 1;
 
-    // loads: q of the group, this thread's K quarter-row, its V column slice
+    // loads, in the order they are needed: q of the group, this thread's K quarter-row, its V
+    // column slice (the scores and their statistics run while V is still in flight)
     const int nq4 = G * HD / 4;
-    float4 qv[(NH * HD / 4 + 255) / 256];
+    float4 qv[QI];
 #pragma unroll
-    for (int i = 0; i < (NH * HD / 4 + 255) / 256; ++i) {
+    for (int i = 0; i < QI; ++i) {
         const int f = t + 256 * i;
         qv[i] = reinterpret_cast<const float4*>(p.q + (int64_t)kvh * G * HD)[f < nq4 ? f : nq4 - 1];
     }
@@ -118,10 +120,12 @@ __global__ __launch_bounds__(256) void k_decode_attn(AttnParams p) {
         const int64_t s = c0 + js * NPOS + pp;
         vr[pp] = vbase[(s < clast ? s : clast) * HD + d];
     }
+    // every thread stores (slots past the group and the padding get zeros): a conditional
+    // store lets the compiler move the q load behind the K/V loads and wait for all of them
 #pragma unroll
-    for (int i = 0; i < (NH * HD / 4 + 255) / 256; ++i) {
+    for (int i = 0; i < QI; ++i) {
         const int f = t + 256 * i;
-        if (f < NH * HD / 4) q4[f] = f < nq4 ? qv[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        q4[f] = f < nq4 ? qv[i] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     __syncthreads();
 
@@ -308,7 +312,7 @@ template <int HD>
 __global__ __launch_bounds__(256) void k_decode_attn_head(AttnParams p) {
     constexpr int PS = 256 / HD;   // position slices in the P.V phase
     constexpr int NPRE = 24;       // V values per thread fetched up front (S <= 24 * PS)
-    __shared__ float q_lds[HD];
+    __shared__ float q_lds[256];  // q, then padding
     __shared__ float sc[kSmallCap];
     __shared__ float red[256];
     __shared__ float lds4[4];
@@ -317,19 +321,28 @@ __global__ __launch_bounds__(256) void k_decode_attn_head(AttnParams p) {
     const float* kb = p.k + (int64_t)kvh * p.capacity * HD;
     const float* vb = p.v + (int64_t)kvh * p.capacity * HD;
     const int d = t % HD, js = t / HD;
-    // all first-round loads in flight together: q, this thread's first K row, first V values
+    // all first-round loads in flight together, in this order: q, this thread's K row, the
+    // first V values. K and V go through buffer resources over the S valid rows, so rows past
+    // S read as zeros with no per-load condition (conditional loads made the compiler wait for
+    // every load before the first use of any).
+    const float qv = p.q[(int64_t)h * HD + (t < HD ? t : HD - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    const int valid_bytes = (int)(S * HD * 4);  // S <= kSmallCap
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc((void*)kb, (short)0, valid_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc((void*)vb, (short)0, valid_bytes, 0x00020000);
     float4 k0[HD / 4];
-    if (t < S) {
 #pragma unroll
-        for (int i = 0; i < HD / 4; ++i) k0[i] = reinterpret_cast<const float4*>(kb + (int64_t)t * HD)[i];
-    }
+    for (int i = 0; i < HD / 4; ++i)
+        k0[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, t * HD * 4 + 16 * i, 0, 0));
+    __builtin_amdgcn_sched_barrier(0);
     float vpre[NPRE];
 #pragma unroll
-    for (int j = 0; j < NPRE; ++j) {
-        const int sp = js + j * PS;
-        vpre[j] = sp < S ? vb[(int64_t)sp * HD + d] : 0.f;
-    }
-    if (t < HD) q_lds[t] = p.q[(int64_t)h * HD + t];
+    for (int j = 0; j < NPRE; ++j)
+        vpre[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                rv, ((js + j * PS) * HD + d) * 4, 0, 0));
+    q_lds[t] = qv;  // every thread stores (a conditional store sinks the q load behind the rest)
     __syncthreads();
     const float NEG_INF = -__builtin_huge_valf();
     float m_loc = NEG_INF;
@@ -391,26 +404,29 @@ __global__ __launch_bounds__(256) void k_decode_attn_head(AttnParams p) {
 
 // ---------------------------------------------------------------------------------------
 // Mid-size caches (kSmallCap < capacity <= kMidCap<HD>): one workgroup of 1024 threads per
-// query head, one launch and no merge. Every V load of the valid positions is issued at kernel
+// query head, one launch and no merge. The V rows of the capacity class CAP (the smallest of
+// 512 / 768 / 1024 at head_dim 64, 384 / 512 at 128 holding the capacity) are loaded at kernel
 // start; K streams in batches of kMidBatch passes (the next batch's loads in flight while one
 // is scored), a row per VQ = HD / 4 lanes (fully coalesced 16-byte loads). Scores go to LDS,
 // the block takes the softmax statistics, and P.V runs over NS = 1024 / VQ position slices
 // (slice js holds positions js, js + NS, ...), combined by lane swaps within a wave and in
-// wave order across waves.
+// wave order across waves. Loads past S return zeros but still cost issue time, hence the
+// classes.
 constexpr int kMidThreads = 1024;
 constexpr int kMidBatch = 4;
 template <int HD>
 constexpr int kMidCap() { return HD == 64 ? 1024 : 512; }
 
-template <int HD>
+template <int HD, int CAP>
 __global__ __launch_bounds__(kMidThreads) void k_decode_attn_mid(AttnParams p) {
     constexpr int VQ = HD / 4;                  // lanes per row
     constexpr int RP = kMidThreads / VQ;        // rows per pass (64 or 32)
     constexpr int NS = kMidThreads / VQ;        // P.V slices
-    constexpr int MPV = kMidCap<HD>() / NS;     // V rows per thread (16)
+    constexpr int MPV = CAP / NS;               // V rows per thread (8 .. 16)
     constexpr int NW = kMidThreads / 64;
     constexpr int SPW = 64 / VQ;                // slices per wave (4 or 2)
-    __shared__ float sc[kMidCap<HD>()];
+    static_assert(CAP <= kMidCap<HD>() && CAP % (RP * kMidBatch) == 0, "capacity class");
+    __shared__ float sc[CAP];
     __shared__ float4 red4[NW][VQ];
     __shared__ float wred[NW];
     const int t = threadIdx.x, w = t >> 6, c = t % VQ, js = t / VQ;
@@ -419,23 +435,26 @@ __global__ __launch_bounds__(kMidThreads) void k_decode_attn_mid(AttnParams p) {
     const float* kb = p.k + (int64_t)kvh * p.capacity * HD;
     const float* vb = p.v + (int64_t)kvh * p.capacity * HD;
     const float4 q4 = reinterpret_cast<const float4*>(p.q + (int64_t)h * HD)[c];
+    __builtin_amdgcn_sched_barrier(0);  // q's load first: the first scores wait for it alone
     const float NEG_INF = -__builtin_huge_valf();
-    // V rows of this thread's slice (positions past S are zero: they contribute nothing)
-    float4 vr[MPV];
-#pragma unroll
-    for (int i = 0; i < MPV; ++i) {
-        const int64_t s = js + (int64_t)NS * i;
-        vr[i] = s < S ? reinterpret_cast<const float4*>(vb + s * HD)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    // K and V of this kv head as buffer resources over the S valid rows: rows past S read as
+    // zeros (positions past S contribute nothing), with no per-load condition or clamp (a
+    // conditional load is followed by a select that waits for it, and 64-bit addresses for
+    // every load in flight exceed the register budget: both serialised the loads).
+    const int valid_bytes = (int)(S * HD * 4);  // S <= CAP
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc((void*)kb, (short)0, valid_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc((void*)vb, (short)0, valid_bytes, 0x00020000);
+    const int lane_off = (js * HD + 4 * c) * 4;
     // scores: pass j covers rows RP j .. RP j + RP - 1; row js of a pass is this thread's
     const int npass = (int)((S + RP - 1) / RP);
     float4 kr[2][kMidBatch];
     auto issue = [&](int b, float4 (&dst)[kMidBatch]) {
 #pragma unroll
-        for (int i = 0; i < kMidBatch; ++i) {
-            const int64_t s = (int64_t)RP * (kMidBatch * b + i) + js;
-            dst[i] = s < S ? reinterpret_cast<const float4*>(kb + s * HD)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+        for (int i = 0; i < kMidBatch; ++i)
+            dst[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    rk, lane_off + RP * (kMidBatch * b + i) * HD * 4, 0, 0));
     };
     const int nbatch = (npass + kMidBatch - 1) / kMidBatch;
     float m_loc = NEG_INF;
@@ -456,14 +475,29 @@ __global__ __launch_bounds__(kMidThreads) void k_decode_attn_mid(AttnParams p) {
             }
         }
     };
-    // two register sets at fixed names (a run-time index into them would go to scratch)
+    // Two register sets, the batches fully unrolled (at most NB of them): straight-line code,
+    // so the compiler waits for exactly the batch being scored. Every batch is issued (past
+    // the valid rows it reads zeros without touching memory): a conditional issue, or a loop
+    // carrying loads across its back edge, made the compiler wait for every load in flight.
+    // The first two K batches go out before V, which is needed only after the scores.
+    constexpr int NB = CAP / (RP * kMidBatch);
+    static_assert(NB >= 2, "two register sets");
+    // (the scheduling barriers keep the loads in this order: the waits count them in order)
     issue(0, kr[0]);
-    for (int b = 0; b < nbatch; b += 2) {
-        if (b + 1 < nbatch) issue(b + 1, kr[1]);
-        score(b, kr[0]);
-        if (b + 1 >= nbatch) break;
-        if (b + 2 < nbatch) issue(b + 2, kr[0]);
-        score(b + 1, kr[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(1, kr[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    // V rows of this thread's slice
+    float4 vr[MPV];
+#pragma unroll
+    for (int i = 0; i < MPV; ++i)
+        vr[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rv, lane_off + NS * i * HD * 4, 0, 0));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        if (b < nbatch) score(b, kr[b & 1]);
+        if (b + 2 < NB) issue(b + 2, kr[b & 1]);
     }
     // softmax statistics over the S scores
     m_loc = wave_max<64>(m_loc);
@@ -729,10 +763,16 @@ static int launch_decode_attn(const float* q, const float* k_cache, const float*
     }
     if (capacity <= (head_dim == 64 ? kMidCap<64>() : kMidCap<128>())) {
         const dim3 grid((unsigned)n_head);
-        if (head_dim == 64)
-            hipLaunchKernelGGL(k_decode_attn_mid<64>, grid, dim3(kMidThreads), 0, s, p);
+        if (head_dim == 64 && capacity <= 512)
+            hipLaunchKernelGGL((k_decode_attn_mid<64, 512>), grid, dim3(kMidThreads), 0, s, p);
+        else if (head_dim == 64 && capacity <= 768)
+            hipLaunchKernelGGL((k_decode_attn_mid<64, 768>), grid, dim3(kMidThreads), 0, s, p);
+        else if (head_dim == 64)
+            hipLaunchKernelGGL((k_decode_attn_mid<64, 1024>), grid, dim3(kMidThreads), 0, s, p);
+        else if (capacity <= 384)
+            hipLaunchKernelGGL((k_decode_attn_mid<128, 384>), grid, dim3(kMidThreads), 0, s, p);
         else
-            hipLaunchKernelGGL(k_decode_attn_mid<128>, grid, dim3(kMidThreads), 0, s, p);
+            hipLaunchKernelGGL((k_decode_attn_mid<128, 512>), grid, dim3(kMidThreads), 0, s, p);
         return launch_status();
     }
     const dim3 grid((unsigned)p.nsplit, (unsigned)n_kv);
