@@ -68,7 +68,7 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
     // LDS ring of kFpStages K / V^T blocks: block b is staged in slot b % kFpStages
     __shared__ __align__(16) _Float16 ks[kFpStages * kFpKeys * kFpRow];  // K blocks, [key][dim]
     __shared__ __align__(16) _Float16 vt[kFpStages * kFpHd * kFpRow];    // V blocks transposed, [dim][key]
-    const int t = threadIdx.x, nt = blockDim.x, l = t & 63;
+    const int t = threadIdx.x, l = t & 63;
     const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave index (wave-uniform)
     const int li = l & 15, lg = l >> 4;
     const int64_t nqb = (p.L + qb_size - 1) / qb_size;

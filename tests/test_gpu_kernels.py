@@ -414,12 +414,16 @@ def test_kv_write(K):
 
 # ---- fused QKV prologue -------------------------------------------------------------------
 
-@pytest.mark.parametrize("types,hidden,nh,nkv,hd", [
-    ((dq.Q5_0, dq.Q5_0, dq.Q8_0), 896, 14, 2, 64),
-    ((dq.Q5_0, dq.Q5_0, dq.Q5_0), 896, 14, 2, 64),
-    ((dq.Q4_K, dq.Q4_K, dq.Q6_K), 3584, 28, 4, 128),
+# Shapes with more than 512 one-pair-per-group blocks (the 7B QKV, hidden 2048 with 64-lane
+# groups) run the looped form (qkv_loop.hip), in both activation layouts; one without biases.
+@pytest.mark.parametrize("types,hidden,nh,nkv,hd,ut,bias", [
+    ((dq.Q5_0, dq.Q5_0, dq.Q8_0), 896, 14, 2, 64, False, True),
+    ((dq.Q5_0, dq.Q5_0, dq.Q5_0), 896, 14, 2, 64, True, True),
+    ((dq.Q4_K, dq.Q4_K, dq.Q6_K), 3584, 28, 4, 128, False, True),
+    ((dq.Q4_K, dq.Q4_K, dq.Q6_K), 3584, 28, 4, 128, True, True),
+    ((dq.Q5_0, dq.Q8_0, dq.Q8_0), 2048, 32, 8, 64, True, False),
 ])
-def test_qkv_rmsnorm_rope(K, types, hidden, nh, nkv, hd):
+def test_qkv_rmsnorm_rope(K, types, hidden, nh, nkv, hd, ut, bias):
     rng = np.random.default_rng(hidden)
     cap, pos, theta = 40, 23, 1e6
     rows = (nh * hd, nkv * hd, nkv * hd)
@@ -434,8 +438,12 @@ def test_qkv_rmsnorm_rope(K, types, hidden, nh, nkv, hd):
     kc = torch.zeros(nkv, cap, hd, device=DEV)
     vc = torch.zeros(nkv, cap, hd, device=DEV)
     T = lambda a: torch.from_numpy(a).to(DEV)
-    q = K.qkv_rmsnorm_rope(T(x), T(nw), 1e-6, *ws, *(T(b) for b in bs), T(cos), T(sin),
-                           torch.tensor([pos], device=DEV), kc, vc, nh).cpu().numpy()
+    xin, nin = (K.to_ut(T(x)), K.to_ut(T(nw))) if ut else (T(x), T(nw))
+    dbias = [T(b) for b in bs] if bias else [None, None, None]
+    q = K.qkv_rmsnorm_rope(xin, nin, 1e-6, *ws, *dbias, T(cos), T(sin), torch.tensor([pos], device=DEV),
+                           kc, vc, nh, layout=K.LAYOUT_X_UT if ut else K.LAYOUT_NATURAL).cpu().numpy()
+    if not bias:
+        bs = [None, None, None]
     h = closed.rmsnorm(x, nw, 1e-6)
     outs = [closed.gemv(dequant_rows(t, raw, r, hidden), h, bias=b)
             for t, raw, r, b in zip(types, raws, rows, bs)]
