@@ -339,6 +339,25 @@ int pe_attn_gproj(const float* q, const float* k_cache, const float* v_cache, in
                   float scale, int round_fp16, int wo_type, const void* wo_tiled, int64_t hidden,
                   float* parts, int layout, pe_stream_t stream);
 
+/* pe_attn_gproj for caches of any length (head_dim 64): the split decode attention of
+ * pe_decode_attn (64-position chunk records in the workspace), then one launch in which
+ * workgroup (row block, kv head j) merges the records of j's query heads (log-sum-exp rule,
+ * fixed order; fp16 rounding when round_fp16) and multiplies them by its rows of Wo's group-j
+ * columns, giving parts[j] as pe_attn_gproj does. Two launches instead of the split, merge and
+ * o-projection launches of pe_decode_attn + pe_qgemv.
+ * workspace: pe_decode_attn_workspace_bytes(n_head, n_kv, 64, capacity) bytes, any contents.
+ * Limits (pe_attn_split_gproj_supported): head_dim 64, n_head / n_kv <= 8, hidden % 32 == 0,
+ * n_head*head_dim a multiple of the Wo block.
+ * Replaces decode_attn (model.py:211, kernels.py:129) and the o-projection addmm (model.py:213)
+ * at long contexts. */
+int pe_attn_split_gproj_supported(int n_head, int n_kv, int head_dim, int64_t capacity,
+                                  int wo_type, int64_t hidden);
+int pe_attn_split_gproj(const float* q, const float* k_cache, const float* v_cache, int n_head,
+                        int n_kv, int head_dim, int64_t capacity, const void* len_dev,
+                        int len_dtype, int64_t len_add, float scale, int round_fp16, int wo_type,
+                        const void* wo_tiled, int64_t hidden, float* parts, void* workspace,
+                        int64_t workspace_bytes, int layout, pe_stream_t stream);
+
 /* ---- the whole decode step in one launch ---------------------------------------------- */
 
 /* One layer of the model for pe_decode_step: the tiled matrices and their ggml types (Q5_0,

@@ -301,6 +301,133 @@ __global__ __launch_bounds__(NT) void k_decode_attn_merge(AttnParams p) {
 }
 
 // ---------------------------------------------------------------------------------------
+// Mid-size caches fused with the o-projection share (the split path's counterpart of
+// pe_attn_gproj): after the split launch, workgroup (rb, j) merges the chunk records of kv
+// head j's G query heads and multiplies the merged outputs (fp16-rounded as kernels.py:126) by
+// its kMgpRows rows of Wo's group-j columns:
+//   parts[j][r] = sum_{h in group j} sum_d Wo[r][h*64 + d] a_h[d].
+// The gate/up GEMV's summed-activation mode adds x + parts[0] + ... as the o-projection's
+// residual add, so the merge launch and the o-projection launch become one. Wave g merges head
+// slot g as k_decode_attn_merge does (lane groups of 16 lanes read a float4 of each record,
+// batches of kMergeBatch records in flight, groups combined at their common maximum by lane
+// swaps); the Wo rows are loaded at kernel start, before the records. Every workgroup of a kv
+// group merges all of its records, so the launch pays for the record count: measured faster
+// than the merge and o-projection launches up to ~4096 positions (1024: 14.2 -> 9.5 us for
+// attention + o-projection; 2048: 11.8 -> 9.9), slower beyond (8192: 14.9 vs 12.9). Two waves
+// per head slot at 1024 threads were slower at every length.
+constexpr int kMgpThreads = 512;             // 8 waves: one per head slot (group <= 8)
+constexpr int kMgpRows = kMgpThreads / 16;   // o-projection rows per workgroup, 16 lanes a row
+constexpr int kMgpMaxGroup = kMgpThreads / 64;
+constexpr int kMgpUnitStride = 36;  // floats per staged 32-float unit (conflict-free float4 reads)
+
+struct MgpParams {
+    AttnParams a;
+    Tiled wo;        // (hidden x n_head*64)
+    int64_t hidden;
+    float* parts;    // (n_kv, hidden)
+    int layout;      // PE_LAYOUT_Y_UT: each part unit-transposed
+};
+
+template <int T>
+__global__ __launch_bounds__(kMgpThreads) void k_attn_merge_gproj(MgpParams mp) {
+    constexpr int HD = 64, REC = attn_rec<64>(), VQ = HD / 4, NG = 64 / VQ;
+    __shared__ float4 o_lds[kMgpMaxGroup * 2 * (kMgpUnitStride / 4)];  // the group's outputs, unit-padded
+    const AttnParams& p = mp.a;
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63, c = lane % VQ, jg = lane / VQ;
+    const int j = blockIdx.y, G = p.group, gunits = 2 * G;
+    const int64_t r0 = (int64_t)blockIdx.x * kMgpRows;
+    // o-projection weights first: row r0 + orow, unit ou of the group's columns
+    const int orow = t >> 4, ou = t & 15;
+    typename Fmt<T>::Raw wr;
+    Fmt<T>::load(mp.wo, r0 + orow < mp.hidden ? r0 + orow : mp.hidden - 1,
+                 j * gunits + (ou < gunits ? ou : gunits - 1), wr);
+    const float NEG_INF = -__builtin_huge_valf();
+    const int64_t S = valid_len(p);
+    const int nvalid = (int)((S + kChunk - 1) / kChunk);
+    const int last = nvalid > 0 ? nvalid - 1 : 0;
+    if (w < G) {  // uniform per wave
+        const float* base = p.partials + (int64_t)j * p.nsplit * G * REC + (int64_t)w * REC;
+        const int64_t rstride = (int64_t)G * REC;
+        float M = NEG_INF, L = 0.f;
+        float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s0 = jg; s0 < nvalid; s0 += NG * kMergeBatch) {
+            float rm[kMergeBatch], rl[kMergeBatch];
+            float4 ra[kMergeBatch];
+#pragma unroll
+            for (int b = 0; b < kMergeBatch; ++b) {
+                const int sp = s0 + NG * b;
+                const float* r = base + (int64_t)(sp < last ? sp : last) * rstride;
+                ra[b] = reinterpret_cast<const float4*>(r)[c];
+                const float2 ml = reinterpret_cast<const float2*>(r + HD)[0];
+                rm[b] = ml.x;
+                rl[b] = ml.y;
+            }
+            float bm = NEG_INF;
+#pragma unroll
+            for (int b = 0; b < kMergeBatch; ++b)
+                if (s0 + NG * b < nvalid) bm = fmaxf(bm, rm[b]);
+            const float Mn = fmaxf(M, bm);
+            const float cs = M == NEG_INF ? 0.f : expf(M - Mn);
+            L *= cs;
+            A.x *= cs;
+            A.y *= cs;
+            A.z *= cs;
+            A.w *= cs;
+#pragma unroll
+            for (int b = 0; b < kMergeBatch; ++b) {
+                if (s0 + NG * b < nvalid) {
+                    const float e = expf(rm[b] - Mn);
+                    L = fmaf(rl[b], e, L);
+                    A.x = fmaf(ra[b].x, e, A.x);
+                    A.y = fmaf(ra[b].y, e, A.y);
+                    A.z = fmaf(ra[b].z, e, A.z);
+                    A.w = fmaf(ra[b].w, e, A.w);
+                }
+            }
+            M = Mn;
+        }
+        // the four lane groups (lanes 16 apart) at their common maximum
+        const float Mw = swap32_max(swap16_max(M));
+        const float cw = M == NEG_INF ? 0.f : expf(M - Mw);
+        float v[5] = {A.x * cw, A.y * cw, A.z * cw, A.w * cw, L * cw};
+#pragma unroll
+        for (int i = 0; i < 5; ++i) v[i] = swap32_sum(swap16_sum(v[i]));
+        if (lane < VQ) {
+            float o[4] = {v[0] / v[4], v[1] / v[4], v[2] / v[4], v[3] / v[4]};
+            if (p.round_fp16) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[i] = round_to_f16(o[i]);
+            }
+            const int k = w * HD + 4 * c;  // input column of the group, a float4 inside one unit
+            o_lds[(k >> 5) * (kMgpUnitStride / 4) + ((k & 31) >> 2)] = make_float4(o[0], o[1], o[2], o[3]);
+        }
+    }
+    __syncthreads();
+    // o-projection share: 16 lanes per row, lane ou dots unit ou of the group's columns
+    float acc = 0.f;
+    {
+        const int uc = ou < gunits ? ou : gunits - 1;
+        float xr[32];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 v = o_lds[uc * (kMgpUnitStride / 4) + i];
+            xr[4 * i] = v.x;
+            xr[4 * i + 1] = v.y;
+            xr[4 * i + 2] = v.z;
+            xr[4 * i + 3] = v.w;
+        }
+        const float d = Fmt<T>::dot(wr, xr, unit_sums(xr));
+        acc = ou < gunits ? d : 0.f;
+    }
+    acc = wave_sum<16>(acc);
+    const int64_t r = r0 + orow;
+    if (ou == 0 && r < mp.hidden) {
+        const int64_t oi = (mp.layout & PE_LAYOUT_Y_UT) ? ut_index(r, mp.hidden >> 5) : r;
+        mp.parts[(int64_t)j * mp.hidden + oi] = acc;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
 // Short caches (capacity <= kSmallCap): one workgroup per query head does the whole softmax
 // in one pass -- scores of all S positions into LDS (thread per position), block max/sum,
 // P.V with a thread per (dim, position slice) -- so there is no split and no merge launch on
@@ -817,5 +944,54 @@ extern "C" int pe_prefill_attn(const float* q, int64_t q_stride, const float* k_
         hipLaunchKernelGGL(k_prefill_attn<64>, grid, dim3(256), 0, s, p);
     else
         hipLaunchKernelGGL(k_prefill_attn<128>, grid, dim3(256), 0, s, p);
+    return launch_status();
+}
+
+extern "C" int pe_attn_split_gproj_supported(int n_head, int n_kv, int head_dim, int64_t capacity,
+                                             int wo_type, int64_t hidden) {
+    if (!is_tiled_type(wo_type)) return PE_ERR_TYPE;
+    if (head_dim != 64 || n_kv <= 0 || n_kv > 64 || n_head <= 0 || n_head % n_kv ||
+        n_head / n_kv > kMgpMaxGroup || capacity <= 0 || attn_nsplit(capacity) > 65535 ||
+        hidden <= 0 || hidden % 32 || (hidden + kMgpRows - 1) / kMgpRows > 65535)
+        return PE_ERR_SHAPE;
+    if (((int64_t)n_head * head_dim) % row_multiple(wo_type)) return PE_ERR_SHAPE;
+    return PE_OK;
+}
+
+extern "C" int pe_attn_split_gproj(const float* q, const float* k_cache, const float* v_cache,
+                                   int n_head, int n_kv, int head_dim, int64_t capacity,
+                                   const void* len_dev, int len_dtype, int64_t len_add, float scale,
+                                   int round_fp16, int wo_type, const void* wo_tiled, int64_t hidden,
+                                   float* parts, void* workspace, int64_t workspace_bytes, int layout,
+                                   pe_stream_t stream) {
+    int st = pe_attn_split_gproj_supported(n_head, n_kv, head_dim, capacity, wo_type, hidden);
+    if (st) return st;
+    if (len_dtype < 0 || len_dtype > 2) return PE_ERR_TYPE;
+    if (layout & ~PE_LAYOUT_Y_UT) return PE_ERR_TYPE;
+    if (!q || !k_cache || !v_cache || !wo_tiled || !parts || !workspace || (len_dtype && !len_dev))
+        return PE_ERR_NULL;
+    if (workspace_bytes < pe_decode_attn_workspace_bytes(n_head, n_kv, head_dim, capacity))
+        return PE_ERR_SPACE;
+    if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 4) || !aligned(wo_tiled, 16) ||
+        !aligned(parts, 4) || !aligned(workspace, 16) || (len_dtype == 1 && !aligned(len_dev, 4)) ||
+        (len_dtype == 2 && !aligned(len_dev, 8)))
+        return PE_ERR_ALIGN;
+    AttnParams p{q, k_cache, v_cache, n_kv, n_head / n_kv, capacity, len_dev, len_dtype, len_add,
+                 scale, round_fp16, nullptr, (unsigned*)workspace,
+                 (float*)((char*)workspace + 256), (int)attn_nsplit(capacity), 0};
+    const int64_t qd = (int64_t)n_head * head_dim;
+    MgpParams mp{p, make_tiled(wo_tiled, hidden, qd / block_elems(wo_type)), hidden, parts, layout};
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL((k_decode_attn<64, 8>), dim3((unsigned)p.nsplit, (unsigned)n_kv), dim3(256), 0, s, p);
+    const dim3 grid((unsigned)((hidden + kMgpRows - 1) / kMgpRows), (unsigned)n_kv);
+    switch (wo_type) {
+        case PE_TYPE_Q8_0: hipLaunchKernelGGL(k_attn_merge_gproj<PE_TYPE_Q8_0>, grid, dim3(kMgpThreads), 0, s, mp); break;
+        case PE_TYPE_Q5_0: hipLaunchKernelGGL(k_attn_merge_gproj<PE_TYPE_Q5_0>, grid, dim3(kMgpThreads), 0, s, mp); break;
+        case PE_TYPE_Q4_K: hipLaunchKernelGGL(k_attn_merge_gproj<PE_TYPE_Q4_K>, grid, dim3(kMgpThreads), 0, s, mp); break;
+        case PE_TYPE_Q6_K: hipLaunchKernelGGL(k_attn_merge_gproj<PE_TYPE_Q6_K>, grid, dim3(kMgpThreads), 0, s, mp); break;
+        case PE_TYPE_F16: hipLaunchKernelGGL(k_attn_merge_gproj<PE_TYPE_F16>, grid, dim3(kMgpThreads), 0, s, mp); break;
+        case PE_TYPE_F32: hipLaunchKernelGGL(k_attn_merge_gproj<PE_TYPE_F32>, grid, dim3(kMgpThreads), 0, s, mp); break;
+        default: return PE_ERR_TYPE;
+    }
     return launch_status();
 }

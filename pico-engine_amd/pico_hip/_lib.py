@@ -112,6 +112,8 @@ _SIGNATURES = {
     "pe_qgemv_sum_rmsnorm_silu": (_I, [_I, _P, _L, _L, _P, _P, _I, _P, _F, _P, _P, _I, _P]),
     "pe_attn_gproj_supported": (_I, [_I, _I, _I, _L, _I, _L]),
     "pe_attn_gproj": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _I, _P, _L, _P, _I, _P]),
+    "pe_attn_split_gproj_supported": (_I, [_I, _I, _I, _L, _I, _L]),
+    "pe_attn_split_gproj": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _I, _P, _L, _P, _P, _L, _I, _P]),
     "pe_rmsnorm": (_I, [_P, _L, _P, _P, _L, _L, _L, _F, _P]),
     "pe_rmsnorm_h16": (_I, [_P, _L, _P, _P, _L, _L, _L, _F, _P]),
     "pe_rope": (_I, [_P, _L, _P, _P, _P, _L, _L, _I, _I, _P]),

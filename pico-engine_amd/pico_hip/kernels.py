@@ -704,6 +704,47 @@ def attn_gproj(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, wo: QWeight,
     return out
 
 
+def attn_split_gproj_supported(n_head: int, n_kv: int, hd: int, capacity: int, wo: QWeight) -> bool:
+    """Whether attn_split_gproj covers these shapes (head_dim 64, up to 8 query heads per kv
+    head, any capacity)."""
+    return lib.pe_attn_split_gproj_supported(n_head, n_kv, hd, capacity, wo.ggml_type, wo.n) == 0
+
+
+def attn_split_gproj(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, wo: QWeight,
+                     S: torch.Tensor | int | None = None, S_offset: int = 0,
+                     workspace: torch.Tensor | None = None, scale: float | None = None,
+                     round_fp16: bool = True, out: torch.Tensor | None = None,
+                     layout: int = LAYOUT_NATURAL) -> torch.Tensor:
+    """attn_gproj for caches of any length: the split attention's chunk records (in
+    ``workspace``, decode_attn_workspace bytes), then one launch that merges them per kv group
+    and multiplies by that group's columns of Wo. Same result conventions as attn_gproj."""
+    dev = _on_gpu(q, k, v, wo.data)
+    n_head, hd = q.shape[-2], q.shape[-1]
+    n_kv, capacity = k.shape[0], k.shape[1]
+    q = _f32c(q.reshape(n_head, hd))
+    if not (k.is_contiguous() and v.is_contiguous()):
+        raise ValueError("KV caches must be contiguous (n_kv, capacity, hd) buffers")
+    if scale is None:
+        scale = 1.0 / float(hd) ** 0.5
+    len_dev, len_dtype, len_add = None, 0, int(S_offset)
+    if isinstance(S, torch.Tensor):
+        len_dev = S
+        len_dtype = {torch.int32: 1, torch.int64: 2}[S.dtype]
+    elif S is not None:
+        len_add += int(S)
+    else:
+        len_add += capacity
+    if workspace is None:
+        workspace = decode_attn_workspace(n_head, n_kv, hd, capacity, dev)
+    if out is None:
+        out = torch.empty(n_kv, wo.n, device=dev, dtype=torch.float32)
+    check(lib.pe_attn_split_gproj(_ptr(q), _ptr(k), _ptr(v), n_head, n_kv, hd, capacity, _ptr(len_dev),
+                                  len_dtype, len_add, float(scale), int(round_fp16), wo.ggml_type,
+                                  _ptr(wo.data), wo.n, _ptr(out), _ptr(workspace), workspace.numel(),
+                                  layout, _stream(dev)), "pe_attn_split_gproj")
+    return out
+
+
 def qgemv_sum_norm_silu(x: torch.Tensor, parts: torch.Tensor, weight: torch.Tensor, w: QWeight,
                         eps: float, out: torch.Tensor | None = None,
                         x_sum: torch.Tensor | None = None,

@@ -18,9 +18,11 @@ layer plus the embedding row and the LM head:
     qgemv + residual   (ffn_down)                         model.py:225-234
   qgemv_norm(_argmax)  (final norm + LM head [+ greedy])  model.py:159-164
 
-Shapes attn_gproj does not cover (head_dim 128, long caches) run decode_attn (split-KV GQA,
-model.py:211) and the o-projection GEMV with the residual (model.py:213) instead, then the
-normed gate/up GEMV.
+Caches of 513..4096 positions (head_dim 64) run attn_split_gproj instead of attn_gproj: the
+split-KV attention, then one launch that merges each kv group's chunk records and multiplies
+them by the group's Wo columns (the parts the gate/up GEMV adds). Other shapes (head_dim 128,
+other cache sizes) run decode_attn (model.py:211) and the o-projection GEMV with the residual
+(model.py:213), then the normed gate/up GEMV.
 
 Prefill (L > 1) follows the reference's L > 1 branch op for op: in fp32 for short prompts (its
 off-CUDA numerics): rmsnorm, one small-M GEMM per QKV segment with bias, RoPE, cache write at
@@ -97,6 +99,13 @@ class Transformer:
         # attention of each kv group fused with its share of the o-projection (attn_gproj),
         # the shares added by the gate/up GEMV: four launches per layer instead of five
         self.use_attn_gproj = True
+        # caches of split_gproj_capacity[0] .. [1] positions run the split attention and a merge
+        # fused with the o-projection shares (attn_split_gproj: two launches where decode_attn +
+        # the o-projection GEMV take two or three). Measured end to end on the 0.5B model: +5.7 %
+        # at a 1000-token prompt, +2.2 % at 3000, -4.7 % at 200 (the one-launch mid-size
+        # attention wins there); slower beyond ~4096 positions, where every workgroup merging
+        # all of its kv group's records costs more than the merge launch
+        self.split_gproj_capacity = (513, 4096)
         # prompts of at least this many tokens are prefilled on the matrix cores (fp16
         # operands, fp32 accumulation: the reference's CUDA autocast prefill, model.py:147-151);
         # shorter ones by the fp32 path (the reference's off-CUDA numerics). None: never.
@@ -255,9 +264,15 @@ class Transformer:
             k_buf, v_buf = cache[i]
             q = K.qkv_rmsnorm_rope(x, L.attn_norm_ut, cfg.eps, L.wq, L.wk, L.wv, L.bq, L.bk, L.bv,
                                    self.cos, self.sin, pos, k_buf, v_buf, cfg.n_head, layout=XU)
-            if (self.use_attn_gproj and L.w_gate_up is not None and
-                    K.attn_gproj_supported(cfg.n_head, cfg.n_kv_head, cfg.head_dim, capacity, L.wo)):
-                parts = K.attn_gproj(q, k_buf, v_buf, L.wo, S=pos, S_offset=1, layout=YU)
+            parts = None
+            if self.use_attn_gproj and L.w_gate_up is not None:
+                if K.attn_gproj_supported(cfg.n_head, cfg.n_kv_head, cfg.head_dim, capacity, L.wo):
+                    parts = K.attn_gproj(q, k_buf, v_buf, L.wo, S=pos, S_offset=1, layout=YU)
+                elif (self.split_gproj_capacity[0] <= capacity <= self.split_gproj_capacity[1] and
+                      K.attn_split_gproj_supported(cfg.n_head, cfg.n_kv_head, cfg.head_dim, capacity, L.wo)):
+                    parts = K.attn_split_gproj(q, k_buf, v_buf, L.wo, S=pos, S_offset=1, workspace=ws,
+                                               layout=YU)
+            if parts is not None:
                 act, x = K.qgemv_sum_norm_silu(x, parts, L.ffn_norm_ut, L.w_gate_up, cfg.eps,
                                                layout=XU | YU)
                 x = K.qgemv(act, L.w_down, residual=x, layout=XU | YU)

@@ -692,6 +692,74 @@ def test_attn_gproj_layout_empty_and_limits(K):
     assert not K.attn_gproj_supported(10, 5, hd, cap, wo)         # 5 kv heads
 
 
+# attn_split_gproj: the split attention's records merged per kv group with that group's Wo
+# columns (long caches; any capacity)
+SPLIT_GPROJ_CASES = [
+    (dq.Q5_0, 14, 2, 2048, [1, 64, 65, 1000, 2047, 2048]),  # config 3 heads: one chunk, ragged, full
+    (dq.Q5_0, 14, 2, 8200, [8193, 8200]),                   # config 3 decode context
+    (dq.Q8_0, 8, 1, 1500, [3, 1500]),                       # MQA: one group of 8 query heads
+    (dq.Q4_K, 8, 2, 1100, [700, 1100]),                     # K-quant o-projection (512 columns)
+    (dq.Q6_K, 16, 4, 300, [129, 300]),                      # four groups (four parts)
+]
+
+
+@pytest.mark.parametrize("t,nh,nkv,cap,Ss", SPLIT_GPROJ_CASES,
+                         ids=[f"t{t}-{nh}x{nkv}-cap{cap}" for t, nh, nkv, cap, _ in SPLIT_GPROJ_CASES])
+def test_attn_split_gproj_matches_closed_form(K, t, nh, nkv, cap, Ss):
+    """Part j = Wo[:, columns of group j] . attention of group j's heads over S positions of a
+    long cache (fp16-rounded attention output); x + the parts in order is the o-projection
+    with its residual."""
+    hd, hidden = 64, 896
+    rng = np.random.default_rng(nh * cap + t + 11)
+    q = rng.standard_normal((nh, hd)).astype(np.float32)
+    k, v = _kv(rng, nkv, cap, hd)
+    x = rng.standard_normal(hidden).astype(np.float32)
+    raw = quantized_normal(t, hidden, nh * hd, seed=cap + t + 1)
+    wo = qweight(K, t, raw, hidden, nh * hd)
+    W = dequant_rows(t, raw, hidden, nh * hd)
+    T = lambda a: torch.from_numpy(a).to(DEV)
+    G = nh // nkv
+    assert K.attn_split_gproj_supported(nh, nkv, hd, cap, wo)
+    ws = K.decode_attn_workspace(nh, nkv, hd, cap, DEV)
+    kd, vd = T(k), T(v)
+    for S in Ss:
+        parts = K.attn_split_gproj(T(q), kd, vd, wo, S=torch.tensor([S - 1], device=DEV), S_offset=1,
+                                   workspace=ws).cpu().numpy()
+        assert parts.shape == (nkv, hidden)
+        attn = closed.attention(q, k, v, S, round_fp16=True).reshape(-1)
+        for j in range(nkv):
+            cols = slice(j * G * hd, (j + 1) * G * hd)
+            assert rel_err(parts[j], closed.gemv(W[:, cols], attn[cols])) < TOL, f"S={S} j={j}"
+        y = x.copy()
+        for pp in parts:
+            y = (y + pp).astype(np.float32)
+        assert rel_err(y, closed.gemv(W, attn, residual=x)) < TOL, f"S={S}"
+
+
+def test_attn_split_gproj_layout_empty_and_limits(K):
+    """Unit-transposed parts equal the natural ones; the same attention as decode_attn + the
+    o-projection GEMV; S = 0 gives NaN; shape limits."""
+    hd, nh, nkv, cap, hidden = 64, 14, 2, 3000, 896
+    rng = np.random.default_rng(16)
+    q = torch.from_numpy(rng.standard_normal((nh, hd)).astype(np.float32)).to(DEV)
+    k, v = (torch.from_numpy(a).to(DEV) for a in _kv(rng, nkv, cap, hd))
+    wo = qweight(K, dq.Q5_0, quantized_normal(dq.Q5_0, hidden, nh * hd, seed=16), hidden, nh * hd)
+    ws = K.decode_attn_workspace(nh, nkv, hd, cap, DEV)
+    nat = K.attn_split_gproj(q, k, v, wo, S=2500, workspace=ws)
+    ut = K.attn_split_gproj(q, k, v, wo, S=2500, workspace=ws, layout=K.LAYOUT_Y_UT)
+    for j in range(nkv):
+        assert torch.equal(K.from_ut(ut[j]), nat[j])
+    a2 = K.decode_attn(q, k, v, S=2500, workspace=ws)
+    y2 = K.qgemv(a2.reshape(-1), wo)
+    assert rel_err(nat.sum(0).cpu().numpy(), y2.cpu().numpy()) < TOL
+    assert torch.isnan(K.attn_split_gproj(q, k, v, wo, S=0, workspace=ws)).all()
+    assert not K.attn_split_gproj_supported(nh, nkv, 128, cap, wo)   # head_dim 128
+    assert not K.attn_split_gproj_supported(28, 2, hd, cap, wo)      # 14 query heads per group
+    small = torch.zeros(64, dtype=torch.uint8, device=DEV)
+    with pytest.raises(RuntimeError):
+        K.attn_split_gproj(q, k, v, wo, S=10, workspace=small)       # workspace too small
+
+
 # ---- prompt-prefill GEMM on the matrix cores (fp16 operands, fp32 accumulate) --------------
 
 @pytest.mark.parametrize("t,n,k", [(dq.Q5_0, 96, 896), (dq.Q8_0, 64, 896), (dq.Q4_K, 40, 4864),

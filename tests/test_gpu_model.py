@@ -103,6 +103,41 @@ def test_graph_equals_eager(tiny, step_kernel):
         eng.model.use_step_kernel = False
 
 
+def test_mid_cache_decode_split_gproj(tiny):
+    """Caches of 513..4096 positions run attn_split_gproj (split attention, then the records
+    merged per kv group with the group's Wo columns): decode logits within 1e-3 of the oracle,
+    and each graph replay equal to the same step run eagerly, bit for bit."""
+    eng, ref = tiny
+    m = eng.model
+    saved = m.prefill_f16_min_tokens
+    m.prefill_f16_min_tokens = None  # the oracle's fp32 prefill
+    try:
+        ids = np.random.default_rng(5).integers(0, 1024, size=520).tolist()
+        cap = len(ids) + 8
+        assert m.split_gproj_capacity[0] <= cap <= m.split_gproj_capacity[1]
+        cache, rcache = eng._empty_cache(cap), ref.empty_cache(cap)
+        graph = eng._build_decode_graph(cache)
+        assert graph is not None, "graph capture failed"
+        greedy = eng._greedy
+        lg = m.forward(torch.tensor(ids, device=eng.device), torch.arange(len(ids), device=eng.device), cache)
+        rl = ref.forward(torch.tensor(ids), torch.arange(len(ids)), rcache)
+        assert rel_err(lg.cpu().numpy(), rl.numpy()) < TOL
+        tok = int(rl.argmax())
+        for step in range(4):
+            pos = len(ids) + step
+            eager = m.forward(torch.tensor([tok], device=eng.device), torch.tensor([pos], device=eng.device),
+                              cache, greedy).clone()
+            rl = ref.forward(torch.tensor([tok]), torch.tensor([pos]), rcache)
+            assert rel_err(eager.cpu().numpy(), rl.numpy()) < TOL, step
+            torch.cuda.synchronize()
+            g = eng._decode_step(tok, pos, cache, graph).clone()
+            torch.cuda.synchronize()
+            assert torch.equal(eager, g), f"graph diverged from eager at step {step}"
+            tok = int(rl.argmax())
+    finally:
+        m.prefill_f16_min_tokens = saved
+
+
 PATHS = {  # model flags of each path of the decode step
     "three_launch": dict(use_attn_gproj=False, use_step_kernel=False),
     "attn_gproj": dict(use_attn_gproj=True, use_step_kernel=False),
