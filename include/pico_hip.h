@@ -129,6 +129,13 @@ int pe_gemm_f16_silu(const float* a, int64_t lda, const void* w_f16_il, float* c
 int pe_gemm_f16_silu_h(const float* a, int64_t lda, const void* w_f16_il, void* c_f16,
                        int64_t ldc, int64_t M, int64_t ffn, int64_t K, pe_stream_t stream);
 
+/* pe_gemm_f16_silu_h with A already fp16 in memory: a_f16 (M, K) with row stride lda
+ * (elements, lda % 8 == 0, 16-byte aligned), e.g. the fp16 output of pe_rmsnorm_h16, which
+ * holds the values pe_gemm_f16_silu_h rounds its fp32 A to: the same bits with half the A
+ * bytes. Replaces model.py:216-224 (L > 1). */
+int pe_gemm_h16_silu_h(const void* a_f16, int64_t lda, const void* w_f16_il, void* c_f16,
+                       int64_t ldc, int64_t M, int64_t ffn, int64_t K, pe_stream_t stream);
+
 /* pe_gemm_f16 with A already fp16 in memory: a_f16 (M, K) with row stride lda (elements,
  * lda % 8 == 0, 16-byte aligned); everything else as pe_gemm_f16.
  * Replaces the prefill down projection of model.py:235 (L > 1) after pe_gemm_f16_silu_h. */
@@ -450,6 +457,17 @@ int pe_qgemm(int ggml_type, const void* w_tiled, int64_t n_rows, int64_t k, cons
 int pe_kv_write(const float* k_src, const float* v_src, int64_t src_stride, int n_kv,
                 int head_dim, int64_t L, int64_t pos0, float* k_cache, float* v_cache,
                 int64_t capacity, pe_stream_t stream);
+
+/* Prefill RoPE and cache write in one pass over the fused QKV rows: qkv (L, (n_head + 2 n_kv)
+ * hd) with row stride qkv_stride (q heads, then k heads, then v heads); cos_rows / sin_rows
+ * (L, hd/2) (the table rows of the L positions). q_out[l][h] = rope(q[l][h]) (L, n_head, hd);
+ * k_cache[h][pos0 + l] = rope(k[l][h]), v_cache[h][pos0 + l] = v[l][h]. The same values as
+ * pe_rope of the q and k heads followed by pe_kv_write. hd % 8 == 0; 16-byte aligned rows.
+ * Replaces rope + index_copy_ of model.py:186-197 (L > 1). */
+int pe_rope_kv_write(const float* qkv, int64_t qkv_stride, const float* cos_rows,
+                     const float* sin_rows, int n_head, int n_kv, int head_dim, int64_t L,
+                     int64_t pos0, float* q_out, float* k_cache, float* v_cache, int64_t capacity,
+                     pe_stream_t stream);
 
 /* Causal GQA attention of L queries at positions pos0..pos0+L-1 over the cache, fp32,
  * no output rounding. q row l at q + l*q_stride (n_head*hd), out row l at out + l*out_stride.

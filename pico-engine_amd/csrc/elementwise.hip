@@ -82,6 +82,48 @@ __global__ void k_kv_write(const float* __restrict__ ks, const float* __restrict
     }
 }
 
+// RoPE of the q and k heads and the cache write of k and v in one pass over the fused QKV rows
+// (pe_rope_kv_write). Item = (row l, slot): slots [0, nq4) rotate four pairs (j .. j + 3,
+// j + half ..) of a q head, then nk4 of a k head, then nv4 float4 copies of v. The same
+// arithmetic as k_rope (x1 c - x2 s, x1 s + x2 c) and a plain copy for v.
+__global__ void k_rope_kv_write(const float* __restrict__ qkv, int64_t qs, const float* __restrict__ cs,
+                                const float* __restrict__ sn, int n_head, int n_kv, int hd, int L,
+                                int64_t pos0, float* __restrict__ q_out, float* kc, float* vc,
+                                int64_t cap) {
+    const int h4 = hd / 8;                  // float4 pairs per head
+    const int nq4 = n_head * h4, nk4 = n_kv * h4, nv4 = n_kv * (hd / 4);
+    const int per = nq4 + nk4 + nv4;
+    const int total = L * per;
+    const int stride = gridDim.x * blockDim.x;
+    const int half = hd / 2;
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
+        const int l = idx / per, it = idx - l * per;
+        const float* row = qkv + (int64_t)l * qs;
+        if (it < nq4 + nk4) {
+            const bool isq = it < nq4;
+            const int hh = isq ? it / h4 : (it - nq4) / h4;
+            const int j = 4 * (isq ? it - hh * h4 : it - nq4 - hh * h4);
+            const float* xp = row + (isq ? hh : n_head + hh) * hd;
+            const float4 x1 = *reinterpret_cast<const float4*>(xp + j);
+            const float4 x2 = *reinterpret_cast<const float4*>(xp + j + half);
+            const float4 c = *reinterpret_cast<const float4*>(cs + (int64_t)l * half + j);
+            const float4 s = *reinterpret_cast<const float4*>(sn + (int64_t)l * half + j);
+            const float4 y1 = make_float4(x1.x * c.x - x2.x * s.x, x1.y * c.y - x2.y * s.y,
+                                          x1.z * c.z - x2.z * s.z, x1.w * c.w - x2.w * s.w);
+            const float4 y2 = make_float4(x1.x * s.x + x2.x * c.x, x1.y * s.y + x2.y * c.y,
+                                          x1.z * s.z + x2.z * c.z, x1.w * s.w + x2.w * c.w);
+            float* yp = isq ? q_out + ((int64_t)l * n_head + hh) * hd
+                            : kc + ((int64_t)hh * cap + pos0 + l) * hd;
+            *reinterpret_cast<float4*>(yp + j) = y1;
+            *reinterpret_cast<float4*>(yp + j + half) = y2;
+        } else {
+            const int iv = it - nq4 - nk4, hh = iv / (hd / 4), d = 4 * (iv - hh * (hd / 4));
+            const float4 v = *reinterpret_cast<const float4*>(row + (int64_t)(n_head + n_kv + hh) * hd + d);
+            *reinterpret_cast<float4*>(vc + ((int64_t)hh * cap + pos0 + l) * hd + d) = v;
+        }
+    }
+}
+
 static unsigned grid1d(int64_t n) {
     int64_t g = (n + 255) / 256;
     if (g > 65536) g = 65536;
@@ -154,5 +196,26 @@ extern "C" int pe_kv_write(const float* k_src, const float* v_src, int64_t src_s
     hipLaunchKernelGGL(k_kv_write, dim3(grid1d(L * n_kv * head_dim)), dim3(256), 0,
                        (hipStream_t)stream, k_src, v_src, src_stride, n_kv, head_dim, L, pos0,
                        k_cache, v_cache, capacity);
+    return launch_status();
+}
+
+extern "C" int pe_rope_kv_write(const float* qkv, int64_t qkv_stride, const float* cos_rows,
+                                const float* sin_rows, int n_head, int n_kv, int head_dim, int64_t L,
+                                int64_t pos0, float* q_out, float* k_cache, float* v_cache,
+                                int64_t capacity, pe_stream_t stream) {
+    if (L < 0 || n_head <= 0 || n_kv <= 0 || head_dim <= 0 || head_dim % 8 || pos0 < 0 ||
+        capacity <= 0 || pos0 + L > capacity || qkv_stride < (int64_t)(n_head + 2 * n_kv) * head_dim ||
+        qkv_stride % 4)
+        return PE_ERR_SHAPE;
+    const int64_t per = (int64_t)(n_head + 2 * n_kv) * head_dim / 8 + (int64_t)n_kv * head_dim / 8;
+    if (L * per > 0x7FFFFFFF) return PE_ERR_SHAPE;
+    if (L == 0) return PE_OK;
+    if (!qkv || !cos_rows || !sin_rows || !q_out || !k_cache || !v_cache) return PE_ERR_NULL;
+    if (!aligned(qkv, 16) || !aligned(cos_rows, 16) || !aligned(sin_rows, 16) || !aligned(q_out, 16) ||
+        !aligned(k_cache, 16) || !aligned(v_cache, 16))
+        return PE_ERR_ALIGN;
+    hipLaunchKernelGGL(k_rope_kv_write, dim3(grid1d(L * per)), dim3(256), 0, (hipStream_t)stream, qkv,
+                       qkv_stride, cos_rows, sin_rows, n_head, n_kv, head_dim, (int)L, pos0, q_out, k_cache,
+                       v_cache, capacity);
     return launch_status();
 }

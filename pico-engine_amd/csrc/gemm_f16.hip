@@ -246,8 +246,8 @@ static dim3 gf_grid(int64_t M, int64_t N) {
     return dim3((unsigned)((N + kGfTile - 1) / kGfTile), (unsigned)((M + 32 * RT - 1) / (32 * RT)));
 }
 
-template <bool CH>
-static int gemm_silu_entry(const float* a, int64_t lda, const void* w_f16_il, void* c, int64_t ldc,
+template <bool AH, bool CH>
+static int gemm_silu_entry(const void* a, int64_t lda, const void* w_f16_il, void* c, int64_t ldc,
                            int64_t M, int64_t ffn, int64_t K, pe_stream_t stream) {
     if (M < 0 || ffn <= 0 || ffn % 16 || K <= 0 || K % kGfK) return PE_ERR_SHAPE;
     if (M == 0) return PE_OK;
@@ -255,15 +255,16 @@ static int gemm_silu_entry(const float* a, int64_t lda, const void* w_f16_il, vo
     if (lda < K || ldc < ffn) return PE_ERR_SHAPE;
     if ((M + kGfTile - 1) / kGfTile > 65535 || (N + kGfTile - 1) / kGfTile > 65535) return PE_ERR_SHAPE;
     if (!a || !w_f16_il || !c) return PE_ERR_NULL;
-    if (!aligned(a, 16) || lda % 4 || !aligned(w_f16_il, 16) || !aligned(c, CH ? 2 : 4))
+    if (!aligned(a, 16) || lda % (AH ? 8 : 4) || !aligned(w_f16_il, 16) || !aligned(c, CH ? 2 : 4))
         return PE_ERR_ALIGN;
-    GemmF16Args p{a, nullptr, lda, (const _Float16*)w_f16_il, nullptr, nullptr, 0,
+    GemmF16Args p{AH ? nullptr : (const float*)a, AH ? (const _Float16*)a : nullptr, lda,
+                  (const _Float16*)w_f16_il, nullptr, nullptr, 0,
                   CH ? nullptr : (float*)c, CH ? (_Float16*)c : nullptr, ldc, M, N, K};
     hipStream_t s = (hipStream_t)stream;
     if (gf_short(M, N))
-        hipLaunchKernelGGL((k_gemm_f16<2, false, false, true, false, CH>), gf_grid<2>(M, N), dim3(256), 0, s, p);
+        hipLaunchKernelGGL((k_gemm_f16<2, false, false, true, AH, CH>), gf_grid<2>(M, N), dim3(256), 0, s, p);
     else
-        hipLaunchKernelGGL((k_gemm_f16<4, false, false, true, false, CH>), gf_grid<4>(M, N), dim3(256), 0, s, p);
+        hipLaunchKernelGGL((k_gemm_f16<4, false, false, true, AH, CH>), gf_grid<4>(M, N), dim3(256), 0, s, p);
     return launch_status();
 }
 
@@ -298,12 +299,17 @@ static int gemm_entry(const void* a, int64_t lda, const void* w_f16, const float
 
 extern "C" int pe_gemm_f16_silu(const float* a, int64_t lda, const void* w_f16_il, float* c,
                                 int64_t ldc, int64_t M, int64_t ffn, int64_t K, pe_stream_t stream) {
-    return gemm_silu_entry<false>(a, lda, w_f16_il, c, ldc, M, ffn, K, stream);
+    return gemm_silu_entry<false, false>(a, lda, w_f16_il, c, ldc, M, ffn, K, stream);
 }
 
 extern "C" int pe_gemm_f16_silu_h(const float* a, int64_t lda, const void* w_f16_il, void* c_f16,
                                   int64_t ldc, int64_t M, int64_t ffn, int64_t K, pe_stream_t stream) {
-    return gemm_silu_entry<true>(a, lda, w_f16_il, c_f16, ldc, M, ffn, K, stream);
+    return gemm_silu_entry<false, true>(a, lda, w_f16_il, c_f16, ldc, M, ffn, K, stream);
+}
+
+extern "C" int pe_gemm_h16_silu_h(const void* a_f16, int64_t lda, const void* w_f16_il, void* c_f16,
+                                  int64_t ldc, int64_t M, int64_t ffn, int64_t K, pe_stream_t stream) {
+    return gemm_silu_entry<true, true>(a_f16, lda, w_f16_il, c_f16, ldc, M, ffn, K, stream);
 }
 
 extern "C" int pe_gemm_f16(const float* a, int64_t lda, const void* w_f16, const float* bias,

@@ -92,6 +92,7 @@ _SIGNATURES = {
     "pe_gemm_f16": (_I, [_P, _L, _P, _P, _P, _L, _P, _L, _L, _L, _L, _P]),
     "pe_gemm_f16_silu": (_I, [_P, _L, _P, _P, _L, _L, _L, _L, _P]),
     "pe_gemm_f16_silu_h": (_I, [_P, _L, _P, _P, _L, _L, _L, _L, _P]),
+    "pe_gemm_h16_silu_h": (_I, [_P, _L, _P, _P, _L, _L, _L, _L, _P]),
     "pe_gemm_h16": (_I, [_P, _L, _P, _P, _P, _L, _P, _L, _L, _L, _L, _P]),
     "pe_flash_prefill": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _L, _F, _P, _L, _P]),
     "pe_flash_prefill_h16": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _L, _F, _P, _L, _P]),
@@ -120,6 +121,7 @@ _SIGNATURES = {
     "pe_silu_mul": (_I, [_P, _L, _P, _L, _L, _L, _P]),
     "pe_qgemm": (_I, [_I, _P, _L, _L, _P, _L, _L, _P, _P, _L, _P, _L, _P]),
     "pe_kv_write": (_I, [_P, _P, _L, _I, _I, _L, _L, _P, _P, _L, _P]),
+    "pe_rope_kv_write": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _P, _P, _P, _L, _P]),
     "pe_prefill_attn": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _L, _F, _P, _L, _P]),
     "pe_decode_step_supported": (_I, [_I, _I, _I, _I, _I, _I, _L, _L]),
     "pe_decode_step_workspace_bytes": (_L, [_I, _I, _I, _I, _I, _I]),

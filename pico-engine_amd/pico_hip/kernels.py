@@ -271,13 +271,18 @@ def gemm_f16_silu(a: torch.Tensor, w16_il: torch.Tensor, out: torch.Tensor | Non
                   half: bool = False) -> torch.Tensor:
     """silu(A Wg^T) * (A Wu^T) on the matrix cores, W = interleave_gate_up_f16([gate; up]):
     gemm_f16 then silu_mul without the (M, 2 ffn) intermediate (model.py:218-224). half: the
-    result is stored in fp16 (pe_gemm_f16_silu_h), ready as gemm_f16's A operand."""
+    result is stored in fp16 (pe_gemm_f16_silu_h), ready as gemm_f16's A operand. An fp16 A
+    (rmsnorm(..., half=True)) needs half (pe_gemm_h16_silu_h) and gives the same bits as its
+    fp32 original."""
     dev = _on_gpu(a, w16_il)
     if a.dim() == 1:
         a = a.unsqueeze(0)
-    if a.dtype != torch.float32:
-        raise ValueError("a must be float32")
-    if a.stride(1) != 1 or a.stride(0) % 4 or a.data_ptr() % 16:
+    ah = a.dtype == torch.float16
+    if a.dtype != torch.float32 and not ah:
+        raise ValueError("a must be float32 or float16")
+    if ah and not half:
+        raise ValueError("an fp16 A needs half=True (pe_gemm_h16_silu_h)")
+    if a.stride(1) != 1 or a.stride(0) % (8 if ah else 4) or a.data_ptr() % 16:
         a = a.contiguous()
     M, K = a.shape
     N = w16_il.shape[0]
@@ -288,9 +293,9 @@ def gemm_f16_silu(a: torch.Tensor, w16_il: torch.Tensor, out: torch.Tensor | Non
         out = torch.empty(M, N // 2, device=dev, dtype=odt)
     if out.dtype != odt or out.stride(1) != 1 or tuple(out.shape) != (M, N // 2):
         raise ValueError(f"out must be a row-major ({M}, {N // 2}) {odt} tensor")
-    fn = lib.pe_gemm_f16_silu_h if half else lib.pe_gemm_f16_silu
-    check(fn(_ptr(a), a.stride(0), _ptr(w16_il), _ptr(out), out.stride(0), M, N // 2, K, _stream(dev)),
-          "pe_gemm_f16_silu_h" if half else "pe_gemm_f16_silu")
+    name = "pe_gemm_h16_silu_h" if ah else "pe_gemm_f16_silu_h" if half else "pe_gemm_f16_silu"
+    check(getattr(lib, name)(_ptr(a), a.stride(0), _ptr(w16_il), _ptr(out), out.stride(0), M, N // 2, K,
+                             _stream(dev)), name)
     return out
 
 
@@ -803,6 +808,29 @@ def kv_write(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: t
         k, v = k.contiguous(), v.contiguous()
     check(lib.pe_kv_write(_ptr(k), _ptr(v), k.stride(0), n_kv, hd, L, pos0, _ptr(k_cache),
                           _ptr(v_cache), k_cache.shape[1], _stream(dev)), "pe_kv_write")
+
+
+def rope_kv_write(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_head: int,
+                  k_cache: torch.Tensor, v_cache: torch.Tensor, pos0: int = 0,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """RoPE of the q and k heads of the fused QKV rows and the cache write of k and v in one
+    pass: returns rope(q) (L, n_head, hd); k_cache[h][pos0 + l] = rope(k[l][h]), v likewise
+    unrotated. qkv (L, (n_head + 2 n_kv) hd) with contiguous rows (row stride allowed), cos/sin
+    (L, hd/2): the same values as rope + kv_write (model.py:186-197)."""
+    dev = _on_gpu(qkv, cos, sin, k_cache, v_cache)
+    n_kv, capacity, hd = k_cache.shape
+    L = qkv.shape[0]
+    if qkv.dtype != torch.float32 or qkv.stride(1) != 1 or qkv.shape[1] != (n_head + 2 * n_kv) * hd:
+        raise ValueError("qkv must be float32 (L, (n_head + 2 n_kv) hd) with contiguous rows")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("KV caches must be contiguous (n_kv, capacity, hd) buffers")
+    c, s = cos.float().contiguous(), sin.float().contiguous()
+    if out is None:
+        out = torch.empty(L, n_head, hd, device=dev, dtype=torch.float32)
+    check(lib.pe_rope_kv_write(_ptr(qkv), qkv.stride(0), _ptr(c), _ptr(s), n_head, n_kv, hd, L, int(pos0),
+                               _ptr(out), _ptr(k_cache), _ptr(v_cache), capacity, _stream(dev)),
+          "pe_rope_kv_write")
+    return out
 
 
 def prefill_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos0: int = 0,

@@ -313,6 +313,7 @@ class Transformer:
         x = K.embed_gather(self.embed, token_ids)                       # (L, hidden)
         x_alt = torch.empty_like(x) if lt else None                    # the residual ping-pong
         qkv = torch.empty(Lt, qd + 2 * kd, device=self.device, dtype=torch.float32)
+        q_rot = torch.empty(Lt, nh, hd, device=self.device, dtype=torch.float32)
         for i, L in enumerate(self.layers):
             k_buf, v_buf = cache[i]
             W = w16[i]
@@ -322,24 +323,26 @@ class Transformer:
             else:
                 h = K.rmsnorm(x, L.attn_norm, cfg.eps)
                 K.gemm_f16(h, W["qkv"], bias=W["qkv_bias"], out=qkv)
-            qk = K.rope(qkv[:, :qd + kd].view(Lt, nh + nkv, hd), cos, sin)
-            v = qkv[:, qd + kd:].view(Lt, nkv, hd)
-            K.kv_write(qk[:, nh:], v, k_buf, v_buf, pos0=pos0)
+            # RoPE of q and k and the cache write of k and v, one pass (model.py:186-197)
+            qr = K.rope_kv_write(qkv, cos, sin, nh, k_buf, v_buf, pos0=pos0, out=q_rot)
             if hd == 64 and lt:
-                attn16 = K.flash_prefill(qk[:, :nh], k_buf, v_buf, pos0=pos0, half=True)
+                attn16 = K.flash_prefill(qr, k_buf, v_buf, pos0=pos0, half=True)
                 x, x_alt = K.gemm_lt(attn16, W["o"], residual=x, out=x_alt, workspace=ws), x
             else:
                 if hd == 64:  # matrix-core flash attention
-                    attn = K.flash_prefill(qk[:, :nh], k_buf, v_buf, pos0=pos0)  # (L, hidden)
+                    attn = K.flash_prefill(qr, k_buf, v_buf, pos0=pos0)  # (L, hidden)
                 else:         # other head sizes: the fp32 causal attention kernel
-                    attn = K.prefill_attn(qk[:, :nh], k_buf, v_buf, pos0=pos0)
+                    attn = K.prefill_attn(qr, k_buf, v_buf, pos0=pos0)
                 x = K.gemm_f16(attn, W["o"], residual=x)
                 if lt and x_alt.shape != x.shape:
                     x_alt = torch.empty_like(x)
-            h = K.rmsnorm(x, L.ffn_norm, cfg.eps)
             if W["gu_il"] is not None:
-                act = K.gemm_f16_silu(h, W["gu_il"], half=True)  # fp16: the down GEMM's operand
+                # the norm stored in fp16 (the values the GEMM rounds an fp32 A to), the SiLU
+                # product in fp16: the down GEMM's operand
+                h16 = K.rmsnorm(x, L.ffn_norm, cfg.eps, half=True)
+                act = K.gemm_f16_silu(h16, W["gu_il"], half=True)
             else:
+                h = K.rmsnorm(x, L.ffn_norm, cfg.eps)
                 act = K.silu_mul(K.gemm_f16(h, W["gu"]), cfg.ffn_dim)
             if lt and act.dtype == torch.float16:
                 x, x_alt = K.gemm_lt(act, W["down"], residual=x, out=x_alt, workspace=ws), x

@@ -907,6 +907,43 @@ def test_gemm_f16_silu_half_output_and_down_product(K, M, ffn, Kd):
     assert torch.equal(K.gemm_f16(act16, wd, residual=res), K.gemm_f16(act32, wd, residual=res))
 
 
+@pytest.mark.parametrize("M,ffn,Kd", [(300, 4864, 896), (13, 512, 3584), (129, 48, 96), (8192, 256, 64)])
+def test_gemm_h16_silu_equals_fp32_operand_path(K, M, ffn, Kd):
+    """The SiLU GEMM on an fp16 A (pe_gemm_h16_silu_h) gives the bits of the fp32-A GEMM on the
+    A those fp16 values came from (the fp32 path rounds A the same way as it reads it), and so
+    does an fp16 A from rmsnorm(half=True) against the fp32 norm."""
+    rng = np.random.default_rng(M + ffn + 5)
+    a = torch.from_numpy(rng.standard_normal((M, Kd)).astype(np.float32)).to(DEV)
+    w16 = torch.from_numpy((rng.standard_normal((2 * ffn, Kd)) * 0.05).astype(np.float16)).to(DEV)
+    wil = K.interleave_gate_up_f16(w16)
+    assert torch.equal(K.gemm_f16_silu(a.half(), wil, half=True), K.gemm_f16_silu(a, wil, half=True))
+    nw = torch.from_numpy(rng.standard_normal(Kd).astype(np.float32)).to(DEV)
+    h32, h16 = K.rmsnorm(a, nw, 1e-6), K.rmsnorm(a, nw, 1e-6, half=True)
+    assert torch.equal(K.gemm_f16_silu(h16, wil, half=True), K.gemm_f16_silu(h32, wil, half=True))
+    with pytest.raises(ValueError):
+        K.gemm_f16_silu(a.half(), wil)  # an fp16 A stores fp16 output
+
+
+@pytest.mark.parametrize("L,nh,nkv,hd,pos0", [(1, 14, 2, 64, 0), (77, 14, 2, 64, 5), (300, 28, 4, 128, 0),
+                                              (8, 4, 4, 64, 3)])
+def test_rope_kv_write_equals_rope_then_kv_write(K, L, nh, nkv, hd, pos0):
+    """One pass of RoPE on the q and k heads plus the cache write of k and v gives the bits of
+    rope followed by kv_write; nothing else in the caches is touched."""
+    rng = np.random.default_rng(L + nh + hd)
+    cap = pos0 + L + 4
+    qkv = torch.from_numpy(rng.standard_normal((L, (nh + 2 * nkv) * hd)).astype(np.float32)).to(DEV)
+    ang = rng.standard_normal((L, hd // 2)).astype(np.float32)
+    cos, sin = torch.from_numpy(np.cos(ang)).to(DEV), torch.from_numpy(np.sin(ang)).to(DEV)
+    k1 = torch.full((nkv, cap, hd), 7.0, device=DEV)
+    v1 = torch.full((nkv, cap, hd), 7.0, device=DEV)
+    k2, v2 = k1.clone(), v1.clone()
+    q = K.rope_kv_write(qkv, cos, sin, nh, k1, v1, pos0=pos0)
+    qk = K.rope(qkv[:, :(nh + nkv) * hd].view(L, nh + nkv, hd), cos, sin)
+    K.kv_write(qk[:, nh:], qkv[:, (nh + nkv) * hd:].view(L, nkv, hd), k2, v2, pos0=pos0)
+    assert torch.equal(q, qk[:, :nh])
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+
+
 @pytest.mark.parametrize("L,pos0", [(1, 0), (5, 0), (64, 0), (100, 7), (130, 0), (513, 0)])
 @pytest.mark.parametrize("n_head,n_kv", [(14, 2), (8, 8), (16, 4), (16, 1), (9, 3)])
 def test_flash_prefill_matches_closed_form(K, L, pos0, n_head, n_kv):
