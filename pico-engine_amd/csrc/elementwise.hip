@@ -124,6 +124,57 @@ __global__ void k_rope_kv_write(const float* __restrict__ qkv, int64_t qs, const
     }
 }
 
+// The same row norm with one wave per row (four rows per 256-thread workgroup): no block
+// barrier and no second read of the row, which stays in registers (E elements per lane, rows
+// up to 64 E). The sum of squares is formed in k_rmsnorm's order, so the results are the same
+// bits: lane l keeps the partial sums k_rmsnorm's threads l, l + 64, l + 128 and l + 192 form
+// (elements l + 64 (w + 4 j), j ascending, for wave w), reduces each with the same butterfly and
+// adds the four in wave order.
+template <typename OutT, int E>
+__global__ __launch_bounds__(256) void k_rmsnorm_wave(const float* __restrict__ x, int64_t xs,
+                                                      const float* __restrict__ w, OutT* __restrict__ y,
+                                                      int64_t ys, int64_t rows, int n, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;  // uniform per wave
+    const float* xr = x + r * xs;
+    float v[E];
+#pragma unroll
+    for (int m = 0; m < E; ++m) {
+        const int i = lane + 64 * m;
+        v[m] = i < n ? xr[i] : 0.f;
+    }
+    float ss[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < E; ++m)
+        if (lane + 64 * m < n) ss[m & 3] += v[m] * v[m];
+    const float tot = ((wave_sum<64>(ss[0]) + wave_sum<64>(ss[1])) + wave_sum<64>(ss[2])) + wave_sum<64>(ss[3]);
+    const float rstd = 1.0f / sqrtf(tot / (float)n + eps);
+    OutT* yr = y + r * ys;
+#pragma unroll
+    for (int m = 0; m < E; ++m) {
+        const int i = lane + 64 * m;
+        if (i < n) {
+            float o = (v[m] * rstd) * w[i];
+            if constexpr (sizeof(OutT) == 2) asm volatile("" : "+v"(o));
+            yr[i] = (OutT)o;
+        }
+    }
+}
+
+// Rows of up to 4096 elements: the one-wave form; longer rows k_rmsnorm.
+template <typename OutT>
+static void launch_rmsnorm(const float* x, int64_t xs, const float* w, OutT* y, int64_t ys, int64_t rows,
+                           int64_t n, float eps, hipStream_t s) {
+    const dim3 g4((unsigned)((rows + 3) / 4));
+    if (n <= 64 * 16)
+        hipLaunchKernelGGL((k_rmsnorm_wave<OutT, 16>), g4, dim3(256), 0, s, x, xs, w, y, ys, rows, (int)n, eps);
+    else if (n <= 64 * 64)
+        hipLaunchKernelGGL((k_rmsnorm_wave<OutT, 64>), g4, dim3(256), 0, s, x, xs, w, y, ys, rows, (int)n, eps);
+    else
+        hipLaunchKernelGGL(k_rmsnorm<OutT>, dim3((unsigned)rows), dim3(256), 0, s, x, xs, w, y, ys, n, eps);
+}
+
 static unsigned grid1d(int64_t n) {
     int64_t g = (n + 255) / 256;
     if (g > 65536) g = 65536;
@@ -140,8 +191,7 @@ extern "C" int pe_rmsnorm(const float* x, int64_t x_stride, const float* w, floa
     if (rows == 0) return PE_OK;
     if (!x || !w || !y) return PE_ERR_NULL;
     if (!aligned(x, 4) || !aligned(w, 4) || !aligned(y, 4)) return PE_ERR_ALIGN;
-    hipLaunchKernelGGL(k_rmsnorm<float>, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, x,
-                       x_stride, w, y, y_stride, n, eps);
+    launch_rmsnorm<float>(x, x_stride, w, y, y_stride, rows, n, eps, (hipStream_t)stream);
     return launch_status();
 }
 
@@ -151,8 +201,7 @@ extern "C" int pe_rmsnorm_h16(const float* x, int64_t x_stride, const float* w, 
     if (rows == 0) return PE_OK;
     if (!x || !w || !y) return PE_ERR_NULL;
     if (!aligned(x, 4) || !aligned(w, 4) || !aligned(y, 2)) return PE_ERR_ALIGN;
-    hipLaunchKernelGGL(k_rmsnorm<_Float16>, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, x,
-                       x_stride, w, (_Float16*)y, y_stride, n, eps);
+    launch_rmsnorm<_Float16>(x, x_stride, w, (_Float16*)y, y_stride, rows, n, eps, (hipStream_t)stream);
     return launch_status();
 }
 

@@ -847,6 +847,49 @@ def test_gemm_lt_matches_fp16_operand_reference(K, M, N, Kd, bias, res, extra):
         assert rel_err(x.cpu().numpy(), ref) < 1e-5
 
 
+def _rmsnorm_f32_emulated(x, w, eps):
+    """The device row norm's float32 arithmetic in its order: thread t = 64 w + l of a 256-wide
+    row sweep sums x[t + 256 j]^2 over j ascending; each wave's partials are added by the DPP /
+    permlane butterfly (partner lanes l^1, l^2, the half-row mirror, the row mirror, l^16, l^32;
+    every lane ends with the same bits), the four wave sums in wave order; rstd by IEEE division
+    and square root."""
+    f32 = np.float32
+    n = x.shape[0]
+    waves = []
+    for wv in range(4):
+        part = np.zeros(64, f32)
+        for ln in range(64):
+            acc = f32(0)
+            for i in range(64 * wv + ln, n, 256):
+                acc = f32(acc + f32(x[i] * x[i]))
+            part[ln] = acc
+        lanes = np.arange(64)
+        for p in (lanes ^ 1, lanes ^ 2, (lanes & ~7) | (7 - (lanes & 7)), (lanes & ~15) | (15 - (lanes & 15)),
+                  lanes ^ 16, lanes ^ 32):
+            part = (part + part[p]).astype(f32)
+        waves.append(part[0])
+    tot = f32(f32(f32(waves[0] + waves[1]) + waves[2]) + waves[3])
+    rstd = f32(f32(1) / np.sqrt(f32(f32(tot / f32(n)) + f32(eps))))
+    return ((x * rstd).astype(f32) * w).astype(f32)
+
+
+@pytest.mark.parametrize("n", [64, 896, 1000, 3584, 4096, 5000])
+def test_rmsnorm_bits_follow_the_summation_order(K, n):
+    """Both row-norm kernels (one wave per row up to 4096 elements, one workgroup per row
+    beyond) give the bits of the float32 emulation of their common summation order, in fp32
+    and rounded to fp16."""
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal((3, n)).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    X, Wt = torch.from_numpy(x).to(DEV), torch.from_numpy(w).to(DEV)
+    got32 = K.rmsnorm(X, Wt, 1e-6).cpu().numpy()
+    got16 = K.rmsnorm(X, Wt, 1e-6, half=True).cpu().numpy()
+    for r in range(3):
+        want = _rmsnorm_f32_emulated(x[r], w, 1e-6)
+        np.testing.assert_array_equal(got32[r].view(np.uint32), want.view(np.uint32))
+        np.testing.assert_array_equal(got16[r].view(np.uint16), want.astype(np.float16).view(np.uint16))
+
+
 def test_rmsnorm_and_flash_half_outputs_are_rounded_fp32_outputs(K):
     """pe_rmsnorm_h16 and pe_flash_prefill_h16 store the fp32 kernels' values rounded to fp16
     (nearest even), bit for bit: the operands the prefill GEMMs would round as they read them."""
