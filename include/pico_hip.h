@@ -171,21 +171,6 @@ int pe_gemm_lt(const void* a_f16, int64_t lda, const void* w_f16, int64_t M, int
                const float* bias, const float* residual, int64_t ldr, float* c, int64_t ldc,
                void* workspace, int64_t workspace_bytes, pe_stream_t stream);
 
-/* Picks pe_gemm_lt's algorithm for one shape by timing: the first (up to 8) candidates of
- * hipBLASLt's heuristic for the shape of the matching pe_gemm_lt call (same M, N, K, lda, ldc,
- * ldr, bias or not, residual or not (has_res), workspace size) run on the given buffers and the
- * fastest is kept for every later pe_gemm_lt call of the shape. Without it the heuristic's first
- * candidate is used (measured on MI355X at 8192 prompt rows: the QKV, o-projection and ffn_down
- * products 36.6 / 39.5 / 82.8 us with it, 31.1 / 28.2 / 77.2 with the fastest of eight). It
- * synchronises the stream (HIP events) and must not be captured in a graph; each candidate runs
- * with beta = 0 into c (the residual is not read), so c may not alias a, w or bias, and holds a
- * product without the residual afterwards. A shape tuned before returns at once. The pick
- * depends on timings, so two processes may pick different candidates (results then differ at
- * most by the accumulation order hipBLASLt uses). No counterpart in the reference. */
-int pe_gemm_lt_tune(const void* a_f16, int64_t lda, const void* w_f16, int64_t M, int64_t N,
-                    int64_t K, const float* bias, int has_res, int64_t ldr, float* c, int64_t ldc,
-                    void* workspace, int64_t workspace_bytes, pe_stream_t stream);
-
 /* out[l][:] = dequantized row ids[l] of a raw GGUF (vocab x hidden) table, l < n_ids.
  * An id outside [0, vocab) yields a row of NaN (no out-of-bounds read). layout: PE_LAYOUT_Y_UT
  * writes each row in the unit-transposed layout (hidden % 32 == 0).

@@ -11,8 +11,8 @@
 // along D's rows (N), and beta = 1 with C = R adds the residual.
 //
 // State: one hipBLASLt handle per device and a cache of matmul plans (descriptors, layouts and
-// the heuristic's first algorithm, or the fastest of its first candidates once
-// pe_gemm_lt_tune has timed them) per shape, guarded by a mutex; the workspace is the caller's.
+// the heuristic's first algorithm) per shape, guarded by a mutex; the workspace is the
+// caller's.
 #include <hipblaslt/hipblaslt.h>
 
 #include <map>
@@ -21,15 +21,12 @@
 
 #include "pe_common.h"
 
-using namespace pe;
-
 namespace {
 
 struct LtPlan {
     hipblasLtMatmulDesc_t op = nullptr;
     hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
     hipblasLtMatmulAlgo_t algo{};
-    bool tuned = false;
 };
 
 using LtKey = std::tuple<int, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int, int, int64_t>;
@@ -92,9 +89,13 @@ const LtPlan* get_plan(hipblasLtHandle_t h, int dev, int64_t M, int64_t N, int64
     return &(g_lt_plans[key] = p);
 }
 
-// Shared checks of pe_gemm_lt and pe_gemm_lt_tune.
-int lt_check(const void* a, int64_t lda, const void* w, int64_t M, int64_t N, int64_t K, const float* bias,
-             const float* res, int64_t ldr, float* c, int64_t ldc, void* workspace, int64_t workspace_bytes) {
+}  // namespace
+
+using namespace pe;
+
+extern "C" int pe_gemm_lt(const void* a, int64_t lda, const void* w, int64_t M, int64_t N, int64_t K,
+                          const float* bias, const float* res, int64_t ldr, float* c, int64_t ldc,
+                          void* workspace, int64_t workspace_bytes, pe_stream_t stream) {
     if (M < 0 || N <= 0 || K <= 0 || lda < K || ldc < N) return PE_ERR_SHAPE;
     if (res && ldr != ldc) return PE_ERR_SHAPE;
     if (M == 0) return PE_OK;
@@ -102,31 +103,17 @@ int lt_check(const void* a, int64_t lda, const void* w, int64_t M, int64_t N, in
     if (!aligned(a, 16) || !aligned(w, 16) || !aligned(c, 16) || !aligned(res, 16) || !aligned(bias, 16) ||
         lda % 8 || ldc % 4 || K % 8 || !aligned(workspace, 256))
         return PE_ERR_ALIGN;
-    return PE_OK;
-}
-
-// The handle of the current device (created on first use); call with g_lt_mutex held.
-hipblasLtHandle_t lt_handle(int dev) {
-    auto hit = g_lt_handles.find(dev);
-    if (hit != g_lt_handles.end()) return hit->second;
-    hipblasLtHandle_t h = nullptr;
-    if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) return nullptr;
-    g_lt_handles[dev] = h;
-    return h;
-}
-
-}  // namespace
-
-extern "C" int pe_gemm_lt(const void* a, int64_t lda, const void* w, int64_t M, int64_t N, int64_t K,
-                          const float* bias, const float* res, int64_t ldr, float* c, int64_t ldc,
-                          void* workspace, int64_t workspace_bytes, pe_stream_t stream) {
-    const int st = lt_check(a, lda, w, M, N, K, bias, res, ldr, c, ldc, workspace, workspace_bytes);
-    if (st || M == 0) return st;
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess) return PE_ERR_LAUNCH;
     std::lock_guard<std::mutex> lock(g_lt_mutex);
-    hipblasLtHandle_t h = lt_handle(dev);
-    if (!h) return PE_ERR_LAUNCH;
+    hipblasLtHandle_t h = nullptr;
+    auto hit = g_lt_handles.find(dev);
+    if (hit == g_lt_handles.end()) {
+        if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) return PE_ERR_LAUNCH;
+        g_lt_handles[dev] = h;
+    } else {
+        h = hit->second;
+    }
     const LtPlan* p = get_plan(h, dev, M, N, K, lda, ldc, ldr, bias != nullptr, res != nullptr, workspace_bytes);
     if (!p) return PE_ERR_LAUNCH;
     if (bias && hipblasLtMatmulDescSetAttribute(p->op, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias)) !=
@@ -134,75 +121,8 @@ extern "C" int pe_gemm_lt(const void* a, int64_t lda, const void* w, int64_t M, 
         return PE_ERR_LAUNCH;
     const float alpha = 1.0f, beta = res ? 1.0f : 0.0f;
     const void* cin = res ? (const void*)res : (const void*)c;
-    const hipblasStatus_t mst = hipblasLtMatmul(h, p->op, &alpha, w, p->la, a, p->lb, &beta, cin, p->lc, c, p->lc,
-                                                &p->algo, workspace, (size_t)workspace_bytes, (hipStream_t)stream);
-    if (mst != HIPBLAS_STATUS_SUCCESS) return PE_ERR_LAUNCH;
-    return launch_status();
-}
-
-// Times the first candidates of the heuristic (up to kLtTuneCandidates) for this shape on the
-// given buffers and keeps the fastest in the shape's plan; later pe_gemm_lt calls of the shape
-// use it. Synchronises the stream (events); not for graph capture. Runs each candidate with
-// beta = 0 into c (res is not read: c may not alias any input), so c holds a product without
-// the residual afterwards. A shape tuned before is not timed again.
-extern "C" int pe_gemm_lt_tune(const void* a, int64_t lda, const void* w, int64_t M, int64_t N, int64_t K,
-                               const float* bias, int has_res, int64_t ldr, float* c, int64_t ldc,
-                               void* workspace, int64_t workspace_bytes, pe_stream_t stream) {
-    constexpr int kLtTuneCandidates = 8, kLtTuneReps = 5;
-    const int st = lt_check(a, lda, w, M, N, K, bias, nullptr, ldr, c, ldc, workspace, workspace_bytes);
-    if (st || M == 0) return st;
-    if (has_res && ldr != ldc) return PE_ERR_SHAPE;
-    int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess) return PE_ERR_LAUNCH;
-    std::lock_guard<std::mutex> lock(g_lt_mutex);
-    hipblasLtHandle_t h = lt_handle(dev);
-    if (!h) return PE_ERR_LAUNCH;
-    LtPlan* p = const_cast<LtPlan*>(
-        get_plan(h, dev, M, N, K, lda, ldc, ldr, bias != nullptr, has_res != 0, workspace_bytes));
-    if (!p) return PE_ERR_LAUNCH;
-    if (p->tuned) return PE_OK;
-    if (bias && hipblasLtMatmulDescSetAttribute(p->op, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias)) !=
-                    HIPBLAS_STATUS_SUCCESS)
-        return PE_ERR_LAUNCH;
-    hipblasLtMatmulPreference_t pref = nullptr;
-    if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return PE_ERR_LAUNCH;
-    const uint64_t wsz = (uint64_t)workspace_bytes;
-    hipblasLtMatmulHeuristicResult_t heur[kLtTuneCandidates]{};
-    int found = 0;
-    bool ok = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz,
-                                                    sizeof(wsz)) == HIPBLAS_STATUS_SUCCESS &&
-              hipblasLtMatmulAlgoGetHeuristic(h, p->op, p->la, p->lb, p->lc, p->lc, pref, kLtTuneCandidates, heur,
-                                              &found) == HIPBLAS_STATUS_SUCCESS && found > 0;
-    hipblasLtMatmulPreferenceDestroy(pref);
-    if (!ok) return PE_ERR_LAUNCH;
-    hipStream_t s = (hipStream_t)stream;
-    hipEvent_t e0 = nullptr, e1 = nullptr;
-    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
-        if (e0) (void)hipEventDestroy(e0);
-        return PE_ERR_LAUNCH;
-    }
-    const float alpha = 1.0f, beta = 0.0f;
-    float best = -1.0f;
-    int best_i = 0;
-    for (int i = 0; i < found; ++i) {
-        auto run = [&]() {
-            return hipblasLtMatmul(h, p->op, &alpha, w, p->la, a, p->lb, &beta, c, p->lc, c, p->lc, &heur[i].algo,
-                                   workspace, (size_t)workspace_bytes, s) == HIPBLAS_STATUS_SUCCESS;
-        };
-        if (!run()) continue;  // a candidate that does not run is skipped
-        bool good = hipEventRecord(e0, s) == hipSuccess;
-        for (int r = 0; r < kLtTuneReps && good; ++r) good = run();
-        good = good && hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
-        float ms = 0.f;
-        if (good && hipEventElapsedTime(&ms, e0, e1) == hipSuccess && (best < 0.f || ms < best)) {
-            best = ms;
-            best_i = i;
-        }
-    }
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
-    if (best < 0.f) return PE_ERR_LAUNCH;
-    p->algo = heur[best_i].algo;
-    p->tuned = true;
+    const hipblasStatus_t st = hipblasLtMatmul(h, p->op, &alpha, w, p->la, a, p->lb, &beta, cin, p->lc, c, p->lc,
+                                               &p->algo, workspace, (size_t)workspace_bytes, (hipStream_t)stream);
+    if (st != HIPBLAS_STATUS_SUCCESS) return PE_ERR_LAUNCH;
     return launch_status();
 }

@@ -883,17 +883,12 @@ def gemm_lt_workspace(device) -> torch.Tensor:
     return torch.empty(GEMM_LT_WORKSPACE, device=device, dtype=torch.uint8)
 
 
-_lt_tuned: set = set()
-
-
 def gemm_lt(a16: torch.Tensor, w16: torch.Tensor, bias: torch.Tensor | None = None,
             residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
-            workspace: torch.Tensor | None = None, tune: bool = False) -> torch.Tensor:
+            workspace: torch.Tensor | None = None) -> torch.Tensor:
     """C = A W^T (+ bias) (+ residual) on hipBLASLt (pe_gemm_lt): A fp16 (M, K) (rows may be
     strided), W fp16 (N, K), fp32 accumulation and result (M, N). ``residual`` may be ``out``
-    (added in place); its row stride must equal out's. ``tune``: the first call of a shape in
-    this process times hipBLASLt's first candidates on a scratch output (pe_gemm_lt_tune,
-    synchronising; not under graph capture) and keeps the fastest for the shape."""
+    (added in place); its row stride must equal out's."""
     dev = _on_gpu(a16, w16, bias, residual)
     if a16.dim() == 1:
         a16 = a16.unsqueeze(0)
@@ -920,15 +915,6 @@ def gemm_lt(a16: torch.Tensor, w16: torch.Tensor, bias: torch.Tensor | None = No
         ldr = residual.stride(0)
     if workspace is None:
         workspace = gemm_lt_workspace(dev)
-    key = (dev.index, M, N, K, a16.stride(0), out.stride(0), ldr, bias is not None, residual is not None,
-           workspace.numel())
-    if tune and key not in _lt_tuned:
-        scratch = torch.empty_like(out)
-        check(lib.pe_gemm_lt_tune(_ptr(a16), a16.stride(0), _ptr(w16), M, N, K,
-                                  _ptr(None if bias is None else _f32c(bias)), int(residual is not None), ldr,
-                                  _ptr(scratch), out.stride(0), _ptr(workspace), workspace.numel(), _stream(dev)),
-              "pe_gemm_lt_tune")
-        _lt_tuned.add(key)
     check(lib.pe_gemm_lt(_ptr(a16), a16.stride(0), _ptr(w16), M, N, K,
                          _ptr(None if bias is None else _f32c(bias)), _ptr(residual), ldr, _ptr(out),
                          out.stride(0), _ptr(workspace), workspace.numel(), _stream(dev)), "pe_gemm_lt")
@@ -940,8 +926,7 @@ __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "
            "q8_0_gemv", "q5_0_gemv", "q5_0_gemv_norm", "q6_k_gemv", "q4_k_gemv", "qgemv_norm",
            "qgemv_norm_silu", "qkv_rmsnorm_rope", "qgemv_sum_norm_silu", "qgemm", "kv_write", "prefill_attn",
            "gemm_lt", "gemm_lt_workspace", "mgemv", "repack_mfma", "mfma_eligible", "MFMA_MIN_WEIGHTS",
-           "attn_gproj", "attn_gproj_supported", "attn_split_gproj", "attn_split_gproj_supported",
-           "rope_kv_write", "qgemv_norm_argmax", "dequantize_weight_f16",
+           "attn_gproj", "attn_gproj_supported", "qgemv_norm_argmax", "dequantize_weight_f16",
            "DecodeStep", "decode_step_supported", "decode_step_workspace",
            "gemm_f16", "gemm_f16_silu", "interleave_gate_up_f16", "flash_prefill",
            "BLOCK_SIZE"]

@@ -113,9 +113,6 @@ class Transformer:
         # the matrix-core prefill's plain products (QKV + bias, o-proj and ffn_down + residual)
         # on hipBLASLt; off: every product on this library's MFMA GEMM (pe_gemm_f16)
         self.prefill_blaslt = True
-        # the first prefill of each product shape times hipBLASLt's first candidates and keeps
-        # the fastest (pe_gemm_lt_tune); off: the heuristic's first candidate
-        self.prefill_blaslt_tune = True
         self._lt_ws: torch.Tensor | None = None
         self._f16: list[dict[str, torch.Tensor]] | None = None
         # greedy decode steps the persistent kernel covers can run as one launch per token
@@ -313,7 +310,6 @@ class Transformer:
         if lt and self._lt_ws is None:
             self._lt_ws = K.gemm_lt_workspace(self.device)
         ws = self._lt_ws
-        tune = self.prefill_blaslt_tune
         x = K.embed_gather(self.embed, token_ids)                       # (L, hidden)
         x_alt = torch.empty_like(x) if lt else None                    # the residual ping-pong
         qkv = torch.empty(Lt, qd + 2 * kd, device=self.device, dtype=torch.float32)
@@ -323,7 +319,7 @@ class Transformer:
             W = w16[i]
             if lt:  # the plain products on hipBLASLt, their operands stored in fp16
                 h16 = K.rmsnorm(x, L.attn_norm, cfg.eps, half=True)
-                K.gemm_lt(h16, W["qkv"], bias=W["qkv_bias"], out=qkv, workspace=ws, tune=tune)
+                K.gemm_lt(h16, W["qkv"], bias=W["qkv_bias"], out=qkv, workspace=ws)
             else:
                 h = K.rmsnorm(x, L.attn_norm, cfg.eps)
                 K.gemm_f16(h, W["qkv"], bias=W["qkv_bias"], out=qkv)
@@ -331,7 +327,7 @@ class Transformer:
             qr = K.rope_kv_write(qkv, cos, sin, nh, k_buf, v_buf, pos0=pos0, out=q_rot)
             if hd == 64 and lt:
                 attn16 = K.flash_prefill(qr, k_buf, v_buf, pos0=pos0, half=True)
-                x, x_alt = K.gemm_lt(attn16, W["o"], residual=x, out=x_alt, workspace=ws, tune=tune), x
+                x, x_alt = K.gemm_lt(attn16, W["o"], residual=x, out=x_alt, workspace=ws), x
             else:
                 if hd == 64:  # matrix-core flash attention
                     attn = K.flash_prefill(qr, k_buf, v_buf, pos0=pos0)  # (L, hidden)
@@ -349,7 +345,7 @@ class Transformer:
                 h = K.rmsnorm(x, L.ffn_norm, cfg.eps)
                 act = K.silu_mul(K.gemm_f16(h, W["gu"]), cfg.ffn_dim)
             if lt and act.dtype == torch.float16:
-                x, x_alt = K.gemm_lt(act, W["down"], residual=x, out=x_alt, workspace=ws, tune=tune), x
+                x, x_alt = K.gemm_lt(act, W["down"], residual=x, out=x_alt, workspace=ws), x
             else:
                 x = K.gemm_f16(act, W["down"], residual=x)
         return self._lm_head(x[-1], self.w["output_norm.weight"], greedy, K.LAYOUT_NATURAL)

@@ -837,14 +837,6 @@ def test_gemm_lt_matches_fp16_operand_reference(K, M, N, Kd, bias, res, extra):
         x = T(r)
         K.gemm_lt(A, T(w16), bias=T(b), residual=x, out=x, workspace=ws)
         assert rel_err(x.cpu().numpy(), ref) < 1e-5
-    # the tuned plan of the shape (pe_gemm_lt_tune, first call only), including the residual
-    # added in place: the tuning runs into a scratch output and leaves the residual alone
-    ct = K.gemm_lt(A, T(w16), bias=T(b), residual=T(r), workspace=ws, tune=True).cpu().numpy()
-    assert rel_err(ct, ref) < 1e-5
-    if res:
-        x = T(r)
-        K.gemm_lt(A, T(w16), bias=T(b), residual=x, out=x, workspace=ws, tune=True)
-        assert rel_err(x.cpu().numpy(), ref) < 1e-5
 
 
 def _rmsnorm_f32_emulated(x, w, eps):
