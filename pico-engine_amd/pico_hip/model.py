@@ -2,8 +2,9 @@
 
 ``ModelConfig`` and ``Transformer(cfg, weights, device, quant).forward(token_ids, positions,
 cache) -> logits`` keep the reference's signatures (model.py:27-57, :60-62, :128-165).
-With ``use_step_kernel`` set (off by default: measured at parity with the four-launch step,
-526 vs 519 us per token at config 0), a greedy decode step of a model the persistent kernel
+With ``use_step_kernel`` set (off by default: about 2 % faster than the four-launch step at
+config 0 in a same-box A/B, 2062 vs 2025 tok/s, but it needs every workgroup resident at once
+and raises if a bounded wait runs out), a greedy decode step of a model the persistent kernel
 covers (head_dim 64, hidden <= 1024, ffn <= 8192, caches up to 128 positions: the 0.5B
 family) is one launch, pe_decode_step. Otherwise decode (one token) runs four launches per
 layer plus the embedding row and the LM head:
@@ -116,8 +117,8 @@ class Transformer:
         self._lt_ws: torch.Tensor | None = None
         self._f16: list[dict[str, torch.Tensor]] | None = None
         # greedy decode steps the persistent kernel covers can run as one launch per token
-        # (pe_decode_step) instead of four launches per layer; off by default while it measures
-        # slower than the per-operation launches
+        # (pe_decode_step) instead of four launches per layer; off by default: ~2 % faster, but
+        # it needs all of its workgroups resident at once (one per CU)
         self.use_step_kernel = False
         self._step_ws: torch.Tensor | None = None
         self._steps: dict[tuple[int, int], K.DecodeStep] = {}
