@@ -10,8 +10,14 @@
  *   - is asynchronous on the given stream and graph-capturable: it performs no
  *     allocation, copy or synchronisation; every buffer (workspaces included) is owned
  *     by the caller, except the scratch array of pe_decode_attn_noalloc (see there);
- *   - is thread-safe: the library keeps no mutable global state (pe_decode_attn_noalloc
- *     caches its scratch array's device address per GPU, set once).
+ *   - is thread-safe. The library's global state is limited to: per-device kernel
+ *     attributes set once (the dynamic LDS limits of pe_mgemv and pe_decode_step, in
+ *     atomics); pe_decode_attn_noalloc's scratch address per GPU, set once; and
+ *     pe_gemm_lt's hipBLASLt handle per device and matmul-plan cache, behind a mutex.
+ *   Exception to "no allocation": pe_gemm_lt creates its device's hipBLASLt handle on the
+ *   first call (or in pe_gemm_lt_init) and a matmul plan on the first call for each shape;
+ *   those host-side allocations make such a first call unsuitable for graph capture. Call
+ *   pe_gemm_lt_init at set-up, and run a shape once before capturing it.
  *
  * Quantized weights: the decode kernels read a "tiled" copy of a GGUF tensor made
  * on the device by pe_repack. Tiling is a pure byte permutation of the GGUF blocks
@@ -164,12 +170,19 @@ int pe_flash_prefill_h16(const float* q, int64_t q_stride, const float* k_cache,
  * K % 8 == 0, 16-byte aligned), fp32 accumulation, c and residual fp32 with row stride ldc
  * (residual == c adds in place; ldr must equal ldc). workspace: device memory for hipBLASLt
  * (32 MiB suffices), any contents; calls that overlap must not share it. The library keeps one
- * hipBLASLt handle per device and a cache of matmul plans per shape, guarded by a mutex.
+ * hipBLASLt handle per device and a cache of matmul plans per shape, guarded by a mutex; the
+ * first call for a device creates the handle (unless pe_gemm_lt_init did) and the first call
+ * for a shape creates its plan (host allocations: not capture-safe on those calls).
  * Replaces the plain prefill F.linear / addmm calls under autocast (model.py:147-151, :177,
  * :213, :235): QKV with its bias, the o-projection and ffn_down with the residual. */
 int pe_gemm_lt(const void* a_f16, int64_t lda, const void* w_f16, int64_t M, int64_t N, int64_t K,
                const float* bias, const float* residual, int64_t ldr, float* c, int64_t ldc,
                void* workspace, int64_t workspace_bytes, pe_stream_t stream);
+
+/* Creates the current device's hipBLASLt handle for pe_gemm_lt now (model load), outside any
+ * graph capture; a no-op when it exists. No counterpart in the reference (torch creates its
+ * cuBLAS handle lazily). */
+int pe_gemm_lt_init(void);
 
 /* out[l][:] = dequantized row ids[l] of a raw GGUF (vocab x hidden) table, l < n_ids.
  * An id outside [0, vocab) yields a row of NaN (no out-of-bounds read). layout: PE_LAYOUT_Y_UT
@@ -222,12 +235,15 @@ int pe_repack_mfma(int ggml_type, const void* blocks, void* w_mfma, int64_t n, i
  *              residual must be NULL),
  * with h = rmsnorm(x) * norm_w (eps) when norm_w is not NULL, else h = x. The activation is
  * split exactly into four int8 planes per 32 elements (every element to 2^-28 of its
- * sub-block's largest), the integer products are exact, scales and sums fp32. k % 256 == 0,
- * k <= 2^20 (the planes of x stay in LDS: about 144 bytes per 32 elements). layout:
+ * sub-block's largest), the integer products are exact, scales and sums fp32. k % 256 == 0;
+ * the planes of x stay in LDS (144 bytes per 32 elements, plus 32 KiB of partial sums; 512 +
+ * 16 bytes per 32 elements when k <= 4096), so k is bounded by the device's LDS per workgroup:
+ * k <= 28928 on a 160 KiB gfx950 CU (larger k returns PE_ERR_SHAPE). layout:
  * PE_LAYOUT_X_UT (x, norm_w) / PE_LAYOUT_Y_UT (y, residual; n % 32 == 0). Deterministic.
  * Replaces q4_k_gemv / q6_k_gemv (kernels.py:286, :326) with the fused RMSNorm + gate/up +
  * SiLU and the residual adds of model.py:213-235, for matrices large enough that HBM bounds
- * them (the 7B-architecture model's gate/up, ffn_down and o-projection). */
+ * them (the 7B-architecture model's gate/up and ffn_down; its 12.8M-weight o-projection stays on
+ * the tiled GEMV, which is faster at that size). */
 int pe_mgemv(int ggml_type, const void* w_mfma, int64_t n, int64_t k, const float* x,
              const float* norm_w, float eps, const float* residual, float* y, int silu,
              int layout, pe_stream_t stream);

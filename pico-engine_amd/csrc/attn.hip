@@ -36,8 +36,7 @@ struct AttnParams {
     float scale;
     int round_fp16;
     float* out;
-    unsigned* counters;
-    float* partials;
+    float* partials;   // the split records (the workspace)
     int nsplit;
     int out_ut;  // write out in the unit-transposed layout
 };
@@ -786,7 +785,7 @@ extern "C" int64_t pe_decode_attn_workspace_bytes(int n_head, int n_kv, int head
         (head_dim != 64 && head_dim != 128) || capacity <= 0)
         return -PE_ERR_SHAPE;
     const int G = n_head / n_kv;
-    return 256 + (int64_t)n_kv * attn_nsplit(capacity) * G * (head_dim + 4) * 4;
+    return (int64_t)n_kv * attn_nsplit(capacity) * G * (head_dim + 4) * 4;
 }
 
 // Host validation shared by pe_decode_attn and pe_decode_attn_noalloc (everything but the
@@ -877,8 +876,7 @@ static int launch_decode_attn(const float* q, const float* k_cache, const float*
                               int round_fp16, float* out, void* workspace, int layout,
                               pe_stream_t stream) {
     AttnParams p{q, k_cache, v_cache, n_kv, n_head / n_kv, capacity, len_dev, len_dtype, len_add,
-                 scale, round_fp16, out, (unsigned*)workspace,
-                 (float*)((char*)workspace + 256), (int)attn_nsplit(capacity),
+                 scale, round_fp16, out, (float*)workspace, (int)attn_nsplit(capacity),
                  (layout & PE_LAYOUT_Y_UT) ? 1 : 0};
     hipStream_t s = (hipStream_t)stream;
     if (capacity <= kSmallCap) {
@@ -978,8 +976,7 @@ extern "C" int pe_attn_split_gproj(const float* q, const float* k_cache, const f
         (len_dtype == 2 && !aligned(len_dev, 8)))
         return PE_ERR_ALIGN;
     AttnParams p{q, k_cache, v_cache, n_kv, n_head / n_kv, capacity, len_dev, len_dtype, len_add,
-                 scale, round_fp16, nullptr, (unsigned*)workspace,
-                 (float*)((char*)workspace + 256), (int)attn_nsplit(capacity), 0};
+                 scale, round_fp16, nullptr, (float*)workspace, (int)attn_nsplit(capacity), 0};
     const int64_t qd = (int64_t)n_head * head_dim;
     MgpParams mp{p, make_tiled(wo_tiled, hidden, qd / block_elems(wo_type)), hidden, parts, layout};
     hipStream_t s = (hipStream_t)stream;

@@ -727,7 +727,11 @@ __global__ __launch_bounds__(kNT, 1) void k_decode_step(StepParams P) {
     uint64_t* wkeys = reinterpret_cast<uint64_t*>(lds + kLdsRed);
     if (lane == 0) wkeys[tid >> 6] = b;
     __syncthreads();
-    if (tid == 0) {
+    // A launch whose waits ran out advances neither the decode state nor the launch counter:
+    // its picks are not valid, and workgroups of it that started late may still publish pairs
+    // under its tag. The host clears the whole workspace (counter, error word and every pair)
+    // when it reads a non-zero error word, before any further launch on it.
+    if (tid == 0 && !c.failed) {
 #pragma unroll
         for (int q = 0; q < kWaves; ++q) b = wkeys[q] > b ? wkeys[q] : b;
         const int64_t tok = argmax_row(b);
@@ -876,12 +880,15 @@ extern "C" int pe_decode_step(const pe_step_args* a, pe_stream_t stream) {
     hipStream_t s = (hipStream_t)stream;
     // more than half of a CU's LDS per workgroup: no two workgroups share a CU
     const size_t lds = kStepLdsBytes;
-    static std::atomic<int> lds_set{0};
-    if (!lds_set.load(std::memory_order_acquire)) {
+    // the dynamic LDS limit is a per-device function attribute: set once per device
+    static std::atomic<int> lds_set[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return PE_ERR_LAUNCH;
+    if (!lds_set[dev].load(std::memory_order_acquire)) {
         if (hipFuncSetAttribute((const void*)k_decode_step, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds) != hipSuccess)
             return PE_ERR_LAUNCH;
-        lds_set.store(1, std::memory_order_release);
+        lds_set[dev].store(1, std::memory_order_release);
     }
     hipLaunchKernelGGL(k_decode_step, dim3(G), dim3(kNT), lds, s, P);
     return launch_status();

@@ -89,9 +89,26 @@ const LtPlan* get_plan(hipblasLtHandle_t h, int dev, int64_t M, int64_t N, int64
     return &(g_lt_plans[key] = p);
 }
 
+// The device's handle, created on first use (the caller holds g_lt_mutex); nullptr on failure.
+hipblasLtHandle_t lt_handle(int dev) {
+    auto hit = g_lt_handles.find(dev);
+    if (hit != g_lt_handles.end()) return hit->second;
+    hipblasLtHandle_t h = nullptr;
+    if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) return nullptr;
+    g_lt_handles[dev] = h;
+    return h;
+}
+
 }  // namespace
 
 using namespace pe;
+
+extern "C" int pe_gemm_lt_init(void) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) return PE_ERR_LAUNCH;
+    std::lock_guard<std::mutex> lock(g_lt_mutex);
+    return lt_handle(dev) ? PE_OK : PE_ERR_LAUNCH;
+}
 
 extern "C" int pe_gemm_lt(const void* a, int64_t lda, const void* w, int64_t M, int64_t N, int64_t K,
                           const float* bias, const float* res, int64_t ldr, float* c, int64_t ldc,
@@ -106,14 +123,8 @@ extern "C" int pe_gemm_lt(const void* a, int64_t lda, const void* w, int64_t M, 
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess) return PE_ERR_LAUNCH;
     std::lock_guard<std::mutex> lock(g_lt_mutex);
-    hipblasLtHandle_t h = nullptr;
-    auto hit = g_lt_handles.find(dev);
-    if (hit == g_lt_handles.end()) {
-        if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) return PE_ERR_LAUNCH;
-        g_lt_handles[dev] = h;
-    } else {
-        h = hit->second;
-    }
+    const hipblasLtHandle_t h = lt_handle(dev);
+    if (!h) return PE_ERR_LAUNCH;
     const LtPlan* p = get_plan(h, dev, M, N, K, lda, ldc, ldr, bias != nullptr, res != nullptr, workspace_bytes);
     if (!p) return PE_ERR_LAUNCH;
     if (bias && hipblasLtMatmulDescSetAttribute(p->op, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias)) !=

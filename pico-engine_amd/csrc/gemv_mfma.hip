@@ -44,6 +44,8 @@
 // every wave's partial row sums go to LDS and are added in wave order once the workgroup's
 // last tile is done (deterministic). Workgroups loop over tiles so that the activation planes
 // are built once per workgroup.
+#include <atomic>
+
 #include "pe_common.h"
 
 namespace pe {
@@ -589,23 +591,28 @@ extern "C" int pe_repack_mfma(int type, const void* blocks, void* out, int64_t n
 namespace {
 
 // Raises the kernel's dynamic LDS limit once per device, then launches min(tiles, resident
-// workgroups) workgroups (they loop over the tiles).
+// workgroups) workgroups (they loop over the tiles). The per-device limit is cached in an
+// atomic: threads that race on the first call each set the same attribute and store the same
+// value, so concurrent callers never read a torn or half-set entry.
 template <int T, bool SILU, bool NORM, bool EXP>
 int launch_mgemv(const MgArgs& a, size_t lds, hipStream_t s) {
-    static int configured[64] = {0};
+    static std::atomic<int> configured[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return PE_ERR_LAUNCH;
-    if (!configured[dev]) {
+    int limit = configured[dev].load(std::memory_order_acquire);
+    if (!limit) {
         int max_lds = 0;
         if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeSharedMemPerBlockOptin, dev) != hipSuccess ||
             max_lds <= 0)
             (void)hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
-        if (hipFuncSetAttribute((const void*)k_mgemv<T, SILU, NORM, EXP>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        if (max_lds <= 0 ||
+            hipFuncSetAttribute((const void*)k_mgemv<T, SILU, NORM, EXP>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 max_lds) != hipSuccess)
             return PE_ERR_LAUNCH;
-        configured[dev] = max_lds;
+        limit = max_lds;
+        configured[dev].store(limit, std::memory_order_release);
     }
-    if ((int64_t)lds > configured[dev]) return PE_ERR_SHAPE;
+    if ((int64_t)lds > limit) return PE_ERR_SHAPE;
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         return PE_ERR_LAUNCH;

@@ -97,6 +97,7 @@ _SIGNATURES = {
     "pe_flash_prefill": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _L, _F, _P, _L, _P]),
     "pe_flash_prefill_h16": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _L, _F, _P, _L, _P]),
     "pe_gemm_lt": (_I, [_P, _L, _P, _L, _L, _L, _P, _P, _L, _P, _L, _P, _L, _P]),
+    "pe_gemm_lt_init": (_I, []),
     "pe_mfma_bytes": (_L, [_I, _L, _L]),
     "pe_repack_mfma": (_I, [_I, _P, _P, _L, _L, _P]),
     "pe_mgemv": (_I, [_I, _P, _L, _L, _P, _P, _F, _P, _P, _I, _I, _P]),

@@ -102,7 +102,11 @@ class Engine:
                 quant["token_embd"] = K.RawTensor(self._upload(raw), t.ggml_type, shape)
                 continue
             if len(shape) == 2 and t.ggml_type in MATRIX_TYPES:
-                quant[t.name] = K.pack_weight(self._upload(raw), t.ggml_type, shape[0], shape[1])
+                # the LM head keeps the tiled copy only: the greedy launch and the normed plain
+                # GEMV both read it (the same lane groups, hence the same logits), so an MFMA
+                # layout copy (447 MB for a Q6_K 7B head) would never be read
+                mfma = False if t.name == "output.weight" else None
+                quant[t.name] = K.pack_weight(self._upload(raw), t.ggml_type, shape[0], shape[1], mfma=mfma)
                 continue
             if len(shape) == 1 and t.ggml_type in (GGML_F32, GGML_F16):
                 weights[t.name] = K.dequantize(t.ggml_type, self._upload(raw), t.n_elements)
@@ -112,7 +116,7 @@ class Engine:
             quant["output"] = quant["output.weight"]
         else:  # no output tensor: tied embeddings (the file's token_embd bytes as the LM head)
             e = quant["token_embd"]
-            quant["output"] = K.pack_weight(e.data, e.ggml_type, e.shape[0], e.shape[1])
+            quant["output"] = K.pack_weight(e.data, e.ggml_type, e.shape[0], e.shape[1], mfma=False)
         torch.cuda.synchronize(self.device)
         return weights, quant
 

@@ -879,7 +879,10 @@ GEMM_LT_WORKSPACE = 32 << 20
 
 
 def gemm_lt_workspace(device) -> torch.Tensor:
-    """Device workspace for gemm_lt (hipBLASLt), reusable by calls made in order on a stream."""
+    """Device workspace for gemm_lt (hipBLASLt), reusable by calls made in order on a stream.
+    Also creates the device's hipBLASLt handle now (pe_gemm_lt_init), outside any capture."""
+    with torch.cuda.device(torch.device(device)):
+        check(lib.pe_gemm_lt_init(), "pe_gemm_lt_init")
     return torch.empty(GEMM_LT_WORKSPACE, device=device, dtype=torch.uint8)
 
 

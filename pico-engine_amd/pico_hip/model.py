@@ -43,6 +43,18 @@ from . import kernels as K
 from .kernels import QWeight, RawTensor
 
 
+def clear_step_workspace_on_error(ws: torch.Tensor | None) -> int:
+    """The error word of a pe_decode_step workspace (bytes 64..67; 0: none); a non-zero word
+    zeroes the whole workspace (launch counter at bytes 0..3, error word, exchange pairs and
+    pick records)."""
+    if ws is None:
+        return 0
+    w = int(ws[64:68].view(torch.int32).item())
+    if w:
+        ws.zero_()
+    return w
+
+
 @dataclass
 class ModelConfig:
     vocab_size: int
@@ -114,7 +126,8 @@ class Transformer:
         # the matrix-core prefill's plain products (QKV + bias, o-proj and ffn_down + residual)
         # on hipBLASLt; off: every product on this library's MFMA GEMM (pe_gemm_f16)
         self.prefill_blaslt = True
-        self._lt_ws: torch.Tensor | None = None
+        # its workspace, and the device's hipBLASLt handle, made at load (outside any capture)
+        self._lt_ws: torch.Tensor | None = K.gemm_lt_workspace(self.device)
         self._f16: list[dict[str, torch.Tensor]] | None = None
         # greedy decode steps the persistent kernel covers can run as one launch per token
         # (pe_decode_step) instead of four launches per layer; off by default: ~2 % faster, but
@@ -232,13 +245,12 @@ class Transformer:
 
     def step_error(self) -> int:
         """pe_decode_step's error word (0: none; 1: a wait ran out; 2: a token or position out
-        of range), cleared by the read."""
-        if self._step_ws is None:
-            return 0
-        w = int(self._step_ws[64:68].view(torch.int32).item())
-        if w:
-            self._step_ws[64:68].zero_()
-        return w
+        of range). A non-zero word clears the whole workspace: the launch counter, the error
+        word and every exchange pair. Workgroups of a failed launch that started after its
+        counter was read may have published pairs under the next launch's tag, which the next
+        launch would otherwise take as ready; after the clear every pair carries tag 0 and the
+        next launch's tag is 1."""
+        return clear_step_workspace_on_error(self._step_ws)
 
     def _decode(self, token_ids, positions, cache, greedy=None):
         """One token. With a greedy state and a model pe_decode_step covers, the whole step is

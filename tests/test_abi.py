@@ -46,7 +46,7 @@ def test_nbytes_and_workspace(lib):
     assert lib.pe_nbytes_for(12, 896) == -3        # not a whole super-block
     assert lib.pe_nbytes_for(99, 32) == -2         # unknown type
     ws = lib.pe_decode_attn_workspace_bytes(14, 2, 64, 77)
-    assert ws == 256 + 2 * 2 * 7 * 68 * 4   # records: P.V[64], max, sum, 2 pad words
+    assert ws == 2 * 2 * 7 * 68 * 4   # records: P.V[64], max, sum, 2 pad words
     assert lib.pe_decode_attn_workspace_bytes(14, 3, 64, 77) == -3   # 14 % 3
     assert lib.pe_decode_attn_workspace_bytes(14, 2, 96, 77) == -3   # head_dim
     assert lib.pe_qgemv_argmax_workspace_bytes(151936) == 256 + 8 * 2048   # grid cap

@@ -414,8 +414,8 @@ def test_kv_write(K):
 
 # ---- fused QKV prologue -------------------------------------------------------------------
 
-# Shapes with more than 512 one-pair-per-group blocks (the 7B QKV, hidden 2048 with 64-lane
-# groups) run the looped form (qkv_loop.hip), in both activation layouts; one without biases.
+# The 0.5B shapes (one row pair per 32-lane group) and the 7B shape (hidden 3584, 128-lane
+# groups) and hidden 2048 (64-lane groups), in both activation layouts; one without biases.
 @pytest.mark.parametrize("types,hidden,nh,nkv,hd,ut,bias", [
     ((dq.Q5_0, dq.Q5_0, dq.Q8_0), 896, 14, 2, 64, False, True),
     ((dq.Q5_0, dq.Q5_0, dq.Q5_0), 896, 14, 2, 64, True, True),

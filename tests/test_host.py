@@ -217,3 +217,20 @@ def test_sampler_known_answers():
         assert seen <= set(case["allowed"]), case["what"]
         if case["all_seen"]:
             assert seen == set(case["allowed"]), case["what"]
+
+
+def test_step_workspace_cleared_after_a_failed_launch():
+    """A pe_decode_step workspace whose error word is set is zeroed whole: the launch counter,
+    the error word and exchange pairs that a late workgroup of the failed launch published under
+    the next launch's tag (counter + 1), which the next launch would otherwise accept."""
+    from pico_hip.model import clear_step_workspace_on_error
+    ws = torch.zeros(4096, dtype=torch.uint8)
+    words = ws.view(torch.int32)
+    pairs = ws.view(torch.int64)
+    words[0] = 41                               # launch counter after the failed launch
+    pairs[40:48] = (42 << 32) | 0x3F800000      # stale pairs tagged 42 (counter + 1), value 1.0
+    assert clear_step_workspace_on_error(ws) == 0 and int(words[0]) == 41   # no error: untouched
+    words[16] = 1                               # a wait ran out
+    assert clear_step_workspace_on_error(ws) == 1
+    assert int(ws.count_nonzero()) == 0
+    assert clear_step_workspace_on_error(None) == 0

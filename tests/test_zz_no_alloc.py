@@ -73,7 +73,7 @@ def test_noalloc_matches_workspace_entry_point_twice_shrinking(hd, n_head, n_kv)
 
 def test_noalloc_rejects_beyond_scratch():
     q = torch.zeros(14, 64, device="cuda")
-    big = 1 << 17   # 131072 positions: 256 + 2*2048*7*68*4 bytes > 4 MiB
+    big = 1 << 17   # 131072 positions: 2*2048*7*68*4 bytes > 4 MiB
     assert lib.pe_decode_attn_workspace_bytes(14, 2, 64, big) > (4 << 20)
     st = lib.pe_decode_attn_noalloc(_ptr(q), _ptr(q), _ptr(q), 14, 2, 64, big, None, 0, 1,
                                     0.125, 1, _ptr(q), 0, _stream())
