@@ -99,6 +99,16 @@ def kernel_launchers(eng, which: str, attn: tuple[int, int] = (45, 80)):
                 f"{h}->2x{cfg.ffn_dim}")
         fn = lambda w: K.qgemv_sum_norm_silu(x, parts, L0.ffn_norm_ut, w, cfg.eps, layout=XU | YU)
         io = 4 * (h * (3 + nkv) + cfg.ffn_dim)
+    elif which == "gate_up_fix":
+        # as the decode step runs it after attn_oproj_fix: x plus 2^-32 times the fixed-point
+        # o-projection accumulator, RMSNorm, [gate; up] pair, SiLU; the sum is stored
+        ws = (L0.w_gate_up,)
+        fix = K.fix_acc(h, eng.device)[0]
+        fix[:h] = (torch.randn(h, device=eng.device, dtype=torch.float64) * 0.1 * 2.0 ** 32).to(torch.int64)
+        name = (f"k_qgemv (Q5_0, x + 2^-32 o-proj acc, rmsnorm+SiLU pair) gate/up "
+                f"{h}->2x{cfg.ffn_dim}")
+        fn = lambda w: K.qgemv_fix_norm_silu(x, fix, L0.ffn_norm_ut, w, cfg.eps, layout=XU | YU)
+        io = 4 * (h * 3 + cfg.ffn_dim) + 8 * (h + 1)
     elif which == "gate_up_norm":
         # the decode step without attn_gproj (head_dim 128: the 7B): RMSNorm, [gate; up], SiLU
         ws = (L0.w_gate_up,)
@@ -143,6 +153,20 @@ def kernel_launchers(eng, which: str, attn: tuple[int, int] = (45, 80)):
         name = f"k_attn_gproj ({tn(ws[0])} o-proj, S={S}, {nh}/{nkv} heads) {nh * hd}->{nkv}x{h}"
         fn = lambda w: K.attn_gproj(q, kc, vc, w, S=S, layout=YU)
         io = 4 * (nh * hd + 2 * nkv * S * hd + nkv * h)
+    elif which == "attn_oproj":
+        # attention of every query head over S cached positions (config 0: 45, the mean
+        # context of a 13-token prompt and 64 decode steps) times its columns of Wo, added into
+        # the fixed-point accumulator (read and written once per row, n_head atomic adds)
+        ws = (L0.wo,)
+        S, cap = attn
+        q = torch.randn(nh, hd, device=eng.device)
+        kc = torch.randn(nkv, cap, hd, device=eng.device)
+        vc = torch.randn(nkv, cap, hd, device=eng.device)
+        pos = torch.tensor([S - 1], device=eng.device)
+        acc = K.fix_acc(h, eng.device)[0]
+        name = f"k_attn_oproj ({tn(ws[0])} o-proj, S={S}, {nh}/{nkv} heads) {nh * hd}->{h}"
+        fn = lambda w: K.attn_oproj_fix(q, kc, vc, w, pos, acc, layout=YU)
+        io = 4 * (nh * hd + 2 * nkv * S * hd) + 16 * (h + 1)
     elif which == "attn":
         # decode attention alone (head_dim 128: the 7B), S valid positions of the cache; its
         # K/V copies rotate instead of weights
@@ -174,7 +198,8 @@ def kernel_launchers(eng, which: str, attn: tuple[int, int] = (45, 80)):
 def decode_kernels(eng, capacity: int) -> list[tuple[str, int]]:
     """(kernel_launchers key, launches per decode token) for the kernels of the model's decode
     step with a cache of ``capacity`` positions: every per-layer launch and the LM head (the
-    embedding row and the greedy pick, a few us each, are left out)."""
+    embedding row, the greedy pick and the fixed-point accumulator fill, a few us each, are
+    left out)."""
     from pico_hip import kernels as K
     from pico_hip.dequant import GGML_Q4_K, GGML_Q6_K
     m, cfg = eng.model, eng.cfg
@@ -183,7 +208,12 @@ def decode_kernels(eng, capacity: int) -> list[tuple[str, int]]:
     gproj = (m.use_attn_gproj and L0.w_gate_up is not None and
              K.attn_gproj_supported(cfg.n_head, cfg.n_kv_head, cfg.head_dim, capacity, L0.wo))
     rows = [("qkv", n)]
-    rows += [("attn_gproj", n), ("gate_up", n)] if gproj else [("attn", n), ("oproj", n), ("gate_up_norm", n)]
+    if m.attn_oproj_ok(capacity):
+        rows += [("attn_oproj", n), ("gate_up_fix", n)]
+    elif gproj:
+        rows += [("attn_gproj", n), ("gate_up", n)]
+    else:
+        rows += [("attn", n), ("oproj", n), ("gate_up_norm", n)]
     for key, t in (("down_q6k", GGML_Q6_K), ("down_q4k", GGML_Q4_K)):
         c = sum(1 for Lr in m.layers if Lr.w_down.ggml_type == t)
         if c:
@@ -579,7 +609,7 @@ def main() -> None:
     ap.add_argument("--kernel", default=None,
                     help="kernel for the roofline object (default: the largest time per token), or the "
                          "kernel --kernel-only times: gate_up, gate_up_norm, lm_head, down_q6k, down_q4k, "
-                         "qkv, attn_gproj, attn, oproj")
+                         "qkv, attn_oproj, gate_up_fix, attn_gproj, attn, oproj")
     ap.add_argument("--no-extra-configs", action="store_true",
                     help="leave the config 3 and config 4 objects off the config-0 line")
     ap.add_argument("--kernel-iters", type=int, default=400)

@@ -343,6 +343,65 @@ int pe_qgemv_sum_rmsnorm_silu(int ggml_type, const void* w_tiled, int64_t ffn, i
                               const float* norm_w, float eps, float* act, float* x_sum,
                               int layout, pe_stream_t stream);
 
+/* "O-projection layout" of a Q5_0 / Q8_0 (n x k) matrix for the integer matrix cores
+ * (k % 64 == 0): one block per (64-column head, 16-row tile), head-major, zero rows padding
+ * the last tile. Q5_0 blocks (704 bytes): for each of 64 lanes (row lane & 15, slot g =
+ * lane >> 4) the qs words g of the head's 2 units, then per lane 16 fifth bits (nibble 2u + c,
+ * bit i: element 16c + 4g + i of unit u), then 32 fp16 d's of (row i & 15, unit i >> 4). Q8_0
+ * blocks (1088 bytes): per lane the 16 code bytes (elements 4g..4g+3 and 16+4g..16+4g+3 of each
+ * unit), then the d's as for Q5_0. The same bytes as the GGUF blocks, rearranged;
+ * pe_oproj_layout_bytes returns -1 for other types or shapes. Built once at load, like
+ * pe_repack; the reference's unpack_q5_0 / unpack_q8_0 (dequant.py:79-105) are its GEMVs'
+ * layouts. */
+int64_t pe_oproj_layout_bytes(int ggml_type, int64_t n, int64_t k);
+int pe_repack_oproj(int ggml_type, const void* blocks, void* w_oproj, int64_t n, int64_t k,
+                    pe_stream_t stream);
+
+/* Decode attention of each query head fused with its share of the o-projection, one launch,
+ * no communication between workgroups. For query head h of kv head j = h / (n_head / n_kv),
+ * with S = *pos + 1 cached positions (the token's own k / v row already written at *pos):
+ *   a_h = softmax(q_h . K_j[0..S) * scale) V_j[0..S), rounded to fp16;
+ *   acc[r] += 2^32 sum_d Wo[r][h*64 + d] a_h[d]   (r < hidden, rounded to an integer),
+ * in 64-bit two's-complement fixed point, over the n_head heads in any order (integer sums are
+ * exact, so the result is deterministic); a value that is not finite or reaches 2^30 in
+ * magnitude adds 1 to acc[hidden] instead (so does every row for a position outside
+ * [0, capacity)). acc holds hidden + 1 int64 and must be zero (or hold the sum to add to)
+ * before the call; pe_qgemv_fix_rmsnorm_silu adds it to x. The products run on the integer
+ * matrix cores over exact int8 planes of the fp16-rounded attention output, Wo in the
+ * o-projection layout (pe_repack_oproj). layout: PE_LAYOUT_Y_UT stores acc in the
+ * unit-transposed layout of x. Limits (pe_attn_oproj_fix_supported): head_dim 64, capacity
+ * <= 128, hidden % 32 == 0.
+ * Replaces decode_attn (model.py:211, kernels.py:90-158) and the o-projection addmm
+ * (model.py:213); its residual add is the consumer's. */
+typedef struct pe_attn_oproj_args {
+    const float* q;          /* (n_head, 64) after RoPE */
+    const float* k_cache;    /* (n_kv, capacity, 64) */
+    const float* v_cache;
+    int64_t capacity;
+    const int64_t* pos;      /* device scalar: the token's position */
+    int n_head, n_kv, head_dim;
+    float scale;             /* softmax scale (1/sqrt(head_dim)) */
+    int type_o;              /* PE_TYPE_Q5_0 or PE_TYPE_Q8_0 */
+    const void* w_o;         /* o-projection layout of Wo (hidden x n_head*64) */
+    int64_t hidden;
+    int64_t* acc;            /* (hidden + 1) fixed-point accumulator */
+    int layout;
+} pe_attn_oproj_args;
+int pe_attn_oproj_fix_supported(int type_o, int64_t hidden, int n_head, int n_kv, int head_dim,
+                                int64_t capacity);
+int pe_attn_oproj_fix(const pe_attn_oproj_args* args, pe_stream_t stream);
+
+/* pe_qgemv_sum_rmsnorm_silu whose summed activation is x + 2^-32 fix: fix holds k 64-bit
+ * two's-complement fixed-point values (the layout of x) and, at index k, a count of values
+ * that its producer could not represent (non-zero: every summed element is NaN). Each element
+ * is x[i] + (float)(2^-32 fix[i]), with one rounding for the conversion and one for the add;
+ * x_sum (NULL: not stored) receives that sum. k <= 6144; fix 16-byte aligned. This is the
+ * consumer of pe_attn_oproj_fix's o-projection accumulator: the residual add of the o-projection
+ * (model.py:213) fused with rmsnorm + gate/up + silu_mul (model.py:216-224). */
+int pe_qgemv_fix_rmsnorm_silu(int ggml_type, const void* w_tiled, int64_t ffn, int64_t k,
+                              const float* x, const int64_t* fix, const float* norm_w, float eps,
+                              float* act, float* x_sum, int layout, pe_stream_t stream);
+
 /* Decode attention of each kv group fused with the group's share of the o-projection, one
  * launch, no communication between workgroups. For kv head j with query heads
  * h = j*G .. j*G+G-1 (G = n_head / n_kv):

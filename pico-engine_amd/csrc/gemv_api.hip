@@ -96,6 +96,30 @@ extern "C" int pe_qgemv_sum_rmsnorm_silu(int type, const void* w, int64_t ffn, i
     return dispatch_gemv(type, a, true, kModeSiluSum, (hipStream_t)stream);
 }
 
+extern "C" int pe_qgemv_fix_rmsnorm_silu(int type, const void* w, int64_t ffn, int64_t k,
+                                         const float* x, const int64_t* fix, const float* norm_w,
+                                         float eps, float* act, float* x_sum, int layout,
+                                         pe_stream_t stream) {
+    int st = check_weight(type, w, 2 * ffn, k);
+    if (st) return st;
+    if ((st = check_layout(layout, ffn))) return st;
+    // the activation is issued with x and staged in LDS (k <= 6144: at most six float4 loads
+    // per thread, the act-first prologue)
+    if ((layout & PE_LAYOUT_X_UT) && k % 32) return PE_ERR_SHAPE;
+    if (k > 6144) return PE_ERR_SHAPE;
+    if (!x || !fix || !act || !norm_w) return PE_ERR_NULL;
+    if (!aligned(x, 16) || !aligned(fix, 16) || !aligned(norm_w, 16) || !aligned(act, 4) ||
+        !aligned(x_sum, 16))
+        return PE_ERR_ALIGN;
+    GemvArgs a{make_tiled(w, 2 * ffn, k / block_elems(type)),
+               ffn, k, x, norm_w, eps, nullptr, nullptr, act, ffn, layout};
+    a.parts = x;  // unused by this mode
+    a.n_parts = 0;
+    a.x_sum = x_sum;
+    a.fix = fix;
+    return dispatch_gemv(type, a, true, kModeSiluFix, (hipStream_t)stream);
+}
+
 extern "C" int pe_qgemm(int type, const void* w, int64_t n_rows, int64_t k, const float* x,
                         int64_t x_stride, int64_t m, const float* bias, const float* residual,
                         int64_t res_stride, float* y, int64_t y_stride, pe_stream_t stream) {

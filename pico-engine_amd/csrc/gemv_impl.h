@@ -18,9 +18,14 @@ namespace pe {
 // most kEarlyParts of them, loaded with x; kModeSiluSumMany: the same for more parts, loaded
 // after the weights. Two modes, so that neither has a load under a run-time branch between the
 // weight loads and the staging (which would make the staging wait for the weights).
-enum { kModePlain = 0, kModeSilu = 1, kModeArgmax = 2, kModeSiluSum = 3, kModeSiluSumMany = 4 };
-// How a staging routine adds parts: not at all, from the early loads, or loading them itself.
-enum { kSumNone = 0, kSumEarly = 1, kSumLate = 2 };
+// kModeSiluFix: kModeSilu whose staged activation is x + 2^-32 f, f a vector of 64-bit
+// fixed-point sums (GemvArgs::fix, the attention block's o-projection accumulator), loaded
+// with x.
+enum { kModePlain = 0, kModeSilu = 1, kModeArgmax = 2, kModeSiluSum = 3, kModeSiluSumMany = 4,
+       kModeSiluFix = 5 };
+// How a staging routine adds parts: not at all, from the early loads, loading them itself, or
+// one fixed-point vector from the early loads.
+enum { kSumNone = 0, kSumEarly = 1, kSumLate = 2, kSumFix = 3 };
 
 struct GemvArgs {
     Tiled w;
@@ -45,7 +50,18 @@ struct GemvArgs {
     const float* parts;
     int n_parts;
     float* x_sum;
+    // kModeSiluFix: k int64 fixed-point values (2^-32 units, the layout of x) and, at index k, a
+    // count of values that could not be represented (non-zero: the sum is NaN)
+    const int64_t* fix;
 };
+
+// 2^-32 v for a 64-bit two's-complement fixed-point v (lo, hi words), rounded once to fp32:
+// hi 2^32 + lo is exact in fp64 below 2^53 in magnitude, the power-of-two scaling is exact,
+// and the cast to fp32 is the only rounding.
+PE_DEV float fix_to_float(uint32_t lo, uint32_t hi) {
+    const double d = __builtin_fma((double)(int32_t)hi, 4294967296.0, (double)lo);
+    return (float)(d * 2.3283064365386962890625e-10);
+}
 
 constexpr int kMaxParts = 16;
 
@@ -391,6 +407,8 @@ struct ActLoads {
     float4 x[M4];
     float4 w[M4];
     float4 p[kEarlyParts][M4];  // summed-activation mode only
+    int4 f[2][M4];              // fixed-point mode: the four 64-bit sums of x's float4
+    uint2 poison;               // fixed-point mode: the unrepresentable-value count
 };
 
 // Issue the float4 loads of x (and the RMSNorm weight) that this thread stages. Indices past
@@ -400,6 +418,7 @@ template <int NT, bool NORM, int M4, int SUM = kSumNone>
 PE_DEV void issue_activation(const GemvArgs& a, int units, ActLoads<M4>& L) {
     if (a.k > kStageMaxK || units * 8 > NT * M4) return;
     const int n4 = units * 8;
+    if constexpr (SUM == kSumFix) L.poison = reinterpret_cast<const uint2*>(a.fix)[a.k];
 #pragma unroll
     for (int m = 0; m < M4; ++m) {
         const int i = (int)threadIdx.x + NT * m;
@@ -407,6 +426,10 @@ PE_DEV void issue_activation(const GemvArgs& a, int units, ActLoads<M4>& L) {
             const int ic = i < n4 ? i : n4 - 1;
             L.x[m] = reinterpret_cast<const float4*>(a.x)[ic];
             if constexpr (NORM) L.w[m] = reinterpret_cast<const float4*>(a.norm_w)[ic];
+            if constexpr (SUM == kSumFix) {
+                L.f[0][m] = reinterpret_cast<const int4*>(a.fix)[2 * ic];
+                L.f[1][m] = reinterpret_cast<const int4*>(a.fix)[2 * ic + 1];
+            }
             if constexpr (SUM == kSumEarly) {
                 // slots past n_parts re-read the last part (never added; parts points at x when
                 // there is none): no branch around a load, and no slot whose address the
@@ -485,7 +508,16 @@ PE_DEV float finish_activation(const GemvArgs& a, int glane, int units,
             const int u = ut ? i % units : i >> 3;
             const int j = ut ? i / units : i & 7;
             float4 v = L.x[m];
-            if constexpr (SUM != kSumNone) {
+            if constexpr (SUM == kSumFix) {
+                // x + 2^-32 f, one fp32 addition per element; NaN if any sum was unrepresentable
+                const int4 f0 = L.f[0][m], f1 = L.f[1][m];
+                v.x += fix_to_float((uint32_t)f0.x, (uint32_t)f0.y);
+                v.y += fix_to_float((uint32_t)f0.z, (uint32_t)f0.w);
+                v.z += fix_to_float((uint32_t)f1.x, (uint32_t)f1.y);
+                v.w += fix_to_float((uint32_t)f1.z, (uint32_t)f1.w);
+                if (L.poison.x | L.poison.y) v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+                if (a.x_sum && blockIdx.x == 0) reinterpret_cast<float4*>(a.x_sum)[i] = v;
+            } else if constexpr (SUM != kSumNone) {
                 // x + parts[0] + parts[1] + ... in that order; late parts are all loaded before
                 // the first add (no chain of dependent round trips)
                 float4 pv[kMaxParts];
@@ -632,7 +664,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
     constexpr int NT = kGemvThreads;
     constexpr int G = NT / GS;
     constexpr int CH = G * TPG;
-    constexpr bool kSilu = MODE == kModeSilu || MODE == kModeSiluSum || MODE == kModeSiluSumMany;
+    constexpr bool kSilu = MODE == kModeSilu || MODE == kModeSiluSum || MODE == kModeSiluSumMany ||
+                           MODE == kModeSiluFix;
     constexpr int R = kSilu ? 2 : 1;
     constexpr bool kEpi = !kSilu;
     // the LM head (the argmax launch, and the normed plain GEMV that serves as the LM head
@@ -664,7 +697,8 @@ __global__ __launch_bounds__(kGemvThreads) void k_qgemv(GemvArgs a) {
     // Longer activations would hold too many registers across the weight loads, so there the
     // weights go first and the activation streams through LDS after them.
     constexpr bool kActFirst = act_loads<NT, GS, UPL>() <= 6;
-    constexpr int kSum = MODE == kModeSiluSum ? kSumEarly : MODE == kModeSiluSumMany ? kSumLate : kSumNone;
+    constexpr int kSum = MODE == kModeSiluSum ? kSumEarly : MODE == kModeSiluSumMany ? kSumLate
+                         : MODE == kModeSiluFix ? kSumFix : kSumNone;
     float xr[UPL][32];
     UnitSums xs[UPL];
     float rstd;
@@ -1014,6 +1048,10 @@ int gemv_dispatch(const GemvArgs& a, bool norm, int mode, hipStream_t s) {
     if (mode == kModeSilu)
         return norm ? launch_qgemv_mode<T, true, kModeSilu>(a, s)
                     : launch_qgemv_mode<T, false, kModeSilu>(a, s);
+    if (mode == kModeSiluFix) {
+        if (!norm || a.k > kStageMaxK) return PE_ERR_SHAPE;
+        return launch_qgemv_mode<T, true, kModeSiluFix>(a, s);
+    }
     if (mode == kModeSiluSum) {
         if (!norm || a.k > kStageMaxK) return PE_ERR_SHAPE;
         return a.n_parts <= kEarlyParts ? launch_qgemv_mode<T, true, kModeSiluSum>(a, s)

@@ -49,6 +49,16 @@ class QkvArgs(ctypes.Structure):
     ]
 
 
+class AttnOprojArgs(ctypes.Structure):
+    """Mirror of pe_attn_oproj_args (include/pico_hip.h)."""
+
+    _fields_ = [
+        ("q", _P), ("k_cache", _P), ("v_cache", _P), ("capacity", _L), ("pos", _P),
+        ("n_head", _I), ("n_kv", _I), ("head_dim", _I), ("scale", _F),
+        ("type_o", _I), ("w_o", _P), ("hidden", _L), ("acc", _P), ("layout", _I),
+    ]
+
+
 class StepLayer(ctypes.Structure):
     """Mirror of pe_step_layer (include/pico_hip.h)."""
 
@@ -127,6 +137,11 @@ _SIGNATURES = {
     "pe_decode_step_supported": (_I, [_I, _I, _I, _I, _I, _I, _L, _L]),
     "pe_decode_step_workspace_bytes": (_L, [_I, _I, _I, _I, _I, _I]),
     "pe_decode_step": (_I, [ctypes.POINTER(StepArgs), _P]),
+    "pe_oproj_layout_bytes": (_L, [_I, _L, _L]),
+    "pe_repack_oproj": (_I, [_I, _P, _P, _L, _L, _P]),
+    "pe_attn_oproj_fix_supported": (_I, [_I, _L, _I, _I, _I, _L]),
+    "pe_attn_oproj_fix": (_I, [ctypes.POINTER(AttnOprojArgs), _P]),
+    "pe_qgemv_fix_rmsnorm_silu": (_I, [_I, _P, _L, _L, _P, _P, _P, _F, _P, _P, _I, _P]),
 }
 
 # Every symbol include/pico_hip.h declares (checked by tests/test_abi.py).

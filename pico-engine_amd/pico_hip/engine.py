@@ -106,7 +106,11 @@ class Engine:
                 # GEMV both read it (the same lane groups, hence the same logits), so an MFMA
                 # layout copy (447 MB for a Q6_K 7B head) would never be read
                 mfma = False if t.name == "output.weight" else None
-                quant[t.name] = K.pack_weight(self._upload(raw), t.ggml_type, shape[0], shape[1], mfma=mfma)
+                # Wo also in the o-projection layout of the per-head attention + o-projection
+                # launch (Q5_0 / Q8_0: the 0.5B family; 0.55 MB a layer at config 0)
+                oproj = t.name.endswith(".attn_output.weight")
+                quant[t.name] = K.pack_weight(self._upload(raw), t.ggml_type, shape[0], shape[1],
+                                              mfma=mfma, oproj=oproj)
                 continue
             if len(shape) == 1 and t.ggml_type in (GGML_F32, GGML_F16):
                 weights[t.name] = K.dequantize(t.ggml_type, self._upload(raw), t.n_elements)

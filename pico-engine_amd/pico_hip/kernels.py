@@ -23,7 +23,7 @@ import os
 
 import torch
 
-from ._lib import (LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT, QkvArgs, StepArgs, StepLayer, check,
+from ._lib import (LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT, AttnOprojArgs, QkvArgs, StepArgs, StepLayer, check,
                    lib)
 from .dequant import (BLOCK_SIZE, GGML_Q4_K, GGML_Q5_0, GGML_Q6_K, GGML_Q8_0, MATRIX_TYPES,
                       QUANT_TYPES, TYPE_NAMES, nbytes_for)
@@ -83,6 +83,9 @@ class QWeight:
     # the same matrix in the MFMA layout (pe_repack_mfma) when the decode GEMVs run it on the
     # integer matrix cores (large Q4_K / Q6_K matrices, see mfma_eligible)
     mfma: torch.Tensor | None = None
+    # the same matrix in the o-projection layout (pe_repack_oproj: Q5_0 / Q8_0 Wo) for the
+    # per-head attention + o-projection launch (attn_oproj_fix)
+    oproj: torch.Tensor | None = None
 
     @property
     def shape(self) -> tuple[int, int]:
@@ -93,9 +96,10 @@ class QWeight:
         return self.data.numel()
 
     def copy(self) -> "QWeight":
-        """A distinct device copy (both layouts)."""
+        """A distinct device copy (every layout it holds)."""
         return QWeight(self.data.clone(), self.ggml_type, self.n, self.k,
-                       None if self.mfma is None else self.mfma.clone())
+                       None if self.mfma is None else self.mfma.clone(),
+                       None if self.oproj is None else self.oproj.clone())
 
     def __repr__(self) -> str:
         return f"QWeight({TYPE_NAMES[self.ggml_type]}, n={self.n}, k={self.k})"
@@ -154,9 +158,17 @@ def repack_mfma(blocks: torch.Tensor, ggml_type: int, n: int, k: int) -> torch.T
     return out
 
 
-def pack_weight(blocks: torch.Tensor, ggml_type: int, n: int, k: int, mfma: bool | None = None) -> QWeight:
+def oproj_eligible(ggml_type: int, n: int, k: int) -> bool:
+    """Whether an (n x k) matrix has an o-projection layout (pe_repack_oproj: Q5_0 / Q8_0,
+    k % 64 == 0)."""
+    return ggml_type in (GGML_Q5_0, GGML_Q8_0) and k % 64 == 0 and n > 0
+
+
+def pack_weight(blocks: torch.Tensor, ggml_type: int, n: int, k: int, mfma: bool | None = None,
+                oproj: bool = False) -> QWeight:
     """Raw GGUF blocks of an (n x k) tensor (device uint8) -> tiled QWeight, with the MFMA
-    layout copy as well when ``mfma`` (default: when mfma_eligible)."""
+    layout copy as well when ``mfma`` (default: when mfma_eligible), and the o-projection
+    layout copy when ``oproj`` and the matrix has one (oproj_eligible)."""
     dev = _on_gpu(blocks)
     if ggml_type not in MATRIX_TYPES:
         raise ValueError(f"no GEMV kernel for {TYPE_NAMES.get(ggml_type, ggml_type)}")
@@ -167,7 +179,23 @@ def pack_weight(blocks: torch.Tensor, ggml_type: int, n: int, k: int, mfma: bool
     check(lib.pe_repack(ggml_type, _ptr(blocks), _ptr(data), n, k, _stream(dev)), "pe_repack")
     if mfma is None:
         mfma = mfma_eligible(ggml_type, n, k)
-    return QWeight(data, ggml_type, n, k, repack_mfma(blocks, ggml_type, n, k) if mfma else None)
+    return QWeight(data, ggml_type, n, k, repack_mfma(blocks, ggml_type, n, k) if mfma else None,
+                   repack_oproj(blocks, ggml_type, n, k) if oproj and oproj_eligible(ggml_type, n, k) else None)
+
+
+def repack_oproj(blocks: torch.Tensor, ggml_type: int, n: int, k: int) -> torch.Tensor:
+    """Raw GGUF blocks of an (n x k) Q5_0 / Q8_0 matrix -> its o-projection layout (device
+    uint8): per 64-column head and 16-row tile, the operand layout of attn_oproj_fix's integer
+    matrix-core products."""
+    dev = _on_gpu(blocks)
+    size = lib.pe_oproj_layout_bytes(ggml_type, n, k)
+    if size < 0:
+        raise ValueError(f"no o-projection layout for a {n}x{k} {TYPE_NAMES.get(ggml_type, ggml_type)} matrix")
+    if blocks.numel() != nbytes_for(ggml_type, n * k):
+        raise ValueError(f"{blocks.numel()} bytes for a {n}x{k} {TYPE_NAMES[ggml_type]} tensor")
+    out = torch.empty(size, device=dev, dtype=torch.uint8)
+    check(lib.pe_repack_oproj(ggml_type, _ptr(blocks), _ptr(out), n, k, _stream(dev)), "pe_repack_oproj")
+    return out
 
 
 def _use_mfma(w: QWeight) -> bool:
@@ -774,6 +802,74 @@ def qgemv_sum_norm_silu(x: torch.Tensor, parts: torch.Tensor, weight: torch.Tens
     return out, x_sum
 
 
+def attn_oproj_supported(n_head: int, n_kv: int, hd: int, capacity: int, wo: QWeight) -> bool:
+    """Whether attn_oproj_fix covers these shapes (head_dim 64, caches of <= 128 positions,
+    a Q5_0 / Q8_0 Wo with its o-projection layout copy)."""
+    return (wo.oproj is not None and
+            lib.pe_attn_oproj_fix_supported(wo.ggml_type, wo.n, n_head, n_kv, hd, capacity) == 0)
+
+
+def fix_acc(hidden: int, device, layers: int = 1) -> torch.Tensor:
+    """Zeroed fixed-point accumulators for attn_oproj_fix: (layers, hidden + 2) int64 (hidden
+    sums, the unrepresentable-value count, padding to 16 bytes)."""
+    return torch.zeros(layers, hidden + 2, device=device, dtype=torch.int64)
+
+
+def attn_oproj_fix(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, wo: QWeight,
+                   pos: torch.Tensor, acc: torch.Tensor, scale: float | None = None,
+                   layout: int = LAYOUT_NATURAL) -> torch.Tensor:
+    """Decode attention of every query head over cache positions 0..pos (the token's own row
+    already written at pos), output rounded to fp16, times the head's columns of Wo, added
+    into ``acc`` (hidden + 1 int64, 2^-32 fixed point; acc[hidden] counts unrepresentable
+    values) by pe_attn_oproj_fix. Wo needs its o-projection layout (QWeight.oproj). Returns
+    acc. layout: LAYOUT_Y_UT stores acc in the unit-transposed layout of x."""
+    dev = _on_gpu(q, k_cache, v_cache, pos, acc, wo.data)
+    if wo.oproj is None:
+        raise ValueError(f"{wo} has no o-projection layout copy")
+    n_head, hd = q.shape[-2], q.shape[-1]
+    n_kv, capacity = k_cache.shape[0], k_cache.shape[1]
+    q = _f32c(q.reshape(n_head, hd))
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("KV caches must be contiguous (n_kv, capacity, hd) buffers")
+    if k_cache.shape != (n_kv, capacity, hd) or v_cache.shape != k_cache.shape:
+        raise ValueError(f"KV caches of shape {tuple(k_cache.shape)}, {tuple(v_cache.shape)} for head_dim {hd}")
+    if wo.k != n_head * hd:
+        raise ValueError(f"{wo} has {wo.k} columns for {n_head} heads of {hd}")
+    if pos.dtype != torch.int64:
+        raise ValueError("pos must be an int64 device tensor")
+    if acc.dtype != torch.int64 or acc.numel() < wo.n + 1 or not acc.is_contiguous():
+        raise ValueError(f"acc must be a contiguous int64 tensor of at least {wo.n + 1} elements")
+    a = AttnOprojArgs(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), capacity, pos.data_ptr(),
+                      n_head, n_kv, hd, float(hd ** -0.5 if scale is None else scale),
+                      wo.ggml_type, wo.oproj.data_ptr(), wo.n, acc.data_ptr(), layout)
+    check(lib.pe_attn_oproj_fix(ctypes.byref(a), _stream(dev)), "pe_attn_oproj_fix")
+    return acc
+
+
+def qgemv_fix_norm_silu(x: torch.Tensor, fix: torch.Tensor, weight: torch.Tensor, w: QWeight,
+                        eps: float, out: torch.Tensor | None = None,
+                        x_sum: torch.Tensor | None = None,
+                        layout: int = LAYOUT_NATURAL) -> tuple[torch.Tensor, torch.Tensor]:
+    """(silu(g) * u, x_sum) with x_sum = x + 2^-32 fix (fix: attn_oproj_fix's accumulator,
+    the layout of x) and [g; u] = W (rmsnorm(x_sum) * weight) (pe_qgemv_fix_rmsnorm_silu)."""
+    dev = _on_gpu(x, fix, weight, w.data)
+    if w.n % 2:
+        raise ValueError("gate/up weight needs an even number of rows")
+    ffn = w.n // 2
+    x = _f32c(x.reshape(-1))
+    nw = _f32c(weight.reshape(-1))
+    if fix.dtype != torch.int64 or fix.numel() < w.k + 1 or not fix.is_contiguous():
+        raise ValueError(f"fix must be a contiguous int64 tensor of at least {w.k + 1} elements")
+    if out is None:
+        out = torch.empty(ffn, device=dev, dtype=torch.float32)
+    if x_sum is None:
+        x_sum = torch.empty_like(x)
+    check(lib.pe_qgemv_fix_rmsnorm_silu(w.ggml_type, _ptr(w.data), ffn, w.k, _ptr(x), _ptr(fix), _ptr(nw),
+                                        float(eps), _ptr(out), _ptr(x_sum), layout, _stream(dev)),
+          "pe_qgemv_fix_rmsnorm_silu")
+    return out, x_sum
+
+
 # ---- prefill (M >= 1) --------------------------------------------------------------------
 
 def qgemm(x: torch.Tensor, w: QWeight, bias: torch.Tensor | None = None,
@@ -929,7 +1025,8 @@ __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "
            "q8_0_gemv", "q5_0_gemv", "q5_0_gemv_norm", "q6_k_gemv", "q4_k_gemv", "qgemv_norm",
            "qgemv_norm_silu", "qkv_rmsnorm_rope", "qgemv_sum_norm_silu", "qgemm", "kv_write", "prefill_attn",
            "gemm_lt", "gemm_lt_workspace", "mgemv", "repack_mfma", "mfma_eligible", "MFMA_MIN_WEIGHTS",
-           "attn_gproj", "attn_gproj_supported", "qgemv_norm_argmax", "dequantize_weight_f16",
+           "attn_gproj", "attn_gproj_supported", "attn_oproj_fix", "attn_oproj_supported", "fix_acc",
+           "repack_oproj", "oproj_eligible", "qgemv_fix_norm_silu", "qgemv_norm_argmax", "dequantize_weight_f16",
            "DecodeStep", "decode_step_supported", "decode_step_workspace",
            "gemm_f16", "gemm_f16_silu", "interleave_gate_up_f16", "flash_prefill",
            "BLOCK_SIZE"]

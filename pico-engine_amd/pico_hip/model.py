@@ -10,15 +10,21 @@ family) is one launch, pe_decode_step. Otherwise decode (one token) runs four la
 layer plus the embedding row and the LM head:
 
   embed_gather                              model.py:152 (Q8_0 row, bit-exact)
+  fill of the fixed-point accumulators (once per token, every layer)
   per layer:
     qkv_rmsnorm_rope   (norm+QKV+bias+RoPE+cache write)   model.py:175-193
-    attn_gproj         (GQA attention per kv group, fp16-  model.py:211-213
-                        rounded, times that group's
-                        columns of Wo: one part per group)
-    qgemv_sum_norm_silu (x + parts, norm, gate/up, SiLU*up) model.py:213-224
+    attn_oproj_fix     (GQA attention per query head,     model.py:211-213
+                        fp16-rounded, times that head's
+                        columns of Wo, added in 64-bit
+                        fixed point into the accumulator)
+    qgemv_fix_norm_silu (x + 2^-32 acc, norm, gate/up,    model.py:213-224
+                        SiLU*up)
     qgemv + residual   (ffn_down)                         model.py:225-234
   qgemv_norm(_argmax)  (final norm + LM head [+ greedy])  model.py:159-164
 
+attn_oproj_fix covers head_dim 64, caches of <= 128 positions and a Q5_0 / Q8_0 Wo (the 0.5B
+family); other formats at those sizes run attn_gproj (attention per kv group times the
+group's columns of Wo, one fp32 part per group) and qgemv_sum_norm_silu (x + parts).
 Caches of 513..4096 positions (head_dim 64) run attn_split_gproj instead of attn_gproj: the
 split-KV attention, then one launch that merges each kv group's chunk records and multiplies
 them by the group's Wo columns (the parts the gate/up GEMV adds). Other shapes (head_dim 128,
@@ -109,6 +115,12 @@ class Transformer:
         self.layers = [self._layer_weights(i) for i in range(cfg.n_layers)]
         self.output_norm_ut = K.to_ut(self.w["output_norm.weight"])
         self._ws: dict[int, torch.Tensor] = {}
+        # attention of each query head fused with its share of the o-projection, added into a
+        # fixed-point accumulator that the gate/up GEMV adds to x (attn_oproj_fix), where the
+        # model and cache qualify (attn_oproj_supported: a Q5_0 / Q8_0 Wo, head_dim 64, caches
+        # of <= 128 positions); else attn_gproj
+        self.use_attn_oproj = True
+        self._acc: torch.Tensor | None = None
         # attention of each kv group fused with its share of the o-projection (attn_gproj),
         # the shares added by the gate/up GEMV: four launches per layer instead of five
         self.use_attn_gproj = True
@@ -252,6 +264,17 @@ class Transformer:
         next launch's tag is 1."""
         return clear_step_workspace_on_error(self._step_ws)
 
+    def attn_oproj_ok(self, capacity: int) -> bool:
+        """Whether decode with a cache of ``capacity`` positions runs attn_oproj_fix: every
+        layer's Wo has its o-projection layout, the shapes and capacity are covered, and
+        [gate; up] is one tensor."""
+        if not self.use_attn_oproj:
+            return False
+        c = self.cfg
+        return all(L.w_gate_up is not None and
+                   K.attn_oproj_supported(c.n_head, c.n_kv_head, c.head_dim, capacity, L.wo)
+                   for L in self.layers)
+
     def _decode(self, token_ids, positions, cache, greedy=None):
         """One token. With a greedy state and a model pe_decode_step covers, the whole step is
         one launch that reads the token and position from the state. Otherwise four launches
@@ -271,8 +294,22 @@ class Transformer:
         if pos.dtype != torch.int64:
             pos = pos.to(torch.int64)
         capacity = cache[0][0].shape[1]
-        ws = self.attn_workspace(capacity)
         x = K.embed_gather(self.embed, token_ids, layout=YU).reshape(-1)
+        if self.attn_oproj_ok(capacity):
+            if self._acc is None:
+                self._acc = K.fix_acc(cfg.hidden, self.device, cfg.n_layers)
+            acc = self._acc
+            acc.zero_()   # a fill kernel (graph-capturable), once per token for every layer
+            for i, L in enumerate(self.layers):
+                k_buf, v_buf = cache[i]
+                q = K.qkv_rmsnorm_rope(x, L.attn_norm_ut, cfg.eps, L.wq, L.wk, L.wv, L.bq, L.bk, L.bv,
+                                       self.cos, self.sin, pos, k_buf, v_buf, cfg.n_head, layout=XU)
+                K.attn_oproj_fix(q, k_buf, v_buf, L.wo, pos, acc[i], layout=YU)
+                act, x = K.qgemv_fix_norm_silu(x, acc[i], L.ffn_norm_ut, L.w_gate_up, cfg.eps,
+                                               layout=XU | YU)
+                x = K.qgemv(act, L.w_down, residual=x, layout=XU | YU)
+            return self._lm_head(x, self.output_norm_ut, greedy, XU)
+        ws = self.attn_workspace(capacity)
         for i, L in enumerate(self.layers):
             k_buf, v_buf = cache[i]
             q = K.qkv_rmsnorm_rope(x, L.attn_norm_ut, cfg.eps, L.wq, L.wk, L.wv, L.bq, L.bk, L.bv,

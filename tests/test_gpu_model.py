@@ -139,9 +139,10 @@ def test_mid_cache_decode_split_gproj(tiny):
 
 
 PATHS = {  # model flags of each path of the decode step
-    "three_launch": dict(use_attn_gproj=False, use_step_kernel=False),
-    "attn_gproj": dict(use_attn_gproj=True, use_step_kernel=False),
-    "step_kernel": dict(use_step_kernel=True),
+    "three_launch": dict(use_attn_oproj=False, use_attn_gproj=False, use_step_kernel=False),
+    "attn_gproj": dict(use_attn_oproj=False, use_attn_gproj=True, use_step_kernel=False),
+    "attn_oproj": dict(use_attn_oproj=True, use_step_kernel=False),
+    "step_kernel": dict(use_attn_oproj=False, use_step_kernel=True),
 }
 
 
@@ -153,10 +154,10 @@ def _set_path(m, path):
 
 
 def test_fused_attention_block_equals_three_launch_path(tiny):
-    """Every path of the greedy decode step -- the fused attention block (attn_gproj with the
-    partial-sum gate/up), the three-launch block (qkv_rmsnorm_rope, decode_attn, qgemv) and
-    the one-launch step kernel -- gives the same decode logits to 1e-3 and the same greedy
-    ids."""
+    """Every path of the greedy decode step -- the per-head attention + o-projection
+    (attn_oproj_fix with the fixed-point gate/up), attn_gproj with the partial-sum gate/up, the
+    three-launch block (qkv_rmsnorm_rope, decode_attn, qgemv) and the one-launch step kernel --
+    gives the same decode logits to 1e-3 and the same greedy ids."""
     from pico_hip import kernels as K
     eng, _ = tiny
     m = eng.model
@@ -197,6 +198,8 @@ def test_config0_greedy_matches_fixture(model_dir, path):
     assert synth.sha256(gguf) == fx["gguf_sha256"], "synthetic model is not byte-identical"
     eng = Engine(gguf)
     _set_path(eng.model, path)
+    cap = len(fx["prompt_ids"]) + fx["n_tokens"]
+    assert eng.model.attn_oproj_ok(cap) == (path == "attn_oproj")
     got = eng.generate_ids(fx["prompt_ids"], fx["n_tokens"], temperature=0.0, use_graph=True)
     first_diff = next((i for i, (a, b) in enumerate(zip(got, fx["tokens"])) if a != b), None)
     assert got == fx["tokens"], f"first mismatch at step {first_diff} (margin {fx['margins'][first_diff]})"
