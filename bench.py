@@ -142,6 +142,40 @@ def kernel_launchers(eng, which: str, attn: tuple[int, int] = (45, 80)):
         fn = lambda wq, wk, wv: K.qkv_rmsnorm_rope(x, L0.attn_norm_ut, cfg.eps, wq, wk, wv, L0.bq, L0.bk,
                                                    L0.bv, m.cos, m.sin, pos, kc, vc, nh, layout=XU)
         io = 4 * (2 * h + (nh + 2 * nkv) * hd + hd + nh * hd + 2 * nkv * hd)
+    elif which == "qkv_fix":
+        # the staged form over x + the four down-product replicas of the previous layer's
+        # fused FFN (every layer but the first); stores the summed vector
+        ws = (L0.wq, L0.wk, L0.wv)
+        cap = 64
+        kc = torch.zeros(nkv, cap, hd, device=eng.device)
+        vc = torch.zeros(nkv, cap, hd, device=eng.device)
+        pos = torch.tensor([40], device=eng.device)
+        acc4 = torch.zeros(K.FFN_REPLICAS, K.fix_stride(h), device=eng.device, dtype=torch.int64)
+        acc4[:, :h] = (torch.randn(K.FFN_REPLICAS, h, device=eng.device, dtype=torch.float64)
+                       * 0.1 * 2.0 ** 32).to(torch.int64)
+        name = (f"k_qkv_fix ({'/'.join(tn(w) for w in ws)}, x + 2^-32 sum of 4 replicas, rmsnorm, bias, "
+                f"RoPE, cache write) {h}->{nh}x{hd}+2x{nkv}x{hd}")
+        fn = lambda wq, wk, wv: K.qkv_fix_rmsnorm_rope(x, acc4, L0.attn_norm_ut, cfg.eps, wq, wk, wv, L0.bq,
+                                                       L0.bk, L0.bv, m.cos, m.sin, pos, kc, vc, nh,
+                                                       layout=XU)
+        io = (4 * (3 * h + (nh + 2 * nkv) * hd + hd + nh * hd + 2 * nkv * hd) +
+              8 * K.FFN_REPLICAS * (h + 1))
+    elif which in ("ffn_fix_q6k", "ffn_fix_q4k"):
+        # the fused FFN as the decode step runs it: x + 2^-32 o-projection accumulator,
+        # RMSNorm, [gate; up], SiLU, and ffn_down's column slices added into the four
+        # fixed-point replicas the next layer's QKV launch reads
+        from pico_hip.dequant import GGML_Q4_K, GGML_Q6_K
+        want = GGML_Q6_K if which == "ffn_fix_q6k" else GGML_Q4_K
+        li = next((i for i, Lr in enumerate(m.layers[:-1]) if Lr.w_down.ggml_type == want), 0)
+        Lr = m.layers[li]
+        ws = (Lr.w_gate_up, Lr.w_down)
+        fix = K.fix_acc(h, eng.device)[0]
+        fix[:h] = (torch.randn(h, device=eng.device, dtype=torch.float64) * 0.1 * 2.0 ** 32).to(torch.int64)
+        acc4 = torch.zeros(K.FFN_REPLICAS, K.fix_stride(h), device=eng.device, dtype=torch.int64)
+        name = (f"k_ffn_fix ({tn(ws[0])} gate/up, {tn(ws[1])} ffn_down slices, x + 2^-32 o-proj acc, "
+                f"rmsnorm, SiLU, 4 fixed-point replicas) {h}->2x{cfg.ffn_dim}->{h}")
+        fn = lambda wgu, wd: K.ffn_fix(x, fix, Lr.ffn_norm_ut, wgu, wd, cfg.eps, acc4, layout=XU | YU)
+        io = 4 * 3 * h + 8 * (h + 1) + 8 * K.FFN_REPLICAS * (h + 1)
     elif which == "attn_gproj":
         # attention over S cached positions (config 0: 45, the mean context of a 13-token
         # prompt and 64 decode steps) times each kv group's columns of Wo
@@ -208,6 +242,18 @@ def decode_kernels(eng, capacity: int) -> list[tuple[str, int]]:
     gproj = (m.use_attn_gproj and L0.w_gate_up is not None and
              K.attn_gproj_supported(cfg.n_head, cfg.n_kv_head, cfg.head_dim, capacity, L0.wo))
     rows = [("qkv", n)]
+    if m.ffn_fix_ok(capacity):
+        # three launches per layer: qkv (first layer) / qkv_fix, attn_oproj, ffn_fix (the last
+        # layer: gate_up_fix and its ffn_down)
+        rows = [("qkv", 1), ("qkv_fix", n - 1), ("attn_oproj", n)]
+        for key, t in (("ffn_fix_q6k", GGML_Q6_K), ("ffn_fix_q4k", GGML_Q4_K)):
+            c = sum(1 for Lr in m.layers[:-1] if Lr.w_down.ggml_type == t)
+            if c:
+                rows.append((key, c))
+        rows.append(("gate_up_fix", 1))
+        rows.append(("down_q6k" if m.layers[-1].w_down.ggml_type == GGML_Q6_K else "down_q4k", 1))
+        rows.append(("lm_head", 1))
+        return rows
     if m.attn_oproj_ok(capacity):
         rows += [("attn_oproj", n), ("gate_up_fix", n)]
     elif gproj:
@@ -243,17 +289,47 @@ def kernel_table(eng, iters: int, config: int, attn: tuple[int, int] = (45, 80))
     return out
 
 
+def kernel_groups(table: list[dict]) -> list[dict]:
+    """The table with the entries of one kernel over several weight formats (keys differing only
+    in a _q6k / _q4k suffix: the alternating ffn_down formats) merged: launches and time per
+    token added, bytes per launch and launch time averaged over the launches, achieved = mean
+    bytes / mean time, traffic the launch-weighted mean when every entry has one."""
+    groups: dict[str, list[dict]] = {}
+    for r in table:
+        k = r["key"]
+        base = k[:-4] if k.endswith(("_q6k", "_q4k")) else k
+        groups.setdefault(base, []).append(r)
+    out = []
+    for base, rows in groups.items():
+        if len(rows) == 1:
+            out.append(rows[0])
+            continue
+        n = sum(r["launches_per_token"] for r in rows)
+        us = sum(r["us_per_token"] for r in rows)
+        alg = sum(r["algorithmic_bytes"] * r["launches_per_token"] for r in rows) / n
+        avg = us / n
+        traffic = (None if any(r["traffic"] is None for r in rows) else
+                   int(sum(r["traffic"] * r["launches_per_token"] for r in rows) / n))
+        achieved = alg / (avg * 1e-6) / 1e9
+        out.append({"key": base, "kernel": " | ".join(r["kernel"] for r in rows), "launches_per_token": n,
+                    "avg_launch_us": round(avg, 3), "us_per_token": round(us, 2),
+                    "algorithmic_bytes": int(alg), "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS,
+                    "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic})
+    return out
+
+
 def roofline_of(table: list[dict], key: str | None) -> dict:
-    """The roofline object: the table entry ``key``, or the one with the largest time per token."""
+    """The roofline object: the table entry ``key``, or the kernel with the largest time per
+    token (its weight-format instantiations together, kernel_groups)."""
     row = next((r for r in table if r["key"] == key), None) if key else None
     if row is None:
-        row = max(table, key=lambda r: r["us_per_token"])
+        row = max(kernel_groups(table), key=lambda r: r["us_per_token"])
     return {"bound": "hbm", "kernel": row["kernel"], "achieved": row["achieved"], "peak": row["peak"],
             "unit": row["unit"], "frac": row["frac"], "traffic": row["traffic"],
             "avg_launch_us": row["avg_launch_us"], "algorithmic_bytes": row["algorithmic_bytes"],
             "launches_per_token": row["launches_per_token"], "us_per_token": row["us_per_token"],
             "selected_as": "requested by --kernel" if key and row["key"] == key else
-                           "largest time per decode token of the kernels timed"}
+                           "largest time per decode token of the kernels timed (weight formats of one kernel together)"}
 
 
 def kernel_only(eng, args) -> None:

@@ -402,6 +402,66 @@ int pe_qgemv_fix_rmsnorm_silu(int ggml_type, const void* w_tiled, int64_t ffn, i
                               const float* x, const int64_t* fix, const float* norm_w, float eps,
                               float* act, float* x_sum, int layout, pe_stream_t stream);
 
+/* Down-slice layout of an (n x k) ffn_down matrix for pe_ffn_fix (Q4_K, Q6_K, Q5_0, Q8_0;
+ * n % 32 == 0, k a whole number of blocks): per 32-column slice u, the records of the n rows
+ * contiguous in the unit-transposed order of the rows (position p holds the row r with
+ * ((r % 32) / 4 * (n / 32) + r / 32) * 4 + r % 4 == p), in two planes (codes, then scales):
+ * Q4_K 16 + 8 bytes per record (packed nibbles; fp32
+ * d*sc, dmin*m), Q6_K 16 + 16 (low nibbles; high bit pairs, fp32 d*sc for each half), Q5_0
+ * 16 + 8 (qs; qh, fp32 d), Q8_0 32 + 4 (codes; fp32 d). Codes keep their bits and the fp32
+ * scales are the exact products, so the weights are the same values. _bytes returns the size
+ * or a negative pe_status. */
+int64_t pe_down_slice_bytes(int ggml_type, int64_t n, int64_t k);
+int pe_repack_down_slices(int ggml_type, const void* blocks, void* w_slices, int64_t n, int64_t k,
+                          pe_stream_t stream);
+
+/* The decode FFN in one launch, its down product split over the FFN dimension and added in
+ * 64-bit fixed point:
+ *   x_sum = x + 2^-32 acc_in            (acc_in: pe_attn_oproj_fix's accumulator, hidden + 1)
+ *   act   = SiLU(W_gate h) * (W_up h),   h = rmsnorm(x_sum) * norm_w
+ *   acc_out[b % replicas][r] += 2^32 sum_{f in unit b} W_down[r][f] act[f]   (rounded)
+ * for every 32-index FFN unit b (one workgroup each, no communication between them). Replica q
+ * starts at acc_out + q * acc_stride; element hidden of a replica counts addends that were
+ * not finite or reached the bound pe_ffn_fix_bound(ffn) in magnitude (chosen so that no sum
+ * over all units overflows). The replicas must be zero (or hold what to add to) before the
+ * call. x + 2^-32 (sum of the replicas) is the FFN output with its residual
+ * (pe_qkv_fix_rmsnorm_rope reads it). layout: PE_LAYOUT_X_UT for x, acc_in, norm_w and
+ * x_sum unit-transposed, PE_LAYOUT_Y_UT for acc_out. Limits (pe_ffn_fix_supported): [gate; up]
+ * tiled Q5_0 / Q8_0 (2 ffn x hidden), W_down in the down-slice layout, hidden % 32 == 0 and
+ * <= 2048; replicas 1, 2, 4 or 8; acc_stride >= hidden + 1 and even.
+ * Replaces, for one token: the o-projection's residual add (model.py:213), rmsnorm + q5_0_gemv_norm
+ * (model.py:215-218, kernels.py:225-266), silu_mul (kernels.py:62-87) and the ffn_down GEMV
+ * (model.py:225-234, kernels.py:269-344) without its residual add (the consumer's). */
+typedef struct pe_ffn_fix_args {
+    int type_gu;              /* PE_TYPE_Q5_0 or PE_TYPE_Q8_0 */
+    const void* w_gu;         /* tiled [gate; up] (2 ffn x hidden) */
+    int type_down;            /* PE_TYPE_Q4_K, Q6_K, Q5_0 or Q8_0 */
+    const void* w_down;       /* down-slice layout of W_down (hidden x ffn) */
+    int64_t hidden, ffn;
+    const float* x;           /* (hidden) */
+    const int64_t* acc_in;    /* (hidden + 1) fixed-point accumulator, 16-byte aligned */
+    const float* norm_w;      /* (hidden) ffn_norm weight */
+    float eps;
+    float* x_sum;             /* (hidden) x + 2^-32 acc_in, or NULL */
+    int64_t* acc_out;         /* replicas x acc_stride int64, 16-byte aligned */
+    int replicas;
+    int64_t acc_stride;
+    int layout;
+} pe_ffn_fix_args;
+int pe_ffn_fix_supported(int type_gu, int type_down, int64_t hidden, int64_t ffn);
+float pe_ffn_fix_bound(int64_t ffn);
+int pe_ffn_fix(const pe_ffn_fix_args* args, pe_stream_t stream);
+
+/* pe_qkv_rmsnorm_rope whose input is x + 2^-32 (acc[0] + ... + acc[replicas-1]), the replicas
+ * of pe_ffn_fix's accumulator (replica q at acc + q * acc_stride; a non-zero count at index
+ * hidden of any replica makes every element NaN); replicas 0 reads x alone. x_sum (NULL: not
+ * stored) receives the summed vector (the layer's residual). The summed activation is staged
+ * once per 256-thread workgroup. Types Q5_0, Q8_0, Q4_K, Q6_K; hidden <= 2048; norm_w
+ * required; replicas 0 or 4; layout 0 or PE_LAYOUT_X_UT (x, norm_w, acc and x_sum).
+ * Replaces, for one token, the ffn_down residual add (model.py:234) and model.py:175-193. */
+int pe_qkv_fix_rmsnorm_rope(const pe_qkv_args* args, const int64_t* acc, int replicas,
+                            int64_t acc_stride, float* x_sum, pe_stream_t stream);
+
 /* Decode attention of each kv group fused with the group's share of the o-projection, one
  * launch, no communication between workgroups. For kv head j with query heads
  * h = j*G .. j*G+G-1 (G = n_head / n_kv):

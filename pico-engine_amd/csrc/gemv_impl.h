@@ -51,8 +51,11 @@ struct GemvArgs {
     int n_parts;
     float* x_sum;
     // kModeSiluFix: k int64 fixed-point values (2^-32 units, the layout of x) and, at index k, a
-    // count of values that could not be represented (non-zero: the sum is NaN)
+    // count of values that could not be represented (non-zero: the sum is NaN); with several
+    // replicas (staged activations of NR > 1), replica r starts at fix + r * fix_stride and the
+    // value is the sum over the replicas
     const int64_t* fix;
+    int64_t fix_stride;
 };
 
 // 2^-32 v for a 64-bit two's-complement fixed-point v (lo, hi words), rounded once to fp32:
@@ -402,23 +405,26 @@ constexpr int act_loads() {
 // are loaded after the weights.
 constexpr int kEarlyParts = 4;
 
-template <int M4>
+template <int M4, int NR = 1>
 struct ActLoads {
     float4 x[M4];
     float4 w[M4];
     float4 p[kEarlyParts][M4];  // summed-activation mode only
-    int4 f[2][M4];              // fixed-point mode: the four 64-bit sums of x's float4
-    uint2 poison;               // fixed-point mode: the unrepresentable-value count
+    int4 f[NR][2][M4];          // fixed-point mode: the four 64-bit sums of x's float4, per replica
+    uint2 poison[NR];           // fixed-point mode: the unrepresentable-value counts
 };
 
 // Issue the float4 loads of x (and the RMSNorm weight) that this thread stages. Indices past
 // the vector are clamped to its last float4 (no branch around the load, which would make the
 // compiler wait for the data right there); finish_activation ignores them.
-template <int NT, bool NORM, int M4, int SUM = kSumNone>
-PE_DEV void issue_activation(const GemvArgs& a, int units, ActLoads<M4>& L) {
+template <int NT, bool NORM, int M4, int SUM = kSumNone, int NR = 1>
+PE_DEV void issue_activation(const GemvArgs& a, int units, ActLoads<M4, NR>& L) {
     if (a.k > kStageMaxK || units * 8 > NT * M4) return;
     const int n4 = units * 8;
-    if constexpr (SUM == kSumFix) L.poison = reinterpret_cast<const uint2*>(a.fix)[a.k];
+    if constexpr (SUM == kSumFix) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) L.poison[r] = reinterpret_cast<const uint2*>(a.fix + r * a.fix_stride)[a.k];
+    }
 #pragma unroll
     for (int m = 0; m < M4; ++m) {
         const int i = (int)threadIdx.x + NT * m;
@@ -427,8 +433,12 @@ PE_DEV void issue_activation(const GemvArgs& a, int units, ActLoads<M4>& L) {
             L.x[m] = reinterpret_cast<const float4*>(a.x)[ic];
             if constexpr (NORM) L.w[m] = reinterpret_cast<const float4*>(a.norm_w)[ic];
             if constexpr (SUM == kSumFix) {
-                L.f[0][m] = reinterpret_cast<const int4*>(a.fix)[2 * ic];
-                L.f[1][m] = reinterpret_cast<const int4*>(a.fix)[2 * ic + 1];
+#pragma unroll
+                for (int r = 0; r < NR; ++r) {
+                    const int4* fr = reinterpret_cast<const int4*>(a.fix + r * a.fix_stride);
+                    L.f[r][0][m] = fr[2 * ic];
+                    L.f[r][1][m] = fr[2 * ic + 1];
+                }
             }
             if constexpr (SUM == kSumEarly) {
                 // slots past n_parts re-read the last part (never added; parts points at x when
@@ -492,9 +502,19 @@ PE_DEV float direct_activation(const GemvArgs& a, int glane, int units, float (&
     return 1.0f;
 }
 
-template <int NT, int GS, int UPL, bool NORM, int SUM = kSumNone, int UM = 0>
+// The sum of NR replicas of a 64-bit fixed-point value (lo, hi words of each), exact in
+// int64 (the producers bound every contribution so that no sum overflows).
+template <int NR>
+PE_DEV float fix_replicas_to_float(const uint32_t (&lo)[NR], const uint32_t (&hi)[NR]) {
+    uint64_t s = 0;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) s += ((uint64_t)hi[r] << 32) | lo[r];
+    return fix_to_float((uint32_t)s, (uint32_t)(s >> 32));
+}
+
+template <int NT, int GS, int UPL, bool NORM, int SUM = kSumNone, int UM = 0, int NR = 1>
 PE_DEV float finish_activation(const GemvArgs& a, int glane, int units,
-                               const ActLoads<act_loads<NT, GS, UPL>()>& L, float (&xr)[UPL][32],
+                               const ActLoads<act_loads<NT, GS, UPL>(), NR>& L, float (&xr)[UPL][32],
                                UnitSums (&xs)[UPL], float* lds4, float* stage) {
     constexpr int M4 = act_loads<NT, GS, UPL>();
     const bool ut = a.layout & PE_LAYOUT_X_UT;
@@ -509,13 +529,24 @@ PE_DEV float finish_activation(const GemvArgs& a, int glane, int units,
             const int j = ut ? i / units : i & 7;
             float4 v = L.x[m];
             if constexpr (SUM == kSumFix) {
-                // x + 2^-32 f, one fp32 addition per element; NaN if any sum was unrepresentable
-                const int4 f0 = L.f[0][m], f1 = L.f[1][m];
-                v.x += fix_to_float((uint32_t)f0.x, (uint32_t)f0.y);
-                v.y += fix_to_float((uint32_t)f0.z, (uint32_t)f0.w);
-                v.z += fix_to_float((uint32_t)f1.x, (uint32_t)f1.y);
-                v.w += fix_to_float((uint32_t)f1.z, (uint32_t)f1.w);
-                if (L.poison.x | L.poison.y) v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+                // x + 2^-32 f (f summed over the replicas in int64), one fp32 addition per
+                // element; NaN if any sum was unrepresentable
+                uint32_t lo[4][NR], hi[4][NR];
+                uint32_t bad = 0;
+#pragma unroll
+                for (int r = 0; r < NR; ++r) {
+                    const int4 f0 = L.f[r][0][m], f1 = L.f[r][1][m];
+                    lo[0][r] = (uint32_t)f0.x; hi[0][r] = (uint32_t)f0.y;
+                    lo[1][r] = (uint32_t)f0.z; hi[1][r] = (uint32_t)f0.w;
+                    lo[2][r] = (uint32_t)f1.x; hi[2][r] = (uint32_t)f1.y;
+                    lo[3][r] = (uint32_t)f1.z; hi[3][r] = (uint32_t)f1.w;
+                    bad |= L.poison[r].x | L.poison[r].y;
+                }
+                v.x += fix_replicas_to_float<NR>(lo[0], hi[0]);
+                v.y += fix_replicas_to_float<NR>(lo[1], hi[1]);
+                v.z += fix_replicas_to_float<NR>(lo[2], hi[2]);
+                v.w += fix_replicas_to_float<NR>(lo[3], hi[3]);
+                if (bad) v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
                 if (a.x_sum && blockIdx.x == 0) reinterpret_cast<float4*>(a.x_sum)[i] = v;
             } else if constexpr (SUM != kSumNone) {
                 // x + parts[0] + parts[1] + ... in that order; late parts are all loaded before

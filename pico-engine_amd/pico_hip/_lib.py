@@ -91,6 +91,17 @@ class StepArgs(ctypes.Structure):
     ]
 
 
+class FfnFixArgs(ctypes.Structure):
+    """Mirror of pe_ffn_fix_args (include/pico_hip.h)."""
+
+    _fields_ = [
+        ("type_gu", _I), ("w_gu", _P), ("type_down", _I), ("w_down", _P),
+        ("hidden", _L), ("ffn", _L),
+        ("x", _P), ("acc_in", _P), ("norm_w", _P), ("eps", _F), ("x_sum", _P),
+        ("acc_out", _P), ("replicas", _I), ("acc_stride", _L), ("layout", _I),
+    ]
+
+
 _SIGNATURES = {
     "pe_strerror": (ctypes.c_char_p, [_I]),
     "pe_abi_version": (_I, []),
@@ -142,6 +153,12 @@ _SIGNATURES = {
     "pe_attn_oproj_fix_supported": (_I, [_I, _L, _I, _I, _I, _L]),
     "pe_attn_oproj_fix": (_I, [ctypes.POINTER(AttnOprojArgs), _P]),
     "pe_qgemv_fix_rmsnorm_silu": (_I, [_I, _P, _L, _L, _P, _P, _P, _F, _P, _P, _I, _P]),
+    "pe_down_slice_bytes": (_L, [_I, _L, _L]),
+    "pe_repack_down_slices": (_I, [_I, _P, _P, _L, _L, _P]),
+    "pe_ffn_fix_supported": (_I, [_I, _I, _L, _L]),
+    "pe_ffn_fix_bound": (_F, [_L]),
+    "pe_ffn_fix": (_I, [ctypes.POINTER(FfnFixArgs), _P]),
+    "pe_qkv_fix_rmsnorm_rope": (_I, [ctypes.POINTER(QkvArgs), _P, _I, _L, _P, _P]),
 }
 
 # Every symbol include/pico_hip.h declares (checked by tests/test_abi.py).

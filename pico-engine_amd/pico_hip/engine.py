@@ -109,8 +109,11 @@ class Engine:
                 # Wo also in the o-projection layout of the per-head attention + o-projection
                 # launch (Q5_0 / Q8_0: the 0.5B family; 0.55 MB a layer at config 0)
                 oproj = t.name.endswith(".attn_output.weight")
+                # ffn_down also in the down-slice layout of the fused FFN launch (hidden <=
+                # 2048: the 0.5B family; 3.3-4.4 MB a layer at config 0)
+                slices = t.name.endswith(".ffn_down.weight")
                 quant[t.name] = K.pack_weight(self._upload(raw), t.ggml_type, shape[0], shape[1],
-                                              mfma=mfma, oproj=oproj)
+                                              mfma=mfma, oproj=oproj, slices=slices)
                 continue
             if len(shape) == 1 and t.ggml_type in (GGML_F32, GGML_F16):
                 weights[t.name] = K.dequantize(t.ggml_type, self._upload(raw), t.n_elements)

@@ -23,8 +23,8 @@ import os
 
 import torch
 
-from ._lib import (LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT, AttnOprojArgs, QkvArgs, StepArgs, StepLayer, check,
-                   lib)
+from ._lib import (LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT, AttnOprojArgs, FfnFixArgs, QkvArgs, StepArgs,
+                   StepLayer, check, lib)
 from .dequant import (BLOCK_SIZE, GGML_Q4_K, GGML_Q5_0, GGML_Q6_K, GGML_Q8_0, MATRIX_TYPES,
                       QUANT_TYPES, TYPE_NAMES, nbytes_for)
 
@@ -86,6 +86,9 @@ class QWeight:
     # the same matrix in the o-projection layout (pe_repack_oproj: Q5_0 / Q8_0 Wo) for the
     # per-head attention + o-projection launch (attn_oproj_fix)
     oproj: torch.Tensor | None = None
+    # the same matrix in the down-slice layout (pe_repack_down_slices: ffn_down of hidden <=
+    # 2048) for the fused FFN launch (ffn_fix)
+    slices: torch.Tensor | None = None
 
     @property
     def shape(self) -> tuple[int, int]:
@@ -99,7 +102,8 @@ class QWeight:
         """A distinct device copy (every layout it holds)."""
         return QWeight(self.data.clone(), self.ggml_type, self.n, self.k,
                        None if self.mfma is None else self.mfma.clone(),
-                       None if self.oproj is None else self.oproj.clone())
+                       None if self.oproj is None else self.oproj.clone(),
+                       None if self.slices is None else self.slices.clone())
 
     def __repr__(self) -> str:
         return f"QWeight({TYPE_NAMES[self.ggml_type]}, n={self.n}, k={self.k})"
@@ -164,11 +168,33 @@ def oproj_eligible(ggml_type: int, n: int, k: int) -> bool:
     return ggml_type in (GGML_Q5_0, GGML_Q8_0) and k % 64 == 0 and n > 0
 
 
+def down_slice_eligible(ggml_type: int, n: int, k: int) -> bool:
+    """Whether an (n x k) ffn_down matrix has a down-slice layout for ffn_fix (Q4_K / Q6_K /
+    Q5_0 / Q8_0, n <= 2048: the 0.5B family)."""
+    return n <= 2048 and n % 32 == 0 and lib.pe_down_slice_bytes(ggml_type, n, k) > 0
+
+
+def repack_down_slices(blocks: torch.Tensor, ggml_type: int, n: int, k: int) -> torch.Tensor:
+    """Raw GGUF blocks of an (n x k) matrix -> its down-slice layout (device uint8): per
+    32-column slice, every row's 32 codes and exact fp32 scales, contiguous over the rows."""
+    dev = _on_gpu(blocks)
+    size = lib.pe_down_slice_bytes(ggml_type, n, k)
+    if size < 0:
+        raise ValueError(f"no down-slice layout for a {n}x{k} {TYPE_NAMES.get(ggml_type, ggml_type)} matrix")
+    if blocks.numel() != nbytes_for(ggml_type, n * k):
+        raise ValueError(f"{blocks.numel()} bytes for a {n}x{k} {TYPE_NAMES[ggml_type]} tensor")
+    out = torch.empty(size, device=dev, dtype=torch.uint8)
+    check(lib.pe_repack_down_slices(ggml_type, _ptr(blocks), _ptr(out), n, k, _stream(dev)),
+          "pe_repack_down_slices")
+    return out
+
+
 def pack_weight(blocks: torch.Tensor, ggml_type: int, n: int, k: int, mfma: bool | None = None,
-                oproj: bool = False) -> QWeight:
+                oproj: bool = False, slices: bool = False) -> QWeight:
     """Raw GGUF blocks of an (n x k) tensor (device uint8) -> tiled QWeight, with the MFMA
-    layout copy as well when ``mfma`` (default: when mfma_eligible), and the o-projection
-    layout copy when ``oproj`` and the matrix has one (oproj_eligible)."""
+    layout copy as well when ``mfma`` (default: when mfma_eligible), the o-projection layout
+    copy when ``oproj`` and the matrix has one (oproj_eligible), and the down-slice layout copy
+    when ``slices`` and the matrix has one (down_slice_eligible)."""
     dev = _on_gpu(blocks)
     if ggml_type not in MATRIX_TYPES:
         raise ValueError(f"no GEMV kernel for {TYPE_NAMES.get(ggml_type, ggml_type)}")
@@ -180,7 +206,9 @@ def pack_weight(blocks: torch.Tensor, ggml_type: int, n: int, k: int, mfma: bool
     if mfma is None:
         mfma = mfma_eligible(ggml_type, n, k)
     return QWeight(data, ggml_type, n, k, repack_mfma(blocks, ggml_type, n, k) if mfma else None,
-                   repack_oproj(blocks, ggml_type, n, k) if oproj and oproj_eligible(ggml_type, n, k) else None)
+                   repack_oproj(blocks, ggml_type, n, k) if oproj and oproj_eligible(ggml_type, n, k) else None,
+                   repack_down_slices(blocks, ggml_type, n, k)
+                   if slices and down_slice_eligible(ggml_type, n, k) else None)
 
 
 def repack_oproj(blocks: torch.Tensor, ggml_type: int, n: int, k: int) -> torch.Tensor:
@@ -870,6 +898,109 @@ def qgemv_fix_norm_silu(x: torch.Tensor, fix: torch.Tensor, weight: torch.Tensor
     return out, x_sum
 
 
+# ---- the fused FFN launch and its consumer -------------------------------------------------
+
+FFN_REPLICAS = 4
+
+
+def fix_stride(hidden: int) -> int:
+    """Elements per fixed-point accumulator copy: hidden sums, the unrepresentable-value count,
+    padding to a multiple of 32 (256-byte aligned copies)."""
+    return hidden + 32
+
+
+def fix_acc_block(hidden: int, device, layers: int, replicas: int = FFN_REPLICAS) -> torch.Tensor:
+    """Zeroed accumulators of a fused decode step: (layers, 1 + replicas, fix_stride(hidden))
+    int64; [l, 0] is layer l's o-projection accumulator (attn_oproj_fix), [l, 1:] the replicas
+    of its down product (ffn_fix). One fill clears them all."""
+    return torch.zeros(layers, 1 + replicas, fix_stride(hidden), device=device, dtype=torch.int64)
+
+
+def ffn_fix_supported(w_gu: QWeight | None, w_down: QWeight) -> bool:
+    """Whether ffn_fix covers this layer: [gate; up] one Q5_0 / Q8_0 tensor, ffn_down with its
+    down-slice layout copy, hidden <= 2048."""
+    return (w_gu is not None and w_down.slices is not None and w_gu.n == 2 * w_down.k and
+            w_gu.k == w_down.n and
+            lib.pe_ffn_fix_supported(w_gu.ggml_type, w_down.ggml_type, w_down.n, w_down.k) == 0)
+
+
+def ffn_fix(x: torch.Tensor, acc_in: torch.Tensor, norm_w: torch.Tensor, w_gu: QWeight,
+            w_down: QWeight, eps: float, acc_out: torch.Tensor, x_sum: torch.Tensor | None = None,
+            layout: int = LAYOUT_NATURAL) -> torch.Tensor:
+    """The decode FFN in one launch (pe_ffn_fix): x_sum = x + 2^-32 acc_in (acc_in:
+    attn_oproj_fix's accumulator), act = SiLU(W_gate h) * (W_up h) with h = rmsnorm(x_sum) *
+    norm_w, and W_down act added in 2^-32 fixed point into the replicas of ``acc_out``
+    ((replicas, stride) int64, zero or holding what to add to). Returns x_sum; the FFN output
+    with its residual is x_sum + 2^-32 acc_out.sum(0) (qkv_fix_rmsnorm_rope reads it).
+    layout: LAYOUT_X_UT for x, acc_in, norm_w and x_sum, LAYOUT_Y_UT for acc_out."""
+    dev = _on_gpu(x, acc_in, norm_w, w_gu.data, acc_out)
+    if w_down.slices is None:
+        raise ValueError(f"{w_down} has no down-slice layout copy")
+    hidden, ffn = w_down.n, w_down.k
+    if w_gu.n != 2 * ffn or w_gu.k != hidden:
+        raise ValueError(f"[gate; up] {w_gu} does not match ffn_down {w_down}")
+    x = _f32c(x.reshape(-1))
+    nw = _f32c(norm_w.reshape(-1))
+    if acc_in.dtype != torch.int64 or acc_in.numel() < hidden + 1 or not acc_in.is_contiguous():
+        raise ValueError(f"acc_in must be a contiguous int64 tensor of at least {hidden + 1} elements")
+    if acc_out.dtype != torch.int64 or acc_out.dim() != 2 or not acc_out.is_contiguous():
+        raise ValueError("acc_out must be a contiguous (replicas, stride) int64 tensor")
+    if x_sum is None:
+        x_sum = torch.empty_like(x)
+    a = FfnFixArgs(w_gu.ggml_type, w_gu.data.data_ptr(), w_down.ggml_type, w_down.slices.data_ptr(),
+                   hidden, ffn, x.data_ptr(), acc_in.data_ptr(), nw.data_ptr(), float(eps),
+                   x_sum.data_ptr(), acc_out.data_ptr(), acc_out.shape[0], acc_out.shape[1], layout)
+    check(lib.pe_ffn_fix(ctypes.byref(a), _stream(dev)), "pe_ffn_fix")
+    return x_sum
+
+
+def ffn_fix_bound(ffn: int) -> float:
+    """The magnitude from which ffn_fix counts an addend as unrepresentable."""
+    return float(lib.pe_ffn_fix_bound(ffn))
+
+
+def qkv_fix_rmsnorm_rope(x: torch.Tensor, acc: torch.Tensor | None, norm_w: torch.Tensor, eps: float,
+                         wq: QWeight, wk: QWeight, wv: QWeight,
+                         bq: torch.Tensor | None, bk: torch.Tensor | None, bv: torch.Tensor | None,
+                         cos_tab: torch.Tensor, sin_tab: torch.Tensor, pos: torch.Tensor,
+                         k_cache: torch.Tensor, v_cache: torch.Tensor, n_head: int,
+                         x_sum: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                         layout: int = LAYOUT_NATURAL) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """qkv_rmsnorm_rope over x + 2^-32 acc.sum(0) (acc: ffn_fix's (4, stride) replicas, or None
+    for x alone), staged once per workgroup (pe_qkv_fix_rmsnorm_rope). Returns (q, x_sum):
+    x_sum receives the summed vector when acc is given (else None: it is x)."""
+    dev = _on_gpu(x, acc, norm_w, wq.data, wk.data, wv.data, pos, k_cache, v_cache)
+    n_kv, capacity, hd = k_cache.shape
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("KV caches must be contiguous (n_kv, capacity, hd) buffers")
+    if pos.dtype != torch.int64:
+        raise ValueError("pos must be an int64 device tensor")
+    x = _f32c(x.reshape(-1))
+    nw = _f32c(norm_w.reshape(-1))
+    replicas, stride = 0, 0
+    if acc is not None:
+        if acc.dtype != torch.int64 or acc.dim() != 2 or not acc.is_contiguous():
+            raise ValueError("acc must be a contiguous (replicas, stride) int64 tensor")
+        replicas, stride = acc.shape
+        if x_sum is None:
+            x_sum = torch.empty_like(x)
+    else:
+        x_sum = None
+    if out is None:
+        out = torch.empty(n_head, hd, device=dev, dtype=torch.float32)
+    a = QkvArgs(wq.ggml_type, wk.ggml_type, wv.ggml_type,
+                wq.data.data_ptr(), wk.data.data_ptr(), wv.data.data_ptr(),
+                None if bq is None else bq.data_ptr(), None if bk is None else bk.data_ptr(),
+                None if bv is None else bv.data_ptr(),
+                x.data_ptr(), nw.data_ptr(), float(eps),
+                cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
+                pos.data_ptr(), out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                capacity, wq.k, n_head, n_kv, hd, layout)
+    check(lib.pe_qkv_fix_rmsnorm_rope(ctypes.byref(a), _ptr(acc), replicas, stride, _ptr(x_sum),
+                                      _stream(dev)), "pe_qkv_fix_rmsnorm_rope")
+    return out, x_sum
+
+
 # ---- prefill (M >= 1) --------------------------------------------------------------------
 
 def qgemm(x: torch.Tensor, w: QWeight, bias: torch.Tensor | None = None,
@@ -1027,6 +1158,8 @@ __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "
            "gemm_lt", "gemm_lt_workspace", "mgemv", "repack_mfma", "mfma_eligible", "MFMA_MIN_WEIGHTS",
            "attn_gproj", "attn_gproj_supported", "attn_oproj_fix", "attn_oproj_supported", "fix_acc",
            "repack_oproj", "oproj_eligible", "qgemv_fix_norm_silu", "qgemv_norm_argmax", "dequantize_weight_f16",
+           "repack_down_slices", "down_slice_eligible", "ffn_fix", "ffn_fix_supported", "ffn_fix_bound",
+           "fix_acc_block", "fix_stride", "qkv_fix_rmsnorm_rope", "FFN_REPLICAS",
            "DecodeStep", "decode_step_supported", "decode_step_workspace",
            "gemm_f16", "gemm_f16_silu", "interleave_gate_up_f16", "flash_prefill",
            "BLOCK_SIZE"]

@@ -6,22 +6,30 @@ With ``use_step_kernel`` set (off by default: about 2 % faster than the four-lau
 config 0 in a same-box A/B, 2062 vs 2025 tok/s, but it needs every workgroup resident at once
 and raises if a bounded wait runs out), a greedy decode step of a model the persistent kernel
 covers (head_dim 64, hidden <= 1024, ffn <= 8192, caches up to 128 positions: the 0.5B
-family) is one launch, pe_decode_step. Otherwise decode (one token) runs four launches per
-layer plus the embedding row and the LM head:
+family) is one launch, pe_decode_step. Otherwise decode (one token) runs three launches per
+layer plus the embedding row and the LM head (the 0.5B family):
 
   embed_gather                              model.py:152 (Q8_0 row, bit-exact)
   fill of the fixed-point accumulators (once per token, every layer)
   per layer:
-    qkv_rmsnorm_rope   (norm+QKV+bias+RoPE+cache write)   model.py:175-193
+    qkv_fix_rmsnorm_rope (x + 2^-32 sum of the previous   model.py:175-193, :234
+                        layer's FFN replicas, norm, QKV +
+                        bias, RoPE, cache write; the first
+                        layer: qkv_rmsnorm_rope over x)
     attn_oproj_fix     (GQA attention per query head,     model.py:211-213
                         fp16-rounded, times that head's
                         columns of Wo, added in 64-bit
                         fixed point into the accumulator)
-    qgemv_fix_norm_silu (x + 2^-32 acc, norm, gate/up,    model.py:213-224
-                        SiLU*up)
-    qgemv + residual   (ffn_down)                         model.py:225-234
+    ffn_fix            (x + 2^-32 acc, norm, gate/up,     model.py:213-234
+                        SiLU*up, ffn_down split over the
+                        FFN dimension, added into four
+                        fixed-point replicas; the last
+                        layer: qgemv_fix_norm_silu and the
+                        ffn_down qgemv with its residual)
   qgemv_norm(_argmax)  (final norm + LM head [+ greedy])  model.py:159-164
 
+Without a down-slice copy of ffn_down (ffn_fix_ok) the FFN runs as qgemv_fix_norm_silu and the
+ffn_down qgemv with its residual, after qkv_rmsnorm_rope (four launches per layer).
 attn_oproj_fix covers head_dim 64, caches of <= 128 positions and a Q5_0 / Q8_0 Wo (the 0.5B
 family); other formats at those sizes run attn_gproj (attention per kv group times the
 group's columns of Wo, one fp32 part per group) and qgemv_sum_norm_silu (x + parts).
@@ -121,6 +129,11 @@ class Transformer:
         # of <= 128 positions); else attn_gproj
         self.use_attn_oproj = True
         self._acc: torch.Tensor | None = None
+        # with attn_oproj_fix: the FFN of every layer but the last in one launch (ffn_fix: gate/up,
+        # SiLU and ffn_down split over the FFN dimension, added into fixed-point replicas that
+        # the next layer's QKV launch reads), where every such layer qualifies (ffn_fix_ok)
+        self.use_ffn_fix = True
+        self._acc_block: torch.Tensor | None = None
         # attention of each kv group fused with its share of the o-projection (attn_gproj),
         # the shares added by the gate/up GEMV: four launches per layer instead of five
         self.use_attn_gproj = True
@@ -275,6 +288,13 @@ class Transformer:
                    K.attn_oproj_supported(c.n_head, c.n_kv_head, c.head_dim, capacity, L.wo)
                    for L in self.layers)
 
+    def ffn_fix_ok(self, capacity: int) -> bool:
+        """Whether decode with a cache of ``capacity`` positions runs the three-launch layers
+        (qkv_fix_rmsnorm_rope, attn_oproj_fix, ffn_fix): attn_oproj_ok and every layer but the
+        last has an FFN that ffn_fix covers."""
+        return (self.use_ffn_fix and self.attn_oproj_ok(capacity) and
+                all(K.ffn_fix_supported(L.w_gate_up, L.w_down) for L in self.layers[:-1]))
+
     def _decode(self, token_ids, positions, cache, greedy=None):
         """One token. With a greedy state and a model pe_decode_step covers, the whole step is
         one launch that reads the token and position from the state. Otherwise four launches
@@ -295,6 +315,33 @@ class Transformer:
             pos = pos.to(torch.int64)
         capacity = cache[0][0].shape[1]
         x = K.embed_gather(self.embed, token_ids, layout=YU).reshape(-1)
+        if self.ffn_fix_ok(capacity):
+            if self._acc_block is None:
+                self._acc_block = K.fix_acc_block(cfg.hidden, self.device, cfg.n_layers)
+            acc = self._acc_block
+            acc.zero_()   # a fill kernel (graph-capturable), once per token for every layer
+            last = len(self.layers) - 1
+            d_acc = None   # the previous layer's down-product replicas
+            for i, L in enumerate(self.layers):
+                k_buf, v_buf = cache[i]
+                if d_acc is None:
+                    q = K.qkv_rmsnorm_rope(x, L.attn_norm_ut, cfg.eps, L.wq, L.wk, L.wv, L.bq, L.bk,
+                                           L.bv, self.cos, self.sin, pos, k_buf, v_buf, cfg.n_head,
+                                           layout=XU)
+                else:
+                    q, x = K.qkv_fix_rmsnorm_rope(x, d_acc, L.attn_norm_ut, cfg.eps, L.wq, L.wk, L.wv,
+                                                  L.bq, L.bk, L.bv, self.cos, self.sin, pos, k_buf,
+                                                  v_buf, cfg.n_head, layout=XU)
+                K.attn_oproj_fix(q, k_buf, v_buf, L.wo, pos, acc[i, 0], layout=YU)
+                if i < last:
+                    d_acc = acc[i, 1:]
+                    x = K.ffn_fix(x, acc[i, 0], L.ffn_norm_ut, L.w_gate_up, L.w_down, cfg.eps, d_acc,
+                                  layout=XU | YU)
+                else:
+                    act, x = K.qgemv_fix_norm_silu(x, acc[i, 0], L.ffn_norm_ut, L.w_gate_up, cfg.eps,
+                                                   layout=XU | YU)
+                    x = K.qgemv(act, L.w_down, residual=x, layout=XU | YU)
+            return self._lm_head(x, self.output_norm_ut, greedy, XU)
         if self.attn_oproj_ok(capacity):
             if self._acc is None:
                 self._acc = K.fix_acc(cfg.hidden, self.device, cfg.n_layers)

@@ -141,7 +141,8 @@ def test_mid_cache_decode_split_gproj(tiny):
 PATHS = {  # model flags of each path of the decode step
     "three_launch": dict(use_attn_oproj=False, use_attn_gproj=False, use_step_kernel=False),
     "attn_gproj": dict(use_attn_oproj=False, use_attn_gproj=True, use_step_kernel=False),
-    "attn_oproj": dict(use_attn_oproj=True, use_step_kernel=False),
+    "attn_oproj": dict(use_attn_oproj=True, use_ffn_fix=False, use_step_kernel=False),
+    "ffn_fix": dict(use_attn_oproj=True, use_ffn_fix=True, use_step_kernel=False),
     "step_kernel": dict(use_attn_oproj=False, use_step_kernel=True),
 }
 
@@ -154,8 +155,9 @@ def _set_path(m, path):
 
 
 def test_fused_attention_block_equals_three_launch_path(tiny):
-    """Every path of the greedy decode step -- the per-head attention + o-projection
-    (attn_oproj_fix with the fixed-point gate/up), attn_gproj with the partial-sum gate/up, the
+    """Every path of the greedy decode step -- the three-launch layers (staged QKV over the
+    down-product replicas, attn_oproj_fix, the fused FFN ffn_fix), the per-head attention +
+    o-projection (attn_oproj_fix with the fixed-point gate/up), attn_gproj with the partial-sum gate/up, the
     three-launch block (qkv_rmsnorm_rope, decode_attn, qgemv) and the one-launch step kernel --
     gives the same decode logits to 1e-3 and the same greedy ids."""
     from pico_hip import kernels as K
@@ -199,7 +201,8 @@ def test_config0_greedy_matches_fixture(model_dir, path):
     eng = Engine(gguf)
     _set_path(eng.model, path)
     cap = len(fx["prompt_ids"]) + fx["n_tokens"]
-    assert eng.model.attn_oproj_ok(cap) == (path == "attn_oproj")
+    assert eng.model.attn_oproj_ok(cap) == (path in ("attn_oproj", "ffn_fix"))
+    assert eng.model.ffn_fix_ok(cap) == (path == "ffn_fix")
     got = eng.generate_ids(fx["prompt_ids"], fx["n_tokens"], temperature=0.0, use_graph=True)
     first_diff = next((i for i, (a, b) in enumerate(zip(got, fx["tokens"])) if a != b), None)
     assert got == fx["tokens"], f"first mismatch at step {first_diff} (margin {fx['margins'][first_diff]})"
