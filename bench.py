@@ -137,8 +137,8 @@ def kernel_launchers(eng, which: str, attn: tuple[int, int] = (45, 80)):
         kc = torch.zeros(nkv, cap, hd, device=eng.device)
         vc = torch.zeros(nkv, cap, hd, device=eng.device)
         pos = torch.tensor([40], device=eng.device)
-        name = (f"k_qkv ({'/'.join(tn(w) for w in ws)}, rmsnorm, bias, RoPE, cache write) "
-                f"{h}->{nh}x{hd}+2x{nkv}x{hd}")
+        name = (f"{'k_mqkv' if K.mqkv_ok(*ws) else 'k_qkv'} ({'/'.join(tn(w) for w in ws)}, rmsnorm, bias, RoPE, "
+                f"cache write) {h}->{nh}x{hd}+2x{nkv}x{hd}")
         fn = lambda wq, wk, wv: K.qkv_rmsnorm_rope(x, L0.attn_norm_ut, cfg.eps, wq, wk, wv, L0.bq, L0.bk,
                                                    L0.bv, m.cos, m.sin, pos, kc, vc, nh, layout=XU)
         io = 4 * (2 * h + (nh + 2 * nkv) * hd + hd + nh * hd + 2 * nkv * hd)

@@ -229,6 +229,13 @@ int64_t pe_mfma_bytes(int ggml_type, int64_t n, int64_t k);
 int pe_repack_mfma(int ggml_type, const void* blocks, void* w_mfma, int64_t n, int64_t k,
                    pe_stream_t stream);
 
+/* pe_repack_mfma with the rows in "RoPE-pair order" for a matrix of heads of head_dim rows
+ * (head_dim % 16 == 0, n % head_dim == 0): position j (0..15) of the jt-th 16-row group of a
+ * head holds the head's row (j / 8) * head_dim/2 + 8 jt + j % 8, so every 16-row group carries 8
+ * whole rotation pairs (i, i + head_dim/2). The weights of pe_mqkv_rmsnorm_rope. */
+int pe_repack_mfma_pairs(int ggml_type, const void* blocks, void* w_mfma, int64_t n, int64_t k,
+                         int head_dim, pe_stream_t stream);
+
 /* Decode GEMV of a large Q4_K / Q6_K matrix on the integer matrix cores, from its MFMA layout:
  *   silu == 0: y[n] = W h + residual[n] (residual may be NULL),
  *   silu != 0: y[j] = silu(g_j) * u_j, [g; u] = W h over the 2 n rows of W (n % 16 == 0,
@@ -293,6 +300,18 @@ typedef struct pe_qkv_args {
     int layout;                        /* PE_LAYOUT_X_UT: x and norm_w unit-transposed */
 } pe_qkv_args;
 int pe_qkv_rmsnorm_rope(const pe_qkv_args* args, pe_stream_t stream);
+
+/* pe_qkv_rmsnorm_rope on the integer matrix cores, with w_q / w_k / w_v the pe_repack_mfma_pairs
+ * layouts (RoPE-pair order) of Q4_K or Q6_K matrices (type_k == type_q). A workgroup takes
+ * consecutive 16-row groups (8 rotation pairs each) of q, k or v, as many as make about one
+ * workgroup per CU; it builds the int8 activation planes of the normed x (pe_mgemv's
+ * arithmetic: exact integer products, fp32 scales and sums) and applies bias, RoPE and the
+ * stores of pe_qkv_rmsnorm_rope to its rows. hidden % 256 == 0 and <= 13568 (the
+ * planes, 144 bytes per 32 elements, stay in 64 KiB of LDS); norm_w required;
+ * layout 0 or PE_LAYOUT_X_UT. Same results as pe_qkv_rmsnorm_rope up to the order of the fp32
+ * additions. Replaces model.py:175-193 (kernels.py:14-59 and F.linear with bias) for the
+ * 7B-architecture shapes. */
+int pe_mqkv_rmsnorm_rope(const pe_qkv_args* args, pe_stream_t stream);
 
 /* Single-query GQA attention over a KV cache. Caches of at most 256 positions: one launch,
  * a workgroup per query head. Up to 1024 positions (head_dim 64) / 512 (head_dim 128): one

@@ -7,6 +7,7 @@
 // RoPE (which mixes exactly those two rows) without any exchange: q heads, then k heads,
 // then v heads (pairs as well, no rotation).
 #include "gemv_impl.h"
+#include "qkv_common.h"
 
 namespace pe {
 
@@ -14,37 +15,6 @@ struct QkvParams {
     pe_qkv_args a;
     int64_t k;  // hidden
 };
-
-// Epilogue of a task (lane 0 of its group): q = RoPE(y) (y = W h + b) returned, RoPE(k) and v
-// written to the caches at the position. An invalid position leaves the caches untouched and
-// stores NaN into q.
-template <int SEG>
-PE_DEV void qkv_store(const pe_qkv_args& a, int64_t head, int i, float y1, float y2, float c,
-                      float sn, bool pos_ok, int64_t pos) {
-    const int hd = a.head_dim, half = hd / 2;
-    if (SEG == 2) {
-        if (pos_ok) {
-            float* dst = a.v_cache + (head * a.capacity + pos) * hd;
-            dst[i] = y1;
-            dst[i + half] = y2;
-        }
-        return;
-    }
-    float o1 = __uint_as_float(0x7FC00000u), o2 = o1;
-    if (pos_ok) {
-        o1 = y1 * c - y2 * sn;
-        o2 = y1 * sn + y2 * c;
-    }
-    if (SEG == 0) {
-        const int64_t r1 = head * hd + i;
-        a.q_out[r1] = o1;
-        a.q_out[r1 + half] = o2;
-    } else if (pos_ok) {
-        float* dst = a.k_cache + (head * a.capacity + pos) * hd;
-        dst[i] = o1;
-        dst[i + half] = o2;
-    }
-}
 
 // One task of one segment: the pair of rows (i, i + hd/2) of head `head`. Weight, bias,
 // position and cos/sin loads are issued before the activation prologue.

@@ -121,6 +121,7 @@ _SIGNATURES = {
     "pe_gemm_lt_init": (_I, []),
     "pe_mfma_bytes": (_L, [_I, _L, _L]),
     "pe_repack_mfma": (_I, [_I, _P, _P, _L, _L, _P]),
+    "pe_repack_mfma_pairs": (_I, [_I, _P, _P, _L, _L, _I, _P]),
     "pe_mgemv": (_I, [_I, _P, _L, _L, _P, _P, _F, _P, _P, _I, _I, _P]),
     "pe_embed_gather": (_I, [_I, _P, _L, _L, _P, _L, _P, _I, _P]),
     "pe_qgemv": (_I, [_I, _P, _L, _L, _P, _P, _P, _P, _I, _P]),
@@ -129,6 +130,7 @@ _SIGNATURES = {
     "pe_qgemv_argmax_workspace_bytes": (_L, [_L]),
     "pe_qgemv_rmsnorm_argmax": (_I, [_I, _P, _L, _L, _P, _P, _F, _P, _P, _P, _L, _P, _L, _I, _P]),
     "pe_qkv_rmsnorm_rope": (_I, [ctypes.POINTER(QkvArgs), _P]),
+    "pe_mqkv_rmsnorm_rope": (_I, [ctypes.POINTER(QkvArgs), _P]),
     "pe_decode_attn_workspace_bytes": (_L, [_I, _I, _I, _L]),
     "pe_decode_attn": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _P, _P, _L, _I, _P]),
     "pe_decode_attn_noalloc": (_I, [_P, _P, _P, _I, _I, _I, _L, _P, _I, _L, _F, _I, _P, _I, _P]),

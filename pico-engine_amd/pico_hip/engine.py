@@ -112,8 +112,12 @@ class Engine:
                 # ffn_down also in the down-slice layout of the fused FFN launch (hidden <=
                 # 2048: the 0.5B family; 3.3-4.4 MB a layer at config 0)
                 slices = t.name.endswith(".ffn_down.weight")
+                # q, k and v also in the RoPE-pair MFMA layout of the QKV launch on the integer
+                # matrix cores (Q4_K / Q6_K with hidden % 256 == 0: the 7B family)
+                pairs_hd = self.cfg.head_dim if t.name.endswith((".attn_q.weight", ".attn_k.weight",
+                                                                  ".attn_v.weight")) else 0
                 quant[t.name] = K.pack_weight(self._upload(raw), t.ggml_type, shape[0], shape[1],
-                                              mfma=mfma, oproj=oproj, slices=slices)
+                                              mfma=mfma, oproj=oproj, slices=slices, pairs_hd=pairs_hd)
                 continue
             if len(shape) == 1 and t.ggml_type in (GGML_F32, GGML_F16):
                 weights[t.name] = K.dequantize(t.ggml_type, self._upload(raw), t.n_elements)

@@ -89,6 +89,10 @@ class QWeight:
     # the same matrix in the down-slice layout (pe_repack_down_slices: ffn_down of hidden <=
     # 2048) for the fused FFN launch (ffn_fix)
     slices: torch.Tensor | None = None
+    # the same matrix in the MFMA layout with its rows in RoPE-pair order
+    # (pe_repack_mfma_pairs: Q4_K / Q6_K attn_q / attn_k / attn_v) for the QKV launch on the
+    # integer matrix cores (mqkv)
+    pairs: torch.Tensor | None = None
 
     @property
     def shape(self) -> tuple[int, int]:
@@ -103,7 +107,8 @@ class QWeight:
         return QWeight(self.data.clone(), self.ggml_type, self.n, self.k,
                        None if self.mfma is None else self.mfma.clone(),
                        None if self.oproj is None else self.oproj.clone(),
-                       None if self.slices is None else self.slices.clone())
+                       None if self.slices is None else self.slices.clone(),
+                       None if self.pairs is None else self.pairs.clone())
 
     def __repr__(self) -> str:
         return f"QWeight({TYPE_NAMES[self.ggml_type]}, n={self.n}, k={self.k})"
@@ -162,6 +167,36 @@ def repack_mfma(blocks: torch.Tensor, ggml_type: int, n: int, k: int) -> torch.T
     return out
 
 
+# QKV of Q4_K / Q6_K matrices on the integer matrix cores (pe_mqkv_rmsnorm_rope) when every
+# segment has its RoPE-pair MFMA layout (the 7B family: 10.0 -> 5.x us); off (or PICO_MQKV=0 in
+# the environment): the tiled QKV launch
+use_mqkv = os.environ.get("PICO_MQKV", "1") != "0"
+# the activation planes of pe_mqkv_rmsnorm_rope stay in 64 KiB of LDS
+MQKV_MAX_HIDDEN = 13568
+
+
+def mqkv_eligible(ggml_type: int, n: int, k: int, head_dim: int) -> bool:
+    """Whether an (n x k) attn_q / attn_k / attn_v matrix of heads of head_dim rows has a
+    RoPE-pair MFMA layout for pe_mqkv_rmsnorm_rope."""
+    return (ggml_type in (GGML_Q4_K, GGML_Q6_K) and k % 256 == 0 and k <= MQKV_MAX_HIDDEN
+            and head_dim > 0 and head_dim % 16 == 0 and n % head_dim == 0)
+
+
+def repack_mfma_pairs(blocks: torch.Tensor, ggml_type: int, n: int, k: int, head_dim: int) -> torch.Tensor:
+    """Raw GGUF blocks of an (n x k) Q4_K / Q6_K matrix of heads of head_dim rows -> its MFMA
+    layout with the rows in RoPE-pair order (every 16-row group holds 8 rotation pairs)."""
+    dev = _on_gpu(blocks)
+    size = lib.pe_mfma_bytes(ggml_type, n, k)
+    if size < 0 or not mqkv_eligible(ggml_type, n, k, head_dim):
+        raise ValueError(f"no RoPE-pair MFMA layout for a {n}x{k} {TYPE_NAMES.get(ggml_type, ggml_type)} matrix")
+    if blocks.numel() != nbytes_for(ggml_type, n * k):
+        raise ValueError(f"{blocks.numel()} bytes for a {n}x{k} {TYPE_NAMES[ggml_type]} tensor")
+    out = torch.empty(size, device=dev, dtype=torch.uint8)
+    check(lib.pe_repack_mfma_pairs(ggml_type, _ptr(blocks), _ptr(out), n, k, head_dim, _stream(dev)),
+          "pe_repack_mfma_pairs")
+    return out
+
+
 def oproj_eligible(ggml_type: int, n: int, k: int) -> bool:
     """Whether an (n x k) matrix has an o-projection layout (pe_repack_oproj: Q5_0 / Q8_0,
     k % 64 == 0)."""
@@ -190,11 +225,13 @@ def repack_down_slices(blocks: torch.Tensor, ggml_type: int, n: int, k: int) -> 
 
 
 def pack_weight(blocks: torch.Tensor, ggml_type: int, n: int, k: int, mfma: bool | None = None,
-                oproj: bool = False, slices: bool = False) -> QWeight:
+                oproj: bool = False, slices: bool = False, pairs_hd: int = 0) -> QWeight:
     """Raw GGUF blocks of an (n x k) tensor (device uint8) -> tiled QWeight, with the MFMA
     layout copy as well when ``mfma`` (default: when mfma_eligible), the o-projection layout
-    copy when ``oproj`` and the matrix has one (oproj_eligible), and the down-slice layout copy
-    when ``slices`` and the matrix has one (down_slice_eligible)."""
+    copy when ``oproj`` and the matrix has one (oproj_eligible), the down-slice layout copy
+    when ``slices`` and the matrix has one (down_slice_eligible), and the RoPE-pair MFMA layout
+    for heads of ``pairs_hd`` rows when that is non-zero and the matrix has one
+    (mqkv_eligible)."""
     dev = _on_gpu(blocks)
     if ggml_type not in MATRIX_TYPES:
         raise ValueError(f"no GEMV kernel for {TYPE_NAMES.get(ggml_type, ggml_type)}")
@@ -208,7 +245,9 @@ def pack_weight(blocks: torch.Tensor, ggml_type: int, n: int, k: int, mfma: bool
     return QWeight(data, ggml_type, n, k, repack_mfma(blocks, ggml_type, n, k) if mfma else None,
                    repack_oproj(blocks, ggml_type, n, k) if oproj and oproj_eligible(ggml_type, n, k) else None,
                    repack_down_slices(blocks, ggml_type, n, k)
-                   if slices and down_slice_eligible(ggml_type, n, k) else None)
+                   if slices and down_slice_eligible(ggml_type, n, k) else None,
+                   repack_mfma_pairs(blocks, ggml_type, n, k, pairs_hd)
+                   if pairs_hd and mqkv_eligible(ggml_type, n, k, pairs_hd) else None)
 
 
 def repack_oproj(blocks: torch.Tensor, ggml_type: int, n: int, k: int) -> torch.Tensor:
@@ -715,16 +754,28 @@ def qkv_rmsnorm_rope(x: torch.Tensor, norm_w: torch.Tensor | None, eps: float,
     x = _f32c(x.reshape(-1))
     if out is None:
         out = torch.empty(n_head, hd, device=dev, dtype=torch.float32)
+    mq = mqkv_ok(wq, wk, wv) and norm_w is not None
     a = QkvArgs(wq.ggml_type, wk.ggml_type, wv.ggml_type,
-                wq.data.data_ptr(), wk.data.data_ptr(), wv.data.data_ptr(),
+                *((wq.pairs.data_ptr(), wk.pairs.data_ptr(), wv.pairs.data_ptr()) if mq else
+                  (wq.data.data_ptr(), wk.data.data_ptr(), wv.data.data_ptr())),
                 None if bq is None else bq.data_ptr(), None if bk is None else bk.data_ptr(),
                 None if bv is None else bv.data_ptr(),
                 x.data_ptr(), None if norm_w is None else norm_w.data_ptr(), float(eps),
                 cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
                 pos.data_ptr(), out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                 capacity, wq.k, n_head, n_kv, hd, layout)
-    check(lib.pe_qkv_rmsnorm_rope(ctypes.byref(a), _stream(dev)), "pe_qkv_rmsnorm_rope")
+    if mq:
+        check(lib.pe_mqkv_rmsnorm_rope(ctypes.byref(a), _stream(dev)), "pe_mqkv_rmsnorm_rope")
+    else:
+        check(lib.pe_qkv_rmsnorm_rope(ctypes.byref(a), _stream(dev)), "pe_qkv_rmsnorm_rope")
     return out
+
+
+def mqkv_ok(wq: QWeight, wk: QWeight, wv: QWeight) -> bool:
+    """Whether qkv_rmsnorm_rope runs on the integer matrix cores (pe_mqkv_rmsnorm_rope): every
+    segment has its RoPE-pair layout and q and k share a format (with an RMSNorm weight)."""
+    return (use_mqkv and wq.pairs is not None and wk.pairs is not None and wv.pairs is not None
+            and wq.ggml_type == wk.ggml_type)
 
 
 def attn_gproj_supported(n_head: int, n_kv: int, hd: int, capacity: int, wo: QWeight) -> bool:
@@ -1156,6 +1207,7 @@ __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "
            "q8_0_gemv", "q5_0_gemv", "q5_0_gemv_norm", "q6_k_gemv", "q4_k_gemv", "qgemv_norm",
            "qgemv_norm_silu", "qkv_rmsnorm_rope", "qgemv_sum_norm_silu", "qgemm", "kv_write", "prefill_attn",
            "gemm_lt", "gemm_lt_workspace", "mgemv", "repack_mfma", "mfma_eligible", "MFMA_MIN_WEIGHTS",
+           "repack_mfma_pairs", "mqkv_eligible", "mqkv_ok", "MQKV_MAX_HIDDEN",
            "attn_gproj", "attn_gproj_supported", "attn_oproj_fix", "attn_oproj_supported", "fix_acc",
            "repack_oproj", "oproj_eligible", "qgemv_fix_norm_silu", "qgemv_norm_argmax", "dequantize_weight_f16",
            "repack_down_slices", "down_slice_eligible", "ffn_fix", "ffn_fix_supported", "ffn_fix_bound",

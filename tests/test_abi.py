@@ -103,6 +103,33 @@ def test_argmax_argument_errors(lib):
     assert call(n=1 << 31, wsb=1 << 40) == 3      # row ids must fit 31 bits
 
 
+def test_mqkv_argument_errors(lib):
+    """pe_mqkv_rmsnorm_rope and pe_repack_mfma_pairs reject bad calls before any launch."""
+    from pico_hip._lib import QkvArgs
+    f = 0x1000
+    def args(**kw):
+        d = dict(type_q=12, type_k=12, type_v=14, w_q=f, w_k=f, w_v=f, b_q=None, b_k=None, b_v=None,
+                 x=f, norm_w=f, eps=1e-6, cos_tab=f, sin_tab=f, rope_rows=64, pos=f, q_out=f,
+                 k_cache=f, v_cache=f, capacity=40, hidden=3584, n_head=28, n_kv=4, head_dim=128, layout=0)
+        d.update(kw)
+        return ctypes.byref(QkvArgs(*[d[n] for n, _ in QkvArgs._fields_]))
+    call = lambda **kw: lib.pe_mqkv_rmsnorm_rope(args(**kw), None)
+    assert call(type_k=14) == 2                 # q and k share a format
+    assert call(type_v=6) == 2                  # K-quants only
+    assert call(hidden=896) == 3                # whole super-blocks
+    assert call(hidden=13824) == 3              # the planes must fit 64 KiB of LDS
+    assert call(head_dim=24) == 3               # 16-row groups of whole pairs
+    assert call(layout=2) == 3                  # only the input may be unit-transposed
+    assert call(norm_w=None) == 1               # the RMSNorm weight is required
+    assert call(w_v=None) == 1
+    assert call(x=0x1004) == 4                  # 16-byte aligned activation
+    assert lib.pe_mqkv_rmsnorm_rope(None, None) == 1
+    P = ctypes.c_void_p
+    assert lib.pe_repack_mfma_pairs(12, P(f), P(f), 96, 256, 64, None) == 3   # n % head_dim
+    assert lib.pe_repack_mfma_pairs(12, P(f), P(f), 96, 256, 24, None) == 3   # head_dim % 16
+    assert lib.pe_repack_mfma_pairs(6, P(f), P(f), 64, 256, 64, None) == 3    # no MFMA layout
+
+
 def test_qkv_args_struct_matches_header():
     """ctypes mirror of pe_qkv_args has the header's fields in the header's order."""
     from pico_hip._lib import QkvArgs
