@@ -481,6 +481,19 @@ int pe_ffn_fix(const pe_ffn_fix_args* args, pe_stream_t stream);
 int pe_qkv_fix_rmsnorm_rope(const pe_qkv_args* args, const int64_t* acc, int replicas,
                             int64_t acc_stride, float* x_sum, pe_stream_t stream);
 
+/* pe_qkv_fix_rmsnorm_rope (replicas 0) of the embedding row of the token *token: the
+ * activation is row *token of the raw GGUF table (vocab rows of `hidden` elements of
+ * embed_type: F32, F16, Q8_0, Q5_0, Q4_K, Q6_K, decoded bit-exactly as pe_embed_gather does,
+ * NaN for an id outside [0, vocab)), stored into x_out (the residual stream, in args->layout)
+ * by the first workgroup; args->x is not read. The launch also sets clear_bytes bytes at
+ * `clear` (16-byte aligned, a multiple of 16; may be 0) to zero, split over its workgroups:
+ * the first layer of a decode step clears the step's fixed-point accumulators there. One
+ * launch in place of pe_embed_gather, a fill and pe_qkv_fix_rmsnorm_rope. Replaces the
+ * embedding lookup (model.py:152) and model.py:175-193 for the first layer. */
+int pe_qkv_embed_rmsnorm_rope(const pe_qkv_args* args, int embed_type, const void* table,
+                              int64_t vocab, const int64_t* token, float* x_out, void* clear,
+                              int64_t clear_bytes, pe_stream_t stream);
+
 /* Decode attention of each kv group fused with the group's share of the o-projection, one
  * launch, no communication between workgroups. For kv head j with query heads
  * h = j*G .. j*G+G-1 (G = n_head / n_kv):

@@ -25,7 +25,7 @@ enum { kModePlain = 0, kModeSilu = 1, kModeArgmax = 2, kModeSiluSum = 3, kModeSi
        kModeSiluFix = 5 };
 // How a staging routine adds parts: not at all, from the early loads, loading them itself, or
 // one fixed-point vector from the early loads.
-enum { kSumNone = 0, kSumEarly = 1, kSumLate = 2, kSumFix = 3 };
+enum { kSumNone = 0, kSumEarly = 1, kSumLate = 2, kSumFix = 3, kSumEmbed = 4 };
 
 struct GemvArgs {
     Tiled w;
@@ -56,6 +56,12 @@ struct GemvArgs {
     // value is the sum over the replicas
     const int64_t* fix;
     int64_t fix_stride;
+    // kSumEmbed staging: the activation is row *embed_token of the raw GGUF table embed
+    // (embed_vocab rows of k elements of ggml type embed_type), NaN for an id outside it
+    const uint8_t* embed;
+    int embed_type;
+    int64_t embed_vocab;
+    const int64_t* embed_token;
 };
 
 // 2^-32 v for a 64-bit two's-complement fixed-point v (lo, hi words), rounded once to fp32:
@@ -414,6 +420,35 @@ struct ActLoads {
     uint2 poison[NR];           // fixed-point mode: the unrepresentable-value counts
 };
 
+// Elements e0 .. e0 + 3 (e0 % 4 == 0) of a raw GGUF table, bit-exact as raw_element: one
+// branch per format with all of its loads issued together (four raw_element calls, each with
+// its own format switch, made the loads wait for one another).
+PE_DEV float4 embed_quad(int type, const uint8_t* raw, int64_t e0) {
+    switch (type) {
+        case PE_TYPE_F32: {
+            const uint32_t* p = reinterpret_cast<const uint32_t*>(raw) + e0;
+            return make_float4(__uint_as_float(p[0]), __uint_as_float(p[1]), __uint_as_float(p[2]),
+                               __uint_as_float(p[3]));
+        }
+        case PE_TYPE_F16: {
+            const uint16_t* p = reinterpret_cast<const uint16_t*>(raw) + e0;
+            return make_float4(h2f(p[0]), h2f(p[1]), h2f(p[2]), h2f(p[3]));
+        }
+        case PE_TYPE_Q8_0: {
+            const uint8_t* b = raw + (e0 >> 5) * 34;
+            const uint8_t* q = b + 2 + (e0 & 31);
+            const uint32_t d16 = rd16(b);
+            const uint32_t q0 = q[0], q1 = q[1], q2 = q[2], q3 = q[3];
+            const float d = h2f(d16);
+            return make_float4((float)(int8_t)q0 * d, (float)(int8_t)q1 * d, (float)(int8_t)q2 * d,
+                               (float)(int8_t)q3 * d);
+        }
+        default:
+            return make_float4(raw_element(type, raw, e0), raw_element(type, raw, e0 + 1),
+                               raw_element(type, raw, e0 + 2), raw_element(type, raw, e0 + 3));
+    }
+}
+
 // Issue the float4 loads of x (and the RMSNorm weight) that this thread stages. Indices past
 // the vector are clamped to its last float4 (no branch around the load, which would make the
 // compiler wait for the data right there); finish_activation ignores them.
@@ -425,12 +460,29 @@ PE_DEV void issue_activation(const GemvArgs& a, int units, ActLoads<M4, NR>& L) 
 #pragma unroll
         for (int r = 0; r < NR; ++r) L.poison[r] = reinterpret_cast<const uint2*>(a.fix + r * a.fix_stride)[a.k];
     }
+    int64_t erow = 0;
+    bool eok = false;
+    if constexpr (SUM == kSumEmbed) {
+        erow = *a.embed_token;
+        eok = erow >= 0 && erow < a.embed_vocab;
+        erow = eok ? erow : 0;
+    }
 #pragma unroll
     for (int m = 0; m < M4; ++m) {
         const int i = (int)threadIdx.x + NT * m;
         if (NT * m < n4) {
             const int ic = i < n4 ? i : n4 - 1;
-            L.x[m] = reinterpret_cast<const float4*>(a.x)[ic];
+            if constexpr (SUM == kSumEmbed) {
+                // the float4 at ic holds elements 4 (ic % 8) + 32 (ic / 8) (natural) or
+                // 32 (ic % units) + 4 (ic / units) (unit-transposed) of the row
+                const bool ut = a.layout & PE_LAYOUT_X_UT;
+                const int64_t e0 = erow * a.k + (ut ? 32 * (ic % units) + 4 * (ic / units) : 4 * (int64_t)ic);
+                const float4 v = embed_quad(a.embed_type, a.embed, e0);
+                const float nan = __builtin_nanf("");
+                L.x[m] = eok ? v : make_float4(nan, nan, nan, nan);
+            } else {
+                L.x[m] = reinterpret_cast<const float4*>(a.x)[ic];
+            }
             if constexpr (NORM) L.w[m] = reinterpret_cast<const float4*>(a.norm_w)[ic];
             if constexpr (SUM == kSumFix) {
 #pragma unroll
@@ -547,6 +599,8 @@ PE_DEV float finish_activation(const GemvArgs& a, int glane, int units,
                 v.z += fix_replicas_to_float<NR>(lo[2], hi[2]);
                 v.w += fix_replicas_to_float<NR>(lo[3], hi[3]);
                 if (bad) v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+                if (a.x_sum && blockIdx.x == 0) reinterpret_cast<float4*>(a.x_sum)[i] = v;
+            } else if constexpr (SUM == kSumEmbed) {
                 if (a.x_sum && blockIdx.x == 0) reinterpret_cast<float4*>(a.x_sum)[i] = v;
             } else if constexpr (SUM != kSumNone) {
                 // x + parts[0] + parts[1] + ... in that order; late parts are all loaded before

@@ -142,6 +142,14 @@ struct QkvFixParams {
     const int64_t* acc;
     int64_t acc_stride;
     float* x_sum;
+    // embedding form (NR < 0): the activation is the embedding row of *token, and the blocks
+    // clear clear_n16 16-byte words at clear between them
+    const uint8_t* embed;
+    int embed_type;
+    int64_t embed_vocab;
+    const int64_t* token;
+    uint4* clear;
+    int64_t clear_n16;
 };
 
 template <int T, int GS, int SEG, int NR>
@@ -149,7 +157,7 @@ PE_DEV void qkv_task_fix(const QkvFixParams& P, int64_t task, int64_t ntask, int
                          float* stage) {
     constexpr int NT = kQkvFixThreads;
     constexpr int NRS = NR > 0 ? NR : 1;
-    constexpr int SUM = NR > 0 ? kSumFix : kSumNone;
+    constexpr int SUM = NR > 0 ? kSumFix : NR < 0 ? kSumEmbed : kSumNone;
     constexpr int M4 = act_loads<NT, GS, 1>();
     const pe_qkv_args& a = P.a;
     const int units = (int)(P.k >> 5);
@@ -173,12 +181,24 @@ PE_DEV void qkv_task_fix(const QkvFixParams& P, int64_t task, int64_t ntask, int
     ga.fix = P.acc;
     ga.fix_stride = P.acc_stride;
     ga.x_sum = P.x_sum;
+    ga.embed = P.embed;
+    ga.embed_type = P.embed_type;
+    ga.embed_vocab = P.embed_vocab;
+    ga.embed_token = P.token;
     ActLoads<M4, NRS> act;
-    issue_activation<NT, true, M4, SUM, NRS>(ga, units, act);
     typename Fmt<T>::Raw p, q;
     const int uc = glane < units ? glane : units - 1;
-    Fmt<T>::load(t, r1, uc, p);
-    Fmt<T>::load(t, r2, uc, q);
+    if constexpr (SUM == kSumEmbed) {
+        // the embedding row's loads depend on the token id (a scalar load): the weights go
+        // first, so that they are in flight while the id arrives
+        Fmt<T>::load(t, r1, uc, p);
+        Fmt<T>::load(t, r2, uc, q);
+        issue_activation<NT, true, M4, SUM, NRS>(ga, units, act);
+    } else {
+        issue_activation<NT, true, M4, SUM, NRS>(ga, units, act);
+        Fmt<T>::load(t, r1, uc, p);
+        Fmt<T>::load(t, r2, uc, q);
+    }
     const int64_t pos = *a.pos;
     const bool pos_ok = pos >= 0 && pos < a.capacity && pos < a.rope_rows;
     float b1 = 0.f, b2 = 0.f, c = 1.f, sn = 0.f;
@@ -194,6 +214,13 @@ PE_DEV void qkv_task_fix(const QkvFixParams& P, int64_t task, int64_t ntask, int
     float xr[1][32];
     UnitSums xs[1];
     const float rstd = finish_activation<NT, GS, 1, true, SUM, 0, NRS>(ga, glane, units, act, xr, xs, lds4, stage);
+    if constexpr (SUM == kSumEmbed) {
+        // this block's share of the words to clear, stored once the activation is staged (at
+        // kernel start the stores sat in the same counter as the loads the staging waits for)
+        const int64_t c0 = (int64_t)blockIdx.x * P.clear_n16 / gridDim.x;
+        const int64_t c1 = ((int64_t)blockIdx.x + 1) * P.clear_n16 / gridDim.x;
+        for (int64_t c = c0 + threadIdx.x; c < c1; c += NT) P.clear[c] = make_uint4(0u, 0u, 0u, 0u);
+    }
     float y1 = 0.f, y2 = 0.f;
     if (glane < units) {
         y1 = Fmt<T>::dot(p, xr[0], xs[0]);
@@ -285,10 +312,15 @@ extern "C" int pe_qkv_rmsnorm_rope(const pe_qkv_args* args, pe_stream_t stream) 
     return launch_status();
 }
 
-extern "C" int pe_qkv_fix_rmsnorm_rope(const pe_qkv_args* args, const int64_t* acc, int replicas,
-                                       int64_t acc_stride, float* x_sum, pe_stream_t stream) {
+namespace {
+
+// pe_qkv_fix_rmsnorm_rope (table == nullptr) and pe_qkv_embed_rmsnorm_rope (table != nullptr).
+int qkv_fix_impl(const pe_qkv_args* args, const int64_t* acc, int replicas, int64_t acc_stride, float* x_sum,
+                 int embed_type, const void* table, int64_t vocab, const int64_t* token, void* clear,
+                 int64_t clear_bytes, pe_stream_t stream) {
     if (!args) return PE_ERR_NULL;
     const pe_qkv_args& a = *args;
+    const bool emb = table != nullptr;
     const int types[3] = {a.type_q, a.type_k, a.type_v};
     const void* ws[3] = {a.w_q, a.w_k, a.w_v};
     for (int i = 0; i < 3; ++i) {
@@ -305,8 +337,17 @@ extern "C" int pe_qkv_fix_rmsnorm_rope(const pe_qkv_args* args, const int64_t* a
     if (!(replicas == 0 || replicas == 4)) return PE_ERR_SHAPE;
     if (replicas && (acc_stride < a.hidden + 1 || acc_stride % 2)) return PE_ERR_SHAPE;
     if (a.layout & ~PE_LAYOUT_X_UT) return PE_ERR_TYPE;
-    if (!a.x || !a.norm_w || !a.cos_tab || !a.sin_tab || !a.pos || !a.q_out || !a.k_cache || !a.v_cache ||
-        (replicas && !acc))
+    if (emb) {
+        if (embed_type != PE_TYPE_F32 && embed_type != PE_TYPE_F16 && embed_type != PE_TYPE_Q8_0 &&
+            embed_type != PE_TYPE_Q5_0 && embed_type != PE_TYPE_Q4_K && embed_type != PE_TYPE_Q6_K)
+            return PE_ERR_TYPE;
+        if (vocab <= 0 || a.hidden % block_elems(embed_type) || clear_bytes < 0 || clear_bytes % 16)
+            return PE_ERR_SHAPE;
+        if (!token || !x_sum || (clear_bytes && !clear)) return PE_ERR_NULL;
+        if (!aligned(token, 8) || !aligned(clear, 16)) return PE_ERR_ALIGN;
+    }
+    if ((!emb && !a.x) || !a.norm_w || !a.cos_tab || !a.sin_tab || !a.pos || !a.q_out || !a.k_cache ||
+        !a.v_cache || (replicas && !acc))
         return PE_ERR_NULL;
     if (!aligned(a.x, 16) || !aligned(a.norm_w, 16) || !aligned(a.pos, 8) || !aligned(a.q_out, 4) ||
         !aligned(a.k_cache, 4) || !aligned(a.v_cache, 4) || !aligned(a.b_q, 4) ||
@@ -317,16 +358,33 @@ extern "C" int pe_qkv_fix_rmsnorm_rope(const pe_qkv_args* args, const int64_t* a
     const int64_t tq = (int64_t)a.n_head * (a.head_dim / 2), tk = (int64_t)a.n_kv * (a.head_dim / 2);
     const int64_t blocks = (tq + gpb - 1) / gpb + 2 * ((tk + gpb - 1) / gpb);
     if (blocks > 65535) return PE_ERR_SHAPE;
-    QkvFixParams P{a, a.hidden, replicas ? acc : nullptr, replicas ? acc_stride : 0, x_sum};
+    QkvFixParams P{a, a.hidden, replicas ? acc : nullptr, replicas ? acc_stride : 0, x_sum,
+                   (const uint8_t*)table, embed_type, vocab, token, (uint4*)clear, clear_bytes / 16};
     const size_t lds = (size_t)(a.hidden / 32) * kUnitStride * 4;
     hipStream_t s = (hipStream_t)stream;
     const dim3 g((unsigned)blocks), bl(kQkvFixThreads);
     if (gs == 32) {
-        if (replicas) hipLaunchKernelGGL((k_qkv_fix<32, 4>), g, bl, lds, s, P);
+        if (emb) hipLaunchKernelGGL((k_qkv_fix<32, -1>), g, bl, lds, s, P);
+        else if (replicas) hipLaunchKernelGGL((k_qkv_fix<32, 4>), g, bl, lds, s, P);
         else hipLaunchKernelGGL((k_qkv_fix<32, 0>), g, bl, lds, s, P);
     } else {
-        if (replicas) hipLaunchKernelGGL((k_qkv_fix<64, 4>), g, bl, lds, s, P);
+        if (emb) hipLaunchKernelGGL((k_qkv_fix<64, -1>), g, bl, lds, s, P);
+        else if (replicas) hipLaunchKernelGGL((k_qkv_fix<64, 4>), g, bl, lds, s, P);
         else hipLaunchKernelGGL((k_qkv_fix<64, 0>), g, bl, lds, s, P);
     }
     return launch_status();
+}
+
+}  // namespace
+
+extern "C" int pe_qkv_fix_rmsnorm_rope(const pe_qkv_args* args, const int64_t* acc, int replicas,
+                                       int64_t acc_stride, float* x_sum, pe_stream_t stream) {
+    return qkv_fix_impl(args, acc, replicas, acc_stride, x_sum, 0, nullptr, 0, nullptr, nullptr, 0, stream);
+}
+
+extern "C" int pe_qkv_embed_rmsnorm_rope(const pe_qkv_args* args, int embed_type, const void* table, int64_t vocab,
+                                         const int64_t* token, float* x_out, void* clear, int64_t clear_bytes,
+                                         pe_stream_t stream) {
+    if (!table) return PE_ERR_NULL;
+    return qkv_fix_impl(args, nullptr, 0, 0, x_out, embed_type, table, vocab, token, clear, clear_bytes, stream);
 }

@@ -161,6 +161,7 @@ _SIGNATURES = {
     "pe_ffn_fix_bound": (_F, [_L]),
     "pe_ffn_fix": (_I, [ctypes.POINTER(FfnFixArgs), _P]),
     "pe_qkv_fix_rmsnorm_rope": (_I, [ctypes.POINTER(QkvArgs), _P, _I, _L, _P, _P]),
+    "pe_qkv_embed_rmsnorm_rope": (_I, [ctypes.POINTER(QkvArgs), _I, _P, _L, _P, _P, _P, _L, _P]),
 }
 
 # Every symbol include/pico_hip.h declares (checked by tests/test_abi.py).

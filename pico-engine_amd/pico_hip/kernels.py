@@ -25,7 +25,7 @@ import torch
 
 from ._lib import (LAYOUT_NATURAL, LAYOUT_X_UT, LAYOUT_Y_UT, AttnOprojArgs, FfnFixArgs, QkvArgs, StepArgs,
                    StepLayer, check, lib)
-from .dequant import (BLOCK_SIZE, GGML_Q4_K, GGML_Q5_0, GGML_Q6_K, GGML_Q8_0, MATRIX_TYPES,
+from .dequant import (BLOCK_SIZE, GGML_F16, GGML_F32, GGML_Q4_K, GGML_Q5_0, GGML_Q6_K, GGML_Q8_0, MATRIX_TYPES,
                       QUANT_TYPES, TYPE_NAMES, nbytes_for)
 
 _VP = ctypes.c_void_p
@@ -1052,6 +1052,56 @@ def qkv_fix_rmsnorm_rope(x: torch.Tensor, acc: torch.Tensor | None, norm_w: torc
     return out, x_sum
 
 
+# embedding table formats the first-layer QKV launch decodes itself (pe_qkv_embed_rmsnorm_rope)
+EMBED_QKV_TYPES = (GGML_F32, GGML_F16, GGML_Q8_0, GGML_Q5_0, GGML_Q4_K, GGML_Q6_K)
+
+
+def qkv_embed_rmsnorm_rope(table: RawTensor, token: torch.Tensor, norm_w: torch.Tensor, eps: float,
+                           wq: QWeight, wk: QWeight, wv: QWeight,
+                           bq: torch.Tensor | None, bk: torch.Tensor | None, bv: torch.Tensor | None,
+                           cos_tab: torch.Tensor, sin_tab: torch.Tensor, pos: torch.Tensor,
+                           k_cache: torch.Tensor, v_cache: torch.Tensor, n_head: int,
+                           x_out: torch.Tensor, clear: torch.Tensor | None = None,
+                           out: torch.Tensor | None = None,
+                           layout: int = LAYOUT_NATURAL) -> torch.Tensor:
+    """qkv_fix_rmsnorm_rope (no replicas) of the embedding row of ``token`` (a device int64
+    scalar): the row is decoded into ``x_out`` (the residual stream, in ``layout``) and
+    ``clear`` (a contiguous tensor of whole 16-byte words, e.g. the step's fixed-point
+    accumulators) is zeroed, in the same launch (pe_qkv_embed_rmsnorm_rope). Returns q."""
+    dev = _on_gpu(table.data, token, norm_w, wq.data, wk.data, wv.data, pos, k_cache, v_cache, x_out)
+    vocab, hidden = table.shape
+    need = nbytes_for(table.ggml_type, vocab * hidden)
+    if table.data.numel() * table.data.element_size() < need:
+        raise ValueError(f"embedding table holds fewer than {need} bytes")
+    n_kv, capacity, hd = k_cache.shape
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("KV caches must be contiguous (n_kv, capacity, hd) buffers")
+    if pos.dtype != torch.int64 or token.dtype != torch.int64:
+        raise ValueError("pos and token must be int64 device tensors")
+    if x_out.dtype != torch.float32 or not x_out.is_contiguous() or x_out.numel() != hidden:
+        raise ValueError("x_out must be a contiguous float32 vector of the hidden size")
+    nbytes = 0
+    if clear is not None:
+        if not clear.is_contiguous():
+            raise ValueError("clear must be contiguous")
+        nbytes = clear.numel() * clear.element_size()
+    nw = _f32c(norm_w.reshape(-1))
+    if out is None:
+        out = torch.empty(n_head, hd, device=dev, dtype=torch.float32)
+    a = QkvArgs(wq.ggml_type, wk.ggml_type, wv.ggml_type,
+                wq.data.data_ptr(), wk.data.data_ptr(), wv.data.data_ptr(),
+                None if bq is None else bq.data_ptr(), None if bk is None else bk.data_ptr(),
+                None if bv is None else bv.data_ptr(),
+                None, nw.data_ptr(), float(eps),
+                cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0],
+                pos.data_ptr(), out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                capacity, wq.k, n_head, n_kv, hd, layout)
+    check(lib.pe_qkv_embed_rmsnorm_rope(ctypes.byref(a), table.ggml_type, _ptr(table.data), vocab,
+                                        _ptr(token), _ptr(x_out), _ptr(clear), nbytes, _stream(dev)),
+          "pe_qkv_embed_rmsnorm_rope")
+    return out
+
+
 # ---- prefill (M >= 1) --------------------------------------------------------------------
 
 def qgemm(x: torch.Tensor, w: QWeight, bias: torch.Tensor | None = None,
@@ -1207,7 +1257,7 @@ __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "
            "q8_0_gemv", "q5_0_gemv", "q5_0_gemv_norm", "q6_k_gemv", "q4_k_gemv", "qgemv_norm",
            "qgemv_norm_silu", "qkv_rmsnorm_rope", "qgemv_sum_norm_silu", "qgemm", "kv_write", "prefill_attn",
            "gemm_lt", "gemm_lt_workspace", "mgemv", "repack_mfma", "mfma_eligible", "MFMA_MIN_WEIGHTS",
-           "repack_mfma_pairs", "mqkv_eligible", "mqkv_ok", "MQKV_MAX_HIDDEN",
+           "repack_mfma_pairs", "mqkv_eligible", "mqkv_ok", "MQKV_MAX_HIDDEN", "qkv_embed_rmsnorm_rope", "EMBED_QKV_TYPES",
            "attn_gproj", "attn_gproj_supported", "attn_oproj_fix", "attn_oproj_supported", "fix_acc",
            "repack_oproj", "oproj_eligible", "qgemv_fix_norm_silu", "qgemv_norm_argmax", "dequantize_weight_f16",
            "repack_down_slices", "down_slice_eligible", "ffn_fix", "ffn_fix_supported", "ffn_fix_bound",

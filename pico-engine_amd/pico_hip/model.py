@@ -7,15 +7,17 @@ config 0 in a same-box A/B, 2062 vs 2025 tok/s, but it needs every workgroup res
 and raises if a bounded wait runs out), a greedy decode step of a model the persistent kernel
 covers (head_dim 64, hidden <= 1024, ffn <= 8192, caches up to 128 positions: the 0.5B
 family) is one launch, pe_decode_step. Otherwise decode (one token) runs three launches per
-layer plus the embedding row and the LM head (the 0.5B family):
+layer plus the LM head (the 0.5B family):
 
-  embed_gather                              model.py:152 (Q8_0 row, bit-exact)
-  fill of the fixed-point accumulators (once per token, every layer)
   per layer:
     qkv_fix_rmsnorm_rope (x + 2^-32 sum of the previous   model.py:175-193, :234
                         layer's FFN replicas, norm, QKV +
                         bias, RoPE, cache write; the first
-                        layer: qkv_rmsnorm_rope over x)
+                        layer: qkv_embed_rmsnorm_rope, which   model.py:152
+                        decodes the token's embedding row
+                        (bit-exact) as x, stores it and
+                        clears the step's fixed-point
+                        accumulators)
     attn_oproj_fix     (GQA attention per query head,     model.py:211-213
                         fp16-rounded, times that head's
                         columns of Wo, added in 64-bit
@@ -134,6 +136,11 @@ class Transformer:
         # the next layer's QKV launch reads), where every such layer qualifies (ffn_fix_ok)
         self.use_ffn_fix = True
         self._acc_block: torch.Tensor | None = None
+        # with ffn_fix: the token's embedding row decoded by the first layer's QKV launch, which
+        # also clears the step's fixed-point accumulators (qkv_embed_rmsnorm_rope), in place of
+        # an embedding-gather launch and a fill
+        self.use_embed_qkv = True
+        self._x0: torch.Tensor | None = None
         # attention of each kv group fused with its share of the o-projection (attn_gproj),
         # the shares added by the gate/up GEMV: four launches per layer instead of five
         self.use_attn_gproj = True
@@ -314,17 +321,32 @@ class Transformer:
         if pos.dtype != torch.int64:
             pos = pos.to(torch.int64)
         capacity = cache[0][0].shape[1]
-        x = K.embed_gather(self.embed, token_ids, layout=YU).reshape(-1)
         if self.ffn_fix_ok(capacity):
             if self._acc_block is None:
                 self._acc_block = K.fix_acc_block(cfg.hidden, self.device, cfg.n_layers)
             acc = self._acc_block
-            acc.zero_()   # a fill kernel (graph-capturable), once per token for every layer
+            embed_first = self.use_embed_qkv and token_ids.numel() == 1 and \
+                self.embed.ggml_type in K.EMBED_QKV_TYPES
+            if embed_first:
+                if self._x0 is None:
+                    self._x0 = torch.empty(cfg.hidden, device=self.device, dtype=torch.float32)
+                x = self._x0
+                tok = token_ids.reshape(-1)[:1]
+                if tok.dtype != torch.int64:
+                    tok = tok.to(torch.int64)
+            else:
+                x = K.embed_gather(self.embed, token_ids, layout=YU).reshape(-1)
+                acc.zero_()   # a fill kernel (graph-capturable), once per token for every layer
             last = len(self.layers) - 1
             d_acc = None   # the previous layer's down-product replicas
             for i, L in enumerate(self.layers):
                 k_buf, v_buf = cache[i]
-                if d_acc is None:
+                if i == 0 and embed_first:
+                    # x = the token's embedding row (stored into x), the accumulators cleared
+                    q = K.qkv_embed_rmsnorm_rope(self.embed, tok, L.attn_norm_ut, cfg.eps, L.wq, L.wk, L.wv,
+                                                 L.bq, L.bk, L.bv, self.cos, self.sin, pos, k_buf, v_buf,
+                                                 cfg.n_head, x_out=x, clear=acc, layout=XU)
+                elif d_acc is None:
                     q = K.qkv_rmsnorm_rope(x, L.attn_norm_ut, cfg.eps, L.wq, L.wk, L.wv, L.bq, L.bk,
                                            L.bv, self.cos, self.sin, pos, k_buf, v_buf, cfg.n_head,
                                            layout=XU)
@@ -342,6 +364,7 @@ class Transformer:
                                                    layout=XU | YU)
                     x = K.qgemv(act, L.w_down, residual=x, layout=XU | YU)
             return self._lm_head(x, self.output_norm_ut, greedy, XU)
+        x = K.embed_gather(self.embed, token_ids, layout=YU).reshape(-1)
         if self.attn_oproj_ok(capacity):
             if self._acc is None:
                 self._acc = K.fix_acc(cfg.hidden, self.device, cfg.n_layers)

@@ -130,6 +130,28 @@ def test_mqkv_argument_errors(lib):
     assert lib.pe_repack_mfma_pairs(6, P(f), P(f), 64, 256, 64, None) == 3    # no MFMA layout
 
 
+def test_qkv_embed_argument_errors(lib):
+    """pe_qkv_embed_rmsnorm_rope rejects bad embedding and clear arguments before any launch."""
+    from pico_hip._lib import QkvArgs
+    f = 0x1000
+    a = ctypes.byref(QkvArgs(6, 6, 8, f, f, f, None, None, None, None, f, 1e-6, f, f, 64, f, f, f, f, 40,
+                             896, 14, 2, 64, 1))
+    P = ctypes.c_void_p
+    call = lambda et=8, table=f, vocab=100, tok=f, xo=f, clr=f, nb=4096: lib.pe_qkv_embed_rmsnorm_rope(
+        a, et, P(table) if table else None, vocab, P(tok) if tok else None, P(xo) if xo else None,
+        P(clr) if clr else None, nb, None)
+    assert call(et=15) == 2            # Q8_K is not an embedding format here
+    assert call(et=12) == 3            # Q4_K rows need hidden % 256 == 0
+    assert call(vocab=0) == 3
+    assert call(nb=4100) == 3          # whole 16-byte words
+    assert call(table=0) == 1
+    assert call(tok=0) == 1
+    assert call(xo=0) == 1             # the embedding row is stored for the residual
+    assert call(clr=0) == 1            # a clear range needs a pointer
+    assert call(clr=0x1008) == 4       # 16-byte aligned
+    assert call(tok=0x1004) == 4
+
+
 def test_qkv_args_struct_matches_header():
     """ctypes mirror of pe_qkv_args has the header's fields in the header's order."""
     from pico_hip._lib import QkvArgs

@@ -323,3 +323,50 @@ def test_abi_rejects_bad_ffn_fix_arguments(K):
     assert call(acc_out=None) == 1
     assert call(x=x.data_ptr() + 4) == 4
     torch.cuda.synchronize()
+
+
+# ---- the first layer's QKV launch over the token's embedding row ---------------------------
+
+@pytest.mark.parametrize("t,et,hidden,nh,nkv,vocab", [(dq.Q5_0, dq.Q8_0, 896, 14, 2, 300),
+                                                      (dq.Q8_0, dq.F16, 896, 14, 2, 100),
+                                                      (dq.Q4_K, dq.Q4_K, 512, 8, 2, 64),
+                                                      (dq.Q6_K, dq.Q6_K, 2048, 16, 4, 40)])
+def test_qkv_embed_matches_gather_then_staged_qkv(K, t, et, hidden, nh, nkv, vocab):
+    """pe_qkv_embed_rmsnorm_rope == pe_embed_gather followed by the staged launch over that
+    row (the same bits: the same decode and the same staged arithmetic), x_out == the gathered
+    row, and the clear range zeroed (the words after it untouched)."""
+    hd, cap, pos = 64, 40, 29
+    rows = (nh * hd, nkv * hd, nkv * hd)
+    raws = [quantized_normal(t, r, hidden, seed=hidden + i) for i, r in enumerate(rows)]
+    ws = [K.pack_weight(dev_bytes(raw), t, r, hidden) for raw, r in zip(raws, rows)]
+    rng = np.random.default_rng(hidden)
+    traw = ((rng.standard_normal(vocab * hidden) * 0.02).astype(np.float16).tobytes() if et == dq.F16
+            else random_quant(et, vocab, hidden, seed=hidden))
+    table = K.RawTensor(dev_bytes(traw), et, (vocab, hidden))
+    bs = [T(rng.standard_normal(r).astype(np.float32) * 0.1) for r in rows]
+    nw = K.to_ut(T(rng.standard_normal(hidden).astype(np.float32)))
+    inv = 1.0 / (1e6 ** (np.arange(0, hd, 2) / hd))
+    ang = (np.arange(64)[:, None] * inv[None, :]).astype(np.float32)
+    cos, sin = T(np.cos(ang).astype(np.float32)), T(np.sin(ang).astype(np.float32))
+    UT = K.LAYOUT_X_UT
+    tok = torch.tensor([vocab - 3], device=DEV)
+    pos_t = torch.tensor([pos], device=DEV)
+    clear = torch.full((3, 4, K.fix_stride(hidden)), -7, dtype=torch.int64, device=DEV)
+    guard = torch.full((64,), 5, dtype=torch.int64, device=DEV)
+    block = torch.cat([clear.reshape(-1), guard])   # the clear range, then words it must not touch
+    xo = torch.empty(hidden, device=DEV)
+    kc, vc = torch.zeros(nkv, cap, hd, device=DEV), torch.zeros(nkv, cap, hd, device=DEV)
+    q = K.qkv_embed_rmsnorm_rope(table, tok, nw, 1e-6, *ws, *bs, cos, sin, pos_t, kc, vc, nh, x_out=xo,
+                                 clear=block[:clear.numel()], layout=UT)
+    row = K.embed_gather(table, tok, layout=K.LAYOUT_Y_UT).reshape(-1)
+    kc2, vc2 = torch.zeros_like(kc), torch.zeros_like(vc)
+    q2, _ = K.qkv_fix_rmsnorm_rope(row, None, nw, 1e-6, *ws, *bs, cos, sin, pos_t, kc2, vc2, nh, layout=UT)
+    assert torch.equal(xo, row)
+    assert torch.equal(q, q2) and torch.equal(kc, kc2) and torch.equal(vc, vc2)
+    assert not block[:clear.numel()].any()
+    assert (block[clear.numel():] == 5).all()
+    # an id outside the table: NaN activation (as pe_embed_gather gives)
+    bad = torch.tensor([vocab], device=DEV)
+    q3 = K.qkv_embed_rmsnorm_rope(table, bad, nw, 1e-6, *ws, *bs, cos, sin, pos_t, kc, vc, nh, x_out=xo,
+                                  layout=UT)
+    assert torch.isnan(xo).all() and torch.isnan(q3).all()
