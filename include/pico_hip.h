@@ -612,6 +612,12 @@ int pe_rope(const float* x, int64_t x_stride, const float* cos_rows, const float
 int pe_silu_mul(const float* gate_up, int64_t gu_stride, float* out, int64_t out_stride,
                 int64_t L, int64_t ffn, pe_stream_t stream);
 
+/* x = fp16(x) in place (round to nearest even, overflow to infinity, stored as fp32) over
+ * rows x cols floats with a row stride (elements). The rounding points of the prefill under
+ * CUDA fp16 autocast (model.py:147-151): every F.linear / addmm / matmul result and every
+ * Triton kernel output whose input is fp16 holds fp16 values there. */
+int pe_round_f16(float* x, int64_t rows, int64_t cols, int64_t stride, pe_stream_t stream);
+
 /* y[m][n] = sum_k W[n][k] x[m][k] (+ bias[n]) (+ residual[m][n]) for m < M, a tiled W.
  * Row strides in elements. residual may alias y. Replaces the prefill F.linear/addmm/matmul
  * on fp32-dequantized weights (model.py:177, :213, :223, :235). */

@@ -22,6 +22,8 @@ reference's own CPU formulations:
 * gate/up, down at L>1            fp32 matmul on dequantized W (model.py:223, :235)
 * LM head                         q8_0 form on the last row (model.py:160-164)
 * greedy                          argmax (sampler.py:26-27)
+* ``autocast=True``               the prefill under CUDA fp16 autocast (model.py:147-151):
+                                  fp16 roundings where the reference's GPU path rounds
 
 Pinned by tests/test_oracle_model.py: against float64 closed forms (tests/../oracle/closed.py)
 op by op, and the whole forward against an independent float64 numpy forward on a small model.
@@ -146,6 +148,26 @@ def gemv_cpu(entry, x, bias=None, residual=None):
     return acc
 
 
+def f16(t):
+    """Round to fp16 (nearest even) and back to fp32: the value an fp16 tensor holds."""
+    return t.half().float()
+
+
+def flash16_causal(q, k, v, group):
+    """Causal GQA attention the way an fp16 flash-attention kernel computes it (SDPA under
+    CUDA autocast, model.py:201-209): fp16 q, K, V; scores and softmax statistics in fp32; the
+    probabilities rounded to fp16 for the P.V product (fp32 accumulation); the output divided
+    by the fp32 sum and rounded to fp16. q (L, nh, hd), k / v (nkv, L, hd) -> (L, nh * hd)."""
+    L, nh, hd = q.shape
+    kr = k.repeat_interleave(group, dim=0)                          # (nh, L, hd)
+    vr = v.repeat_interleave(group, dim=0)
+    s = torch.einsum("lhd,hsd->hls", q, kr) * (hd ** -0.5)          # (nh, L, L)
+    s = s.masked_fill(torch.ones(L, L, dtype=torch.bool).triu(1), float("-inf"))
+    p = torch.exp(s - s.amax(-1, keepdim=True))
+    o = torch.einsum("hls,hsd->hld", f16(p), vr) / p.sum(-1, keepdim=True)
+    return f16(o).transpose(0, 1).reshape(L, nh * hd)
+
+
 def rmsnorm_cpu(x, w, eps):
     """model.py:292-295."""
     var = (x * x).mean(-1, keepdim=True)
@@ -237,34 +259,65 @@ class RefModel:
         return [(z(), z()) for _ in range(c.n_layers)]
 
     @torch.inference_mode()
-    def forward(self, ids: torch.Tensor, positions: torch.Tensor, cache) -> torch.Tensor:
+    def forward(self, ids: torch.Tensor, positions: torch.Tensor, cache,
+                autocast: bool = False, return_hidden: bool = False):
+        """``autocast`` restates the reference's prefill on CUDA (L > 1 runs under fp16
+        autocast, model.py:147-151): F.linear, addmm and matmul take fp16 operands (fp32 weights,
+        activations and biases rounded to fp16) and return fp16 (fp32 accumulation, one rounding
+        of the result); SDPA runs on fp16 q, K, V (flash16_causal); the Triton RMSNorm, RoPE and
+        SiLU kernels compute in fp32 and store in their input's dtype (kernels.py:22, :46-47,
+        :74), so from the first o-projection on the residual stream is fp16 and the KV cache
+        holds fp16 values; the Q8_0 LM head reads its input as fp32 (kernels.py:180). Decode
+        (L == 1) is unaffected. ``return_hidden``: (logits, the normed last row the LM head
+        multiplies)."""
         c = self.cfg
         L = ids.shape[0]
+        ac = autocast and L > 1
         x = self.w["token_embd.weight"][ids]
         cos, sin = self.cos[positions], self.sin[positions]
         for i in range(c.n_layers):
-            x = self._layer(i, x, positions, cos, sin, cache[i])
+            x = self._layer(i, x, positions, cos, sin, cache[i], ac)
         h = rmsnorm_cpu(x, self.w["output_norm.weight"], c.eps)
+        if ac:
+            h = f16(h)
         if "output" in self.q:
-            return gemv_cpu(self.q["output"], h[-1])
-        # model.py:163-164; a file without output.weight ties the head to token_embd (the
-        # reference requires the tensor; this is the usual GGUF convention for tied models)
-        return h[-1] @ self.w.get("output.weight", self.w["token_embd.weight"]).T
+            logits = gemv_cpu(self.q["output"], h[-1])
+        else:
+            # model.py:163-164; a file without output.weight ties the head to token_embd (the
+            # reference requires the tensor; this is the usual GGUF convention for tied models)
+            w = self.w.get("output.weight", self.w["token_embd.weight"])
+            logits = f16(h[-1] @ f16(w).T) if ac else h[-1] @ w.T
+        return (logits, h[-1]) if return_hidden else logits
 
-    def _layer(self, i, x, positions, cos, sin, cache):
+    def _layer(self, i, x, positions, cos, sin, cache, ac=False):
         c = self.cfg
         p = f"blk.{i}."
         L = x.shape[0]
         hd, nh, nkv = c.head_dim, c.n_head, c.n_kv
         k_buf, v_buf = cache
         h = rmsnorm_cpu(x, self.w[p + "attn_norm.weight"], c.eps)
-        qkv = F.linear(h, self.qkv_w[i], self.qkv_b[i])
+        if ac:
+            qkv = f16(F.linear(f16(h), f16(self.qkv_w[i]), f16(self.qkv_b[i])))
+        else:
+            qkv = F.linear(h, self.qkv_w[i], self.qkv_b[i])
         q = qkv[:, :nh * hd].view(L, nh, hd)
         k = qkv[:, nh * hd:(nh + nkv) * hd].view(L, nkv, hd)
         v = qkv[:, (nh + nkv) * hd:].view(L, nkv, hd)
         q = rope_cpu(q, cos[:, None, :], sin[:, None, :])
         k = rope_cpu(k, cos[:, None, :], sin[:, None, :])
+        if ac:
+            q, k = f16(q), f16(k)
         group = nh // nkv
+        if ac:
+            k_buf[:, :L] = k.transpose(0, 1)
+            v_buf[:, :L] = v.transpose(0, 1)
+            out = flash16_causal(q, k_buf[:, :L], v_buf[:, :L], group)
+            x = f16(torch.addmm(f16(x), out, f16(self.w[p + "attn_output.weight"]).T))
+            hn = f16(rmsnorm_cpu(x, self.w[p + "ffn_norm.weight"], c.eps))
+            gate_up = f16(hn @ f16(self.gu_w[i]).T)
+            g, u = gate_up[:, :c.ffn], gate_up[:, c.ffn:]
+            act = f16(g * torch.sigmoid(g) * u)
+            return f16(torch.addmm(x, act, f16(self.w[p + "ffn_down.weight"]).T))
         if L == 1:
             pos = int(positions[0])
             k_buf[:, pos] = k[0]

@@ -66,6 +66,17 @@ __global__ void k_silu_mul(const float* __restrict__ gu, int64_t gs, float* __re
     }
 }
 
+// x = fp16(x) (round to nearest even, overflow to infinity) in place over rows x cols with a
+// row stride.
+__global__ void k_round_f16(float* __restrict__ x, int64_t rows, int64_t cols, int64_t stride) {
+    const int64_t total = rows * cols;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += step) {
+        float* p = x + (idx / cols) * stride + idx % cols;
+        *p = round_to_f16(*p);
+    }
+}
+
 __global__ void k_kv_write(const float* __restrict__ ks, const float* __restrict__ vs, int64_t ss,
                            int n_kv, int hd, int64_t L, int64_t pos0, float* kc, float* vc,
                            int64_t cap) {
@@ -229,6 +240,16 @@ extern "C" int pe_silu_mul(const float* gate_up, int64_t gu_stride, float* out, 
     if (!aligned(gate_up, 4) || !aligned(out, 4)) return PE_ERR_ALIGN;
     hipLaunchKernelGGL(k_silu_mul, dim3(grid1d(L * ffn)), dim3(256), 0, (hipStream_t)stream,
                        gate_up, gu_stride, out, out_stride, L, ffn);
+    return launch_status();
+}
+
+extern "C" int pe_round_f16(float* x, int64_t rows, int64_t cols, int64_t stride, pe_stream_t stream) {
+    if (rows < 0 || cols < 0 || (rows > 1 && stride < cols)) return PE_ERR_SHAPE;
+    if (rows == 0 || cols == 0) return PE_OK;
+    if (!x) return PE_ERR_NULL;
+    if (!aligned(x, 4)) return PE_ERR_ALIGN;
+    hipLaunchKernelGGL(k_round_f16, dim3(grid1d(rows * cols)), dim3(256), 0, (hipStream_t)stream, x, rows,
+                       cols, stride);
     return launch_status();
 }
 

@@ -143,6 +143,7 @@ _SIGNATURES = {
     "pe_rmsnorm_h16": (_I, [_P, _L, _P, _P, _L, _L, _L, _F, _P]),
     "pe_rope": (_I, [_P, _L, _P, _P, _P, _L, _L, _I, _I, _P]),
     "pe_silu_mul": (_I, [_P, _L, _P, _L, _L, _L, _P]),
+    "pe_round_f16": (_I, [_P, _L, _L, _L, _P]),
     "pe_qgemm": (_I, [_I, _P, _L, _L, _P, _L, _L, _P, _P, _L, _P, _L, _P]),
     "pe_kv_write": (_I, [_P, _P, _L, _I, _I, _L, _L, _P, _P, _L, _P]),
     "pe_rope_kv_write": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _P, _P, _P, _L, _P]),

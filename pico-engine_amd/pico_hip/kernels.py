@@ -463,6 +463,20 @@ def silu_mul(gate_up: torch.Tensor, ffn: int) -> torch.Tensor:
     return out
 
 
+def round_f16_(x: torch.Tensor) -> torch.Tensor:
+    """x = fp16(x) in place (round to nearest even, stored as fp32; pe_round_f16) for a float32
+    tensor whose last dim is contiguous (rows of the leading dims with any row stride)."""
+    _on_gpu(x)
+    if x.dtype != torch.float32 or x.stride(-1) != 1:
+        raise ValueError("round_f16_ needs a float32 tensor with a contiguous last dim")
+    v = x if x.dim() == 2 else x.reshape(-1, x.shape[-1]) if x.is_contiguous() else None
+    if v is None:
+        raise ValueError("round_f16_ needs 2-D rows (or a contiguous tensor)")
+    check(lib.pe_round_f16(_ptr(v), v.shape[0], v.shape[1], v.stride(0) if v.shape[0] > 1 else v.shape[1],
+                           _stream(x.device)), "pe_round_f16")
+    return x
+
+
 def decode_attn_workspace(n_head: int, n_kv: int, hd: int, capacity: int, device) -> torch.Tensor:
     """Zero-filled workspace for decode_attn (reusable by any number of in-order calls)."""
     nbytes = lib.pe_decode_attn_workspace_bytes(n_head, n_kv, hd, capacity)
@@ -1257,7 +1271,7 @@ __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "
            "q8_0_gemv", "q5_0_gemv", "q5_0_gemv_norm", "q6_k_gemv", "q4_k_gemv", "qgemv_norm",
            "qgemv_norm_silu", "qkv_rmsnorm_rope", "qgemv_sum_norm_silu", "qgemm", "kv_write", "prefill_attn",
            "gemm_lt", "gemm_lt_workspace", "mgemv", "repack_mfma", "mfma_eligible", "MFMA_MIN_WEIGHTS",
-           "repack_mfma_pairs", "mqkv_eligible", "mqkv_ok", "MQKV_MAX_HIDDEN", "qkv_embed_rmsnorm_rope", "EMBED_QKV_TYPES",
+           "repack_mfma_pairs", "mqkv_eligible", "mqkv_ok", "MQKV_MAX_HIDDEN", "qkv_embed_rmsnorm_rope", "EMBED_QKV_TYPES", "round_f16_",
            "attn_gproj", "attn_gproj_supported", "attn_oproj_fix", "attn_oproj_supported", "fix_acc",
            "repack_oproj", "oproj_eligible", "qgemv_fix_norm_silu", "qgemv_norm_argmax", "dequantize_weight_f16",
            "repack_down_slices", "down_slice_eligible", "ffn_fix", "ffn_fix_supported", "ffn_fix_bound",

@@ -155,6 +155,10 @@ class Transformer:
         # operands, fp32 accumulation: the reference's CUDA autocast prefill, model.py:147-151);
         # shorter ones by the fp32 path (the reference's off-CUDA numerics). None: never.
         self.prefill_f16_min_tokens: int | None = 512
+        # prefills (L > 1) with the reference's GPU numerics instead: every product's operands
+        # and result, the norms, RoPE, attention and SiLU outputs and the residual stream held in
+        # fp16 where CUDA fp16 autocast holds them (model.py:147-151; _prefill_autocast)
+        self.prefill_autocast = False
         # the matrix-core prefill's plain products (QKV + bias, o-proj and ffn_down + residual)
         # on hipBLASLt; off: every product on this library's MFMA GEMM (pe_gemm_f16)
         self.prefill_blaslt = True
@@ -215,6 +219,8 @@ class Transformer:
         (token_ids/positions may then be its ``token``/``pos`` views)."""
         if token_ids.shape[0] == 1:
             return self._decode(token_ids, positions, cache, greedy)
+        if self.prefill_autocast:
+            return self._prefill_autocast(token_ids, positions, cache, greedy)
         m = self.prefill_f16_min_tokens
         if m is not None and token_ids.shape[0] >= m:
             return self._prefill_f16(token_ids, positions, cache, greedy)
@@ -469,6 +475,68 @@ class Transformer:
             else:
                 x = K.gemm_f16(act, W["down"], residual=x)
         return self._lm_head(x[-1], self.w["output_norm.weight"], greedy, K.LAYOUT_NATURAL)
+
+    def _prefill_autocast(self, token_ids, positions, cache, greedy=None):
+        """The prompt prefill as the reference computes it on CUDA, under fp16 autocast
+        (model.py:147-151, :175-235): the products take fp16 operands (pe_gemm_f16 rounds A as
+        it reads it; the weights and the QKV bias rounded once) with fp32 accumulation, and each
+        result is rounded to fp16 (pe_round_f16); RoPE, the SiLU product and the norms compute
+        in fp32 from fp16 values and their outputs are rounded (the Triton kernels store in
+        their input's dtype, kernels.py:22, :46-47, :74); attention runs on the fp16 q, K, V
+        with fp16 probabilities and an fp16 output (pe_flash_prefill_h16; head_dim 64, else the
+        fp32 kernel rounded after); the residual stream is fp16 from the first o-projection on
+        (addmm, model.py:213) and the KV cache holds fp16 values. The LM head multiplies the
+        fp16-rounded normed last row (the Q8_0 GEMV reads it as fp32, kernels.py:180)."""
+        cfg = self.cfg
+        Lt = token_ids.shape[0]
+        hd, nh, nkv = cfg.head_dim, cfg.n_head, cfg.n_kv_head
+        qd, kd = nh * hd, nkv * hd
+        cos = self.cos[positions]
+        sin = self.sin[positions]
+        pos0 = int(positions[0].item()) if positions.numel() else 0
+        w16 = self.f16_weights()
+        x = K.embed_gather(self.embed, token_ids)                       # (L, hidden), fp32
+        qkv = torch.empty(Lt, qd + 2 * kd, device=self.device, dtype=torch.float32)
+        q_rot = torch.empty(Lt, nh, hd, device=self.device, dtype=torch.float32)
+        for i, L in enumerate(self.layers):
+            k_buf, v_buf = cache[i]
+            W = w16[i]
+            bias = W["qkv_bias"]
+            if bias is not None:
+                bias = K.round_f16_(bias.clone())
+            h = K.rmsnorm(x, L.attn_norm, cfg.eps)                     # rounded by the GEMM's read
+            K.round_f16_(K.gemm_f16(h, W["qkv"], bias=bias, out=qkv))
+            qr = K.rope_kv_write(qkv, cos, sin, nh, k_buf, v_buf, pos0=pos0, out=q_rot)
+            K.round_f16_(qr.view(Lt, qd))
+            K.round_f16_(k_buf.view(nkv, -1)[:, pos0 * hd:(pos0 + Lt) * hd])
+            if hd == 64:
+                attn = K.flash_prefill(qr, k_buf, v_buf, pos0=pos0, half=True)
+            else:
+                attn = K.round_f16_(K.prefill_attn(qr, k_buf, v_buf, pos0=pos0).view(Lt, qd))
+            if i == 0:
+                x = K.round_f16_(x.clone())                             # addmm casts x to fp16
+            x = K.round_f16_(K.gemm_f16(attn, W["o"], residual=x))
+            h = K.round_f16_(K.rmsnorm(x, L.ffn_norm, cfg.eps))
+            if W["gu"] is not None:
+                gu = K.gemm_f16(h, W["gu"])
+            else:  # [gate; up] interleaved in groups of 16 rows: the product's columns put back
+                g4 = K.gemm_f16(h, W["gu_il"]).view(Lt, -1, 2, 16)
+                gu = torch.cat([g4[:, :, 0].reshape(Lt, -1), g4[:, :, 1].reshape(Lt, -1)], dim=1)
+            K.round_f16_(gu)
+            act = K.round_f16_(K.silu_mul(gu, cfg.ffn_dim))
+            x = K.round_f16_(K.gemm_f16(act, W["down"], residual=x))
+        h = K.round_f16_(K.rmsnorm(x[-1:], self.w["output_norm.weight"], cfg.eps))
+        logits = K.qgemv(h[0], self.output)
+        if greedy is not None:
+            # the pick of this prefill made on the host (once per prompt): the device pick of
+            # the LM-head launch normalises its input itself, which would skip the fp16
+            # rounding of the normed row; torch.argmax's rule (sampler.py:27)
+            pos, c = (int(v) for v in greedy.state[1:3].tolist())
+            pick = int(torch.argmax(logits).item())
+            greedy.state.copy_(torch.tensor([pick, pos + 1, c + 1], dtype=torch.int64))
+            if 0 <= c < greedy.log_cap:
+                greedy.log[c] = pick
+        return logits
 
     def _prefill(self, token_ids, positions, cache, greedy=None):
         cfg = self.cfg

@@ -18,6 +18,9 @@ from helpers import rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
+# the autocast prefill against the oracle's autocast mode (both fp16 at the same points; the
+# fp32 forward is ~1e-3 away at config 0)
+AUTOCAST_TOL = 1e-3
 
 
 @pytest.fixture(scope="module")
@@ -347,3 +350,61 @@ def test_7b_family_prefill_f16_close_to_fp32_path(tiny7b):
         m.prefill_f16_min_tokens = saved
     assert rel_err(out["f16"][0], out["fp32"][0]) < 2e-2
     assert rel_err(out["f16"][1], out["fp32"][1]) < 2e-2
+
+
+# ---- the reference's CUDA prefill numerics (fp16 autocast, model.py:147-151) ----------------
+
+def _autocast_prefill(eng, ids):
+    m = eng.model
+    old = m.prefill_autocast
+    m.prefill_autocast = True
+    try:
+        cache = eng._empty_cache(len(ids) + 4)
+        lg = m.forward(torch.tensor(ids, device=eng.device), torch.arange(len(ids), device=eng.device), cache)
+        return lg.cpu().numpy(), cache
+    finally:
+        m.prefill_autocast = old
+
+
+def test_autocast_prefill_matches_oracle_autocast(tiny):
+    """prefill_autocast against the oracle's autocast mode: far closer than to the fp32
+    forward (whose distance is the size of the fp16 roundings), and the KV cache it leaves holds
+    fp16 values equal to the oracle's."""
+    eng, ref = tiny
+    ids = [3, 500, 17, 999, 42, 7, 256, 1023, 0, 64, 65, 300, 12]
+    lg, cache = _autocast_prefill(eng, ids)
+    rcache = ref.empty_cache(len(ids) + 4)
+    ra = ref.forward(torch.tensor(ids), torch.arange(len(ids)), rcache, autocast=True).numpy()
+    rf = ref.forward(torch.tensor(ids), torch.arange(len(ids)), ref.empty_cache(len(ids))).numpy()
+    d_ac, d_fp32 = rel_err(lg, ra), rel_err(lg, rf)
+    print(f"tiny autocast: vs oracle autocast {d_ac:.3e}, vs oracle fp32 {d_fp32:.3e}")
+    assert d_ac < AUTOCAST_TOL
+    assert d_fp32 > 3 * d_ac
+    for c, rc in zip(cache, rcache):
+        k = c[0][:, :len(ids)].cpu()
+        assert torch.equal(k, k.half().float())                      # fp16 values
+        assert rel_err(k.numpy(), rc[0][:, :len(ids)].numpy()) < AUTOCAST_TOL
+
+
+def test_config0_autocast_prefill_matches_fixture(model_dir):
+    """Config 0's 13-token prompt prefilled with the reference's CUDA numerics: the logits at
+    the fixture's 4096 indices (the 2048 largest and 2048 random others) against the oracle's
+    autocast mode, relative to the largest logit. Over 24 layers two implementations of the
+    same fp16 rounding points drift apart (an fp32 sum that lands near an fp16 tie rounds to
+    either neighbour, and the difference feeds every later layer): 5.0e-4 measured, against
+    9.8e-4 to the fp32 forward; the tiny model above separates the two by 20x."""
+    from pico_hip import synth
+    from pico_hip.engine import Engine
+    fx = json.loads((GOLDEN / "config0_autocast_logits.json").read_text())
+    gguf = synth.cached(synth.ARCHES["qwen2.5-0.5b"], seed=0, cache_dir=model_dir)
+    assert synth.sha256(gguf) == fx["gguf_sha256"], "synthetic model is not byte-identical"
+    eng = Engine(gguf)
+    lg, _ = _autocast_prefill(eng, fx["prompt_ids"])
+    idx = np.array(fx["idx"])
+    scale = fx["max_abs_autocast"]
+    d_ac = float(np.abs(lg[idx] - np.array(fx["autocast"])).max() / scale)
+    d_fp32 = float(np.abs(lg[idx] - np.array(fx["fp32"])).max() / scale)
+    print(f"config 0 autocast: vs oracle autocast {d_ac:.3e}, vs oracle fp32 {d_fp32:.3e}")
+    assert d_ac < AUTOCAST_TOL
+    assert d_ac < 0.75 * d_fp32
+    assert int(np.argmax(lg)) == fx["argmax_autocast"]

@@ -89,6 +89,34 @@ def test_ref_forward_matches_float64_forward(small):
     assert rel_err(got, want) < 1e-4
 
 
+def test_autocast_prefill_matches_float64_with_fp16_roundings(small):
+    """The autocast mode (the reference's CUDA prefill, model.py:147-151) against the float64
+    forward with fp16 roundings at the same points. The normed last row (an fp16 vector in
+    both) is the same fp16 number in almost every element: fp32 and float64 arithmetic round
+    to different fp16 neighbours only near a tie, while a rounding point missing from (or
+    added to) one of the two would leave most elements different. The plain forwards are not
+    fp16 vectors at all."""
+    ids = [3, 1000, 17, 42, 512, 9, 77]
+    W64 = _weights64(small)
+    cos, sin = small.cos.double().numpy(), small.sin.double().numpy()
+    got, h = small.forward(torch.tensor(ids), torch.arange(len(ids)), small.empty_cache(len(ids)),
+                           autocast=True, return_hidden=True)
+    want, h64 = closed.forward64(W64, small.cfg, ids, cos, sin, fp16=True,
+                                 head_fp16="output" not in small.q, return_hidden=True)
+    h = h.double().numpy()
+    assert np.array_equal(h, closed.round16(h))            # an fp16 vector
+    assert np.mean(h == h64) > 0.85, np.mean(h == h64)   # 0.93 on the tiny model; 0.72 with
+    # the probabilities left unrounded in the attention, 0.0 with no roundings at all
+    assert rel_err(got.numpy(), want) < 3e-4
+    _, h32 = small.forward(torch.tensor(ids), torch.arange(len(ids)), small.empty_cache(len(ids)),
+                           return_hidden=True)
+    assert np.mean(h32.double().numpy() == h64) < 0.5      # the plain forward is not
+    # decode is not under autocast
+    one = small.forward(torch.tensor([ids[0]]), torch.tensor([0]), small.empty_cache(2), autocast=True)
+    ref = small.forward(torch.tensor([ids[0]]), torch.tensor([0]), small.empty_cache(2))
+    assert torch.equal(one, ref)
+
+
 def test_ref_decode_matches_recompute(small):
     """Decoding token by token with the cache gives the prefill logits of the longer prompt
     (up to the decode path's fp16 attention rounding and quantized-form GEMVs)."""
