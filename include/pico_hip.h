@@ -143,8 +143,11 @@ int pe_gemm_h16_silu_h(const void* a_f16, int64_t lda, const void* w_f16_il, voi
                        int64_t ldc, int64_t M, int64_t ffn, int64_t K, pe_stream_t stream);
 
 /* pe_gemm_f16 with A already fp16 in memory: a_f16 (M, K) with row stride lda (elements,
- * lda % 8 == 0, 16-byte aligned); everything else as pe_gemm_f16.
- * Replaces the prefill down projection of model.py:235 (L > 1) after pe_gemm_f16_silu_h. */
+ * lda % 8 == 0, 16-byte aligned); everything else as pe_gemm_f16, with the same bits. residual
+ * may be c itself (added in place). Long prompts (M >= 1024, K % 64 == 0, N % 16 == 0, c / bias /
+ * residual 16-byte aligned, ldc and ldr multiples of 4) run on a 256-row-tile kernel with
+ * direct-to-LDS loads (about 160 KB of LDS per workgroup).
+ * Replaces the prefill QKV, o-projection and down products of model.py:177, :213, :235 (L > 1). */
 int pe_gemm_h16(const void* a_f16, int64_t lda, const void* w_f16, const float* bias,
                 const float* residual, int64_t ldr, float* c, int64_t ldc, int64_t M, int64_t N,
                 int64_t K, pe_stream_t stream);

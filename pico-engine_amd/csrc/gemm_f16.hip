@@ -14,6 +14,11 @@
 // buffer, one barrier per step. LDS rows are padded to 40 halves (80 bytes), which makes the
 // 16-byte operand reads of 8 consecutive rows cover all 32 banks. Rows and columns past M / N
 // are clamped on load and masked on store.
+//
+// Long-prompt products with fp16 A (M >= 1024) run on k_gemm_h16_dl below instead: 256-row
+// tiles, direct-to-LDS loads through three stages, the same accumulation order.
+#include <atomic>
+
 #include "pe_common.h"
 
 namespace pe {
@@ -231,9 +236,277 @@ __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
     }
 }
 
+// ---- large-M products with fp16 A: direct-to-LDS loads, three LDS stages ----------------------
+//
+// pe_gemm_h16 for M >= kDlMinM (the long-prompt prefill's QKV, o-projection and ffn_down): a
+// 256-thread workgroup computes a 256 x BN tile (BN = 16 WTN), its four waves stacked along M,
+// each a 64 x BN slab of 4 x WTN MFMA 16x16x32 tiles. K advances 64 at a time through three LDS
+// stages, each holding the step's 256 A rows and BN W rows as 128-byte rows whose 16-byte chunk c
+// sits at position c ^ (row & 7) (the operand reads of 8 consecutive rows then touch all 32
+// banks). Global data goes straight into LDS (global_load_lds_dwordx4: lane l of a wave writes
+// M0 + 16 l, so a wave instruction fills 8 rows; each lane fetches the chunk that lands in its
+// slot), issued from inline assembly so that this wave's own vmcnt accounting decides what it
+// waits for (the compiler would otherwise wait for every outstanding load before each LDS read).
+// A step's 32-wide K slices are software-pipelined: the operands of the slice being multiplied
+// are in registers while the next slice's are read, and the barrier sits between a step's two
+// slices:
+//   A: MFMAs of slice 0 (R0)  | reads of slice 1 of stage S(k) -> R1
+//   B: wait for this wave's loads of step k + 1, barrier
+//   C: MFMAs of slice 1 (R1)  | reads of slice 0 of S(k + 1) -> R0 | loads of step k + 3 -> S(k)
+// Every wave read its last slice of S(k) in A, before the barrier, so S(k) is free in C; the
+// loads of a step are in flight for two steps. Per output element the MFMAs accumulate the
+// 32-wide K slices in ascending order, as k_gemm_f16 does, so the two kernels give the same bits.
+// The epilogue stages each wave's fp32 tile through LDS and adds bias and residual and stores C
+// as 16-byte row pieces (a residual row may be the C row it is added into).
+constexpr int kDlBM = 256, kDlK = 64, kDlStages = 3;
+constexpr int64_t kDlMinM = 1024;
+
+PE_DEV void dl_load16(const void* g, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+}
+template <int N>
+PE_DEV void dl_wait_loads() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+PE_DEV void dl_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left alone
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int WTN>
+constexpr size_t dl_lds_bytes() {
+    return (size_t)kDlStages * (kDlBM + 16 * WTN) * 128;
+}
+
+template <int WTN, bool BIAS, bool RES>
+__global__ __launch_bounds__(256) void k_gemm_h16_dl(GemmF16Args p) {
+    constexpr int BN = 16 * WTN, ROWS = kDlBM + BN, NBLK = ROWS / 8, NPW = (NBLK + 3) / 4;
+    constexpr int SCH = ROWS * 8;  // 16-byte chunks per stage
+    static_assert(2 * (4 + WTN) <= 4 * WTN + 1, "a slice's reads fit between the MFMAs");
+    static_assert(4 * 64 * (BN + 4) * 4 <= dl_lds_bytes<WTN>(), "epilogue tiles fit in the stages");
+    extern __shared__ uint4 dls[];
+    const int tid = threadIdx.x, l = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // tiles: the XCD of linear id lin (lin % 8) walks a contiguous range of row-major tiles,
+    // so its resident workgroups share A row tiles and the W in its L2
+    const int64_t NT = gridDim.x, MT = gridDim.y, total = NT * MT;
+    const int64_t lin = (int64_t)blockIdx.y * NT + blockIdx.x;
+    const int64_t t = total % 8 == 0 ? (lin % 8) * (total / 8) + lin / 8 : lin;
+    const int64_t bm = (t / NT) * kDlBM, bn = (t % NT) * BN;
+    // this lane's loads: 8-row block b = w + 4 i (the wave's last block repeated when NBLK is not
+    // a multiple of 4, so every wave issues NPW loads per step), row 8 b + (l >> 3), chunk
+    // (l & 7) ^ (l >> 3) -> slot l & 7 of that row; rows past M or N read the last row
+    const _Float16* src[NPW];
+#pragma unroll
+    for (int i = 0; i < NPW; ++i) {
+        const int b = w + 4 * i < NBLK ? w + 4 * i : w + 4 * i - 4;
+        const int rr = 8 * b + (l >> 3), c = (l & 7) ^ (l >> 3);
+        if (rr < kDlBM) {
+            const int64_t m = bm + rr;
+            src[i] = p.ah + (m < p.M ? m : p.M - 1) * p.lda + 8 * c;
+        } else {
+            const int64_t n = bn + rr - kDlBM;
+            src[i] = p.w + (n < p.N ? n : p.N - 1) * p.K + 8 * c;
+        }
+    }
+    const uint32_t lbase = (uint32_t)(uintptr_t)(&dls[0]);
+    auto load_step = [&](int64_t kk, int stage_chunk, int d) {
+        const int b = w + 4 * d < NBLK ? w + 4 * d : w + 4 * d - 4;
+        dl_load16(src[d] + kk * kDlK, lbase + (uint32_t)(stage_chunk + 64 * b) * 16);
+    };
+    f4v acc[4][WTN];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) acc[i][j] = f4v{0.f, 0.f, 0.f, 0.f};
+    const int li = l & 15, lq = l >> 4, wm = 64 * w;
+    int aoff[2], boff[2];  // operand chunks of this lane in a stage, per K slice
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const int cs = (4 * s + lq) ^ (li & 7);
+        aoff[s] = (wm + li) * 8 + cs;
+        boff[s] = (kDlBM + li) * 8 + cs;
+    }
+    h8 ra0[4], rb0[WTN], ra1[4], rb1[WTN];
+    // The MFMAs of one slice (av, bv), with the next slice's operand reads (stage chunk rdn,
+    // slice sn) and this step's share of loads (step kk into stage chunk wr) placed between
+    // them; scheduling barriers keep the placement.
+    auto part = [&](const h8(&av)[4], const h8(&bv)[WTN], h8(&na)[4], h8(&nb)[WTN], int rdn, int sn,
+                    bool rnext, int wr, int64_t kk, bool load) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < WTN; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
+                const int q = i * WTN + j;
+                if (rnext && (q & 1) == 0 && q / 2 < 4 + WTN) {
+                    const int r = q / 2;
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (r < 4) na[r] = *reinterpret_cast<const h8*>(&dls[rdn + aoff[sn] + 128 * r]);
+                    else nb[r - 4] = *reinterpret_cast<const h8*>(&dls[rdn + boff[sn] + 128 * (r - 4)]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if (load && (q & 1) == 1 && q / 2 < NPW) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    load_step(kk, wr, q / 2);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        if (load) {
+#pragma unroll
+            for (int d = 2 * WTN; d < NPW; ++d) load_step(kk, wr, d);  // loads past the MFMA slots
+        }
+    };
+    auto next_stage = [](int c) { return c == 2 * SCH ? 0 : c + SCH; };
+    const int nk = (int)(p.K / kDlK);
+    for (int s = 0; s < kDlStages && s < nk; ++s)
+#pragma unroll
+        for (int d = 0; d < NPW; ++d) load_step(s, s * SCH, d);
+    if (nk > 2) dl_wait_loads<2 * NPW>();
+    else if (nk > 1) dl_wait_loads<NPW>();
+    else dl_wait_loads<0>();
+    dl_barrier();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ra0[i] = *reinterpret_cast<const h8*>(&dls[aoff[0] + 128 * i]);
+#pragma unroll
+    for (int j = 0; j < WTN; ++j) rb0[j] = *reinterpret_cast<const h8*>(&dls[boff[0] + 128 * j]);
+    int rd = 0, k = 0;
+    for (; k + 3 < nk; ++k) {  // steady state: the loads of step k + 3 ride along
+        part(ra0, rb0, ra1, rb1, rd, 1, true, 0, 0, false);
+        dl_wait_loads<NPW>();
+        dl_barrier();
+        part(ra1, rb1, ra0, rb0, next_stage(rd), 0, true, rd, k + 3, true);
+        rd = next_stage(rd);
+    }
+    for (; k < nk; ++k) {  // the last (up to) three steps
+        part(ra0, rb0, ra1, rb1, rd, 1, true, 0, 0, false);
+        if (k + 2 < nk) dl_wait_loads<NPW>();
+        else dl_wait_loads<0>();
+        dl_barrier();
+        part(ra1, rb1, ra0, rb0, next_stage(rd), 0, k + 1 < nk, 0, 0, false);
+        rd = next_stage(rd);
+    }
+
+    // epilogue: the wave's 64 x BN tile into LDS (row stride BN + 4 floats), read back as
+    // 16-byte row pieces: residual loads first, then bias, sums and 16-byte stores
+    constexpr int ES = BN + 4, C4 = BN / 4, NIT = C4;  // 64 C4 pieces, 64 lanes
+    __syncthreads();
+    float* et = reinterpret_cast<float*>(dls) + w * 64 * ES;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < WTN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) et[(16 * i + 4 * lq + r) * ES + 16 * j + li] = acc[i][j][r];
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
+    const int64_t m0 = bm + wm;
+    float4 rv[NIT];
+    if constexpr (RES) {
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+            const int idx = it * 64 + l, row = idx / C4, c4 = idx % C4;
+            const int64_t m = m0 + row, n = bn + 4 * c4;
+            rv[it] = m < p.M && n < p.N ? *reinterpret_cast<const float4*>(p.res + m * p.ldr + n)
+                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int idx = it * 64 + l, row = idx / C4, c4 = idx % C4;
+        const int64_t m = m0 + row, n = bn + 4 * c4;
+        if (m >= p.M || n >= p.N) continue;
+        float4 v = *reinterpret_cast<const float4*>(&et[row * ES + 4 * c4]);
+        if constexpr (BIAS) {
+            const float4 bb = *reinterpret_cast<const float4*>(p.bias + n);
+            v.x += bb.x;
+            v.y += bb.y;
+            v.z += bb.z;
+            v.w += bb.w;
+        }
+        if constexpr (RES) {
+            v.x += rv[it].x;
+            v.y += rv[it].y;
+            v.z += rv[it].z;
+            v.w += rv[it].w;
+        }
+        *reinterpret_cast<float4*>(p.c + m * p.ldc + n) = v;
+    }
+}
+
 }  // namespace pe
 
 using namespace pe;
+
+// Per device: the dynamic-LDS limit set on the direct-to-LDS kernels (0 = not yet). Concurrent
+// first calls set the same attribute and store the same value.
+static std::atomic<int> g_dl_lds[64];
+
+template <int WTN>
+static int dl_launch(const GemmF16Args& p, hipStream_t s) {
+    constexpr size_t lds = dl_lds_bytes<WTN>();
+    const dim3 grid((unsigned)((p.N + 16 * WTN - 1) / (16 * WTN)), (unsigned)((p.M + kDlBM - 1) / kDlBM));
+    if (p.bias && p.res) hipLaunchKernelGGL((k_gemm_h16_dl<WTN, true, true>), grid, dim3(256), lds, s, p);
+    else if (p.bias) hipLaunchKernelGGL((k_gemm_h16_dl<WTN, true, false>), grid, dim3(256), lds, s, p);
+    else if (p.res) hipLaunchKernelGGL((k_gemm_h16_dl<WTN, false, true>), grid, dim3(256), lds, s, p);
+    else hipLaunchKernelGGL((k_gemm_h16_dl<WTN, false, false>), grid, dim3(256), lds, s, p);
+    return launch_status();
+}
+
+template <int WTN>
+static bool dl_configure() {
+    constexpr int lds = (int)dl_lds_bytes<WTN>();
+    const void* fns[4] = {(const void*)k_gemm_h16_dl<WTN, false, false>, (const void*)k_gemm_h16_dl<WTN, true, false>,
+                          (const void*)k_gemm_h16_dl<WTN, false, true>, (const void*)k_gemm_h16_dl<WTN, true, true>};
+    for (const void* f : fns)
+        if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess) return false;
+    return true;
+}
+
+// Runs pe_gemm_h16 on k_gemm_h16_dl when its shape and strides allow (else returns false and the
+// caller uses k_gemm_f16): M >= kDlMinM, K % 64, N % 16, C / bias / residual 16-byte aligned with
+// row strides % 4, and a device with the LDS the three stages need. The tile width WTN (16 WTN
+// columns) takes the fewest waves of workgroups over the CUs times the tile width, so a grid of
+// one workgroup per CU wins over a wider tile needing two rounds.
+static bool dl_try(const GemmF16Args& p, hipStream_t s, int* status) {
+    if (p.M < kDlMinM || p.K % kDlK || p.N % 16 || !aligned(p.c, 16) || p.ldc % 4 ||
+        (p.bias && !aligned(p.bias, 16)) || (p.res && (!aligned(p.res, 16) || p.ldr % 4)))
+        return false;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    int state = g_dl_lds[dev].load(std::memory_order_acquire);
+    if (state == 0) {
+        int max_lds = 0;
+        if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeSharedMemPerBlockOptin, dev) != hipSuccess || max_lds <= 0)
+            (void)hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+        const bool ok = max_lds >= (int)dl_lds_bytes<9>() && dl_configure<6>() && dl_configure<7>() &&
+                        dl_configure<8>() && dl_configure<9>();
+        state = ok ? 1 : -1;
+        g_dl_lds[dev].store(state, std::memory_order_release);
+    }
+    if (state < 0) return false;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return false;
+    const int64_t mt = (p.M + kDlBM - 1) / kDlBM;
+    int best = 0;
+    int64_t best_cost = 0;
+    for (int wtn = 6; wtn <= 9; ++wtn) {
+        const int64_t tiles = mt * ((p.N + 16 * wtn - 1) / (16 * wtn));
+        const int64_t cost = ((tiles + cus - 1) / cus) * wtn;
+        if (!best || cost < best_cost) {
+            best = wtn;
+            best_cost = cost;
+        }
+    }
+    switch (best) {
+        case 6: *status = dl_launch<6>(p, s); break;
+        case 7: *status = dl_launch<7>(p, s); break;
+        case 8: *status = dl_launch<8>(p, s); break;
+        default: *status = dl_launch<9>(p, s); break;
+    }
+    return true;
+}
 
 // 64 x 128 workgroup tiles when 128 x 128 ones would make fewer than 512 workgroups (two per
 // CU) and the shorter tile still makes at least 512.
@@ -283,6 +556,10 @@ static int gemm_entry(const void* a, int64_t lda, const void* w_f16, const float
     GemmF16Args p{AH ? nullptr : (const float*)a, AH ? (const _Float16*)a : nullptr, lda,
                   (const _Float16*)w_f16, bias, residual, ldr, c, nullptr, ldc, M, N, K};
     hipStream_t s = (hipStream_t)stream;
+    if constexpr (AH) {
+        int st = PE_OK;
+        if (dl_try(p, s, &st)) return st;
+    }
 #define PE_GF_LAUNCH(RT_)                                                                          \
     do {                                                                                           \
         const dim3 grid = gf_grid<RT_>(M, N);                                                      \

@@ -160,10 +160,10 @@ class Transformer:
         # fp16 where CUDA fp16 autocast holds them (model.py:147-151; _prefill_autocast)
         self.prefill_autocast = False
         # the matrix-core prefill's plain products (QKV + bias, o-proj and ffn_down + residual)
-        # on hipBLASLt; off: every product on this library's MFMA GEMM (pe_gemm_f16)
-        self.prefill_blaslt = True
-        # its workspace, and the device's hipBLASLt handle, made at load (outside any capture)
-        self._lt_ws: torch.Tensor | None = K.gemm_lt_workspace(self.device)
+        # on hipBLASLt instead of this library's MFMA GEMM (pe_gemm_h16); its workspace and the
+        # device's hipBLASLt handle are made on first use (outside any graph capture)
+        self.prefill_blaslt = False
+        self._lt_ws: torch.Tensor | None = None
         self._f16: list[dict[str, torch.Tensor]] | None = None
         # greedy decode steps the persistent kernel covers can run as one launch per token
         # (pe_decode_step) instead of four launches per layer; off by default: ~2 % faster, but
@@ -419,11 +419,12 @@ class Transformer:
     def _prefill_f16(self, token_ids, positions, cache, greedy=None):
         """The prefill on the matrix cores: GEMMs with fp16 operands and flash attention
         (pe_flash_prefill; head_dim 64, else the fp32 prefill attention), fp32 residual
-        stream, norms, RoPE and KV cache. The plain products (QKV + bias, o-proj and ffn_down
-        + residual) run on hipBLASLt (pe_gemm_lt) over operands stored in fp16 by their
+        stream, norms, RoPE and KV cache. Every product reads operands stored in fp16 by their
         producers (pe_rmsnorm_h16, pe_flash_prefill_h16, the SiLU GEMM), the same values
-        pe_gemm_f16 would round as it reads them; gate/up with its SiLU epilogue stays on
-        pe_gemm_f16_silu_h. prefill_blaslt = False runs every product on pe_gemm_f16."""
+        pe_gemm_f16 would round as it reads them: QKV + bias, o-proj and ffn_down + residual
+        (added in place) on pe_gemm_h16 (its direct-to-LDS kernel for long prompts), gate/up
+        with its SiLU epilogue on pe_gemm_h16_silu_h. prefill_blaslt = True runs the three
+        plain products on hipBLASLt (pe_gemm_lt) instead."""
         cfg = self.cfg
         Lt = token_ids.shape[0]
         hd, nh, nkv = cfg.head_dim, cfg.n_head, cfg.n_kv_head
@@ -443,23 +444,22 @@ class Transformer:
         for i, L in enumerate(self.layers):
             k_buf, v_buf = cache[i]
             W = w16[i]
-            if lt:  # the plain products on hipBLASLt, their operands stored in fp16
-                h16 = K.rmsnorm(x, L.attn_norm, cfg.eps, half=True)
+            # products on operands stored in fp16 by their producers
+            h16 = K.rmsnorm(x, L.attn_norm, cfg.eps, half=True)
+            if lt:
                 K.gemm_lt(h16, W["qkv"], bias=W["qkv_bias"], out=qkv, workspace=ws)
             else:
-                h = K.rmsnorm(x, L.attn_norm, cfg.eps)
-                K.gemm_f16(h, W["qkv"], bias=W["qkv_bias"], out=qkv)
+                K.gemm_f16(h16, W["qkv"], bias=W["qkv_bias"], out=qkv)
             # RoPE of q and k and the cache write of k and v, one pass (model.py:186-197)
             qr = K.rope_kv_write(qkv, cos, sin, nh, k_buf, v_buf, pos0=pos0, out=q_rot)
-            if hd == 64 and lt:
-                attn16 = K.flash_prefill(qr, k_buf, v_buf, pos0=pos0, half=True)
-                x, x_alt = K.gemm_lt(attn16, W["o"], residual=x, out=x_alt, workspace=ws), x
+            if hd == 64:  # matrix-core flash attention, fp16 output
+                attn = K.flash_prefill(qr, k_buf, v_buf, pos0=pos0, half=True)
+            else:         # other head sizes: the fp32 causal attention kernel
+                attn = K.prefill_attn(qr, k_buf, v_buf, pos0=pos0)
+            if lt and attn.dtype == torch.float16:
+                x, x_alt = K.gemm_lt(attn, W["o"], residual=x, out=x_alt, workspace=ws), x
             else:
-                if hd == 64:  # matrix-core flash attention
-                    attn = K.flash_prefill(qr, k_buf, v_buf, pos0=pos0)  # (L, hidden)
-                else:         # other head sizes: the fp32 causal attention kernel
-                    attn = K.prefill_attn(qr, k_buf, v_buf, pos0=pos0)
-                x = K.gemm_f16(attn, W["o"], residual=x)
+                x = K.gemm_f16(attn, W["o"], residual=x, out=x)
                 if lt and x_alt.shape != x.shape:
                     x_alt = torch.empty_like(x)
             if W["gu_il"] is not None:
@@ -473,7 +473,7 @@ class Transformer:
             if lt and act.dtype == torch.float16:
                 x, x_alt = K.gemm_lt(act, W["down"], residual=x, out=x_alt, workspace=ws), x
             else:
-                x = K.gemm_f16(act, W["down"], residual=x)
+                x = K.gemm_f16(act, W["down"], residual=x, out=x)
         return self._lm_head(x[-1], self.w["output_norm.weight"], greedy, K.LAYOUT_NATURAL)
 
     def _prefill_autocast(self, token_ids, positions, cache, greedy=None):

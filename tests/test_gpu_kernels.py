@@ -930,6 +930,38 @@ def test_gemm_h16_equals_gemm_f16_on_fp16_values(K, M, N, Kd, bias, res, extra):
     assert torch.equal(got, ref)
 
 
+@pytest.mark.parametrize("M,N,Kd,bias,res,extra", [
+    (8192, 896, 4864, False, True, 0), (8192, 896, 896, False, True, 0), (8192, 1152, 896, True, False, 0),
+    (1100, 160, 128, True, True, 64), (1024, 4000, 64, False, True, 0), (2049, 896, 896, True, True, 0),
+    (1023, 896, 896, False, True, 0)])
+def test_gemm_h16_long_prompt_kernel(K, M, N, Kd, bias, res, extra):
+    """Products with M >= 1024, K % 64 == 0 and N % 16 == 0 run on pe_gemm_h16's direct-to-LDS
+    kernel (256-row tiles, ragged M and N included; M = 1023 stays on the other kernel): the
+    bits of the fp32-A kernel on the same fp16 values (the same MFMA accumulation order), also
+    with the residual added in place (residual is out)."""
+    rng = np.random.default_rng(M + N + Kd + 11)
+    a = rng.standard_normal((M, Kd + extra)).astype(np.float16)
+    w16 = (rng.standard_normal((N, Kd)) * 0.05).astype(np.float16)
+    b = rng.standard_normal(N).astype(np.float32) if bias else None
+    r = rng.standard_normal((M, N)).astype(np.float32) if res else None
+    T = lambda v: None if v is None else torch.from_numpy(v).to(DEV)
+    A16 = T(a)[:, :Kd]
+    ref = K.gemm_f16(A16.float(), T(w16), bias=T(b), residual=T(r))
+    got = K.gemm_f16(A16, T(w16), bias=T(b), residual=T(r))
+    assert torch.equal(got, ref)
+    if res:
+        x = T(r)
+        K.gemm_f16(A16, T(w16), bias=T(b), residual=x, out=x)
+        assert torch.equal(x, ref)
+    if M * N * Kd <= 2 ** 31:
+        want = a[:, :Kd].astype(np.float64) @ w16.astype(np.float64).T
+        if b is not None:
+            want = want + b
+        if r is not None:
+            want = want + r
+        assert rel_err(got.cpu().numpy(), want) < 1e-5
+
+
 @pytest.mark.parametrize("M,ffn,Kd", [(300, 4864, 896), (13, 512, 3584), (129, 48, 96), (1, 16, 32),
                                       (4096, 2048, 64), (8192, 256, 64)])
 def test_gemm_f16_silu_half_output_and_down_product(K, M, ffn, Kd):

@@ -237,13 +237,15 @@ def test_prefill_f16_close_to_fp32_path(tiny):
     assert m._f16 is not None and len(m._f16) == len(m.layers)
 
 
-def test_prefill_hipblaslt_products_match_mfma_products(tiny):
+@pytest.mark.parametrize("n_tokens", [300, 1100])
+def test_prefill_hipblaslt_products_match_mfma_products(tiny, n_tokens):
     """The matrix-core prefill with its plain products (QKV + bias, o-proj and ffn_down +
-    residual) on hipBLASLt against the same prefill with every product on pe_gemm_f16: the
-    operands are the same fp16 values, only the fp32 summation order differs (1e-4)."""
+    residual) on hipBLASLt against the default prefill with every product on this library's
+    GEMMs (pe_gemm_h16; 1100 tokens: its long-prompt kernel): the operands are the same fp16
+    values, only the fp32 summation order differs (1e-4)."""
     eng, _ = tiny
     m = eng.model
-    ids = [(5 * i + 1) % 1024 for i in range(300)]
+    ids = [(5 * i + 1) % 1024 for i in range(n_tokens)]
     saved = m.prefill_f16_min_tokens, m.prefill_blaslt
     out = {}
     try:
