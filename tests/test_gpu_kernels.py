@@ -982,7 +982,8 @@ def test_gemm_f16_silu_half_output_and_down_product(K, M, ffn, Kd):
     assert torch.equal(K.gemm_f16(act16, wd, residual=res), K.gemm_f16(act32, wd, residual=res))
 
 
-@pytest.mark.parametrize("M,ffn,Kd", [(300, 4864, 896), (13, 512, 3584), (129, 48, 96), (8192, 256, 64)])
+@pytest.mark.parametrize("M,ffn,Kd", [(300, 4864, 896), (13, 512, 3584), (129, 48, 96), (8192, 256, 64),
+                                      (8192, 4864, 896), (1100, 48, 128), (2048, 1008, 64)])
 def test_gemm_h16_silu_equals_fp32_operand_path(K, M, ffn, Kd):
     """The SiLU GEMM on an fp16 A (pe_gemm_h16_silu_h) gives the bits of the fp32-A GEMM on the
     A those fp16 values came from (the fp32 path rounds A the same way as it reads it), and so
