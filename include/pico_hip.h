@@ -168,6 +168,16 @@ int pe_flash_prefill_h16(const float* q, int64_t q_stride, const float* k_cache,
                          int64_t capacity, int64_t L, int64_t pos0, float scale, void* out_f16,
                          int64_t out_stride, pe_stream_t stream);
 
+/* pe_flash_prefill_h16 of a prompt starting at position 0 with K and V taken from the fp16 key
+ * blocks of pe_rope_kv_write_blocks (kv16, kv16_blocks per kv head, L <= 64 kv16_blocks; the
+ * positions past L in the last block must be finite, e.g. zero): the blocks are copied into LDS
+ * with direct-to-LDS loads instead of being converted from the fp32 caches. The same fp16
+ * operand values in the same positions, so the same output bits. head_dim 64.
+ * Replaces the fp16 SDPA prefill call of model.py:201-209 (pos0 = 0). */
+int pe_flash_prefill_blocks(const float* q, int64_t q_stride, const void* kv16, int64_t kv16_blocks,
+                            int n_head, int n_kv, int head_dim, int64_t L, float scale, void* out,
+                            int64_t out_stride, pe_stream_t stream);
+
 /* Plain prefill GEMM on ROCm's hipBLASLt: c (M, N) = a (M, K) . w (N, K)^T (+ bias[N])
  * (+ residual (M, N)); a and w fp16 row-major (row strides lda and K elements; lda % 8 == 0,
  * K % 8 == 0, 16-byte aligned), fp32 accumulation, c and residual fp32 with row stride ldc
@@ -644,6 +654,19 @@ int pe_rope_kv_write(const float* qkv, int64_t qkv_stride, const float* cos_rows
                      const float* sin_rows, int n_head, int n_kv, int head_dim, int64_t L,
                      int64_t pos0, float* q_out, float* k_cache, float* v_cache, int64_t capacity,
                      pe_stream_t stream);
+
+/* pe_rope_kv_write that also writes k and v, rounded to fp16 (nearest even), as the key blocks
+ * pe_flash_prefill_blocks reads (head_dim 64): kv16 holds, per kv head, kv16_blocks blocks of
+ * 16384 bytes, block b = positions 64 b .. 64 b + 63: the K block [key][dim] then the V^T block
+ * [dim][key slot], each 64 rows of 128 bytes whose 16-byte chunk c is stored at chunk position
+ * c ^ (row & 7); V^T's key slots: in each 32-key slab, slot 8 g + i holds key 4 g + i (i < 4)
+ * or 16 + 4 g + (i - 4) (i >= 4). Positions not written keep their bytes (zero them for the
+ * block tail). pos0 + L <= 64 kv16_blocks, kv16 16-byte aligned. No counterpart in the
+ * reference: the layout of this build's flash-attention operands. */
+int pe_rope_kv_write_blocks(const float* qkv, int64_t qkv_stride, const float* cos_rows,
+                            const float* sin_rows, int n_head, int n_kv, int head_dim, int64_t L,
+                            int64_t pos0, float* q_out, float* k_cache, float* v_cache,
+                            int64_t capacity, void* kv16, int64_t kv16_blocks, pe_stream_t stream);
 
 /* Causal GQA attention of L queries at positions pos0..pos0+L-1 over the cache, fp32,
  * no output rounding. q row l at q + l*q_stride (n_head*hd), out row l at out + l*out_stride.

@@ -97,10 +97,22 @@ __global__ void k_kv_write(const float* __restrict__ ks, const float* __restrict
 // (pe_rope_kv_write). Item = (row l, slot): slots [0, nq4) rotate four pairs (j .. j + 3,
 // j + half ..) of a q head, then nk4 of a k head, then nv4 float4 copies of v. The same
 // arithmetic as k_rope (x1 c - x2 s, x1 s + x2 c) and a plain copy for v.
+// Flash-attention key blocks (kv16, head_dim 64, pe_rope_kv_write_blocks): per kv head, per
+// 64-key block b, the fp16 K block [key][dim] and then the fp16 V^T block [dim][key slot], each
+// 64 rows of 128 bytes whose 16-byte chunk c sits at chunk position c ^ (row & 7) -- the LDS
+// image k_flash_prefill reads, so it copies a block with direct-to-LDS loads. V^T's key slots
+// follow the P^T operand: in each 32-key slab, slot 8 g + i holds key 4 g + i (i < 4) or
+// 16 + 4 g + (i - 4) (i >= 4).
+PE_DEV int kv16_slot(int key) {  // key within its 64-key block -> V^T column
+    const int kw = key & 31, hi = kw >> 4, r = kw & 15;
+    return 32 * (key >> 5) + 8 * (r >> 2) + 4 * hi + (r & 3);
+}
+PE_DEV int64_t kv16_chunk_byte(int row, int chunk) { return (int64_t)row * 128 + 16 * (chunk ^ (row & 7)); }
+
 __global__ void k_rope_kv_write(const float* __restrict__ qkv, int64_t qs, const float* __restrict__ cs,
                                 const float* __restrict__ sn, int n_head, int n_kv, int hd, int L,
                                 int64_t pos0, float* __restrict__ q_out, float* kc, float* vc,
-                                int64_t cap) {
+                                int64_t cap, uint8_t* __restrict__ kv16, int64_t kv16_blocks) {
     const int h4 = hd / 8;                  // float4 pairs per head
     const int nq4 = n_head * h4, nk4 = n_kv * h4, nv4 = n_kv * (hd / 4);
     const int per = nq4 + nk4 + nv4;
@@ -127,10 +139,30 @@ __global__ void k_rope_kv_write(const float* __restrict__ qkv, int64_t qs, const
                             : kc + ((int64_t)hh * cap + pos0 + l) * hd;
             *reinterpret_cast<float4*>(yp + j) = y1;
             *reinterpret_cast<float4*>(yp + j + half) = y2;
+            if (!isq && kv16) {  // head_dim 64: dims j .. j + 3 and j + 32 .. j + 35 of the key row
+                typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+                const int64_t key = pos0 + l;
+                uint8_t* blk = kv16 + ((int64_t)hh * kv16_blocks + (key >> 6)) * 16384;
+                const int row = (int)(key & 63);
+                *reinterpret_cast<h4v*>(blk + kv16_chunk_byte(row, j >> 3) + 2 * (j & 7)) =
+                    h4v{(_Float16)y1.x, (_Float16)y1.y, (_Float16)y1.z, (_Float16)y1.w};
+                *reinterpret_cast<h4v*>(blk + kv16_chunk_byte(row, (j + half) >> 3) + 2 * ((j + half) & 7)) =
+                    h4v{(_Float16)y2.x, (_Float16)y2.y, (_Float16)y2.z, (_Float16)y2.w};
+            }
         } else {
             const int iv = it - nq4 - nk4, hh = iv / (hd / 4), d = 4 * (iv - hh * (hd / 4));
             const float4 v = *reinterpret_cast<const float4*>(row + (int64_t)(n_head + n_kv + hh) * hd + d);
             *reinterpret_cast<float4*>(vc + ((int64_t)hh * cap + pos0 + l) * hd + d) = v;
+            if (kv16) {  // V^T rows d .. d + 3 at this key's slot
+                const int64_t key = pos0 + l;
+                uint8_t* blk = kv16 + ((int64_t)hh * kv16_blocks + (key >> 6)) * 16384 + 8192;
+                const int slot = kv16_slot((int)(key & 63));
+                const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    *reinterpret_cast<_Float16*>(blk + kv16_chunk_byte(d + e, slot >> 3) + 2 * (slot & 7)) =
+                        (_Float16)vv[e];
+            }
         }
     }
 }
@@ -269,10 +301,10 @@ extern "C" int pe_kv_write(const float* k_src, const float* v_src, int64_t src_s
     return launch_status();
 }
 
-extern "C" int pe_rope_kv_write(const float* qkv, int64_t qkv_stride, const float* cos_rows,
-                                const float* sin_rows, int n_head, int n_kv, int head_dim, int64_t L,
-                                int64_t pos0, float* q_out, float* k_cache, float* v_cache,
-                                int64_t capacity, pe_stream_t stream) {
+static int rope_kv_write(const float* qkv, int64_t qkv_stride, const float* cos_rows, const float* sin_rows,
+                         int n_head, int n_kv, int head_dim, int64_t L, int64_t pos0, float* q_out,
+                         float* k_cache, float* v_cache, int64_t capacity, void* kv16, int64_t kv16_blocks,
+                         pe_stream_t stream) {
     if (L < 0 || n_head <= 0 || n_kv <= 0 || head_dim <= 0 || head_dim % 8 || pos0 < 0 ||
         capacity <= 0 || pos0 + L > capacity || qkv_stride < (int64_t)(n_head + 2 * n_kv) * head_dim ||
         qkv_stride % 4)
@@ -286,6 +318,25 @@ extern "C" int pe_rope_kv_write(const float* qkv, int64_t qkv_stride, const floa
         return PE_ERR_ALIGN;
     hipLaunchKernelGGL(k_rope_kv_write, dim3(grid1d(L * per)), dim3(256), 0, (hipStream_t)stream, qkv,
                        qkv_stride, cos_rows, sin_rows, n_head, n_kv, head_dim, (int)L, pos0, q_out, k_cache,
-                       v_cache, capacity);
+                       v_cache, capacity, (uint8_t*)kv16, kv16_blocks);
     return launch_status();
+}
+
+extern "C" int pe_rope_kv_write(const float* qkv, int64_t qkv_stride, const float* cos_rows,
+                                const float* sin_rows, int n_head, int n_kv, int head_dim, int64_t L,
+                                int64_t pos0, float* q_out, float* k_cache, float* v_cache,
+                                int64_t capacity, pe_stream_t stream) {
+    return rope_kv_write(qkv, qkv_stride, cos_rows, sin_rows, n_head, n_kv, head_dim, L, pos0, q_out, k_cache,
+                         v_cache, capacity, nullptr, 0, stream);
+}
+
+extern "C" int pe_rope_kv_write_blocks(const float* qkv, int64_t qkv_stride, const float* cos_rows,
+                                       const float* sin_rows, int n_head, int n_kv, int head_dim, int64_t L,
+                                       int64_t pos0, float* q_out, float* k_cache, float* v_cache,
+                                       int64_t capacity, void* kv16, int64_t kv16_blocks, pe_stream_t stream) {
+    if (head_dim != 64 || kv16_blocks <= 0 || pos0 + L > kv16_blocks * 64) return PE_ERR_SHAPE;
+    if (!kv16) return PE_ERR_NULL;
+    if (!aligned(kv16, 16)) return PE_ERR_ALIGN;
+    return rope_kv_write(qkv, qkv_stride, cos_rows, sin_rows, n_head, n_kv, head_dim, L, pos0, q_out, k_cache,
+                         v_cache, capacity, kv16, kv16_blocks, stream);
 }

@@ -52,7 +52,26 @@ struct FlashParams {
     float scale;
     float* out;          // (L, n_head, 64), token rows out_stride elements apart
     int64_t out_stride;
+    const uint8_t* kv16; // BLK: the fp16 K / V^T key blocks of pe_rope_kv_write_blocks
+    int64_t kv16_blocks; // BLK: key blocks per kv head in kv16
 };
+
+constexpr int kFpBlkSlots = 4;  // BLK: LDS ring depth (16 KB per key block)
+
+// BLK: 16 bytes per lane from global g into LDS at m0 + 16 lane (one wave instruction: 1 KB)
+PE_DEV void fp_load16(const void* g, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+}
+template <int N>
+PE_DEV void fp_wait_loads() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+PE_DEV void fp_lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); the key-block loads stay in flight
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 
 PE_DEV fh8 f8_to_h8(float4 a, float4 b) {
     fh8 r;
@@ -63,11 +82,24 @@ PE_DEV fh8 f8_to_h8(float4 a, float4 b) {
 
 // OutT _Float16: the output rounded to fp16 (nearest even), the operand of the o-projection
 // GEMM (p.out then points to fp16 rows).
-template <typename OutT>
+// BLK: K and V^T come as fp16 blocks already laid out as LDS images (pe_rope_kv_write_blocks:
+// 64 rows of 128 bytes, chunk c at position c ^ (row & 7), which keeps the 16-byte operand
+// reads of 8 consecutive rows on all 32 banks) and are copied by direct-to-LDS loads, waves 0-7
+// two 1 KB instructions each per block, into a ring of kFpBlkSlots blocks: the loads of block
+// b + 3 are issued in the step of block b, right after the barrier that frees its slot, and
+// waited for with this wave's own vmcnt count. Without BLK, waves 0-7 load fp32 K / V,
+// convert and store them into a ring of kFpStages padded blocks. The products are the same
+// either way (the same fp16 values in the same operand positions).
+template <typename OutT, bool BLK>
 __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_size) {
-    // LDS ring of kFpStages K / V^T blocks: block b is staged in slot b % kFpStages
-    __shared__ __align__(16) _Float16 ks[kFpStages * kFpKeys * kFpRow];  // K blocks, [key][dim]
-    __shared__ __align__(16) _Float16 vt[kFpStages * kFpHd * kFpRow];    // V blocks transposed, [dim][key]
+    // LDS ring of K / V^T blocks: block b is staged in slot b % (ring depth)
+    constexpr int kKs = BLK ? kFpBlkSlots * kFpKeys * kFpHd : kFpStages * kFpKeys * kFpRow;
+    constexpr int kVs = BLK ? kFpBlkSlots * kFpHd * kFpKeys : kFpStages * kFpHd * kFpRow;
+    constexpr int kSlotHalves = BLK ? kFpKeys * kFpHd : kFpKeys * kFpRow;  // one block's K (or V^T)
+    __shared__ __align__(16) _Float16 ks[kKs];  // K blocks, [key][dim]
+    __shared__ __align__(16) _Float16 vt[kVs];  // V blocks transposed, [dim][key]
+    // LDS element offset of 16-byte chunk c of row `row` within a block
+    auto lofs = [](int row, int c) { return BLK ? row * kFpHd + 8 * (c ^ (row & 7)) : row * kFpRow + 8 * c; };
     const int t = threadIdx.x, l = t & 63;
     const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave index (wave-uniform)
     const int li = l & 15, lg = l >> 4;
@@ -120,6 +152,7 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
     // position (masked out of the scores).
     float4 r4[4];
     auto kv_load = [&](int j0) {
+        if constexpr (BLK) return;
         if (w < 4) {
             const int kg = t & 15, d4 = t >> 4;
 #pragma unroll
@@ -142,6 +175,7 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
     // consecutive slots, one 8-byte store per dim (16 threads fill 128 contiguous bytes).
     auto stage = [&](int slot) {
         typedef _Float16 fh4 __attribute__((ext_vector_type(4)));
+        if constexpr (BLK) return;
         if (w < 4) {
             _Float16* vd = vt + slot * (kFpHd * kFpRow);
             const int kg = t & 15, d4 = t >> 4;
@@ -166,13 +200,13 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
     };
     // S^T = K Q^T for the 4 key tiles of 16 of the block in ring slot `slot`
     auto scores = [&](int slot, fv4 (&s)[4]) {
-        const _Float16* kd = ks + slot * (kFpKeys * kFpRow);
+        const _Float16* kd = ks + slot * kSlotHalves;
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
             s[jt] = fv4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const fh8 kbv = *reinterpret_cast<const fh8*>(kd + (16 * jt + li) * kFpRow + 32 * u + 8 * lg);
+                const fh8 kbv = *reinterpret_cast<const fh8*>(kd + lofs(16 * jt + li, 4 * u + lg));
                 s[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kbv, qa[u], s[jt], 0, 0, 0);
             }
         }
@@ -227,12 +261,12 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
         }
         m_run = m_new;
         // A = V^T (16 dims x 32 keys) per dim tile, B = P^T (32 keys x 16 queries)
-        const _Float16* vd = vt + slot * (kFpHd * kFpRow);
+        const _Float16* vd = vt + slot * kSlotHalves;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
 #pragma unroll
             for (int d = 0; d < 4; ++d) {
-                const fh8 va = *reinterpret_cast<const fh8*>(vd + (16 * d + li) * kFpRow + 32 * u + 8 * lg);
+                const fh8 va = *reinterpret_cast<const fh8*>(vd + lofs(16 * d + li, 4 * u + lg));
                 o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[u], o[d], 0, 0, 0);
             }
         }
@@ -244,39 +278,90 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
     // barrier after block b's staging, so none still reads block b - 1's K (its scores were
     // computed before that barrier) and the slowest still reads only block b's K / V (slot
     // b % 3) and block b - 1's V (slot (b - 1) % 3).
-    kv_load(0);
-    stage(0);
-    __syncthreads();
-    kv_load(kFpKeys < key_end ? kFpKeys : 0);
-    fv4 sa[4], sb[4];
-    scores(0, sa);
-    int slot = 0;
-    // one pipelined block: softmax and P.V of block b (scores in cur, K / V in ring slot
-    // `slot`), scores of block b + 1 into nxt
-    auto step = [&](int b, fv4 (&cur)[4], fv4 (&nxt)[4]) {
-        const int j0 = b * kFpKeys;
-        const int nslot = slot == kFpStages - 1 ? 0 : slot + 1;
-        stage(nslot);
-        __syncthreads();
-        kv_load(j0 + 2 * kFpKeys < key_end ? j0 + 2 * kFpKeys : j0 + kFpKeys);
-        mask(j0, cur);
-        scores(nslot, nxt);
-        softmax_pv(cur, slot);
-        slot = nslot;
-    };
-    // unrolled by two so that the score tiles alternate between sa and sb without copies
-    int b = 0;
-    for (; b + 2 < nblk; b += 2) {
-        step(b, sa, sb);
-        step(b + 1, sb, sa);
-    }
-    if (b + 1 < nblk) {
-        step(b, sa, sb);
-        mask((b + 1) * kFpKeys, sb);
-        softmax_pv(sb, slot);
+    if constexpr (BLK) {
+        // key block b of this kv head: 16 wave instructions of 1 KB (8 for K, 8 for V^T), two
+        // per wave for waves 0-7
+        const uint8_t* kvh_blocks = p.kv16 + (int64_t)kvh * p.kv16_blocks * 16384 + 16 * l;
+        const uint32_t ks_base = (uint32_t)(uintptr_t)ks, vt_base = (uint32_t)(uintptr_t)vt;
+        auto blk_load = [&](int b) {
+            if (w >= 8) return;
+            const int slot = b & (kFpBlkSlots - 1);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int q = 2 * w + i, half = q >> 3, part = q & 7;
+                fp_load16(kvh_blocks + (int64_t)b * 16384 + half * 8192 + part * 1024,
+                          (half ? vt_base : ks_base) + (uint32_t)(slot * kSlotHalves * 2 + part * 1024));
+            }
+        };
+        blk_load(0);
+        if (nblk > 1) blk_load(1);
+        if (nblk > 2) blk_load(2);
+        if (nblk > 2) fp_wait_loads<4>();
+        else if (nblk > 1) fp_wait_loads<2>();
+        else fp_wait_loads<0>();
+        fp_lds_barrier();
+        fv4 sa[4], sb[4];
+        scores(0, sa);
+        // block b: wait for block b + 1's loads (block b + 2's may stay in flight), barrier
+        // (every wave is past block b - 1, whose slot takes block b + 3), then block b + 1's
+        // scores and block b's softmax and P.V
+        auto step = [&](int b, fv4 (&cur)[4], fv4 (&nxt)[4]) {
+            if (b + 2 < nblk) fp_wait_loads<2>();
+            else fp_wait_loads<0>();
+            fp_lds_barrier();
+            if (b + 3 < nblk) blk_load(b + 3);
+            mask(b * kFpKeys, cur);
+            scores((b + 1) & (kFpBlkSlots - 1), nxt);
+            softmax_pv(cur, b & (kFpBlkSlots - 1));
+        };
+        int b = 0;
+        for (; b + 2 < nblk; b += 2) {
+            step(b, sa, sb);
+            step(b + 1, sb, sa);
+        }
+        if (b + 1 < nblk) {
+            step(b, sa, sb);
+            mask((b + 1) * kFpKeys, sb);
+            softmax_pv(sb, (b + 1) & (kFpBlkSlots - 1));
+        } else {
+            mask(b * kFpKeys, sa);
+            softmax_pv(sa, b & (kFpBlkSlots - 1));
+        }
     } else {
-        mask(b * kFpKeys, sa);
-        softmax_pv(sa, slot);
+        kv_load(0);
+        stage(0);
+        __syncthreads();
+        kv_load(kFpKeys < key_end ? kFpKeys : 0);
+        fv4 sa[4], sb[4];
+        scores(0, sa);
+        int slot = 0;
+        // one pipelined block: softmax and P.V of block b (scores in cur, K / V in ring slot
+        // `slot`), scores of block b + 1 into nxt
+        auto step = [&](int b, fv4 (&cur)[4], fv4 (&nxt)[4]) {
+            const int j0 = b * kFpKeys;
+            const int nslot = slot == kFpStages - 1 ? 0 : slot + 1;
+            stage(nslot);
+            __syncthreads();
+            kv_load(j0 + 2 * kFpKeys < key_end ? j0 + 2 * kFpKeys : j0 + kFpKeys);
+            mask(j0, cur);
+            scores(nslot, nxt);
+            softmax_pv(cur, slot);
+            slot = nslot;
+        };
+        // unrolled by two so that the score tiles alternate between sa and sb without copies
+        int b = 0;
+        for (; b + 2 < nblk; b += 2) {
+            step(b, sa, sb);
+            step(b + 1, sb, sa);
+        }
+        if (b + 1 < nblk) {
+            step(b, sa, sb);
+            mask((b + 1) * kFpKeys, sb);
+            softmax_pv(sb, slot);
+        } else {
+            mask(b * kFpKeys, sa);
+            softmax_pv(sa, slot);
+        }
     }
 
     // out: O[query q0 + li][dim 16 d + 4 lg + r] / l
@@ -302,7 +387,8 @@ using namespace pe;
 static int flash_prefill(const float* q, int64_t q_stride, const float* k_cache,
                          const float* v_cache, int n_head, int n_kv, int head_dim,
                          int64_t capacity, int64_t L, int64_t pos0, float scale, void* out,
-                         int64_t out_stride, bool half_out, pe_stream_t stream) {
+                         int64_t out_stride, bool half_out, pe_stream_t stream,
+                         const void* kv16 = nullptr, int64_t kv16_blocks = 0) {
     if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > kFpMaxWaves ||
         head_dim != kFpHd || capacity <= 0 || capacity > kFpMaxCapacity || L < 0 || pos0 < 0 || pos0 + L > capacity || n_kv > 65535)
         return PE_ERR_SHAPE;
@@ -316,15 +402,17 @@ static int flash_prefill(const float* q, int64_t q_stride, const float* k_cache,
         !aligned(out, half_out ? 2 : 4))
         return PE_ERR_ALIGN;
     FlashParams p{q, q_stride, k_cache, v_cache, n_head / n_kv, n_kv, capacity, L, pos0, scale, (float*)out,
-                  out_stride};
+                  out_stride, (const uint8_t*)kv16, kv16_blocks};
     const int waves = group * (qb / 16);  // 9..16 (kv_load and stage use the first 8 waves)
     const int64_t nblocks = (L + qb - 1) / qb * (int64_t)n_kv;
     if (nblocks > 0x7FFFFFFF) return PE_ERR_SHAPE;
     const dim3 grid((unsigned)nblocks);
-    if (half_out)
-        hipLaunchKernelGGL(k_flash_prefill<_Float16>, grid, dim3(64 * waves), 0, (hipStream_t)stream, p, qb);
+    if (kv16)
+        hipLaunchKernelGGL((k_flash_prefill<_Float16, true>), grid, dim3(64 * waves), 0, (hipStream_t)stream, p, qb);
+    else if (half_out)
+        hipLaunchKernelGGL((k_flash_prefill<_Float16, false>), grid, dim3(64 * waves), 0, (hipStream_t)stream, p, qb);
     else
-        hipLaunchKernelGGL(k_flash_prefill<float>, grid, dim3(64 * waves), 0, (hipStream_t)stream, p, qb);
+        hipLaunchKernelGGL((k_flash_prefill<float, false>), grid, dim3(64 * waves), 0, (hipStream_t)stream, p, qb);
     return launch_status();
 }
 
@@ -342,4 +430,16 @@ extern "C" int pe_flash_prefill_h16(const float* q, int64_t q_stride, const floa
                                     int64_t out_stride, pe_stream_t stream) {
     return flash_prefill(q, q_stride, k_cache, v_cache, n_head, n_kv, head_dim, capacity, L, pos0,
                          scale, out, out_stride, true, stream);
+}
+
+extern "C" int pe_flash_prefill_blocks(const float* q, int64_t q_stride, const void* kv16, int64_t kv16_blocks,
+                                       int n_head, int n_kv, int head_dim, int64_t L, float scale, void* out,
+                                       int64_t out_stride, pe_stream_t stream) {
+    if (head_dim != kFpHd || kv16_blocks <= 0 || L > kv16_blocks * kFpKeys || kv16_blocks > (1 << 18))
+        return PE_ERR_SHAPE;
+    if (L > 0 && !kv16) return PE_ERR_NULL;
+    if (kv16 && !aligned(kv16, 16)) return PE_ERR_ALIGN;
+    // the fp32 caches are not read: any valid pointers satisfy the shared checks
+    return flash_prefill(q, q_stride, (const float*)kv16, (const float*)kv16, n_head, n_kv, head_dim,
+                         kv16_blocks * kFpKeys, L, 0, scale, out, out_stride, true, stream, kv16, kv16_blocks);
 }

@@ -117,6 +117,7 @@ _SIGNATURES = {
     "pe_gemm_h16": (_I, [_P, _L, _P, _P, _P, _L, _P, _L, _L, _L, _L, _P]),
     "pe_flash_prefill": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _L, _F, _P, _L, _P]),
     "pe_flash_prefill_h16": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _L, _F, _P, _L, _P]),
+    "pe_flash_prefill_blocks": (_I, [_P, _L, _P, _L, _I, _I, _I, _L, _F, _P, _L, _P]),
     "pe_gemm_lt": (_I, [_P, _L, _P, _L, _L, _L, _P, _P, _L, _P, _L, _P, _L, _P]),
     "pe_gemm_lt_init": (_I, []),
     "pe_mfma_bytes": (_L, [_I, _L, _L]),
@@ -147,6 +148,7 @@ _SIGNATURES = {
     "pe_qgemm": (_I, [_I, _P, _L, _L, _P, _L, _L, _P, _P, _L, _P, _L, _P]),
     "pe_kv_write": (_I, [_P, _P, _L, _I, _I, _L, _L, _P, _P, _L, _P]),
     "pe_rope_kv_write": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _P, _P, _P, _L, _P]),
+    "pe_rope_kv_write_blocks": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _P, _P, _P, _L, _P, _L, _P]),
     "pe_prefill_attn": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _L, _F, _P, _L, _P]),
     "pe_decode_step_supported": (_I, [_I, _I, _I, _I, _I, _I, _L, _L]),
     "pe_decode_step_workspace_bytes": (_L, [_I, _I, _I, _I, _I, _I]),

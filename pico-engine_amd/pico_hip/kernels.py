@@ -1152,13 +1152,22 @@ def kv_write(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: t
                           _ptr(v_cache), k_cache.shape[1], _stream(dev)), "pe_kv_write")
 
 
+def kv16_blocks(n_kv: int, length: int, device) -> torch.Tensor:
+    """A zeroed buffer for the fp16 key blocks of ``length`` positions (head_dim 64), filled by
+    rope_kv_write(kv16=...) and read by flash_prefill_blocks: (n_kv, ceil(length / 64), 16384)
+    bytes; positions past ``length`` in the last block stay zero."""
+    return torch.zeros(n_kv, (length + 63) // 64, 16384, device=device, dtype=torch.uint8)
+
+
 def rope_kv_write(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_head: int,
                   k_cache: torch.Tensor, v_cache: torch.Tensor, pos0: int = 0,
-                  out: torch.Tensor | None = None) -> torch.Tensor:
+                  out: torch.Tensor | None = None, kv16: torch.Tensor | None = None) -> torch.Tensor:
     """RoPE of the q and k heads of the fused QKV rows and the cache write of k and v in one
     pass: returns rope(q) (L, n_head, hd); k_cache[h][pos0 + l] = rope(k[l][h]), v likewise
     unrotated. qkv (L, (n_head + 2 n_kv) hd) with contiguous rows (row stride allowed), cos/sin
-    (L, hd/2): the same values as rope + kv_write (model.py:186-197)."""
+    (L, hd/2): the same values as rope + kv_write (model.py:186-197). ``kv16`` (kv16_blocks,
+    head_dim 64): the same k and v also go there, rounded to fp16, as flash_prefill_blocks'
+    key blocks (pe_rope_kv_write_blocks)."""
     dev = _on_gpu(qkv, cos, sin, k_cache, v_cache)
     n_kv, capacity, hd = k_cache.shape
     L = qkv.shape[0]
@@ -1169,9 +1178,18 @@ def rope_kv_write(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_hea
     c, s = cos.float().contiguous(), sin.float().contiguous()
     if out is None:
         out = torch.empty(L, n_head, hd, device=dev, dtype=torch.float32)
-    check(lib.pe_rope_kv_write(_ptr(qkv), qkv.stride(0), _ptr(c), _ptr(s), n_head, n_kv, hd, L, int(pos0),
-                               _ptr(out), _ptr(k_cache), _ptr(v_cache), capacity, _stream(dev)),
-          "pe_rope_kv_write")
+    if kv16 is None:
+        check(lib.pe_rope_kv_write(_ptr(qkv), qkv.stride(0), _ptr(c), _ptr(s), n_head, n_kv, hd, L, int(pos0),
+                                   _ptr(out), _ptr(k_cache), _ptr(v_cache), capacity, _stream(dev)),
+              "pe_rope_kv_write")
+    else:
+        if kv16.dtype != torch.uint8 or not kv16.is_contiguous() or kv16.dim() != 3 or kv16.shape[0] != n_kv \
+                or kv16.shape[2] != 16384:
+            raise ValueError("kv16 must be a contiguous uint8 (n_kv, blocks, 16384) buffer (kv16_blocks)")
+        check(lib.pe_rope_kv_write_blocks(_ptr(qkv), qkv.stride(0), _ptr(c), _ptr(s), n_head, n_kv, hd, L,
+                                          int(pos0), _ptr(out), _ptr(k_cache), _ptr(v_cache), capacity,
+                                          _ptr(kv16), kv16.shape[1], _stream(dev)),
+              "pe_rope_kv_write_blocks")
     return out
 
 
@@ -1214,6 +1232,30 @@ def flash_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     check(fn(_ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache), n_head, n_kv, hd,
              capacity, L, pos0, float(scale), _ptr(out), out.stride(0), _stream(dev)),
           "pe_flash_prefill_h16" if half else "pe_flash_prefill")
+    return out
+
+
+def flash_prefill_blocks(q: torch.Tensor, kv16: torch.Tensor, scale: float | None = None,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+    """flash_prefill(half=True) of a prompt from position 0, reading K and V from the fp16 key
+    blocks rope_kv_write(kv16=...) wrote (pe_flash_prefill_blocks): the same fp16 values in the
+    same operand positions, so the same bits; head_dim 64."""
+    dev = _on_gpu(q, kv16)
+    L, n_head, hd = q.shape
+    n_kv, nblk = kv16.shape[0], kv16.shape[1]
+    if kv16.dtype != torch.uint8 or not kv16.is_contiguous() or kv16.dim() != 3 or kv16.shape[2] != 16384:
+        raise ValueError("kv16 must be a contiguous uint8 (n_kv, blocks, 16384) buffer (kv16_blocks)")
+    if q.stride(2) != 1 or q.stride(1) != hd or q.stride(0) % 4 or q.data_ptr() % 16:
+        q = q.contiguous()
+    if scale is None:
+        scale = hd ** -0.5
+    if out is None:
+        out = torch.empty(L, n_head * hd, device=dev, dtype=torch.float16)
+    if out.dtype != torch.float16:
+        raise ValueError("out must be float16")
+    check(lib.pe_flash_prefill_blocks(_ptr(q), q.stride(0), _ptr(kv16), nblk, n_head, n_kv, hd, L, float(scale),
+                                      _ptr(out), out.stride(0), _stream(dev)),
+          "pe_flash_prefill_blocks")
     return out
 
 
@@ -1275,6 +1317,7 @@ __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "
            "attn_gproj", "attn_gproj_supported", "attn_oproj_fix", "attn_oproj_supported", "fix_acc",
            "repack_oproj", "oproj_eligible", "qgemv_fix_norm_silu", "qgemv_norm_argmax", "dequantize_weight_f16",
            "repack_down_slices", "down_slice_eligible", "ffn_fix", "ffn_fix_supported", "ffn_fix_bound",
+           "kv16_blocks", "flash_prefill_blocks",
            "fix_acc_block", "fix_stride", "qkv_fix_rmsnorm_rope", "FFN_REPLICAS",
            "DecodeStep", "decode_step_supported", "decode_step_workspace",
            "gemm_f16", "gemm_f16_silu", "interleave_gate_up_f16", "flash_prefill",

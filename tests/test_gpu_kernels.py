@@ -1020,6 +1020,65 @@ def test_rope_kv_write_equals_rope_then_kv_write(K, L, nh, nkv, hd, pos0):
     assert torch.equal(k1, k2) and torch.equal(v1, v2)
 
 
+def _kv16_layout_ref(k, v, length):
+    """numpy restatement of the fp16 key blocks (pe_rope_kv_write_blocks): per kv head and
+    64-key block, K [key][dim] then V^T [dim][key slot] as 64 rows of 8 chunks of 8 halves,
+    chunk c of row r at chunk position c ^ (r & 7); slot 8 g + i of a 32-key slab holds key
+    4 g + i (i < 4) or 16 + 4 g + (i - 4)."""
+    n_kv, _, hd = k.shape
+    nblk = (length + 63) // 64
+    out = np.zeros((n_kv, nblk, 2, 64, 8, 8), np.float16)
+    slot_key = np.zeros(64, np.int64)
+    for key in range(64):
+        kw = key % 32
+        g, i = (kw // 4, kw % 4) if kw < 16 else ((kw - 16) // 4, 4 + (kw - 16) % 4)
+        slot_key[32 * (key // 32) + 8 * g + i] = key
+    for h in range(n_kv):
+        for b in range(nblk):
+            kb = np.zeros((64, 64), np.float16)
+            vb = np.zeros((64, 64), np.float16)
+            n = min(64, length - 64 * b)
+            kb[:n] = k[h, 64 * b:64 * b + n].astype(np.float16)
+            vb[:n] = v[h, 64 * b:64 * b + n].astype(np.float16)
+            vt = vb[slot_key].T  # [dim][slot]
+            for r in range(64):
+                for c in range(8):
+                    out[h, b, 0, r, c ^ (r & 7)] = kb[r, 8 * c:8 * c + 8]
+                    out[h, b, 1, r, c ^ (r & 7)] = vt[r, 8 * c:8 * c + 8]
+    return out.view(np.uint8).reshape(n_kv, nblk, 16384)
+
+
+@pytest.mark.parametrize("L", [1, 64, 77, 300, 1000])
+@pytest.mark.parametrize("n_head,n_kv", [(14, 2), (8, 8), (16, 1), (9, 3)])
+def test_flash_prefill_blocks_equals_fp32_cache_path(K, L, n_head, n_kv):
+    """The RoPE pass writing the fp16 key blocks (pe_rope_kv_write_blocks) leaves the caches and
+    q as pe_rope_kv_write does and fills the blocks as the numpy restatement of their layout
+    says; flash attention from the blocks (pe_flash_prefill_blocks, direct-to-LDS copies) gives
+    the bits of pe_flash_prefill_h16 on the fp32 caches."""
+    rng = np.random.default_rng(L + 31 * n_head + n_kv)
+    hd, cap = 64, L + 5
+    qkv = torch.from_numpy(rng.standard_normal((L, (n_head + 2 * n_kv) * hd)).astype(np.float32)).to(DEV)
+    ang = rng.standard_normal((L, hd // 2)).astype(np.float32)
+    cos, sin = torch.from_numpy(np.cos(ang)).to(DEV), torch.from_numpy(np.sin(ang)).to(DEV)
+    k1, v1 = torch.zeros(n_kv, cap, hd, device=DEV), torch.zeros(n_kv, cap, hd, device=DEV)
+    k2, v2 = k1.clone(), v1.clone()
+    q1 = K.rope_kv_write(qkv, cos, sin, n_head, k1, v1)
+    kv16 = K.kv16_blocks(n_kv, L, DEV)
+    q2 = K.rope_kv_write(qkv, cos, sin, n_head, k2, v2, kv16=kv16)
+    assert torch.equal(q1, q2) and torch.equal(k1, k2) and torch.equal(v1, v2)
+    if L <= 300:
+        want = _kv16_layout_ref(k1.cpu().numpy(), v1.cpu().numpy(), L)
+        np.testing.assert_array_equal(kv16.cpu().numpy(), want)
+    ref = K.flash_prefill(q1, k1, v1, half=True)
+    got = K.flash_prefill_blocks(q2, kv16)
+    assert torch.equal(got, ref)
+
+
+def test_flash_prefill_blocks_full_length(K):
+    """The block path at the config-3 length (8192 positions, 14/2 heads): the same bits."""
+    test_flash_prefill_blocks_equals_fp32_cache_path(K, 8192, 14, 2)
+
+
 @pytest.mark.parametrize("L,pos0", [(1, 0), (5, 0), (64, 0), (100, 7), (130, 0), (513, 0)])
 @pytest.mark.parametrize("n_head,n_kv", [(14, 2), (8, 8), (16, 4), (16, 1), (9, 3)])
 def test_flash_prefill_matches_closed_form(K, L, pos0, n_head, n_kv):
