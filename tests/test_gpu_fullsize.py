@@ -298,5 +298,29 @@ def test_7b_model_matches_oracle_graph_and_pick(model_dir, K):
         err = rel_err(lg.cpu().numpy(), rl.cpu().numpy())
         print(f"7B 128-token fp16 prefill logits relative error {err:.2e}")
         assert err < TOL_F16_PREFILL
+        # decode where the benchmark runs it: a cache of 384 positions (its 128-token prompt +
+        # 256 steps), positions 360..365 after a 360-token matrix-core prefill, graph-replayed
+        # steps against the same steps run eagerly (bit for bit) and against the oracle
+        # continuing on its own fp32-prefilled cache (the fp16 prefill's tolerance)
+        n0, cap = 360, 384
+        ids = torch.from_numpy(rng.integers(0, arch.vocab, size=n0)).to(DEV)
+        cache, rcache = eng._empty_cache(cap), ref.empty_cache(cap)
+        graph = eng._build_decode_graph(cache)
+        lg = eng.model.forward(ids, torch.arange(n0, device=DEV), cache)
+        rl = ref.forward(ids, torch.arange(n0, device=DEV), rcache)
+        assert rel_err(lg.cpu().numpy(), rl.cpu().numpy()) < TOL_F16_PREFILL
+        eager_cache = [(kc.clone(), vc.clone()) for kc, vc in cache]
+        tok = int(rl.argmax())
+        for s in range(6):
+            pos = n0 + s
+            got = eng._decode_step(tok, pos, cache, graph).clone()
+            eager = eng.model.forward(torch.tensor([tok], device=DEV), torch.tensor([pos], device=DEV),
+                                      eager_cache)
+            assert torch.equal(got, eager), pos
+            assert int(eng._greedy.token) == int(torch.argmax(eager)), pos
+            rl = ref.forward(torch.tensor([tok], device=DEV), torch.tensor([pos], device=DEV), rcache)
+            err = rel_err(got.cpu().numpy(), rl.cpu().numpy())
+            assert err < TOL_F16_PREFILL, (pos, err)
+            tok = int(rl.argmax())
     finally:
         eng.model.prefill_f16_min_tokens = saved
