@@ -16,7 +16,8 @@
 // are clamped on load and masked on store.
 //
 // Long-prompt products with fp16 A (M >= 1024) run on k_gemm_h16_dl below instead: 256-row
-// tiles, direct-to-LDS loads through three stages, the same accumulation order.
+// tiles, direct-to-LDS loads through three stages, the same accumulation order; the long-prompt
+// SiLU product with fp16 A and output on k_gemm_h16_silu_dl (256 x 256 tiles).
 #include <atomic>
 
 #include "pe_common.h"
@@ -38,6 +39,7 @@ struct GemmF16Args {
     _Float16* ch;       // (M, N / 2), row stride ldc (fp16 SiLU output, CH)
     int64_t ldc;
     int64_t M, N, K;
+    int round_wgs;      // k_gemm_h16_silu_dl: workgroups per round (a multiple of 8)
 };
 
 constexpr int kGfTile = 128;  // workgroup tile (M and N)
@@ -436,6 +438,161 @@ __global__ __launch_bounds__(256) void k_gemm_h16_dl(GemmF16Args p) {
     }
 }
 
+// ---- long-prompt [gate; up] + SiLU with fp16 A and output: 256 x 256 tiles ---------------------
+//
+// pe_gemm_h16_silu_h for M > 31 * 256 (the long-prompt prefill's SiLU product): the kernels above
+// load (BM + BN) x K operand bytes per BM x BN tile, so k_gemm_f16's 128 x 128 tiles move 2.2 GB
+// of L2 data for the 8192 x 9728 x 896 product, and at the ~45 GB/s per CU these kernels draw
+// from L2 that bounds it. A 512-thread workgroup here computes a 256 x 256 tile (twice the MACs
+// per loaded byte): waves 4 (M) x 2 (N), each a 64 x 128 slab of 4 x 8 MFMA 16x16x32 tiles.
+// K advances 32 at a time through three LDS stages of 64-byte rows (chunk c of row r at
+// c ^ ((r >> 1) & 3): conflict-free 16-byte reads of 8 consecutive rows), filled by direct-to-LDS
+// loads (a wave instruction fills 16 rows) issued from inline assembly and waited for by this
+// wave's vmcnt. Step k (stage S(k)): wait for step k + 1's loads and barrier (every wave has read
+// S(k) into registers during step k - 1), then the MFMAs of step k with step k + 1's operand reads
+// (A row i into its registers right after row i's last MFMA, B into the second set) and the loads
+// of step k + 3 into S(k) placed between them. K % 64 == 0 and K >= 128 keep the register sets'
+// roles fixed at compile time (a step count that is even and at least 4; alternating roles under
+// a runtime branch made the allocator copy the accumulators). Per output element the 32-wide
+// slices accumulate in ascending K order with the same instruction as k_gemm_f16, and the SiLU
+// epilogue (through LDS, 16-byte stores) uses its formula and rounding, so the two give the same
+// bits. Tiles go in rounds of one workgroup per CU: XCD k runs ceil(slots / 8) row tiles x 8
+// column tiles per round, so its workgroups share A and W rows in its L2.
+constexpr int kSbBM = 256, kSbBN = 256, kSbK = 32, kSbRows = kSbBM + kSbBN, kSbSch = kSbRows * 4;
+constexpr size_t kSbLds = (size_t)3 * kSbRows * 64;
+constexpr int64_t kSbMinM = 31 * kSbBM + 1;
+
+__global__ __launch_bounds__(512) void k_gemm_h16_silu_dl(GemmF16Args p) {
+    extern __shared__ uint4 sls[];  // three stages of kSbRows 64-byte rows
+    const int tid = threadIdx.x, l = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = 64 * (w & 3), wn = 128 * (w >> 2);
+    const int64_t NT = (p.N + kSbBN - 1) / kSbBN, MT = (p.M + kSbBM - 1) / kSbBM;
+    const int64_t G = p.round_wgs, Q = G / 8, MQ = (Q + 7) / 8, R = (NT + 7) / 8;
+    const int64_t lin = blockIdx.x, ri = lin / G, x = lin % G, xk = x % 8, xj = x / 8;
+    const int64_t tm = ((ri / R) * 8 + xk) * MQ + xj / 8, tn = 8 * (ri % R) + xj % 8;
+    if (tm >= MT || tn >= NT) return;
+    const int64_t bm = tm * kSbBM, bn = tn * kSbBN;
+    // loads: 16-row blocks bb = w + 8 d (d < 4): row 16 bb + (l >> 2), chunk (l & 3) ^ ((l >> 3) & 3)
+    const _Float16* src[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const int bb = w + 8 * d, rr = 16 * bb + (l >> 2), c = (l & 3) ^ ((l >> 3) & 3);
+        if (rr < kSbBM) {
+            const int64_t m = bm + rr;
+            src[d] = p.ah + (m < p.M ? m : p.M - 1) * p.lda + 8 * c;
+        } else {
+            const int64_t n = bn + rr - kSbBM;
+            src[d] = p.w + (n < p.N ? n : p.N - 1) * p.K + 8 * c;
+        }
+    }
+    const uint32_t lbase = (uint32_t)(uintptr_t)(&sls[0]);
+    auto load = [&](int64_t kk, int stage_chunk, int d) {
+        dl_load16(src[d] + kk * kSbK, lbase + (uint32_t)(stage_chunk + 64 * (w + 8 * d)) * 16);
+    };
+    f4v acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = f4v{0.f, 0.f, 0.f, 0.f};
+    const int li = l & 15, lq = l >> 4;
+    const int pos = lq ^ ((li >> 1) & 3);
+    const int aoff = (wm + li) * 4 + pos, boff = (kSbBM + wn + li) * 4 + pos;
+    h8 ra[4], rb0[8], rb1[8];
+    // MFMAs of one step (A operands ra, B operands bv) with the next step's operand reads from
+    // stage chunk rdn (A row i overwrites ra[i] right after row i's last MFMA; B into nb) and
+    // this step's loads (step kk into stage chunk wr) spread between them
+    auto part = [&](const h8(&bv)[8], h8(&nb)[8], int rdn, bool rnext, int wr, int64_t kk, bool ld) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ra[i], bv[j], acc[i][j], 0, 0, 0);
+                const int q = i * 8 + j;
+                if (rnext && j == 7) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    ra[i] = *reinterpret_cast<const h8*>(&sls[rdn + aoff + 64 * i]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if (rnext && (q & 3) == 1) {
+                    const int r = q >> 2;  // 0..7
+                    __builtin_amdgcn_sched_barrier(0);
+                    nb[r] = *reinterpret_cast<const h8*>(&sls[rdn + boff + 64 * r]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                if (ld && (q & 7) == 3) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    load(kk, wr, q >> 3);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+    };
+    auto nxt = [](int c) { return c == 2 * kSbSch ? 0 : c + kSbSch; };
+    const int nk = (int)(p.K / kSbK);  // even, >= 4 (checked by the host)
+    for (int s = 0; s < 3; ++s)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) load(s, s * kSbSch, d);
+    dl_wait_loads<8>();
+    dl_barrier();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ra[i] = *reinterpret_cast<const h8*>(&sls[aoff + 64 * i]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) rb0[j] = *reinterpret_cast<const h8*>(&sls[boff + 64 * j]);
+    int rd = 0, k = 0;
+    // step k: wait for step k + 1's loads, barrier (every wave has read stage S(k) into
+    // registers), then MFMAs of step k | reads of step k + 1 | loads of step k + 3 into S(k)
+    for (; k + 4 < nk; k += 2) {
+        dl_wait_loads<4>();
+        dl_barrier();
+        part(rb0, rb1, nxt(rd), true, rd, k + 3, true);
+        rd = nxt(rd);
+        dl_wait_loads<4>();
+        dl_barrier();
+        part(rb1, rb0, nxt(rd), true, rd, k + 4, true);
+        rd = nxt(rd);
+    }
+    // the last four steps: k = nk - 4 .. nk - 1
+    dl_wait_loads<4>();
+    dl_barrier();
+    part(rb0, rb1, nxt(rd), true, rd, k + 3, true);
+    rd = nxt(rd);
+    dl_wait_loads<4>();
+    dl_barrier();
+    part(rb1, rb0, nxt(rd), true, rd, 0, false);
+    rd = nxt(rd);
+    dl_wait_loads<0>();
+    dl_barrier();
+    part(rb0, rb1, nxt(rd), true, rd, 0, false);
+    rd = nxt(rd);
+    dl_wait_loads<0>();
+    dl_barrier();
+    part(rb1, rb0, 0, false, rd, 0, false);
+    __syncthreads();
+    // SiLU epilogue: tiles 2 c and 2 c + 1 are gate and up of 16 ffn columns
+    constexpr int EH = 64 + 8;
+    _Float16* eh = reinterpret_cast<_Float16*>(sls) + w * 64 * EH;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float g = acc[i][2 * c][r], u = acc[i][2 * c + 1][r];
+                float y = (g * (1.0f / (1.0f + expf(-g)))) * u;
+                asm volatile("" : "+v"(y));
+                eh[(16 * i + 4 * lq + r) * EH + 16 * c + li] = (_Float16)y;
+            }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
+    const int64_t m0 = bm + wm, f0 = (bn + wn) / 2, ffn = p.N / 2;
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+        const int idx = it * 64 + l, row = idx / 8, c8 = idx % 8;
+        const int64_t m = m0 + row, f = f0 + 8 * c8;
+        if (m < p.M && f < ffn)
+            *reinterpret_cast<uint4*>(p.ch + m * p.ldc + f) = *reinterpret_cast<const uint4*>(&eh[row * EH + 8 * c8]);
+    }
+}
 }  // namespace pe
 
 using namespace pe;
@@ -470,24 +627,33 @@ static bool dl_configure() {
 // row strides % 4, and a device with the LDS the three stages need. The tile width WTN (16 WTN
 // columns) takes the fewest waves of workgroups over the CUs times the tile width, so a grid of
 // one workgroup per CU wins over a wider tile needing two rounds.
-static bool dl_try(const GemmF16Args& p, hipStream_t s, int* status) {
-    if (p.M < kDlMinM || p.K % kDlK || p.N % 16 || !aligned(p.c, 16) || p.ldc % 4 ||
-        (p.bias && !aligned(p.bias, 16)) || (p.res && (!aligned(p.res, 16) || p.ldr % 4)))
-        return false;
+// The device's CU count once the direct-to-LDS kernels may run on it (their LDS limits set), else 0.
+static int dl_device_cus() {
     int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
     int state = g_dl_lds[dev].load(std::memory_order_acquire);
     if (state == 0) {
         int max_lds = 0;
         if (hipDeviceGetAttribute(&max_lds, hipDeviceAttributeSharedMemPerBlockOptin, dev) != hipSuccess || max_lds <= 0)
             (void)hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
         const bool ok = max_lds >= (int)dl_lds_bytes<9>() && dl_configure<6>() && dl_configure<7>() &&
-                        dl_configure<8>() && dl_configure<9>();
+                        dl_configure<8>() && dl_configure<9>() &&
+                        hipFuncSetAttribute((const void*)k_gemm_h16_silu_dl, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            (int)kSbLds) == hipSuccess;
         state = ok ? 1 : -1;
         g_dl_lds[dev].store(state, std::memory_order_release);
     }
-    if (state < 0) return false;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return false;
+    if (state < 0) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
+    return cus;
+}
+
+static bool dl_try(const GemmF16Args& p, hipStream_t s, int* status) {
+    if (p.M < kDlMinM || p.K % kDlK || p.N % 16 || !aligned(p.c, 16) || p.ldc % 4 ||
+        (p.bias && !aligned(p.bias, 16)) || (p.res && (!aligned(p.res, 16) || p.ldr % 4)))
+        return false;
+    const int cus = dl_device_cus();
+    if (!cus) return false;
     const int64_t mt = (p.M + kDlBM - 1) / kDlBM;
     int best = 0;
     int64_t best_cost = 0;
@@ -505,6 +671,24 @@ static bool dl_try(const GemmF16Args& p, hipStream_t s, int* status) {
         case 8: *status = dl_launch<8>(p, s); break;
         default: *status = dl_launch<9>(p, s); break;
     }
+    return true;
+}
+
+// pe_gemm_h16_silu_h on k_gemm_h16_silu_dl when M > 31 * 256, K % 64 == 0, K >= 128, the output
+// is 16-byte aligned with ldc % 8 == 0 and the device has at least 8 CUs (else false: the caller
+// uses k_gemm_f16). Grid: rounds of round_wgs = CUs rounded down to a multiple of 8.
+static bool silu_dl_try(const GemmF16Args& p, hipStream_t s, int* status) {
+    if (p.M < kSbMinM || p.K % 64 || p.K < 128 || !aligned(p.ch, 16) || p.ldc % 8) return false;
+    const int cus = dl_device_cus();
+    if (cus < 8) return false;
+    GemmF16Args q = p;
+    q.round_wgs = cus / 8 * 8;
+    const int64_t NT = (p.N + kSbBN - 1) / kSbBN, MT = (p.M + kSbBM - 1) / kSbBM;
+    const int64_t Q = q.round_wgs / 8, MQ = (Q + 7) / 8, R = (NT + 7) / 8;
+    const int64_t rounds = R * ((MT + 8 * MQ - 1) / (8 * MQ));
+    if (rounds * q.round_wgs > 0x7FFFFFFF) return false;
+    hipLaunchKernelGGL(k_gemm_h16_silu_dl, dim3((unsigned)(rounds * q.round_wgs)), dim3(512), kSbLds, s, q);
+    *status = launch_status();
     return true;
 }
 
@@ -534,6 +718,10 @@ static int gemm_silu_entry(const void* a, int64_t lda, const void* w_f16_il, voi
                   (const _Float16*)w_f16_il, nullptr, nullptr, 0,
                   CH ? nullptr : (float*)c, CH ? (_Float16*)c : nullptr, ldc, M, N, K};
     hipStream_t s = (hipStream_t)stream;
+    if constexpr (AH && CH) {
+        int st = PE_OK;
+        if (silu_dl_try(p, s, &st)) return st;
+    }
     if (gf_short(M, N))
         hipLaunchKernelGGL((k_gemm_f16<2, false, false, true, AH, CH>), gf_grid<2>(M, N), dim3(256), 0, s, p);
     else

@@ -983,11 +983,15 @@ def test_gemm_f16_silu_half_output_and_down_product(K, M, ffn, Kd):
 
 
 @pytest.mark.parametrize("M,ffn,Kd", [(300, 4864, 896), (13, 512, 3584), (129, 48, 96), (8192, 256, 64),
-                                      (8192, 4864, 896), (1100, 48, 128), (2048, 1008, 64)])
+                                      (8192, 4864, 896), (1100, 48, 128), (2048, 1008, 64),
+                                      (8000, 1008, 128), (7937, 16, 192), (9000, 2448, 896), (7936, 4864, 896)])
 def test_gemm_h16_silu_equals_fp32_operand_path(K, M, ffn, Kd):
     """The SiLU GEMM on an fp16 A (pe_gemm_h16_silu_h) gives the bits of the fp32-A GEMM on the
     A those fp16 values came from (the fp32 path rounds A the same way as it reads it), and so
-    does an fp16 A from rmsnorm(half=True) against the fp32 norm."""
+    does an fp16 A from rmsnorm(half=True) against the fp32 norm. From M = 7937 with K % 64 == 0
+    and K >= 128 the fp16 product runs on the 256 x 256 tile kernel (ragged row and column tiles
+    here, K at its minimum 128 and an odd multiple of 64), below that and for the fp32 A on the
+    128 x 128 one."""
     rng = np.random.default_rng(M + ffn + 5)
     a = torch.from_numpy(rng.standard_normal((M, Kd)).astype(np.float32)).to(DEV)
     w16 = torch.from_numpy((rng.standard_normal((2 * ffn, Kd)) * 0.05).astype(np.float16)).to(DEV)
