@@ -23,6 +23,8 @@
 // scheduled so that light blocks share CUs with heavy ones.
 #include "pe_common.h"
 
+#include <type_traits>
+
 namespace pe {
 
 typedef _Float16 fh8 __attribute__((ext_vector_type(8)));
@@ -52,13 +54,13 @@ struct FlashParams {
     float scale;
     float* out;          // (L, n_head, 64), token rows out_stride elements apart
     int64_t out_stride;
-    const uint8_t* kv16; // BLK: the fp16 K / V^T key blocks of pe_rope_kv_write_blocks
-    int64_t kv16_blocks; // BLK: key blocks per kv head in kv16
+    const uint8_t* kv16; // k_flash_prefill_blocks: the fp16 K / V^T key blocks of pe_rope_kv_write_blocks
+    int64_t kv16_blocks; // k_flash_prefill_blocks: key blocks per kv head in kv16
 };
 
-constexpr int kFpBlkSlots = 4;  // BLK: LDS ring depth (16 KB per key block)
+constexpr int kFpBlkSlots = 4;  // k_flash_prefill_blocks: LDS ring depth (16 KB per key block)
 
-// BLK: 16 bytes per lane from global g into LDS at m0 + 16 lane (one wave instruction: 1 KB)
+// 16 bytes per lane from global g into LDS at m0 + 16 lane (one wave instruction: 1 KB)
 PE_DEV void fp_load16(const void* g, uint32_t m0) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
 }
@@ -82,24 +84,16 @@ PE_DEV fh8 f8_to_h8(float4 a, float4 b) {
 
 // OutT _Float16: the output rounded to fp16 (nearest even), the operand of the o-projection
 // GEMM (p.out then points to fp16 rows).
-// BLK: K and V^T come as fp16 blocks already laid out as LDS images (pe_rope_kv_write_blocks:
-// 64 rows of 128 bytes, chunk c at position c ^ (row & 7), which keeps the 16-byte operand
-// reads of 8 consecutive rows on all 32 banks) and are copied by direct-to-LDS loads, waves 0-7
-// two 1 KB instructions each per block, into a ring of kFpBlkSlots blocks: the loads of block
-// b + 3 are issued in the step of block b, right after the barrier that frees its slot, and
-// waited for with this wave's own vmcnt count. Without BLK, waves 0-7 load fp32 K / V,
-// convert and store them into a ring of kFpStages padded blocks. The products are the same
-// either way (the same fp16 values in the same operand positions).
-template <typename OutT, bool BLK>
+template <typename OutT>
 __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_size) {
-    // LDS ring of K / V^T blocks: block b is staged in slot b % (ring depth)
-    constexpr int kKs = BLK ? kFpBlkSlots * kFpKeys * kFpHd : kFpStages * kFpKeys * kFpRow;
-    constexpr int kVs = BLK ? kFpBlkSlots * kFpHd * kFpKeys : kFpStages * kFpHd * kFpRow;
-    constexpr int kSlotHalves = BLK ? kFpKeys * kFpHd : kFpKeys * kFpRow;  // one block's K (or V^T)
+    // LDS ring of K / V^T blocks: block b is staged in slot b % kFpStages
+    constexpr int kKs = kFpStages * kFpKeys * kFpRow;
+    constexpr int kVs = kFpStages * kFpHd * kFpRow;
+    constexpr int kSlotHalves = kFpKeys * kFpRow;  // one block's K (or V^T)
     __shared__ __align__(16) _Float16 ks[kKs];  // K blocks, [key][dim]
     __shared__ __align__(16) _Float16 vt[kVs];  // V blocks transposed, [dim][key]
     // LDS element offset of 16-byte chunk c of row `row` within a block
-    auto lofs = [](int row, int c) { return BLK ? row * kFpHd + 8 * (c ^ (row & 7)) : row * kFpRow + 8 * c; };
+    auto lofs = [](int row, int c) { return row * kFpRow + 8 * c; };
     const int t = threadIdx.x, l = t & 63;
     const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave index (wave-uniform)
     const int li = l & 15, lg = l >> 4;
@@ -152,7 +146,6 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
     // position (masked out of the scores).
     float4 r4[4];
     auto kv_load = [&](int j0) {
-        if constexpr (BLK) return;
         if (w < 4) {
             const int kg = t & 15, d4 = t >> 4;
 #pragma unroll
@@ -175,7 +168,6 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
     // consecutive slots, one 8-byte store per dim (16 threads fill 128 contiguous bytes).
     auto stage = [&](int slot) {
         typedef _Float16 fh4 __attribute__((ext_vector_type(4)));
-        if constexpr (BLK) return;
         if (w < 4) {
             _Float16* vd = vt + slot * (kFpHd * kFpRow);
             const int kg = t & 15, d4 = t >> 4;
@@ -278,56 +270,7 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
     // barrier after block b's staging, so none still reads block b - 1's K (its scores were
     // computed before that barrier) and the slowest still reads only block b's K / V (slot
     // b % 3) and block b - 1's V (slot (b - 1) % 3).
-    if constexpr (BLK) {
-        // key block b of this kv head: 16 wave instructions of 1 KB (8 for K, 8 for V^T), two
-        // per wave for waves 0-7
-        const uint8_t* kvh_blocks = p.kv16 + (int64_t)kvh * p.kv16_blocks * 16384 + 16 * l;
-        const uint32_t ks_base = (uint32_t)(uintptr_t)ks, vt_base = (uint32_t)(uintptr_t)vt;
-        auto blk_load = [&](int b) {
-            if (w >= 8) return;
-            const int slot = b & (kFpBlkSlots - 1);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int q = 2 * w + i, half = q >> 3, part = q & 7;
-                fp_load16(kvh_blocks + (int64_t)b * 16384 + half * 8192 + part * 1024,
-                          (half ? vt_base : ks_base) + (uint32_t)(slot * kSlotHalves * 2 + part * 1024));
-            }
-        };
-        blk_load(0);
-        if (nblk > 1) blk_load(1);
-        if (nblk > 2) blk_load(2);
-        if (nblk > 2) fp_wait_loads<4>();
-        else if (nblk > 1) fp_wait_loads<2>();
-        else fp_wait_loads<0>();
-        fp_lds_barrier();
-        fv4 sa[4], sb[4];
-        scores(0, sa);
-        // block b: wait for block b + 1's loads (block b + 2's may stay in flight), barrier
-        // (every wave is past block b - 1, whose slot takes block b + 3), then block b + 1's
-        // scores and block b's softmax and P.V
-        auto step = [&](int b, fv4 (&cur)[4], fv4 (&nxt)[4]) {
-            if (b + 2 < nblk) fp_wait_loads<2>();
-            else fp_wait_loads<0>();
-            fp_lds_barrier();
-            if (b + 3 < nblk) blk_load(b + 3);
-            mask(b * kFpKeys, cur);
-            scores((b + 1) & (kFpBlkSlots - 1), nxt);
-            softmax_pv(cur, b & (kFpBlkSlots - 1));
-        };
-        int b = 0;
-        for (; b + 2 < nblk; b += 2) {
-            step(b, sa, sb);
-            step(b + 1, sb, sa);
-        }
-        if (b + 1 < nblk) {
-            step(b, sa, sb);
-            mask((b + 1) * kFpKeys, sb);
-            softmax_pv(sb, (b + 1) & (kFpBlkSlots - 1));
-        } else {
-            mask(b * kFpKeys, sa);
-            softmax_pv(sa, b & (kFpBlkSlots - 1));
-        }
-    } else {
+    {
         kv_load(0);
         stage(0);
         __syncthreads();
@@ -380,6 +323,195 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
             }
     }
 }
+
+// The same attention of a prompt from position 0 with K and V^T read from the fp16 key blocks
+// of pe_rope_kv_write_blocks, which are already laid out as LDS images (64 rows of 128 bytes,
+// chunk c at position c ^ (row & 7), so the 16-byte operand reads of 8 consecutive rows fall
+// on all 32 banks). A wave computes two 16-query tiles of one query head (queries q0 .. q0 + 31):
+// per 64-key block both tiles' score MFMAs, then tile 0's softmax and P.V, then tile 1's, so
+// one tile's vector work runs while the other's matrix work is in the pipe, and every K / V^T
+// operand read from LDS serves 32 queries. Workgroup = QS sets of 32 queries x the group's
+// query heads (QS = 1 from 4 heads per kv head up, so at least 4 waves: 7 for the 0.5B model,
+// two workgroups per CU at 64 KB of LDS each). The blocks are copied by direct-to-LDS loads (the
+// first LW waves, 16 / LW instructions of 1 KB each per block) into a ring of kFpBlkSlots
+// slots: block b + 3's loads are issued after the barrier of block b (every wave is then past
+// block b - 1, whose slot they overwrite) and waited for with the wave's own vmcnt count. The
+// blocks a wave's 32 queries all see in full run without the causal mask (no branch in the
+// loop body), the rest with it. Per query the products, the softmax and their order are
+// k_flash_prefill's, so the results are the same bits.
+template <int LW>
+__global__ __launch_bounds__(1024) void k_flash_prefill_blocks(FlashParams p, int qb_size) {
+    constexpr int kSlotHalves = kFpKeys * kFpHd;  // one block's K (or V^T), fp16
+    constexpr int NL = 16 / LW;                    // load instructions per loading wave and block
+    __shared__ __align__(16) _Float16 ks[kFpBlkSlots * kSlotHalves];  // K blocks, [key][dim]
+    __shared__ __align__(16) _Float16 vt[kFpBlkSlots * kSlotHalves];  // V^T blocks, [dim][key slot]
+    auto lofs = [](int row, int c) { return row * kFpHd + 8 * (c ^ (row & 7)); };
+    const int t = threadIdx.x, l = t & 63;
+    const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int li = l & 15, lg = l >> 4;
+    // heaviest query blocks first, paired with light ones (k_flash_prefill's order)
+    const int64_t nqb = (p.L + qb_size - 1) / qb_size;
+    const int64_t total = nqb * p.n_kv, half = (total + 1) / 2, lin = blockIdx.x;
+    const int64_t rank = lin < half ? lin : total - 1 - (lin - half);
+    const int64_t qb = nqb - 1 - rank / p.n_kv;
+    const int kvh = (int)(rank % p.n_kv);
+    const int h = kvh * p.group + w % p.group;
+    const int64_t q0 = qb * qb_size + 32 * (w / p.group);
+    const int n_keys = (int)p.L;
+    const float NEG_INF = -__builtin_huge_valf();
+    const float sl2 = p.scale * 1.4426950408889634f;
+
+    fh8 qa[2][2];  // tile tt: row li = query q0 + 16 tt + li, dims 32 s + 8 lg .. + 8
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int64_t qi = q0 + 16 * tt + li < p.L ? q0 + 16 * tt + li : p.L - 1;
+        const float* qr = p.q + qi * p.q_stride + (int64_t)h * kFpHd;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const float4 a = *reinterpret_cast<const float4*>(qr + 32 * s + 8 * lg);
+            const float4 b = *reinterpret_cast<const float4*>(qr + 32 * s + 8 * lg + 4);
+            qa[tt][s] = f8_to_h8(a, b);
+        }
+    }
+    float m_run[2] = {NEG_INF, NEG_INF}, l_run[2] = {0.f, 0.f};
+    fv4 o[2][4];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) o[tt][d] = fv4{0.f, 0.f, 0.f, 0.f};
+    const int64_t q_last = (qb + 1) * qb_size - 1 < p.L - 1 ? (qb + 1) * qb_size - 1 : p.L - 1;
+    const int nblk = (int)((q_last + kFpKeys) / kFpKeys);  // blocks this workgroup's queries see
+
+    // S^T = K Q^T of one tile for the block in ring slot `slot`
+    auto scores = [&](int slot, const fh8 (&qq)[2], fv4 (&s)[4]) {
+        const _Float16* kd = ks + slot * kSlotHalves;
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+            s[jt] = fv4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const fh8 kbv = *reinterpret_cast<const fh8*>(kd + lofs(16 * jt + li, 4 * u + lg));
+                s[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kbv, qq[u], s[jt], 0, 0, 0);
+            }
+        }
+    };
+    auto mask = [&](int j0, int64_t qt0, fv4 (&s)[4]) {
+        const int qpos = (int)qt0 + li;
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = j0 + 16 * jt + 4 * lg + r;
+                if (!(key <= qpos && key < n_keys)) s[jt][r] = NEG_INF;
+            }
+    };
+    // k_flash_prefill's online softmax and O^T += V^T P^T for one tile
+    auto softmax_pv = [&](const fv4 (&s)[4], int slot, float& mr, float& lr, fv4 (&oo)[4]) {
+        float mx = NEG_INF;
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[jt][r]);
+        mx = swap32_max(swap16_max(mx));
+        const float m_new = fmaxf(mr, mx * sl2);
+        float psum = 0.f;
+        fh8 pb[2];
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float e = __builtin_amdgcn_exp2f(fmaf(s[jt][r], sl2, -m_new));
+                psum += e;
+                pb[jt >> 1][4 * (jt & 1) + r] = (_Float16)e;
+            }
+        psum = swap32_sum(swap16_sum(psum));
+        if (__builtin_amdgcn_ballot_w64(m_new != mr)) {
+            const float corr = __builtin_amdgcn_exp2f(mr - m_new);
+            lr = lr * corr + psum;
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) oo[d][r] *= corr;
+        } else {
+            lr = lr + psum;
+        }
+        mr = m_new;
+        const _Float16* vd = vt + slot * kSlotHalves;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const fh8 va = *reinterpret_cast<const fh8*>(vd + lofs(16 * d + li, 4 * u + lg));
+                oo[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[u], oo[d], 0, 0, 0);
+            }
+        }
+    };
+    // block b of this kv head: 16 instructions of 1 KB (8 for K, 8 for V^T), NL per loading wave
+    const uint8_t* kvh_blocks = p.kv16 + (int64_t)kvh * p.kv16_blocks * 16384 + 16 * l;
+    const uint32_t ks_base = (uint32_t)(uintptr_t)ks, vt_base = (uint32_t)(uintptr_t)vt;
+    auto blk_load = [&](int b) {
+        if (w >= LW) return;
+        const int slot = b & (kFpBlkSlots - 1);
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int q = NL * w + i, hf = q >> 3, part = q & 7;
+            fp_load16(kvh_blocks + (int64_t)b * 16384 + hf * 8192 + part * 1024,
+                      (hf ? vt_base : ks_base) + (uint32_t)(slot * kSlotHalves * 2 + part * 1024));
+        }
+    };
+    auto body = [&](int b, auto masked) {
+        const int slot = b & (kFpBlkSlots - 1);
+        fv4 s0[4], s1[4];
+        scores(slot, qa[0], s0);
+        scores(slot, qa[1], s1);
+        if constexpr (decltype(masked)::value) {
+            mask(b * kFpKeys, q0, s0);
+            mask(b * kFpKeys, q0 + 16, s1);
+        }
+        softmax_pv(s0, slot, m_run[0], l_run[0], o[0]);
+        softmax_pv(s1, slot, m_run[1], l_run[1], o[1]);
+    };
+    blk_load(0);
+    if (nblk > 1) blk_load(1);
+    if (nblk > 2) blk_load(2);
+    // Each wave passes one barrier per block in both loops, with the same waits and loads for
+    // the same b, so waves whose unmasked prefix differs (QS > 1) stay matched.
+    const int nfull = (int)((q0 + 1) / kFpKeys) < nblk ? (int)((q0 + 1) / kFpKeys) : nblk;
+    const int nsteady = nfull < nblk - 3 ? nfull : nblk - 3;
+    int b = 0;
+    for (; b < nsteady; ++b) {
+        fp_wait_loads<2 * NL>();  // block b + 1's loads are done, b + 2's may be in flight
+        fp_lds_barrier();
+        blk_load(b + 3);
+        body(b, std::false_type{});
+    }
+    for (; b < nblk; ++b) {
+        if (b + 2 < nblk) fp_wait_loads<2 * NL>();
+        else if (b + 1 < nblk) fp_wait_loads<NL>();
+        else fp_wait_loads<0>();
+        fp_lds_barrier();
+        if (b + 3 < nblk) blk_load(b + 3);
+        body(b, std::true_type{});  // the mask changes nothing in a fully visible block
+    }
+
+    // out: O[query][dim 16 d + 4 lg + r] / l, rounded to fp16
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int64_t qi = q0 + 16 * tt + li;
+        if (qi < p.L) {
+            _Float16* orow = reinterpret_cast<_Float16*>(p.out) + qi * p.out_stride + (int64_t)h * kFpHd;
+            const float inv = 1.0f / l_run[tt];
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float v = o[tt][d][r] * inv;
+                    asm volatile("" : "+v"(v));  // rounded to fp16 as a value of its own
+                    orow[16 * d + 4 * lg + r] = (_Float16)v;
+                }
+        }
+    }
+}
 }  // namespace pe
 
 using namespace pe;
@@ -403,16 +535,25 @@ static int flash_prefill(const float* q, int64_t q_stride, const float* k_cache,
         return PE_ERR_ALIGN;
     FlashParams p{q, q_stride, k_cache, v_cache, n_head / n_kv, n_kv, capacity, L, pos0, scale, (float*)out,
                   out_stride, (const uint8_t*)kv16, kv16_blocks};
+    if (kv16) {
+        // QS sets of 32 queries per workgroup, at least 4 waves (the loading waves)
+        const int qs = group >= 4 ? 1 : (4 + group - 1) / group, waves = group * qs, qb2 = 32 * qs;
+        const int64_t nb2 = (L + qb2 - 1) / qb2 * (int64_t)n_kv;
+        if (nb2 > 0x7FFFFFFF) return PE_ERR_SHAPE;
+        if (waves >= 8)
+            hipLaunchKernelGGL(k_flash_prefill_blocks<8>, dim3((unsigned)nb2), dim3(64 * waves), 0, (hipStream_t)stream, p, qb2);
+        else
+            hipLaunchKernelGGL(k_flash_prefill_blocks<4>, dim3((unsigned)nb2), dim3(64 * waves), 0, (hipStream_t)stream, p, qb2);
+        return launch_status();
+    }
     const int waves = group * (qb / 16);  // 9..16 (kv_load and stage use the first 8 waves)
     const int64_t nblocks = (L + qb - 1) / qb * (int64_t)n_kv;
     if (nblocks > 0x7FFFFFFF) return PE_ERR_SHAPE;
     const dim3 grid((unsigned)nblocks);
-    if (kv16)
-        hipLaunchKernelGGL((k_flash_prefill<_Float16, true>), grid, dim3(64 * waves), 0, (hipStream_t)stream, p, qb);
-    else if (half_out)
-        hipLaunchKernelGGL((k_flash_prefill<_Float16, false>), grid, dim3(64 * waves), 0, (hipStream_t)stream, p, qb);
+    if (half_out)
+        hipLaunchKernelGGL(k_flash_prefill<_Float16>, grid, dim3(64 * waves), 0, (hipStream_t)stream, p, qb);
     else
-        hipLaunchKernelGGL((k_flash_prefill<float, false>), grid, dim3(64 * waves), 0, (hipStream_t)stream, p, qb);
+        hipLaunchKernelGGL(k_flash_prefill<float>, grid, dim3(64 * waves), 0, (hipStream_t)stream, p, qb);
     return launch_status();
 }
 

@@ -1053,12 +1053,15 @@ def _kv16_layout_ref(k, v, length):
 
 
 @pytest.mark.parametrize("L", [1, 64, 77, 300, 1000])
-@pytest.mark.parametrize("n_head,n_kv", [(14, 2), (8, 8), (16, 1), (9, 3)])
+@pytest.mark.parametrize("n_head,n_kv", [(14, 2), (8, 8), (16, 1), (9, 3), (4, 2), (16, 2)])
 def test_flash_prefill_blocks_equals_fp32_cache_path(K, L, n_head, n_kv):
     """The RoPE pass writing the fp16 key blocks (pe_rope_kv_write_blocks) leaves the caches and
     q as pe_rope_kv_write does and fills the blocks as the numpy restatement of their layout
-    says; flash attention from the blocks (pe_flash_prefill_blocks, direct-to-LDS copies) gives
-    the bits of pe_flash_prefill_h16 on the fp32 caches."""
+    says; flash attention from the blocks (pe_flash_prefill_blocks: two 16-query tiles per wave,
+    direct-to-LDS copies) gives the bits of pe_flash_prefill_h16 on the fp32 caches. Groups of 1,
+    2 and 3 query heads per kv head put 4, 2 and 2 sets of 32 queries in a workgroup (waves
+    whose unmasked prefixes differ), 7 the 0.5B model's shape, 8 and 16 the eight loading
+    waves."""
     rng = np.random.default_rng(L + 31 * n_head + n_kv)
     hd, cap = 64, L + 5
     qkv = torch.from_numpy(rng.standard_normal((L, (n_head + 2 * n_kv) * hd)).astype(np.float32)).to(DEV)
