@@ -100,12 +100,12 @@ __global__ void k_kv_write(const float* __restrict__ ks, const float* __restrict
 // Flash-attention key blocks (kv16, head_dim 64, pe_rope_kv_write_blocks): per kv head, per
 // 64-key block b, the fp16 K block [key][dim] and then the fp16 V^T block [dim][key slot], each
 // 64 rows of 128 bytes whose 16-byte chunk c sits at chunk position c ^ (row & 7) -- the LDS
-// image k_flash_prefill reads, so it copies a block with direct-to-LDS loads. V^T's key slots
-// follow the P^T operand: in each 32-key slab, slot 8 g + i holds key 4 g + i (i < 4) or
-// 16 + 4 g + (i - 4) (i >= 4).
-PE_DEV int kv16_slot(int key) {  // key within its 64-key block -> V^T column
-    const int kw = key & 31, hi = kw >> 4, r = kw & 15;
-    return 32 * (key >> 5) + 8 * (r >> 2) + 4 * hi + (r & 3);
+// image k_flash_prefill_blocks reads, so it copies a block with direct-to-LDS loads. V^T's key
+// slots follow the P^T operand: in each 32-key slab, slot 8 g + i holds key 4 g + i (i < 4) or
+// 16 + 4 g + (i - 4) (i >= 4). K rows are written by the k items (8-byte pieces); V^T by items
+// of their own after the token items, one 16-byte chunk (8 key slots of one dim row) each.
+PE_DEV int kv16_chunk_key(int c, int i) {  // key (within its 64-key block) of slot 8 c + i
+    return 32 * (c >> 2) + 16 * (i >> 2) + 4 * (c & 3) + (i & 3);
 }
 PE_DEV int64_t kv16_chunk_byte(int row, int chunk) { return (int64_t)row * 128 + 16 * (chunk ^ (row & 7)); }
 
@@ -117,9 +117,42 @@ __global__ void k_rope_kv_write(const float* __restrict__ qkv, int64_t qs, const
     const int nq4 = n_head * h4, nk4 = n_kv * h4, nv4 = n_kv * (hd / 4);
     const int per = nq4 + nk4 + nv4;
     const int total = L * per;
+    // kv16: V^T chunk items after the token items, (kv head, block, dim row, chunk) with the
+    // chunk fastest, so a wave writes 8 whole 128-byte V^T rows (1 KB)
+    const int64_t blk0 = pos0 >> 6;
+    const int nvt = kv16 ? n_kv * (int)(((pos0 + L - 1) >> 6) - blk0 + 1) * 512 : 0;
     const int stride = gridDim.x * blockDim.x;
     const int half = hd / 2;
-    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total + nvt; idx += stride) {
+        if (idx >= total) {
+            // chunk c of V^T row d of block b: slots 8 c .. 8 c + 7
+            const int i2 = idx - total, c = i2 & 7, d = (i2 >> 3) & 63, rest = i2 >> 9;
+            const int nbt = (int)(((pos0 + L - 1) >> 6) - blk0 + 1);
+            const int hh = rest / nbt;
+            const int64_t b = blk0 + (rest - hh * nbt);
+            const float* vcol = qkv + (int64_t)(n_head + n_kv + hh) * hd + d;
+            typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+            h8v hv;
+            bool all = true;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int64_t l = 64 * b + kv16_chunk_key(c, i) - pos0;
+                const bool ok = l >= 0 && l < L;
+                all = all && ok;
+                hv[i] = ok ? (_Float16)vcol[l * qs] : (_Float16)0.f;
+            }
+            uint8_t* dst = kv16 + ((int64_t)hh * kv16_blocks + b) * 16384 + 8192 + kv16_chunk_byte(d, c);
+            if (all) {
+                *reinterpret_cast<h8v*>(dst) = hv;
+            } else {  // a block the call only partly covers: its other keys keep their values
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int64_t l = 64 * b + kv16_chunk_key(c, i) - pos0;
+                    if (l >= 0 && l < L) reinterpret_cast<_Float16*>(dst)[i] = hv[i];
+                }
+            }
+            continue;
+        }
         const int l = idx / per, it = idx - l * per;
         const float* row = qkv + (int64_t)l * qs;
         if (it < nq4 + nk4) {
@@ -153,16 +186,6 @@ __global__ void k_rope_kv_write(const float* __restrict__ qkv, int64_t qs, const
             const int iv = it - nq4 - nk4, hh = iv / (hd / 4), d = 4 * (iv - hh * (hd / 4));
             const float4 v = *reinterpret_cast<const float4*>(row + (int64_t)(n_head + n_kv + hh) * hd + d);
             *reinterpret_cast<float4*>(vc + ((int64_t)hh * cap + pos0 + l) * hd + d) = v;
-            if (kv16) {  // V^T rows d .. d + 3 at this key's slot
-                const int64_t key = pos0 + l;
-                uint8_t* blk = kv16 + ((int64_t)hh * kv16_blocks + (key >> 6)) * 16384 + 8192;
-                const int slot = kv16_slot((int)(key & 63));
-                const float vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    *reinterpret_cast<_Float16*>(blk + kv16_chunk_byte(d + e, slot >> 3) + 2 * (slot & 7)) =
-                        (_Float16)vv[e];
-            }
         }
     }
 }
@@ -310,13 +333,15 @@ static int rope_kv_write(const float* qkv, int64_t qkv_stride, const float* cos_
         qkv_stride % 4)
         return PE_ERR_SHAPE;
     const int64_t per = (int64_t)(n_head + 2 * n_kv) * head_dim / 8 + (int64_t)n_kv * head_dim / 8;
-    if (L * per > 0x7FFFFFFF) return PE_ERR_SHAPE;
+    // kv16: one V^T chunk item per (kv head, touched block, dim row, chunk)
+    const int64_t nvt = kv16 && L > 0 ? (int64_t)n_kv * (((pos0 + L - 1) >> 6) - (pos0 >> 6) + 1) * 512 : 0;
+    if (L * per + nvt > 0x7FFFFFFF) return PE_ERR_SHAPE;
     if (L == 0) return PE_OK;
     if (!qkv || !cos_rows || !sin_rows || !q_out || !k_cache || !v_cache) return PE_ERR_NULL;
     if (!aligned(qkv, 16) || !aligned(cos_rows, 16) || !aligned(sin_rows, 16) || !aligned(q_out, 16) ||
         !aligned(k_cache, 16) || !aligned(v_cache, 16))
         return PE_ERR_ALIGN;
-    hipLaunchKernelGGL(k_rope_kv_write, dim3(grid1d(L * per)), dim3(256), 0, (hipStream_t)stream, qkv,
+    hipLaunchKernelGGL(k_rope_kv_write, dim3(grid1d(L * per + nvt)), dim3(256), 0, (hipStream_t)stream, qkv,
                        qkv_stride, cos_rows, sin_rows, n_head, n_kv, head_dim, (int)L, pos0, q_out, k_cache,
                        v_cache, capacity, (uint8_t*)kv16, kv16_blocks);
     return launch_status();

@@ -1052,6 +1052,29 @@ def _kv16_layout_ref(k, v, length):
     return out.view(np.uint8).reshape(n_kv, nblk, 16384)
 
 
+@pytest.mark.parametrize("splits", [(37, 100), (64, 64, 9), (1, 5, 130)])
+def test_rope_kv_write_blocks_in_pieces(K, splits):
+    """Key blocks written by several calls at increasing pos0 (blocks shared by two calls: the
+    V^T chunks a call only partly covers keep the other call's keys) equal the numpy layout of
+    the caches the calls wrote, and the fp32 caches equal one call over the whole prompt."""
+    rng = np.random.default_rng(sum(splits))
+    nh, nkv, hd = 14, 2, 64
+    L = sum(splits)
+    qkv = torch.from_numpy(rng.standard_normal((L, (nh + 2 * nkv) * hd)).astype(np.float32)).to(DEV)
+    ang = rng.standard_normal((L, hd // 2)).astype(np.float32)
+    cos, sin = torch.from_numpy(np.cos(ang)).to(DEV), torch.from_numpy(np.sin(ang)).to(DEV)
+    k1, v1 = torch.zeros(nkv, L, hd, device=DEV), torch.zeros(nkv, L, hd, device=DEV)
+    k2, v2 = k1.clone(), v1.clone()
+    K.rope_kv_write(qkv, cos, sin, nh, k1, v1)
+    kv16 = K.kv16_blocks(nkv, L, DEV)
+    pos = 0
+    for n in splits:
+        K.rope_kv_write(qkv[pos:pos + n], cos[pos:pos + n], sin[pos:pos + n], nh, k2, v2, pos0=pos, kv16=kv16)
+        pos += n
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    np.testing.assert_array_equal(kv16.cpu().numpy(), _kv16_layout_ref(k1.cpu().numpy(), v1.cpu().numpy(), L))
+
+
 @pytest.mark.parametrize("L", [1, 64, 77, 300, 1000])
 @pytest.mark.parametrize("n_head,n_kv", [(14, 2), (8, 8), (16, 1), (9, 3), (4, 2), (16, 2)])
 def test_flash_prefill_blocks_equals_fp32_cache_path(K, L, n_head, n_kv):
