@@ -171,12 +171,25 @@ int pe_flash_prefill_h16(const float* q, int64_t q_stride, const float* k_cache,
 /* pe_flash_prefill_h16 of a prompt starting at position 0 with K and V taken from the fp16 key
  * blocks of pe_rope_kv_write_blocks (kv16, kv16_blocks per kv head, L <= 64 kv16_blocks; the
  * positions past L in the last block must be finite, e.g. zero): the blocks are copied into LDS
- * with direct-to-LDS loads instead of being converted from the fp32 caches. The same fp16
- * operand values in the same positions, so the same output bits. head_dim 64.
- * Replaces the fp16 SDPA prefill call of model.py:201-209 (pos0 = 0). */
+ * with direct-to-LDS loads instead of being converted from the fp32 caches. head_dim 64.
+ * workspace NULL: every set of 32 queries runs in one workgroup over all the keys it sees, with
+ * the same fp16 operand values in the same positions and the same order as pe_flash_prefill_h16,
+ * so the same output bits. workspace non-NULL (16-byte aligned, workspace_bytes >=
+ * pe_flash_prefill_blocks_workspace(n_head, n_kv, L), any contents): when the longest set sees
+ * more than 64 key blocks (L > 4096), the sets that do are split into P = ceil(longest / 64)
+ * key ranges run by separate workgroups (so no workgroup walks more than about 64 blocks), each
+ * writing its unnormalised output, maximum and sum into the workspace, and a second launch
+ * merges them with the log-sum-exp rule: the same attention within fp32 rounding of the two
+ * orders (the fp16 outputs then differ by at most an ulp or so). Calls that overlap must not
+ * share a workspace. Replaces the fp16 SDPA prefill call of model.py:201-209 (pos0 = 0). */
 int pe_flash_prefill_blocks(const float* q, int64_t q_stride, const void* kv16, int64_t kv16_blocks,
                             int n_head, int n_kv, int head_dim, int64_t L, float scale, void* out,
-                            int64_t out_stride, pe_stream_t stream);
+                            int64_t out_stride, void* workspace, int64_t workspace_bytes,
+                            pe_stream_t stream);
+
+/* Workspace bytes pe_flash_prefill_blocks uses for L queries (0: nothing is split, any
+ * workspace or NULL gives the unsplit schedule). No counterpart in the reference. */
+int64_t pe_flash_prefill_blocks_workspace(int n_head, int n_kv, int64_t L);
 
 /* Plain prefill GEMM on ROCm's hipBLASLt: c (M, N) = a (M, K) . w (N, K)^T (+ bias[N])
  * (+ residual (M, N)); a and w fp16 row-major (row strides lda and K elements; lda % 8 == 0,

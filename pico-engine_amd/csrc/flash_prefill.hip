@@ -56,9 +56,14 @@ struct FlashParams {
     int64_t out_stride;
     const uint8_t* kv16; // k_flash_prefill_blocks: the fp16 K / V^T key blocks of pe_rope_kv_write_blocks
     int64_t kv16_blocks; // k_flash_prefill_blocks: key blocks per kv head in kv16
+    float* part;         // k_flash_prefill_blocks: partial records of the split query sets
+    int nparts;          // parts per split query set (1: no split)
+    int64_t split0;      // first split query set (query sets split0 .. are split)
 };
 
 constexpr int kFpBlkSlots = 4;  // k_flash_prefill_blocks: LDS ring depth (16 KB per key block)
+constexpr int kFpSplitBlocks = 64;  // key blocks per workgroup above which a query set is split
+constexpr int kFpRec = 68;          // partial record: unnormalised O[64], running max, sum, 2 pad
 
 // 16 bytes per lane from global g into LDS at m0 + 16 lane (one wave instruction: 1 KB)
 PE_DEV void fp_load16(const void* g, uint32_t m0) {
@@ -349,12 +354,24 @@ __global__ __launch_bounds__(1024) void k_flash_prefill_blocks(FlashParams p, in
     const int t = threadIdx.x, l = t & 63;
     const int w = __builtin_amdgcn_readfirstlane(t >> 6);
     const int li = l & 15, lg = l >> 4;
-    // heaviest query blocks first, paired with light ones (k_flash_prefill's order)
-    const int64_t nqb = (p.L + qb_size - 1) / qb_size;
-    const int64_t total = nqb * p.n_kv, half = (total + 1) / 2, lin = blockIdx.x;
-    const int64_t rank = lin < half ? lin : total - 1 - (lin - half);
-    const int64_t qb = nqb - 1 - rank / p.n_kv;
-    const int kvh = (int)(rank % p.n_kv);
+    // Items, heaviest first: the parts of the split query sets (set descending, then part, then
+    // kv head), then the unsplit sets (descending, then kv head).
+    const int64_t nqb = (p.L + qb_size - 1) / qb_size, lin = blockIdx.x;
+    const int64_t n_split_items = (nqb - p.split0) * p.nparts * p.n_kv;
+    int64_t qb;
+    int kvh, part;
+    if (lin < n_split_items) {
+        const int64_t per_set = (int64_t)p.nparts * p.n_kv;
+        qb = nqb - 1 - lin / per_set;
+        const int rem = (int)(lin % per_set);
+        part = rem / p.n_kv;
+        kvh = rem % p.n_kv;
+    } else {
+        const int64_t i2 = lin - n_split_items;
+        qb = p.split0 - 1 - i2 / p.n_kv;
+        kvh = (int)(i2 % p.n_kv);
+        part = -1;
+    }
     const int h = kvh * p.group + w % p.group;
     const int64_t q0 = qb * qb_size + 32 * (w / p.group);
     const int n_keys = (int)p.L;
@@ -380,7 +397,10 @@ __global__ __launch_bounds__(1024) void k_flash_prefill_blocks(FlashParams p, in
 #pragma unroll
         for (int d = 0; d < 4; ++d) o[tt][d] = fv4{0.f, 0.f, 0.f, 0.f};
     const int64_t q_last = (qb + 1) * qb_size - 1 < p.L - 1 ? (qb + 1) * qb_size - 1 : p.L - 1;
-    const int nblk = (int)((q_last + kFpKeys) / kFpKeys);  // blocks this workgroup's queries see
+    const int nblk_all = (int)((q_last + kFpKeys) / kFpKeys);  // blocks this workgroup's queries see
+    // this item's blocks: all of them, or part `part` of nparts near-equal ranges
+    const int b_begin = part < 0 ? 0 : (int)((int64_t)part * nblk_all / p.nparts);
+    const int b_end = part < 0 ? nblk_all : (int)((int64_t)(part + 1) * nblk_all / p.nparts);
 
     // S^T = K Q^T of one tile for the block in ring slot `slot`
     auto scores = [&](int slot, const fh8 (&qq)[2], fv4 (&s)[4]) {
@@ -471,29 +491,48 @@ __global__ __launch_bounds__(1024) void k_flash_prefill_blocks(FlashParams p, in
         softmax_pv(s0, slot, m_run[0], l_run[0], o[0]);
         softmax_pv(s1, slot, m_run[1], l_run[1], o[1]);
     };
-    blk_load(0);
-    if (nblk > 1) blk_load(1);
-    if (nblk > 2) blk_load(2);
+    blk_load(b_begin);
+    if (b_begin + 1 < b_end) blk_load(b_begin + 1);
+    if (b_begin + 2 < b_end) blk_load(b_begin + 2);
     // Each wave passes one barrier per block in both loops, with the same waits and loads for
     // the same b, so waves whose unmasked prefix differs (QS > 1) stay matched.
-    const int nfull = (int)((q0 + 1) / kFpKeys) < nblk ? (int)((q0 + 1) / kFpKeys) : nblk;
-    const int nsteady = nfull < nblk - 3 ? nfull : nblk - 3;
-    int b = 0;
+    const int nfull = (int)((q0 + 1) / kFpKeys) < b_end ? (int)((q0 + 1) / kFpKeys) : b_end;
+    const int nsteady = nfull < b_end - 3 ? nfull : b_end - 3;
+    int b = b_begin;
     for (; b < nsteady; ++b) {
         fp_wait_loads<2 * NL>();  // block b + 1's loads are done, b + 2's may be in flight
         fp_lds_barrier();
         blk_load(b + 3);
         body(b, std::false_type{});
     }
-    for (; b < nblk; ++b) {
-        if (b + 2 < nblk) fp_wait_loads<2 * NL>();
-        else if (b + 1 < nblk) fp_wait_loads<NL>();
+    for (; b < b_end; ++b) {
+        if (b + 2 < b_end) fp_wait_loads<2 * NL>();
+        else if (b + 1 < b_end) fp_wait_loads<NL>();
         else fp_wait_loads<0>();
         fp_lds_barrier();
-        if (b + 3 < nblk) blk_load(b + 3);
+        if (b + 3 < b_end) blk_load(b + 3);
         body(b, std::true_type{});  // the mask changes nothing in a fully visible block
     }
 
+    if (part >= 0) {
+        // partial record of (query, head): unnormalised O, running max (log2 units), sum
+        const int64_t q_split0 = p.split0 * qb_size, rows = p.L - q_split0;
+        const int n_head = p.group * p.n_kv;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int64_t qi = q0 + 16 * tt + li;
+            if (qi < p.L) {
+                float* rec = p.part + (((int64_t)part * rows + (qi - q_split0)) * n_head + h) * kFpRec;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) *reinterpret_cast<fv4*>(rec + 16 * d + 4 * lg) = o[tt][d];
+                if (lg == 0) {
+                    rec[kFpHd] = m_run[tt];
+                    rec[kFpHd + 1] = l_run[tt];
+                }
+            }
+        }
+        return;
+    }
     // out: O[query][dim 16 d + 4 lg + r] / l, rounded to fp16
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
@@ -512,15 +551,77 @@ __global__ __launch_bounds__(1024) void k_flash_prefill_blocks(FlashParams p, in
         }
     }
 }
+
+// Merge of the split query sets' partial records (queries q_split0 .. L - 1): thread = (query,
+// head, 4 dims). With m = the largest part maximum, O = sum_p O_p 2^(m_p - m) and
+// l = sum_p l_p 2^(m_p - m) in part order, out = O * (1 / l) rounded to fp16 (the unsplit
+// kernel's normalisation).
+__global__ __launch_bounds__(256) void k_flash_merge(const float* __restrict__ part, int nparts, int64_t rows,
+                                                     int n_head, int64_t q_split0, _Float16* __restrict__ out,
+                                                     int64_t out_stride) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= rows * n_head * 16) return;
+    const int dq = (int)(idx & 15);
+    const int64_t rh = idx >> 4, r = rh / n_head;
+    const int h = (int)(rh - r * n_head);
+    const int64_t pstride = rows * n_head * kFpRec;
+    const float* rec = part + rh * kFpRec;
+    float m = rec[kFpHd];
+    for (int i = 1; i < nparts; ++i) m = fmaxf(m, rec[i * pstride + kFpHd]);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float lsum = 0.f;
+    for (int i = 0; i < nparts; ++i) {
+        const float* ri = rec + i * pstride;
+        const float f = __builtin_amdgcn_exp2f(ri[kFpHd] - m);
+        const float4 oi = *reinterpret_cast<const float4*>(ri + 4 * dq);
+        acc.x = fmaf(oi.x, f, acc.x);
+        acc.y = fmaf(oi.y, f, acc.y);
+        acc.z = fmaf(oi.z, f, acc.z);
+        acc.w = fmaf(oi.w, f, acc.w);
+        lsum = fmaf(ri[kFpHd + 1], f, lsum);
+    }
+    const float inv = 1.0f / lsum;
+    float v[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+    _Float16* orow = out + (q_split0 + r) * out_stride + (int64_t)h * kFpHd + 4 * dq;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        asm volatile("" : "+v"(v[e]));  // rounded to fp16 as a value of its own
+        orow[e] = (_Float16)v[e];
+    }
+}
 }  // namespace pe
 
 using namespace pe;
+
+// The split of pe_flash_prefill_blocks for L queries in sets of qb (see k_flash_prefill_blocks):
+// parts per split set (1 = no split), the first split set, and the partial-record bytes.
+struct FlashSplit {
+    int nparts;
+    int64_t split0, bytes;
+};
+static FlashSplit flash_split(int64_t L, int qb, int n_head) {
+    const int64_t nqb = (L + qb - 1) / qb;
+    auto nblk = [&](int64_t s) {  // key blocks set s sees: ceil(min((s + 1) qb, L) / 64)
+        const int64_t end = (s + 1) * qb < L ? (s + 1) * qb : L;
+        return (end + kFpKeys - 1) / kFpKeys;
+    };
+    const int64_t P = (nblk(nqb - 1) + kFpSplitBlocks - 1) / kFpSplitBlocks;
+    if (P <= 1 || P > 64) return FlashSplit{1, nqb, 0};
+    // Split sets s0 .. nqb - 1: each has more than kFpSplitBlocks blocks, and each of its parts
+    // starts at a key all of the set's queries see (so a part's running maximum is finite from
+    // its first block on): the smallest s0 from which on every set qualifies.
+    int64_t s0 = nqb;
+    while (s0 > 0 && nblk(s0 - 1) > kFpSplitBlocks && (P - 1) * nblk(s0 - 1) / P * kFpKeys <= (s0 - 1) * qb) --s0;
+    if (s0 >= nqb) return FlashSplit{1, nqb, 0};
+    return FlashSplit{(int)P, s0, P * (L - s0 * qb) * n_head * kFpRec * (int64_t)sizeof(float)};
+}
 
 static int flash_prefill(const float* q, int64_t q_stride, const float* k_cache,
                          const float* v_cache, int n_head, int n_kv, int head_dim,
                          int64_t capacity, int64_t L, int64_t pos0, float scale, void* out,
                          int64_t out_stride, bool half_out, pe_stream_t stream,
-                         const void* kv16 = nullptr, int64_t kv16_blocks = 0) {
+                         const void* kv16 = nullptr, int64_t kv16_blocks = 0, void* ws = nullptr,
+                         int64_t ws_bytes = 0) {
     if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > kFpMaxWaves ||
         head_dim != kFpHd || capacity <= 0 || capacity > kFpMaxCapacity || L < 0 || pos0 < 0 || pos0 + L > capacity || n_kv > 65535)
         return PE_ERR_SHAPE;
@@ -534,16 +635,33 @@ static int flash_prefill(const float* q, int64_t q_stride, const float* k_cache,
         !aligned(out, half_out ? 2 : 4))
         return PE_ERR_ALIGN;
     FlashParams p{q, q_stride, k_cache, v_cache, n_head / n_kv, n_kv, capacity, L, pos0, scale, (float*)out,
-                  out_stride, (const uint8_t*)kv16, kv16_blocks};
+                  out_stride, (const uint8_t*)kv16, kv16_blocks, nullptr, 1, (L + qb - 1) / qb};
     if (kv16) {
         // QS sets of 32 queries per workgroup, at least 4 waves (the loading waves)
         const int qs = group >= 4 ? 1 : (4 + group - 1) / group, waves = group * qs, qb2 = 32 * qs;
-        const int64_t nb2 = (L + qb2 - 1) / qb2 * (int64_t)n_kv;
+        const int64_t nqb = (L + qb2 - 1) / qb2;
+        p.split0 = nqb;
+        if (ws) {
+            const FlashSplit sp = flash_split(L, qb2, n_head);
+            if (ws_bytes < sp.bytes) return PE_ERR_SHAPE;
+            if (!aligned(ws, 16)) return PE_ERR_ALIGN;
+            p.part = (float*)ws;
+            p.nparts = sp.nparts;
+            p.split0 = sp.split0;
+        }
+        const int64_t nb2 = ((nqb - p.split0) * p.nparts + p.split0) * (int64_t)n_kv;
         if (nb2 > 0x7FFFFFFF) return PE_ERR_SHAPE;
         if (waves >= 8)
             hipLaunchKernelGGL(k_flash_prefill_blocks<8>, dim3((unsigned)nb2), dim3(64 * waves), 0, (hipStream_t)stream, p, qb2);
         else
             hipLaunchKernelGGL(k_flash_prefill_blocks<4>, dim3((unsigned)nb2), dim3(64 * waves), 0, (hipStream_t)stream, p, qb2);
+        if (p.split0 < nqb) {
+            const int rc = launch_status();
+            if (rc != PE_OK) return rc;
+            const int64_t rows = L - p.split0 * qb2, items = rows * n_head * 16;
+            hipLaunchKernelGGL(k_flash_merge, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                               p.part, p.nparts, rows, n_head, p.split0 * qb2, (_Float16*)out, out_stride);
+        }
         return launch_status();
     }
     const int waves = group * (qb / 16);  // 9..16 (kv_load and stage use the first 8 waves)
@@ -573,14 +691,23 @@ extern "C" int pe_flash_prefill_h16(const float* q, int64_t q_stride, const floa
                          scale, out, out_stride, true, stream);
 }
 
+extern "C" int64_t pe_flash_prefill_blocks_workspace(int n_head, int n_kv, int64_t L) {
+    if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_head / n_kv > kFpMaxWaves || L <= 0) return 0;
+    const int group = n_head / n_kv;
+    const int qs = group >= 4 ? 1 : (4 + group - 1) / group;
+    return flash_split(L, 32 * qs, n_head).bytes;
+}
+
 extern "C" int pe_flash_prefill_blocks(const float* q, int64_t q_stride, const void* kv16, int64_t kv16_blocks,
                                        int n_head, int n_kv, int head_dim, int64_t L, float scale, void* out,
-                                       int64_t out_stride, pe_stream_t stream) {
+                                       int64_t out_stride, void* workspace, int64_t workspace_bytes,
+                                       pe_stream_t stream) {
     if (head_dim != kFpHd || kv16_blocks <= 0 || L > kv16_blocks * kFpKeys || kv16_blocks > (1 << 18))
         return PE_ERR_SHAPE;
     if (L > 0 && !kv16) return PE_ERR_NULL;
     if (kv16 && !aligned(kv16, 16)) return PE_ERR_ALIGN;
     // the fp32 caches are not read: any valid pointers satisfy the shared checks
     return flash_prefill(q, q_stride, (const float*)kv16, (const float*)kv16, n_head, n_kv, head_dim,
-                         kv16_blocks * kFpKeys, L, 0, scale, out, out_stride, true, stream, kv16, kv16_blocks);
+                         kv16_blocks * kFpKeys, L, 0, scale, out, out_stride, true, stream, kv16, kv16_blocks,
+                         workspace, workspace_bytes);
 }

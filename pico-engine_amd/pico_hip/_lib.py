@@ -117,7 +117,8 @@ _SIGNATURES = {
     "pe_gemm_h16": (_I, [_P, _L, _P, _P, _P, _L, _P, _L, _L, _L, _L, _P]),
     "pe_flash_prefill": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _L, _F, _P, _L, _P]),
     "pe_flash_prefill_h16": (_I, [_P, _L, _P, _P, _I, _I, _I, _L, _L, _L, _F, _P, _L, _P]),
-    "pe_flash_prefill_blocks": (_I, [_P, _L, _P, _L, _I, _I, _I, _L, _F, _P, _L, _P]),
+    "pe_flash_prefill_blocks": (_I, [_P, _L, _P, _L, _I, _I, _I, _L, _F, _P, _L, _P, _L, _P]),
+    "pe_flash_prefill_blocks_workspace": (_L, [_I, _I, _L]),
     "pe_gemm_lt": (_I, [_P, _L, _P, _L, _L, _L, _P, _P, _L, _P, _L, _P, _L, _P]),
     "pe_gemm_lt_init": (_I, []),
     "pe_mfma_bytes": (_L, [_I, _L, _L]),

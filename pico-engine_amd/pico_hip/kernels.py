@@ -1235,11 +1235,20 @@ def flash_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     return out
 
 
+def flash_prefill_blocks_workspace(n_head: int, n_kv: int, L: int) -> int:
+    """Bytes of the workspace flash_prefill_blocks splits long prompts with (0: none needed)."""
+    return int(lib.pe_flash_prefill_blocks_workspace(n_head, n_kv, L))
+
+
 def flash_prefill_blocks(q: torch.Tensor, kv16: torch.Tensor, scale: float | None = None,
-                         out: torch.Tensor | None = None) -> torch.Tensor:
+                         out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                         split: bool = True) -> torch.Tensor:
     """flash_prefill(half=True) of a prompt from position 0, reading K and V from the fp16 key
-    blocks rope_kv_write(kv16=...) wrote (pe_flash_prefill_blocks): the same fp16 values in the
-    same operand positions, so the same bits; head_dim 64."""
+    blocks rope_kv_write(kv16=...) wrote (pe_flash_prefill_blocks); head_dim 64. split=False:
+    one workgroup per 32-query set over all its keys, the same bits as flash_prefill(half=True).
+    split=True: query sets that see more than 64 key blocks (L > 4096) run as several key
+    ranges merged by a second launch (within fp32 rounding of the unsplit order), in
+    ``workspace`` (uint8, at least flash_prefill_blocks_workspace bytes; allocated when None)."""
     dev = _on_gpu(q, kv16)
     L, n_head, hd = q.shape
     n_kv, nblk = kv16.shape[0], kv16.shape[1]
@@ -1253,8 +1262,17 @@ def flash_prefill_blocks(q: torch.Tensor, kv16: torch.Tensor, scale: float | Non
         out = torch.empty(L, n_head * hd, device=dev, dtype=torch.float16)
     if out.dtype != torch.float16:
         raise ValueError("out must be float16")
+    ws_ptr, ws_bytes = None, 0
+    if split:
+        need = flash_prefill_blocks_workspace(n_head, n_kv, L)
+        if need:
+            if workspace is None:
+                workspace = torch.empty(need, device=dev, dtype=torch.uint8)
+            if workspace.dtype != torch.uint8 or not workspace.is_contiguous():
+                raise ValueError("workspace must be a contiguous uint8 buffer")
+            ws_ptr, ws_bytes = _ptr(workspace), workspace.numel()
     check(lib.pe_flash_prefill_blocks(_ptr(q), q.stride(0), _ptr(kv16), nblk, n_head, n_kv, hd, L, float(scale),
-                                      _ptr(out), out.stride(0), _stream(dev)),
+                                      _ptr(out), out.stride(0), ws_ptr, ws_bytes, _stream(dev)),
           "pe_flash_prefill_blocks")
     return out
 
@@ -1317,7 +1335,7 @@ __all__ = ["LAYOUT_NATURAL", "LAYOUT_X_UT", "LAYOUT_Y_UT", "to_ut", "from_ut", "
            "attn_gproj", "attn_gproj_supported", "attn_oproj_fix", "attn_oproj_supported", "fix_acc",
            "repack_oproj", "oproj_eligible", "qgemv_fix_norm_silu", "qgemv_norm_argmax", "dequantize_weight_f16",
            "repack_down_slices", "down_slice_eligible", "ffn_fix", "ffn_fix_supported", "ffn_fix_bound",
-           "kv16_blocks", "flash_prefill_blocks",
+           "kv16_blocks", "flash_prefill_blocks", "flash_prefill_blocks_workspace",
            "fix_acc_block", "fix_stride", "qkv_fix_rmsnorm_rope", "FFN_REPLICAS",
            "DecodeStep", "decode_step_supported", "decode_step_workspace",
            "gemm_f16", "gemm_f16_silu", "interleave_gate_up_f16", "flash_prefill",

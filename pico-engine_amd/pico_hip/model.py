@@ -167,6 +167,10 @@ class Transformer:
         # prompts from position 0 at head_dim 64: K and V also written as fp16 key blocks for the
         # flash kernel's direct-to-LDS copies (same bits); off: it converts the fp32 caches
         self.prefill_kv_blocks = True
+        # with the key blocks, prompts past 4096 tokens split the long query sets' key ranges
+        # over workgroups and merge them (within fp32 rounding); off: one workgroup per query
+        # set, the same bits as the fp32-cache path
+        self.prefill_flash_split = True
         self._f16: list[dict[str, torch.Tensor]] | None = None
         # greedy decode steps the persistent kernel covers can run as one launch per token
         # (pe_decode_step) instead of four launches per layer; off by default: ~2 % faster, but
@@ -447,6 +451,12 @@ class Transformer:
         # a prompt from position 0 at head_dim 64: the RoPE pass also writes K and V as fp16 key
         # blocks that the flash kernel copies straight into LDS (the same values, the same bits)
         kv16 = K.kv16_blocks(nkv, Lt, self.device) if self.prefill_kv_blocks and hd == 64 and pos0 == 0 else None
+        # past 4096 tokens the long query sets' key ranges are split over workgroups and merged
+        # (a second launch), in one workspace for every layer
+        fws = None
+        if kv16 is not None and self.prefill_flash_split:
+            need = K.flash_prefill_blocks_workspace(nh, nkv, Lt)
+            fws = torch.empty(need, device=self.device, dtype=torch.uint8) if need else None
         for i, L in enumerate(self.layers):
             k_buf, v_buf = cache[i]
             W = w16[i]
@@ -459,7 +469,7 @@ class Transformer:
             # RoPE of q and k and the cache write of k and v, one pass (model.py:186-197)
             qr = K.rope_kv_write(qkv, cos, sin, nh, k_buf, v_buf, pos0=pos0, out=q_rot, kv16=kv16)
             if kv16 is not None:  # matrix-core flash attention from the key blocks, fp16 output
-                attn = K.flash_prefill_blocks(qr, kv16)
+                attn = K.flash_prefill_blocks(qr, kv16, workspace=fws, split=self.prefill_flash_split)
             elif hd == 64:  # the same from the fp32 caches
                 attn = K.flash_prefill(qr, k_buf, v_buf, pos0=pos0, half=True)
             else:         # other head sizes: the fp32 causal attention kernel
@@ -506,9 +516,6 @@ class Transformer:
         x = K.embed_gather(self.embed, token_ids)                       # (L, hidden), fp32
         qkv = torch.empty(Lt, qd + 2 * kd, device=self.device, dtype=torch.float32)
         q_rot = torch.empty(Lt, nh, hd, device=self.device, dtype=torch.float32)
-        # a prompt from position 0 at head_dim 64: the RoPE pass also writes K and V as fp16 key
-        # blocks that the flash kernel copies straight into LDS (the same values, the same bits)
-        kv16 = K.kv16_blocks(nkv, Lt, self.device) if self.prefill_kv_blocks and hd == 64 and pos0 == 0 else None
         for i, L in enumerate(self.layers):
             k_buf, v_buf = cache[i]
             W = w16[i]

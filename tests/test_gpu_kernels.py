@@ -1100,13 +1100,64 @@ def test_flash_prefill_blocks_equals_fp32_cache_path(K, L, n_head, n_kv):
         want = _kv16_layout_ref(k1.cpu().numpy(), v1.cpu().numpy(), L)
         np.testing.assert_array_equal(kv16.cpu().numpy(), want)
     ref = K.flash_prefill(q1, k1, v1, half=True)
-    got = K.flash_prefill_blocks(q2, kv16)
+    got = K.flash_prefill_blocks(q2, kv16, split=False)
     assert torch.equal(got, ref)
+    if L <= 4096:  # nothing to split: the default schedule is the same
+        assert K.flash_prefill_blocks_workspace(n_head, n_kv, L) == 0
+        assert torch.equal(K.flash_prefill_blocks(q2, kv16), ref)
 
 
 def test_flash_prefill_blocks_full_length(K):
     """The block path at the config-3 length (8192 positions, 14/2 heads): the same bits."""
     test_flash_prefill_blocks_equals_fp32_cache_path(K, 8192, 14, 2)
+
+
+def _blocks_case(K, L, n_head, n_kv, seed):
+    rng = np.random.default_rng(seed)
+    hd = 64
+    qkv = torch.from_numpy(rng.standard_normal((L, (n_head + 2 * n_kv) * hd)).astype(np.float32)).to(DEV)
+    ang = rng.standard_normal((L, hd // 2)).astype(np.float32)
+    cos, sin = torch.from_numpy(np.cos(ang)).to(DEV), torch.from_numpy(np.sin(ang)).to(DEV)
+    kc, vc = torch.zeros(n_kv, L, hd, device=DEV), torch.zeros(n_kv, L, hd, device=DEV)
+    kv16 = K.kv16_blocks(n_kv, L, DEV)
+    q = K.rope_kv_write(qkv, cos, sin, n_head, kc, vc, kv16=kv16)
+    return q, kc, vc, kv16
+
+
+@pytest.mark.parametrize("L,n_head,n_kv", [(4097, 14, 2), (4200, 8, 8), (5000, 9, 3), (6001, 4, 2),
+                                           (9000, 14, 2), (8192, 16, 1)])
+def test_flash_prefill_blocks_split_merge(K, L, n_head, n_kv):
+    """Past 4096 positions the long query sets run as several key ranges merged by a second
+    launch: the queries below 4096 (unsplit sets) keep the unsplit bits, the others stay within
+    two fp16 ulps of them, plus 2^-14 where the sum cancels (the same sums in another fp32
+    order); the workspace's prior contents
+    do not matter, and one byte too few is refused."""
+    q, _, _, kv16 = _blocks_case(K, L, n_head, n_kv, L + n_head)
+    need = K.flash_prefill_blocks_workspace(n_head, n_kv, L)
+    assert need > 0
+    un = K.flash_prefill_blocks(q, kv16, split=False)
+    ws = torch.full((need,), 0xFF, device=DEV, dtype=torch.uint8)  # NaN bit patterns
+    sp = K.flash_prefill_blocks(q, kv16, workspace=ws)
+    assert torch.equal(sp[:4096], un[:4096])
+    a, b = un.float(), sp.float()
+    ulp = torch.exp2(torch.floor(torch.log2(a.abs().clamp_min(2.0 ** -14))) - 10)
+    excess = ((a - b).abs() - 2 * ulp).max().item()  # plus 2^-14 absolute near cancellation
+    assert excess <= 2.0 ** -14, excess
+    assert torch.equal(K.flash_prefill_blocks(q, kv16, workspace=ws), sp)  # deterministic
+    with pytest.raises(RuntimeError):
+        K.flash_prefill_blocks(q, kv16, workspace=ws[:need - 1])
+
+
+def test_flash_prefill_blocks_split_matches_closed_form(K):
+    """The split schedule (4608 positions, 4 heads on one kv head: sets of up to 72 key blocks
+    in two ranges) against float64 attention on the same fp16-rounded q, k, v."""
+    L, n_head, n_kv = 4608, 4, 1
+    q, kc, vc, kv16 = _blocks_case(K, L, n_head, n_kv, 77)
+    assert K.flash_prefill_blocks_workspace(n_head, n_kv, L) > 0
+    out = K.flash_prefill_blocks(q, kv16).float().cpu().numpy()
+    h16 = lambda t: t.cpu().numpy().astype(np.float16).astype(np.float32)
+    ref = closed.causal_attention(h16(q), h16(kc), h16(vc), 0).reshape(L, n_head * 64)
+    assert rel_err(out, ref) < 2e-3
 
 
 @pytest.mark.parametrize("L,pos0", [(1, 0), (5, 0), (64, 0), (100, 7), (130, 0), (513, 0)])
