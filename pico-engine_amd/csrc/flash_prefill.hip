@@ -87,6 +87,47 @@ PE_DEV fh8 f8_to_h8(float4 a, float4 b) {
     return r;
 }
 
+// Online softmax of one 16-query tile's 64-key block (one query per lane: lane (li, lg) holds
+// the raw scores of query li against keys 16 jt + 4 lg + r in s[jt][r]), in base 2 with
+// scale * log2 e (sl2) applied in the exponent's fma. Lazy rescaling: the running maximum m
+// moves (and o and l are scaled by 2^(m_old - m_new)) only when a lane's block maximum exceeds
+// it by more than kFpLazy, so the probabilities 2^(s sl2 - m) stay below 2^kFpLazy (exact in
+// fp16's range) and most blocks skip the rescale (a wave-uniform branch). l sums the fp32
+// probabilities, which are rounded to fp16 into the P^T operand pb of the 32-key slabs (keys
+// 4 lg + i, 16 + 4 lg + i). Every query sees a key in the first block of its range, so m is
+// finite from then on.
+constexpr float kFpLazy = 8.0f;
+PE_DEV void fp_softmax(const fv4 (&s)[4], float sl2, float& m_run, float& l_run, fv4 (&o)[4], fh8 (&pb)[2]) {
+    float mx = s[0][0];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (jt | r) mx = fmaxf(mx, s[jt][r]);
+    mx = swap32_max(swap16_max(mx));
+    const float m_blk = mx * sl2;
+    const bool grow = m_blk > m_run + kFpLazy;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float corr = grow ? __builtin_amdgcn_exp2f(m_run - m_blk) : 1.0f;
+        l_run *= corr;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[d][r] *= corr;
+        m_run = grow ? m_blk : m_run;
+    }
+    float psum = 0.f;
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float e = __builtin_amdgcn_exp2f(fmaf(s[jt][r], sl2, -m_run));
+            psum += e;
+            pb[jt >> 1][4 * (jt & 1) + r] = (_Float16)e;
+        }
+    l_run += swap32_sum(swap16_sum(psum));
+}
+
 // OutT _Float16: the output rounded to fp16 (nearest even), the operand of the o-projection
 // GEMM (p.out then points to fp16 rows).
 template <typename OutT>
@@ -226,37 +267,8 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
     // applied in its fma. Every query sees key 0 in the first block, so the running maximum is
     // finite from then on.
     auto softmax_pv = [&](const fv4 (&s)[4], int slot) {
-        float mx = NEG_INF;
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[jt][r]);
-        mx = swap32_max(swap16_max(mx));
-        const float m_new = fmaxf(m_run, mx * sl2);
-        float psum = 0.f;
-        fh8 pb[2];  // P^T operand of each 32-key slab: keys 4 lg + i, 16 + 4 lg + i
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float e = __builtin_amdgcn_exp2f(fmaf(s[jt][r], sl2, -m_new));
-                psum += e;
-                pb[jt >> 1][4 * (jt & 1) + r] = (_Float16)e;
-            }
-        psum = swap32_sum(swap16_sum(psum));
-        // rescale by 2^(m_run - m_new) only when some lane's maximum grew: otherwise the factor
-        // is exactly 1 and the products would change nothing (a wave-uniform branch)
-        if (__builtin_amdgcn_ballot_w64(m_new != m_run)) {
-            const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
-            l_run = l_run * corr + psum;
-#pragma unroll
-            for (int d = 0; d < 4; ++d)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) o[d][r] *= corr;
-        } else {
-            l_run = l_run + psum;
-        }
-        m_run = m_new;
+        fh8 pb[2];
+        fp_softmax(s, sl2, m_run, l_run, o, pb);
         // A = V^T (16 dims x 32 keys) per dim tile, B = P^T (32 keys x 16 queries)
         const _Float16* vd = vt + slot * kSlotHalves;
 #pragma unroll
@@ -427,35 +439,8 @@ __global__ __launch_bounds__(1024) void k_flash_prefill_blocks(FlashParams p, in
     };
     // k_flash_prefill's online softmax and O^T += V^T P^T for one tile
     auto softmax_pv = [&](const fv4 (&s)[4], int slot, float& mr, float& lr, fv4 (&oo)[4]) {
-        float mx = NEG_INF;
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[jt][r]);
-        mx = swap32_max(swap16_max(mx));
-        const float m_new = fmaxf(mr, mx * sl2);
-        float psum = 0.f;
         fh8 pb[2];
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float e = __builtin_amdgcn_exp2f(fmaf(s[jt][r], sl2, -m_new));
-                psum += e;
-                pb[jt >> 1][4 * (jt & 1) + r] = (_Float16)e;
-            }
-        psum = swap32_sum(swap16_sum(psum));
-        if (__builtin_amdgcn_ballot_w64(m_new != mr)) {
-            const float corr = __builtin_amdgcn_exp2f(mr - m_new);
-            lr = lr * corr + psum;
-#pragma unroll
-            for (int d = 0; d < 4; ++d)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) oo[d][r] *= corr;
-        } else {
-            lr = lr + psum;
-        }
-        mr = m_new;
+        fp_softmax(s, sl2, mr, lr, oo, pb);
         const _Float16* vd = vt + slot * kSlotHalves;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
