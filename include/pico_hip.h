@@ -171,10 +171,12 @@ int pe_flash_prefill_h16(const float* q, int64_t q_stride, const float* k_cache,
 /* pe_flash_prefill_h16 of a prompt starting at position 0 with K and V taken from the fp16 key
  * blocks of pe_rope_kv_write_blocks (kv16, kv16_blocks per kv head, L <= 64 kv16_blocks; the
  * positions past L in the last block must be finite, e.g. zero): the blocks are copied into LDS
- * with direct-to-LDS loads instead of being converted from the fp32 caches. head_dim 64.
- * workspace NULL: every set of 32 queries runs in one workgroup over all the keys it sees, with
- * the same fp16 operand values in the same positions and the same order as pe_flash_prefill_h16,
- * so the same output bits. workspace non-NULL (16-byte aligned, workspace_bytes >=
+ * with direct-to-LDS loads instead of being converted from the fp32 caches. head_dim 64. q is
+ * scaled by scale * log2 e before it is rounded to fp16 (pe_flash_prefill_h16 rounds q itself)
+ * and the scores are accumulated onto minus the running maximum: the same attention within that
+ * rounding (outputs within a few fp16 ulps of pe_flash_prefill_h16's).
+ * workspace NULL: every set of 32 queries runs in one workgroup over all the keys it sees.
+ * workspace non-NULL (16-byte aligned, workspace_bytes >=
  * pe_flash_prefill_blocks_workspace(n_head, n_kv, L), any contents): when the longest set sees
  * more than 64 key blocks (L > 4096), the sets that do are split into P = ceil(longest / 64)
  * key ranges run by separate workgroups (so no workgroup walks more than about 64 blocks), each

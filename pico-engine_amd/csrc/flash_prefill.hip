@@ -128,6 +128,48 @@ PE_DEV void fp_softmax(const fv4 (&s)[4], float sl2, float& m_run, float& l_run,
     l_run += swap32_sum(swap16_sum(psum));
 }
 
+// fp_softmax for scores that arrive in log2 units with the running maximum already subtracted
+// (k_flash_prefill_blocks: q is scaled by scale * log2 e before its fp16 rounding, and the score
+// MFMAs accumulate onto cvec = -m), so a probability is one exp2 of the score. `first` (the
+// range's first block) sets m to the block maximum. When m moves by d (lazily, as above), o and
+// l are scaled by 2^-d, the block's scores lose d, and cvec follows m.
+PE_DEV void fp_softmax_offset(fv4 (&s)[4], bool first, float& m_run, float& l_run, fv4& cvec, fv4 (&o)[4],
+                       fh8 (&pb)[2]) {
+    float mx = s[0][0];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (jt | r) mx = fmaxf(mx, s[jt][r]);
+    mx = swap32_max(swap16_max(mx));
+    const bool grow = first || mx > kFpLazy;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float shift = grow ? mx : 0.f;
+        const float corr = grow ? __builtin_amdgcn_exp2f(-mx) : 1.0f;
+        l_run *= corr;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[d][r] *= corr;
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[jt][r] -= shift;
+        m_run += shift;
+        cvec = fv4{-m_run, -m_run, -m_run, -m_run};
+    }
+    float psum = 0.f;
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float e = __builtin_amdgcn_exp2f(s[jt][r]);
+            psum += e;
+            pb[jt >> 1][4 * (jt & 1) + r] = (_Float16)e;
+        }
+    l_run += swap32_sum(swap16_sum(psum));
+}
+
 // OutT _Float16: the output rounded to fp16 (nearest even), the operand of the o-projection
 // GEMM (p.out then points to fp16 rows).
 template <typename OutT>
@@ -354,8 +396,10 @@ __global__ __launch_bounds__(1024) void k_flash_prefill(FlashParams p, int qb_si
 // slots: block b + 3's loads are issued after the barrier of block b (every wave is then past
 // block b - 1, whose slot they overwrite) and waited for with the wave's own vmcnt count. The
 // blocks a wave's 32 queries all see in full run without the causal mask (no branch in the
-// loop body), the rest with it. Per query the products, the softmax and their order are
-// k_flash_prefill's, so the results are the same bits.
+// loop body), the rest with it. q is scaled by scale * log2 e before its fp16 rounding and the
+// score MFMAs accumulate onto minus the running maximum (fp_softmax_offset), which takes the
+// exponent's fma out of the softmax: the same attention as k_flash_prefill within the fp16
+// rounding of the scaled q (not the same bits).
 template <int LW>
 __global__ __launch_bounds__(1024) void k_flash_prefill_blocks(FlashParams p, int qb_size) {
     constexpr int kSlotHalves = kFpKeys * kFpHd;  // one block's K (or V^T), fp16
@@ -390,7 +434,7 @@ __global__ __launch_bounds__(1024) void k_flash_prefill_blocks(FlashParams p, in
     const float NEG_INF = -__builtin_huge_valf();
     const float sl2 = p.scale * 1.4426950408889634f;
 
-    fh8 qa[2][2];  // tile tt: row li = query q0 + 16 tt + li, dims 32 s + 8 lg .. + 8
+    fh8 qa[2][2];  // tile tt: row li = query q0 + 16 tt + li, dims 32 s + 8 lg .. + 8, times sl2
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
         const int64_t qi = q0 + 16 * tt + li < p.L ? q0 + 16 * tt + li : p.L - 1;
@@ -399,10 +443,12 @@ __global__ __launch_bounds__(1024) void k_flash_prefill_blocks(FlashParams p, in
         for (int s = 0; s < 2; ++s) {
             const float4 a = *reinterpret_cast<const float4*>(qr + 32 * s + 8 * lg);
             const float4 b = *reinterpret_cast<const float4*>(qr + 32 * s + 8 * lg + 4);
-            qa[tt][s] = f8_to_h8(a, b);
+            qa[tt][s] = f8_to_h8(make_float4(a.x * sl2, a.y * sl2, a.z * sl2, a.w * sl2), make_float4(b.x * sl2, b.y * sl2, b.z * sl2, b.w * sl2));
         }
     }
-    float m_run[2] = {NEG_INF, NEG_INF}, l_run[2] = {0.f, 0.f};
+    float m_run[2] = {0.f, 0.f}, l_run[2] = {0.f, 0.f};
+    fv4 cvec[2] = {fv4{0.f, 0.f, 0.f, 0.f}, fv4{0.f, 0.f, 0.f, 0.f}};
+    bool first = true;
     fv4 o[2][4];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
@@ -415,11 +461,11 @@ __global__ __launch_bounds__(1024) void k_flash_prefill_blocks(FlashParams p, in
     const int b_end = part < 0 ? nblk_all : (int)((int64_t)(part + 1) * nblk_all / p.nparts);
 
     // S^T = K Q^T of one tile for the block in ring slot `slot`
-    auto scores = [&](int slot, const fh8 (&qq)[2], fv4 (&s)[4]) {
+    auto scores = [&](int slot, const fh8 (&qq)[2], const fv4& cv, fv4 (&s)[4]) {
         const _Float16* kd = ks + slot * kSlotHalves;
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt) {
-            s[jt] = fv4{0.f, 0.f, 0.f, 0.f};
+            s[jt] = cv;
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const fh8 kbv = *reinterpret_cast<const fh8*>(kd + lofs(16 * jt + li, 4 * u + lg));
@@ -438,9 +484,9 @@ __global__ __launch_bounds__(1024) void k_flash_prefill_blocks(FlashParams p, in
             }
     };
     // k_flash_prefill's online softmax and O^T += V^T P^T for one tile
-    auto softmax_pv = [&](const fv4 (&s)[4], int slot, float& mr, float& lr, fv4 (&oo)[4]) {
+    auto softmax_pv = [&](fv4 (&s)[4], int slot, float& mr, float& lr, fv4& cv, fv4 (&oo)[4]) {
         fh8 pb[2];
-        fp_softmax(s, sl2, mr, lr, oo, pb);
+        fp_softmax_offset(s, first, mr, lr, cv, oo, pb);
         const _Float16* vd = vt + slot * kSlotHalves;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -467,14 +513,15 @@ __global__ __launch_bounds__(1024) void k_flash_prefill_blocks(FlashParams p, in
     auto body = [&](int b, auto masked) {
         const int slot = b & (kFpBlkSlots - 1);
         fv4 s0[4], s1[4];
-        scores(slot, qa[0], s0);
-        scores(slot, qa[1], s1);
+        scores(slot, qa[0], cvec[0], s0);
+        scores(slot, qa[1], cvec[1], s1);
         if constexpr (decltype(masked)::value) {
             mask(b * kFpKeys, q0, s0);
             mask(b * kFpKeys, q0 + 16, s1);
         }
-        softmax_pv(s0, slot, m_run[0], l_run[0], o[0]);
-        softmax_pv(s1, slot, m_run[1], l_run[1], o[1]);
+        softmax_pv(s0, slot, m_run[0], l_run[0], cvec[0], o[0]);
+        softmax_pv(s1, slot, m_run[1], l_run[1], cvec[1], o[1]);
+        first = false;
     };
     blk_load(b_begin);
     if (b_begin + 1 < b_end) blk_load(b_begin + 1);

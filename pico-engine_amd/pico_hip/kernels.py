@@ -1244,8 +1244,9 @@ def flash_prefill_blocks(q: torch.Tensor, kv16: torch.Tensor, scale: float | Non
                          out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
                          split: bool = True) -> torch.Tensor:
     """flash_prefill(half=True) of a prompt from position 0, reading K and V from the fp16 key
-    blocks rope_kv_write(kv16=...) wrote (pe_flash_prefill_blocks); head_dim 64. split=False:
-    one workgroup per 32-query set over all its keys, the same bits as flash_prefill(half=True).
+    blocks rope_kv_write(kv16=...) wrote (pe_flash_prefill_blocks); head_dim 64; q is rounded to
+    fp16 after its scale * log2 e scaling (within a few fp16 ulps of flash_prefill(half=True)).
+    split=False: one workgroup per 32-query set over all its keys.
     split=True: query sets that see more than 64 key blocks (L > 4096) run as several key
     ranges merged by a second launch (within fp32 rounding of the unsplit order), in
     ``workspace`` (uint8, at least flash_prefill_blocks_workspace bytes; allocated when None)."""

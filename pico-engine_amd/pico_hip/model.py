@@ -165,11 +165,10 @@ class Transformer:
         self.prefill_blaslt = False
         self._lt_ws: torch.Tensor | None = None
         # prompts from position 0 at head_dim 64: K and V also written as fp16 key blocks for the
-        # flash kernel's direct-to-LDS copies (same bits); off: it converts the fp32 caches
+        # flash kernel's direct-to-LDS copies; off: the flash kernel that converts the fp32 caches
         self.prefill_kv_blocks = True
         # with the key blocks, prompts past 4096 tokens split the long query sets' key ranges
-        # over workgroups and merge them (within fp32 rounding); off: one workgroup per query
-        # set, the same bits as the fp32-cache path
+        # over workgroups and merge them (within fp32 rounding); off: one workgroup per query set
         self.prefill_flash_split = True
         self._f16: list[dict[str, torch.Tensor]] | None = None
         # greedy decode steps the persistent kernel covers can run as one launch per token
@@ -449,7 +448,7 @@ class Transformer:
         qkv = torch.empty(Lt, qd + 2 * kd, device=self.device, dtype=torch.float32)
         q_rot = torch.empty(Lt, nh, hd, device=self.device, dtype=torch.float32)
         # a prompt from position 0 at head_dim 64: the RoPE pass also writes K and V as fp16 key
-        # blocks that the flash kernel copies straight into LDS (the same values, the same bits)
+        # blocks that the flash kernel copies straight into LDS (the same values)
         kv16 = K.kv16_blocks(nkv, Lt, self.device) if self.prefill_kv_blocks and hd == 64 and pos0 == 0 else None
         # past 4096 tokens the long query sets' key ranges are split over workgroups and merged
         # (a second launch), in one workspace for every layer
