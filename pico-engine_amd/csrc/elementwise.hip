@@ -62,7 +62,7 @@ __global__ void k_silu_mul(const float* __restrict__ gu, int64_t gs, float* __re
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
         const int64_t l = idx / ffn, j = idx % ffn;
         const float g = gu[l * gs + j], u = gu[l * gs + ffn + j];
-        out[l * os + j] = (g * (1.0f / (1.0f + expf(-g)))) * u;
+        out[l * os + j] = silu_mul_prefill(g, u);
     }
 }
 

@@ -203,7 +203,7 @@ __global__ __launch_bounds__(256) void k_gemm_f16(GemmF16Args p) {
                     const int64_t m = m0 + 16 * i + 4 * (l >> 4) + r;
                     if (m >= p.M) continue;
                     const float g = acc[i][2 * c][r], u = acc[i][2 * c + 1][r];
-                    float y = (g * (1.0f / (1.0f + expf(-g)))) * u;
+                    float y = silu_mul_prefill(g, u);
                     if constexpr (CH) {
                         // y is rounded to fp32 first, then to fp16 (the reference's silu_mul
                         // result, then autocast's operand rounding): without the barrier the
@@ -578,7 +578,7 @@ __global__ __launch_bounds__(512) void k_gemm_h16_silu_dl(GemmF16Args p) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float g = acc[i][2 * c][r], u = acc[i][2 * c + 1][r];
-                float y = (g * (1.0f / (1.0f + expf(-g)))) * u;
+                float y = silu_mul_prefill(g, u);
                 asm volatile("" : "+v"(y));
                 eh[(16 * i + 4 * lq + r) * EH + 16 * c + li] = (_Float16)y;
             }

@@ -42,6 +42,14 @@ PE_DEV float h2f_fast(uint32_t h) {
 // fp32 -> fp16 (round to nearest even) -> fp32, for the reference's fp16 output rounding.
 PE_DEV float round_to_f16(float v) { return __half2float(__float2half_rn(v)); }
 
+// silu(g) * u = g / (1 + e^-g) * u of the prefill products (the SiLU GEMM epilogues and
+// silu_mul), on the hardware exp2 and reciprocal (about 1 ulp each) instead of the library
+// expf and an IEEE division, which took ~13 % of the 8192 x 9728 x 896 SiLU GEMM. The decode
+// kernels keep expf and the division.
+PE_DEV float silu_mul_prefill(float g, float u) {
+    return (g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f))) * u;
+}
+
 // Sum over aligned groups of W lanes (W a power of two <= 64) by butterfly; every lane of
 // a group ends with the same bits (IEEE addition is commutative).
 template <int W>
