@@ -20,7 +20,13 @@
 // exponent's fma) keeps one running max and sum per lane with two cross-lane steps, and the
 // probabilities go straight from registers into the B operand of O^T += V^T P^T (8 MFMAs),
 // with V^T staged in the matching key order. The heaviest query blocks (most keys) are
-// scheduled so that light blocks share CUs with heavy ones.
+// scheduled so that light blocks share CUs with heavy ones. (The running maximum moves lazily:
+// fp_softmax.)
+//
+// k_flash_prefill_blocks (pe_flash_prefill_blocks, a prompt from position 0) is the faster
+// form for K / V already stored as fp16 LDS images by the RoPE pass: two 16-query tiles per
+// wave, 7-wave workgroups two per CU, long query sets split over workgroups and merged by
+// k_flash_merge, and scores offset by the running maximum inside the MFMAs (its comment).
 #include "pe_common.h"
 
 #include <type_traits>
