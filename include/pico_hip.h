@@ -190,7 +190,9 @@ int pe_flash_prefill_blocks(const float* q, int64_t q_stride, const void* kv16, 
                             pe_stream_t stream);
 
 /* Workspace bytes pe_flash_prefill_blocks uses for L queries (0: nothing is split, any
- * workspace or NULL gives the unsplit schedule). No counterpart in the reference. */
+ * workspace or NULL gives the unsplit schedule): P x (L - first split query) x n_head x 272
+ * (config 3, L = 8192, 14 heads: P = 2, 31 MB; it grows as L^2 / 64, 0.9 GB at L = 32768).
+ * No counterpart in the reference. */
 int64_t pe_flash_prefill_blocks_workspace(int n_head, int n_kv, int64_t L);
 
 /* Plain prefill GEMM on ROCm's hipBLASLt: c (M, N) = a (M, K) . w (N, K)^T (+ bias[N])
